@@ -1,0 +1,180 @@
+"""Headline benchmark: warm-median ms/step of the Karpathy char-nanoGPT f32
+training step on one MI355X.
+
+A step = zero_grad -> forward -> cross_entropy -> backward -> "AdamW"
+(examples/nanogpt_modular.ml:167-189) through libmalus_hip's C ABI, with a
+device flush inside the timed step (docs/adr/0038-benchmark-methodology.md).
+Token batches are synthetic (int32 i.i.d. uniform in [0, 65) from a fixed
+seed) and resident in HBM before timing starts.  Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+CFG = dict(V=65, T=256, C=384, H=6, L=6, B=64)
+OPT = dict(lr=1e-3, b1=0.9, b2=0.99, eps=1e-8, wd=0.1)
+METRIC = "warm-median ms/step, char-nanoGPT f32 train step; HBM GB/s & MFMA % of peak"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemm_flops_per_step(cfg) -> float:
+    """Algorithmic GEMM FLOPs of one step: forward plus both VJP GEMMs."""
+    B, T, Cn, H, L, V = cfg["B"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["V"]
+    N, hs = B * T, Cn // H
+    fwd_layer = 2 * N * Cn * Cn * 4 + 2 * N * Cn * 4 * Cn * 2 + 2 * (B * H) * T * T * hs * 2
+    fwd = L * fwd_layer + 2 * N * Cn * V
+    return 3.0 * fwd
+
+
+def cpu_baseline(sample_batch: int, threads: int):
+    """The oracle (plain-C restatement of the reference CPU path) on a
+    bounded sample: one full step at batch `sample_batch`, scaled to the
+    configured batch (every cost in the step is linear in the batch)."""
+    from oracle import oracle as O
+    import numpy as np
+
+    cfg = dict(CFG, B=sample_batch)
+    O.set_threads(threads)
+    g = O.Gpt(**cfg, rng_call_idx=0, **OPT)
+    rng = np.random.default_rng(7)
+    n = cfg["B"] * cfg["T"]
+    x = rng.integers(0, cfg["V"], n).astype(np.int32)
+    y = rng.integers(0, cfg["V"], n).astype(np.int32)
+    t0 = time.perf_counter()
+    g.step(x, y, 1)
+    dt = time.perf_counter() - t0
+    scale = CFG["B"] / sample_batch
+    return dict(value=round(dt * 1e3 * scale, 1), unit="ms/step", cores=threads, kind="port",
+                sample=f"1 full step at batch {sample_batch} of {CFG['B']} ({dt:.1f} s), scaled x{scale:g}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-batch", type=int, default=1)
+    ap.add_argument("--cpu-threads", type=int, default=1)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
+              "multi-GPU data parallelism is designed but not built", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    import malus_amd as M
+
+    rt = M.Runtime()
+    L = rt.L
+    name = C.create_string_buffer(64)
+    cus, clk = C.c_int(), C.c_int()
+    L.malus_device_info(name, 64, C.byref(cus), C.byref(clk))
+    log(f"device {name.value.decode()} CUs {cus.value} clock {clk.value / 1e6:.2f} GHz")
+
+    L.malus_rng_set_counter(0)
+    g = L.malus_gpt_create(CFG["V"], CFG["T"], CFG["C"], CFG["H"], CFG["L"], CFG["B"], OPT["lr"], OPT["b1"],
+                           OPT["b2"], OPT["eps"], OPT["wd"])
+    n = CFG["B"] * CFG["T"]
+    rng = np.random.default_rng(2024)
+    batches = []
+    for _ in range(a.warmup + a.steps):
+        x = rng.integers(0, CFG["V"], n).astype(np.int32)
+        y = rng.integers(0, CFG["V"], n).astype(np.int32)
+        batches.append((rt.tensor(x), rt.tensor(y)))
+    L.gpu_barrier()
+
+    t = 0
+    first_loss = last_loss = None
+    for i in range(a.warmup):
+        t += 1
+        hl = L.malus_gpt_step(g, batches[i][0], batches[i][1], t)
+        L.gpu_barrier()
+        if first_loss is None:
+            first_loss = L.malus_tensor_get_f32(hl, 0)
+        rt.free(hl)
+
+    L.malus_ktimer_collect(None, C.byref(C.c_double()), C.byref(C.c_double()))  # drop warmup records
+    L.malus_ktimer_enable(1)
+    L.gpu_barrier()
+    times = []
+    t_all = time.perf_counter()
+    for i in range(a.steps):
+        t += 1
+        x, y = batches[a.warmup + i]
+        t0 = time.perf_counter()
+        hl = L.malus_gpt_step(g, x, y, t)
+        L.gpu_barrier()  # flush inside the timed step
+        times.append((time.perf_counter() - t0) * 1e3)
+        if i == a.steps - 1:
+            last_loss = L.malus_tensor_get_f32(hl, 0)
+        rt.free(hl)
+    L.gpu_barrier()
+    wall = time.perf_counter() - t_all
+    L.malus_ktimer_enable(0)
+    gms, gflop = C.c_double(), C.c_double()
+    ng = L.malus_ktimer_collect(b"gemm", C.byref(gms), C.byref(gflop))
+
+    med = statistics.median(times)
+    step_flops = gemm_flops_per_step(CFG)
+    gemm_tflops = gflop.value / (gms.value * 1e-3) / 1e12 if gms.value > 0 else 0.0
+    log(f"steps {a.steps}: median {med:.3f} ms  min {min(times):.3f}  max {max(times):.3f}  wall {wall:.2f} s")
+    log(f"loss first {first_loss:.4f} last {last_loss:.4f}")
+    log(f"gemm: {ng} launches, {gms.value / a.steps:.3f} ms/step, {gemm_tflops:.1f} TFLOP/s "
+        f"({gflop.value / a.steps / 1e9:.1f} GFLOP/step; algorithmic {step_flops / 1e9:.1f})")
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(a.cpu_sample_batch, a.cpu_threads)
+            log(f"cpu baseline: {cpu}")
+        except Exception as e:  # the CPU leg is a reported baseline only
+            log(f"cpu baseline failed: {e!r}")
+
+    for x, y in batches:
+        rt.free(x, y)
+    L.malus_gpt_free(g)
+
+    out = {
+        "metric": METRIC,
+        "value": round(med, 3),
+        "unit": "ms/step",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(med, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic int32 tokens i.i.d. uniform in [0,65) (seed 2024); weights randn*0.02 (Philox, call 0)",
+        "config": {"workload": "C5 Karpathy char-nanoGPT train step (fwd+bwd+AdamW)", "vocab": CFG["V"],
+                   "block_size": CFG["T"], "n_embd": CFG["C"], "n_head": CFG["H"], "n_layer": CFG["L"],
+                   "batch": CFG["B"], "tokens_per_step": n, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "k_sgemm (all GEMM launches of the step)",
+                     "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
+                     "gemm_ms_per_step": round(gms.value / a.steps, 3),
+                     "gemm_gflop_per_step": round(gflop.value / a.steps / 1e9, 1)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,229 @@
+/*
+ * libmalus_hip — the malus runtime C ABI on AMD MI355X (gfx950).
+ *
+ * Drop-in for crates/malus-runtime (the Metal runtime): every symbol the
+ * Cranelift JIT imports through RuntimeSymbols
+ * (crates/malus-codegen-cpu/src/lib.rs:115-184) plus the Rust-side helpers
+ * of crates/malus-runtime/src/lib.rs:117-176, with the same names, argument
+ * meaning and ownership rules.  Each declaration cites the reference
+ * function it replaces.
+ *
+ * Handles: an int64_t tensor handle is an opaque pointer; 0 is "null".
+ * Returned handles carry refcount 1 and are owned by the caller; input
+ * handles are borrowed.  Errors follow the reference's panic model
+ * ("malus: ..." on stderr, then abort) unless malus_set_abort_on_error(0)
+ * selects return mode (the call returns 0 and malus_last_error() holds the
+ * message).
+ *
+ * Execution: every GPU op is enqueued on one in-order HIP stream; a host
+ * read (tensor_print, malus_tensor_get_f32, malus_tensor_read) waits only
+ * when the tensor still has an unfinished write.
+ */
+#ifndef MALUS_HIP_H
+#define MALUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype tags (metal.rs:26-50): F32=0 F16=1 BF16=2 I8=3 I16=4 I32=5 I64=6
+ * U8=7 U16=8 U32=9 U64=10; tensors support F32, I32 and I64. */
+
+/* ---- context ---------------------------------------------------------- */
+/* Initialize the device context (lazy in every entry point; explicit here).
+ * Replaces the lazy MetalContext singleton, metal.rs:62-112. */
+void malus_init(void);
+/* runtime_init(&HashMap<u64, String>) as a C ABI, metal.rs:304-336.
+ * Builtin stdlib kernels are recognized by a "//@malus-builtin <name>" tag;
+ * other sources are HIP C++ compiled with hipRTC (cached by source text). */
+void malus_runtime_init(const uint64_t* ids, const char* const* sources, size_t n);
+int malus_kernel_is_builtin(uint64_t id);
+
+/* ---- tensor creation and lifetime (metal.rs:340-558) -------------------- */
+int64_t tensor_alloc_gpu(int32_t dtype, const size_t* shape, size_t ndim, const void* data); /* metal.rs:341-348 */
+int64_t tensor_alloc_zeros_gpu(const size_t* shape, size_t ndim);                          /* metal.rs:458-484 */
+int64_t tensor_alloc_ones_gpu(const size_t* shape, size_t ndim);                           /* metal.rs:486-492 */
+void tensor_retain(int64_t h);                                                              /* metal.rs:499-507 */
+void tensor_release(int64_t h);                                                             /* metal.rs:520-552 */
+void tensor_free(int64_t h);                                                                /* metal.rs:556-558 */
+
+/* ---- metadata and host reads (metal.rs:560-672, 1763-1769) -------------- */
+void tensor_print(int64_t h);                     /* metal.rs:561-588 (Rust `{}` float formatting) */
+int64_t tensor_len(int64_t h);                    /* metal.rs:651-655 */
+int64_t tensor_ndim(int64_t h);                   /* metal.rs:657-661 */
+int64_t tensor_dim(int64_t h, int64_t i);         /* metal.rs:663-672 (negative i allowed) */
+float malus_tensor_get_f32(int64_t h, int64_t i); /* metal.rs:1763-1769 */
+/* No reference counterpart: bulk host I/O used by tests and the bench. */
+int32_t malus_tensor_dtype(int64_t h);
+void malus_tensor_shape(int64_t h, size_t* out /* [8] */);
+void malus_tensor_read(int64_t h, void* dst, size_t bytes);
+void malus_tensor_write(int64_t h, const void* src, size_t bytes);
+size_t malus_format_f32(float v, char* buf, size_t cap);
+
+/* ---- synchronization (metal.rs:201-259, 677-694) ------------------------ */
+void gpu_barrier(void);                 /* metal.rs:677-694 */
+void malus_flush_if_pending(int64_t h); /* flush_if_pending, metal.rs:244-252 */
+int tensor_is_pending(int64_t h);       /* metal.rs:256-259 */
+
+/* ---- kernel launches (metal.rs:1860-2065) -------------------------------- */
+int64_t kernel_dispatch(uint64_t kernel_id, const int64_t* handles, size_t count); /* metal.rs:1860-1931 */
+int64_t kernel_dispatch_v2(uint64_t kernel_id, const int64_t* handles, size_t handle_count,
+                           const size_t* grid_dims /*[3]*/, const size_t* tg_dims /*[3]*/,
+                           const size_t* out_shape, size_t out_ndim, int32_t out_dtype_tag,
+                           const void* uniforms, size_t uniforms_bytes); /* metal.rs:1944-2065 */
+
+/* ---- matmul, shapes, masks, RNG ----------------------------------------- */
+int64_t tensor_matmul(int64_t a, int64_t b);                            /* metal.rs:820-962 (FP32 MFMA) */
+int64_t tensor_reshape(int64_t h, const size_t* dims, size_t ndim);     /* metal.rs:1421-1435 */
+int64_t tensor_permute(int64_t h, const size_t* perm, size_t ndims);    /* metal.rs:1405-1417 */
+int64_t tensor_causal_mask(int64_t t);                                  /* metal.rs:1600-1612 */
+int64_t tensor_randn(const size_t* shape, size_t ndim);                 /* metal.rs:1720-1740 */
+float malus_rand_uniform(void);                                         /* metal.rs:1744-1750 */
+int64_t malus_rand_int(int64_t n);                                      /* metal.rs:1752-1759 */
+/* No reference counterpart: read/set the per-thread RNG call counter. */
+uint64_t malus_rng_get_counter(void);
+void malus_rng_set_counter(uint64_t v);
+
+/* ---- Buffer<i32> staging (buffer.rs:1-50) -------------------------------- */
+int64_t malus_buffer_i32(int64_t len);
+int64_t malus_buffer_get_i32(int64_t h, int64_t i);
+void malus_buffer_set_i32(int64_t h, int64_t i, int64_t v);
+void malus_buffer_free(int64_t h);
+int64_t malus_buffer_freeze_i32(int64_t h);
+
+/* ---- autograd tape (tape.rs) -------------------------------------------- */
+void tape_record_binop(int32_t op_tag, int64_t a, int64_t b, int64_t out);                    /* tape.rs:206-218 */
+void tape_record_unary(int32_t op_tag, int64_t x, int64_t out);                               /* tape.rs:221-231 */
+void tape_record_reduce(int32_t op_tag, int64_t x, int64_t out, int64_t axis, int64_t keepdim); /* tape.rs:236-255 */
+void tape_record_perm(int32_t op_tag, int64_t x, int64_t out, const size_t* dims, size_t ndims); /* tape.rs:259-283 */
+void tape_record_layernorm(int32_t op_tag, int64_t x, int64_t out, int64_t var_h, int64_t axis); /* tape.rs:289-310 */
+void tape_record_cross_entropy(int32_t op_tag, int64_t logits, int64_t out, int64_t softmax_h,
+                               int64_t targets);                                               /* tape.rs:315-337 */
+void tape_record_embedding(int32_t op_tag, int64_t weight, int64_t indices, int64_t out);      /* tape.rs:342-353 */
+void tape_register_leaf(int64_t h);                                                            /* tape.rs:358-363 */
+void tape_pause(void);                                                                         /* tape.rs:365-368 */
+void tape_resume(void);                                                                        /* tape.rs:370-373 */
+void tape_clear(void);                                                                         /* tape.rs:377-389 */
+int64_t tape_get_grad(int64_t h);                                                              /* tape.rs:395-411 */
+void backward(int64_t loss);                                                                   /* tape.rs:421-729 */
+void tape_zero_grad(const int64_t* handles, size_t count);                                     /* tape.rs:757-774 */
+void tape_reset(void);                                                                         /* tape.rs:735-750 */
+void tape_register_backward_fn(int32_t slot, size_t fnptr);                                    /* tape.rs:143-147 */
+/* No reference counterpart: the pointer currently held by a BwdSlot. */
+size_t malus_tape_backward_fn(int32_t slot);
+size_t malus_tape_len(void);
+void malus_tape_registry_lens(size_t* out2);
+
+/* ---- bench timer (bench.rs:1-76) ----------------------------------------- */
+void bench_enable(void);
+void bench_reset(void);
+void bench_step_begin(void);
+void bench_step_end(void);
+/* bench_report (bench.rs:51-70) through out-params; returns 0 when <= 3 steps. */
+int bench_report(double* median_ms, double* min_ms, double* max_ms, int64_t* warm_steps);
+void malus_bench_record(double ms);
+
+/* ---- counters and pool (runtime/lib.rs:1-94, metal.rs:114-199) ----------- */
+int64_t malus_cpu_compute_count(void); /* always 0: the library has no CPU compute path */
+void malus_cpu_compute_reset(void);
+void malus_rc_counts(int64_t* out3 /* retain, release, alloc */);
+void malus_rc_reset(void);
+void malus_record_diff(float v);
+float malus_gradcheck_max_diff(void);
+void malus_gradcheck_reset(void);
+void malus_pool_stats(int64_t* out4 /* hits, misses, pooled_bytes, peak_device_bytes */);
+int64_t malus_pool_live_bytes(void);
+size_t malus_pool_buckets(size_t* sizes, size_t* counts, size_t cap);
+void malus_pool_reset(void);
+void malus_set_mem_budget(int64_t bytes);
+size_t malus_alloc_histogram(size_t* sizes, uint64_t* counts, size_t cap);
+
+/* ---- instrumentation and errors (no reference counterparts) ------------- */
+void malus_ktimer_enable(int on);
+int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
+int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
+void malus_set_abort_on_error(int on);
+const char* malus_last_error(void);
+void malus_clear_error(void);
+
+/* ---- stdlib host functions ------------------------------------------------
+ * The .ml host fns of crates/malus-stdlib/stdlib (names prefixed malus_std_),
+ * on hand-written gfx950 kernels.  The backward ones are the default BwdSlot
+ * entries (codegen-cpu/lib.rs:189-220). */
+int64_t malus_std_broadcast_fwd(int32_t op /*0 add,1 sub,2 mul,3 div*/, int64_t a, int64_t b); /* broadcast_binop.ml:82-112 */
+int64_t malus_std_broadcast_add_fwd(int64_t a, int64_t b);
+int64_t malus_std_broadcast_sub_fwd(int64_t a, int64_t b);
+int64_t malus_std_broadcast_mul_fwd(int64_t a, int64_t b);
+int64_t malus_std_broadcast_div_fwd(int64_t a, int64_t b);
+int64_t malus_std_scalar_op(int32_t op, int64_t a, float s, int32_t scalar_on_right);    /* codegen-gpu/lib.rs:400-418 */
+int64_t malus_std_scalar_op_dev(int32_t op, int64_t a, int64_t s1, int32_t scalar_on_right);
+int64_t malus_std_unary(int32_t op /*relu,sigmoid,tanh,exp,log,sqrt,abs,gelu*/, int64_t x); /* codegen-gpu/lib.rs:373-390 */
+int64_t malus_std_reduce_fwd(int32_t op /*sum,mean,max,var*/, int64_t x, int64_t axis, int64_t keepdim); /* reduce_*.ml */
+int64_t malus_std_reduce_all_sum_fwd(int64_t x);                             /* reduce_all.ml:9-12 */
+int64_t malus_std_softmax_fwd(int64_t x, int64_t axis);                      /* softmax.ml:30-40 */
+int64_t malus_std_layernorm_fwd(int64_t x, int64_t axis, int64_t* var_out);  /* layernorm.ml:59-72 */
+int64_t malus_std_gelu_fwd(int64_t x);                                       /* gelu.ml:12-14 */
+int64_t malus_std_cross_entropy_fwd(int64_t logits, int64_t targets, int64_t* probs_out); /* cross_entropy.ml:18-28 */
+int64_t malus_std_embedding_fwd(int64_t weight, int64_t indices);            /* embedding.ml:18-23 */
+int64_t malus_std_transpose_2d_fwd(int64_t x);                               /* permute.ml:21-25 */
+int64_t malus_std_permute_3d_fwd(int64_t x, int64_t p0, int64_t p1, int64_t p2); /* permute.ml:62-67 */
+int64_t malus_std_permute_nd_fwd(int64_t x, int64_t p0, int64_t p1, int64_t p2, int64_t p3, int64_t p4,
+                                 int64_t p5, int64_t p6, int64_t p7);        /* permute.ml:107-126 */
+int64_t malus_std_scale_fwd(int64_t x, float c);                             /* unary_bwd.ml:10-12 */
+int64_t malus_std_fill_like_fwd(int64_t x, float c);                         /* unary_bwd.ml:20-22 */
+int64_t malus_std_eq_fwd(int64_t a, int64_t b);                              /* unary_bwd.ml:32-34 */
+int64_t malus_std_expand_axis_fwd(int64_t small, int64_t x_template, int64_t axis); /* reduce_bwd.ml:22-38 */
+int64_t malus_std_sum_to_shape_bwd(int64_t dout, int64_t target);            /* elementwise_bwd.ml:8-22 */
+int64_t malus_std_add_bwd_a(int64_t dout, int64_t a);                        /* elementwise_bwd.ml:25-26 */
+int64_t malus_std_add_bwd_b(int64_t dout, int64_t b);                        /* elementwise_bwd.ml:28-29 */
+int64_t malus_std_sub_bwd_a(int64_t dout, int64_t a);                        /* elementwise_bwd.ml:32-33 */
+int64_t malus_std_sub_bwd_b(int64_t dout, int64_t b);                        /* elementwise_bwd.ml:35-37 */
+int64_t malus_std_mul_bwd_a(int64_t dout, int64_t a, int64_t b);             /* elementwise_bwd.ml:41-43 */
+int64_t malus_std_mul_bwd_b(int64_t dout, int64_t a, int64_t b);             /* elementwise_bwd.ml:45-47 */
+int64_t malus_std_div_bwd_a(int64_t dout, int64_t a, int64_t b);             /* elementwise_bwd.ml:51-53 */
+int64_t malus_std_div_bwd_b(int64_t dout, int64_t a, int64_t b);             /* elementwise_bwd.ml:55-60 */
+int64_t malus_std_sigmoid_bwd(int64_t s, int64_t dout);                      /* unary_bwd.ml:42-44 */
+int64_t malus_std_relu_bwd(int64_t x, int64_t dout);                         /* unary_bwd.ml:54-56 */
+int64_t malus_std_tanh_bwd(int64_t t, int64_t dout);                         /* unary_bwd.ml:64-66 */
+int64_t malus_std_sqrt_bwd(int64_t s, int64_t dout);                         /* unary_bwd.ml:73-75 */
+int64_t malus_std_abs_bwd(int64_t x, int64_t dout);                          /* unary_bwd.ml:89-91 */
+int64_t malus_std_sum_bwd(int64_t x, int64_t dout);                          /* reduce_bwd.ml:74-76 */
+int64_t malus_std_reduce_sum_axis_bwd(int64_t x, int64_t dout, int64_t axis);   /* reduce_bwd.ml:41-42 */
+int64_t malus_std_reduce_mean_axis_bwd(int64_t x, int64_t dout, int64_t axis);  /* reduce_bwd.ml:45-51 */
+int64_t malus_std_reduce_max_axis_bwd(int64_t x, int64_t y, int64_t dout, int64_t axis); /* reduce_bwd.ml:54-58 */
+int64_t malus_std_reduce_var_axis_bwd(int64_t x, int64_t dout, int64_t axis);   /* reduce_bwd.ml:61-71 */
+int64_t malus_std_softmax_bwd(int64_t s, int64_t dout, int64_t axis);           /* transformer_bwd.ml:15-20 */
+int64_t malus_std_layernorm_bwd(int64_t y, int64_t var, int64_t dout, int64_t axis); /* tape.rs:1162-1186 */
+int64_t malus_std_gelu_bwd(int64_t x, int64_t dout);                         /* transformer_bwd.ml:50-52 */
+int64_t malus_std_cross_entropy_bwd(int64_t probs, int64_t targets, int64_t dout); /* transformer_bwd.ml:67-75 */
+int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout);    /* transformer_bwd.ml:93-98 */
+int64_t malus_std_matmul_bwd_a(int64_t a, int64_t b, int64_t dout);          /* matmul_bwd.ml:15-19 */
+int64_t malus_std_matmul_bwd_b(int64_t a, int64_t b, int64_t dout);          /* matmul_bwd.ml:21-29 */
+/* examples/nanogpt_modular.ml:97-108 fused into one pass; returns the new
+ * parameter, *m_out / *v_out the new moments. */
+int64_t malus_std_adam_l2(int64_t p, int64_t g, int64_t m, int64_t v, float lr, float b1, float b2, float eps,
+                          float wd, int64_t t, int64_t* m_out, int64_t* v_out);
+
+/* ---- workload drivers (the examples' programs replayed through this ABI) - */
+void* malus_gpt_create(int vocab, int block, int n_embd, int n_head, int n_layer, int batch, float lr, float beta1,
+                       float beta2, float eps, float wd); /* nanogpt_modular.ml:138-164 */
+void malus_gpt_free(void* g);
+int malus_gpt_nparams(void* g);
+int64_t malus_gpt_param(void* g, int i);              /* borrowed */
+int64_t malus_gpt_moment(void* g, int i, int which);  /* borrowed; which 0 = m, 1 = v */
+void malus_gpt_set_fused_optimizer(void* g, int on);
+int64_t malus_gpt_forward_loss(void* g, int64_t toks, int64_t targets); /* nanogpt_modular.ml:75-91 + cross_entropy */
+int64_t malus_gpt_logits(void* g, int64_t toks);
+void malus_gpt_zero_grad(void* g);
+void malus_gpt_optimizer_step(void* g, int64_t t);    /* nanogpt_modular.ml:186-188 */
+int64_t malus_gpt_step(void* g, int64_t toks, int64_t targets, int64_t t); /* nanogpt_modular.ml:167-189 */
+float malus_xor_run(int steps, float lr, uint64_t sigmoid_backward_id, float* loss_at, float* preds,
+                    float* params); /* examples/xor.ml */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MALUS_HIP_H */

@@ -1,0 +1,242 @@
+"""malus_amd — MI355X (gfx950) backend for the malus runtime ABI.
+
+The product is ``libmalus_hip.so``: a C-ABI shared library exporting the
+malus runtime symbols (include/malus_hip.h).  This module loads it with
+ctypes for tests and benchmarks.  There is no CPU fallback: if the library
+is missing or no HIP device is present, calls fail loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libmalus_hip.so"
+
+F32, I32, I64 = 0, 5, 6
+_NP_DTYPE = {F32: np.float32, I32: np.int32, I64: np.int64}
+_TAG_OF = {np.dtype(np.float32): F32, np.dtype(np.int32): I32, np.dtype(np.int64): I64}
+
+# op codes shared with the library
+ADD, SUB, MUL, DIV = 0, 1, 2, 3
+RELU, SIGMOID, TANH, EXP, LOG, SQRT, ABS, GELU = range(8)
+R_SUM, R_MEAN, R_MAX, R_VAR = range(4)
+
+_i64, _i32, _u64, _f32, _sz, _vp = C.c_int64, C.c_int32, C.c_uint64, C.c_float, C.c_size_t, C.c_void_p
+_P = C.POINTER
+
+# name: (restype, argtypes)
+SIGNATURES = {
+    # tensors (metal.rs)
+    "malus_init": (None, []),
+    "tensor_alloc_gpu": (_i64, [_i32, _P(_sz), _sz, _vp]),
+    "tensor_alloc_zeros_gpu": (_i64, [_P(_sz), _sz]),
+    "tensor_alloc_ones_gpu": (_i64, [_P(_sz), _sz]),
+    "tensor_retain": (None, [_i64]),
+    "tensor_release": (None, [_i64]),
+    "tensor_free": (None, [_i64]),
+    "tensor_print": (None, [_i64]),
+    "tensor_len": (_i64, [_i64]),
+    "tensor_ndim": (_i64, [_i64]),
+    "tensor_dim": (_i64, [_i64, _i64]),
+    "malus_tensor_dtype": (_i32, [_i64]),
+    "malus_tensor_shape": (None, [_i64, _P(_sz)]),
+    "malus_tensor_get_f32": (_f32, [_i64, _i64]),
+    "malus_tensor_read": (None, [_i64, _vp, _sz]),
+    "malus_tensor_write": (None, [_i64, _vp, _sz]),
+    "malus_format_f32": (_sz, [_f32, C.c_char_p, _sz]),
+    "gpu_barrier": (None, []),
+    "malus_flush_if_pending": (None, [_i64]),
+    "tensor_is_pending": (C.c_int, [_i64]),
+    "tensor_matmul": (_i64, [_i64, _i64]),
+    "tensor_reshape": (_i64, [_i64, _P(_sz), _sz]),
+    "tensor_permute": (_i64, [_i64, _P(_sz), _sz]),
+    "tensor_causal_mask": (_i64, [_i64]),
+    "tensor_randn": (_i64, [_P(_sz), _sz]),
+    "malus_rand_uniform": (_f32, []),
+    "malus_rand_int": (_i64, [_i64]),
+    "malus_rng_get_counter": (_u64, []),
+    "malus_rng_set_counter": (None, [_u64]),
+    "kernel_dispatch": (_i64, [_u64, _P(_i64), _sz]),
+    "kernel_dispatch_v2": (_i64, [_u64, _P(_i64), _sz, _P(_sz), _P(_sz), _P(_sz), _sz, _i32, _vp, _sz]),
+    "malus_runtime_init": (None, [_P(_u64), _P(C.c_char_p), _sz]),
+    "malus_kernel_is_builtin": (C.c_int, [_u64]),
+    # buffers (buffer.rs)
+    "malus_buffer_i32": (_i64, [_i64]),
+    "malus_buffer_get_i32": (_i64, [_i64, _i64]),
+    "malus_buffer_set_i32": (None, [_i64, _i64, _i64]),
+    "malus_buffer_free": (None, [_i64]),
+    "malus_buffer_freeze_i32": (_i64, [_i64]),
+    # tape (tape.rs)
+    "tape_record_binop": (None, [_i32, _i64, _i64, _i64]),
+    "tape_record_unary": (None, [_i32, _i64, _i64]),
+    "tape_record_reduce": (None, [_i32, _i64, _i64, _i64, _i64]),
+    "tape_record_perm": (None, [_i32, _i64, _i64, _P(_sz), _sz]),
+    "tape_record_layernorm": (None, [_i32, _i64, _i64, _i64, _i64]),
+    "tape_record_cross_entropy": (None, [_i32, _i64, _i64, _i64, _i64]),
+    "tape_record_embedding": (None, [_i32, _i64, _i64, _i64]),
+    "tape_register_leaf": (None, [_i64]),
+    "tape_pause": (None, []),
+    "tape_resume": (None, []),
+    "tape_clear": (None, []),
+    "tape_get_grad": (_i64, [_i64]),
+    "backward": (None, [_i64]),
+    "tape_zero_grad": (None, [_P(_i64), _sz]),
+    "tape_reset": (None, []),
+    "tape_register_backward_fn": (None, [_i32, _sz]),
+    "malus_tape_backward_fn": (_sz, [_i32]),
+    "malus_tape_len": (_sz, []),
+    "malus_tape_registry_lens": (None, [_P(_sz)]),
+    # bench / counters / pool
+    "bench_enable": (None, []),
+    "bench_reset": (None, []),
+    "bench_step_begin": (None, []),
+    "bench_step_end": (None, []),
+    "bench_report": (C.c_int, [_P(C.c_double), _P(C.c_double), _P(C.c_double), _P(_i64)]),
+    "malus_bench_record": (None, [C.c_double]),
+    "malus_cpu_compute_count": (_i64, []),
+    "malus_cpu_compute_reset": (None, []),
+    "malus_rc_counts": (None, [_P(_i64)]),
+    "malus_rc_reset": (None, []),
+    "malus_record_diff": (None, [_f32]),
+    "malus_gradcheck_max_diff": (_f32, []),
+    "malus_gradcheck_reset": (None, []),
+    "malus_pool_stats": (None, [_P(_i64)]),
+    "malus_pool_live_bytes": (_i64, []),
+    "malus_pool_buckets": (_sz, [_P(_sz), _P(_sz), _sz]),
+    "malus_pool_reset": (None, []),
+    "malus_set_mem_budget": (None, [_i64]),
+    "malus_alloc_histogram": (_sz, [_P(_sz), _P(_u64), _sz]),
+    "malus_ktimer_enable": (None, [C.c_int]),
+    "malus_ktimer_collect": (_i64, [C.c_char_p, _P(C.c_double), _P(C.c_double)]),
+    "malus_device_info": (C.c_int, [C.c_char_p, _sz, _P(C.c_int), _P(C.c_int)]),
+    "malus_set_abort_on_error": (None, [C.c_int]),
+    "malus_last_error": (C.c_char_p, []),
+    "malus_clear_error": (None, []),
+    # stdlib host fns
+    "malus_std_broadcast_fwd": (_i64, [_i32, _i64, _i64]),
+    "malus_std_scalar_op": (_i64, [_i32, _i64, _f32, _i32]),
+    "malus_std_scalar_op_dev": (_i64, [_i32, _i64, _i64, _i32]),
+    "malus_std_unary": (_i64, [_i32, _i64]),
+    "malus_std_reduce_fwd": (_i64, [_i32, _i64, _i64, _i64]),
+    "malus_std_reduce_all_sum_fwd": (_i64, [_i64]),
+    "malus_std_softmax_fwd": (_i64, [_i64, _i64]),
+    "malus_std_layernorm_fwd": (_i64, [_i64, _i64, _P(_i64)]),
+    "malus_std_gelu_fwd": (_i64, [_i64]),
+    "malus_std_cross_entropy_fwd": (_i64, [_i64, _i64, _P(_i64)]),
+    "malus_std_embedding_fwd": (_i64, [_i64, _i64]),
+    "malus_std_transpose_2d_fwd": (_i64, [_i64]),
+    "malus_std_permute_3d_fwd": (_i64, [_i64, _i64, _i64, _i64]),
+    "malus_std_permute_nd_fwd": (_i64, [_i64] + [_i64] * 8),
+    "malus_std_scale_fwd": (_i64, [_i64, _f32]),
+    "malus_std_fill_like_fwd": (_i64, [_i64, _f32]),
+    "malus_std_eq_fwd": (_i64, [_i64, _i64]),
+    "malus_std_expand_axis_fwd": (_i64, [_i64, _i64, _i64]),
+    "malus_std_sum_to_shape_bwd": (_i64, [_i64, _i64]),
+    "malus_std_softmax_bwd": (_i64, [_i64, _i64, _i64]),
+    "malus_std_layernorm_bwd": (_i64, [_i64, _i64, _i64, _i64]),
+    "malus_std_gelu_bwd": (_i64, [_i64, _i64]),
+    "malus_std_cross_entropy_bwd": (_i64, [_i64, _i64, _i64]),
+    "malus_std_embedding_bwd": (_i64, [_i64, _i64, _i64]),
+    "malus_std_matmul_bwd_a": (_i64, [_i64, _i64, _i64]),
+    "malus_std_matmul_bwd_b": (_i64, [_i64, _i64, _i64]),
+    "malus_std_sigmoid_bwd": (_i64, [_i64, _i64]),
+    "malus_std_relu_bwd": (_i64, [_i64, _i64]),
+    "malus_std_tanh_bwd": (_i64, [_i64, _i64]),
+    "malus_std_sqrt_bwd": (_i64, [_i64, _i64]),
+    "malus_std_abs_bwd": (_i64, [_i64, _i64]),
+    "malus_std_sum_bwd": (_i64, [_i64, _i64]),
+    "malus_std_adam_l2": (_i64, [_i64, _i64, _i64, _i64, _f32, _f32, _f32, _f32, _f32, _i64, _P(_i64), _P(_i64)]),
+    # workload drivers
+    "malus_gpt_create": (_vp, [C.c_int] * 6 + [_f32] * 5),
+    "malus_gpt_free": (None, [_vp]),
+    "malus_gpt_nparams": (C.c_int, [_vp]),
+    "malus_gpt_param": (_i64, [_vp, C.c_int]),
+    "malus_gpt_moment": (_i64, [_vp, C.c_int, C.c_int]),
+    "malus_gpt_set_fused_optimizer": (None, [_vp, C.c_int]),
+    "malus_gpt_forward_loss": (_i64, [_vp, _i64, _i64]),
+    "malus_gpt_logits": (_i64, [_vp, _i64]),
+    "malus_gpt_zero_grad": (None, [_vp]),
+    "malus_gpt_optimizer_step": (None, [_vp, _i64]),
+    "malus_gpt_step": (_i64, [_vp, _i64, _i64, _i64]),
+    "malus_xor_run": (_f32, [C.c_int, _f32, _u64, _P(_f32), _P(_f32), _P(_f32)]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libmalus_hip.so (built in-tree by ``python -m malus_amd.build``)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m malus_amd.build` (no CPU fallback exists)")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def sizes(vals) -> "C.Array":
+    vals = list(vals)
+    return (_sz * max(1, len(vals)))(*vals)
+
+
+def handles(vals) -> "C.Array":
+    vals = list(vals)
+    return (_i64 * max(1, len(vals)))(*vals)
+
+
+class Runtime:
+    """Convenience wrapper over the C ABI for tests and benchmarks."""
+
+    def __init__(self):
+        self.L = lib()
+        self.L.malus_init()
+
+    # -- tensors --------------------------------------------------------------
+    def tensor(self, arr) -> int:
+        a = np.ascontiguousarray(arr)
+        if a.dtype not in _TAG_OF:
+            a = a.astype(np.float32)
+        tag = _TAG_OF[a.dtype]
+        shape = a.shape if a.ndim else (1,)
+        return self.L.tensor_alloc_gpu(tag, sizes(shape), len(shape), a.ctypes.data_as(_vp))
+
+    def shape(self, h: int) -> tuple:
+        nd = self.L.tensor_ndim(h)
+        buf = (_sz * 8)()
+        self.L.malus_tensor_shape(h, buf)
+        return tuple(buf[i] for i in range(nd))
+
+    def numpy(self, h: int) -> np.ndarray:
+        tag = self.L.malus_tensor_dtype(h)
+        shp = self.shape(h)
+        out = np.empty(shp, dtype=_NP_DTYPE[tag])
+        if out.size:
+            self.L.malus_tensor_read(h, out.ctypes.data_as(_vp), out.nbytes)
+        return out
+
+    def free(self, *hs):
+        for h in hs:
+            if h:
+                self.L.tensor_free(h)
+
+    def last_error(self) -> str:
+        e = self.L.malus_last_error()
+        return e.decode() if e else ""
+
+
+def device_count_hint() -> int:
+    """Number of visible GPUs without initializing HIP (for test gating)."""
+    try:
+        import torch  # noqa: F401  (torch.cuda.device_count does not initialize HIP on this image)
+
+        return int(torch.cuda.device_count())
+    except Exception:
+        return 1 if os.path.exists("/dev/kfd") else 0

@@ -1,0 +1,94 @@
+// Internal glue between the C ABI entry points: error mode, tape hooks and
+// the stdlib host functions other translation units call directly.
+#pragma once
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace malus {
+
+// Raised by fail() when the library runs in "return" error mode (tests);
+// in the default abort mode fail() prints "malus: ..." and aborts, which is
+// the reference's panic-only model (docs/adr/0006-panic-only-error-model.md).
+struct MalusError : std::runtime_error {
+  explicit MalusError(const char* m) : std::runtime_error(m) {}
+};
+void set_last_error(const char* msg);
+
+// tape.cpp
+void tape_on_release(int64_t handle);
+void register_default_backward_fns();
+std::vector<size_t> tape_normalize_perm(const std::vector<size_t>& raw, size_t rank);
+
+}  // namespace malus
+
+#define API_TRY try {
+#define API_CATCH(...)                                   \
+  }                                                      \
+  catch (const ::malus::MalusError& e) {                 \
+    ::malus::set_last_error(e.what());                   \
+    return __VA_ARGS__;                                  \
+  }
+
+// Stdlib host functions (stdlib.cpp), exported with a malus_std_ prefix.
+extern "C" {
+int64_t malus_std_broadcast_fwd(int32_t op, int64_t a, int64_t b);
+int64_t malus_std_broadcast_add_fwd(int64_t a, int64_t b);
+int64_t malus_std_broadcast_sub_fwd(int64_t a, int64_t b);
+int64_t malus_std_broadcast_mul_fwd(int64_t a, int64_t b);
+int64_t malus_std_broadcast_div_fwd(int64_t a, int64_t b);
+int64_t malus_std_scalar_op(int32_t op, int64_t a, float s, int32_t scalar_on_right);
+int64_t malus_std_scalar_op_dev(int32_t op, int64_t a, int64_t s1, int32_t scalar_on_right);
+int64_t malus_std_unary(int32_t op, int64_t x);
+int64_t malus_std_reduce_fwd(int32_t op, int64_t x, int64_t axis, int64_t keepdim);
+int64_t malus_std_reduce_all_sum_fwd(int64_t x);
+int64_t malus_std_softmax_fwd(int64_t x, int64_t axis);
+int64_t malus_std_layernorm_fwd(int64_t x, int64_t axis, int64_t* var_out);
+int64_t malus_std_gelu_fwd(int64_t x);
+int64_t malus_std_cross_entropy_fwd(int64_t logits, int64_t targets, int64_t* probs_out);
+int64_t malus_std_embedding_fwd(int64_t weight, int64_t indices);
+int64_t malus_std_transpose_2d_fwd(int64_t x);
+int64_t malus_std_permute_3d_fwd(int64_t x, int64_t p0, int64_t p1, int64_t p2);
+int64_t malus_std_permute_nd_fwd(int64_t x, int64_t p0, int64_t p1, int64_t p2, int64_t p3, int64_t p4, int64_t p5,
+                                 int64_t p6, int64_t p7);
+int64_t malus_std_scale_fwd(int64_t x, float c);
+int64_t malus_std_fill_like_fwd(int64_t x, float c);
+int64_t malus_std_eq_fwd(int64_t a, int64_t b);
+int64_t malus_std_expand_axis_fwd(int64_t small, int64_t x_template, int64_t axis);
+int64_t malus_std_sum_to_shape_bwd(int64_t dout, int64_t target);
+int64_t malus_std_add_bwd_a(int64_t dout, int64_t a);
+int64_t malus_std_add_bwd_b(int64_t dout, int64_t b);
+int64_t malus_std_sub_bwd_a(int64_t dout, int64_t a);
+int64_t malus_std_sub_bwd_b(int64_t dout, int64_t b);
+int64_t malus_std_mul_bwd_a(int64_t dout, int64_t a, int64_t b);
+int64_t malus_std_mul_bwd_b(int64_t dout, int64_t a, int64_t b);
+int64_t malus_std_div_bwd_a(int64_t dout, int64_t a, int64_t b);
+int64_t malus_std_div_bwd_b(int64_t dout, int64_t a, int64_t b);
+int64_t malus_std_sigmoid_bwd(int64_t s, int64_t dout);
+int64_t malus_std_relu_bwd(int64_t x, int64_t dout);
+int64_t malus_std_tanh_bwd(int64_t t, int64_t dout);
+int64_t malus_std_sqrt_bwd(int64_t s, int64_t dout);
+int64_t malus_std_abs_bwd(int64_t x, int64_t dout);
+int64_t malus_std_sum_bwd(int64_t x, int64_t dout);
+int64_t malus_std_reduce_sum_axis_bwd(int64_t x, int64_t dout, int64_t axis);
+int64_t malus_std_reduce_mean_axis_bwd(int64_t x, int64_t dout, int64_t axis);
+int64_t malus_std_reduce_max_axis_bwd(int64_t x, int64_t y, int64_t dout, int64_t axis);
+int64_t malus_std_reduce_var_axis_bwd(int64_t x, int64_t dout, int64_t axis);
+int64_t malus_std_softmax_bwd(int64_t s, int64_t dout, int64_t axis);
+int64_t malus_std_layernorm_bwd(int64_t y, int64_t var, int64_t dout, int64_t axis);
+int64_t malus_std_gelu_bwd(int64_t x, int64_t dout);
+int64_t malus_std_cross_entropy_bwd(int64_t probs, int64_t targets, int64_t dout);
+int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout);
+int64_t malus_std_matmul_bwd_a(int64_t a, int64_t b, int64_t dout);
+int64_t malus_std_matmul_bwd_b(int64_t a, int64_t b, int64_t dout);
+int64_t malus_std_adam_l2(int64_t p, int64_t g, int64_t m, int64_t v, float lr, float b1, float b2, float eps, float wd,
+                          int64_t t, int64_t* m_out, int64_t* v_out);
+
+int64_t tensor_matmul(int64_t a, int64_t b);
+int64_t tensor_permute(int64_t h, const size_t* perm, size_t ndims);
+int64_t tensor_reshape(int64_t h, const size_t* dims, size_t ndim);
+void tape_register_backward_fn(int32_t slot, size_t fnptr);
+size_t malus_tape_backward_fn(int32_t slot);
+}

@@ -1,0 +1,168 @@
+// Shared runtime types for libmalus_hip: tensor handles, the device pool,
+// stream ordering, error reporting, and the host-side launch wrappers of
+// every hand-written gfx950 kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+namespace malus {
+
+// ---- dtype tags (metal.rs:26-50; the numbering is part of the ABI) ----------
+enum Dtype : int32_t {
+  F32 = 0, F16 = 1, BF16 = 2, I8 = 3, I16 = 4, I32 = 5, I64 = 6,
+  U8 = 7, U16 = 8, U32 = 9, U64 = 10
+};
+size_t dtype_size(int32_t tag);  // aborts on unknown tags
+
+constexpr int kMaxRank = 8;
+
+// Device allocation shared by a tensor and its reshape aliases
+// (metal.rs:262-276 PoolState + the MTLBuffer it guards).
+struct Storage {
+  void* ptr = nullptr;
+  size_t bytes = 0;              // bucketed allocation size
+  std::atomic<int> aliases{0};   // TensorBuffers referencing this storage
+};
+
+// One tensor handle (metal.rs:280-296 TensorBuffer).  The i64 handle the ABI
+// passes around is a TensorBuffer*.
+struct TensorBuffer {
+  Storage* st = nullptr;
+  int32_t dtype = F32;
+  size_t len = 0;
+  int ndim = 0;
+  size_t shape[kMaxRank] = {0};
+  std::atomic<int64_t> rc{1};
+  uint64_t write_seq = 0;        // stream sequence of the last GPU write (0 = ready)
+
+  float* f32() const { return static_cast<float*>(st->ptr); }
+  int32_t* i32() const { return static_cast<int32_t*>(st->ptr); }
+  void* data() const { return st->ptr; }
+  size_t bytes() const { return len * dtype_size(dtype); }
+};
+
+inline TensorBuffer* T(int64_t h) { return reinterpret_cast<TensorBuffer*>(h); }
+inline int64_t H(TensorBuffer* t) { return reinterpret_cast<int64_t>(t); }
+
+// ---- errors (ADR-0006 panic-only model: "malus: ..." then abort) -----------
+[[noreturn]] void fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void check_hip(hipError_t e, const char* what);
+#define MALUS_HIP(x) ::malus::check_hip((x), #x)
+std::string shape_str(const TensorBuffer* t);
+
+// ---- context ---------------------------------------------------------------
+void ensure_init();
+hipStream_t stream();
+// Marks one enqueued GPU operation; returns its sequence number.  Every op
+// that writes a tensor stamps that tensor's write_seq with it.
+uint64_t enqueue_mark(const char* op_name);
+void flush_if_pending(TensorBuffer* t);   // metal.rs:244-252
+void sync_all();                          // gpu_barrier body
+
+// ---- allocation ------------------------------------------------------------
+// Allocate an uninitialized tensor (kernels must write every element).
+TensorBuffer* alloc_tensor(int32_t dtype, const size_t* shape, int ndim);
+TensorBuffer* alloc_like(const TensorBuffer* t);
+TensorBuffer* alloc_f32(std::initializer_list<size_t> shape);
+TensorBuffer* make_alias(TensorBuffer* src, const size_t* shape, int ndim);  // reshape_to
+void release(TensorBuffer* t);
+void retain(TensorBuffer* t);
+// Scratch device memory from the same pool, released with pool_free.
+void* pool_alloc(size_t bytes, size_t* bucket_out);
+void pool_free(void* p, size_t bucket);
+
+// Host -> device copy on the runtime stream via pinned staging.
+void upload(void* dst, const void* src, size_t bytes);
+// Device -> host copy after waiting for the producing work.
+void download(void* dst, const TensorBuffer* t, size_t bytes);
+
+// Device-side error flag (index out of range in gathers); checked at flush.
+int32_t* device_error_flag();
+
+// ---- RNG (metal.rs:1690-1759) ----------------------------------------------
+void philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+uint64_t rng_next_call();
+
+// ---- kernel launch wrappers (k_*.hip) --------------------------------------
+namespace k {
+enum BinOp : int { ADD = 0, SUB = 1, MUL = 2, DIV = 3 };
+enum UnOp : int { RELU = 0, SIGMOID, TANH, EXP, LOG, SQRT, ABS, GELU, NEG_UNUSED };
+enum UnBwd : int { B_SIGMOID = 0, B_RELU, B_TANH, B_SQRT, B_ABS, B_GELU, B_EXP, B_LOG };
+
+struct BcastDesc {          // NumPy right-aligned broadcast of (p op q) into out
+  int ndim;
+  uint32_t out_shape[kMaxRank];
+  uint32_t p_stride[kMaxRank];  // 0 where p is broadcast
+  uint32_t q_stride[kMaxRank];
+};
+
+// out[i] = p[i] op q[i]
+void binary_same(int op, const float* p, const float* q, float* out, size_t n, hipStream_t s);
+// out = p op q with q broadcast along rows: q_flat = i % qn (trailing-block broadcast)
+void binary_rowbcast(int op, const float* p, const float* q, float* out, size_t n, size_t qn, hipStream_t s);
+// out = p op q with p broadcast: p_flat = i % pn
+void binary_rowbcast_rev(int op, const float* p, size_t pn, const float* q, float* out, size_t n, hipStream_t s);
+// out = p op q[0] (qdev != null: scalar read from device) or p op qval
+void binary_scalar(int op, const float* p, const float* qdev, float qval, bool scalar_on_right,
+                   float* out, size_t n, hipStream_t s);
+void binary_general(int op, const float* p, const float* q, float* out, size_t n, const BcastDesc& d, hipStream_t s);
+void unary(int op, const float* x, float* out, size_t n, hipStream_t s);
+void unary_bwd(int op, const float* xy, const float* dout, float* out, size_t n, hipStream_t s);
+void fill(float* out, float v, size_t n, hipStream_t s);
+void fill_bytes0(void* out, size_t bytes, hipStream_t s);
+void fill_from_device(float* out, const float* v, size_t n, hipStream_t s);
+void eq(const float* a, const float* b, float* out, size_t n, hipStream_t s);
+void rsqrt_eps(const float* v, float eps, float* out, size_t n, hipStream_t s);
+void copy(const void* src, void* dst, size_t bytes, hipStream_t s);
+void causal_mask(float* out, size_t t, hipStream_t s);
+void iota_rows(int32_t* out, size_t rows, size_t t, hipStream_t s);
+
+// Axis reductions over a contiguous [outer, axis, inner] view.
+enum RedOp : int { R_SUM = 0, R_MEAN = 1, R_MAX = 2, R_VAR = 3 };
+void reduce_axis(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
+// Broadcast [outer, inner] back to [outer, axis, inner] (expand_axis).
+void expand_axis(const float* small, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
+
+// Row ops over [outer, axis, inner] (inner may be > 1).
+void softmax(const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
+void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
+void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s);
+void layernorm_bwd(const float* y, const float* var, const float* dout, float* dx, size_t outer, size_t axis, size_t inner,
+                   float eps, hipStream_t s);
+// probs = softmax(logits) rows; nll[i] = -log(probs[i, t_i]).
+void ce_fwd(const float* logits, const int32_t* tgt, float* probs, float* nll, size_t n, size_t v, int32_t* err, hipStream_t s);
+// scale = dout[0] / n when dout is given (read on the device), else scale_host.
+void ce_bwd(const float* probs, const int32_t* tgt, const float* dout, float scale_host, float* dx, size_t n, size_t v,
+            hipStream_t s);
+// nll[i] = -log(probs[i, t_i])  (cross_entropy.ml:13-16)
+void nll_gather(const float* probs, const int32_t* tgt, float* nll, size_t n, size_t v, int32_t* err, hipStream_t s);
+
+// Gathers / index ops.
+void embedding(const float* w, const int32_t* idx, float* out, size_t t, size_t v, size_t d, int32_t* err, hipStream_t s);
+void embedding_bwd(const float* dout, const int32_t* idx, float* dw, size_t t, size_t v, size_t d, hipStream_t s);
+void permute(const float* x, float* out, int ndim, const size_t* in_shape, const size_t* perm, hipStream_t s);
+
+// Batched GEMM: C[b] = op(A[b]) @ op(B[b]); transA: A stored [K,M]; transB: B stored [N,K].
+// strideA/B/C are element strides between batches (0 broadcasts).
+void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
+          long strideA, long strideB, long strideC, hipStream_t s);
+
+// Fused Adam + L2 update (examples/nanogpt_modular.ml:97-108 op order).
+void adam_l2(const float* p, const float* g, const float* m, const float* v, float* p_out, float* m_out, float* v_out,
+             size_t n, float lr, float b1, float b2, float omb1, float omb2, float bc1, float bc2, float eps, float wd,
+             hipStream_t s);
+}  // namespace k
+
+// ---- per-kernel timing (bench instrumentation) ------------------------------
+struct KTimer;
+KTimer* ktimer_begin(const char* cls);     // null when timing is off
+void ktimer_end(KTimer* t, double algorithmic_units);
+
+}  // namespace malus

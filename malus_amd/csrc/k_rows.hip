@@ -1,0 +1,422 @@
+// Row kernels: softmax, layernorm, cross-entropy (forward and VJP).
+// Contiguous rows (inner == 1) up to 4096 wide run one wave64 per row with
+// the whole row held in registers: one HBM read per input element and one
+// write per output element, reductions by wave shuffles.  Other shapes
+// (reductions over a non-last axis, rows wider than 4096) use a sequential
+// per-(outer, inner) kernel that follows the reference loops directly.
+#include "common.h"
+
+namespace malus {
+namespace k {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kRowsPerBlock = 4;  // 256 threads
+
+__device__ __forceinline__ float wsum(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ float wmax(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// Register tile of one row: NV float4 chunks per lane.  Element e of the
+// lane's tile is column col(e).  VEC: chunk j covers columns 4*(lane+64j)..+3;
+// scalar: element e is column lane + 64*e.
+template <int NV, bool VEC>
+struct RowTile {
+  float v[NV * 4];
+  __device__ __forceinline__ static uint32_t col(int e, int lane) {
+    return VEC ? 4u * (uint32_t)(lane + kWave * (e / 4)) + (uint32_t)(e % 4) : (uint32_t)(lane + kWave * e);
+  }
+  __device__ __forceinline__ void load(const float* __restrict__ row, uint32_t axis, int lane, float pad) {
+    if (VEC) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        uint32_t c4 = (uint32_t)(lane + kWave * j);
+        if (4 * c4 < axis) {
+          float4 t = reinterpret_cast<const float4*>(row)[c4];
+          v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+        } else {
+          v[4 * j] = v[4 * j + 1] = v[4 * j + 2] = v[4 * j + 3] = pad;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < NV * 4; ++e) {
+        uint32_t c = col(e, lane);
+        v[e] = c < axis ? row[c] : pad;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(float* __restrict__ row, uint32_t axis, int lane) const {
+    if (VEC) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        uint32_t c4 = (uint32_t)(lane + kWave * j);
+        if (4 * c4 < axis) reinterpret_cast<float4*>(row)[c4] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < NV * 4; ++e) {
+        uint32_t c = col(e, lane);
+        if (c < axis) row[c] = v[e];
+      }
+    }
+  }
+  __device__ __forceinline__ bool valid(int e, int lane, uint32_t axis) const { return col(e, lane) < axis; }
+};
+
+// softmax_axis_cpu (metal.rs:1439-1467): m = max, e = exp(x - m), s = sum e, y = e / s
+template <int NV, bool VEC>
+__global__ __launch_bounds__(256) void k_softmax_rows(const float* __restrict__ x, float* __restrict__ y, size_t rows,
+                                                      uint32_t axis) {
+  const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (row >= rows) return;
+  RowTile<NV, VEC> t;
+  t.load(x + row * axis, axis, lane, -INFINITY);
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) m = fmaxf(m, t.v[e]);
+  m = wmax(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) {
+    float ex = t.valid(e, lane, axis) ? expf(t.v[e] - m) : 0.0f;
+    t.v[e] = ex;
+    s += ex;
+  }
+  s = wsum(s);
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) t.v[e] = t.v[e] / s;
+  t.store(y + row * axis, axis, lane);
+}
+
+// tape.rs:1150-1161: dx = s * (dout - sum(dout * s))
+template <int NV, bool VEC>
+__global__ __launch_bounds__(256) void k_softmax_bwd_rows(const float* __restrict__ y, const float* __restrict__ dout,
+                                                          float* __restrict__ dx, size_t rows, uint32_t axis) {
+  const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (row >= rows) return;
+  RowTile<NV, VEC> s, d;
+  s.load(y + row * axis, axis, lane, 0.0f);
+  d.load(dout + row * axis, axis, lane, 0.0f);
+  float acc = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) { float p = d.v[e] * s.v[e]; acc += p; }
+  acc = wsum(acc);
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) { float diff = d.v[e] - acc; s.v[e] = s.v[e] * diff; }
+  s.store(dx + row * axis, axis, lane);
+}
+
+// tensor_layernorm_axis (metal.rs:1486-1533): y = (x - mu) / sqrt(var + eps)
+template <int NV, bool VEC>
+__global__ __launch_bounds__(256) void k_layernorm_rows(const float* __restrict__ x, float* __restrict__ y,
+                                                        float* __restrict__ var, size_t rows, uint32_t axis, float eps) {
+  const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (row >= rows) return;
+  RowTile<NV, VEC> t;
+  t.load(x + row * axis, axis, lane, 0.0f);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) s += t.v[e];
+  s = wsum(s);
+  const float mu = s / (float)axis;
+  float q = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) {
+    if (t.valid(e, lane, axis)) { float dd = t.v[e] - mu; q += dd * dd; }
+  }
+  q = wsum(q);
+  const float va = q / (float)axis;
+  const float sigma = sqrtf(va + eps);
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) t.v[e] = (t.v[e] - mu) / sigma;
+  t.store(y + row * axis, axis, lane);
+  if (lane == 0 && var) var[row] = va;
+}
+
+// tape.rs:1162-1186: dx = ((dy - mean(dy)) - y * mean(dy*y)) * (1 / sqrt(var + eps))
+template <int NV, bool VEC>
+__global__ __launch_bounds__(256) void k_layernorm_bwd_rows(const float* __restrict__ y, const float* __restrict__ var,
+                                                            const float* __restrict__ dout, float* __restrict__ dx,
+                                                            size_t rows, uint32_t axis, float eps) {
+  const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (row >= rows) return;
+  RowTile<NV, VEC> yt, dt;
+  yt.load(y + row * axis, axis, lane, 0.0f);
+  dt.load(dout + row * axis, axis, lane, 0.0f);
+  float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) { s1 += dt.v[e]; float p = dt.v[e] * yt.v[e]; s2 += p; }
+  s1 = wsum(s1);
+  s2 = wsum(s2);
+  const float dy_mean = s1 / (float)axis;
+  const float dyy_mean = s2 / (float)axis;
+  const float inv_sigma = 1.0f / sqrtf(var[row] + eps);
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) {
+    float y_term = yt.v[e] * dyy_mean;
+    float tmp = dt.v[e] - dy_mean;
+    float numer = tmp - y_term;
+    yt.v[e] = numer * inv_sigma;
+  }
+  yt.store(dx + row * axis, axis, lane);
+}
+
+// cross_entropy.ml:18-28 / metal.rs:1555-1598: probs = softmax(logits, 1),
+// nll[i] = -log(probs[i, t_i]) read back from the rounded probability.
+template <int NV, bool VEC>
+__global__ __launch_bounds__(256) void k_ce_fwd_rows(const float* __restrict__ logits, const int32_t* __restrict__ tgt,
+                                                     float* __restrict__ probs, float* __restrict__ nll, size_t rows,
+                                                     uint32_t axis, int32_t* __restrict__ err) {
+  const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (row >= rows) return;
+  RowTile<NV, VEC> t;
+  t.load(logits + row * axis, axis, lane, -INFINITY);
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) m = fmaxf(m, t.v[e]);
+  m = wmax(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) {
+    float ex = t.valid(e, lane, axis) ? expf(t.v[e] - m) : 0.0f;
+    t.v[e] = ex;
+    s += ex;
+  }
+  s = wsum(s);
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) t.v[e] = t.v[e] / s;
+  t.store(probs + row * axis, axis, lane);
+  const int32_t tg = tgt[row];
+  if (tg < 0 || (uint32_t)tg >= axis) {
+    if (lane == 0) { nll[row] = NAN; *err = 2; }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e)
+    if (t.col(e, lane) == (uint32_t)tg) nll[row] = -logf(t.v[e]);
+}
+
+// transformer_bwd.ml:57-65 / tape.rs:1200-1214: (p - 1{j == t}) * (dout[0] / N)
+__global__ __launch_bounds__(256) void k_ce_bwd(const float* __restrict__ probs, const int32_t* __restrict__ tgt,
+                                                const float* __restrict__ dout, float scale_host, float* __restrict__ dx,
+                                                size_t n, uint32_t v) {
+  const float scale = dout ? dout[0] / (float)n : scale_host;
+  const size_t total = n * v, stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t f = (size_t)blockIdx.x * blockDim.x + threadIdx.x; f < total; f += stride) {
+    size_t i = f / v;
+    uint32_t j = (uint32_t)(f % v);
+    float g = probs[f];
+    if ((int32_t)j == tgt[i]) g = g - 1.0f;
+    dx[f] = g * scale;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_nll_gather(const float* __restrict__ probs, const int32_t* __restrict__ tgt,
+                                                    float* __restrict__ nll, size_t n, uint32_t v, int32_t* __restrict__ err) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int32_t t = tgt[i];
+  if (t < 0 || (uint32_t)t >= v) { nll[i] = NAN; *err = 2; return; }
+  nll[i] = -logf(probs[i * v + (uint32_t)t]);
+}
+
+// ---- sequential fallbacks: one thread per (outer, inner) ------------------
+__global__ void k_softmax_seq(const float* __restrict__ x, float* __restrict__ y, size_t outer, size_t axis, size_t inner) {
+  size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= outer * inner) return;
+  size_t o = id / inner, i = id % inner;
+  const float* xb = x + o * axis * inner + i;
+  float* yb = y + o * axis * inner + i;
+  float mx = -INFINITY;
+  for (size_t k = 0; k < axis; ++k) if (xb[k * inner] > mx) mx = xb[k * inner];
+  float sum = 0.0f;
+  for (size_t k = 0; k < axis; ++k) { float e = expf(xb[k * inner] - mx); yb[k * inner] = e; sum += e; }
+  for (size_t k = 0; k < axis; ++k) yb[k * inner] = yb[k * inner] / sum;
+}
+
+__global__ void k_softmax_bwd_seq(const float* __restrict__ s, const float* __restrict__ d, float* __restrict__ dx,
+                                  size_t outer, size_t axis, size_t inner) {
+  size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= outer * inner) return;
+  size_t base = (id / inner) * axis * inner + id % inner;
+  float acc = 0.0f;
+  for (size_t k = 0; k < axis; ++k) { float p = d[base + k * inner] * s[base + k * inner]; acc += p; }
+  for (size_t k = 0; k < axis; ++k) { float diff = d[base + k * inner] - acc; dx[base + k * inner] = s[base + k * inner] * diff; }
+}
+
+__global__ void k_layernorm_seq(const float* __restrict__ x, float* __restrict__ y, float* __restrict__ var, size_t outer,
+                                size_t axis, size_t inner, float eps) {
+  size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= outer * inner) return;
+  size_t base = (id / inner) * axis * inner + id % inner;
+  float mu = 0.0f;
+  for (size_t k = 0; k < axis; ++k) mu += x[base + k * inner];
+  mu = mu / (float)axis;
+  float va = 0.0f;
+  for (size_t k = 0; k < axis; ++k) { float d = x[base + k * inner] - mu; va += d * d; }
+  va = va / (float)axis;
+  float sigma = sqrtf(va + eps);
+  if (var) var[id] = va;
+  for (size_t k = 0; k < axis; ++k) y[base + k * inner] = (x[base + k * inner] - mu) / sigma;
+}
+
+__global__ void k_layernorm_bwd_seq(const float* __restrict__ y, const float* __restrict__ var, const float* __restrict__ d,
+                                    float* __restrict__ dx, size_t outer, size_t axis, size_t inner, float eps) {
+  size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= outer * inner) return;
+  size_t base = (id / inner) * axis * inner + id % inner;
+  float inv_sigma = 1.0f / sqrtf(var[id] + eps);
+  float s1 = 0.0f, s2 = 0.0f;
+  for (size_t k = 0; k < axis; ++k) s1 += d[base + k * inner];
+  for (size_t k = 0; k < axis; ++k) { float p = d[base + k * inner] * y[base + k * inner]; s2 += p; }
+  float dym = s1 / (float)axis, dyym = s2 / (float)axis;
+  for (size_t k = 0; k < axis; ++k) {
+    float y_term = y[base + k * inner] * dyym;
+    float tmp = d[base + k * inner] - dym;
+    float numer = tmp - y_term;
+    dx[base + k * inner] = numer * inv_sigma;
+  }
+}
+
+__global__ void k_ce_fwd_seq(const float* __restrict__ logits, const int32_t* __restrict__ tgt, float* __restrict__ probs,
+                             float* __restrict__ nll, size_t n, size_t v, int32_t* __restrict__ err) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float* x = logits + i * v;
+  float* p = probs + i * v;
+  float mx = -INFINITY;
+  for (size_t k = 0; k < v; ++k) if (x[k] > mx) mx = x[k];
+  float sum = 0.0f;
+  for (size_t k = 0; k < v; ++k) { float e = expf(x[k] - mx); p[k] = e; sum += e; }
+  for (size_t k = 0; k < v; ++k) p[k] = p[k] / sum;
+  int32_t t = tgt[i];
+  if (t < 0 || (size_t)t >= v) { nll[i] = NAN; *err = 2; return; }
+  nll[i] = -logf(p[t]);
+}
+
+// Launch helper: choose the register-tile width for a row length.
+template <template <int, bool> class KSel, class Launch>
+void row_dispatch(uint32_t axis, Launch launch) {
+  const bool vec = (axis % 4) == 0;
+  // elements per lane needed: ceil(axis / 64)
+  uint32_t per_lane = (axis + 63) / 64;
+  int nv = per_lane <= 4 ? 1 : per_lane <= 8 ? 2 : per_lane <= 16 ? 4 : per_lane <= 32 ? 8 : 16;
+#define MALUS_ROW_CASE(NV)                                       \
+  case NV:                                                       \
+    if (vec) launch(KSel<NV, true>{}); else launch(KSel<NV, false>{}); \
+    break;
+  switch (nv) {
+    MALUS_ROW_CASE(1)
+    MALUS_ROW_CASE(2)
+    MALUS_ROW_CASE(4)
+    MALUS_ROW_CASE(8)
+    MALUS_ROW_CASE(16)
+  }
+#undef MALUS_ROW_CASE
+}
+
+template <int NV, bool VEC> struct SelSoftmax { static constexpr auto fn = k_softmax_rows<NV, VEC>; };
+template <int NV, bool VEC> struct SelSoftmaxBwd { static constexpr auto fn = k_softmax_bwd_rows<NV, VEC>; };
+template <int NV, bool VEC> struct SelLN { static constexpr auto fn = k_layernorm_rows<NV, VEC>; };
+template <int NV, bool VEC> struct SelLNBwd { static constexpr auto fn = k_layernorm_bwd_rows<NV, VEC>; };
+template <int NV, bool VEC> struct SelCE { static constexpr auto fn = k_ce_fwd_rows<NV, VEC>; };
+
+constexpr uint32_t kMaxRowAxis = 4096;
+inline unsigned row_grid(size_t rows) { return (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock); }
+inline unsigned seq_grid(size_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+void softmax(const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {
+  if (!outer || !axis || !inner) return;
+  if (inner == 1 && axis <= kMaxRowAxis) {
+    row_dispatch<SelSoftmax>((uint32_t)axis, [&](auto sel) {
+      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(x, out, outer, (uint32_t)axis);
+    });
+  } else {
+    k_softmax_seq<<<seq_grid(outer * inner), 256, 0, s>>>(x, out, outer, axis, inner);
+  }
+  MALUS_HIP(hipGetLastError());
+}
+
+void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {
+  if (!outer || !axis || !inner) return;
+  if (inner == 1 && axis <= kMaxRowAxis) {
+    row_dispatch<SelSoftmaxBwd>((uint32_t)axis, [&](auto sel) {
+      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(y, dout, out, outer, (uint32_t)axis);
+    });
+  } else {
+    k_softmax_bwd_seq<<<seq_grid(outer * inner), 256, 0, s>>>(y, dout, out, outer, axis, inner);
+  }
+  MALUS_HIP(hipGetLastError());
+}
+
+void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s) {
+  if (!outer || !axis || !inner) return;
+  if (inner == 1 && axis <= kMaxRowAxis) {
+    row_dispatch<SelLN>((uint32_t)axis, [&](auto sel) {
+      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(x, y, var, outer, (uint32_t)axis, eps);
+    });
+  } else {
+    k_layernorm_seq<<<seq_grid(outer * inner), 256, 0, s>>>(x, y, var, outer, axis, inner, eps);
+  }
+  MALUS_HIP(hipGetLastError());
+}
+
+void layernorm_bwd(const float* y, const float* var, const float* dout, float* dx, size_t outer, size_t axis, size_t inner,
+                   float eps, hipStream_t s) {
+  if (!outer || !axis || !inner) return;
+  if (inner == 1 && axis <= kMaxRowAxis) {
+    row_dispatch<SelLNBwd>((uint32_t)axis, [&](auto sel) {
+      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(y, var, dout, dx, outer, (uint32_t)axis, eps);
+    });
+  } else {
+    k_layernorm_bwd_seq<<<seq_grid(outer * inner), 256, 0, s>>>(y, var, dout, dx, outer, axis, inner, eps);
+  }
+  MALUS_HIP(hipGetLastError());
+}
+
+void ce_fwd(const float* logits, const int32_t* tgt, float* probs, float* nll, size_t n, size_t v, int32_t* err,
+            hipStream_t s) {
+  if (!n || !v) return;
+  if (v <= kMaxRowAxis) {
+    row_dispatch<SelCE>((uint32_t)v, [&](auto sel) {
+      decltype(sel)::fn<<<row_grid(n), 256, 0, s>>>(logits, tgt, probs, nll, n, (uint32_t)v, err);
+    });
+  } else {
+    k_ce_fwd_seq<<<seq_grid(n), 256, 0, s>>>(logits, tgt, probs, nll, n, v, err);
+  }
+  MALUS_HIP(hipGetLastError());
+}
+
+void ce_bwd(const float* probs, const int32_t* tgt, const float* dout, float scale_host, float* dx, size_t n, size_t v,
+            hipStream_t s) {
+  size_t total = n * v;
+  if (!total) return;
+  size_t blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  k_ce_bwd<<<(unsigned)blocks, 256, 0, s>>>(probs, tgt, dout, scale_host, dx, n, (uint32_t)v);
+  MALUS_HIP(hipGetLastError());
+}
+
+void nll_gather(const float* probs, const int32_t* tgt, float* nll, size_t n, size_t v, int32_t* err, hipStream_t s) {
+  if (!n) return;
+  k_nll_gather<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(probs, tgt, nll, n, (uint32_t)v, err);
+  MALUS_HIP(hipGetLastError());
+}
+
+}  // namespace k
+}  // namespace malus

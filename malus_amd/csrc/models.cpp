@@ -1,0 +1,413 @@
+// Workload drivers: the runtime-call sequences the Cranelift JIT issues for
+// examples/xor.ml and examples/nanogpt_modular.ml, replayed in C++ through
+// the same C ABI (tensor_matmul, the stdlib host fns, tape_record_*,
+// backward, tape_get_grad ...).  Op order, tape records and operand order
+// follow codegen-cpu's lowering (lib.rs:1525-1850, 2765-3082); the
+// nanoGPT driver is generalized to L blocks and H heads for the C4/C5
+// configurations.
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "api.h"
+#include "common.h"
+
+extern "C" {
+int64_t tensor_alloc_gpu(int32_t dtype, const size_t* shape, size_t ndim, const void* data);
+int64_t tensor_alloc_ones_gpu(const size_t* shape, size_t ndim);
+int64_t tensor_randn(const size_t* shape, size_t ndim);
+int64_t tensor_causal_mask(int64_t t);
+void tensor_release(int64_t h);
+void tensor_retain(int64_t h);
+float malus_tensor_get_f32(int64_t h, int64_t i);
+void malus_tensor_read(int64_t h, void* dst, size_t bytes);
+void tape_record_binop(int32_t op, int64_t a, int64_t b, int64_t out);
+void tape_record_unary(int32_t op, int64_t x, int64_t out);
+void tape_record_reduce(int32_t op, int64_t x, int64_t out, int64_t axis, int64_t keepdim);
+void tape_record_perm(int32_t op, int64_t x, int64_t out, const size_t* dims, size_t ndims);
+void tape_record_layernorm(int32_t op, int64_t x, int64_t out, int64_t var_h, int64_t axis);
+void tape_record_cross_entropy(int32_t op, int64_t logits, int64_t out, int64_t softmax_h, int64_t targets);
+void tape_record_embedding(int32_t op, int64_t weight, int64_t indices, int64_t out);
+void tape_register_leaf(int64_t h);
+void tape_zero_grad(const int64_t* handles, size_t count);
+int64_t tape_get_grad(int64_t h);
+void backward(int64_t loss);
+void tape_pause(void);
+void tape_resume(void);
+int64_t kernel_dispatch(uint64_t id, const int64_t* handles, size_t count);
+}
+
+using namespace malus;
+
+namespace {
+
+enum Op : int32_t {
+  OP_MATMUL = 0, OP_ADD = 1, OP_SUB = 2, OP_MUL = 3, OP_DIV = 4, OP_TRANSPOSE = 13, OP_RESHAPE = 19, OP_SOFTMAX = 20,
+  OP_LAYERNORM = 21, OP_GELU = 22, OP_CE = 23, OP_EMBEDDING = 24
+};
+
+// grad-tracked binop: lower + tape_record_binop (codegen-cpu/lib.rs:1531-1552)
+int64_t binop(int32_t op, int64_t a, int64_t b) {
+  int64_t out = op == OP_MATMUL ? tensor_matmul(a, b) : malus_std_broadcast_fwd(op - 1, a, b);
+  tape_record_binop(op, a, b, out);
+  return out;
+}
+
+int64_t reshape(int64_t x, std::initializer_list<size_t> dims) {
+  std::vector<size_t> d(dims);
+  int64_t out = tensor_reshape(x, d.data(), d.size());
+  tape_record_unary(OP_RESHAPE, x, out);
+  return out;
+}
+
+int64_t permute(int64_t x, std::initializer_list<size_t> perm) {
+  std::vector<size_t> p(perm);
+  int64_t out;
+  if (p.size() == 3) out = malus_std_permute_3d_fwd(x, (int64_t)p[0], (int64_t)p[1], (int64_t)p[2]);  // lib.rs:3012
+  else out = tensor_permute(x, p.data(), p.size());
+  tape_record_perm(OP_TRANSPOSE, x, out, p.data(), p.size());
+  return out;
+}
+
+int64_t layernorm(int64_t x) {
+  int64_t var;
+  int64_t y = malus_std_layernorm_fwd(x, 1, &var);
+  tape_record_layernorm(OP_LAYERNORM, x, y, var, 1);
+  return y;
+}
+
+void rel(std::initializer_list<int64_t> hs) {
+  for (int64_t h : hs) tensor_release(h);
+}
+
+struct Gpt {
+  int V, Tn, C, H, L, B;
+  float lr, b1, b2, eps, wd;
+  bool fused_opt = true;
+  std::vector<int64_t> p, m, v;  // block l params at 8l..8l+7, then wte, wpe, ln_f, lm_head
+  int64_t pos = 0;               // [B*T] i32 position ids
+
+  int np() const { return 8 * L + 4; }
+  int64_t& top(int j) { return p[8 * L + j]; }
+};
+
+int64_t block_forward(Gpt& g, int l, int64_t x) {
+  const size_t B = g.B, Tn = g.Tn, C = g.C, H = g.H, hs = C / H, N = B * Tn;
+  int64_t* P = &g.p[8 * l];
+  // nanogpt_modular.ml:47-68
+  int64_t y1 = layernorm(x);
+  int64_t xn1 = binop(OP_MUL, y1, P[0]);
+  auto head_fold = [&](int64_t w) {
+    int64_t q = binop(OP_MATMUL, xn1, w);
+    int64_t q4 = reshape(q, {B, Tn, H, hs});
+    int64_t qp = permute(q4, {0, 2, 1, 3});
+    int64_t Q = reshape(qp, {B * H, Tn, hs});
+    rel({q, q4, qp});
+    return Q;
+  };
+  int64_t Q = head_fold(P[1]);
+  int64_t K = head_fold(P[2]);
+  int64_t Vv = head_fold(P[3]);
+  int64_t Kt = permute(K, {0, 2, 1});
+  size_t s11[2] = {1, 1};
+  int64_t ones11 = tensor_alloc_ones_gpu(s11, 2);
+  int64_t scale = malus_std_scalar_op(k::MUL, ones11, 1.0f / sqrtf((float)hs), 1);  // ones(1,1) * (1/sqrt(hs))
+  tensor_release(ones11);
+  tape_register_leaf(scale);  // variable(...)
+  int64_t S = binop(OP_MATMUL, Q, Kt);
+  int64_t Ss = binop(OP_MUL, S, scale);
+  int64_t mask = tensor_causal_mask((int64_t)Tn);
+  tape_register_leaf(mask);  // variable(mask)
+  int64_t Sm = binop(OP_ADD, Ss, mask);
+  int64_t Pm = malus_std_softmax_fwd(Sm, 2);
+  tape_record_reduce(OP_SOFTMAX, Sm, Pm, 2, 0);
+  int64_t AO = binop(OP_MATMUL, Pm, Vv);
+  int64_t ao4 = reshape(AO, {B, H, Tn, hs});
+  int64_t aop = permute(ao4, {0, 2, 1, 3});
+  int64_t att = reshape(aop, {N, C});
+  int64_t proj = binop(OP_MATMUL, att, P[4]);
+  int64_t x2 = binop(OP_ADD, x, proj);
+  int64_t y2 = layernorm(x2);
+  int64_t xn2 = binop(OP_MUL, y2, P[5]);
+  int64_t h = binop(OP_MATMUL, xn2, P[6]);
+  int64_t ge = malus_std_gelu_fwd(h);
+  tape_record_unary(OP_GELU, h, ge);
+  int64_t mo = binop(OP_MATMUL, ge, P[7]);
+  int64_t x3 = binop(OP_ADD, x2, mo);
+  rel({y1, xn1, Q, K, Vv, Kt, scale, S, Ss, mask, Sm, Pm, AO, ao4, aop, att, proj, x2, y2, xn2, h, ge, mo});
+  return x3;
+}
+
+// GPT.forward (nanogpt_modular.ml:75-91) + cross_entropy (lib.rs:2945-2972)
+int64_t gpt_forward_loss(Gpt& g, int64_t toks, int64_t targets, int64_t* logits_out) {
+  int64_t te = malus_std_embedding_fwd(g.top(0), toks);
+  tape_record_embedding(OP_EMBEDDING, g.top(0), toks, te);
+  int64_t pe = malus_std_embedding_fwd(g.top(1), g.pos);
+  tape_record_embedding(OP_EMBEDDING, g.top(1), g.pos, pe);
+  int64_t x = binop(OP_ADD, te, pe);
+  rel({te, pe});
+  for (int l = 0; l < g.L; ++l) {
+    int64_t nx = block_forward(g, l, x);
+    tensor_release(x);
+    x = nx;
+  }
+  int64_t yf = layernorm(x);
+  int64_t xf = binop(OP_MUL, yf, g.top(2));
+  int64_t logits = binop(OP_MATMUL, xf, g.top(3));
+  rel({x, yf, xf});
+  if (!targets) {
+    *logits_out = logits;
+    return 0;
+  }
+  int64_t probs;
+  int64_t loss = malus_std_cross_entropy_fwd(logits, targets, &probs);
+  tape_record_cross_entropy(OP_CE, logits, loss, probs, targets);
+  if (logits_out) *logits_out = logits;
+  else tensor_release(logits);
+  return loss;
+}
+
+// adamw (nanogpt_modular.ml:97-108) for params [beg, end)
+void adamw_range(Gpt& g, int beg, int end, int64_t t) {
+  const float bc1 = 1.0f - powf(g.b1, (float)t), bc2 = 1.0f - powf(g.b2, (float)t);
+  for (int i = beg; i < end; ++i) {
+    int64_t grad = tape_get_grad(g.p[i]);
+    int64_t np_, nm, nv;
+    if (g.fused_opt) {
+      np_ = malus_std_adam_l2(g.p[i], grad, g.m[i], g.v[i], g.lr, g.b1, g.b2, g.eps, g.wd, t, &nm, &nv);
+    } else {  // the op-by-op sequence the JIT emits
+      int64_t wdp = malus_std_scalar_op(k::MUL, g.p[i], g.wd, 0);
+      int64_t gg = malus_std_broadcast_fwd(k::ADD, grad, wdp);
+      int64_t t1 = malus_std_scalar_op(k::MUL, g.m[i], g.b1, 0);
+      int64_t t2 = malus_std_scalar_op(k::MUL, gg, 1.0f - g.b1, 0);
+      nm = malus_std_broadcast_fwd(k::ADD, t1, t2);
+      int64_t t3 = malus_std_scalar_op(k::MUL, g.v[i], g.b2, 0);
+      int64_t t4 = malus_std_scalar_op(k::MUL, gg, 1.0f - g.b2, 0);
+      int64_t t5 = malus_std_broadcast_fwd(k::MUL, t4, gg);
+      nv = malus_std_broadcast_fwd(k::ADD, t3, t5);
+      int64_t mh = malus_std_scalar_op(k::DIV, nm, bc1, 1);
+      int64_t vh = malus_std_scalar_op(k::DIV, nv, bc2, 1);
+      int64_t t6 = malus_std_scalar_op(k::MUL, mh, g.lr, 0);
+      int64_t t7 = malus_std_unary(k::SQRT, vh);
+      int64_t t8 = malus_std_scalar_op(k::ADD, t7, g.eps, 1);
+      int64_t t9 = malus_std_broadcast_fwd(k::DIV, t6, t8);
+      np_ = malus_std_broadcast_fwd(k::SUB, g.p[i], t9);
+      rel({wdp, gg, t1, t2, t3, t4, t5, mh, vh, t6, t7, t8, t9});
+    }
+    tensor_release(grad);
+    tape_register_leaf(np_);  // ps[i] = variable(...)
+    rel({g.p[i], g.m[i], g.v[i]});
+    g.p[i] = np_;
+    g.m[i] = nm;
+    g.v[i] = nv;
+  }
+}
+
+int64_t zeros_like_param(int64_t p) {
+  TensorBuffer* t = T(p);
+  TensorBuffer* z = alloc_tensor(F32, t->shape, t->ndim);
+  k::fill(z->f32(), 0.0f, z->len, stream());
+  z->write_seq = enqueue_mark("zeros");
+  return H(z);
+}
+
+}  // namespace
+
+extern "C" {
+
+// Builds the model of nanogpt_modular.ml main() (lines 138-164) with L
+// blocks: randn draws in the reference order (block 0..L-1: wq wk wv wo w1
+// w2; then wte, wpe, lm_head), each scaled by 0.02.
+void* malus_gpt_create(int V, int Tn, int C, int H, int L, int B, float lr, float b1, float b2, float eps, float wd) {
+  API_TRY
+  if (H <= 0 || C % H) fail("malus: n_embd %d is not divisible by n_head %d", C, H);
+  auto* g = new Gpt{V, Tn, C, H, L, B, lr, b1, b2, eps, wd};
+  size_t s11[2] = {1, 1};
+  int64_t ones11 = tensor_alloc_ones_gpu(s11, 2);
+  int64_t init_scale = malus_std_scalar_op(k::MUL, ones11, 0.02f, 1);  // ones(1,1) * 0.02
+  tensor_release(ones11);
+  auto randn_scaled = [&](size_t r, size_t c) {
+    size_t sh[2] = {r, c};
+    int64_t rn = tensor_randn(sh, 2);
+    int64_t w = malus_std_broadcast_fwd(k::MUL, rn, init_scale);
+    tensor_release(rn);
+    tape_register_leaf(w);
+    return w;
+  };
+  auto ones_vec = [&](size_t c) {
+    size_t sh[1] = {c};
+    int64_t o = tensor_alloc_ones_gpu(sh, 1);
+    tape_register_leaf(o);
+    return o;
+  };
+  const size_t Cs = (size_t)C, C4 = 4 * (size_t)C;
+  for (int l = 0; l < L; ++l) {
+    g->p.push_back(ones_vec(Cs));
+    for (int j = 0; j < 4; ++j) g->p.push_back(randn_scaled(Cs, Cs));
+    g->p.push_back(ones_vec(Cs));
+    g->p.push_back(randn_scaled(Cs, C4));
+    g->p.push_back(randn_scaled(C4, Cs));
+  }
+  g->p.push_back(randn_scaled((size_t)V, Cs));
+  g->p.push_back(randn_scaled((size_t)Tn, Cs));
+  g->p.push_back(ones_vec(Cs));
+  g->p.push_back(randn_scaled(Cs, (size_t)V));
+  tensor_release(init_scale);
+  for (int64_t p : g->p) {
+    g->m.push_back(zeros_like_param(p));
+    g->v.push_back(zeros_like_param(p));
+  }
+  // position ids [B*T] (nanogpt_modular.ml:80-84), built once on the device
+  size_t sh[1] = {(size_t)B * Tn};
+  TensorBuffer* pos = alloc_tensor(I32, sh, 1);
+  k::iota_rows(pos->i32(), (size_t)B, (size_t)Tn, stream());
+  pos->write_seq = enqueue_mark("positions");
+  g->pos = malus::H(pos);
+  return g;
+  API_CATCH(nullptr)
+}
+
+void malus_gpt_free(void* gp) {
+  API_TRY
+  auto* g = static_cast<Gpt*>(gp);
+  if (!g) return;
+  for (size_t i = 0; i < g->p.size(); ++i) rel({g->p[i], g->m[i], g->v[i]});
+  tensor_release(g->pos);
+  delete g;
+  API_CATCH()
+}
+
+int malus_gpt_nparams(void* gp) { return static_cast<Gpt*>(gp)->np(); }
+int64_t malus_gpt_param(void* gp, int i) { return static_cast<Gpt*>(gp)->p[(size_t)i]; }
+int64_t malus_gpt_moment(void* gp, int i, int which) {
+  auto* g = static_cast<Gpt*>(gp);
+  return which ? g->v[(size_t)i] : g->m[(size_t)i];
+}
+void malus_gpt_set_fused_optimizer(void* gp, int on) { static_cast<Gpt*>(gp)->fused_opt = on != 0; }
+
+// Forward + cross-entropy (recorded on the tape); returns the loss [1].
+int64_t malus_gpt_forward_loss(void* gp, int64_t toks, int64_t targets) {
+  API_TRY
+  return gpt_forward_loss(*static_cast<Gpt*>(gp), toks, targets, nullptr);
+  API_CATCH(0)
+}
+
+// Forward only, no tape; returns logits [B*T, V].
+int64_t malus_gpt_logits(void* gp, int64_t toks) {
+  API_TRY
+  tape_pause();
+  int64_t logits = 0;
+  gpt_forward_loss(*static_cast<Gpt*>(gp), toks, 0, &logits);
+  tape_resume();
+  return logits;
+  API_CATCH(0)
+}
+
+void malus_gpt_zero_grad(void* gp) {
+  auto* g = static_cast<Gpt*>(gp);
+  // zero_grad per submodule (nanogpt_modular.ml:178-182)
+  for (int l = 0; l < g->L; ++l) tape_zero_grad(&g->p[8 * l], 8);
+  tape_zero_grad(&g->p[8 * g->L], 4);
+}
+
+void malus_gpt_optimizer_step(void* gp, int64_t t) {
+  API_TRY
+  auto* g = static_cast<Gpt*>(gp);
+  for (int l = 0; l < g->L; ++l) adamw_range(*g, 8 * l, 8 * l + 8, t);  // lines 186-187
+  adamw_range(*g, 8 * g->L, 8 * g->L + 4, t);                        // line 188
+  API_CATCH()
+}
+
+// One training step (nanogpt_modular.ml:167-189 minus the host batch build):
+// zero_grad, forward, cross_entropy, backward, AdamW.  Returns the loss [1]
+// (owned by the caller; nothing is read back to the host).
+int64_t malus_gpt_step(void* gp, int64_t toks, int64_t targets, int64_t t) {
+  API_TRY
+  auto* g = static_cast<Gpt*>(gp);
+  malus_gpt_zero_grad(g);
+  int64_t loss = gpt_forward_loss(*g, toks, targets, nullptr);
+  backward(loss);
+  malus_gpt_optimizer_step(g, t);
+  return loss;
+  API_CATCH(0)
+}
+
+// examples/xor.ml main(): returns the final loss; loss_at[6] receives the
+// printed losses (steps 0, 500, 1000, 2000, 5000, 9999), preds[4] the final
+// predictions, params[33] = w1 (16), b1 (8), w2 (8), b2 (1).
+// `sigmoid_backward_id` is the kernel id of the user kernel xor.ml:1-2,
+// registered through malus_runtime_init.
+float malus_xor_run(int steps, float lr, uint64_t sigmoid_backward_id, float* loss_at, float* preds, float* params) {
+  API_TRY
+  const float xd[8] = {0, 0, 0, 1, 1, 0, 1, 1}, td[4] = {0, 1, 1, 0}, od[4] = {1, 1, 1, 1};
+  const float w1d[16] = {0.5f, -0.6f, 0.7f, -0.4f, 0.3f, -0.5f, 0.6f, -0.3f,
+                         -0.4f, 0.5f, -0.6f, 0.7f, -0.3f, 0.4f, -0.5f, 0.6f};
+  const float b1d[8] = {0.1f, -0.1f, 0.1f, -0.1f, 0.1f, -0.1f, 0.1f, -0.1f};
+  const float w2d[8] = {0.6f, -0.5f, 0.4f, -0.6f, 0.5f, -0.4f, 0.6f, -0.5f};
+  const float b2d[1] = {0.0f};
+  size_t s42[2] = {4, 2}, s41[2] = {4, 1}, s28[2] = {2, 8}, s18[2] = {1, 8}, s81[2] = {8, 1}, s11[2] = {1, 1};
+  int64_t x = tensor_alloc_gpu(F32, s42, 2, xd), target = tensor_alloc_gpu(F32, s41, 2, td);
+  int64_t ones41 = tensor_alloc_gpu(F32, s41, 2, od);
+  int64_t w1 = tensor_alloc_gpu(F32, s28, 2, w1d), b1 = tensor_alloc_gpu(F32, s18, 2, b1d);
+  int64_t w2 = tensor_alloc_gpu(F32, s81, 2, w2d), b2 = tensor_alloc_gpu(F32, s11, 2, b2d);
+  const int report[6] = {0, 500, 1000, 2000, 5000, 9999};
+  float loss_v = 0.0f;
+  int64_t out = 0;
+  for (int step = 0; step < steps; ++step) {
+    int64_t a1 = tensor_matmul(x, w1), a2 = tensor_matmul(ones41, b1);
+    int64_t z1 = malus_std_broadcast_fwd(k::ADD, a1, a2);
+    int64_t h = malus_std_unary(k::SIGMOID, z1);
+    int64_t c1 = tensor_matmul(h, w2), c2 = tensor_matmul(ones41, b2);
+    int64_t z2 = malus_std_broadcast_fwd(k::ADD, c1, c2);
+    if (out) tensor_release(out);
+    out = malus_std_unary(k::SIGMOID, z2);
+    int64_t diff = malus_std_broadcast_fwd(k::SUB, out, target);
+    int64_t sq = malus_std_broadcast_fwd(k::MUL, diff, diff);
+    int64_t loss = malus_std_reduce_all_sum_fwd(sq);
+    for (int r = 0; r < 6; ++r)
+      if (step == report[r]) {
+        float lv = malus_tensor_get_f32(loss, 0);  // println reads the loss (flush)
+        if (loss_at) loss_at[r] = lv;
+      }
+    if (step == steps - 1) loss_v = malus_tensor_get_f32(loss, 0);
+    int64_t dout = malus_std_scalar_op(k::MUL, diff, 2.0f, 0);
+    int64_t hs1[2] = {dout, out};
+    int64_t dz2 = kernel_dispatch(sigmoid_backward_id, hs1, 2);
+    int64_t hT = malus_std_transpose_2d_fwd(h);
+    int64_t dw2 = tensor_matmul(hT, dz2);
+    int64_t oT = malus_std_transpose_2d_fwd(ones41);
+    int64_t db2 = tensor_matmul(oT, dz2);
+    int64_t w2T = malus_std_transpose_2d_fwd(w2);
+    int64_t dh = tensor_matmul(dz2, w2T);
+    int64_t hs2[2] = {dh, h};
+    int64_t dz1 = kernel_dispatch(sigmoid_backward_id, hs2, 2);
+    int64_t xT = malus_std_transpose_2d_fwd(x);
+    int64_t dw1 = tensor_matmul(xT, dz1);
+    int64_t oT2 = malus_std_transpose_2d_fwd(ones41);
+    int64_t db1 = tensor_matmul(oT2, dz1);
+    auto sgd = [&](int64_t& w, int64_t dw) {
+      int64_t u = malus_std_scalar_op(k::MUL, dw, lr, 0);
+      int64_t nw = malus_std_broadcast_fwd(k::SUB, w, u);
+      rel({u, w});
+      w = nw;
+    };
+    sgd(w1, dw1);
+    sgd(b1, db1);
+    sgd(w2, dw2);
+    sgd(b2, db2);
+    rel({a1, a2, z1, h, c1, c2, z2, diff, sq, loss, dout, dz2, hT, dw2, oT, db2, w2T, dh, dz1, xT, dw1, oT2, db1});
+  }
+  if (preds && out) malus_tensor_read(out, preds, 4 * sizeof(float));
+  if (params) {
+    malus_tensor_read(w1, params, 16 * sizeof(float));
+    malus_tensor_read(b1, params + 16, 8 * sizeof(float));
+    malus_tensor_read(w2, params + 24, 8 * sizeof(float));
+    malus_tensor_read(b2, params + 32, sizeof(float));
+  }
+  rel({x, target, ones41, w1, b1, w2, b2});
+  if (out) tensor_release(out);
+  return loss_v;
+  API_CATCH(0.0f)
+}
+
+}  // extern "C"

@@ -1,0 +1,691 @@
+// Stdlib host functions: the operations malus `fn` bodies dispatch
+// implicitly (crates/malus-stdlib/stdlib/*.ml and backward/*.ml), each
+// implemented on the hand-written gfx950 kernels with its own launch
+// geometry.  Names mirror the .ml host fns with a malus_std_ prefix; the
+// backward ones are what the tape's BwdSlot table holds by default.
+//
+// Where the .ml composition launches several kernels (softmax VJP: 5,
+// layernorm VJP: ~10, cross-entropy: 3, AdamW: ~16 per tensor) one fused
+// kernel computes the same f32 expression tree.  Output handles are owned
+// by the caller (refcount 1); inputs are borrowed.
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "api.h"
+#include "common.h"
+
+using namespace malus;
+
+namespace {
+
+int norm_axis(int64_t axis, int ndim) {
+  int64_t a = axis < 0 ? axis + ndim : axis;  // normalize_axis, metal.rs:1124-1131
+  if (a < 0 || a >= ndim) fail("malus: axis %lld is out of range for tensor with %d dimensions", (long long)axis, ndim);
+  return (int)a;
+}
+
+void split_axis(const TensorBuffer* t, int axis, size_t* outer, size_t* a, size_t* inner) {
+  size_t o = 1, in = 1;
+  for (int i = 0; i < axis; ++i) o *= t->shape[i];
+  for (int i = axis + 1; i < t->ndim; ++i) in *= t->shape[i];
+  *outer = o;
+  *a = t->shape[axis];
+  *inner = in;
+}
+
+void need_f32(const TensorBuffer* t, const char* what) {
+  if (t->dtype != F32) fail("malus: %s expects a Tensor<f32>, got dtype tag %d", what, t->dtype);
+}
+
+int64_t done(TensorBuffer* t, const char* name) {
+  t->write_seq = enqueue_mark(name);
+  return H(t);
+}
+
+bool same_shape(const TensorBuffer* a, const TensorBuffer* b) {
+  if (a->ndim != b->ndim) return false;
+  for (int i = 0; i < a->ndim; ++i)
+    if (a->shape[i] != b->shape[i]) return false;
+  return true;
+}
+
+TensorBuffer* copy_of(const TensorBuffer* t) {
+  TensorBuffer* o = alloc_like(t);
+  k::copy(t->data(), o->data(), t->bytes(), stream());
+  o->write_seq = enqueue_mark("copy");
+  return o;
+}
+
+// p op q with NumPy right-aligned broadcasting; p has rank >= q's rank.
+TensorBuffer* broadcast_binop(int op, const TensorBuffer* p, const TensorBuffer* q) {
+  const int n = p->ndim;
+  size_t qq[kMaxRank], os[kMaxRank];
+  for (int i = 0; i < n; ++i) {
+    qq[i] = i >= n - q->ndim ? q->shape[i - (n - q->ndim)] : 1;
+    size_t pd = p->shape[i];
+    if (pd == qq[i] || qq[i] == 1) os[i] = pd;
+    else if (pd == 1) os[i] = qq[i];
+    else
+      fail("malus: broadcast shape mismatch at dim %d: %zu vs %zu\n  left shape:  %s\n  right shape: %s", i, pd, qq[i],
+           shape_str(p).c_str(), shape_str(q).c_str());
+  }
+  TensorBuffer* out = alloc_tensor(F32, os, n);
+  hipStream_t s = stream();
+  const size_t total = out->len;
+  bool out_is_p = true;
+  for (int i = 0; i < n; ++i) out_is_p &= (os[i] == p->shape[i]);
+  if (out_is_p && q->len == p->len) {
+    k::binary_same(op, p->f32(), q->f32(), out->f32(), total, s);
+  } else if (out_is_p && q->len == 1) {
+    k::binary_scalar(op, p->f32(), q->f32(), 0.0f, true, out->f32(), total, s);
+  } else {
+    // q is a trailing block of p: q's padded shape = [1.., p.shape[k..]]
+    bool trailing = out_is_p;
+    if (trailing) {
+      int k0 = 0;
+      while (k0 < n && qq[k0] == 1) ++k0;
+      for (int i = k0; i < n; ++i) trailing &= (qq[i] == p->shape[i]);
+    }
+    if (trailing && total % q->len == 0) {
+      k::binary_rowbcast(op, p->f32(), q->f32(), out->f32(), total, q->len, s);
+    } else {
+      k::BcastDesc d{};
+      d.ndim = n;
+      size_t ps = 1, qs = 1;
+      for (int i = n - 1; i >= 0; --i) {
+        d.out_shape[i] = (uint32_t)os[i];
+        d.p_stride[i] = p->shape[i] == 1 ? 0u : (uint32_t)ps;
+        d.q_stride[i] = qq[i] == 1 ? 0u : (uint32_t)qs;
+        ps *= p->shape[i];
+        qs *= qq[i];
+      }
+      k::binary_general(op, p->f32(), q->f32(), out->f32(), total, d, s);
+    }
+  }
+  return out;
+}
+
+// Reduce `dout` down to `target`'s shape (sum over broadcast dims),
+// elementwise_bwd.ml:8-22.  Equal shapes return a retained alias.
+TensorBuffer* sum_to_shape(TensorBuffer* g, const TensorBuffer* target) {
+  if (same_shape(g, target)) {
+    retain(g);
+    return g;
+  }
+  const int gn = g->ndim, tn = target->ndim;
+  if (tn > gn) fail("malus: sum_to_shape: target rank %d exceeds gradient rank %d", tn, gn);
+  size_t padded[kMaxRank];
+  for (int i = 0; i < gn; ++i) padded[i] = i >= gn - tn ? target->shape[i - (gn - tn)] : 1;
+  for (int i = 0; i < gn; ++i)
+    if (padded[i] != 1 && padded[i] != g->shape[i])
+      fail("malus: sum_to_shape: %s is not broadcastable to %s", shape_str(target).c_str(), shape_str(g).c_str());
+  // classify dims: reduce (padded 1, g > 1) or keep; merge runs
+  struct Run { bool red; size_t n; };
+  std::vector<Run> runs;
+  for (int i = 0; i < gn; ++i) {
+    bool red = padded[i] == 1 && g->shape[i] != 1;
+    size_t n = g->shape[i];
+    if (n == 1) continue;  // size-1 dims are layout-neutral
+    if (!runs.empty() && runs.back().red == red) runs.back().n *= n;
+    else runs.push_back({red, n});
+  }
+  TensorBuffer* out = alloc_tensor(F32, target->shape, tn);
+  hipStream_t s = stream();
+  // reduce runs one at a time from the last, keeping a running [.., R, K] view
+  const float* src = g->f32();
+  std::vector<std::pair<void*, size_t>> temps;
+  size_t cur_len = g->len;
+  for (int r = (int)runs.size() - 1; r >= 0; --r) {
+    if (!runs[r].red) continue;
+    size_t inner = 1, outer = 1;
+    for (size_t j = r + 1; j < runs.size(); ++j) inner *= runs[j].n;
+    outer = cur_len / (runs[r].n * inner);
+    size_t out_len = outer * inner;
+    bool last = true;
+    for (int j = r - 1; j >= 0; --j) last &= !runs[j].red;
+    float* dst;
+    if (last) {
+      dst = out->f32();
+    } else {
+      size_t b;
+      dst = static_cast<float*>(pool_alloc(out_len * sizeof(float), &b));
+      temps.push_back({dst, b});
+    }
+    k::reduce_axis(k::R_SUM, src, dst, outer, runs[r].n, inner, s);
+    src = dst;
+    cur_len = out_len;
+    runs[r].n = 1;
+  }
+  if (src != out->f32()) k::copy(src, out->f32(), out->bytes(), s);  // nothing to reduce (all size-1)
+  for (auto& t : temps) pool_free(t.first, t.second);
+  return out;
+}
+
+// [outer, a, inner] broadcast of a keepdim/non-keepdim reduced tensor
+TensorBuffer* expand_to(const TensorBuffer* small, const TensorBuffer* tmpl, int axis) {
+  size_t o, a, in;
+  split_axis(tmpl, axis, &o, &a, &in);
+  if (small->len != o * in)
+    fail("malus: expand_axis: small tensor %s does not match %s reduced over axis %d", shape_str(small).c_str(),
+         shape_str(tmpl).c_str(), axis);
+  TensorBuffer* out = alloc_tensor(F32, tmpl->shape, tmpl->ndim);
+  k::expand_axis(small->f32(), out->f32(), o, a, in, stream());
+  return out;
+}
+
+TensorBuffer* as_i32_indices(TensorBuffer* idx, bool* owned) {
+  *owned = false;
+  if (idx->dtype == I32) return idx;
+  fail("malus: index tensors must be Tensor<i32> (got dtype tag %d)", idx->dtype);
+}
+
+int64_t gemm_out(TensorBuffer* a, TensorBuffer* b, bool ta, bool tb, int batch, int M, int N, int K, long sA, long sB,
+                 const size_t* oshape, int ond) {
+  TensorBuffer* c = alloc_tensor(F32, oshape, ond);
+  KTimer* kt = ktimer_begin("gemm");
+  k::gemm(a->f32(), b->f32(), c->f32(), batch, M, N, K, ta, tb, sA, sB, (long)M * N, stream());
+  ktimer_end(kt, 2.0 * batch * (double)M * N * K);
+  return done(c, "matmul");
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---- broadcast binops (broadcast_binop.ml:82-112, operand swap kept) -------
+int64_t malus_std_broadcast_fwd(int32_t op, int64_t a, int64_t b) {
+  API_TRY
+  TensorBuffer *ta = T(a), *tb = T(b);
+  need_f32(ta, "broadcast op");
+  need_f32(tb, "broadcast op");
+  TensorBuffer* out = ta->ndim >= tb->ndim ? broadcast_binop(op, ta, tb) : broadcast_binop(op, tb, ta);
+  return done(out, "broadcast");
+  API_CATCH(0)
+}
+int64_t malus_std_broadcast_add_fwd(int64_t a, int64_t b) { return malus_std_broadcast_fwd(k::ADD, a, b); }
+int64_t malus_std_broadcast_sub_fwd(int64_t a, int64_t b) { return malus_std_broadcast_fwd(k::SUB, a, b); }
+int64_t malus_std_broadcast_mul_fwd(int64_t a, int64_t b) { return malus_std_broadcast_fwd(k::MUL, a, b); }
+int64_t malus_std_broadcast_div_fwd(int64_t a, int64_t b) { return malus_std_broadcast_fwd(k::DIV, a, b); }
+
+// ---- scalar builtins (codegen-gpu/lib.rs:400-418) ---------------------------
+int64_t malus_std_scalar_op(int32_t op, int64_t a, float s, int32_t right) {
+  API_TRY
+  TensorBuffer* t = T(a);
+  need_f32(t, "scalar op");
+  TensorBuffer* out = alloc_like(t);
+  k::binary_scalar(op, t->f32(), nullptr, s, right != 0, out->f32(), t->len, stream());
+  return done(out, "scalar_op");
+  API_CATCH(0)
+}
+int64_t malus_std_scalar_op_dev(int32_t op, int64_t a, int64_t s1, int32_t right) {
+  API_TRY
+  TensorBuffer *t = T(a), *sv = T(s1);
+  need_f32(t, "scalar op");
+  if (sv->len < 1) fail("malus: scalar operand tensor is empty");
+  TensorBuffer* out = alloc_like(t);
+  k::binary_scalar(op, t->f32(), sv->f32(), 0.0f, right != 0, out->f32(), t->len, stream());
+  return done(out, "scalar_op");
+  API_CATCH(0)
+}
+
+// ---- unary builtins (codegen-gpu/lib.rs:375-381) ---------------------------
+int64_t malus_std_unary(int32_t op, int64_t x) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  need_f32(t, "unary op");
+  TensorBuffer* out = alloc_like(t);
+  k::unary(op, t->f32(), out->f32(), t->len, stream());
+  return done(out, "unary");
+  API_CATCH(0)
+}
+int64_t malus_std_gelu_fwd(int64_t x) { return malus_std_unary(k::GELU, x); }
+
+// ---- axis reductions (reduce_{sum,mean,max,var}.ml) ------------------------
+int64_t malus_std_reduce_fwd(int32_t op, int64_t x, int64_t axis, int64_t keepdim) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  need_f32(t, "reduction");
+  int ax = norm_axis(axis, t->ndim);
+  size_t o, a, in;
+  split_axis(t, ax, &o, &a, &in);
+  size_t sh[kMaxRank];
+  int nd = 0;
+  if (t->ndim == 1) {
+    sh[nd++] = 1;  // reduce_sum.ml:32-33: rank-1 input -> [1]
+  } else {
+    for (int i = 0; i < t->ndim; ++i) {
+      if (i == ax) { if (keepdim) sh[nd++] = 1; }
+      else sh[nd++] = t->shape[i];
+    }
+  }
+  TensorBuffer* out = alloc_tensor(F32, sh, nd);
+  k::reduce_axis(op, t->f32(), out->f32(), o, a, in, stream());
+  return done(out, "reduce");
+  API_CATCH(0)
+}
+
+// reduce_all.ml:9-12: whole-tensor sum -> [1] (no 1024-element cap here)
+int64_t malus_std_reduce_all_sum_fwd(int64_t x) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  need_f32(t, "sum");
+  TensorBuffer* out = alloc_f32({1});
+  k::reduce_axis(k::R_SUM, t->f32(), out->f32(), 1, t->len, 1, stream());
+  return done(out, "sum_all");
+  API_CATCH(0)
+}
+
+// ---- softmax / layernorm / cross-entropy ------------------------------------
+int64_t malus_std_softmax_fwd(int64_t x, int64_t axis) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  need_f32(t, "softmax");
+  int ax = norm_axis(axis, t->ndim);
+  size_t o, a, in;
+  split_axis(t, ax, &o, &a, &in);
+  TensorBuffer* out = alloc_like(t);
+  k::softmax(t->f32(), out->f32(), o, a, in, stream());
+  return done(out, "softmax");
+  API_CATCH(0)
+}
+
+// Returns normed; *var_out receives the population variance, keepdim at the
+// axis (the tape takes ownership, tape.rs:289-310).
+int64_t malus_std_layernorm_fwd(int64_t x, int64_t axis, int64_t* var_out) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  need_f32(t, "layernorm");
+  int ax = norm_axis(axis, t->ndim);
+  size_t o, a, in;
+  split_axis(t, ax, &o, &a, &in);
+  TensorBuffer* y = alloc_like(t);
+  size_t vsh[kMaxRank];
+  for (int i = 0; i < t->ndim; ++i) vsh[i] = i == ax ? 1 : t->shape[i];
+  TensorBuffer* var = alloc_tensor(F32, vsh, t->ndim);
+  k::layernorm(t->f32(), y->f32(), var->f32(), o, a, in, 1e-5f, stream());
+  uint64_t seq = enqueue_mark("layernorm");
+  y->write_seq = var->write_seq = seq;
+  if (var_out) *var_out = H(var);
+  else release(var);
+  return H(y);
+  API_CATCH(0)
+}
+
+// cross_entropy.ml:18-28: returns loss [1]; *probs_out receives the softmax
+// probabilities [N, V].
+int64_t malus_std_cross_entropy_fwd(int64_t logits, int64_t targets, int64_t* probs_out) {
+  API_TRY
+  TensorBuffer *lg = T(logits), *tg = T(targets);
+  need_f32(lg, "cross_entropy");
+  if (lg->ndim != 2) fail("malus: cross_entropy logits must be rank-2 [N, C], got shape %s", shape_str(lg).c_str());
+  if (tg->ndim != 1) fail("malus: cross_entropy targets must be rank-1 [N], got shape %s", shape_str(tg).c_str());
+  const size_t n = lg->shape[0], v = lg->shape[1];
+  if (tg->shape[0] != n) fail("malus: cross_entropy logits N=%zu but targets has %zu elements", n, tg->shape[0]);
+  bool owned;
+  TensorBuffer* ti = as_i32_indices(tg, &owned);
+  TensorBuffer* probs = alloc_like(lg);
+  TensorBuffer* loss = alloc_f32({1});
+  size_t b;
+  float* nll = static_cast<float*>(pool_alloc(n * sizeof(float), &b));
+  hipStream_t s = stream();
+  k::ce_fwd(lg->f32(), ti->i32(), probs->f32(), nll, n, v, device_error_flag(), s);
+  k::reduce_axis(k::R_MEAN, nll, loss->f32(), 1, n, 1, s);  // reduce_mean_fwd(nll, 0, 1)
+  pool_free(nll, b);
+  uint64_t seq = enqueue_mark("cross_entropy");
+  probs->write_seq = loss->write_seq = seq;
+  if (probs_out) *probs_out = H(probs);
+  else release(probs);
+  return H(loss);
+  API_CATCH(0)
+}
+
+// ---- embedding (embedding.ml:18-23) -----------------------------------------
+int64_t malus_std_embedding_fwd(int64_t weight, int64_t indices) {
+  API_TRY
+  TensorBuffer *w = T(weight), *idx = T(indices);
+  need_f32(w, "embedding");
+  if (w->ndim != 2) fail("malus: embedding weight must be rank-2 [V, D], got shape %s", shape_str(w).c_str());
+  if (idx->ndim != 1) fail("malus: embedding indices must be rank-1 [T], got shape %s", shape_str(idx).c_str());
+  bool owned;
+  TensorBuffer* ii = as_i32_indices(idx, &owned);
+  size_t sh[2] = {idx->len, w->shape[1]};
+  TensorBuffer* out = alloc_tensor(F32, sh, 2);
+  k::embedding(w->f32(), ii->i32(), out->f32(), idx->len, w->shape[0], w->shape[1], device_error_flag(), stream());
+  return done(out, "embedding");
+  API_CATCH(0)
+}
+
+// ---- permutes (permute.ml) ---------------------------------------------------
+static int64_t permute_impl(TensorBuffer* t, const std::vector<size_t>& perm) {
+  need_f32(t, "permute");
+  if ((int)perm.size() != t->ndim) fail("malus: permute of rank %zu for a rank-%d tensor", perm.size(), t->ndim);
+  size_t osh[kMaxRank];
+  for (int d = 0; d < t->ndim; ++d) osh[d] = t->shape[perm[d]];
+  TensorBuffer* out = alloc_tensor(F32, osh, t->ndim);
+  k::permute(t->f32(), out->f32(), t->ndim, t->shape, perm.data(), stream());
+  return done(out, "permute");
+}
+
+int64_t malus_std_transpose_2d_fwd(int64_t x) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  if (t->ndim != 2) fail("malus: transpose requires a 2-D tensor, got shape %s", shape_str(t).c_str());
+  return permute_impl(t, {1, 0});
+  API_CATCH(0)
+}
+int64_t malus_std_permute_3d_fwd(int64_t x, int64_t p0, int64_t p1, int64_t p2) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  std::vector<size_t> perm = tape_normalize_perm({(size_t)p0, (size_t)p1, (size_t)p2}, (size_t)t->ndim);
+  return permute_impl(t, perm);
+  API_CATCH(0)
+}
+int64_t malus_std_permute_nd_fwd(int64_t x, int64_t p0, int64_t p1, int64_t p2, int64_t p3, int64_t p4, int64_t p5,
+                                 int64_t p6, int64_t p7) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  int64_t all[8] = {p0, p1, p2, p3, p4, p5, p6, p7};
+  std::vector<size_t> perm;
+  for (int i = 0; i < t->ndim; ++i) perm.push_back((size_t)all[i]);
+  return permute_impl(t, tape_normalize_perm(perm, (size_t)t->ndim));
+  API_CATCH(0)
+}
+
+// tensor_permute, metal.rs:1405-1417: normalize, then the PermuteNdFwd slot.
+int64_t tensor_permute(int64_t h, const size_t* perm_ptr, size_t n) {
+  API_TRY
+  TensorBuffer* t = T(h);
+  std::vector<size_t> raw;
+  if (perm_ptr && n) raw.assign(perm_ptr, perm_ptr + n);
+  std::vector<size_t> perm = tape_normalize_perm(raw, (size_t)t->ndim);
+  int64_t p[8] = {0};
+  for (size_t i = 0; i < perm.size(); ++i) p[i] = (int64_t)perm[i];
+  using FnPerm = int64_t (*)(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t);
+  auto f = reinterpret_cast<FnPerm>(malus_tape_backward_fn(17));
+  return f(h, p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
+  API_CATCH(0)
+}
+
+// ---- unary_bwd.ml helpers ------------------------------------------------------
+int64_t malus_std_scale_fwd(int64_t x, float c) { return malus_std_scalar_op(k::MUL, x, c, 1); }
+int64_t malus_std_fill_like_fwd(int64_t x, float c) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  TensorBuffer* out = alloc_tensor(F32, t->shape, t->ndim);
+  k::fill(out->f32(), c, out->len, stream());
+  return done(out, "fill_like");
+  API_CATCH(0)
+}
+int64_t malus_std_eq_fwd(int64_t a, int64_t b) {
+  API_TRY
+  TensorBuffer *ta = T(a), *tb = T(b);
+  if (ta->len != tb->len) fail("malus: eq requires equal lengths, got %zu and %zu", ta->len, tb->len);
+  TensorBuffer* out = alloc_like(ta);
+  k::eq(ta->f32(), tb->f32(), out->f32(), ta->len, stream());
+  return done(out, "eq");
+  API_CATCH(0)
+}
+int64_t malus_std_expand_axis_fwd(int64_t small, int64_t x_template, int64_t axis) {
+  API_TRY
+  TensorBuffer* tmpl = T(x_template);
+  return done(expand_to(T(small), tmpl, norm_axis(axis, tmpl->ndim)), "expand_axis");
+  API_CATCH(0)
+}
+int64_t malus_std_sum_to_shape_bwd(int64_t dout, int64_t target) {
+  API_TRY
+  TensorBuffer* r = sum_to_shape(T(dout), T(target));
+  if (r == T(dout)) return H(r);  // retained alias, already complete
+  return done(r, "sum_to_shape");
+  API_CATCH(0)
+}
+
+// ---- elementwise_bwd.ml ------------------------------------------------------
+int64_t malus_std_add_bwd_a(int64_t dout, int64_t a) { return malus_std_sum_to_shape_bwd(dout, a); }
+int64_t malus_std_add_bwd_b(int64_t dout, int64_t b) { return malus_std_sum_to_shape_bwd(dout, b); }
+int64_t malus_std_sub_bwd_a(int64_t dout, int64_t a) { return malus_std_sum_to_shape_bwd(dout, a); }
+int64_t malus_std_sub_bwd_b(int64_t dout, int64_t b) {
+  API_TRY
+  int64_t neg = malus_std_scale_fwd(dout, -1.0f);
+  int64_t r = malus_std_sum_to_shape_bwd(neg, b);
+  release(T(neg));
+  return r;
+  API_CATCH(0)
+}
+int64_t malus_std_mul_bwd_a(int64_t dout, int64_t a, int64_t b) {
+  API_TRY
+  int64_t full = malus_std_broadcast_mul_fwd(dout, b);
+  int64_t r = malus_std_sum_to_shape_bwd(full, a);
+  release(T(full));
+  return r;
+  API_CATCH(0)
+}
+int64_t malus_std_mul_bwd_b(int64_t dout, int64_t a, int64_t b) {
+  API_TRY
+  int64_t full = malus_std_broadcast_mul_fwd(dout, a);
+  int64_t r = malus_std_sum_to_shape_bwd(full, b);
+  release(T(full));
+  return r;
+  API_CATCH(0)
+}
+int64_t malus_std_div_bwd_a(int64_t dout, int64_t a, int64_t b) {
+  API_TRY
+  int64_t full = malus_std_broadcast_div_fwd(dout, b);
+  int64_t r = malus_std_sum_to_shape_bwd(full, a);
+  release(T(full));
+  return r;
+  API_CATCH(0)
+}
+int64_t malus_std_div_bwd_b(int64_t dout, int64_t a, int64_t b) {
+  API_TRY
+  int64_t t1 = malus_std_broadcast_mul_fwd(dout, a);
+  int64_t neg = malus_std_scale_fwd(t1, -1.0f);
+  int64_t bsq = malus_std_broadcast_mul_fwd(b, b);
+  int64_t full = malus_std_broadcast_div_fwd(neg, bsq);
+  int64_t r = malus_std_sum_to_shape_bwd(full, b);
+  release(T(t1)); release(T(neg)); release(T(bsq)); release(T(full));
+  return r;
+  API_CATCH(0)
+}
+
+// ---- unary VJPs (unary_bwd.ml:37-91) -------------------------------------------
+static int64_t unary_bwd_impl(int op, int64_t xy, int64_t dout) {
+  TensorBuffer *a = T(xy), *d = T(dout);
+  if (a->len != d->len) fail("malus: unary VJP length mismatch %zu vs %zu", a->len, d->len);
+  TensorBuffer* out = alloc_like(a);
+  k::unary_bwd(op, a->f32(), d->f32(), out->f32(), a->len, stream());
+  return done(out, "unary_bwd");
+}
+int64_t malus_std_sigmoid_bwd(int64_t s, int64_t dout) { API_TRY return unary_bwd_impl(k::B_SIGMOID, s, dout); API_CATCH(0) }
+int64_t malus_std_relu_bwd(int64_t x, int64_t dout) { API_TRY return unary_bwd_impl(k::B_RELU, x, dout); API_CATCH(0) }
+int64_t malus_std_tanh_bwd(int64_t t, int64_t dout) { API_TRY return unary_bwd_impl(k::B_TANH, t, dout); API_CATCH(0) }
+int64_t malus_std_sqrt_bwd(int64_t s, int64_t dout) { API_TRY return unary_bwd_impl(k::B_SQRT, s, dout); API_CATCH(0) }
+int64_t malus_std_abs_bwd(int64_t x, int64_t dout) { API_TRY return unary_bwd_impl(k::B_ABS, x, dout); API_CATCH(0) }
+int64_t malus_std_gelu_bwd(int64_t x, int64_t dout) { API_TRY return unary_bwd_impl(k::B_GELU, x, dout); API_CATCH(0) }
+
+// reduce_bwd.ml:73-76: fill_like(x, dout[0]) with dout[0] read on the device
+// (the reference reads it on the host, forcing a flush mid-backward).
+int64_t malus_std_sum_bwd(int64_t x, int64_t dout) {
+  API_TRY
+  TensorBuffer *t = T(x), *d = T(dout);
+  TensorBuffer* out = alloc_tensor(F32, t->shape, t->ndim);
+  k::fill_from_device(out->f32(), d->f32(), out->len, stream());
+  return done(out, "sum_bwd");
+  API_CATCH(0)
+}
+
+// ---- reduce VJPs (reduce_bwd.ml:40-71) --------------------------------------------
+int64_t malus_std_reduce_sum_axis_bwd(int64_t x, int64_t dout, int64_t axis) {
+  return malus_std_expand_axis_fwd(dout, x, axis);
+}
+int64_t malus_std_reduce_mean_axis_bwd(int64_t x, int64_t dout, int64_t axis) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  float n_f = (float)t->shape[norm_axis(axis, t->ndim)];
+  int64_t scaled = malus_std_scale_fwd(dout, 1.0f / n_f);
+  int64_t r = malus_std_expand_axis_fwd(scaled, x, axis);
+  release(T(scaled));
+  return r;
+  API_CATCH(0)
+}
+int64_t malus_std_reduce_max_axis_bwd(int64_t x, int64_t y, int64_t dout, int64_t axis) {
+  API_TRY
+  int64_t y_bc = malus_std_expand_axis_fwd(y, x, axis);
+  int64_t mask = malus_std_eq_fwd(x, y_bc);
+  int64_t d_bc = malus_std_expand_axis_fwd(dout, x, axis);
+  int64_t r = malus_std_broadcast_mul_fwd(d_bc, mask);
+  release(T(y_bc)); release(T(mask)); release(T(d_bc));
+  return r;
+  API_CATCH(0)
+}
+int64_t malus_std_reduce_var_axis_bwd(int64_t x, int64_t dout, int64_t axis) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  int64_t mean_h = malus_std_reduce_fwd(k::R_MEAN, x, axis, 1);
+  int64_t mean_bc = malus_std_expand_axis_fwd(mean_h, x, axis);
+  int64_t xm = malus_std_broadcast_sub_fwd(x, mean_bc);
+  float n_f = (float)t->shape[norm_axis(axis, t->ndim)];
+  int64_t scaled = malus_std_scale_fwd(xm, 2.0f / n_f);
+  int64_t d_bc = malus_std_expand_axis_fwd(dout, x, axis);
+  int64_t r = malus_std_broadcast_mul_fwd(d_bc, scaled);
+  release(T(mean_h)); release(T(mean_bc)); release(T(xm)); release(T(scaled)); release(T(d_bc));
+  return r;
+  API_CATCH(0)
+}
+
+// ---- transformer VJPs (transformer_bwd.ml) -------------------------------------------
+int64_t malus_std_softmax_bwd(int64_t s, int64_t dout, int64_t axis) {
+  API_TRY
+  TensorBuffer *ts = T(s), *td = T(dout);
+  if (!same_shape(ts, td)) fail("malus: softmax VJP shape mismatch %s vs %s", shape_str(ts).c_str(), shape_str(td).c_str());
+  size_t o, a, in;
+  split_axis(ts, norm_axis(axis, ts->ndim), &o, &a, &in);
+  TensorBuffer* out = alloc_like(ts);
+  k::softmax_bwd(ts->f32(), td->f32(), out->f32(), o, a, in, stream());
+  return done(out, "softmax_bwd");
+  API_CATCH(0)
+}
+// tape.rs:1162-1186 (per-row variance broadcast correctly; see layernorm.ml:71)
+int64_t malus_std_layernorm_bwd(int64_t y, int64_t var, int64_t dout, int64_t axis) {
+  API_TRY
+  TensorBuffer *ty = T(y), *tv = T(var), *td = T(dout);
+  int ax = norm_axis(axis, ty->ndim);
+  size_t o, a, in;
+  split_axis(ty, ax, &o, &a, &in);
+  if (tv->len != o * in) fail("malus: layernorm VJP expects a keepdim variance of %zu elements, got %zu", o * in, tv->len);
+  TensorBuffer* out = alloc_like(ty);
+  k::layernorm_bwd(ty->f32(), tv->f32(), td->f32(), out->f32(), o, a, in, 1e-5f, stream());
+  return done(out, "layernorm_bwd");
+  API_CATCH(0)
+}
+int64_t malus_std_cross_entropy_bwd(int64_t probs, int64_t targets, int64_t dout) {
+  API_TRY
+  TensorBuffer *p = T(probs), *tg = T(targets), *d = T(dout);
+  bool owned;
+  TensorBuffer* ti = as_i32_indices(tg, &owned);
+  TensorBuffer* out = alloc_like(p);
+  k::ce_bwd(p->f32(), ti->i32(), d->f32(), 0.0f, out->f32(), p->shape[0], p->shape[1], stream());
+  return done(out, "cross_entropy_bwd");
+  API_CATCH(0)
+}
+int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout) {
+  API_TRY
+  TensorBuffer *w = T(weight), *idx = T(indices), *d = T(dout);
+  bool owned;
+  TensorBuffer* ii = as_i32_indices(idx, &owned);
+  TensorBuffer* out = alloc_tensor(F32, w->shape, 2);
+  k::embedding_bwd(d->f32(), ii->i32(), out->f32(), idx->len, w->shape[0], w->shape[1], stream());
+  return done(out, "embedding_bwd");
+  API_CATCH(0)
+}
+
+// ---- matmul (metal.rs:820-962) and its VJPs (matmul_bwd.ml:15-29) ---------------------
+int64_t tensor_matmul(int64_t ha, int64_t hb) {
+  API_TRY
+  TensorBuffer *a = T(ha), *b = T(hb);
+  need_f32(a, "matmul");
+  need_f32(b, "matmul");
+  if (a->ndim == 2 && b->ndim == 2) {
+    size_t m = a->shape[0], k = a->shape[1], k2 = b->shape[0], n = b->shape[1];
+    if (k != k2)
+      fail("malus: matmul shape mismatch: [%zux%zu] @ [%zux%zu] - inner dims %zu != %zu\n  left shape:  %s\n  right shape: %s",
+           m, k, k2, n, k, k2, shape_str(a).c_str(), shape_str(b).c_str());
+    size_t osh[2] = {m, n};
+    return gemm_out(a, b, false, false, 1, (int)m, (int)n, (int)k, 0, 0, osh, 2);
+  }
+  if (a->ndim == 3 && b->ndim == 3) {
+    size_t bt = a->shape[0], m = a->shape[1], k = a->shape[2], bt2 = b->shape[0], k2 = b->shape[1], n = b->shape[2];
+    if (bt != bt2)
+      fail("malus: batched matmul batch dims must match: %zu vs %zu\n  left shape:  %s\n  right shape: %s", bt, bt2,
+           shape_str(a).c_str(), shape_str(b).c_str());
+    if (k != k2)
+      fail("malus: batched matmul inner dims must match: %zu vs %zu\n  left shape:  %s\n  right shape: %s", k, k2,
+           shape_str(a).c_str(), shape_str(b).c_str());
+    size_t osh[3] = {bt, m, n};
+    return gemm_out(a, b, false, false, (int)bt, (int)m, (int)n, (int)k, (long)(m * k), (long)(k * n), osh, 3);
+  }
+  if (a->ndim == 3 && b->ndim == 2) {  // weight broadcast over the batch: one [B*M, K] GEMM
+    size_t bt = a->shape[0], m = a->shape[1], k = a->shape[2], k2 = b->shape[0], n = b->shape[1];
+    if (k != k2)
+      fail("malus: matmul shape mismatch: [%zux%zux%zu] @ [%zux%zu] - inner dims %zu != %zu\n  left shape:  %s\n  right shape: %s",
+           bt, m, k, k2, n, k, k2, shape_str(a).c_str(), shape_str(b).c_str());
+    size_t osh[3] = {bt, m, n};
+    return gemm_out(a, b, false, false, 1, (int)(bt * m), (int)n, (int)k, 0, 0, osh, 3);
+  }
+  fail("malus: tensor_matmul requires both inputs to be 2-D, both 3-D, or (3-D, 2-D)\n  left shape:  %s\n  right shape: %s",
+       shape_str(a).c_str(), shape_str(b).c_str());
+  API_CATCH(0)
+}
+
+// dA = dout @ op(B)^T
+int64_t malus_std_matmul_bwd_a(int64_t ha, int64_t hb, int64_t hd) {
+  API_TRY
+  TensorBuffer *a = T(ha), *b = T(hb), *d = T(hd);
+  if (b->ndim == 3) {  // 3x3: dout[b] @ B[b]^T
+    size_t bt = d->shape[0], m = d->shape[1], n = d->shape[2], k = b->shape[1];
+    return gemm_out(d, b, false, true, (int)bt, (int)m, (int)k, (int)n, (long)(m * n), (long)(k * n), a->shape, a->ndim);
+  }
+  // b is 2-D [K, N]; dout is [.., N] flattened to rows
+  size_t n = b->shape[1], k = b->shape[0], rows = d->len / n;
+  return gemm_out(d, b, false, true, 1, (int)rows, (int)k, (int)n, 0, 0, a->shape, a->ndim);
+  API_CATCH(0)
+}
+
+// dB = op(A)^T @ dout (the 3x2 case sums over the batch inside one GEMM)
+int64_t malus_std_matmul_bwd_b(int64_t ha, int64_t hb, int64_t hd) {
+  API_TRY
+  TensorBuffer *a = T(ha), *b = T(hb), *d = T(hd);
+  if (a->ndim == 3 && b->ndim == 3) {
+    size_t bt = a->shape[0], m = a->shape[1], k = a->shape[2], n = d->shape[2];
+    return gemm_out(a, d, true, false, (int)bt, (int)k, (int)n, (int)m, (long)(m * k), (long)(m * n), b->shape, b->ndim);
+  }
+  // A flattened to [rows, K] (2-D, or 3-D with B broadcast): A^T @ dout[rows, N]
+  size_t k = a->shape[a->ndim - 1], rows = a->len / k, n = d->shape[d->ndim - 1];
+  return gemm_out(a, d, true, false, 1, (int)k, (int)n, (int)rows, 0, 0, b->shape, b->ndim);
+  API_CATCH(0)
+}
+
+// ---- fused optimizer ------------------------------------------------------------------------
+// examples/nanogpt_modular.ml:97-108 ("AdamW" with coupled L2).  Returns the
+// new parameter; *m_out / *v_out receive the new moments.
+int64_t malus_std_adam_l2(int64_t p, int64_t g, int64_t m, int64_t v, float lr, float b1, float b2, float eps, float wd,
+                          int64_t t, int64_t* m_out, int64_t* v_out) {
+  API_TRY
+  TensorBuffer *tp = T(p), *tg = T(g), *tm = T(m), *tv = T(v);
+  if (tg->len != tp->len || tm->len != tp->len || tv->len != tp->len) fail("malus: adam update: length mismatch");
+  float bc1 = 1.0f - powf(b1, (float)t);  // `opt.beta1 ** t`: f32 powf (codegen-cpu/lib.rs:275)
+  float bc2 = 1.0f - powf(b2, (float)t);
+  TensorBuffer* po = alloc_like(tp);
+  TensorBuffer* mo = alloc_like(tp);
+  TensorBuffer* vo = alloc_like(tp);
+  k::adam_l2(tp->f32(), tg->f32(), tm->f32(), tv->f32(), po->f32(), mo->f32(), vo->f32(), tp->len, lr, b1, b2,
+             1.0f - b1, 1.0f - b2, bc1, bc2, eps, wd, stream());
+  uint64_t seq = enqueue_mark("adam");
+  po->write_seq = mo->write_seq = vo->write_seq = seq;
+  *m_out = H(mo);
+  *v_out = H(vo);
+  return H(po);
+  API_CATCH(0)
+}
+
+}  // extern "C"

@@ -1,0 +1,438 @@
+// Define-by-run autograd tape: a C++ restatement of
+// crates/malus-runtime/src/tape.rs (OpTag 14-79, BwdSlot 92-175, records
+// 206-373, backward 421-729, grad registry 391-411 and 731-789).  The
+// numbering of OpTag and BwdSlot is part of the ABI (the JIT emits the tags
+// and registers slot pointers), so it is kept identical.  Every VJP runs
+// through the registered slot function; by default the slots hold this
+// library's stdlib host functions, and a JIT can overwrite them through
+// tape_register_backward_fn exactly as compile_and_run does.
+#include <cstdint>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "api.h"
+#include "common.h"
+
+namespace malus {
+namespace {
+
+enum OpTag : int32_t {
+  Matmul = 0, Add = 1, Sub = 2, Mul = 3, Div = 4, Sigmoid = 5, Relu = 6, Tanh = 7, Exp = 8, Log = 9, Sqrt = 10,
+  Abs = 11, Sum = 12, Transpose = 13, Neg = 14, ReduceSumAxis = 15, ReduceMeanAxis = 16, ReduceMaxAxis = 17,
+  ReduceVarAxis = 18, Reshape = 19, Softmax = 20, Layernorm = 21, Gelu = 22, CrossEntropy = 23, Embedding = 24
+};
+
+enum BwdSlot : int32_t {
+  AddBwdA = 0, AddBwdB, SubBwdA, SubBwdB, MulBwdA, MulBwdB, DivBwdA, DivBwdB, SigmoidBwd, ReluBwd, TanhBwd, ExpBwd,
+  LogBwd, SqrtBwd, AbsBwd, NegBwd, SumBwd, PermuteNdFwd, ReduceSumAxisBwd, ReduceMeanAxisBwd, ReduceMaxAxisBwd,
+  ReduceVarAxisBwd, SoftmaxBwd, LayernormBwd, GeluBwd, CrossEntropyBwd, EmbeddingBwd, MatmulBwdA, MatmulBwdB, GradAcc,
+  kNumSlots
+};
+
+struct TapeNode {
+  int32_t op;
+  std::vector<int64_t> saved;
+  int64_t output;
+  std::vector<int64_t> meta;
+};
+
+// Thread-local state, tape.rs:132-134 and 194-202.
+thread_local bool t_recording = true;
+thread_local std::vector<TapeNode> t_nodes;
+thread_local std::unordered_set<int64_t> t_leaves;
+thread_local std::unordered_map<int64_t, int64_t> t_leaf_grad;
+thread_local size_t t_slots[kNumSlots] = {0};
+thread_local bool t_slots_init = false;
+
+void check_tag(int32_t tag) {
+  if (tag < 0 || tag > Embedding) fail("malus: unknown op tag %d", tag);
+}
+
+void ensure_slots();
+
+size_t slot(int32_t s) {
+  ensure_slots();
+  size_t p = t_slots[s];
+  if (!p)
+    fail("malus: backward kernel slot %d not registered - every stdlib backward fn must be registered before backward()", s);
+  return p;
+}
+
+template <class F>
+F slot_fn(int32_t s) {
+  return reinterpret_cast<F>(slot(s));
+}
+
+using Fn1 = int64_t (*)(int64_t);
+using Fn2 = int64_t (*)(int64_t, int64_t);
+using Fn3 = int64_t (*)(int64_t, int64_t, int64_t);
+using Fn4 = int64_t (*)(int64_t, int64_t, int64_t, int64_t);
+using FnNeg = int64_t (*)(int64_t, float);
+using FnPerm = int64_t (*)(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t);
+
+int64_t grad_acc(int64_t old_g, int64_t new_g) { return slot_fn<Fn2>(GradAcc)(old_g, new_g); }
+
+// tape.rs:815-828: take ownership of new_grad, fold it into grads[input].
+void accumulate(std::unordered_map<int64_t, int64_t>& grads, int64_t input, int64_t new_grad) {
+  auto it = grads.find(input);
+  if (it == grads.end()) {
+    grads.emplace(input, new_grad);
+    return;
+  }
+  int64_t old = it->second;
+  int64_t summed = grad_acc(old, new_grad);
+  release(T(old));
+  release(T(new_grad));
+  it->second = summed;
+}
+
+// normalize_perm / invert_perm (metal.rs:1275-1325)
+std::vector<size_t> normalize_perm(const std::vector<size_t>& raw, size_t rank) {
+  if (raw.empty()) {
+    if (rank != 2) fail("malus: transpose() with no dim args requires a 2-D tensor, got rank %zu", rank);
+    return {1, 0};
+  }
+  if (raw.size() == 2) {
+    size_t i = raw[0], j = raw[1];
+    if (i >= rank || j >= rank) fail("malus: transpose axis %zu or %zu out of range for rank-%zu tensor", i, j, rank);
+    std::vector<size_t> p(rank);
+    for (size_t k = 0; k < rank; ++k) p[k] = k;
+    std::swap(p[i], p[j]);
+    return p;
+  }
+  if (raw.size() == rank) {
+    std::vector<bool> seen(rank, false);
+    for (size_t p : raw) {
+      if (p >= rank) fail("malus: permute dim %zu out of range for rank-%zu tensor", p, rank);
+      if (seen[p]) fail("malus: permute has duplicate dim %zu", p);
+      seen[p] = true;
+    }
+    return raw;
+  }
+  fail("malus: permute/transpose got %zu dim args for rank-%zu tensor; expected 0 (reverse 2-D), 2 (swap two axes), or %zu "
+       "(full permute)",
+       raw.size(), rank, rank);
+}
+
+int64_t permute_nd(int64_t h, const std::vector<size_t>& perm) {
+  if (perm.size() > 8) fail("malus: permute supports rank <= 8, got rank %zu", perm.size());
+  int64_t p[8] = {0};
+  for (size_t i = 0; i < perm.size(); ++i) p[i] = (int64_t)perm[i];
+  return slot_fn<FnPerm>(PermuteNdFwd)(h, p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]);
+}
+
+}  // namespace
+
+std::vector<size_t> tape_normalize_perm(const std::vector<size_t>& raw, size_t rank) { return normalize_perm(raw, rank); }
+
+void tape_on_release(int64_t handle) {
+  // tape.rs:783-789
+  auto it = t_leaf_grad.find(handle);
+  int64_t g = 0;
+  if (it != t_leaf_grad.end()) {
+    g = it->second;
+    t_leaf_grad.erase(it);
+  }
+  t_leaves.erase(handle);
+  if (g) release(T(g));
+}
+
+namespace {
+void ensure_slots() {
+  if (t_slots_init) return;
+  t_slots_init = true;
+  auto reg = [](int32_t s, auto fn) { if (!t_slots[s]) t_slots[s] = reinterpret_cast<size_t>(fn); };
+  reg(AddBwdA, &malus_std_add_bwd_a);
+  reg(AddBwdB, &malus_std_add_bwd_b);
+  reg(SubBwdA, &malus_std_sub_bwd_a);
+  reg(SubBwdB, &malus_std_sub_bwd_b);
+  reg(MulBwdA, &malus_std_mul_bwd_a);
+  reg(MulBwdB, &malus_std_mul_bwd_b);
+  reg(DivBwdA, &malus_std_div_bwd_a);
+  reg(DivBwdB, &malus_std_div_bwd_b);
+  reg(SigmoidBwd, &malus_std_sigmoid_bwd);
+  reg(ReluBwd, &malus_std_relu_bwd);
+  reg(TanhBwd, &malus_std_tanh_bwd);
+  reg(ExpBwd, &malus_std_broadcast_mul_fwd);  // BWD_SLOT_FNS (codegen-cpu/lib.rs:201): dout * e
+  reg(LogBwd, &malus_std_broadcast_div_fwd);  // dout / x
+  reg(SqrtBwd, &malus_std_sqrt_bwd);
+  reg(AbsBwd, &malus_std_abs_bwd);
+  reg(NegBwd, &malus_std_scale_fwd);
+  reg(SumBwd, &malus_std_sum_bwd);
+  reg(PermuteNdFwd, &malus_std_permute_nd_fwd);
+  reg(ReduceSumAxisBwd, &malus_std_reduce_sum_axis_bwd);
+  reg(ReduceMeanAxisBwd, &malus_std_reduce_mean_axis_bwd);
+  reg(ReduceMaxAxisBwd, &malus_std_reduce_max_axis_bwd);
+  reg(ReduceVarAxisBwd, &malus_std_reduce_var_axis_bwd);
+  reg(SoftmaxBwd, &malus_std_softmax_bwd);
+  reg(LayernormBwd, &malus_std_layernorm_bwd);
+  reg(GeluBwd, &malus_std_gelu_bwd);
+  reg(CrossEntropyBwd, &malus_std_cross_entropy_bwd);
+  reg(EmbeddingBwd, &malus_std_embedding_bwd);
+  reg(MatmulBwdA, &malus_std_matmul_bwd_a);
+  reg(MatmulBwdB, &malus_std_matmul_bwd_b);
+  reg(GradAcc, &malus_std_broadcast_add_fwd);  // codegen-cpu/lib.rs:219
+}
+}  // namespace
+
+void register_default_backward_fns() { ensure_slots(); }
+
+}  // namespace malus
+
+using namespace malus;
+
+extern "C" {
+
+void tape_register_backward_fn(int32_t s, size_t fnptr) {
+  API_TRY
+  if (s < 0 || s >= kNumSlots) fail("malus: backward slot %d out of range", s);
+  ensure_slots();
+  t_slots[s] = fnptr;
+  API_CATCH()
+}
+
+size_t malus_tape_backward_fn(int32_t s) {
+  if (s < 0 || s >= kNumSlots) return 0;
+  ensure_slots();
+  return t_slots[s];
+}
+
+void tape_record_binop(int32_t op, int64_t a, int64_t b, int64_t out) {
+  API_TRY
+  if (!t_recording) return;
+  check_tag(op);
+  retain(T(a)); retain(T(b)); retain(T(out));
+  t_nodes.push_back({op, {a, b}, out, {}});
+  API_CATCH()
+}
+
+void tape_record_unary(int32_t op, int64_t x, int64_t out) {
+  API_TRY
+  if (!t_recording) return;
+  check_tag(op);
+  retain(T(x)); retain(T(out));
+  t_nodes.push_back({op, {x}, out, {}});
+  API_CATCH()
+}
+
+void tape_record_reduce(int32_t op, int64_t x, int64_t out, int64_t axis, int64_t keepdim) {
+  API_TRY
+  if (!t_recording) return;
+  check_tag(op);
+  retain(T(x)); retain(T(out));
+  t_nodes.push_back({op, {x}, out, {axis, keepdim}});
+  API_CATCH()
+}
+
+void tape_record_perm(int32_t op, int64_t x, int64_t out, const size_t* dims, size_t ndims) {
+  API_TRY
+  if (!t_recording) return;
+  check_tag(op);
+  retain(T(x)); retain(T(out));
+  std::vector<int64_t> meta;
+  if (dims && ndims)
+    for (size_t i = 0; i < ndims; ++i) meta.push_back((int64_t)dims[i]);
+  t_nodes.push_back({op, {x}, out, meta});
+  API_CATCH()
+}
+
+// var_h: ownership transferred from the caller (tape.rs:289-310)
+void tape_record_layernorm(int32_t op, int64_t x, int64_t out, int64_t var_h, int64_t axis) {
+  API_TRY
+  if (!t_recording) { release(T(var_h)); return; }
+  check_tag(op);
+  retain(T(x)); retain(T(out));
+  t_nodes.push_back({op, {x, var_h}, out, {axis}});
+  API_CATCH()
+}
+
+// softmax_h: ownership transferred (tape.rs:312-337)
+void tape_record_cross_entropy(int32_t op, int64_t logits, int64_t out, int64_t softmax_h, int64_t targets) {
+  API_TRY
+  if (!t_recording) { release(T(softmax_h)); return; }
+  check_tag(op);
+  retain(T(logits)); retain(T(out)); retain(T(targets));
+  t_nodes.push_back({op, {logits, softmax_h, targets}, out, {}});
+  API_CATCH()
+}
+
+void tape_record_embedding(int32_t op, int64_t weight, int64_t indices, int64_t out) {
+  API_TRY
+  if (!t_recording) return;
+  check_tag(op);
+  retain(T(weight)); retain(T(indices)); retain(T(out));
+  t_nodes.push_back({op, {weight, indices}, out, {}});
+  API_CATCH()
+}
+
+void tape_register_leaf(int64_t h) { t_leaves.insert(h); }
+void tape_pause(void) { t_recording = false; }
+void tape_resume(void) { t_recording = true; }
+
+void tape_clear(void) {
+  API_TRY
+  std::vector<TapeNode> nodes;
+  nodes.swap(t_nodes);
+  for (auto& n : nodes) {
+    for (int64_t h : n.saved) release(T(h));
+    release(T(n.output));
+  }
+  API_CATCH()
+}
+
+int64_t tape_get_grad(int64_t h) {
+  API_TRY
+  auto it = t_leaf_grad.find(h);
+  if (it != t_leaf_grad.end()) {
+    retain(T(it->second));
+    return it->second;
+  }
+  TensorBuffer* t = T(h);
+  TensorBuffer* z = alloc_tensor(F32, t->shape, t->ndim);
+  k::fill(z->f32(), 0.0f, z->len, stream());
+  z->write_seq = enqueue_mark("zeros_like");
+  return H(z);
+  API_CATCH(0)
+}
+
+size_t malus_tape_len(void) { return t_nodes.size(); }
+void malus_tape_registry_lens(size_t* out2) { out2[0] = t_leaves.size(); out2[1] = t_leaf_grad.size(); }
+
+// tape.rs:421-729
+void backward(int64_t loss) {
+  API_TRY
+  std::vector<TapeNode> nodes = t_nodes;  // snapshot
+  std::unordered_map<int64_t, int64_t> grads;
+  {
+    TensorBuffer* lt = T(loss);
+    TensorBuffer* seed = alloc_tensor(F32, lt->shape, lt->ndim);
+    k::fill(seed->f32(), 1.0f, seed->len, stream());
+    seed->write_seq = enqueue_mark("seed");
+    grads.emplace(loss, H(seed));
+  }
+  for (auto it = nodes.rbegin(); it != nodes.rend(); ++it) {
+    const TapeNode& n = *it;
+    auto g = grads.find(n.output);
+    if (g == grads.end()) continue;
+    const int64_t dout = g->second;
+    switch (n.op) {
+      case Matmul: {
+        int64_t a = n.saved[0], b = n.saved[1];
+        int64_t da = slot_fn<Fn3>(MatmulBwdA)(a, b, dout);
+        int64_t db = slot_fn<Fn3>(MatmulBwdB)(a, b, dout);
+        accumulate(grads, a, da);
+        accumulate(grads, b, db);
+        break;
+      }
+      case Add: case Sub: {
+        int64_t a = n.saved[0], b = n.saved[1];
+        int32_t sa = n.op == Add ? AddBwdA : SubBwdA, sb = n.op == Add ? AddBwdB : SubBwdB;
+        int64_t da = slot_fn<Fn2>(sa)(dout, a);
+        int64_t db = slot_fn<Fn2>(sb)(dout, b);
+        accumulate(grads, a, da);
+        accumulate(grads, b, db);
+        break;
+      }
+      case Mul: case Div: {
+        int64_t a = n.saved[0], b = n.saved[1];
+        int32_t sa = n.op == Mul ? MulBwdA : DivBwdA, sb = n.op == Mul ? MulBwdB : DivBwdB;
+        int64_t da = slot_fn<Fn3>(sa)(dout, a, b);
+        int64_t db = slot_fn<Fn3>(sb)(dout, a, b);
+        accumulate(grads, a, da);
+        accumulate(grads, b, db);
+        break;
+      }
+      case Sigmoid: accumulate(grads, n.saved[0], slot_fn<Fn2>(SigmoidBwd)(n.output, dout)); break;
+      case Relu: accumulate(grads, n.saved[0], slot_fn<Fn2>(ReluBwd)(n.saved[0], dout)); break;
+      case Tanh: accumulate(grads, n.saved[0], slot_fn<Fn2>(TanhBwd)(n.output, dout)); break;
+      case Exp: accumulate(grads, n.saved[0], slot_fn<Fn2>(ExpBwd)(dout, n.output)); break;
+      case Log: accumulate(grads, n.saved[0], slot_fn<Fn2>(LogBwd)(dout, n.saved[0])); break;
+      case Sqrt: accumulate(grads, n.saved[0], slot_fn<Fn2>(SqrtBwd)(n.output, dout)); break;
+      case Abs: accumulate(grads, n.saved[0], slot_fn<Fn2>(AbsBwd)(n.saved[0], dout)); break;
+      case Sum: accumulate(grads, n.saved[0], slot_fn<Fn2>(SumBwd)(n.saved[0], dout)); break;
+      case Transpose: {
+        int64_t x = n.saved[0];
+        std::vector<size_t> raw;
+        for (int64_t v : n.meta) raw.push_back((size_t)v);
+        std::vector<size_t> perm = normalize_perm(raw, (size_t)T(x)->ndim);
+        std::vector<size_t> inv(perm.size());
+        for (size_t i = 0; i < perm.size(); ++i) inv[perm[i]] = i;
+        accumulate(grads, x, permute_nd(dout, inv));
+        break;
+      }
+      case Reshape: {
+        int64_t x = n.saved[0];
+        accumulate(grads, x, H(make_alias(T(dout), T(x)->shape, T(x)->ndim)));
+        break;
+      }
+      case Neg: accumulate(grads, n.saved[0], slot_fn<FnNeg>(NegBwd)(dout, -1.0f)); break;
+      case ReduceSumAxis: accumulate(grads, n.saved[0], slot_fn<Fn3>(ReduceSumAxisBwd)(n.saved[0], dout, n.meta[0])); break;
+      case ReduceMeanAxis: accumulate(grads, n.saved[0], slot_fn<Fn3>(ReduceMeanAxisBwd)(n.saved[0], dout, n.meta[0])); break;
+      case ReduceMaxAxis:
+        accumulate(grads, n.saved[0], slot_fn<Fn4>(ReduceMaxAxisBwd)(n.saved[0], n.output, dout, n.meta[0]));
+        break;
+      case ReduceVarAxis: accumulate(grads, n.saved[0], slot_fn<Fn3>(ReduceVarAxisBwd)(n.saved[0], dout, n.meta[0])); break;
+      case Softmax: accumulate(grads, n.saved[0], slot_fn<Fn3>(SoftmaxBwd)(n.output, dout, n.meta[0])); break;
+      case Layernorm:
+        accumulate(grads, n.saved[0], slot_fn<Fn4>(LayernormBwd)(n.output, n.saved[1], dout, n.meta[0]));
+        break;
+      case Gelu: accumulate(grads, n.saved[0], slot_fn<Fn2>(GeluBwd)(n.saved[0], dout)); break;
+      case CrossEntropy:
+        accumulate(grads, n.saved[0], slot_fn<Fn3>(CrossEntropyBwd)(n.saved[1], n.saved[2], dout));
+        break;
+      case Embedding: accumulate(grads, n.saved[0], slot_fn<Fn3>(EmbeddingBwd)(n.saved[0], n.saved[1], dout)); break;
+      default: fail("malus: backward: unhandled op tag %d", n.op);
+    }
+  }
+  // fold leaf grads into the persistent registry (tape.rs:694-721)
+  std::vector<int64_t> to_release;
+  for (int64_t leaf : t_leaves) {
+    auto g = grads.find(leaf);
+    if (g == grads.end()) continue;
+    int64_t new_g = g->second;
+    grads.erase(g);
+    auto old = t_leaf_grad.find(leaf);
+    if (old == t_leaf_grad.end()) {
+      t_leaf_grad.emplace(leaf, new_g);
+    } else {
+      int64_t summed = grad_acc(old->second, new_g);
+      to_release.push_back(old->second);
+      to_release.push_back(new_g);
+      old->second = summed;
+    }
+  }
+  for (int64_t h : to_release) release(T(h));
+  for (auto& kv : grads) release(T(kv.second));
+  tape_clear();
+  API_CATCH()
+}
+
+void tape_reset(void) {
+  API_TRY
+  t_leaves.clear();
+  std::vector<int64_t> gs;
+  for (auto& kv : t_leaf_grad) gs.push_back(kv.second);
+  t_leaf_grad.clear();
+  for (int64_t g : gs) release(T(g));
+  tape_clear();
+  t_recording = true;
+  API_CATCH()
+}
+
+void tape_zero_grad(const int64_t* handles, size_t count) {
+  API_TRY
+  if (!handles || !count) return;
+  std::vector<int64_t> rel;
+  for (size_t i = 0; i < count; ++i) {
+    auto it = t_leaf_grad.find(handles[i]);
+    if (it != t_leaf_grad.end()) {
+      rel.push_back(it->second);
+      t_leaf_grad.erase(it);
+    }
+  }
+  for (int64_t g : rel) release(T(g));
+  API_CATCH()
+}
+
+}  // extern "C"

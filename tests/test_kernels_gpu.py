@@ -1,0 +1,324 @@
+"""GPU parity tests: each stdlib op through the C ABI vs the CPU oracle.
+
+Run on the MI355X box (``-m gpu``).  Inputs are seeded; sizes keep the oracle
+in seconds.  Tolerances: see tests/helpers.py.
+"""
+import ctypes as C
+import itertools
+
+import numpy as np
+import pytest
+
+import malus_amd as M
+from oracle import oracle as O
+from tests.helpers import assert_bitexact, assert_normwise, assert_reduction, assert_ulp
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(1234)
+
+
+def rand(*shape, lo=-1.0, hi=1.0):
+    return RNG.uniform(lo, hi, size=shape).astype(np.float32)
+
+
+def run(rt, h):
+    out = rt.numpy(h)
+    rt.free(h)
+    return out
+
+
+# ---------------------------------------------------------------- elementwise
+@pytest.mark.parametrize("op", [M.ADD, M.SUB, M.MUL, M.DIV])
+@pytest.mark.parametrize("shapes", [((1000003,), (1000003,)), ((257, 64), (64,)), ((6, 5, 7), (5, 7)),
+                                    ((384, 16, 16), (16, 16)), ((33, 65), (1, 65)), ((8, 9, 10), (1, 1)),
+                                    ((4, 1, 3), (5, 1)), ((1, 4), (3, 4)), ((7,), (3, 7))])
+def test_broadcast_binop(rt, op, shapes):
+    a, b = rand(*shapes[0]), rand(*shapes[1], lo=0.5, hi=2.0)
+    ha, hb = rt.tensor(a), rt.tensor(b)
+    got = run(rt, rt.L.malus_std_broadcast_fwd(op, ha, hb))
+    want = O.broadcast(op, a, b)
+    assert_bitexact(got, want, f"op {op} {shapes}")
+    rt.free(ha, hb)
+
+
+def test_broadcast_operand_swap_quirk(rt):
+    # broadcast_binop.ml:90-112: rank(a) < rank(b) computes b - a
+    a, b = rand(8), rand(4, 8)
+    ha, hb = rt.tensor(a), rt.tensor(b)
+    got = run(rt, rt.L.malus_std_broadcast_fwd(M.SUB, ha, hb))
+    assert_bitexact(got, b - a, "swapped sub")
+    rt.free(ha, hb)
+
+
+@pytest.mark.parametrize("op,right", [(M.ADD, 1), (M.SUB, 1), (M.SUB, 0), (M.MUL, 1), (M.DIV, 1), (M.DIV, 0)])
+def test_scalar_ops(rt, op, right):
+    a = rand(100001, lo=0.25, hi=4.0)
+    ha = rt.tensor(a)
+    got = run(rt, rt.L.malus_std_scalar_op(op, ha, C.c_float(0.37), right))
+    assert_bitexact(got, O.scalar_op(op, a, np.float32(0.37), bool(right)), f"scalar op {op} right={right}")
+    rt.free(ha)
+
+
+@pytest.mark.parametrize("op,lo,hi,ulp", [(M.RELU, -3, 3, 0), (M.ABS, -3, 3, 0), (M.SQRT, 0, 100, 0),
+                                          (M.EXP, -20, 20, 2), (M.LOG, 1e-3, 1e3, 2), (M.TANH, -6, 6, 2),
+                                          (M.SIGMOID, -20, 20, 2)])
+def test_unary(rt, op, lo, hi, ulp):
+    x = rand(262147, lo=lo, hi=hi)
+    hx = rt.tensor(x)
+    got = run(rt, rt.L.malus_std_unary(op, hx))
+    assert_ulp(got, O.unary(op, x), ulp, f"unary {op}")
+    rt.free(hx)
+
+
+def test_gelu_fwd_bwd(rt):
+    # GELU = 0.5x(1 + tanh(g)): a 1-ulp difference in tanh near t = -1 is
+    # amplified by the cancellation in (1 + t); the bound is 2 ulp of the
+    # result plus the propagated 2-ulp tanh uncertainty 0.5|x| * 2ulp(1).
+    x = rand(200003, lo=-8, hi=8)
+    hx = rt.tensor(x)
+    got = run(rt, rt.L.malus_std_gelu_fwd(hx))
+    want = O.unary(O.GELU, x)
+    bound = 2 * np.spacing(np.abs(want)) + 0.5 * np.abs(x) * 2 * np.spacing(np.float32(1.0)) * 2
+    assert np.all(np.abs(got - want) <= bound), "gelu beyond the derived bound"
+    d = rand(200003)
+    hd = rt.tensor(d)
+    gb = run(rt, rt.L.malus_std_gelu_bwd(hx, hd))
+    wb = O.unary_bwd(O.GELU, x, d)
+    assert_normwise(gb, wb, 1e-5, "gelu bwd")
+    rt.free(hx, hd)
+
+
+@pytest.mark.parametrize("fn,op", [("malus_std_sigmoid_bwd", O.SIGMOID), ("malus_std_relu_bwd", O.RELU),
+                                   ("malus_std_tanh_bwd", O.TANH), ("malus_std_sqrt_bwd", O.SQRT),
+                                   ("malus_std_abs_bwd", O.ABS)])
+def test_unary_vjp_bitexact(rt, fn, op):
+    v = rand(65539, lo=0.1 if op == O.SQRT else -2, hi=2)
+    d = rand(65539)
+    hv, hd = rt.tensor(v), rt.tensor(d)
+    got = run(rt, getattr(rt.L, fn)(hv, hd))
+    assert_bitexact(got, O.unary_bwd(op, v, d), fn)
+    rt.free(hv, hd)
+
+
+# ---------------------------------------------------------------- reductions
+@pytest.mark.parametrize("shape,axis", [((65, 1024), 1), ((65, 1024), 0), ((3, 70001), 1), ((70001, 3), 0),
+                                        ((4, 5, 6), 1), ((4, 5, 6), 2), ((4, 5, 6), 0), ((2, 300, 50), -2),
+                                        ((1, 1), 0), ((17,), 0)])
+@pytest.mark.parametrize("op", [M.R_SUM, M.R_MEAN, M.R_MAX, M.R_VAR])
+def test_reduce_axis(rt, shape, axis, op):
+    x = rand(*shape, lo=-2, hi=2)
+    hx = rt.tensor(x)
+    got = run(rt, rt.L.malus_std_reduce_fwd(op, hx, axis, 1))
+    want = O.reduce_axis(op, x, axis, keepdim=True)
+    if len(shape) == 1:
+        want = want.reshape(1)
+    if op == M.R_MAX:
+        assert_bitexact(got, want, f"max {shape} {axis}")
+    else:
+        x64 = x.astype(np.float64)
+        exact = {M.R_SUM: x64.sum, M.R_MEAN: x64.mean, M.R_VAR: x64.var}[op](axis=axis, keepdims=True)
+        assert_reduction(got, want, exact.reshape(want.shape), 1e-5, f"reduce {op} {shape} {axis}")
+    rt.free(hx)
+
+
+def test_reduce_keepdim_shapes(rt):
+    x = rand(2, 3)
+    hx = rt.tensor(x)
+    for axis, keep, shape in [(0, 0, (3,)), (1, 1, (2, 1)), (0, 1, (1, 3)), (-1, 0, (2,))]:
+        h = rt.L.malus_std_reduce_fwd(M.R_SUM, hx, axis, keep)
+        assert rt.shape(h) == shape
+        rt.free(h)
+    rt.free(hx)
+
+
+def test_sum_all_over_1024_cap(rt):
+    x = rand(1 << 20)
+    hx = rt.tensor(x)
+    got = run(rt, rt.L.malus_std_reduce_all_sum_fwd(hx))
+    assert_reduction(got, [O.sum_all(x)], [x.astype(np.float64).sum()], 1e-5, "sum_all")
+    rt.free(hx)
+
+
+# ------------------------------------------------------- softmax / layernorm
+@pytest.mark.parametrize("shape,axis", [((37, 1024), 1), ((96, 256), 1), ((64, 65), 1), ((3, 5000), 1),
+                                        ((5, 7, 9), 1), ((6, 16, 16), 2), ((8, 3), 0)])
+def test_softmax_fwd_bwd(rt, shape, axis):
+    x = rand(*shape, lo=-4, hi=4)
+    d = rand(*shape)
+    hx, hd = rt.tensor(x), rt.tensor(d)
+    hy = rt.L.malus_std_softmax_fwd(hx, axis)
+    y = rt.numpy(hy)
+    ys = O.softmax(x, axis)
+    assert_normwise(y, ys, 1e-5, "softmax")
+    got = run(rt, rt.L.malus_std_softmax_bwd(hy, hd, axis))
+    assert_normwise(got, O.softmax_bwd(y, d, axis), 1e-5, "softmax bwd")
+    rt.free(hx, hd, hy)
+
+
+@pytest.mark.parametrize("shape,axis", [((65, 1024), 1), ((100, 384), 1), ((33, 128), 1), ((4, 70), 1),
+                                        ((3, 5000), 1), ((6, 8, 5), 1)])
+def test_layernorm_fwd_bwd(rt, shape, axis):
+    x = rand(*shape, lo=-3, hi=3) + 0.5
+    d = rand(*shape)
+    hx, hd = rt.tensor(x), rt.tensor(d)
+    hv = C.c_int64()
+    hy = rt.L.malus_std_layernorm_fwd(hx, axis, C.byref(hv))
+    y, var = rt.numpy(hy), rt.numpy(hv.value)
+    ys, vs = O.layernorm(x, axis)
+    assert_normwise(y, ys, 1e-5, "layernorm y")
+    assert_normwise(var, vs, 1e-5, "layernorm var")
+    assert var.shape == vs.shape
+    got = run(rt, rt.L.malus_std_layernorm_bwd(hy, hv.value, hd, axis))
+    assert_normwise(got, O.layernorm_bwd(y, var, d, axis), 1e-5, "layernorm bwd")
+    rt.free(hx, hd, hy, hv.value)
+
+
+def test_layernorm_kat(rt):
+    # metal_integration.rs:296-301 inputs
+    x = np.array([[1, 2, 3, 4, 5, 6, 7, 8], [.1, .2, .3, .4, .5, .6, .7, .8],
+                  [-3, -2, -1, 0, 1, 2, 3, 4], [10, 10.1, 9.9, 10.2, 9.8, 10.3, 9.7, 10.4]], np.float32)
+    hx = rt.tensor(x)
+    hy = rt.L.malus_std_layernorm_fwd(hx, 1, None)
+    got = run(rt, hy)
+    mu = x.mean(1, keepdims=True, dtype=np.float64)
+    ref = (x - mu) / np.sqrt(x.var(1, keepdims=True, dtype=np.float64) + 1e-5)
+    assert np.max(np.abs(got - ref)) < 1e-5
+    rt.free(hx)
+
+
+@pytest.mark.parametrize("n,v", [(50, 65), (20, 1024), (7, 5000)])
+def test_cross_entropy_fwd_bwd(rt, n, v):
+    logits = (RNG.standard_normal((n, v)) * 2).astype(np.float32)
+    t = RNG.integers(0, v, n).astype(np.int32)
+    hl, ht = rt.tensor(logits), rt.tensor(t)
+    hp = C.c_int64()
+    hloss = rt.L.malus_std_cross_entropy_fwd(hl, ht, C.byref(hp))
+    loss, probs = rt.numpy(hloss), rt.numpy(hp.value)
+    wl, wp = O.cross_entropy(logits, t)
+    assert_normwise(probs, wp, 1e-5, "probs")
+    assert_normwise(loss, np.array([wl]), 1e-5, "loss")
+    hd = rt.tensor(np.array([1.0], np.float32))
+    got = run(rt, rt.L.malus_std_cross_entropy_bwd(hp.value, ht, hd))
+    assert_normwise(got, O.cross_entropy_bwd(probs, t, 1.0), 1e-6, "ce bwd")
+    rt.free(hl, ht, hloss, hp.value, hd)
+
+
+# ------------------------------------------------------------ index ops
+@pytest.mark.parametrize("v,d,t", [(65, 384, 4096), (256, 384, 2048), (65, 65, 777), (4, 3, 4)])
+def test_embedding_fwd_bwd_bitexact(rt, v, d, t):
+    w = rand(v, d)
+    idx = RNG.integers(0, v, t).astype(np.int32)
+    dout = rand(t, d)
+    hw, hi, hd = rt.tensor(w), rt.tensor(idx), rt.tensor(dout)
+    got = run(rt, rt.L.malus_std_embedding_fwd(hw, hi))
+    assert_bitexact(got, O.embedding(w, idx), "embedding")
+    gb = run(rt, rt.L.malus_std_embedding_bwd(hw, hi, hd))
+    assert_bitexact(gb, O.embedding_bwd(dout, idx, v), "embedding bwd (token-ordered sums)")
+    rt.free(hw, hi, hd)
+
+
+def test_embedding_kat(rt):
+    # tests.rs:1388-1404: W = [[0,1,2],[3,4,5],[6,7,8],[9,10,11]], idx = [1,0,2]
+    w = np.arange(12, dtype=np.float32).reshape(4, 3)
+    hw, hi = rt.tensor(w), rt.tensor(np.array([1, 0, 2], np.int32))
+    assert run(rt, rt.L.malus_std_embedding_fwd(hw, hi)).ravel().tolist() == [3, 4, 5, 0, 1, 2, 6, 7, 8]
+    rt.free(hw, hi)
+
+
+@pytest.mark.parametrize("perm", list(itertools.permutations(range(4))))
+def test_permute_4d_bitexact(rt, perm):
+    x = rand(3, 4, 5, 8)
+    hx = rt.tensor(x)
+    got = run(rt, rt.L.tensor_permute(hx, M.sizes(perm), 4))
+    assert_bitexact(got, O.permute(x, perm), f"perm {perm}")
+    rt.free(hx)
+
+
+@pytest.mark.parametrize("shape", [(65, 130), (1, 7), (384, 64), (129, 257)])
+def test_transpose_2d(rt, shape):
+    x = rand(*shape)
+    hx = rt.tensor(x)
+    got = run(rt, rt.L.malus_std_transpose_2d_fwd(hx))
+    assert_bitexact(got, x.T.copy(), "transpose")
+    rt.free(hx)
+
+
+def test_permute_3d_batched_transpose(rt):
+    x = rand(384, 64, 256)
+    hx = rt.tensor(x)
+    got = run(rt, rt.L.malus_std_permute_3d_fwd(hx, 0, 2, 1))
+    assert_bitexact(got, np.ascontiguousarray(x.transpose(0, 2, 1)), "permute(0,2,1)")
+    rt.free(hx)
+
+
+# ------------------------------------------------------------------- matmul
+MM_SHAPES = [((2, 3), (3, 2)), ((1, 1), (1, 1)), ((65, 127), (127, 129)), ((128, 128), (128, 128)),
+             ((300, 384), (384, 65)), ((4, 8), (8, 1)), ((8, 64, 32), (8, 32, 48)), ((3, 5, 7), (7, 9)),
+             ((384, 1024), (1024, 384)), ((16384, 4), (4, 8))]
+
+
+@pytest.mark.parametrize("sa,sb", MM_SHAPES)
+def test_matmul_and_vjps(rt, sa, sb):
+    a, b = rand(*sa), rand(*sb)
+    ha, hb = rt.tensor(a), rt.tensor(b)
+    hc = rt.L.tensor_matmul(ha, hb)
+    c = rt.numpy(hc)
+    assert_normwise(c, O.matmul(a, b), 1e-5, f"matmul {sa}@{sb}")
+    d = rand(*c.shape)
+    hd = rt.tensor(d)
+    da = run(rt, rt.L.malus_std_matmul_bwd_a(ha, hb, hd))
+    db = run(rt, rt.L.malus_std_matmul_bwd_b(ha, hb, hd))
+    bt = O.permute(b, (0, 2, 1)) if b.ndim == 3 else O.permute(b, (1, 0))
+    wa = O.matmul(d, bt)
+    if a.ndim == 3 and b.ndim == 2:
+        # matmul_bwd.ml:28-29: reduce_sum(permute(a) @ dC, 0)
+        wb = O.reduce_axis(O.R_SUM, O.matmul(O.permute(a, (0, 2, 1)), d), 0)
+    elif a.ndim == 3:
+        wb = O.matmul(O.permute(a, (0, 2, 1)), d)
+    else:
+        wb = O.matmul(O.permute(a, (1, 0)), d)
+    assert_normwise(da, wa.reshape(a.shape), 1e-5, "dA")
+    assert_normwise(db, wb.reshape(b.shape), 1e-5, "dB")
+    rt.free(ha, hb, hc, hd)
+
+
+def test_matmul_kats(rt):
+    # tests.rs:207-240
+    ha = rt.tensor(np.array([[1, 2, 3], [4, 5, 6]], np.float32))
+    hb = rt.tensor(np.array([[1, 0], [0, 1], [1, 0]], np.float32))
+    assert run(rt, rt.L.tensor_matmul(ha, hb)).ravel().tolist() == [4, 2, 10, 5]
+    o1 = rt.L.tensor_alloc_ones_gpu(M.sizes([2, 3]), 2)
+    o2 = rt.L.tensor_alloc_ones_gpu(M.sizes([3, 4]), 2)
+    out = run(rt, rt.L.tensor_matmul(o1, o2))
+    assert out.shape == (2, 4) and np.all(out == 3.0)
+    rt.free(ha, hb, o1, o2)
+
+
+def test_matmul_split_k_weight_grad_shape(rt):
+    # dW of a C5 projection: [384, 16384] @ [16384, 384] through the TN path
+    x = rand(16384, 384)
+    d = rand(16384, 384)
+    w = rand(384, 384)
+    hx, hd, hw = rt.tensor(x), rt.tensor(d), rt.tensor(w)
+    got = run(rt, rt.L.malus_std_matmul_bwd_b(hx, hw, hd))
+    O.set_threads(8)
+    want = O.matmul(O.permute(x, (1, 0)), d)
+    assert_normwise(got, want, 1e-5, "split-K dW")
+    rt.free(hx, hd, hw)
+
+
+# ---------------------------------------------------------------- optimizer
+def test_adam_l2_fused_bitexact(rt):
+    n = 100003
+    p, g, m = rand(n), rand(n), rand(n) * 0.1
+    v = np.abs(rand(n)) * 0.01
+    hs = [rt.tensor(a) for a in (p, g, m, v)]
+    mo, vo = C.c_int64(), C.c_int64()
+    for t in (1, 7):
+        hp = rt.L.malus_std_adam_l2(*hs, 1e-3, 0.9, 0.99, 1e-8, 0.1, t, C.byref(mo), C.byref(vo))
+        wp, wm, wv = O.adam_l2(p, g, m, v, 1e-3, 0.9, 0.99, 1e-8, 0.1, t)
+        assert_bitexact(run(rt, hp), wp, "p'")
+        assert_bitexact(run(rt, mo.value), wm, "m'")
+        assert_bitexact(run(rt, vo.value), wv, "v'")
+    rt.free(*hs)

@@ -1,0 +1,174 @@
+"""End-to-end parity of the workload drivers against the CPU oracle:
+examples/xor.ml (C1), the toy char-nanoGPT (C4) and the Karpathy
+char-nanoGPT (C5).  Loss trajectories: within 1e-3 relative (north star);
+single-step gradients: normwise 1e-4 (per-op 1e-5 errors compound through
+~40 dependent ops per block)."""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import malus_amd as M
+from oracle import oracle as O
+from tests.helpers import normwise_err
+
+pytestmark = pytest.mark.gpu
+
+SIGMOID_BACKWARD_HIP = """
+extern "C" __global__ void malus_kernel_{id}(const float* grad_out, const float* sig_z, float* out, unsigned n) {{
+  unsigned tid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= n) return;
+  out[tid] = ((grad_out[tid] * sig_z[tid]) * (1.0f - sig_z[tid]));
+}}
+"""
+
+C4 = dict(V=65, T=64, C=128, H=4, L=4, B=32)
+C5 = dict(V=65, T=256, C=384, H=6, L=6, B=64)
+OPT = dict(lr=1e-3, b1=0.9, b2=0.99, eps=1e-8, wd=0.1)
+
+
+def oracle_threads():
+    return min(16, os.cpu_count() or 1)
+
+
+def test_xor_10000_steps_vs_oracle(rt):
+    kid = 9100
+    rt.L.malus_runtime_init((C.c_uint64 * 1)(kid), (C.c_char_p * 1)(SIGMOID_BACKWARD_HIP.format(id=kid).encode()), 1)
+    loss_at = np.zeros(6, np.float32)
+    preds = np.zeros(4, np.float32)
+    params = np.zeros(33, np.float32)
+    f = C.POINTER(C.c_float)
+    loss = rt.L.malus_xor_run(10000, 1.5, kid, loss_at.ctypes.data_as(f), preds.ctypes.data_as(f),
+                              params.ctypes.data_as(f))
+    wl, wla, wp, wparams = O.xor_train(10000, 1.5)
+    np.testing.assert_allclose(loss_at, wla, rtol=1e-3)
+    np.testing.assert_allclose(preds, wp, rtol=1e-3)
+    np.testing.assert_allclose(loss, wl, rtol=1e-3)
+    # README.md:66-67 golden (Metal, fast-math): soft check
+    np.testing.assert_allclose(preds, [0.0056860363, 0.99518234, 0.9939387, 0.005444207], rtol=1e-3)
+    np.testing.assert_allclose(loss, 0.00012191984, rtol=1e-3)
+
+
+class GpuGpt:
+    def __init__(self, rt, cfg, rng_call_idx=0, fused=True):
+        self.rt = rt
+        self.cfg = cfg
+        rt.L.tape_reset()
+        rt.L.malus_rng_set_counter(rng_call_idx)
+        self.g = rt.L.malus_gpt_create(cfg["V"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["B"], OPT["lr"],
+                                       OPT["b1"], OPT["b2"], OPT["eps"], OPT["wd"])
+        rt.L.malus_gpt_set_fused_optimizer(self.g, int(fused))
+
+    def close(self):
+        self.rt.L.malus_gpt_free(self.g)
+        self.rt.L.tape_reset()
+
+    def param(self, i):
+        return self.rt.numpy(self.rt.L.malus_gpt_param(self.g, i)).ravel()
+
+    def grad(self, i):
+        g = self.rt.L.tape_get_grad(self.rt.L.malus_gpt_param(self.g, i))
+        out = self.rt.numpy(g).ravel()
+        self.rt.free(g)
+        return out
+
+    def loss_and_grads(self, x, y):
+        rt = self.rt
+        hx, hy = rt.tensor(x), rt.tensor(y)
+        rt.L.malus_gpt_zero_grad(self.g)
+        loss = rt.L.malus_gpt_forward_loss(self.g, hx, hy)
+        rt.L.backward(loss)
+        v = rt.numpy(loss)[0]
+        rt.free(hx, hy, loss)
+        return v
+
+    def step(self, x, y, t):
+        rt = self.rt
+        hx, hy = rt.tensor(x), rt.tensor(y)
+        loss = rt.L.malus_gpt_step(self.g, hx, hy, t)
+        v = rt.numpy(loss)[0]
+        rt.free(hx, hy, loss)
+        return v
+
+
+def tokens(cfg, call_idx):
+    n = cfg["B"] * cfg["T"]
+    return O.rand_tokens(call_idx, n, cfg["V"]), O.rand_tokens(call_idx + n, n, cfg["V"])
+
+
+def test_gpt_init_matches_oracle_bitexact(rt):
+    g = GpuGpt(rt, C4)
+    og = O.Gpt(**C4)
+    try:
+        for i in range(og.nparams):
+            np.testing.assert_array_equal(g.param(i), og.param(i), err_msg=f"param {i}")
+    finally:
+        g.close()
+
+
+def test_gpt_c4_loss_and_grads_vs_oracle(rt):
+    g = GpuGpt(rt, C4)
+    og = O.Gpt(**C4)
+    O.set_threads(oracle_threads())
+    x, y = tokens(C4, 1 << 20)
+    try:
+        loss = g.loss_and_grads(x, y)
+        wloss = og.loss_and_grads(x, y)
+        assert abs(loss - wloss) <= 1e-5 * abs(wloss), (loss, wloss)
+        worst = max(normwise_err(g.grad(i), og.grad(i)) for i in range(og.nparams))
+        assert worst <= 1e-4, f"worst normwise gradient error {worst:.2e}"
+    finally:
+        g.close()
+
+
+def test_gpt_fused_optimizer_equals_op_by_op(rt):
+    cfg = dict(V=65, T=16, C=32, H=4, L=2, B=4)
+    x, y = tokens(cfg, 5000)
+    a, b = GpuGpt(rt, cfg, fused=True), None
+    try:
+        la = [a.step(x, y, t) for t in (1, 2)]
+        pa = [a.param(i) for i in range(8 * cfg["L"] + 4)]
+    finally:
+        a.close()
+    b = GpuGpt(rt, cfg, fused=False)
+    try:
+        lb = [b.step(x, y, t) for t in (1, 2)]
+        pb = [b.param(i) for i in range(8 * cfg["L"] + 4)]
+    finally:
+        b.close()
+    assert la == lb
+    for i, (u, v) in enumerate(zip(pa, pb)):
+        np.testing.assert_array_equal(u, v, err_msg=f"param {i}")
+
+
+def test_gpt_c4_200_step_loss_trajectory(rt):
+    g = GpuGpt(rt, C4)
+    og = O.Gpt(**C4)
+    O.set_threads(oracle_threads())
+    try:
+        worst = 0.0
+        for t in range(1, 201):
+            x, y = tokens(C4, 10_000_000 + 2 * 2048 * t)
+            lg = g.step(x, y, t)
+            lo = og.step(x, y, t)
+            worst = max(worst, abs(lg - lo) / abs(lo))
+            assert worst <= 1e-3, f"step {t}: {lg} vs {lo}"
+        print(f"C4 200-step worst relative loss difference {worst:.2e}")
+    finally:
+        g.close()
+
+
+def test_gpt_c5_one_step_vs_oracle(rt):
+    g = GpuGpt(rt, C5)
+    og = O.Gpt(**C5)
+    O.set_threads(oracle_threads())
+    x, y = tokens(C5, 1 << 24)
+    try:
+        loss = g.loss_and_grads(x, y)
+        wloss = og.loss_and_grads(x, y)
+        assert abs(loss - wloss) <= 1e-5 * abs(wloss), (loss, wloss)
+        worst = max(normwise_err(g.grad(i), og.grad(i)) for i in range(og.nparams))
+        assert worst <= 1e-4, f"worst normwise gradient error {worst:.2e}"
+    finally:
+        g.close()
