@@ -143,6 +143,10 @@ size_t malus_alloc_histogram(size_t* sizes, uint64_t* counts, size_t cap);
 
 /* ---- instrumentation and errors (no reference counterparts) ------------- */
 void malus_ktimer_enable(int on);
+/* Tuning: pin the GEMM block tile to (64*tm) x (64*tn); (0, 0) = automatic. */
+int malus_gemm_set_tile(int tm, int tn);
+/* Tuning: workgroups a split-K GEMM aims for; 0 = the cost model decides. */
+void malus_gemm_set_split(int target_blocks);
 int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
 int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
 void malus_set_abort_on_error(int on);

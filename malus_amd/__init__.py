@@ -110,6 +110,8 @@ SIGNATURES = {
     "malus_set_mem_budget": (None, [_i64]),
     "malus_alloc_histogram": (_sz, [_P(_sz), _P(_u64), _sz]),
     "malus_ktimer_enable": (None, [C.c_int]),
+    "malus_gemm_set_tile": (C.c_int, [C.c_int, C.c_int]),
+    "malus_gemm_set_split": (None, [C.c_int]),
     "malus_ktimer_collect": (_i64, [C.c_char_p, _P(C.c_double), _P(C.c_double)]),
     "malus_device_info": (C.c_int, [C.c_char_p, _sz, _P(C.c_int), _P(C.c_int)]),
     "malus_set_abort_on_error": (None, [C.c_int]),

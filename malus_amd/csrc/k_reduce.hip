@@ -132,16 +132,32 @@ __global__ __launch_bounds__(256) void k_col(const float* __restrict__ x, const 
   else dst[(o * nsplit + sp) * inner + i] = acc;
 }
 
-// Combine column partials in split order.
+// Combine column partials.  Block (x, o) owns kCombCols consecutive columns;
+// its 256 threads form 16 split groups, group g summing splits g, g+16, ...
+// in order (each group's loads of one split row are contiguous), then the 16
+// group sums are folded in group order.  Fixed order, so deterministic.
+constexpr int kCombCols = 16;
 template <int OP>
 __global__ __launch_bounds__(256) void k_col_combine(const float* __restrict__ partial, float* __restrict__ out,
-                                                     size_t outer, uint32_t nsplit, size_t inner, uint32_t count) {
-  size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= outer * inner) return;
-  size_t o = idx / inner, i = idx % inner;
+                                                     uint32_t nsplit, size_t inner, uint32_t count) {
+  constexpr int G = 256 / kCombCols;
+  __shared__ float red[G][kCombCols + 1];
+  const int lc = threadIdx.x % kCombCols, g = threadIdx.x / kCombCols;
+  const size_t o = blockIdx.y;
+  const size_t i = (size_t)blockIdx.x * kCombCols + lc;
   float acc = rinit<OP>();
-  for (uint32_t s = 0; s < nsplit; ++s) acc = rcomb<OP>(acc, partial[(o * nsplit + s) * inner + i]);
-  out[idx] = rfinal<OP>(acc, count);
+  if (i < inner) {
+    const float* p = partial + o * nsplit * inner + i;
+    for (uint32_t s = g; s < nsplit; s += G) acc = rcomb<OP>(acc, p[(size_t)s * inner]);
+  }
+  red[g][lc] = acc;
+  __syncthreads();
+  if (g == 0 && i < inner) {
+    float r = red[0][lc];
+#pragma unroll
+    for (int w = 1; w < G; ++w) r = rcomb<OP>(r, red[w][lc]);
+    out[o * inner + i] = rfinal<OP>(r, count);
+  }
 }
 
 __global__ __launch_bounds__(256) void k_expand_axis(const float* __restrict__ small, float* __restrict__ out,
@@ -216,9 +232,9 @@ void reduce_impl(const float* x, const float* mean, float* out, size_t outer, si
   k_col<OP><<<(unsigned)(base_blocks * nsplit), 256, 0, s>>>(x, mean, partial, outer, axis, inner, nsplit, chunk,
                                                               col_blocks, false);
   MALUS_HIP(hipGetLastError());
-  constexpr int COMB = (OP == R_MAX) ? R_MAX : R_SUM;
-  (void)COMB;
-  k_col_combine<OP><<<(unsigned)((n_out + 255) / 256), 256, 0, s>>>(partial, out, outer, nsplit, inner, (uint32_t)axis);
+  // base_blocks < 1024 here, so outer fits gridDim.y
+  dim3 cgrid((unsigned)((inner + kCombCols - 1) / kCombCols), (unsigned)outer);
+  k_col_combine<OP><<<cgrid, 256, 0, s>>>(partial, out, nsplit, inner, (uint32_t)axis);
   MALUS_HIP(hipGetLastError());
   pool_free(partial, bucket);
 }

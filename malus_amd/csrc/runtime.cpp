@@ -830,8 +830,8 @@ int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_un
     }
   }
   g_ktimers.swap(keep);
-  *total_ms = ms;
-  *total_units = units;
+  if (total_ms) *total_ms = ms;
+  if (total_units) *total_units = units;
   return n;
   API_CATCH(0)
 }

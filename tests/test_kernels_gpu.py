@@ -103,7 +103,8 @@ def test_unary_vjp_bitexact(rt, fn, op):
 
 # ---------------------------------------------------------------- reductions
 @pytest.mark.parametrize("shape,axis", [((65, 1024), 1), ((65, 1024), 0), ((3, 70001), 1), ((70001, 3), 0),
-                                        ((4, 5, 6), 1), ((4, 5, 6), 2), ((4, 5, 6), 0), ((2, 300, 50), -2),
+                                        ((4, 5, 6), 1), ((4, 5, 6), 2), ((4, 5, 6), 0), ((2, 300, 50), -2), ((4096, 384), 0),
+                                        ((3, 999, 40), 1),
                                         ((1, 1), 0), ((17,), 0)])
 @pytest.mark.parametrize("op", [M.R_SUM, M.R_MEAN, M.R_MAX, M.R_VAR])
 def test_reduce_axis(rt, shape, axis, op):
