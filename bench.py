@@ -40,6 +40,49 @@ def gemm_flops_per_step(cfg) -> float:
     return 3.0 * fwd
 
 
+def gemm_bytes_per_step(cfg) -> float:
+    """Algorithmic HBM bytes of the step's GEMMs: each launch reads both
+    operands once and writes its output once (4 bytes per element)."""
+    B, T, Cn, H, L, V = cfg["B"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["V"]
+    N, hs, F, BH = B * T, Cn // H, 4 * cfg["C"], B * H
+
+    def mm(m, n, k, batch=1):  # one GEMM and its two VJP GEMMs (dA: m x k, dB: k x n)
+        fwd = m * k + k * n + m * n
+        return 4.0 * batch * (3 * fwd)
+
+    layer = 4 * mm(N, Cn, Cn) + mm(N, F, Cn) + mm(N, Cn, F) + mm(T, T, hs, BH) + mm(T, hs, T, BH)
+    return L * layer + mm(N, V, Cn)
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c5_gemm_hbm_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per step of all GEMM launches, as measured by the rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs recorded in profiles/ (None if absent)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("gemm_hbm_bytes_per_step:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(rt, sizes):
+    """A plain copy of known size for counter calibration: out = x * 1.0 over
+    2^26 f32 (256 MiB read, 256 MiB written), three launches."""
+    L = rt.L
+    x = L.tensor_alloc_ones_gpu(sizes((1 << 26,)), 1)
+    for _ in range(3):
+        y = L.malus_std_scalar_op(2, x, 1.0, 1)
+        L.gpu_barrier()
+        rt.free(y)
+    rt.free(x)
+    log("copy calibration: 3 x k_binary_scalar<MUL> over 2^26 f32 (268435456 B read + 268435456 B written each)")
+
+
 def cpu_baseline(sample_batch: int, threads: int):
     """The oracle (plain-C restatement of the reference CPU path) on a
     bounded sample: one full step at batch `sample_batch`, scaled to the
@@ -70,6 +113,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=1)
     ap.add_argument("--cpu-threads", type=int, default=1)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 256 MiB copy (counter calibration for the traffic figure)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
@@ -82,6 +127,9 @@ def main():
 
     rt = M.Runtime()
     L = rt.L
+    if a.copy_calibration:
+        copy_calibration(rt, M.sizes)
+        return
     name = C.create_string_buffer(64)
     cus, clk = C.c_int(), C.c_int()
     L.malus_device_info(name, 64, C.byref(cus), C.byref(clk))
@@ -150,6 +198,7 @@ def main():
         rt.free(x, y)
     L.malus_gpt_free(g)
 
+    traffic = measured_traffic()
     out = {
         "metric": METRIC,
         "value": round(med, 3),
@@ -168,7 +217,9 @@ def main():
                    "batch": CFG["B"], "tokens_per_step": n, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "k_sgemm (all GEMM launches of the step)",
                      "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
+                     "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic,
+                     "traffic_unit": "HBM bytes per step, all GEMM launches (rocprofv3 FETCH_SIZE+WRITE_SIZE)",
+                     "algorithmic_bytes": gemm_bytes_per_step(CFG),
                      "gemm_ms_per_step": round(gms.value / a.steps, 3),
                      "gemm_gflop_per_step": round(gflop.value / a.steps / 1e9, 1)},
         "cpu_baseline": cpu,

@@ -301,7 +301,7 @@ Plan plan_gemm(int batch, int M, int N, int K, bool ta, bool tb, bool va, bool v
     const int occ = occupancy(ti, ta, tb, va, vb);
     int cand[3] = {1, 1, 1};
     if (batch == 1 && K >= 1024) {
-      const int max_split = K / 128;
+      const int max_split = K / 512;  // >= 32 K steps per workgroup amortize its prologue and partial tile
       for (int w = 1; w <= 2; ++w) {
         long want = g_split_target > 0 ? g_split_target * w : (long)w * occ * 256;
         long sp = want / tiles;
