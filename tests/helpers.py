@@ -13,6 +13,12 @@ Tolerance rules (stated once, used by every test):
     reference result is (that result alone drifts ~1e-5 at n ~ 70k).
 """
 import numpy as np
+import json as _json
+import pathlib as _pathlib
+
+# Known answers from the reference's tests and README (see the fixture's
+# "source" fields).
+KATS = _json.loads((_pathlib.Path(__file__).parent / "golden" / "reference_kats.json").read_text())
 
 
 def ulp_dist(a, b):

@@ -11,7 +11,7 @@ import pytest
 
 import malus_amd as M
 from oracle import oracle as O
-from tests.helpers import assert_bitexact, assert_normwise, assert_reduction, assert_ulp
+from tests.helpers import KATS, assert_bitexact, assert_normwise, assert_reduction, assert_ulp
 
 pytestmark = pytest.mark.gpu
 
@@ -220,11 +220,17 @@ def test_embedding_fwd_bwd_bitexact(rt, v, d, t):
 
 
 def test_embedding_kat(rt):
-    # tests.rs:1388-1404: W = [[0,1,2],[3,4,5],[6,7,8],[9,10,11]], idx = [1,0,2]
-    w = np.arange(12, dtype=np.float32).reshape(4, 3)
-    hw, hi = rt.tensor(w), rt.tensor(np.array([1, 0, 2], np.int32))
-    assert run(rt, rt.L.malus_std_embedding_fwd(hw, hi)).ravel().tolist() == [3, 4, 5, 0, 1, 2, 6, 7, 8]
-    rt.free(hw, hi)
+    for kat in KATS["embedding"]:
+        hw, hi = rt.tensor(np.array(kat["w"], np.float32)), rt.tensor(np.array(kat["idx"], np.int32))
+        assert_bitexact(run(rt, rt.L.malus_std_embedding_fwd(hw, hi)), np.array(kat["out"], np.float32), kat["source"])
+        rt.free(hw, hi)
+    kat = KATS["embedding_bwd_counts"]
+    hw = rt.tensor(np.zeros((kat["vocab"], 3), np.float32))
+    hd = rt.tensor(np.ones((len(kat["idx"]), 3), np.float32))
+    hi = rt.tensor(np.array(kat["idx"], np.int32))
+    g = run(rt, rt.L.malus_std_embedding_bwd(hw, hi, hd))
+    assert g[:, 0].tolist() == kat["row_counts"] and np.all(g == g[:, :1])
+    rt.free(hw, hd, hi)
 
 
 @pytest.mark.parametrize("perm", list(itertools.permutations(range(4))))
@@ -285,15 +291,33 @@ def test_matmul_and_vjps(rt, sa, sb):
 
 
 def test_matmul_kats(rt):
-    # tests.rs:207-240
-    ha = rt.tensor(np.array([[1, 2, 3], [4, 5, 6]], np.float32))
-    hb = rt.tensor(np.array([[1, 0], [0, 1], [1, 0]], np.float32))
-    assert run(rt, rt.L.tensor_matmul(ha, hb)).ravel().tolist() == [4, 2, 10, 5]
+    for kat in KATS["matmul"]:
+        ha, hb = rt.tensor(np.array(kat["a"], np.float32)), rt.tensor(np.array(kat["b"], np.float32))
+        assert_bitexact(run(rt, rt.L.tensor_matmul(ha, hb)), np.array(kat["out"], np.float32), kat["source"])
+        rt.free(ha, hb)
     o1 = rt.L.tensor_alloc_ones_gpu(M.sizes([2, 3]), 2)
     o2 = rt.L.tensor_alloc_ones_gpu(M.sizes([3, 4]), 2)
     out = run(rt, rt.L.tensor_matmul(o1, o2))
     assert out.shape == (2, 4) and np.all(out == 3.0)
-    rt.free(ha, hb, o1, o2)
+    rt.free(o1, o2)
+    # kernel -> matmul -> kernel with one flush at the read
+    kat = KATS["add_matmul_add_chain"]
+    ha = rt.tensor(np.array(kat["a"], np.float32))
+    x = rt.L.malus_std_broadcast_fwd(M.ADD, ha, ha)
+    y = rt.L.tensor_matmul(x, x)
+    z = rt.L.malus_std_broadcast_fwd(M.ADD, y, y)
+    assert rt.L.tensor_is_pending(z)
+    assert_bitexact(run(rt, z), np.array(kat["out"], np.float32), kat["source"])
+    rt.free(ha, x, y)
+
+
+@pytest.mark.parametrize("kat", KATS["reduce"], ids=lambda k: k["op"] + str(k["axis"]))
+def test_reduce_kats(rt, kat):
+    op = {"sum": M.R_SUM, "mean": M.R_MEAN, "max": M.R_MAX, "var": M.R_VAR}[kat["op"]]
+    hx = rt.tensor(np.array(kat["x"], np.float32))
+    got = run(rt, rt.L.malus_std_reduce_fwd(op, hx, kat["axis"], kat["keepdim"]))
+    assert_bitexact(got, np.array(kat["out"], np.float32), kat["source"])
+    rt.free(hx)
 
 
 def test_matmul_split_k_weight_grad_shape(rt):

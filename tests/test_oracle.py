@@ -11,6 +11,8 @@ import pytest
 
 from oracle import oracle as O
 
+from tests.helpers import KATS
+
 RNG = np.random.default_rng(7)
 
 
@@ -19,12 +21,9 @@ def r(*s, lo=-1, hi=1):
 
 
 # --------------------------------------------------------------------- RNG
-def test_philox_random123_kat_vectors():
-    # Random123 kat_vectors, philox4x32 with 10 rounds
-    assert O.philox([0, 0, 0, 0], [0, 0]) == [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]
-    assert O.philox([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2) == [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]
-    assert O.philox([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0]) == [
-        0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]
+@pytest.mark.parametrize("kat", KATS["philox4x32_10"], ids=lambda k: "%08x" % k["ctr"][0])
+def test_philox_random123_kat_vectors(kat):
+    assert O.philox(kat["ctr"], kat["key"]) == kat["out"]
 
 
 def test_randn_is_box_muller_of_philox_pairs():
@@ -57,60 +56,67 @@ def test_rand_uniform_and_int():
 
 
 # -------------------------------------------------------------- known answers
+def f32(x):
+    return np.array(x, np.float32)
+
+
 def test_matmul_kats():
-    assert O.matmul([[1, 2, 3], [4, 5, 6]], [[1, 0], [0, 1], [1, 0]]).ravel().tolist() == [4, 2, 10, 5]
-    assert np.all(O.matmul(np.ones((2, 3)), np.ones((3, 4))) == 3)
-    # tests.rs:1664-1682 chain: ([[1,2],[3,4]] @ [[1,2],[3,4]]) @ [[1,2],[3,4]]
-    m = np.array([[1, 2], [3, 4]], np.float32)
-    assert O.matmul(O.matmul(m, m), m).ravel().tolist() == [37, 54, 81, 118]
+    for kat in KATS["matmul"]:
+        assert np.array_equal(O.matmul(f32(kat["a"]), f32(kat["b"])), f32(kat["out"])), kat["source"]
+    kat = KATS["add_matmul_add_chain"]
+    a = f32(kat["a"])
+    x = O.broadcast(O.ADD, a, a)
+    y = O.matmul(x, x)
+    assert np.array_equal(O.broadcast(O.ADD, y, y), f32(kat["out"])), kat["source"]
 
 
 def test_broadcast_and_reduce_kats():
-    assert np.all(O.broadcast(O.ADD, np.ones((4, 8)), np.arange(1, 9)) == np.arange(2, 10))
-    assert np.all(O.broadcast(O.SUB, [[1, 2, 3, 4]], np.ones((3, 4))) == [0, 1, 2, 3])
-    assert O.broadcast(O.ADD, [1, 2, 3, 4], [10, 20, 30, 40]).tolist() == [11, 22, 33, 44]
-    x = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
-    assert O.reduce_axis(O.R_SUM, x, 0).tolist() == [5, 7, 9]
-    assert O.reduce_axis(O.R_SUM, x, 1, keepdim=True).tolist() == [[6], [15]]
-    assert O.reduce_axis(O.R_MEAN, x, 0).tolist() == [2.5, 3.5, 4.5]
-    assert O.reduce_axis(O.R_MAX, np.array([[1, 5, 3], [4, 2, 6]], np.float32), 1).tolist() == [5, 6]
-    assert O.reduce_axis(O.R_VAR, np.array([[1, 2], [4, 8]], np.float32), 0).tolist() == [2.25, 9.0]
-    assert O.reduce_axis(O.R_SUM, np.arange(12, dtype=np.float32).reshape(3, 4), -1).tolist() == [6, 22, 38]
+    ops = {"add": O.ADD, "sub": O.SUB}
+    for kat in KATS["broadcast"]:
+        got = O.broadcast(ops[kat["op"]], f32(kat["a"]), f32(kat["b"]))
+        assert np.array_equal(got, f32(kat["out"])), kat["source"]
+    rops = {"sum": O.R_SUM, "mean": O.R_MEAN, "max": O.R_MAX, "var": O.R_VAR}
+    for kat in KATS["reduce"]:
+        got = O.reduce_axis(rops[kat["op"]], f32(kat["x"]), kat["axis"], keepdim=bool(kat["keepdim"]))
+        assert np.array_equal(got, f32(kat["out"])), kat["source"]
+    # negative axis == positive axis (tests.rs:1087-1100)
+    x = np.arange(12, dtype=np.float32).reshape(3, 4)
+    assert np.array_equal(O.reduce_axis(O.R_SUM, x, -1), O.reduce_axis(O.R_SUM, x, 1))
     assert O.sum_all([1, 2, 3, 4]) == 10
 
 
 def test_embedding_and_transpose_kats():
-    w = np.arange(12, dtype=np.float32).reshape(4, 3)
-    assert O.embedding(w, [1, 0, 2]).ravel().tolist() == [3, 4, 5, 0, 1, 2, 6, 7, 8]
-    assert O.embedding(w, [2, 1, 0]).ravel().tolist() == [6, 7, 8, 3, 4, 5, 0, 1, 2]
-    # tests.rs:1420-1460: counts row0 = 2, rows 1-2 = 1, row 3 = 0
-    g = O.embedding_bwd(np.ones((4, 3)), [0, 1, 0, 2], 4)
-    assert g[:, 0].tolist() == [2, 1, 1, 0]
-    assert O.permute([[1, 2, 3], [4, 5, 6]], (1, 0)).ravel().tolist() == [1, 4, 2, 5, 3, 6]
+    for kat in KATS["embedding"]:
+        assert np.array_equal(O.embedding(f32(kat["w"]), kat["idx"]), f32(kat["out"])), kat["source"]
+    kat = KATS["embedding_bwd_counts"]
+    g = O.embedding_bwd(np.ones((len(kat["idx"]), 3), np.float32), kat["idx"], kat["vocab"])
+    assert g[:, 0].tolist() == kat["row_counts"] and np.all(g == g[:, :1])
+    kat = KATS["transpose"]
+    assert np.array_equal(O.permute(f32(kat["x"]), (1, 0)), f32(kat["out"])), kat["source"]
 
 
 def test_softmax_layernorm_gelu_integration_kats():
-    # metal_integration.rs:166-431 inputs, compared with their inline refs at 1e-5
-    x = np.array([[1, 2, 3, 4, 5, 6, 7, 8], [8, 7, 6, 5, 4, 3, 2, 1], [1] * 8,
-                  [.1, .9, .2, .8, .3, .7, .4, .6]], np.float32)
+    # the reference's inputs, compared with their inline formulas at the tolerance they use
+    kat = KATS["integration_inputs"]
+    tol = kat["tolerance"]
+    x = f32(kat["softmax_x"])
     e = np.exp(x - x.max(1, keepdims=True))
-    assert np.max(np.abs(O.softmax(x, 1) - e / e.sum(1, keepdims=True))) < 1e-5
-    y = np.array([[1, 2, 3, 4, 5, 6, 7, 8], [.1, .2, .3, .4, .5, .6, .7, .8],
-                  [-3, -2, -1, 0, 1, 2, 3, 4], [10, 10.1, 9.9, 10.2, 9.8, 10.3, 9.7, 10.4]], np.float32)
+    assert np.max(np.abs(O.softmax(x, 1) - e / e.sum(1, keepdims=True))) < tol
+    y = f32(kat["layernorm_x"])
     ln, var = O.layernorm(y, 1)
     ref = (y - y.mean(1, keepdims=True)) / np.sqrt(y.var(1, keepdims=True) + 1e-5)
-    assert np.max(np.abs(ln - ref)) < 1e-5
-    assert np.allclose(var.ravel(), y.var(1), rtol=1e-5)
-    g = np.array([1, -1, 0, 2, -2, 0.5, -0.5, 3], np.float32)
+    assert np.max(np.abs(ln - ref)) < tol
+    assert np.allclose(var.ravel(), y.var(1), rtol=tol)
+    g = f32(kat["gelu_x"])
     inner = 0.7978845608028654 * (g + 0.044715 * g**3)
-    assert np.max(np.abs(O.unary(O.GELU, g) - 0.5 * g * (1 + np.tanh(inner)))) < 1e-5
+    assert np.max(np.abs(O.unary(O.GELU, g) - 0.5 * g * (1 + np.tanh(inner)))) < tol
 
 
 def test_xor_readme_golden():
-    # README.md:66-67 (Metal run): loss [0.00012191984], predictions below
+    kat = KATS["xor_readme"]
     loss, loss_at, preds, _ = O.xor_train()
-    assert abs(loss - 0.00012191984) <= 1e-3 * 0.00012191984
-    np.testing.assert_allclose(preds, [0.0056860363, 0.99518234, 0.9939387, 0.005444207], rtol=1e-3)
+    assert abs(loss - kat["loss"]) <= kat["rtol"] * kat["loss"]
+    np.testing.assert_allclose(preds, kat["predictions"], rtol=kat["rtol"])
     assert loss_at[0] > 1.0 and np.all(np.diff(loss_at) < 0)
 
 
@@ -205,6 +211,42 @@ def test_adam_l2_matches_numpy_float32_expression():
     got, gm, gv = O.adam_l2(p, g, m, v, 1e-3, 0.9, 0.99, 1e-8, 0.1, 3)
     assert np.array_equal(gm, mm) and np.array_equal(gv, vv)
     assert np.max(np.abs(got - want)) <= 2 * np.max(np.spacing(np.abs(want)))  # powf vs numpy pow
+
+
+def test_adam_l2_invariants():
+    """Closed forms of the coupled-L2 Adam update that a dropped bias
+    correction, a swapped beta or a misplaced weight-decay term would break."""
+    p, g = r(400), r(400)
+    z = np.zeros(400, np.float32)
+    # t = 1 from zero moments: m_hat = g', v_hat = g'^2, so the step is lr * sign(g')
+    # (up to eps) with g' = g + wd * p.
+    for wd in (0.0, 0.1):
+        got, gm, gv = O.adam_l2(p, g, z, z, 1e-3, 0.9, 0.99, 1e-8, wd, 1)
+        gp = g.astype(np.float64) + wd * p.astype(np.float64)
+        np.testing.assert_allclose(gm, 0.1 * gp, rtol=1e-6, atol=1e-9)
+        np.testing.assert_allclose(gv, 0.01 * gp * gp, rtol=1e-5, atol=1e-12)
+        step = p.astype(np.float64) - got
+        keep = np.abs(gp) > 1e-3
+        np.testing.assert_allclose(step[keep], 1e-3 * np.sign(gp[keep]), rtol=1e-4)
+    # a constant gradient keeps m_hat = g and v_hat = g^2 at every t (bias
+    # correction exactly undoes the zero start), so the second step is again
+    # lr * sign(g); without the corrections it would be 0.19 / sqrt(0.0199) ~ 1.35x
+    p1, m1, v1 = O.adam_l2(p, g, z, z, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1)
+    p2, m2, v2 = O.adam_l2(p1, g, m1, v1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 2)
+    keep = np.abs(g) > 1e-3
+    np.testing.assert_allclose((p1 - p2)[keep].astype(np.float64), 1e-3 * np.sign(g[keep]), rtol=2e-3)
+    np.testing.assert_allclose(m2, 0.19 * g.astype(np.float64), rtol=1e-5, atol=1e-9)
+    # moments already at their fixed point (m = g', v = g'^2) stay there, and
+    # for large t the step tends to lr * g' / (|g'| + eps)
+    gp = g + np.float32(0.1) * p
+    got, gm, gv = O.adam_l2(p, g, gp, gp * gp, 1e-3, 0.9, 0.99, 1e-8, 0.1, 5000)
+    np.testing.assert_allclose(gm, gp, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(gv, gp * gp, rtol=1e-5, atol=1e-9)
+    keep = np.abs(gp) > 1e-3
+    np.testing.assert_allclose((p - got)[keep], 1e-3 * np.sign(gp[keep]), rtol=1e-3)
+    # zero gradient and zero decay leave parameters and moments unchanged
+    got, gm, gv = O.adam_l2(p, z, z, z, 1e-3, 0.9, 0.99, 1e-8, 0.0, 7)
+    assert np.array_equal(got, p) and not gm.any() and not gv.any()
 
 
 # ------------------------------------------------- adjoints / finite differences

@@ -10,7 +10,7 @@ import pytest
 
 import malus_amd as M
 from oracle import oracle as O
-from tests.helpers import assert_bitexact, assert_normwise
+from tests.helpers import KATS, assert_bitexact, assert_normwise
 
 pytestmark = pytest.mark.gpu
 
@@ -200,12 +200,10 @@ def tape(rt):
     rt.L.tape_reset()
 
 
-@pytest.mark.parametrize("op,a,b,ga,gb", [("Add", (1, 2), (3, 4), (1, 1), (1, 1)),
-                                          ("Sub", (5, 6), (2, 1), (1, 1), (-1, -1)),
-                                          ("Mul", (2, 3), (4, 5), (4, 5), (2, 3)),
-                                          ("Div", (6, 8), (2, 4), (0.5, 0.25), (-1.5, -0.5))])
-def test_backward_binop_kats(tape, op, a, b, ga, gb):
+@pytest.mark.parametrize("kat", KATS["backward_binop"], ids=lambda k: k["op"])
+def test_backward_binop_kats(tape, kat):
     rt = tape
+    op, a, b, ga, gb = kat["op"], kat["a"], kat["b"], kat["ga"], kat["gb"]
     ha, hb = leaf(rt, *a), leaf(rt, *b)
     out = rt.L.malus_std_broadcast_fwd(OP[op] - 1, ha, hb)
     rt.L.tape_record_binop(OP[op], ha, hb, out)
@@ -215,14 +213,16 @@ def test_backward_binop_kats(tape, op, a, b, ga, gb):
     rt.free(ha, hb, out)
 
 
-@pytest.mark.parametrize("op,x,fn,want", [("Relu", (-1, 0, 2, 3), M.RELU, (0, 0, 1, 1)),
-                                          ("Sigmoid", (0,), M.SIGMOID, (0.25,)), ("Tanh", (0,), M.TANH, (1,)),
-                                          ("Exp", (1,), M.EXP, (np.float32(np.e),)), ("Log", (2,), M.LOG, (0.5,)),
-                                          ("Sqrt", (4,), M.SQRT, (0.25,)), ("Abs", (-3, 0, 2), M.ABS, (-1, 0, 1))])
-def test_backward_unary_kats(tape, op, x, fn, want):
+UNARY_FN = {"Relu": M.RELU, "Sigmoid": M.SIGMOID, "Tanh": M.TANH, "Exp": M.EXP, "Log": M.LOG, "Sqrt": M.SQRT,
+            "Abs": M.ABS}
+
+
+@pytest.mark.parametrize("kat", [k for k in KATS["backward_unary"] if k["op"] in UNARY_FN], ids=lambda k: k["op"])
+def test_backward_unary_kats(tape, kat):
     rt = tape
+    op, x, want = kat["op"], kat["x"], kat["gx"]
     hx = leaf(rt, *x)
-    out = rt.L.malus_std_unary(fn, hx)
+    out = rt.L.malus_std_unary(UNARY_FN[op], hx)
     rt.L.tape_record_unary(OP[op], hx, out)
     rt.L.backward(out)
     np.testing.assert_allclose(grad(rt, hx), want, atol=1e-6)
