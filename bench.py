@@ -183,6 +183,9 @@ def main():
     gemm_tflops = gflop.value / (gms.value * 1e-3) / 1e12 if gms.value > 0 else 0.0
     log(f"steps {a.steps}: median {med:.3f} ms  min {min(times):.3f}  max {max(times):.3f}  wall {wall:.2f} s")
     log(f"loss first {first_loss:.4f} last {last_loss:.4f}")
+    ps = (C.c_int64 * 4)()
+    L.malus_pool_stats(ps)
+    log(f"pool: hits {ps[0]} misses {ps[1]} peak device bytes {ps[3] / 1e9:.2f} GB")
     log(f"gemm: {ng} launches, {gms.value / a.steps:.3f} ms/step, {gemm_tflops:.1f} TFLOP/s "
         f"({gflop.value / a.steps / 1e9:.1f} GFLOP/step; algorithmic {step_flops / 1e9:.1f})")
 
