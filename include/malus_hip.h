@@ -147,6 +147,8 @@ void malus_ktimer_enable(int on);
 int malus_gemm_set_tile(int tm, int tn);
 /* Tuning: workgroups a split-K GEMM aims for; 0 = the cost model decides. */
 void malus_gemm_set_split(int target_blocks);
+/* Tuning: 0 keeps every GEMM on the register-staged path; 1 (default) allows the LDS-DMA path. */
+void malus_gemm_set_dma(int on);
 int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
 int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
 void malus_set_abort_on_error(int on);

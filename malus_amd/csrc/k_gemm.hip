@@ -10,9 +10,8 @@
 //
 // Tiling: 256 threads = 4 waves in a 2x2 grid; each wave owns TM x TN
 // MFMA 32x32 accumulators, so the block tile is (64 TM) x (64 TN) with
-// BK = 16.  Operand tiles are staged in LDS as [k][m] / [k][n] (every MFMA
-// operand read is 32 consecutive floats per half-wave); global->LDS staging
-// is double-buffered with one barrier per K step, and all MFMA operand
+// BK = 16.  Operand tiles are staged in LDS in their global orientation
+// (see Tile), double-buffered with one barrier per K step; all MFMA operand
 // fragments of a K step are read from LDS before its MFMAs issue, so LDS
 // latency stays off the matrix pipe.  The host picks TM x TN and a K split
 // per shape from a cost model of the busiest CU (256 CUs, the variant's
@@ -37,82 +36,94 @@ namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int BK = 16, PAD = 4;
+constexpr int BK = 16;
 
-template <int BM, bool TA, bool VA>
-struct ALoader {
-  static constexpr int N4 = BM * BK / 4 / 256;  // float4 per thread
-  static constexpr int NS = BM * BK / 256;      // scalars per thread
-  static constexpr int LDS = BM + PAD;
+// One operand's tile: BX rows of its free dimension x (m for A, n for B) by
+// BK of k, staged in LDS in the operand's global orientation, so staging
+// never transposes:
+//   KC (k-contiguous: A as [M][K], B^T as [N][K]) -> LDS [x][BK + 4];
+//   XC (x-contiguous: A^T as [K][M], B as [K][N]) -> LDS [k][BX + 4].
+// MFMA step s (0..7) of a K step gives lane (i, h) = (lane % 32, lane / 32)
+// the element k = 8h + s, for A and B alike (any bijection of k works as
+// long as both operands use the same one).  A KC lane then reads its 8 k
+// values with two 128-bit LDS reads (row stride 20 floats: 8 lanes of a
+// 128-bit phase hit disjoint banks); an XC lane reads one float per step,
+// 32 consecutive floats per half-wave.
+template <int BX, bool KC, bool VEC>
+struct Tile {
+  static constexpr int LD = KC ? BK + 4 : BX + 4;
+  static constexpr int SIZE = KC ? BX * LD : BK * LD;
+  static constexpr int NV = BX * BK / 4 / 256;  // float4 per thread
+  static constexpr int NS = BX * BK / 256;      // floats per thread
   float r[NS];
-  // Tile (m0.., k0..) of A.  K is the row stride of a row-major A ([M][K]);
-  // k >= klim reads as zero.
-  __device__ __forceinline__ void load(const float* __restrict__ A, int M, int K, int klim, int m0, int k0) {
+
+  // Rows x0.. and k0.. of the operand P (row stride ld); x >= X or k >= klim
+  // read as zero.
+  __device__ __forceinline__ void load(const float* __restrict__ P, int X, long ld, int klim, int x0, int k0) {
     const int t = threadIdx.x;
-    if (VA) {
+    if (VEC) {
 #pragma unroll
-      for (int q = 0; q < N4; ++q) {
-        int idx = t + 256 * q;
+      for (int q = 0; q < NV; ++q) {
+        const int idx = t + 256 * q;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (!TA) {
-          int rr = idx >> 2, c4 = idx & 3;
-          int m = m0 + rr, k = k0 + c4 * 4;
-          if (m < M && k < klim) v = *reinterpret_cast<const float4*>(A + (size_t)m * K + k);
+        if (KC) {
+          const int x = x0 + idx / (BK / 4), k = k0 + 4 * (idx % (BK / 4));
+          if (x < X && k < klim) v = *reinterpret_cast<const float4*>(P + (size_t)x * ld + k);
         } else {
-          int kr = idx / (BM / 4), c4 = idx % (BM / 4);
-          int k = k0 + kr, m = m0 + c4 * 4;
-          if (k < klim && m < M) v = *reinterpret_cast<const float4*>(A + (size_t)k * M + m);
+          const int k = k0 + idx / (BX / 4), x = x0 + 4 * (idx % (BX / 4));
+          if (k < klim && x < X) v = *reinterpret_cast<const float4*>(P + (size_t)k * ld + x);
         }
         r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
       }
     } else {
 #pragma unroll
       for (int q = 0; q < NS; ++q) {
-        int e = t + 256 * q;
+        const int e = t + 256 * q;
         float v = 0.f;
-        if (!TA) {
-          int rr = e >> 4, kk = e & 15;
-          int m = m0 + rr, k = k0 + kk;
-          if (m < M && k < klim) v = A[(size_t)m * K + k];
+        if (KC) {
+          const int x = x0 + e / BK, k = k0 + e % BK;
+          if (x < X && k < klim) v = P[(size_t)x * ld + k];
         } else {
-          int kr = e / BM, mm = e % BM;
-          int k = k0 + kr, m = m0 + mm;
-          if (k < klim && m < M) v = A[(size_t)k * M + m];
+          const int k = k0 + e / BX, x = x0 + e % BX;
+          if (k < klim && x < X) v = P[(size_t)k * ld + x];
         }
         r[q] = v;
       }
     }
   }
-  __device__ __forceinline__ void store(float* __restrict__ As) const {
+
+  __device__ __forceinline__ void store(float* __restrict__ S) const {
     const int t = threadIdx.x;
-    if (VA) {
+    if (VEC) {
 #pragma unroll
-      for (int q = 0; q < N4; ++q) {
-        int idx = t + 256 * q;
-        if (!TA) {
-          int rr = idx >> 2, c4 = idx & 3;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) As[(c4 * 4 + j) * LDS + rr] = r[4 * q + j];
-        } else {
-          int kr = idx / (BM / 4), c4 = idx % (BM / 4);
-          *reinterpret_cast<float4*>(As + kr * LDS + c4 * 4) = make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
-        }
+      for (int q = 0; q < NV; ++q) {
+        const int idx = t + 256 * q;
+        const int off = KC ? (idx / (BK / 4)) * LD + 4 * (idx % (BK / 4)) : (idx / (BX / 4)) * LD + 4 * (idx % (BX / 4));
+        *reinterpret_cast<float4*>(S + off) = make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
       }
     } else {
 #pragma unroll
       for (int q = 0; q < NS; ++q) {
-        int e = t + 256 * q;
-        if (!TA) As[(e & 15) * LDS + (e >> 4)] = r[q];
-        else As[(e / BM) * LDS + (e % BM)] = r[q];
+        const int e = t + 256 * q;
+        S[KC ? (e / BK) * LD + e % BK : (e / BX) * LD + e % BX] = r[q];
       }
     }
   }
-};
 
-// B is the same problem with (m, M, TA) replaced by (n, N, !TB): a
-// transposed B ([N][K]) is stored like a row-major A.
-template <int BN, bool TB, bool VB>
-using BLoader = ALoader<BN, !TB, VB>;
+  // The 8 MFMA-step values of this lane for tile rows xw .. xw + 31.
+  __device__ __forceinline__ static void frag(const float* __restrict__ S, int xw, float f[8]) {
+    const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+    if (KC) {
+      const float4* p = reinterpret_cast<const float4*>(S + (xw + i) * LD + 8 * h);
+      const float4 a = p[0], b = p[1];
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+      f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) f[s] = S[(8 * h + s) * LD + xw + i];
+    }
+  }
+};
 
 // grid: x = output tiles (XCD-remapped), y = K splits, z = batch.
 // Split s writes its partial tile to C + s * split_stride.
@@ -121,9 +132,10 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
                                                   float* __restrict__ C, int M, int N, int K, long sA, long sB, long sC,
                                                   int k_chunk, int tiles_n, long split_stride) {
   constexpr int BM = 64 * TM, BN = 64 * TN;
-  constexpr int LDA = BM + PAD, LDB = BN + PAD;
-  __shared__ __attribute__((aligned(16))) float As[2][BK * LDA];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDB];
+  using TileA = Tile<BM, !TA, VA>;  // A [M][K] is k-contiguous
+  using TileB = Tile<BN, TB, VB>;   // B^T [N][K] is k-contiguous
+  __shared__ __attribute__((aligned(16))) float As[2][TileA::SIZE];
+  __shared__ __attribute__((aligned(16))) float Bs[2][TileB::SIZE];
 
   const int nt = gridDim.x;
   int tile = blockIdx.x;
@@ -136,6 +148,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
   C += (size_t)b * sC + (size_t)blockIdx.y * split_stride;
   const int kbeg = blockIdx.y * k_chunk;
   const int kend = min(K, kbeg + k_chunk);
+  const long lda = TA ? M : K, ldb = TB ? K : N;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * 32 * TM, wn = (wave & 1) * 32 * TN;
@@ -147,12 +160,12 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = v16f{0};
 
-  ALoader<BM, TA, VA> la;
-  BLoader<BN, TB, VB> lb;
+  TileA la;
+  TileB lb;
   const int nk = (kend - kbeg + BK - 1) / BK;
   if (nk > 0) {
-    la.load(A, M, K, kend, m0, kbeg);
-    lb.load(B, N, K, kend, n0, kbeg);
+    la.load(A, M, lda, kend, m0, kbeg);
+    lb.load(B, N, ldb, kend, n0, kbeg);
     la.store(As[0]);
     lb.store(Bs[0]);
   }
@@ -161,25 +174,21 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      la.load(A, M, K, kend, m0, kbeg + (kt + 1) * BK);
-      lb.load(B, N, K, kend, n0, kbeg + (kt + 1) * BK);
+      la.load(A, M, lda, kend, m0, kbeg + (kt + 1) * BK);
+      lb.load(B, N, ldb, kend, n0, kbeg + (kt + 1) * BK);
     }
-    const float* as = As[cur] + lk * LDA + wm + li;
-    const float* bs = Bs[cur] + lk * LDB + wn + li;
-    float fa[BK / 2][TM], fb[BK / 2][TN];
+    float fa[TM][8], fb[TN][8];
 #pragma unroll
-    for (int kk = 0; kk < BK / 2; ++kk) {
+    for (int i = 0; i < TM; ++i) TileA::frag(As[cur], wm + 32 * i, fa[i]);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) fa[kk][i] = as[2 * kk * LDA + 32 * i];
+    for (int j = 0; j < TN; ++j) TileB::frag(Bs[cur], wn + 32 * j, fb[j]);
+    __builtin_amdgcn_sched_barrier(0);  // keep every fragment read ahead of the MFMA chain
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[kk][j] = bs[2 * kk * LDB + 32 * j];
-    }
-#pragma unroll
-    for (int kk = 0; kk < BK / 2; ++kk)
+    for (int s = 0; s < 8; ++s)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[kk][i], fb[kk][j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
     if (more) {
       la.store(As[cur ^ 1]);
       lb.store(Bs[cur ^ 1]);
@@ -203,6 +212,164 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
     }
 }
 
+// ---- LDS-DMA path --------------------------------------------------------------
+// When K is a multiple of 16 (and the x-contiguous operands' rows are
+// 16-byte multiples), operand slabs move global -> LDS with
+// buffer_load_dwordx4 ... lds: no VGPR staging and no LDS store
+// instructions.  Lane l of such a wave instruction writes LDS bytes
+// [16 l, 16 l + 16) past the wave's base (M0), so each instruction fills a
+// dense 1 KB run; the runtime picks which global 16-byte chunk each lane
+// fetches.  Layouts (dense, no padding):
+//   KC slab: [BX rows][16 k], chunk c of row r stored at chunk c ^ ((r >> 1) & 3)
+//            (the swizzle makes the two 128-bit fragment reads per lane
+//            bank-conflict-free);
+//   XC slab: [16 k][BX] (a half-wave reads 32 consecutive floats).
+// Buffer loads past the descriptor's byte count return 0; other reads past a
+// matrix edge only feed output rows/columns that are never stored.
+typedef __attribute__((address_space(3))) void lds_void;
+
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, (int)bytes, 0x00020000);
+}
+#endif
+
+template <int BX, bool KC>
+struct DmaSlab {
+  static constexpr int SIZE = BX * BK;        // floats
+  static constexpr int PER_WAVE = SIZE / 1024;  // 1 KB instructions per wave (4 waves)
+  int off[PER_WAVE];                          // byte offset of this lane's chunk at k0 = 0
+
+  // x0: first row/column of the tile; X: extent of x; ld: row stride of the
+  // operand in floats (K for KC, X for XC)
+  __device__ __forceinline__ void init(int x0, int ld, int wave, int lane) {
+#pragma unroll
+    for (int q = 0; q < PER_WAVE; ++q) {
+      const int c = q * 4 + wave;  // 256-float run of the slab
+      if (KC) {
+        const int r = c * 16 + lane / 4;
+        const int chunk = (lane & 3) ^ ((r >> 1) & 3);
+        off[q] = ((x0 + r) * ld + 4 * chunk) * 4;
+      } else {
+        const int f = c * 256 + 4 * lane;
+        off[q] = ((f / BX) * ld + x0 + f % BX) * 4;
+      }
+    }
+  }
+#if defined(__HIP_DEVICE_COMPILE__)
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, float* S, int wave, int k0, int ld) const {
+    const int dk = KC ? 4 * k0 : 4 * k0 * ld;
+#pragma unroll
+    for (int q = 0; q < PER_WAVE; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(S + (q * 4 + wave) * 256), 16, off[q] + dk, 0, 0, 0);
+  }
+#endif
+  // The 8 MFMA-step values (k = 8h .. 8h + 7) of lane (i, h) for tile rows xw ..
+  __device__ __forceinline__ static void frag(const float* __restrict__ S, int xw, float f[8]) {
+    const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+    if (KC) {
+      const int r = xw + i, sw = (r >> 1) & 3;
+      const float4 a = *reinterpret_cast<const float4*>(S + r * BK + 4 * ((2 * h) ^ sw));
+      const float4 b = *reinterpret_cast<const float4*>(S + r * BK + 4 * ((2 * h + 1) ^ sw));
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+      f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) f[s] = S[(8 * h + s) * BX + xw + i];
+    }
+  }
+};
+
+// Same contract as k_sgemm; the host guarantees K % 16 == 0, rows of the
+// x-contiguous operands a multiple of 4 floats, and per-batch operand bytes
+// below 2^31.
+template <int TM, int TN, bool TA, bool TB>
+__global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ A, const float* __restrict__ B,
+                                                      float* __restrict__ C, int M, int N, int K, long sA, long sB,
+                                                      long sC, int k_chunk, int tiles_n, long split_stride) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int BM = 64 * TM, BN = 64 * TN;
+  using SlabA = DmaSlab<BM, !TA>;  // A [M][K] is k-contiguous
+  using SlabB = DmaSlab<BN, TB>;   // B^T [N][K] is k-contiguous
+  __shared__ __attribute__((aligned(1024))) float As[2][SlabA::SIZE];
+  __shared__ __attribute__((aligned(1024))) float Bs[2][SlabB::SIZE];
+
+  const int nt = gridDim.x;
+  int tile = blockIdx.x;
+  if ((nt & 7) == 0) tile = (tile & 7) * (nt >> 3) + (tile >> 3);  // XCD-contiguous tile ranges
+  const int tm = tile / tiles_n, tn = tile % tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int b = blockIdx.z;
+  A += (size_t)b * sA;
+  B += (size_t)b * sB;
+  C += (size_t)b * sC + (size_t)blockIdx.y * split_stride;
+  const int kbeg = blockIdx.y * k_chunk;
+  const int kend = min(K, kbeg + k_chunk);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * 32 * TM, wn = (wave & 1) * 32 * TN;
+  const int li = lane & 31, lk = lane >> 5;
+  const int lda = TA ? M : K, ldb = TB ? K : N;
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, (unsigned)((size_t)M * K * 4));
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, (unsigned)((size_t)K * N * 4));
+  SlabA sa;
+  SlabB sb;
+  sa.init(m0, lda, wave, lane);
+  sb.init(n0, ldb, wave, lane);
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = v16f{0};
+
+  const int nk = (kend - kbeg) / BK;
+  if (nk > 0) {
+    sa.issue(ra, As[0], wave, kbeg, lda);
+    sb.issue(rb, Bs[0], wave, kbeg, ldb);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    float fa[TM][8], fb[TN][8];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) SlabA::frag(As[cur], wm + 32 * i, fa[i]);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur], wn + 32 * j, fb[j]);
+    __builtin_amdgcn_sched_barrier(0);
+    // the other buffer was last read before the previous barrier
+    if (kt + 1 < nk) {
+      sa.issue(ra, As[cur ^ 1], wave, kbeg + (kt + 1) * BK, lda);
+      sb.issue(rb, Bs[cur ^ 1], wave, kbeg + (kt + 1) * BK, ldb);
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs ahead of the wait below
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn + 32 * j + li;
+      if (n < N) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
+          if (m < M) C[(size_t)m * N + n] = acc[i][j][r];
+        }
+      }
+    }
+#endif
+}
+
 // C[i] = sum over splits s (in order) of partial[s * mn + i]
 __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ partial, float* __restrict__ C, size_t mn,
                                                       int nsplit) {
@@ -219,8 +386,15 @@ struct TileCfg { int tm, tn; };
 constexpr TileCfg kTiles[] = {{2, 3}, {2, 2}, {2, 1}, {1, 2}, {1, 1}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
+// Variant code: bit 4 = LDS-DMA path, bits 3..0 = transA, transB, vecA, vecB.
+inline int variant(bool ta, bool tb, bool va, bool vb, bool dma) {
+  return (dma << 4) | (ta << 3) | (tb << 2) | (va << 1) | (int)vb;
+}
+
 template <int TM, int TN, bool TA, bool TB>
-const void* kernel_of(bool va, bool vb) {
+const void* kernel_of(int v) {
+  if (v & 16) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB>);
+  const bool va = v & 2, vb = v & 1;
   if (va && vb) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, true>);
   if (va) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, false>);
   if (vb) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, false, true>);
@@ -228,43 +402,47 @@ const void* kernel_of(bool va, bool vb) {
 }
 
 template <int TM, int TN>
-const void* kernel_of_layout(bool ta, bool tb, bool va, bool vb) {
-  if (!ta && !tb) return kernel_of<TM, TN, false, false>(va, vb);
-  if (!ta && tb) return kernel_of<TM, TN, false, true>(va, vb);
-  if (ta && !tb) return kernel_of<TM, TN, true, false>(va, vb);
-  return kernel_of<TM, TN, true, true>(va, vb);
+const void* kernel_of_layout(int v) {
+  const bool ta = v & 8, tb = v & 4;
+  if (!ta && !tb) return kernel_of<TM, TN, false, false>(v);
+  if (!ta && tb) return kernel_of<TM, TN, false, true>(v);
+  if (ta && !tb) return kernel_of<TM, TN, true, false>(v);
+  return kernel_of<TM, TN, true, true>(v);
 }
 
-const void* kernel_for(int ti, bool ta, bool tb, bool va, bool vb) {
+const void* kernel_for(int ti, int v) {
   switch (ti) {
-    case 0: return kernel_of_layout<2, 3>(ta, tb, va, vb);
-    case 1: return kernel_of_layout<2, 2>(ta, tb, va, vb);
-    case 2: return kernel_of_layout<2, 1>(ta, tb, va, vb);
-    case 3: return kernel_of_layout<1, 2>(ta, tb, va, vb);
-    default: return kernel_of_layout<1, 1>(ta, tb, va, vb);
+    case 0: return kernel_of_layout<2, 3>(v);
+    case 1: return kernel_of_layout<2, 2>(v);
+    case 2: return kernel_of_layout<2, 1>(v);
+    case 3: return kernel_of_layout<1, 2>(v);
+    default: return kernel_of_layout<1, 1>(v);
   }
 }
 
 // Co-resident workgroups per CU of each kernel variant (VGPR and LDS
 // limited), from the runtime's occupancy calculator; cached per variant.
-int occupancy(int ti, bool ta, bool tb, bool va, bool vb) {
-  static int cache[kNumTiles][16];
-  const int v = (ta << 3) | (tb << 2) | (va << 1) | (int)vb;
+int occupancy(int ti, int v) {
+  static int cache[kNumTiles][32];
   int& o = cache[ti][v];
   if (o == 0) {
     int n = 0;
-    MALUS_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel_for(ti, ta, tb, va, vb), 256, 0));
+    MALUS_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel_for(ti, v), 256, 0));
     o = n > 0 ? n : 1;
   }
   return o;
 }
 
 // ---- planning -----------------------------------------------------------------
-// Relative MFMA efficiency of one workgroup of each tile (bigger tiles read
-// fewer LDS fragments per MFMA and amortize the K-step barrier further).
-inline double tile_base(int ti) {
-  static const double e[kNumTiles] = {1.0, 0.97, 0.9, 0.9, 0.8};
-  return e[ti];
+// Relative MFMA efficiency of one workgroup of each tile, measured on the
+// C5 shapes.  Register-staged: bigger tiles read fewer LDS fragments per
+// MFMA and amortize the K-step barrier further.  LDS-DMA: staging costs no
+// VGPRs or issue slots, and the 128-wide tiles keep up with the 256-wide
+// ones while running more workgroups per CU.
+inline double tile_base(int ti, bool dma) {
+  static const double reg[kNumTiles] = {1.0, 0.97, 0.9, 0.9, 0.8};
+  static const double lds_dma[kNumTiles] = {0.80, 0.85, 1.0, 1.0, 0.99};
+  return dma ? lds_dma[ti] : reg[ti];
 }
 // Matrix-pipe utilization of a CU running `conc` workgroups at once (one
 // workgroup is one wave per SIMD, which cannot hide its own LDS latency).
@@ -274,13 +452,14 @@ struct Plan { int ti, nsplit, k_chunk; };
 
 int g_forced_tile = -2;    // -2: read MALUS_GEMM_TILE once; -1: automatic
 int g_split_target = 0;    // workgroups a split-K launch aims for; 0: model
+bool g_allow_dma = true;   // LDS-DMA path where the shape allows it
 
 // Pick the tile and the K split with the smallest modelled time: the
 // busiest CU's MFMA work (256 CUs at 75 % of 157.3 TFLOP/s, scaled by the
 // tile's efficiency and the CU's concurrency), plus the split-K partials'
 // HBM round trip.  Long-K shapes with few output tiles (the weight-gradient
 // GEMMs, K = tokens) split K so the grid fills the chip's workgroup slots.
-Plan plan_gemm(int batch, int M, int N, int K, bool ta, bool tb, bool va, bool vb) {
+Plan plan_gemm(int batch, int M, int N, int K, int v) {
   if (g_forced_tile == -2) {  // MALUS_GEMM_TILE=TMxTN pins a tile (tuning sweeps)
     g_forced_tile = -1;
     if (const char* e = getenv("MALUS_GEMM_TILE"))
@@ -298,7 +477,7 @@ Plan plan_gemm(int batch, int M, int N, int K, bool ta, bool tb, bool va, bool v
     if (g_forced_tile >= 0 && ti != g_forced_tile) continue;
     const int bm = 64 * kTiles[ti].tm, bn = 64 * kTiles[ti].tn;
     const long tiles = (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch;
-    const int occ = occupancy(ti, ta, tb, va, vb);
+    const int occ = occupancy(ti, v);
     int cand[3] = {1, 1, 1};
     if (batch == 1 && K >= 1024) {
       const int max_split = K / 512;  // >= 32 K steps per workgroup amortize its prologue and partial tile
@@ -315,7 +494,7 @@ Plan plan_gemm(int batch, int M, int N, int K, bool ta, bool tb, bool va, bool v
       const long blocks = tiles * ns;
       const long per_cu = (blocks + 255) / 256;
       const int conc = (int)(per_cu < occ ? per_cu : occ);
-      double t = per_cu * 2.0 * bm * bn * kc / (kCuRate * tile_base(ti) * cu_util(conc));
+      double t = per_cu * 2.0 * bm * bn * kc / (kCuRate * tile_base(ti, v & 16) * cu_util(conc));
       if (ns > 1) t += (ns + 1.0) * M * N * 4.0 / kHbm + 3e-6;
       if (t < best_t * 0.999) { best_t = t; best = Plan{ti, ns, kc}; }
     }
@@ -336,12 +515,16 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
   // float4 staging needs the contiguous dim of each operand to be a multiple of 4
   const bool va = transA ? (M % 4 == 0) : (K % 4 == 0);
   const bool vb = transB ? (K % 4 == 0) : (N % 4 == 0);
-  const Plan p = plan_gemm(batch, M, N, K, transA, transB, va, vb);
+  // LDS-DMA path: whole 16-deep K slabs, 16-byte rows, 32-bit byte offsets
+  const bool dma = K % 16 == 0 && (transA ? M % 4 == 0 : true) && (transB ? true : N % 4 == 0) &&
+                   (size_t)M * K * 4 < (1ull << 31) && (size_t)K * N * 4 < (1ull << 31) && g_allow_dma;
+  const int v = variant(transA, transB, va, vb, dma);
+  const Plan p = plan_gemm(batch, M, N, K, v);
   static const bool trace = getenv("MALUS_GEMM_TRACE") != nullptr;
   if (trace)
-    fprintf(stderr, "malus gemm b%d %dx%dx%d t%d%d -> tile %dx%d occ %d split %d k_chunk %d\n", batch, M, N, K, transA,
-            transB, 64 * kTiles[p.ti].tm, 64 * kTiles[p.ti].tn, occupancy(p.ti, transA, transB, va, vb), p.nsplit,
-            p.k_chunk);
+    fprintf(stderr, "malus gemm b%d %dx%dx%d t%d%d -> %s tile %dx%d occ %d split %d k_chunk %d\n", batch, M, N, K,
+            transA, transB, dma ? "dma" : "reg", 64 * kTiles[p.ti].tm, 64 * kTiles[p.ti].tn, occupancy(p.ti, v),
+            p.nsplit, p.k_chunk);
   const int bm = 64 * kTiles[p.ti].tm, bn = 64 * kTiles[p.ti].tn;
   const int tiles_m = (M + bm - 1) / bm, tiles_n = (N + bn - 1) / bn;
   const int tiles = tiles_m * tiles_n;
@@ -352,7 +535,7 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
   if (nsplit > 1) dst = static_cast<float*>(pool_alloc(mn * nsplit * sizeof(float), &bucket));
   long split_stride = nsplit > 1 ? (long)mn : 0;
   void* args[] = {&A, &B, &dst, &M, &N, &K, &sA, &sB, &sC, &k_chunk, const_cast<int*>(&tiles_n), &split_stride};
-  MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, transA, transB, va, vb), dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch),
+  MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, v), dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch),
                             dim3(256), args, 0, s));
   if (nsplit > 1) {
     size_t blocks = (mn + 255) / 256;
@@ -375,6 +558,10 @@ extern "C" int malus_gemm_set_tile(int tm, int tn) {
     if (kTiles[i].tm == tm && kTiles[i].tn == tn) { g_forced_tile = i; return 1; }
   return 0;
 }
+
+// Tuning knob: 0 keeps every GEMM on the register-staged path (for A/B
+// comparisons); 1 (default) uses the LDS-DMA path where the shape allows.
+extern "C" void malus_gemm_set_dma(int on) { malus::k::g_allow_dma = on != 0; }
 
 // Tuning knob: the number of workgroups a split-K GEMM aims for (0 restores
 // the cost model's choice).
