@@ -161,12 +161,14 @@ def main():
     L.malus_ktimer_enable(1)
     L.gpu_barrier()
     times = []
+    enq = []
     t_all = time.perf_counter()
     for i in range(a.steps):
         t += 1
         x, y = batches[a.warmup + i]
         t0 = time.perf_counter()
         hl = L.malus_gpt_step(g, x, y, t)
+        enq.append((time.perf_counter() - t0) * 1e3)
         L.gpu_barrier()  # flush inside the timed step
         times.append((time.perf_counter() - t0) * 1e3)
         if i == a.steps - 1:
@@ -181,7 +183,8 @@ def main():
     med = statistics.median(times)
     step_flops = gemm_flops_per_step(CFG)
     gemm_tflops = gflop.value / (gms.value * 1e-3) / 1e12 if gms.value > 0 else 0.0
-    log(f"steps {a.steps}: median {med:.3f} ms  min {min(times):.3f}  max {max(times):.3f}  wall {wall:.2f} s")
+    log(f"steps {a.steps}: median {med:.3f} ms  min {min(times):.3f}  max {max(times):.3f}  wall {wall:.2f} s  "
+        f"(host enqueue median {statistics.median(enq):.3f} ms)")
     log(f"loss first {first_loss:.4f} last {last_loss:.4f}")
     ps = (C.c_int64 * 4)()
     L.malus_pool_stats(ps)

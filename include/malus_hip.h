@@ -221,6 +221,8 @@ int malus_gpt_nparams(void* g);
 int64_t malus_gpt_param(void* g, int i);              /* borrowed */
 int64_t malus_gpt_moment(void* g, int i, int which);  /* borrowed; which 0 = m, 1 = v */
 void malus_gpt_set_fused_optimizer(void* g, int on);
+/* 1 (default): attention scale + mask + softmax as one kernel; 0: three separate ops (same values and tape). */
+void malus_gpt_set_fused_attention(void* g, int on);
 int64_t malus_gpt_forward_loss(void* g, int64_t toks, int64_t targets); /* nanogpt_modular.ml:75-91 + cross_entropy */
 int64_t malus_gpt_logits(void* g, int64_t toks);
 void malus_gpt_zero_grad(void* g);

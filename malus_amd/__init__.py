@@ -138,6 +138,8 @@ SIGNATURES = {
     "malus_std_eq_fwd": (_i64, [_i64, _i64]),
     "malus_std_expand_axis_fwd": (_i64, [_i64, _i64, _i64]),
     "malus_std_sum_to_shape_bwd": (_i64, [_i64, _i64]),
+    "malus_std_mul_bwd_a": (_i64, [_i64, _i64, _i64]),
+    "malus_std_mul_bwd_b": (_i64, [_i64, _i64, _i64]),
     "malus_std_softmax_bwd": (_i64, [_i64, _i64, _i64]),
     "malus_std_layernorm_bwd": (_i64, [_i64, _i64, _i64, _i64]),
     "malus_std_gelu_bwd": (_i64, [_i64, _i64]),
@@ -159,6 +161,7 @@ SIGNATURES = {
     "malus_gpt_param": (_i64, [_vp, C.c_int]),
     "malus_gpt_moment": (_i64, [_vp, C.c_int, C.c_int]),
     "malus_gpt_set_fused_optimizer": (None, [_vp, C.c_int]),
+    "malus_gpt_set_fused_attention": (None, [_vp, C.c_int]),
     "malus_gpt_forward_loss": (_i64, [_vp, _i64, _i64]),
     "malus_gpt_logits": (_i64, [_vp, _i64]),
     "malus_gpt_zero_grad": (None, [_vp]),

@@ -72,6 +72,10 @@ TensorBuffer* alloc_tensor(int32_t dtype, const size_t* shape, int ndim);
 TensorBuffer* alloc_like(const TensorBuffer* t);
 TensorBuffer* alloc_f32(std::initializer_list<size_t> shape);
 TensorBuffer* make_alias(TensorBuffer* src, const size_t* shape, int ndim);  // reshape_to
+// A handle with shape and dtype but no device storage: the tape node of an
+// intermediate a fused kernel keeps in registers (only its shape is ever
+// consulted).  Host reads of it fail loudly.
+TensorBuffer* alloc_virtual(int32_t dtype, const size_t* shape, int ndim);
 void release(TensorBuffer* t);
 void retain(TensorBuffer* t);
 // Scratch device memory from the same pool, released with pool_free.
@@ -127,6 +131,12 @@ void iota_rows(int32_t* out, size_t rows, size_t t, hipStream_t s);
 // Axis reductions over a contiguous [outer, axis, inner] view.
 enum RedOp : int { R_SUM = 0, R_MEAN = 1, R_MAX = 2, R_VAR = 3 };
 void reduce_axis(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
+// P = softmax over the last axis of (S * scale[0]) + mask[row % mask_rows],
+// each op rounded as the separate broadcast kernels round it.
+void scale_mask_softmax(const float* S, const float* scale, const float* mask, float* P, size_t rows, size_t axis,
+                        size_t mask_rows, hipStream_t s);
+// Sum over the axis of x * y (y has x's layout); each product rounded to f32.
+void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 // Broadcast [outer, inner] back to [outer, axis, inner] (expand_axis).
 void expand_axis(const float* small, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 
@@ -155,6 +165,16 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
           long strideA, long strideB, long strideC, hipStream_t s);
 
 // Fused Adam + L2 update (examples/nanogpt_modular.ml:97-108 op order).
+// One parameter tensor of a multi-tensor Adam update (device pointers).
+struct AdamSeg {
+  const float *p, *g, *m, *v;
+  float *po, *mo, *vo;
+  size_t n;
+};
+constexpr size_t kAdamChunk = 4096;  // floats per workgroup
+// Every tensor of `segs` in one launch; same per-element expression as adam_l2.
+void adam_l2_multi(const AdamSeg* segs_host, int count, float lr, float b1, float b2, float omb1, float omb2, float bc1,
+                   float bc2, float eps, float wd, hipStream_t s);
 void adam_l2(const float* p, const float* g, const float* m, const float* v, float* p_out, float* m_out, float* v_out,
              size_t n, float lr, float b1, float b2, float omb1, float omb2, float bc1, float bc2, float eps, float wd,
              hipStream_t s);

@@ -1,11 +1,17 @@
-// Axis reductions (sum / mean / max / population variance) over any axis
-// length — the reference's single-threadgroup kernels cap the axis at 1024
-// (reduce_sum.ml:13); these do not.  A contiguous tensor is viewed as
-// [outer, axis, inner]:
+// Axis reductions (sum / mean / max / population variance, and the sum of a
+// product) over any axis length — the reference's single-threadgroup
+// kernels cap the axis at 1024 (reduce_sum.ml:13); these do not.  A
+// contiguous tensor is viewed as [outer, axis, inner]:
 //   inner == 1 : row reduction, one wave64 per row (shuffle tree), or a
 //                two-stage split when rows are long and few;
-//   inner  > 1 : column reduction, coalesced over inner, the axis split into
-//                chunks whose partials are combined in chunk order.
+//   inner  > 1 : column reduction.  Each workgroup owns a strip of columns
+//                (float4 per thread when inner % 4 == 0) and a chunk of the
+//                axis; its row-threads sum strided rows, fold through LDS in
+//                fixed order, and chunk partials are combined in chunk
+//                order by a second kernel.
+// R_PROD sums x * y elementwise (y has x's shape): the VJP of a broadcast
+// multiply reduces dout * a without materializing the product; each product
+// is rounded to f32 exactly as the materialized tensor would be.
 // Every order is fixed, so results are run-to-run deterministic.
 #include "common.h"
 
@@ -14,6 +20,7 @@ namespace k {
 namespace {
 
 constexpr int kWave = 64;
+constexpr int R_PROD = 4;
 
 template <int OP>
 __device__ __forceinline__ float rinit() { return OP == R_MAX ? -INFINITY : 0.0f; }
@@ -21,10 +28,11 @@ __device__ __forceinline__ float rinit() { return OP == R_MAX ? -INFINITY : 0.0f
 template <int OP>
 __device__ __forceinline__ float rcomb(float a, float b) { return OP == R_MAX ? fmaxf(a, b) : a + b; }
 
-// element transform: VAR accumulates (x - mean)^2; others use x.
+// Element transform: VAR accumulates (x - mean)^2, PROD x * y, the rest x.
 template <int OP>
-__device__ __forceinline__ float rload(float x, float mean) {
+__device__ __forceinline__ float rload(float x, float y, float mean) {
   if constexpr (OP == R_VAR) { float d = x - mean; return d * d; }
+  else if constexpr (OP == R_PROD) return x * y;
   else return x;
 }
 
@@ -43,29 +51,32 @@ __device__ __forceinline__ float rfinal(float s, uint32_t count) {
 }
 
 // One wave per row; rows are contiguous of length `axis`.  `mean` (VAR
-// only) holds one value per row.  FINAL divides by `count`.
+// only) holds one value per row; `y` (PROD only) has x's layout.
 template <int OP, bool VEC>
-__global__ __launch_bounds__(256) void k_row_wave(const float* __restrict__ x, const float* __restrict__ mean,
-                                                  float* __restrict__ out, size_t rows, uint32_t axis, uint32_t count,
-                                                  bool finalize) {
+__global__ __launch_bounds__(256) void k_row_wave(const float* __restrict__ x, const float* __restrict__ y,
+                                                  const float* __restrict__ mean, float* __restrict__ out, size_t rows,
+                                                  uint32_t axis, uint32_t count, bool finalize) {
   const size_t row = (size_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
   const float* xr = x + row * axis;
+  const float* yr = OP == R_PROD ? y + row * axis : nullptr;
   const float mu = (OP == R_VAR) ? mean[row] : 0.0f;
   float acc = rinit<OP>();
   if (VEC) {
     const float4* x4 = reinterpret_cast<const float4*>(xr);
+    const float4* y4 = reinterpret_cast<const float4*>(yr);
     const uint32_t n4 = axis / 4;
     for (uint32_t i = lane; i < n4; i += kWave) {
-      float4 v = x4[i];
-      acc = rcomb<OP>(acc, rload<OP>(v.x, mu));
-      acc = rcomb<OP>(acc, rload<OP>(v.y, mu));
-      acc = rcomb<OP>(acc, rload<OP>(v.z, mu));
-      acc = rcomb<OP>(acc, rload<OP>(v.w, mu));
+      const float4 v = x4[i];
+      const float4 w = OP == R_PROD ? y4[i] : v;
+      acc = rcomb<OP>(acc, rload<OP>(v.x, w.x, mu));
+      acc = rcomb<OP>(acc, rload<OP>(v.y, w.y, mu));
+      acc = rcomb<OP>(acc, rload<OP>(v.z, w.z, mu));
+      acc = rcomb<OP>(acc, rload<OP>(v.w, w.w, mu));
     }
   } else {
-    for (uint32_t i = lane; i < axis; i += kWave) acc = rcomb<OP>(acc, rload<OP>(xr[i], mu));
+    for (uint32_t i = lane; i < axis; i += kWave) acc = rcomb<OP>(acc, rload<OP>(xr[i], OP == R_PROD ? yr[i] : 0.f, mu));
   }
   acc = wave_reduce<OP>(acc);
   if (lane == 0) out[row] = finalize ? rfinal<OP>(acc, count) : acc;
@@ -74,29 +85,33 @@ __global__ __launch_bounds__(256) void k_row_wave(const float* __restrict__ x, c
 // Split long rows: block (row, split) reduces [split*chunk, ...) of the row
 // into partial[row * nsplit + split].
 template <int OP>
-__global__ __launch_bounds__(256) void k_row_split(const float* __restrict__ x, const float* __restrict__ mean,
-                                                   float* __restrict__ partial, size_t rows, size_t axis,
-                                                   uint32_t nsplit, size_t chunk) {
+__global__ __launch_bounds__(256) void k_row_split(const float* __restrict__ x, const float* __restrict__ y,
+                                                   const float* __restrict__ mean, float* __restrict__ partial,
+                                                   size_t axis, uint32_t nsplit, size_t chunk) {
   __shared__ float red[256 / kWave];
   const size_t bid = blockIdx.x;
   const size_t row = bid / nsplit;
   const uint32_t sp = (uint32_t)(bid % nsplit);
   const float* xr = x + row * axis;
+  const float* yr = OP == R_PROD ? y + row * axis : nullptr;
   const float mu = (OP == R_VAR) ? mean[row] : 0.0f;
   size_t beg = sp * chunk, end = beg + chunk < axis ? beg + chunk : axis;
   float acc = rinit<OP>();
   // chunk is a multiple of 4 and rows are 16-byte aligned when axis % 4 == 0
   if ((axis & 3) == 0) {
     const float4* x4 = reinterpret_cast<const float4*>(xr);
+    const float4* y4 = reinterpret_cast<const float4*>(yr);
     for (size_t i = beg / 4 + threadIdx.x; i < end / 4; i += blockDim.x) {
-      float4 v = x4[i];
-      acc = rcomb<OP>(acc, rload<OP>(v.x, mu));
-      acc = rcomb<OP>(acc, rload<OP>(v.y, mu));
-      acc = rcomb<OP>(acc, rload<OP>(v.z, mu));
-      acc = rcomb<OP>(acc, rload<OP>(v.w, mu));
+      const float4 v = x4[i];
+      const float4 w = OP == R_PROD ? y4[i] : v;
+      acc = rcomb<OP>(acc, rload<OP>(v.x, w.x, mu));
+      acc = rcomb<OP>(acc, rload<OP>(v.y, w.y, mu));
+      acc = rcomb<OP>(acc, rload<OP>(v.z, w.z, mu));
+      acc = rcomb<OP>(acc, rload<OP>(v.w, w.w, mu));
     }
   } else {
-    for (size_t i = beg + threadIdx.x; i < end; i += blockDim.x) acc = rcomb<OP>(acc, rload<OP>(xr[i], mu));
+    for (size_t i = beg + threadIdx.x; i < end; i += blockDim.x)
+      acc = rcomb<OP>(acc, rload<OP>(xr[i], OP == R_PROD ? yr[i] : 0.f, mu));
   }
   acc = wave_reduce<OP>(acc);
   if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = acc;
@@ -105,17 +120,76 @@ __global__ __launch_bounds__(256) void k_row_split(const float* __restrict__ x, 
     float r = red[0];
     for (int w = 1; w < (int)(blockDim.x / kWave); ++w) r = rcomb<OP>(r, red[w]);
     partial[row * nsplit + sp] = r;
-    (void)rows;
   }
 }
 
-// Column reduction: out[o, i] over a = 0..axis-1 of x[o, a, i].  Thread
-// handles one column i for the axis chunk [sp*chunk, ...).  nsplit == 1
-// writes the finalized value; otherwise partial[(o * nsplit + sp) * inner + i].
+// Column reduction, float4 path (inner % 4 == 0).  Block (cb, sp, o): CT
+// column-threads x RT row-threads (CT * RT = 256); thread (ct, rt) owns
+// columns 4 * (cb * CT + ct) .. +3 and rows beg + rt, beg + rt + RT, ... of
+// the axis chunk [beg, end).  The RT partial sums of a column are folded in
+// rt order through LDS.  nsplit == 1 writes the finalized value; otherwise
+// partial[(o * nsplit + sp) * inner + i].
+template <int OP, int CT>
+__global__ __launch_bounds__(256) void k_col4(const float* __restrict__ x, const float* __restrict__ y,
+                                              const float* __restrict__ mean, float* __restrict__ dst, size_t axis,
+                                              size_t inner, uint32_t nsplit, size_t chunk, bool finalize) {
+  constexpr int RT = 256 / CT;
+  __shared__ float4 red[RT][CT];
+  const int ct = threadIdx.x % CT, rt = threadIdx.x / CT;
+  const uint32_t sp = blockIdx.y;
+  const size_t o = blockIdx.z;
+  const size_t i4 = (size_t)blockIdx.x * CT + ct;  // float4 column group
+  const bool live = 4 * i4 < inner;
+  float4 acc = make_float4(rinit<OP>(), rinit<OP>(), rinit<OP>(), rinit<OP>());
+  if (live) {
+    float4 mu = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (OP == R_VAR) mu = reinterpret_cast<const float4*>(mean + o * inner)[i4];
+    const size_t beg = sp * chunk, end = beg + chunk < axis ? beg + chunk : axis;
+    const float4* xp = reinterpret_cast<const float4*>(x + o * axis * inner) + i4;
+    const float4* yp = OP == R_PROD ? reinterpret_cast<const float4*>(y + o * axis * inner) + i4 : nullptr;
+    const size_t stride4 = inner / 4;
+    for (size_t a = beg + rt; a < end; a += RT) {
+      const float4 v = xp[a * stride4];
+      const float4 w = OP == R_PROD ? yp[a * stride4] : v;
+      acc.x = rcomb<OP>(acc.x, rload<OP>(v.x, w.x, mu.x));
+      acc.y = rcomb<OP>(acc.y, rload<OP>(v.y, w.y, mu.y));
+      acc.z = rcomb<OP>(acc.z, rload<OP>(v.z, w.z, mu.z));
+      acc.w = rcomb<OP>(acc.w, rload<OP>(v.w, w.w, mu.w));
+    }
+  }
+  red[rt][ct] = acc;
+  __syncthreads();
+  if (rt == 0 && live) {
+    float4 r = red[0][ct];
+#pragma unroll
+    for (int k = 1; k < RT; ++k) {
+      const float4 q = red[k][ct];
+      r.x = rcomb<OP>(r.x, q.x);
+      r.y = rcomb<OP>(r.y, q.y);
+      r.z = rcomb<OP>(r.z, q.z);
+      r.w = rcomb<OP>(r.w, q.w);
+    }
+    if (nsplit == 1) {
+      if (finalize) {
+        r.x = rfinal<OP>(r.x, (uint32_t)axis);
+        r.y = rfinal<OP>(r.y, (uint32_t)axis);
+        r.z = rfinal<OP>(r.z, (uint32_t)axis);
+        r.w = rfinal<OP>(r.w, (uint32_t)axis);
+      }
+      reinterpret_cast<float4*>(dst + o * inner)[i4] = r;
+    } else {
+      reinterpret_cast<float4*>(dst + (o * nsplit + sp) * inner)[i4] = r;
+    }
+  }
+}
+
+// Column reduction, scalar path: thread handles one column i for the axis
+// chunk [sp*chunk, ...).
 template <int OP>
-__global__ __launch_bounds__(256) void k_col(const float* __restrict__ x, const float* __restrict__ mean,
-                                             float* __restrict__ dst, size_t outer, size_t axis, size_t inner,
-                                             uint32_t nsplit, size_t chunk, uint32_t col_blocks, bool finalize) {
+__global__ __launch_bounds__(256) void k_col(const float* __restrict__ x, const float* __restrict__ y,
+                                             const float* __restrict__ mean, float* __restrict__ dst, size_t outer,
+                                             size_t axis, size_t inner, uint32_t nsplit, size_t chunk,
+                                             uint32_t col_blocks, bool finalize) {
   size_t bid = blockIdx.x;
   const uint32_t cb = (uint32_t)(bid % col_blocks);
   bid /= col_blocks;
@@ -126,8 +200,9 @@ __global__ __launch_bounds__(256) void k_col(const float* __restrict__ x, const 
   const float mu = (OP == R_VAR) ? mean[o * inner + i] : 0.0f;
   size_t beg = sp * chunk, end = beg + chunk < axis ? beg + chunk : axis;
   const float* xp = x + o * axis * inner + i;
+  const float* yp = OP == R_PROD ? y + o * axis * inner + i : nullptr;
   float acc = rinit<OP>();
-  for (size_t a = beg; a < end; ++a) acc = rcomb<OP>(acc, rload<OP>(xp[a * inner], mu));
+  for (size_t a = beg; a < end; ++a) acc = rcomb<OP>(acc, rload<OP>(xp[a * inner], OP == R_PROD ? yp[a * inner] : 0.f, mu));
   if (nsplit == 1) dst[o * inner + i] = finalize ? rfinal<OP>(acc, (uint32_t)axis) : acc;
   else dst[(o * nsplit + sp) * inner + i] = acc;
 }
@@ -135,7 +210,7 @@ __global__ __launch_bounds__(256) void k_col(const float* __restrict__ x, const 
 // Combine column partials.  Block (x, o) owns kCombCols consecutive columns;
 // its 256 threads form 16 split groups, group g summing splits g, g+16, ...
 // in order (each group's loads of one split row are contiguous), then the 16
-// group sums are folded in group order.  Fixed order, so deterministic.
+// group sums are folded in group order.
 constexpr int kCombCols = 16;
 template <int OP>
 __global__ __launch_bounds__(256) void k_col_combine(const float* __restrict__ partial, float* __restrict__ out,
@@ -170,13 +245,31 @@ __global__ __launch_bounds__(256) void k_expand_axis(const float* __restrict__ s
   }
 }
 
+// The partials of MEAN / VAR / PROD are plain sums: combine them with SUM
+// (finalizing divides where the op needs it).
 template <int OP>
-void reduce_impl(const float* x, const float* mean, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {
+constexpr int combine_op() { return OP == R_MAX ? R_MAX : OP == R_PROD ? R_SUM : OP; }
+
+template <int OP>
+void launch_col4(int ct, dim3 grid, const float* x, const float* y, const float* mean, float* dst, size_t axis,
+                 size_t inner, uint32_t nsplit, size_t chunk, bool finalize, hipStream_t s) {
+  switch (ct) {
+    case 8: k_col4<OP, 8><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize); break;
+    case 16: k_col4<OP, 16><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize); break;
+    case 32: k_col4<OP, 32><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize); break;
+    default: k_col4<OP, 64><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize); break;
+  }
+}
+
+template <int OP>
+void reduce_impl(const float* x, const float* y, const float* mean, float* out, size_t outer, size_t axis, size_t inner,
+                 hipStream_t s) {
+  constexpr int COMB = combine_op<OP>();
   const size_t n_out = outer * inner;
   if (n_out == 0) return;
   if (axis == 0) {  // empty reduction: sum/mean identities (mean/var of nothing -> NaN like 0/0)
     if (OP == R_MAX) fill(out, -INFINITY, n_out, s);
-    else if (OP == R_SUM) fill(out, 0.0f, n_out, s);
+    else if (OP == R_SUM || OP == R_PROD) fill(out, 0.0f, n_out, s);
     else fill(out, NAN, n_out, s);
     return;
   }
@@ -191,12 +284,11 @@ void reduce_impl(const float* x, const float* mean, float* out, size_t outer, si
       nsplit = (uint32_t)((axis + chunk - 1) / chunk);
       size_t bucket;
       float* partial = static_cast<float*>(pool_alloc(rows * nsplit * sizeof(float), &bucket));
-      k_row_split<OP><<<(unsigned)(rows * nsplit), 256, 0, s>>>(x, mean, partial, rows, axis, nsplit, chunk);
+      k_row_split<OP><<<(unsigned)(rows * nsplit), 256, 0, s>>>(x, y, mean, partial, axis, nsplit, chunk);
       MALUS_HIP(hipGetLastError());
       // combine partials of each row with one wave per row, then finalize
-      // (MEAN/VAR: the partials are plain sums, so combine them with SUM)
-      constexpr int COMB = (OP == R_MAX) ? R_MAX : R_SUM;
-      k_row_wave<COMB, false><<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(partial, nullptr, out, rows, nsplit, nsplit, false);
+      k_row_wave<COMB == R_MAX ? R_MAX : R_SUM, false>
+          <<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, rows, nsplit, nsplit, false);
       MALUS_HIP(hipGetLastError());
       if (OP == R_MEAN || OP == R_VAR) {
         // divide in place by the axis length
@@ -207,59 +299,84 @@ void reduce_impl(const float* x, const float* mean, float* out, size_t outer, si
     }
     const bool vec = (axis % 4) == 0;
     unsigned grid = (unsigned)((rows + 3) / 4);
-    if (vec) k_row_wave<OP, true><<<grid, 256, 0, s>>>(x, mean, out, rows, (uint32_t)axis, (uint32_t)axis, true);
-    else k_row_wave<OP, false><<<grid, 256, 0, s>>>(x, mean, out, rows, (uint32_t)axis, (uint32_t)axis, true);
+    if (vec) k_row_wave<OP, true><<<grid, 256, 0, s>>>(x, y, mean, out, rows, (uint32_t)axis, (uint32_t)axis, true);
+    else k_row_wave<OP, false><<<grid, 256, 0, s>>>(x, y, mean, out, rows, (uint32_t)axis, (uint32_t)axis, true);
     MALUS_HIP(hipGetLastError());
     return;
   }
   // column reduction
-  const uint32_t col_blocks = (uint32_t)((inner + 255) / 256);
-  size_t base_blocks = outer * col_blocks;
+  const bool aligned = ((uintptr_t)x | (uintptr_t)y | (uintptr_t)mean | (uintptr_t)out) % 16 == 0;
+  const bool vec = inner % 4 == 0 && outer <= 65535 && aligned;
+  size_t col_blocks, per_block_cols;
+  int ct = 64;
+  if (vec) {
+    const size_t groups = inner / 4;  // float4 columns
+    while (ct > 8 && groups % ct != 0) ct >>= 1;
+    if (groups % ct != 0) ct = 64;
+    per_block_cols = 4 * (size_t)ct;
+    col_blocks = (groups + ct - 1) / ct;
+  } else {
+    per_block_cols = 256;
+    col_blocks = (inner + 255) / 256;
+  }
+  const size_t base_blocks = outer * col_blocks;
+  // split the axis until the grid holds ~2048 workgroups, keeping >= 4 rows
+  // per row-thread (vec) or >= 16 rows per thread (scalar)
+  const size_t rows_per_block = vec ? (size_t)(256 / ct) * 4 : 16;
   uint32_t nsplit = 1;
-  if (base_blocks < 1024 && axis >= 64) {
-    nsplit = (uint32_t)((1024 + base_blocks - 1) / base_blocks);
-    if (nsplit > axis / 16) nsplit = (uint32_t)(axis / 16 > 0 ? axis / 16 : 1);
+  if (base_blocks < 2048) {
+    size_t want = (2048 + base_blocks - 1) / base_blocks;
+    size_t cap = axis / rows_per_block > 0 ? axis / rows_per_block : 1;
+    nsplit = (uint32_t)(want < cap ? want : cap);
+    if (nsplit > 65535) nsplit = 65535;
   }
   size_t chunk = (axis + nsplit - 1) / nsplit;
   nsplit = (uint32_t)((axis + chunk - 1) / chunk);
-  if (nsplit == 1) {
-    k_col<OP><<<(unsigned)(base_blocks), 256, 0, s>>>(x, mean, out, outer, axis, inner, 1, chunk, col_blocks, true);
-    MALUS_HIP(hipGetLastError());
-    return;
+  (void)per_block_cols;
+  float* dst = out;
+  size_t bucket = 0;
+  if (nsplit > 1) dst = static_cast<float*>(pool_alloc(outer * nsplit * inner * sizeof(float), &bucket));
+  if (vec) {
+    launch_col4<OP>(ct, dim3((unsigned)col_blocks, nsplit, (unsigned)outer), x, y, mean, dst, axis, inner, nsplit, chunk,
+                    nsplit == 1, s);
+  } else {
+    k_col<OP><<<(unsigned)(base_blocks * nsplit), 256, 0, s>>>(x, y, mean, dst, outer, axis, inner, nsplit, chunk,
+                                                                (uint32_t)col_blocks, nsplit == 1);
   }
-  size_t bucket;
-  float* partial = static_cast<float*>(pool_alloc(outer * nsplit * inner * sizeof(float), &bucket));
-  k_col<OP><<<(unsigned)(base_blocks * nsplit), 256, 0, s>>>(x, mean, partial, outer, axis, inner, nsplit, chunk,
-                                                              col_blocks, false);
   MALUS_HIP(hipGetLastError());
-  // base_blocks < 1024 here, so outer fits gridDim.y
-  dim3 cgrid((unsigned)((inner + kCombCols - 1) / kCombCols), (unsigned)outer);
-  k_col_combine<OP><<<cgrid, 256, 0, s>>>(partial, out, nsplit, inner, (uint32_t)axis);
-  MALUS_HIP(hipGetLastError());
-  pool_free(partial, bucket);
+  if (nsplit > 1) {
+    // base_blocks < 2048 here, so outer fits gridDim.y
+    dim3 cgrid((unsigned)((inner + kCombCols - 1) / kCombCols), (unsigned)outer);
+    if (OP == R_MAX) k_col_combine<R_MAX><<<cgrid, 256, 0, s>>>(dst, out, nsplit, inner, (uint32_t)axis);
+    else if (OP == R_MEAN || OP == R_VAR) k_col_combine<R_MEAN><<<cgrid, 256, 0, s>>>(dst, out, nsplit, inner, (uint32_t)axis);
+    else k_col_combine<R_SUM><<<cgrid, 256, 0, s>>>(dst, out, nsplit, inner, (uint32_t)axis);
+    MALUS_HIP(hipGetLastError());
+    pool_free(dst, bucket);
+  }
 }
 
 }  // namespace
 
-// k_col_combine<R_VAR>/<R_MEAN> sum partials then divide: rcomb is "+" for
-// both, and the element transform is applied only in the first stage.
-
 void reduce_axis(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {
   switch (op) {
-    case R_SUM: reduce_impl<R_SUM>(x, nullptr, out, outer, axis, inner, s); break;
-    case R_MEAN: reduce_impl<R_MEAN>(x, nullptr, out, outer, axis, inner, s); break;
-    case R_MAX: reduce_impl<R_MAX>(x, nullptr, out, outer, axis, inner, s); break;
+    case R_SUM: reduce_impl<R_SUM>(x, nullptr, nullptr, out, outer, axis, inner, s); break;
+    case R_MEAN: reduce_impl<R_MEAN>(x, nullptr, nullptr, out, outer, axis, inner, s); break;
+    case R_MAX: reduce_impl<R_MAX>(x, nullptr, nullptr, out, outer, axis, inner, s); break;
     case R_VAR: {
       // two-pass population variance (reduce_var.ml:11-22)
       size_t bucket;
       float* mean = static_cast<float*>(pool_alloc(outer * inner * sizeof(float), &bucket));
-      reduce_impl<R_MEAN>(x, nullptr, mean, outer, axis, inner, s);
-      reduce_impl<R_VAR>(x, mean, out, outer, axis, inner, s);
+      reduce_impl<R_MEAN>(x, nullptr, nullptr, mean, outer, axis, inner, s);
+      reduce_impl<R_VAR>(x, nullptr, mean, out, outer, axis, inner, s);
       pool_free(mean, bucket);
       break;
     }
     default: fail("malus: bad reduction op %d", op);
   }
+}
+
+void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {
+  reduce_impl<R_PROD>(x, y, nullptr, out, outer, axis, inner, s);
 }
 
 void expand_axis(const float* small, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {

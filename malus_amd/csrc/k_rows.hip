@@ -97,6 +97,43 @@ __global__ __launch_bounds__(256) void k_softmax_rows(const float* __restrict__ 
   t.store(y + row * axis, axis, lane);
 }
 
+// Attention scores: y = softmax((x * scale[0]) + mask[row % mask_rows]) over
+// the row, fusing nanogpt_modular.ml's `scores * scale`, `+ mask` and
+// softmax.  Each op rounds like its own kernel (the product, then the sum,
+// then softmax_axis_cpu), so y equals the three-kernel result bit for bit.
+template <int NV, bool VEC>
+__global__ __launch_bounds__(256) void k_scale_mask_softmax_rows(const float* __restrict__ x, const float* __restrict__ scale,
+                                                                 const float* __restrict__ mask, float* __restrict__ y,
+                                                                 size_t rows, uint32_t axis, uint32_t mask_rows) {
+  const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (row >= rows) return;
+  const float sc = scale[0];
+  RowTile<NV, VEC> t, mk;
+  t.load(x + row * axis, axis, lane, 0.0f);
+  mk.load(mask + (row % mask_rows) * axis, axis, lane, 0.0f);
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) {
+    const float ss = t.v[e] * sc;
+    t.v[e] = t.valid(e, lane, axis) ? ss + mk.v[e] : -INFINITY;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) m = fmaxf(m, t.v[e]);
+  m = wmax(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) {
+    float ex = t.valid(e, lane, axis) ? expf(t.v[e] - m) : 0.0f;
+    t.v[e] = ex;
+    s += ex;
+  }
+  s = wsum(s);
+#pragma unroll
+  for (int e = 0; e < NV * 4; ++e) t.v[e] = t.v[e] / s;
+  t.store(y + row * axis, axis, lane);
+}
+
 // tape.rs:1150-1161: dx = s * (dout - sum(dout * s))
 template <int NV, bool VEC>
 __global__ __launch_bounds__(256) void k_softmax_bwd_rows(const float* __restrict__ y, const float* __restrict__ dout,
@@ -330,6 +367,7 @@ void row_dispatch(uint32_t axis, Launch launch) {
 
 template <int NV, bool VEC> struct SelSoftmax { static constexpr auto fn = k_softmax_rows<NV, VEC>; };
 template <int NV, bool VEC> struct SelSoftmaxBwd { static constexpr auto fn = k_softmax_bwd_rows<NV, VEC>; };
+template <int NV, bool VEC> struct SelScaleMaskSoftmax { static constexpr auto fn = k_scale_mask_softmax_rows<NV, VEC>; };
 template <int NV, bool VEC> struct SelLN { static constexpr auto fn = k_layernorm_rows<NV, VEC>; };
 template <int NV, bool VEC> struct SelLNBwd { static constexpr auto fn = k_layernorm_bwd_rows<NV, VEC>; };
 template <int NV, bool VEC> struct SelCE { static constexpr auto fn = k_ce_fwd_rows<NV, VEC>; };
@@ -350,6 +388,26 @@ void softmax(const float* x, float* out, size_t outer, size_t axis, size_t inner
     k_softmax_seq<<<seq_grid(outer * inner), 256, 0, s>>>(x, out, outer, axis, inner);
   }
   MALUS_HIP(hipGetLastError());
+}
+
+void scale_mask_softmax(const float* S, const float* scale, const float* mask, float* P, size_t rows, size_t axis,
+                        size_t mask_rows, hipStream_t s) {
+  if (!rows || !axis) return;
+  if (axis <= kMaxRowAxis && mask_rows > 0) {
+    row_dispatch<SelScaleMaskSoftmax>((uint32_t)axis, [&](auto sel) {
+      decltype(sel)::fn<<<row_grid(rows), 256, 0, s>>>(S, scale, mask, P, rows, (uint32_t)axis, (uint32_t)mask_rows);
+    });
+    MALUS_HIP(hipGetLastError());
+    return;
+  }
+  // wide rows: the three separate kernels through a temporary
+  const size_t n = rows * axis;
+  size_t bucket;
+  float* tmp = static_cast<float*>(pool_alloc(n * sizeof(float), &bucket));
+  binary_scalar(MUL, S, scale, 0.0f, true, tmp, n, s);
+  binary_rowbcast(ADD, tmp, mask, tmp, n, mask_rows * axis, s);
+  softmax(tmp, P, rows, axis, 1, s);
+  pool_free(tmp, bucket);
 }
 
 void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {

@@ -84,6 +84,7 @@ struct Gpt {
   int V, Tn, C, H, L, B;
   float lr, b1, b2, eps, wd;
   bool fused_opt = true;
+  bool fused_attn = true;  // scale + mask + softmax in one kernel (same values, same tape records)
   std::vector<int64_t> p, m, v;  // block l params at 8l..8l+7, then wte, wpe, ln_f, lm_head
   int64_t pos = 0;               // [B*T] i32 position ids
 
@@ -115,11 +116,27 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   tensor_release(ones11);
   tape_register_leaf(scale);  // variable(...)
   int64_t S = binop(OP_MATMUL, Q, Kt);
-  int64_t Ss = binop(OP_MUL, S, scale);
   int64_t mask = tensor_causal_mask((int64_t)Tn);
   tape_register_leaf(mask);  // variable(mask)
-  int64_t Sm = binop(OP_ADD, Ss, mask);
-  int64_t Pm = malus_std_softmax_fwd(Sm, 2);
+  int64_t Ss, Sm, Pm;
+  if (g.fused_attn) {
+    // scores * scale + mask -> softmax in one pass.  The tape gets the same
+    // three records; the two intermediates are shape-only handles because
+    // no VJP reads their values (add: shapes; mul: S and scale; softmax: P).
+    TensorBuffer* st = T(S);
+    Ss = malus::H(alloc_virtual(F32, st->shape, st->ndim));
+    Sm = malus::H(alloc_virtual(F32, st->shape, st->ndim));
+    TensorBuffer* p = alloc_tensor(F32, st->shape, st->ndim);
+    k::scale_mask_softmax(st->f32(), T(scale)->f32(), T(mask)->f32(), p->f32(), st->len / Tn, Tn, Tn, stream());
+    p->write_seq = enqueue_mark("scale_mask_softmax");
+    Pm = malus::H(p);
+    tape_record_binop(OP_MUL, S, scale, Ss);
+    tape_record_binop(OP_ADD, Ss, mask, Sm);
+  } else {
+    Ss = binop(OP_MUL, S, scale);
+    Sm = binop(OP_ADD, Ss, mask);
+    Pm = malus_std_softmax_fwd(Sm, 2);
+  }
   tape_record_reduce(OP_SOFTMAX, Sm, Pm, 2, 0);
   int64_t AO = binop(OP_MATMUL, Pm, Vv);
   int64_t ao4 = reshape(AO, {B, H, Tn, hs});
@@ -167,15 +184,43 @@ int64_t gpt_forward_loss(Gpt& g, int64_t toks, int64_t targets, int64_t* logits_
   return loss;
 }
 
-// adamw (nanogpt_modular.ml:97-108) for params [beg, end)
+// adamw (nanogpt_modular.ml:97-108) for params [beg, end).  The fused form
+// updates every tensor in one multi-tensor launch with the same per-element
+// expression tree as the op-by-op sequence the JIT emits.
 void adamw_range(Gpt& g, int beg, int end, int64_t t) {
   const float bc1 = 1.0f - powf(g.b1, (float)t), bc2 = 1.0f - powf(g.b2, (float)t);
+  if (g.fused_opt) {
+    std::vector<k::AdamSeg> segs;
+    std::vector<int64_t> grads, np_(end - beg), nm(end - beg), nv(end - beg);
+    for (int i = beg; i < end; ++i) {
+      int64_t grad = tape_get_grad(g.p[i]);
+      grads.push_back(grad);
+      TensorBuffer *tp = T(g.p[i]), *tg = T(grad), *tm = T(g.m[i]), *tv = T(g.v[i]);
+      if (tg->len != tp->len || tm->len != tp->len || tv->len != tp->len) fail("malus: adam update: length mismatch");
+      TensorBuffer *po = alloc_like(tp), *mo = alloc_like(tp), *vo = alloc_like(tp);
+      np_[i - beg] = H(po);
+      nm[i - beg] = H(mo);
+      nv[i - beg] = H(vo);
+      segs.push_back(k::AdamSeg{tp->f32(), tg->f32(), tm->f32(), tv->f32(), po->f32(), mo->f32(), vo->f32(), tp->len});
+    }
+    k::adam_l2_multi(segs.data(), (int)segs.size(), g.lr, g.b1, g.b2, 1.0f - g.b1, 1.0f - g.b2, bc1, bc2, g.eps, g.wd,
+                     stream());
+    const uint64_t seq = enqueue_mark("adam");
+    for (int i = beg; i < end; ++i) {
+      T(np_[i - beg])->write_seq = T(nm[i - beg])->write_seq = T(nv[i - beg])->write_seq = seq;
+      tensor_release(grads[i - beg]);
+      tape_register_leaf(np_[i - beg]);  // ps[i] = variable(...)
+      rel({g.p[i], g.m[i], g.v[i]});
+      g.p[i] = np_[i - beg];
+      g.m[i] = nm[i - beg];
+      g.v[i] = nv[i - beg];
+    }
+    return;
+  }
   for (int i = beg; i < end; ++i) {
     int64_t grad = tape_get_grad(g.p[i]);
     int64_t np_, nm, nv;
-    if (g.fused_opt) {
-      np_ = malus_std_adam_l2(g.p[i], grad, g.m[i], g.v[i], g.lr, g.b1, g.b2, g.eps, g.wd, t, &nm, &nv);
-    } else {  // the op-by-op sequence the JIT emits
+    {  // the op-by-op sequence the JIT emits
       int64_t wdp = malus_std_scalar_op(k::MUL, g.p[i], g.wd, 0);
       int64_t gg = malus_std_broadcast_fwd(k::ADD, grad, wdp);
       int64_t t1 = malus_std_scalar_op(k::MUL, g.m[i], g.b1, 0);
@@ -283,6 +328,10 @@ int64_t malus_gpt_moment(void* gp, int i, int which) {
   auto* g = static_cast<Gpt*>(gp);
   return which ? g->v[(size_t)i] : g->m[(size_t)i];
 }
+// 1 (default): scores * scale + mask -> softmax as one kernel; 0: the three
+// separate ops.  Values and tape records are the same either way.
+void malus_gpt_set_fused_attention(void* gp, int on) { static_cast<Gpt*>(gp)->fused_attn = on != 0; }
+
 void malus_gpt_set_fused_optimizer(void* gp, int on) { static_cast<Gpt*>(gp)->fused_opt = on != 0; }
 
 // Forward + cross-entropy (recorded on the tape); returns the loss [1].

@@ -290,6 +290,23 @@ TensorBuffer* alloc_f32(std::initializer_list<size_t> shape) {
   return alloc_tensor(F32, s, n);
 }
 
+TensorBuffer* alloc_virtual(int32_t dtype, const size_t* shape, int ndim) {
+  if (ndim < 0 || ndim > kMaxRank) fail("malus: tensor rank %d exceeds %d", ndim, kMaxRank);
+  auto* t = new TensorBuffer();
+  t->dtype = dtype;
+  t->ndim = ndim;
+  size_t n = 1;
+  for (int i = 0; i < ndim; ++i) { t->shape[i] = shape[i]; n *= shape[i]; }
+  t->len = n;
+  auto* st = new Storage();
+  st->ptr = nullptr;
+  st->bytes = 0;
+  st->aliases = 1;
+  t->st = st;
+  g_alloc++;
+  return t;
+}
+
 TensorBuffer* make_alias(TensorBuffer* src, const size_t* shape, int ndim) {
   // reshape_to, metal.rs:1385-1403: same storage, inherited pending state
   auto* t = new TensorBuffer();
@@ -363,6 +380,7 @@ void upload(void* dst, const void* src, size_t bytes) {
 void download(void* dst, const TensorBuffer* t, size_t bytes) {
   flush_if_pending(const_cast<TensorBuffer*>(t));
   if (!bytes) return;
+  if (!t->st->ptr) fail("malus: tensor %s has no device storage (an intermediate of a fused kernel)", shape_str(t).c_str());
   Context& c = ctx();
   MALUS_HIP(hipMemcpyAsync(dst, t->data(), bytes, hipMemcpyDeviceToHost, c.stream));
   MALUS_HIP(hipStreamSynchronize(c.stream));

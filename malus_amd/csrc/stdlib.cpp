@@ -107,11 +107,19 @@ TensorBuffer* broadcast_binop(int op, const TensorBuffer* p, const TensorBuffer*
 }
 
 // Reduce `dout` down to `target`'s shape (sum over broadcast dims),
-// elementwise_bwd.ml:8-22.  Equal shapes return a retained alias.
-TensorBuffer* sum_to_shape(TensorBuffer* g, const TensorBuffer* target) {
+// elementwise_bwd.ml:8-22.  Equal shapes return a retained alias.  With
+// `mul` (same shape as g), reduces g * mul without materializing it: the
+// first reduction pass multiplies on load, every product rounded to f32 as
+// the materialized tensor's would be, so results are bit-identical.
+TensorBuffer* sum_to_shape(TensorBuffer* g, const TensorBuffer* target, const TensorBuffer* mul = nullptr) {
   if (same_shape(g, target)) {
-    retain(g);
-    return g;
+    if (!mul) {
+      retain(g);
+      return g;
+    }
+    TensorBuffer* out = alloc_tensor(F32, target->shape, target->ndim);
+    k::binary_same(k::MUL, g->f32(), mul->f32(), out->f32(), out->len, stream());
+    return out;
   }
   const int gn = g->ndim, tn = target->ndim;
   if (tn > gn) fail("malus: sum_to_shape: target rank %d exceeds gradient rank %d", tn, gn);
@@ -134,6 +142,7 @@ TensorBuffer* sum_to_shape(TensorBuffer* g, const TensorBuffer* target) {
   hipStream_t s = stream();
   // reduce runs one at a time from the last, keeping a running [.., R, K] view
   const float* src = g->f32();
+  const float* src_mul = mul ? mul->f32() : nullptr;  // applies to the first pass only
   std::vector<std::pair<void*, size_t>> temps;
   size_t cur_len = g->len;
   for (int r = (int)runs.size() - 1; r >= 0; --r) {
@@ -152,12 +161,17 @@ TensorBuffer* sum_to_shape(TensorBuffer* g, const TensorBuffer* target) {
       dst = static_cast<float*>(pool_alloc(out_len * sizeof(float), &b));
       temps.push_back({dst, b});
     }
-    k::reduce_axis(k::R_SUM, src, dst, outer, runs[r].n, inner, s);
+    if (src_mul) k::reduce_axis_prod(src, src_mul, dst, outer, runs[r].n, inner, s);
+    else k::reduce_axis(k::R_SUM, src, dst, outer, runs[r].n, inner, s);
+    src_mul = nullptr;
     src = dst;
     cur_len = out_len;
     runs[r].n = 1;
   }
-  if (src != out->f32()) k::copy(src, out->f32(), out->bytes(), s);  // nothing to reduce (all size-1)
+  if (src != out->f32()) {  // nothing to reduce (all size-1)
+    if (src_mul) k::binary_same(k::MUL, src, src_mul, out->f32(), out->len, s);
+    else k::copy(src, out->f32(), out->bytes(), s);
+  }
   for (auto& t : temps) pool_free(t.first, t.second);
   return out;
 }
@@ -454,6 +468,8 @@ int64_t malus_std_sub_bwd_b(int64_t dout, int64_t b) {
 }
 int64_t malus_std_mul_bwd_a(int64_t dout, int64_t a, int64_t b) {
   API_TRY
+  if (same_shape(T(dout), T(b)) && !same_shape(T(dout), T(a)))  // reduce dout * b without materializing it
+    return done(sum_to_shape(T(dout), T(a), T(b)), "mul_bwd_a");
   int64_t full = malus_std_broadcast_mul_fwd(dout, b);
   int64_t r = malus_std_sum_to_shape_bwd(full, a);
   release(T(full));
@@ -462,6 +478,8 @@ int64_t malus_std_mul_bwd_a(int64_t dout, int64_t a, int64_t b) {
 }
 int64_t malus_std_mul_bwd_b(int64_t dout, int64_t a, int64_t b) {
   API_TRY
+  if (same_shape(T(dout), T(a)) && !same_shape(T(dout), T(b)))  // reduce dout * a without materializing it
+    return done(sum_to_shape(T(dout), T(b), T(a)), "mul_bwd_b");
   int64_t full = malus_std_broadcast_mul_fwd(dout, a);
   int64_t r = malus_std_sum_to_shape_bwd(full, b);
   release(T(full));

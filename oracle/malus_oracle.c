@@ -161,16 +161,22 @@ static float gelu_f(float x) {
     return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-/* codegen-gpu/lib.rs:375-381 synthesize_unary_builtin; gelu per above. */
+/* codegen-gpu/lib.rs:375-381 synthesize_unary_builtin; gelu per above.
+ * exp / log / tanh (also inside sigmoid) are the correctly rounded f32
+ * functions: evaluated in double and rounded once.  The reference's host f32
+ * calls go to the platform libm (Apple's on its Metal hosts, glibc here),
+ * which is within 1 ulp but not correctly rounded; the sigmoid formula
+ * amplifies that last-bit choice (1 + e rounds at e's spacing), so the
+ * platform-independent correctly rounded functions are the restatement. */
 void or_unary(int op, const float* a, size_t n, float* out) {
     for (size_t i = 0; i < n; ++i) {
         float x = a[i];
         switch (op) {
         case OR_RELU: out[i] = fmaxf(0.0f, x); break;
-        case OR_SIGMOID: out[i] = 1.0f / (1.0f + expf(-x)); break;
-        case OR_TANH: out[i] = tanhf(x); break;
-        case OR_EXP: out[i] = expf(x); break;
-        case OR_LOG: out[i] = logf(x); break;
+        case OR_SIGMOID: out[i] = 1.0f / (1.0f + (float)exp(-(double)x)); break;
+        case OR_TANH: out[i] = (float)tanh((double)x); break;
+        case OR_EXP: out[i] = (float)exp((double)x); break;
+        case OR_LOG: out[i] = (float)log((double)x); break;
         case OR_SQRT: out[i] = sqrtf(x); break;
         case OR_ABS: out[i] = fabsf(x); break;
         case OR_GELU: out[i] = gelu_f(x); break;
@@ -738,7 +744,6 @@ float or_gpt_loss_and_grads(or_gpt* g, const int32_t* xt, const int32_t* yt, flo
     const int B = g->B, Tn = g->Tn, C = g->C, H = g->H, L = g->L, V = g->V;
     const int hs = C / H;
     const size_t N = (size_t)B * Tn;
-    const size_t C4 = (size_t)4 * C;
     const float scale = 1.0f / sqrtf((float)hs);
     /* forward (nanogpt_modular.ml:75-91, 38-68) */
     T te = tnew2(N, (size_t)C), pe = tnew2(N, (size_t)C);

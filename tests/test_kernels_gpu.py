@@ -42,6 +42,29 @@ def test_broadcast_binop(rt, op, shapes):
     rt.free(ha, hb)
 
 
+@pytest.mark.parametrize("big,small", [((64, 384), (384,)), ((64, 384), (1, 384)), ((6, 40, 52), (1, 1)),
+                                       ((3, 5, 7), (5, 1)), ((4, 8, 16), (1, 8, 1)), ((1, 5), (5,)), ((33, 70001), (1, 1))])
+def test_mul_vjp_fused_reduction_matches_materialized(rt, big, small):
+    """The broadcast-multiply VJP reduces dout * a without materializing the
+    product; it must equal broadcast_mul then sum_to_shape bit for bit, and
+    the oracle's sum_to_shape of the product to the reduction bar."""
+    dout, a, b = rand(*big), rand(*big), rand(*small)
+    hd, ha, hb = rt.tensor(dout), rt.tensor(a), rt.tensor(b)
+    fused_b = run(rt, rt.L.malus_std_mul_bwd_b(hd, ha, hb))
+    fused_a = run(rt, rt.L.malus_std_mul_bwd_a(hd, hb, ha))  # roles swapped: grad of the broadcast operand
+    full = rt.L.malus_std_broadcast_fwd(M.MUL, hd, ha)
+    ref = run(rt, rt.L.malus_std_sum_to_shape_bwd(full, hb))
+    assert_bitexact(fused_b, ref, f"mul_bwd_b {big} {small}")
+    assert_bitexact(fused_a, ref, f"mul_bwd_a {big} {small}")
+    prod = dout * a  # f32 products, as the kernel rounds them
+    want = O.sum_to_shape(prod, small)
+    pad = (1,) * (len(big) - len(small)) + tuple(small)
+    axes = tuple(i for i in range(len(big)) if pad[i] == 1 and big[i] != 1)
+    exact = prod.astype(np.float64).sum(axis=axes, keepdims=True).reshape(small)
+    assert_reduction(fused_b, want, exact, 1e-5, f"vs oracle {big} {small}")
+    rt.free(hd, ha, hb, full)
+
+
 def test_broadcast_operand_swap_quirk(rt):
     # broadcast_binop.ml:90-112: rank(a) < rank(b) computes b - a
     a, b = rand(8), rand(4, 8)

@@ -51,7 +51,7 @@ def test_xor_10000_steps_vs_oracle(rt):
 
 
 class GpuGpt:
-    def __init__(self, rt, cfg, rng_call_idx=0, fused=True):
+    def __init__(self, rt, cfg, rng_call_idx=0, fused=True, fused_attention=True):
         self.rt = rt
         self.cfg = cfg
         rt.L.tape_reset()
@@ -59,6 +59,7 @@ class GpuGpt:
         self.g = rt.L.malus_gpt_create(cfg["V"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["B"], OPT["lr"],
                                        OPT["b1"], OPT["b2"], OPT["eps"], OPT["wd"])
         rt.L.malus_gpt_set_fused_optimizer(self.g, int(fused))
+        rt.L.malus_gpt_set_fused_attention(self.g, int(fused_attention))
 
     def close(self):
         self.rt.L.malus_gpt_free(self.g)
@@ -140,6 +141,30 @@ def test_gpt_fused_optimizer_equals_op_by_op(rt):
     assert la == lb
     for i, (u, v) in enumerate(zip(pa, pb)):
         np.testing.assert_array_equal(u, v, err_msg=f"param {i}")
+
+
+def test_gpt_fused_attention_equals_three_ops(rt):
+    """scale + mask + softmax as one kernel (shape-only intermediates on the
+    tape) gives the same loss, gradients and updated parameters as the three
+    separate ops, bit for bit."""
+    cfg = dict(V=65, T=64, C=64, H=4, L=2, B=4)
+    x, y = tokens(cfg, 6000)
+    out = []
+    for fa in (True, False):
+        g = GpuGpt(rt, cfg, fused_attention=fa)
+        try:
+            loss = g.loss_and_grads(x, y)
+            grads = [g.grad(i) for i in range(8 * cfg["L"] + 4)]
+            l2 = g.step(x, y, 1)
+            params = [g.param(i) for i in range(8 * cfg["L"] + 4)]
+        finally:
+            g.close()
+        out.append((loss, grads, l2, params))
+    (la, ga, sa, pa), (lb, gb, sb, pb) = out
+    assert la == lb and sa == sb
+    for i in range(len(ga)):
+        np.testing.assert_array_equal(ga[i], gb[i], err_msg=f"grad {i}")
+        np.testing.assert_array_equal(pa[i], pb[i], err_msg=f"param {i}")
 
 
 def test_gpt_c4_200_step_loss_trajectory(rt):
