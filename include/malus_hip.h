@@ -112,6 +112,8 @@ void backward(int64_t loss);                                                    
 void tape_zero_grad(const int64_t* handles, size_t count);                                     /* tape.rs:757-774 */
 void tape_reset(void);                                                                         /* tape.rs:735-750 */
 void tape_register_backward_fn(int32_t slot, size_t fnptr);                                    /* tape.rs:143-147 */
+/* 1 (default): gradient accumulation folded into matmul/layernorm VJP kernels; 0: separate adds (same values). */
+void malus_tape_set_fused_vjps(int on);
 /* No reference counterpart: the pointer currently held by a BwdSlot. */
 size_t malus_tape_backward_fn(int32_t slot);
 size_t malus_tape_len(void);
@@ -221,8 +223,8 @@ int malus_gpt_nparams(void* g);
 int64_t malus_gpt_param(void* g, int i);              /* borrowed */
 int64_t malus_gpt_moment(void* g, int i, int which);  /* borrowed; which 0 = m, 1 = v */
 void malus_gpt_set_fused_optimizer(void* g, int on);
-/* 1 (default): attention scale + mask + softmax as one kernel; 0: three separate ops (same values and tape). */
-void malus_gpt_set_fused_attention(void* g, int on);
+/* 1 (default): forward fusions (attention scale+mask+softmax, residual adds in GEMM epilogues); 0: separate ops (same values and tape). */
+void malus_gpt_set_fused_forward(void* g, int on);
 int64_t malus_gpt_forward_loss(void* g, int64_t toks, int64_t targets); /* nanogpt_modular.ml:75-91 + cross_entropy */
 int64_t malus_gpt_logits(void* g, int64_t toks);
 void malus_gpt_zero_grad(void* g);

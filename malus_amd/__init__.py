@@ -161,7 +161,8 @@ SIGNATURES = {
     "malus_gpt_param": (_i64, [_vp, C.c_int]),
     "malus_gpt_moment": (_i64, [_vp, C.c_int, C.c_int]),
     "malus_gpt_set_fused_optimizer": (None, [_vp, C.c_int]),
-    "malus_gpt_set_fused_attention": (None, [_vp, C.c_int]),
+    "malus_gpt_set_fused_forward": (None, [_vp, C.c_int]),
+    "malus_tape_set_fused_vjps": (None, [C.c_int]),
     "malus_gpt_forward_loss": (_i64, [_vp, _i64, _i64]),
     "malus_gpt_logits": (_i64, [_vp, _i64]),
     "malus_gpt_zero_grad": (None, [_vp]),

@@ -24,6 +24,15 @@ std::vector<size_t> tape_normalize_perm(const std::vector<size_t>& raw, size_t r
 
 }  // namespace malus
 
+namespace malus { struct TensorBuffer; }
+// Matmul and its VJPs with an optional addend of the output's shape: returns
+// D + product from one GEMM (the product rounded before the add, as a
+// separate broadcast add would round it).  D == nullptr is the plain op.
+int64_t matmul_impl(int64_t a, int64_t b, const malus::TensorBuffer* D);
+int64_t matmul_bwd_a_impl(int64_t a, int64_t b, int64_t dout, const malus::TensorBuffer* D);
+int64_t matmul_bwd_b_impl(int64_t a, int64_t b, int64_t dout, const malus::TensorBuffer* D);
+int64_t layernorm_bwd_impl(int64_t y, int64_t var, int64_t dout, int64_t axis, const malus::TensorBuffer* D);
+
 #define API_TRY try {
 #define API_CATCH(...)                                   \
   }                                                      \

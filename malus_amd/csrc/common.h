@@ -144,8 +144,10 @@ void expand_axis(const float* small, float* out, size_t outer, size_t axis, size
 void softmax(const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s);
+// With addend: dx = addend + VJP (gradient accumulation folded in).
 void layernorm_bwd(const float* y, const float* var, const float* dout, float* dx, size_t outer, size_t axis, size_t inner,
-                   float eps, hipStream_t s);
+                   float eps, hipStream_t s,
+                   const float* addend = nullptr);
 // probs = softmax(logits) rows; nll[i] = -log(probs[i, t_i]).
 void ce_fwd(const float* logits, const int32_t* tgt, float* probs, float* nll, size_t n, size_t v, int32_t* err, hipStream_t s);
 // scale = dout[0] / n when dout is given (read on the device), else scale_host.
@@ -161,8 +163,11 @@ void permute(const float* x, float* out, int ndim, const size_t* in_shape, const
 
 // Batched GEMM: C[b] = op(A[b]) @ op(B[b]); transA: A stored [K,M]; transB: B stored [N,K].
 // strideA/B/C are element strides between batches (0 broadcasts).
+// With D (C's layout and batch stride), C = D + op(A) @ op(B): the GEMM
+// result is rounded to f32 before the add, exactly as a separate add of the
+// stored product would round.
 void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
-          long strideA, long strideB, long strideC, hipStream_t s);
+          long strideA, long strideB, long strideC, hipStream_t s, const float* D = nullptr);
 
 // Fused Adam + L2 update (examples/nanogpt_modular.ml:97-108 op order).
 // One parameter tensor of a multi-tensor Adam update (device pointers).

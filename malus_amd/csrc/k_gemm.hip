@@ -130,7 +130,8 @@ struct Tile {
 template <int TM, int TN, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, const float* __restrict__ B,
                                                   float* __restrict__ C, int M, int N, int K, long sA, long sB, long sC,
-                                                  int k_chunk, int tiles_n, long split_stride) {
+                                                  int k_chunk, int tiles_n, long split_stride,
+                                                  const float* __restrict__ D) {
   constexpr int BM = 64 * TM, BN = 64 * TN;
   using TileA = Tile<BM, !TA, VA>;  // A [M][K] is k-contiguous
   using TileB = Tile<BN, TB, VB>;   // B^T [N][K] is k-contiguous
@@ -146,6 +147,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
   A += (size_t)b * sA;
   B += (size_t)b * sB;
   C += (size_t)b * sC + (size_t)blockIdx.y * split_stride;
+  if (D) D += (size_t)b * sC;
   const int kbeg = blockIdx.y * k_chunk;
   const int kend = min(K, kbeg + k_chunk);
   const long lda = TA ? M : K, ldb = TB ? K : N;
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
-          if (m < M) C[(size_t)m * N + n] = acc[i][j][r];
+          if (m < M) C[(size_t)m * N + n] = D ? D[(size_t)m * N + n] + acc[i][j][r] : acc[i][j][r];
         }
       }
     }
@@ -286,7 +288,8 @@ struct DmaSlab {
 template <int TM, int TN, bool TA, bool TB>
 __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int M, int N, int K, long sA, long sB,
-                                                      long sC, int k_chunk, int tiles_n, long split_stride) {
+                                                      long sC, int k_chunk, int tiles_n, long split_stride,
+                                                      const float* __restrict__ D) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 64 * TM, BN = 64 * TN;
   using SlabA = DmaSlab<BM, !TA>;  // A [M][K] is k-contiguous
@@ -303,6 +306,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   A += (size_t)b * sA;
   B += (size_t)b * sB;
   C += (size_t)b * sC + (size_t)blockIdx.y * split_stride;
+  if (D) D += (size_t)b * sC;
   const int kbeg = blockIdx.y * k_chunk;
   const int kend = min(K, kbeg + k_chunk);
 
@@ -363,21 +367,22 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
-          if (m < M) C[(size_t)m * N + n] = acc[i][j][r];
+          if (m < M) C[(size_t)m * N + n] = D ? D[(size_t)m * N + n] + acc[i][j][r] : acc[i][j][r];
         }
       }
     }
 #endif
 }
 
-// C[i] = sum over splits s (in order) of partial[s * mn + i]
+// C[i] = sum over splits s (in order) of partial[s * mn + i], then + D[i]
+// when an addend is given (the same rounding as adding to the stored sum).
 __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ partial, float* __restrict__ C, size_t mn,
-                                                      int nsplit) {
+                                                      int nsplit, const float* __restrict__ D) {
   size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += stride) {
     float acc = partial[i];
     for (int s = 1; s < nsplit; ++s) acc += partial[(size_t)s * mn + i];
-    C[i] = acc;
+    C[i] = D ? D[i] + acc : acc;
   }
 }
 
@@ -505,7 +510,7 @@ Plan plan_gemm(int batch, int M, int N, int K, int v) {
 }  // namespace
 
 void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB, long sA,
-          long sB, long sC, hipStream_t s) {
+          long sB, long sC, hipStream_t s, const float* D) {
   if (batch <= 0 || M <= 0 || N <= 0) return;
   if (K <= 0) {  // empty inner dimension: all-zero result (metal.rs:837-839 falls to the CPU loop)
     fill(C, 0.0f, (size_t)batch * M * N, s);
@@ -534,13 +539,14 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
   float* dst = C;
   if (nsplit > 1) dst = static_cast<float*>(pool_alloc(mn * nsplit * sizeof(float), &bucket));
   long split_stride = nsplit > 1 ? (long)mn : 0;
-  void* args[] = {&A, &B, &dst, &M, &N, &K, &sA, &sB, &sC, &k_chunk, const_cast<int*>(&tiles_n), &split_stride};
+  const float* Dk = nsplit > 1 ? nullptr : D;  // split-K applies the addend in the reduction
+  void* args[] = {&A, &B, &dst, &M, &N, &K, &sA, &sB, &sC, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk};
   MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, v), dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch),
                             dim3(256), args, 0, s));
   if (nsplit > 1) {
     size_t blocks = (mn + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    k_split_reduce<<<(unsigned)blocks, 256, 0, s>>>(dst, C, mn, nsplit);
+    k_split_reduce<<<(unsigned)blocks, 256, 0, s>>>(dst, C, mn, nsplit, D);
     MALUS_HIP(hipGetLastError());
     pool_free(dst, bucket);
   }

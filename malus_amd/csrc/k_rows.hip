@@ -185,7 +185,8 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(const float* __restrict_
 template <int NV, bool VEC>
 __global__ __launch_bounds__(256) void k_layernorm_bwd_rows(const float* __restrict__ y, const float* __restrict__ var,
                                                             const float* __restrict__ dout, float* __restrict__ dx,
-                                                            size_t rows, uint32_t axis, float eps) {
+                                                            size_t rows, uint32_t axis, float eps,
+                                                            const float* __restrict__ addend) {
   const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
@@ -206,6 +207,11 @@ __global__ __launch_bounds__(256) void k_layernorm_bwd_rows(const float* __restr
     float tmp = dt.v[e] - dy_mean;
     float numer = tmp - y_term;
     yt.v[e] = numer * inv_sigma;
+  }
+  if (addend) {  // gradient accumulation: old + this VJP's value
+    dt.load(addend + row * axis, axis, lane, 0.0f);
+#pragma unroll
+    for (int e = 0; e < NV * 4; ++e) yt.v[e] = dt.v[e] + yt.v[e];
   }
   yt.store(dx + row * axis, axis, lane);
 }
@@ -435,14 +441,15 @@ void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, 
 }
 
 void layernorm_bwd(const float* y, const float* var, const float* dout, float* dx, size_t outer, size_t axis, size_t inner,
-                   float eps, hipStream_t s) {
+                   float eps, hipStream_t s, const float* addend) {
   if (!outer || !axis || !inner) return;
   if (inner == 1 && axis <= kMaxRowAxis) {
     row_dispatch<SelLNBwd>((uint32_t)axis, [&](auto sel) {
-      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(y, var, dout, dx, outer, (uint32_t)axis, eps);
+      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(y, var, dout, dx, outer, (uint32_t)axis, eps, addend);
     });
   } else {
     k_layernorm_bwd_seq<<<seq_grid(outer * inner), 256, 0, s>>>(y, var, dout, dx, outer, axis, inner, eps);
+    if (addend) binary_same(ADD, addend, dx, dx, outer * axis * inner, s);
   }
   MALUS_HIP(hipGetLastError());
 }

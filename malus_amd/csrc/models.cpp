@@ -76,6 +76,17 @@ int64_t layernorm(int64_t x) {
   return y;
 }
 
+// out = x + a @ w with the add in the GEMM epilogue.  The tape gets the
+// reference's two records, MATMUL(a, w -> prod) and ADD(x, prod -> out);
+// prod is a shape-only handle since neither VJP reads its values.
+void residual_matmul(int64_t x, int64_t a, int64_t w, int64_t* prod, int64_t* out) {
+  *out = matmul_impl(a, w, T(x));
+  TensorBuffer* o = T(*out);
+  *prod = malus::H(alloc_virtual(F32, o->shape, o->ndim));
+  tape_record_binop(OP_MATMUL, a, w, *prod);
+  tape_record_binop(OP_ADD, x, *prod, *out);
+}
+
 void rel(std::initializer_list<int64_t> hs) {
   for (int64_t h : hs) tensor_release(h);
 }
@@ -84,7 +95,7 @@ struct Gpt {
   int V, Tn, C, H, L, B;
   float lr, b1, b2, eps, wd;
   bool fused_opt = true;
-  bool fused_attn = true;  // scale + mask + softmax in one kernel (same values, same tape records)
+  bool fused_fwd = true;  // forward fusions: scale+mask+softmax, residual adds in GEMM epilogues (same values, same tape)
   std::vector<int64_t> p, m, v;  // block l params at 8l..8l+7, then wte, wpe, ln_f, lm_head
   int64_t pos = 0;               // [B*T] i32 position ids
 
@@ -119,7 +130,7 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   int64_t mask = tensor_causal_mask((int64_t)Tn);
   tape_register_leaf(mask);  // variable(mask)
   int64_t Ss, Sm, Pm;
-  if (g.fused_attn) {
+  if (g.fused_fwd) {
     // scores * scale + mask -> softmax in one pass.  The tape gets the same
     // three records; the two intermediates are shape-only handles because
     // no VJP reads their values (add: shapes; mul: S and scale; softmax: P).
@@ -142,15 +153,23 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   int64_t ao4 = reshape(AO, {B, H, Tn, hs});
   int64_t aop = permute(ao4, {0, 2, 1, 3});
   int64_t att = reshape(aop, {N, C});
-  int64_t proj = binop(OP_MATMUL, att, P[4]);
-  int64_t x2 = binop(OP_ADD, x, proj);
+  int64_t proj, x2;
+  if (g.fused_fwd) residual_matmul(x, att, P[4], &proj, &x2);
+  else {
+    proj = binop(OP_MATMUL, att, P[4]);
+    x2 = binop(OP_ADD, x, proj);
+  }
   int64_t y2 = layernorm(x2);
   int64_t xn2 = binop(OP_MUL, y2, P[5]);
   int64_t h = binop(OP_MATMUL, xn2, P[6]);
   int64_t ge = malus_std_gelu_fwd(h);
   tape_record_unary(OP_GELU, h, ge);
-  int64_t mo = binop(OP_MATMUL, ge, P[7]);
-  int64_t x3 = binop(OP_ADD, x2, mo);
+  int64_t mo, x3;
+  if (g.fused_fwd) residual_matmul(x2, ge, P[7], &mo, &x3);
+  else {
+    mo = binop(OP_MATMUL, ge, P[7]);
+    x3 = binop(OP_ADD, x2, mo);
+  }
   rel({y1, xn1, Q, K, Vv, Kt, scale, S, Ss, mask, Sm, Pm, AO, ao4, aop, att, proj, x2, y2, xn2, h, ge, mo});
   return x3;
 }
@@ -328,9 +347,10 @@ int64_t malus_gpt_moment(void* gp, int i, int which) {
   auto* g = static_cast<Gpt*>(gp);
   return which ? g->v[(size_t)i] : g->m[(size_t)i];
 }
-// 1 (default): scores * scale + mask -> softmax as one kernel; 0: the three
-// separate ops.  Values and tape records are the same either way.
-void malus_gpt_set_fused_attention(void* gp, int on) { static_cast<Gpt*>(gp)->fused_attn = on != 0; }
+// 1 (default): forward fusions on — scores * scale + mask -> softmax as one
+// kernel, and the residual adds folded into the producing GEMM's epilogue;
+// 0: every op separately.  Values and tape records are the same either way.
+void malus_gpt_set_fused_forward(void* gp, int on) { static_cast<Gpt*>(gp)->fused_fwd = on != 0; }
 
 void malus_gpt_set_fused_optimizer(void* gp, int on) { static_cast<Gpt*>(gp)->fused_opt = on != 0; }
 

@@ -195,10 +195,13 @@ TensorBuffer* as_i32_indices(TensorBuffer* idx, bool* owned) {
 }
 
 int64_t gemm_out(TensorBuffer* a, TensorBuffer* b, bool ta, bool tb, int batch, int M, int N, int K, long sA, long sB,
-                 const size_t* oshape, int ond) {
+                 const size_t* oshape, int ond, const TensorBuffer* addend = nullptr) {
   TensorBuffer* c = alloc_tensor(F32, oshape, ond);
+  if (addend && (addend->dtype != F32 || addend->len != c->len))
+    fail("malus: matmul accumulate: addend %s does not match the product %s", shape_str(addend).c_str(), shape_str(c).c_str());
   KTimer* kt = ktimer_begin("gemm");
-  k::gemm(a->f32(), b->f32(), c->f32(), batch, M, N, K, ta, tb, sA, sB, (long)M * N, stream());
+  k::gemm(a->f32(), b->f32(), c->f32(), batch, M, N, K, ta, tb, sA, sB, (long)M * N, stream(),
+          addend ? addend->f32() : nullptr);
   ktimer_end(kt, 2.0 * batch * (double)M * N * K);
   return done(c, "matmul");
 }
@@ -586,14 +589,7 @@ int64_t malus_std_softmax_bwd(int64_t s, int64_t dout, int64_t axis) {
 // tape.rs:1162-1186 (per-row variance broadcast correctly; see layernorm.ml:71)
 int64_t malus_std_layernorm_bwd(int64_t y, int64_t var, int64_t dout, int64_t axis) {
   API_TRY
-  TensorBuffer *ty = T(y), *tv = T(var), *td = T(dout);
-  int ax = norm_axis(axis, ty->ndim);
-  size_t o, a, in;
-  split_axis(ty, ax, &o, &a, &in);
-  if (tv->len != o * in) fail("malus: layernorm VJP expects a keepdim variance of %zu elements, got %zu", o * in, tv->len);
-  TensorBuffer* out = alloc_like(ty);
-  k::layernorm_bwd(ty->f32(), tv->f32(), td->f32(), out->f32(), o, a, in, 1e-5f, stream());
-  return done(out, "layernorm_bwd");
+  return layernorm_bwd_impl(y, var, dout, axis, nullptr);
   API_CATCH(0)
 }
 int64_t malus_std_cross_entropy_bwd(int64_t probs, int64_t targets, int64_t dout) {
@@ -617,9 +613,13 @@ int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout) {
   API_CATCH(0)
 }
 
+}  // extern "C"
+
 // ---- matmul (metal.rs:820-962) and its VJPs (matmul_bwd.ml:15-29) ---------------------
-int64_t tensor_matmul(int64_t ha, int64_t hb) {
-  API_TRY
+// The *_impl forms take an optional addend D of the output's shape and
+// return D + product (one GEMM, the product rounded before the add), which
+// is how a gradient accumulation or residual add folds into the GEMM.
+int64_t matmul_impl(int64_t ha, int64_t hb, const TensorBuffer* D) {
   TensorBuffer *a = T(ha), *b = T(hb);
   need_f32(a, "matmul");
   need_f32(b, "matmul");
@@ -629,7 +629,7 @@ int64_t tensor_matmul(int64_t ha, int64_t hb) {
       fail("malus: matmul shape mismatch: [%zux%zu] @ [%zux%zu] - inner dims %zu != %zu\n  left shape:  %s\n  right shape: %s",
            m, k, k2, n, k, k2, shape_str(a).c_str(), shape_str(b).c_str());
     size_t osh[2] = {m, n};
-    return gemm_out(a, b, false, false, 1, (int)m, (int)n, (int)k, 0, 0, osh, 2);
+    return gemm_out(a, b, false, false, 1, (int)m, (int)n, (int)k, 0, 0, osh, 2, D);
   }
   if (a->ndim == 3 && b->ndim == 3) {
     size_t bt = a->shape[0], m = a->shape[1], k = a->shape[2], bt2 = b->shape[0], k2 = b->shape[1], n = b->shape[2];
@@ -640,7 +640,7 @@ int64_t tensor_matmul(int64_t ha, int64_t hb) {
       fail("malus: batched matmul inner dims must match: %zu vs %zu\n  left shape:  %s\n  right shape: %s", k, k2,
            shape_str(a).c_str(), shape_str(b).c_str());
     size_t osh[3] = {bt, m, n};
-    return gemm_out(a, b, false, false, (int)bt, (int)m, (int)n, (int)k, (long)(m * k), (long)(k * n), osh, 3);
+    return gemm_out(a, b, false, false, (int)bt, (int)m, (int)n, (int)k, (long)(m * k), (long)(k * n), osh, 3, D);
   }
   if (a->ndim == 3 && b->ndim == 2) {  // weight broadcast over the batch: one [B*M, K] GEMM
     size_t bt = a->shape[0], m = a->shape[1], k = a->shape[2], k2 = b->shape[0], n = b->shape[1];
@@ -648,38 +648,66 @@ int64_t tensor_matmul(int64_t ha, int64_t hb) {
       fail("malus: matmul shape mismatch: [%zux%zux%zu] @ [%zux%zu] - inner dims %zu != %zu\n  left shape:  %s\n  right shape: %s",
            bt, m, k, k2, n, k, k2, shape_str(a).c_str(), shape_str(b).c_str());
     size_t osh[3] = {bt, m, n};
-    return gemm_out(a, b, false, false, 1, (int)(bt * m), (int)n, (int)k, 0, 0, osh, 3);
+    return gemm_out(a, b, false, false, 1, (int)(bt * m), (int)n, (int)k, 0, 0, osh, 3, D);
   }
   fail("malus: tensor_matmul requires both inputs to be 2-D, both 3-D, or (3-D, 2-D)\n  left shape:  %s\n  right shape: %s",
        shape_str(a).c_str(), shape_str(b).c_str());
-  API_CATCH(0)
+}
+
+// transformer_bwd.ml:24-36 with the per-row variance (tape.rs:1162-1186);
+// with D, returns D + dx (gradient accumulation folded into the kernel).
+int64_t layernorm_bwd_impl(int64_t y, int64_t var, int64_t dout, int64_t axis, const TensorBuffer* D) {
+  TensorBuffer *ty = T(y), *tv = T(var), *td = T(dout);
+  int ax = norm_axis(axis, ty->ndim);
+  size_t o, a, in;
+  split_axis(ty, ax, &o, &a, &in);
+  if (tv->len != o * in) fail("malus: layernorm VJP expects a keepdim variance of %zu elements, got %zu", o * in, tv->len);
+  if (D && (D->dtype != F32 || D->len != ty->len))
+    fail("malus: layernorm VJP accumulate: addend %s does not match %s", shape_str(D).c_str(), shape_str(ty).c_str());
+  TensorBuffer* out = alloc_like(ty);
+  k::layernorm_bwd(ty->f32(), tv->f32(), td->f32(), out->f32(), o, a, in, 1e-5f, stream(), D ? D->f32() : nullptr);
+  return done(out, "layernorm_bwd");
 }
 
 // dA = dout @ op(B)^T
-int64_t malus_std_matmul_bwd_a(int64_t ha, int64_t hb, int64_t hd) {
-  API_TRY
+int64_t matmul_bwd_a_impl(int64_t ha, int64_t hb, int64_t hd, const TensorBuffer* D) {
   TensorBuffer *a = T(ha), *b = T(hb), *d = T(hd);
   if (b->ndim == 3) {  // 3x3: dout[b] @ B[b]^T
     size_t bt = d->shape[0], m = d->shape[1], n = d->shape[2], k = b->shape[1];
-    return gemm_out(d, b, false, true, (int)bt, (int)m, (int)k, (int)n, (long)(m * n), (long)(k * n), a->shape, a->ndim);
+    return gemm_out(d, b, false, true, (int)bt, (int)m, (int)k, (int)n, (long)(m * n), (long)(k * n), a->shape, a->ndim, D);
   }
   // b is 2-D [K, N]; dout is [.., N] flattened to rows
   size_t n = b->shape[1], k = b->shape[0], rows = d->len / n;
-  return gemm_out(d, b, false, true, 1, (int)rows, (int)k, (int)n, 0, 0, a->shape, a->ndim);
-  API_CATCH(0)
+  return gemm_out(d, b, false, true, 1, (int)rows, (int)k, (int)n, 0, 0, a->shape, a->ndim, D);
 }
 
 // dB = op(A)^T @ dout (the 3x2 case sums over the batch inside one GEMM)
-int64_t malus_std_matmul_bwd_b(int64_t ha, int64_t hb, int64_t hd) {
-  API_TRY
+int64_t matmul_bwd_b_impl(int64_t ha, int64_t hb, int64_t hd, const TensorBuffer* D) {
   TensorBuffer *a = T(ha), *b = T(hb), *d = T(hd);
   if (a->ndim == 3 && b->ndim == 3) {
     size_t bt = a->shape[0], m = a->shape[1], k = a->shape[2], n = d->shape[2];
-    return gemm_out(a, d, true, false, (int)bt, (int)k, (int)n, (int)m, (long)(m * k), (long)(m * n), b->shape, b->ndim);
+    return gemm_out(a, d, true, false, (int)bt, (int)k, (int)n, (int)m, (long)(m * k), (long)(m * n), b->shape, b->ndim, D);
   }
   // A flattened to [rows, K] (2-D, or 3-D with B broadcast): A^T @ dout[rows, N]
   size_t k = a->shape[a->ndim - 1], rows = a->len / k, n = d->shape[d->ndim - 1];
-  return gemm_out(a, d, true, false, 1, (int)k, (int)n, (int)rows, 0, 0, b->shape, b->ndim);
+  return gemm_out(a, d, true, false, 1, (int)k, (int)n, (int)rows, 0, 0, b->shape, b->ndim, D);
+}
+
+extern "C" {
+
+int64_t tensor_matmul(int64_t ha, int64_t hb) {
+  API_TRY
+  return matmul_impl(ha, hb, nullptr);
+  API_CATCH(0)
+}
+int64_t malus_std_matmul_bwd_a(int64_t ha, int64_t hb, int64_t hd) {
+  API_TRY
+  return matmul_bwd_a_impl(ha, hb, hd, nullptr);
+  API_CATCH(0)
+}
+int64_t malus_std_matmul_bwd_b(int64_t ha, int64_t hb, int64_t hd) {
+  API_TRY
+  return matmul_bwd_b_impl(ha, hb, hd, nullptr);
   API_CATCH(0)
 }
 

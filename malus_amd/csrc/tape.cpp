@@ -73,6 +73,32 @@ using FnPerm = int64_t (*)(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
 
 int64_t grad_acc(int64_t old_g, int64_t new_g) { return slot_fn<Fn2>(GradAcc)(old_g, new_g); }
 
+thread_local bool t_fuse_vjps = true;  // fold GradAcc into matmul / layernorm VJP kernels
+
+template <class F>
+bool slot_is(int32_t s, F fn) { return t_fuse_vjps && slot(s) == reinterpret_cast<size_t>(fn); }
+
+// Matmul VJP folded into the gradient accumulation: with the library's own
+// MatmulBwd and GradAcc slots, grads[x] = old + dX comes out of one GEMM
+// whose epilogue adds `old` (the product is rounded first, exactly as the
+// GradAcc add of a separate result would round).  Accumulation order is the
+// reference's: dA into grads[a], then dB into grads[b].
+void accumulate_matmul(std::unordered_map<int64_t, int64_t>& grads, int64_t a, int64_t b, int64_t dout) {
+  auto fold = [&](int64_t x, bool is_a) {
+    auto it = grads.find(x);
+    const TensorBuffer* old = it == grads.end() ? nullptr : T(it->second);
+    int64_t g = is_a ? matmul_bwd_a_impl(a, b, dout, old) : matmul_bwd_b_impl(a, b, dout, old);
+    if (it == grads.end()) {
+      grads.emplace(x, g);
+    } else {
+      release(T(it->second));
+      it->second = g;
+    }
+  };
+  fold(a, true);
+  fold(b, false);
+}
+
 // tape.rs:815-828: take ownership of new_grad, fold it into grads[input].
 void accumulate(std::unordered_map<int64_t, int64_t>& grads, int64_t input, int64_t new_grad) {
   auto it = grads.find(input);
@@ -183,6 +209,11 @@ void register_default_backward_fns() { ensure_slots(); }
 using namespace malus;
 
 extern "C" {
+
+// 1 (default): fold gradient accumulation into the matmul and layernorm VJP
+// kernels when the library's own slots are registered; 0: separate GradAcc
+// adds.  Values are the same either way (testing and comparison knob).
+void malus_tape_set_fused_vjps(int on) { t_fuse_vjps = on != 0; }
 
 void tape_register_backward_fn(int32_t s, size_t fnptr) {
   API_TRY
@@ -319,6 +350,11 @@ void backward(int64_t loss) {
     switch (n.op) {
       case Matmul: {
         int64_t a = n.saved[0], b = n.saved[1];
+        if (slot_is(MatmulBwdA, &malus_std_matmul_bwd_a) && slot_is(MatmulBwdB, &malus_std_matmul_bwd_b) &&
+            slot_is(GradAcc, &malus_std_broadcast_add_fwd)) {
+          accumulate_matmul(grads, a, b, dout);
+          break;
+        }
         int64_t da = slot_fn<Fn3>(MatmulBwdA)(a, b, dout);
         int64_t db = slot_fn<Fn3>(MatmulBwdB)(a, b, dout);
         accumulate(grads, a, da);
@@ -375,6 +411,19 @@ void backward(int64_t loss) {
       case ReduceVarAxis: accumulate(grads, n.saved[0], slot_fn<Fn3>(ReduceVarAxisBwd)(n.saved[0], dout, n.meta[0])); break;
       case Softmax: accumulate(grads, n.saved[0], slot_fn<Fn3>(SoftmaxBwd)(n.output, dout, n.meta[0])); break;
       case Layernorm:
+        if (slot_is(LayernormBwd, &malus_std_layernorm_bwd) && slot_is(GradAcc, &malus_std_broadcast_add_fwd)) {
+          // grads[x] = old + dx from one kernel (same rounding as GradAcc)
+          auto it = grads.find(n.saved[0]);
+          const TensorBuffer* old = it == grads.end() ? nullptr : T(it->second);
+          int64_t g = layernorm_bwd_impl(n.output, n.saved[1], dout, n.meta[0], old);
+          if (it == grads.end()) {
+            grads.emplace(n.saved[0], g);
+          } else {
+            release(T(it->second));
+            it->second = g;
+          }
+          break;
+        }
         accumulate(grads, n.saved[0], slot_fn<Fn4>(LayernormBwd)(n.output, n.saved[1], dout, n.meta[0]));
         break;
       case Gelu: accumulate(grads, n.saved[0], slot_fn<Fn2>(GeluBwd)(n.saved[0], dout)); break;

@@ -51,7 +51,7 @@ def test_xor_10000_steps_vs_oracle(rt):
 
 
 class GpuGpt:
-    def __init__(self, rt, cfg, rng_call_idx=0, fused=True, fused_attention=True):
+    def __init__(self, rt, cfg, rng_call_idx=0, fused=True, fused_forward=True):
         self.rt = rt
         self.cfg = cfg
         rt.L.tape_reset()
@@ -59,7 +59,7 @@ class GpuGpt:
         self.g = rt.L.malus_gpt_create(cfg["V"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["B"], OPT["lr"],
                                        OPT["b1"], OPT["b2"], OPT["eps"], OPT["wd"])
         rt.L.malus_gpt_set_fused_optimizer(self.g, int(fused))
-        rt.L.malus_gpt_set_fused_attention(self.g, int(fused_attention))
+        rt.L.malus_gpt_set_fused_forward(self.g, int(fused_forward))
 
     def close(self):
         self.rt.L.malus_gpt_free(self.g)
@@ -143,15 +143,18 @@ def test_gpt_fused_optimizer_equals_op_by_op(rt):
         np.testing.assert_array_equal(u, v, err_msg=f"param {i}")
 
 
-def test_gpt_fused_attention_equals_three_ops(rt):
-    """scale + mask + softmax as one kernel (shape-only intermediates on the
-    tape) gives the same loss, gradients and updated parameters as the three
-    separate ops, bit for bit."""
+def test_gpt_fusions_equal_separate_ops(rt):
+    """The forward fusions (scale + mask + softmax in one kernel, residual adds
+    in GEMM epilogues, shape-only intermediates on the tape) and the VJP
+    fusions (gradient accumulation inside the matmul / layernorm VJP kernels)
+    give the same loss, gradients and updated parameters as the separate
+    ops, bit for bit."""
     cfg = dict(V=65, T=64, C=64, H=4, L=2, B=4)
     x, y = tokens(cfg, 6000)
     out = []
     for fa in (True, False):
-        g = GpuGpt(rt, cfg, fused_attention=fa)
+        rt.L.malus_tape_set_fused_vjps(int(fa))
+        g = GpuGpt(rt, cfg, fused_forward=fa)
         try:
             loss = g.loss_and_grads(x, y)
             grads = [g.grad(i) for i in range(8 * cfg["L"] + 4)]
@@ -159,6 +162,7 @@ def test_gpt_fused_attention_equals_three_ops(rt):
             params = [g.param(i) for i in range(8 * cfg["L"] + 4)]
         finally:
             g.close()
+            rt.L.malus_tape_set_fused_vjps(1)
         out.append((loss, grads, l2, params))
     (la, ga, sa, pa), (lb, gb, sb, pb) = out
     assert la == lb and sa == sb
