@@ -83,6 +83,96 @@ def copy_calibration(rt, sizes):
     log("copy calibration: 3 x k_binary_scalar<MUL> over 2^26 f32 (268435456 B read + 268435456 B written each)")
 
 
+def kernel_suite(rt, M, reps: int):
+    """C2 (elementwise, 2^26 f32) and C3 (row ops on [65536, 1024]) kernels
+    through the C ABI, each timed over `reps` launches between device
+    flushes; bandwidth = algorithmic bytes / time (
+    configs[2]).  Returns a list of rows; prints a table to stderr."""
+    import numpy as np
+
+    L = rt.L
+    rng = np.random.default_rng(99)
+    rows = []
+
+    def timed(name, bytes_per_call, fn, shape):
+        for _ in range(3):
+            L.tensor_free(fn())
+        L.gpu_barrier()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            L.tensor_free(fn())
+        L.gpu_barrier()
+        dt = (time.perf_counter() - t0) / reps
+        gbs = bytes_per_call / dt / 1e9
+        rows.append({"op": name, "shape": shape, "us": round(dt * 1e6, 1), "GB/s": round(gbs, 1),
+                     "frac_hbm": round(gbs / PEAK_HBM_GBS, 3), "bytes": int(bytes_per_call)})
+        log(f"  {name:28s} {shape:14s} {dt * 1e6:8.1f} us  {gbs:7.1f} GB/s  {gbs / PEAK_HBM_GBS:5.1%} of HBM")
+
+    # C2: z = a*b + 0.5*c - relu(a); r = A + bias, and the VJPs
+    n = 1 << 26
+    R, Cc = 8192, 8192
+    a, b, c = (rt.tensor(rng.uniform(-1, 1, (R, Cc)).astype(np.float32)) for _ in range(3))
+    bias = rt.tensor(rng.uniform(-1, 1, (1, Cc)).astype(np.float32))
+    dz = L.tensor_alloc_ones_gpu(M.sizes((R, Cc)), 2)
+    t1 = L.malus_std_broadcast_fwd(M.MUL, a, b)
+    t2 = L.malus_std_scalar_op(M.MUL, c, 0.5, 0)
+    t3 = L.malus_std_broadcast_fwd(M.ADD, t1, t2)
+    t4 = L.malus_std_unary(M.RELU, a)
+    log("C2 elementwise, [8192, 8192] f32:")
+    timed("a * b", 12 * n, lambda: L.malus_std_broadcast_fwd(M.MUL, a, b), "8192x8192")
+    timed("0.5 * c (scalar)", 8 * n, lambda: L.malus_std_scalar_op(M.MUL, c, 0.5, 0), "8192x8192")
+    timed("t1 + t2", 12 * n, lambda: L.malus_std_broadcast_fwd(M.ADD, t1, t2), "8192x8192")
+    timed("relu(a)", 8 * n, lambda: L.malus_std_unary(M.RELU, a), "8192x8192")
+    timed("t3 - t4", 12 * n, lambda: L.malus_std_broadcast_fwd(M.SUB, t3, t4), "8192x8192")
+    timed("A + bias (row broadcast)", 8 * n + 4 * Cc, lambda: L.malus_std_broadcast_fwd(M.ADD, a, bias), "8192x8192")
+    timed("relu VJP", 12 * n, lambda: L.malus_std_relu_bwd(a, dz), "8192x8192")
+    timed("mul VJP (dz * b)", 12 * n, lambda: L.malus_std_mul_bwd_a(dz, a, b), "8192x8192")
+    timed("neg VJP (-dz)", 8 * n, lambda: L.malus_std_scale_fwd(dz, -1.0), "8192x8192")
+    timed("bias VJP (sum over rows)", 4 * n + 4 * Cc, lambda: L.malus_std_sum_to_shape_bwd(dz, bias), "8192x8192")
+    rt.free(a, b, c, bias, dz, t1, t2, t3, t4)
+
+    # C3: row ops on [65536, 1024]
+    Rr, V = 65536, 1024
+    n = Rr * V
+    x = rt.tensor(rng.standard_normal((Rr, V)).astype(np.float32))
+    dout = rt.tensor(rng.standard_normal((Rr, V)).astype(np.float32))
+    logits = rt.tensor((2.0 * rng.standard_normal((Rr, V))).astype(np.float32))
+    tg = rt.tensor(rng.integers(0, V, Rr).astype(np.int32))
+    sm = L.malus_std_softmax_fwd(x, 1)
+    var = C.c_int64()
+    ln = L.malus_std_layernorm_fwd(x, 1, C.byref(var))
+    probs = C.c_int64()
+    loss = L.malus_std_cross_entropy_fwd(logits, tg, C.byref(probs))
+    one = L.tensor_alloc_ones_gpu(M.sizes((1,)), 1)
+    log("C3 row ops, [65536, 1024] f32:")
+    timed("softmax", 8 * n, lambda: L.malus_std_softmax_fwd(x, 1), "65536x1024")
+    timed("softmax VJP", 12 * n, lambda: L.malus_std_softmax_bwd(sm, dout, 1), "65536x1024")
+
+    def ln_fwd():
+        v = C.c_int64()
+        y = L.malus_std_layernorm_fwd(x, 1, C.byref(v))
+        L.tensor_free(v.value)
+        return y
+
+    timed("layernorm", 8 * n + 4 * Rr, ln_fwd, "65536x1024")
+    timed("layernorm VJP", 12 * n + 4 * Rr, lambda: L.malus_std_layernorm_bwd(ln, var.value, dout, 1), "65536x1024")
+    timed("gelu", 8 * n, lambda: L.malus_std_gelu_fwd(x), "65536x1024")
+    timed("gelu VJP", 12 * n, lambda: L.malus_std_gelu_bwd(x, dout), "65536x1024")
+
+    def ce_fwd():
+        p = C.c_int64()
+        l = L.malus_std_cross_entropy_fwd(logits, tg, C.byref(p))
+        L.tensor_free(p.value)
+        return l
+
+    timed("cross_entropy", 8 * n + 8 * Rr, ce_fwd, "65536x1024")
+    timed("cross_entropy VJP", 8 * n + 4 * Rr, lambda: L.malus_std_cross_entropy_bwd(probs.value, tg, one), "65536x1024")
+    timed("sum axis 1", 4 * n + 4 * Rr, lambda: L.malus_std_reduce_fwd(M.R_SUM, x, 1, 0), "65536x1024")
+    timed("sum axis 0", 4 * n + 4 * V, lambda: L.malus_std_reduce_fwd(M.R_SUM, x, 0, 0), "65536x1024")
+    rt.free(x, dout, logits, tg, sm, var.value, ln, probs.value, loss, one)
+    return rows
+
+
 def cpu_baseline(sample_batch: int, threads: int):
     """The oracle (plain-C restatement of the reference CPU path) on a
     bounded sample: one full step at batch `sample_batch`, scaled to the
@@ -115,6 +205,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB copy (counter calibration for the traffic figure)")
+    ap.add_argument("--suite", choices=["kernels"],
+                    help="kernels: the C2/C3 elementwise and row-op kernels' HBM bandwidth (one JSON line)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
@@ -129,6 +221,10 @@ def main():
     L = rt.L
     if a.copy_calibration:
         copy_calibration(rt, M.sizes)
+        return
+    if a.suite == "kernels":
+        rows = kernel_suite(rt, M, reps=10)
+        print(json.dumps({"suite": "kernels", "unit": "GB/s", "peak_hbm_GBs": PEAK_HBM_GBS, "rows": rows}), flush=True)
         return
     name = C.create_string_buffer(64)
     cus, clk = C.c_int(), C.c_int()

@@ -21,6 +21,19 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr int R_PROD = 4;
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// 128-bit loads; non-temporal when the operands exceed the 256 MB
+// last-level cache (a streamed reduction input is read once), cached
+// otherwise (the training step's operands are re-read by later kernels).
+__device__ __forceinline__ float4 ld(const float4* p, bool nt) {
+  if (nt) {
+    const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+  }
+  return *p;
+}
+constexpr size_t kStreamBytes = 256ull << 20;
 
 template <int OP>
 __device__ __forceinline__ float rinit() { return OP == R_MAX ? -INFINITY : 0.0f; }
@@ -55,7 +68,7 @@ __device__ __forceinline__ float rfinal(float s, uint32_t count) {
 template <int OP, bool VEC>
 __global__ __launch_bounds__(256) void k_row_wave(const float* __restrict__ x, const float* __restrict__ y,
                                                   const float* __restrict__ mean, float* __restrict__ out, size_t rows,
-                                                  uint32_t axis, uint32_t count, bool finalize) {
+                                                  uint32_t axis, uint32_t count, bool finalize, bool nt) {
   const size_t row = (size_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
@@ -68,8 +81,8 @@ __global__ __launch_bounds__(256) void k_row_wave(const float* __restrict__ x, c
     const float4* y4 = reinterpret_cast<const float4*>(yr);
     const uint32_t n4 = axis / 4;
     for (uint32_t i = lane; i < n4; i += kWave) {
-      const float4 v = x4[i];
-      const float4 w = OP == R_PROD ? y4[i] : v;
+      const float4 v = ld(x4 + i, nt);
+      const float4 w = OP == R_PROD ? ld(y4 + i, nt) : v;
       acc = rcomb<OP>(acc, rload<OP>(v.x, w.x, mu));
       acc = rcomb<OP>(acc, rload<OP>(v.y, w.y, mu));
       acc = rcomb<OP>(acc, rload<OP>(v.z, w.z, mu));
@@ -87,7 +100,7 @@ __global__ __launch_bounds__(256) void k_row_wave(const float* __restrict__ x, c
 template <int OP>
 __global__ __launch_bounds__(256) void k_row_split(const float* __restrict__ x, const float* __restrict__ y,
                                                    const float* __restrict__ mean, float* __restrict__ partial,
-                                                   size_t axis, uint32_t nsplit, size_t chunk) {
+                                                   size_t axis, uint32_t nsplit, size_t chunk, bool nt) {
   __shared__ float red[256 / kWave];
   const size_t bid = blockIdx.x;
   const size_t row = bid / nsplit;
@@ -102,8 +115,8 @@ __global__ __launch_bounds__(256) void k_row_split(const float* __restrict__ x, 
     const float4* x4 = reinterpret_cast<const float4*>(xr);
     const float4* y4 = reinterpret_cast<const float4*>(yr);
     for (size_t i = beg / 4 + threadIdx.x; i < end / 4; i += blockDim.x) {
-      const float4 v = x4[i];
-      const float4 w = OP == R_PROD ? y4[i] : v;
+      const float4 v = ld(x4 + i, nt);
+      const float4 w = OP == R_PROD ? ld(y4 + i, nt) : v;
       acc = rcomb<OP>(acc, rload<OP>(v.x, w.x, mu));
       acc = rcomb<OP>(acc, rload<OP>(v.y, w.y, mu));
       acc = rcomb<OP>(acc, rload<OP>(v.z, w.z, mu));
@@ -132,7 +145,7 @@ __global__ __launch_bounds__(256) void k_row_split(const float* __restrict__ x, 
 template <int OP, int CT>
 __global__ __launch_bounds__(256) void k_col4(const float* __restrict__ x, const float* __restrict__ y,
                                               const float* __restrict__ mean, float* __restrict__ dst, size_t axis,
-                                              size_t inner, uint32_t nsplit, size_t chunk, bool finalize) {
+                                              size_t inner, uint32_t nsplit, size_t chunk, bool finalize, bool nt) {
   constexpr int RT = 256 / CT;
   __shared__ float4 red[RT][CT];
   const int ct = threadIdx.x % CT, rt = threadIdx.x / CT;
@@ -149,8 +162,8 @@ __global__ __launch_bounds__(256) void k_col4(const float* __restrict__ x, const
     const float4* yp = OP == R_PROD ? reinterpret_cast<const float4*>(y + o * axis * inner) + i4 : nullptr;
     const size_t stride4 = inner / 4;
     for (size_t a = beg + rt; a < end; a += RT) {
-      const float4 v = xp[a * stride4];
-      const float4 w = OP == R_PROD ? yp[a * stride4] : v;
+      const float4 v = ld(xp + a * stride4, nt);
+      const float4 w = OP == R_PROD ? ld(yp + a * stride4, nt) : v;
       acc.x = rcomb<OP>(acc.x, rload<OP>(v.x, w.x, mu.x));
       acc.y = rcomb<OP>(acc.y, rload<OP>(v.y, w.y, mu.y));
       acc.z = rcomb<OP>(acc.z, rload<OP>(v.z, w.z, mu.z));
@@ -252,12 +265,12 @@ constexpr int combine_op() { return OP == R_MAX ? R_MAX : OP == R_PROD ? R_SUM :
 
 template <int OP>
 void launch_col4(int ct, dim3 grid, const float* x, const float* y, const float* mean, float* dst, size_t axis,
-                 size_t inner, uint32_t nsplit, size_t chunk, bool finalize, hipStream_t s) {
+                 size_t inner, uint32_t nsplit, size_t chunk, bool finalize, bool nt, hipStream_t s) {
   switch (ct) {
-    case 8: k_col4<OP, 8><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize); break;
-    case 16: k_col4<OP, 16><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize); break;
-    case 32: k_col4<OP, 32><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize); break;
-    default: k_col4<OP, 64><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize); break;
+    case 8: k_col4<OP, 8><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize, nt); break;
+    case 16: k_col4<OP, 16><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize, nt); break;
+    case 32: k_col4<OP, 32><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize, nt); break;
+    default: k_col4<OP, 64><<<grid, 256, 0, s>>>(x, y, mean, dst, axis, inner, nsplit, chunk, finalize, nt); break;
   }
 }
 
@@ -266,6 +279,7 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
                  hipStream_t s) {
   constexpr int COMB = combine_op<OP>();
   const size_t n_out = outer * inner;
+  const bool nt = outer * axis * inner * sizeof(float) * (OP == R_PROD ? 2 : 1) >= kStreamBytes;
   if (n_out == 0) return;
   if (axis == 0) {  // empty reduction: sum/mean identities (mean/var of nothing -> NaN like 0/0)
     if (OP == R_MAX) fill(out, -INFINITY, n_out, s);
@@ -284,11 +298,11 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
       nsplit = (uint32_t)((axis + chunk - 1) / chunk);
       size_t bucket;
       float* partial = static_cast<float*>(pool_alloc(rows * nsplit * sizeof(float), &bucket));
-      k_row_split<OP><<<(unsigned)(rows * nsplit), 256, 0, s>>>(x, y, mean, partial, axis, nsplit, chunk);
+      k_row_split<OP><<<(unsigned)(rows * nsplit), 256, 0, s>>>(x, y, mean, partial, axis, nsplit, chunk, nt);
       MALUS_HIP(hipGetLastError());
       // combine partials of each row with one wave per row, then finalize
       k_row_wave<COMB == R_MAX ? R_MAX : R_SUM, false>
-          <<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, rows, nsplit, nsplit, false);
+          <<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, rows, nsplit, nsplit, false, false);
       MALUS_HIP(hipGetLastError());
       if (OP == R_MEAN || OP == R_VAR) {
         // divide in place by the axis length
@@ -299,8 +313,8 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
     }
     const bool vec = (axis % 4) == 0;
     unsigned grid = (unsigned)((rows + 3) / 4);
-    if (vec) k_row_wave<OP, true><<<grid, 256, 0, s>>>(x, y, mean, out, rows, (uint32_t)axis, (uint32_t)axis, true);
-    else k_row_wave<OP, false><<<grid, 256, 0, s>>>(x, y, mean, out, rows, (uint32_t)axis, (uint32_t)axis, true);
+    if (vec) k_row_wave<OP, true><<<grid, 256, 0, s>>>(x, y, mean, out, rows, (uint32_t)axis, (uint32_t)axis, true, nt);
+    else k_row_wave<OP, false><<<grid, 256, 0, s>>>(x, y, mean, out, rows, (uint32_t)axis, (uint32_t)axis, true, nt);
     MALUS_HIP(hipGetLastError());
     return;
   }
@@ -338,7 +352,7 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
   if (nsplit > 1) dst = static_cast<float*>(pool_alloc(outer * nsplit * inner * sizeof(float), &bucket));
   if (vec) {
     launch_col4<OP>(ct, dim3((unsigned)col_blocks, nsplit, (unsigned)outer), x, y, mean, dst, axis, inner, nsplit, chunk,
-                    nsplit == 1, s);
+                    nsplit == 1, nt, s);
   } else {
     k_col<OP><<<(unsigned)(base_blocks * nsplit), 256, 0, s>>>(x, y, mean, dst, outer, axis, inner, nsplit, chunk,
                                                                 (uint32_t)col_blocks, nsplit == 1);

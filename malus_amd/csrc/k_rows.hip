@@ -12,6 +12,7 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr int kRowsPerBlock = 4;  // 256 threads
+typedef float v4f __attribute__((ext_vector_type(4)));  // non-temporal 128-bit row access
 
 __device__ __forceinline__ float wsum(float v) {
 #pragma unroll
@@ -25,10 +26,13 @@ __device__ __forceinline__ float wmax(float v) {
 }
 
 // Register tile of one row: NV float4 chunks per lane.  Element e of the
-// lane's tile is column col(e).  VEC: chunk j covers columns 4*(lane+64j)..+3;
+// lane's tile is column col(e).  VM: 0 scalar, 1 float4, 2 float4 with
+// non-temporal loads (for operands too large to stay in the 256 MB
+// last-level cache between kernels).  VEC: chunk j covers columns 4*(lane+64j)..+3;
 // scalar: element e is column lane + 64*e.
-template <int NV, bool VEC>
+template <int NV, int VM>
 struct RowTile {
+  static constexpr bool VEC = VM > 0, NT = VM == 2;
   float v[NV * 4];
   __device__ __forceinline__ static uint32_t col(int e, int lane) {
     return VEC ? 4u * (uint32_t)(lane + kWave * (e / 4)) + (uint32_t)(e % 4) : (uint32_t)(lane + kWave * e);
@@ -39,7 +43,8 @@ struct RowTile {
       for (int j = 0; j < NV; ++j) {
         uint32_t c4 = (uint32_t)(lane + kWave * j);
         if (4 * c4 < axis) {
-          float4 t = reinterpret_cast<const float4*>(row)[c4];
+          const v4f t = NT ? __builtin_nontemporal_load(reinterpret_cast<const v4f*>(row) + c4)
+                           : reinterpret_cast<const v4f*>(row)[c4];
           v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
         } else {
           v[4 * j] = v[4 * j + 1] = v[4 * j + 2] = v[4 * j + 3] = pad;
@@ -58,6 +63,7 @@ struct RowTile {
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
         uint32_t c4 = (uint32_t)(lane + kWave * j);
+        // ordinary store: the next op (often a GEMM) reads this row back from cache
         if (4 * c4 < axis) reinterpret_cast<float4*>(row)[c4] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
       }
     } else {
@@ -72,13 +78,13 @@ struct RowTile {
 };
 
 // softmax_axis_cpu (metal.rs:1439-1467): m = max, e = exp(x - m), s = sum e, y = e / s
-template <int NV, bool VEC>
+template <int NV, int VM>
 __global__ __launch_bounds__(256) void k_softmax_rows(const float* __restrict__ x, float* __restrict__ y, size_t rows,
                                                       uint32_t axis) {
   const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
-  RowTile<NV, VEC> t;
+  RowTile<NV, VM> t;
   t.load(x + row * axis, axis, lane, -INFINITY);
   float m = -INFINITY;
 #pragma unroll
@@ -101,7 +107,7 @@ __global__ __launch_bounds__(256) void k_softmax_rows(const float* __restrict__ 
 // the row, fusing nanogpt_modular.ml's `scores * scale`, `+ mask` and
 // softmax.  Each op rounds like its own kernel (the product, then the sum,
 // then softmax_axis_cpu), so y equals the three-kernel result bit for bit.
-template <int NV, bool VEC>
+template <int NV, int VM>
 __global__ __launch_bounds__(256) void k_scale_mask_softmax_rows(const float* __restrict__ x, const float* __restrict__ scale,
                                                                  const float* __restrict__ mask, float* __restrict__ y,
                                                                  size_t rows, uint32_t axis, uint32_t mask_rows) {
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(256) void k_scale_mask_softmax_rows(const float* __
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
   const float sc = scale[0];
-  RowTile<NV, VEC> t, mk;
+  RowTile<NV, VM> t, mk;
   t.load(x + row * axis, axis, lane, 0.0f);
   mk.load(mask + (row % mask_rows) * axis, axis, lane, 0.0f);
 #pragma unroll
@@ -135,13 +141,13 @@ __global__ __launch_bounds__(256) void k_scale_mask_softmax_rows(const float* __
 }
 
 // tape.rs:1150-1161: dx = s * (dout - sum(dout * s))
-template <int NV, bool VEC>
+template <int NV, int VM>
 __global__ __launch_bounds__(256) void k_softmax_bwd_rows(const float* __restrict__ y, const float* __restrict__ dout,
                                                           float* __restrict__ dx, size_t rows, uint32_t axis) {
   const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
-  RowTile<NV, VEC> s, d;
+  RowTile<NV, VM> s, d;
   s.load(y + row * axis, axis, lane, 0.0f);
   d.load(dout + row * axis, axis, lane, 0.0f);
   float acc = 0.0f;
@@ -154,13 +160,13 @@ __global__ __launch_bounds__(256) void k_softmax_bwd_rows(const float* __restric
 }
 
 // tensor_layernorm_axis (metal.rs:1486-1533): y = (x - mu) / sqrt(var + eps)
-template <int NV, bool VEC>
+template <int NV, int VM>
 __global__ __launch_bounds__(256) void k_layernorm_rows(const float* __restrict__ x, float* __restrict__ y,
                                                         float* __restrict__ var, size_t rows, uint32_t axis, float eps) {
   const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
-  RowTile<NV, VEC> t;
+  RowTile<NV, VM> t;
   t.load(x + row * axis, axis, lane, 0.0f);
   float s = 0.0f;
 #pragma unroll
@@ -182,7 +188,7 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(const float* __restrict_
 }
 
 // tape.rs:1162-1186: dx = ((dy - mean(dy)) - y * mean(dy*y)) * (1 / sqrt(var + eps))
-template <int NV, bool VEC>
+template <int NV, int VM>
 __global__ __launch_bounds__(256) void k_layernorm_bwd_rows(const float* __restrict__ y, const float* __restrict__ var,
                                                             const float* __restrict__ dout, float* __restrict__ dx,
                                                             size_t rows, uint32_t axis, float eps,
@@ -190,7 +196,7 @@ __global__ __launch_bounds__(256) void k_layernorm_bwd_rows(const float* __restr
   const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
-  RowTile<NV, VEC> yt, dt;
+  RowTile<NV, VM> yt, dt;
   yt.load(y + row * axis, axis, lane, 0.0f);
   dt.load(dout + row * axis, axis, lane, 0.0f);
   float s1 = 0.0f, s2 = 0.0f;
@@ -218,14 +224,14 @@ __global__ __launch_bounds__(256) void k_layernorm_bwd_rows(const float* __restr
 
 // cross_entropy.ml:18-28 / metal.rs:1555-1598: probs = softmax(logits, 1),
 // nll[i] = -log(probs[i, t_i]) read back from the rounded probability.
-template <int NV, bool VEC>
+template <int NV, int VM>
 __global__ __launch_bounds__(256) void k_ce_fwd_rows(const float* __restrict__ logits, const int32_t* __restrict__ tgt,
                                                      float* __restrict__ probs, float* __restrict__ nll, size_t rows,
                                                      uint32_t axis, int32_t* __restrict__ err) {
   const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
-  RowTile<NV, VEC> t;
+  RowTile<NV, VM> t;
   t.load(logits + row * axis, axis, lane, -INFINITY);
   float m = -INFINITY;
 #pragma unroll
@@ -264,6 +270,26 @@ __global__ __launch_bounds__(256) void k_ce_bwd(const float* __restrict__ probs,
     float g = probs[f];
     if ((int32_t)j == tgt[i]) g = g - 1.0f;
     dx[f] = g * scale;
+  }
+}
+
+// Same expression, four consecutive columns of one row per thread (v % 4 == 0,
+// fewer than 2^32 elements): 32-bit index math, non-temporal streaming.
+__global__ __launch_bounds__(256) void k_ce_bwd4(const float* __restrict__ probs, const int32_t* __restrict__ tgt,
+                                                 const float* __restrict__ dout, float scale_host, float* __restrict__ dx,
+                                                 uint32_t n, uint32_t v, uint32_t total4) {
+  const float scale = dout ? dout[0] / (float)n : scale_host;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t f4 = blockIdx.x * blockDim.x + threadIdx.x; f4 < total4; f4 += stride) {
+    const uint32_t f = 4 * f4, i = f / v, j = f - i * v;
+    const int32_t t = tgt[i];
+    const v4f p = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(probs) + f4);
+    float g0 = p.x, g1 = p.y, g2 = p.z, g3 = p.w;
+    if ((int32_t)j == t) g0 = g0 - 1.0f;
+    if ((int32_t)(j + 1) == t) g1 = g1 - 1.0f;
+    if ((int32_t)(j + 2) == t) g2 = g2 - 1.0f;
+    if ((int32_t)(j + 3) == t) g3 = g3 - 1.0f;
+    __builtin_nontemporal_store(v4f{g0 * scale, g1 * scale, g2 * scale, g3 * scale}, reinterpret_cast<v4f*>(dx) + f4);
   }
 }
 
@@ -351,15 +377,23 @@ __global__ void k_ce_fwd_seq(const float* __restrict__ logits, const int32_t* __
 }
 
 // Launch helper: choose the register-tile width for a row length.
-template <template <int, bool> class KSel, class Launch>
-void row_dispatch(uint32_t axis, Launch launch) {
+// Stream with non-temporal loads when an op's operands exceed the 256 MB
+// last-level cache (measured: ~+15 % on [65536, 1024] rows; on the training
+// step's <= 100 MB operands cached loads are faster).
+constexpr size_t kStreamBytes = 256ull << 20;
+
+template <template <int, int> class KSel, class Launch>
+void row_dispatch(uint32_t axis, Launch launch, size_t bytes = 0) {
   const bool vec = (axis % 4) == 0;
+  const bool nt = bytes >= kStreamBytes;
   // elements per lane needed: ceil(axis / 64)
   uint32_t per_lane = (axis + 63) / 64;
   int nv = per_lane <= 4 ? 1 : per_lane <= 8 ? 2 : per_lane <= 16 ? 4 : per_lane <= 32 ? 8 : 16;
 #define MALUS_ROW_CASE(NV)                                       \
   case NV:                                                       \
-    if (vec) launch(KSel<NV, true>{}); else launch(KSel<NV, false>{}); \
+    if (vec && nt) launch(KSel<NV, 2>{});                             \
+    else if (vec) launch(KSel<NV, 1>{});                             \
+    else launch(KSel<NV, 0>{});                                      \
     break;
   switch (nv) {
     MALUS_ROW_CASE(1)
@@ -371,12 +405,12 @@ void row_dispatch(uint32_t axis, Launch launch) {
 #undef MALUS_ROW_CASE
 }
 
-template <int NV, bool VEC> struct SelSoftmax { static constexpr auto fn = k_softmax_rows<NV, VEC>; };
-template <int NV, bool VEC> struct SelSoftmaxBwd { static constexpr auto fn = k_softmax_bwd_rows<NV, VEC>; };
-template <int NV, bool VEC> struct SelScaleMaskSoftmax { static constexpr auto fn = k_scale_mask_softmax_rows<NV, VEC>; };
-template <int NV, bool VEC> struct SelLN { static constexpr auto fn = k_layernorm_rows<NV, VEC>; };
-template <int NV, bool VEC> struct SelLNBwd { static constexpr auto fn = k_layernorm_bwd_rows<NV, VEC>; };
-template <int NV, bool VEC> struct SelCE { static constexpr auto fn = k_ce_fwd_rows<NV, VEC>; };
+template <int NV, int VM> struct SelSoftmax { static constexpr auto fn = k_softmax_rows<NV, VM>; };
+template <int NV, int VM> struct SelSoftmaxBwd { static constexpr auto fn = k_softmax_bwd_rows<NV, VM>; };
+template <int NV, int VM> struct SelScaleMaskSoftmax { static constexpr auto fn = k_scale_mask_softmax_rows<NV, VM>; };
+template <int NV, int VM> struct SelLN { static constexpr auto fn = k_layernorm_rows<NV, VM>; };
+template <int NV, int VM> struct SelLNBwd { static constexpr auto fn = k_layernorm_bwd_rows<NV, VM>; };
+template <int NV, int VM> struct SelCE { static constexpr auto fn = k_ce_fwd_rows<NV, VM>; };
 
 constexpr uint32_t kMaxRowAxis = 4096;
 inline unsigned row_grid(size_t rows) { return (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock); }
@@ -389,7 +423,7 @@ void softmax(const float* x, float* out, size_t outer, size_t axis, size_t inner
   if (inner == 1 && axis <= kMaxRowAxis) {
     row_dispatch<SelSoftmax>((uint32_t)axis, [&](auto sel) {
       decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(x, out, outer, (uint32_t)axis);
-    });
+    }, 2 * outer * (size_t)axis * sizeof(float));
   } else {
     k_softmax_seq<<<seq_grid(outer * inner), 256, 0, s>>>(x, out, outer, axis, inner);
   }
@@ -402,7 +436,7 @@ void scale_mask_softmax(const float* S, const float* scale, const float* mask, f
   if (axis <= kMaxRowAxis && mask_rows > 0) {
     row_dispatch<SelScaleMaskSoftmax>((uint32_t)axis, [&](auto sel) {
       decltype(sel)::fn<<<row_grid(rows), 256, 0, s>>>(S, scale, mask, P, rows, (uint32_t)axis, (uint32_t)mask_rows);
-    });
+    }, 2 * rows * (size_t)axis * sizeof(float));
     MALUS_HIP(hipGetLastError());
     return;
   }
@@ -421,7 +455,7 @@ void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, si
   if (inner == 1 && axis <= kMaxRowAxis) {
     row_dispatch<SelSoftmaxBwd>((uint32_t)axis, [&](auto sel) {
       decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(y, dout, out, outer, (uint32_t)axis);
-    });
+    }, 3 * outer * (size_t)axis * sizeof(float));
   } else {
     k_softmax_bwd_seq<<<seq_grid(outer * inner), 256, 0, s>>>(y, dout, out, outer, axis, inner);
   }
@@ -433,7 +467,7 @@ void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, 
   if (inner == 1 && axis <= kMaxRowAxis) {
     row_dispatch<SelLN>((uint32_t)axis, [&](auto sel) {
       decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(x, y, var, outer, (uint32_t)axis, eps);
-    });
+    }, 2 * outer * (size_t)axis * sizeof(float));
   } else {
     k_layernorm_seq<<<seq_grid(outer * inner), 256, 0, s>>>(x, y, var, outer, axis, inner, eps);
   }
@@ -446,7 +480,7 @@ void layernorm_bwd(const float* y, const float* var, const float* dout, float* d
   if (inner == 1 && axis <= kMaxRowAxis) {
     row_dispatch<SelLNBwd>((uint32_t)axis, [&](auto sel) {
       decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(y, var, dout, dx, outer, (uint32_t)axis, eps, addend);
-    });
+    }, 3 * outer * (size_t)axis * sizeof(float));
   } else {
     k_layernorm_bwd_seq<<<seq_grid(outer * inner), 256, 0, s>>>(y, var, dout, dx, outer, axis, inner, eps);
     if (addend) binary_same(ADD, addend, dx, dx, outer * axis * inner, s);
@@ -460,7 +494,7 @@ void ce_fwd(const float* logits, const int32_t* tgt, float* probs, float* nll, s
   if (v <= kMaxRowAxis) {
     row_dispatch<SelCE>((uint32_t)v, [&](auto sel) {
       decltype(sel)::fn<<<row_grid(n), 256, 0, s>>>(logits, tgt, probs, nll, n, (uint32_t)v, err);
-    });
+    }, 2 * n * (size_t)v * sizeof(float));
   } else {
     k_ce_fwd_seq<<<seq_grid(n), 256, 0, s>>>(logits, tgt, probs, nll, n, v, err);
   }
@@ -471,6 +505,14 @@ void ce_bwd(const float* probs, const int32_t* tgt, const float* dout, float sca
             hipStream_t s) {
   size_t total = n * v;
   if (!total) return;
+  if (v % 4 == 0 && total < (1ull << 32)) {
+    const size_t total4 = total / 4;
+    size_t blocks = (total4 + 255) / 256;
+    if (blocks > (1u << 20)) blocks = 1u << 20;
+    k_ce_bwd4<<<(unsigned)blocks, 256, 0, s>>>(probs, tgt, dout, scale_host, dx, (uint32_t)n, (uint32_t)v, (uint32_t)total4);
+    MALUS_HIP(hipGetLastError());
+    return;
+  }
   size_t blocks = (total + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   k_ce_bwd<<<(unsigned)blocks, 256, 0, s>>>(probs, tgt, dout, scale_host, dx, n, (uint32_t)v);
