@@ -386,6 +386,28 @@ __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ 
   }
 }
 
+// float4 form of k_split_reduce (same per-element order): eight partial
+// loads are in flight before their adds, and 64-thread workgroups spread the
+// few thousand float4 columns of a weight gradient over every CU.
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(64) void k_split_reduce4(const v4f_t* __restrict__ partial, v4f_t* __restrict__ C,
+                                                      size_t mn4, int nsplit, const v4f_t* __restrict__ D) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn4; i += stride) {
+    v4f_t acc = partial[i];
+    int s = 1;
+    for (; s + 7 < nsplit; s += 8) {
+      v4f_t t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = partial[(size_t)(s + u) * mn4 + i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += t[u];
+    }
+    for (; s < nsplit; ++s) acc += partial[(size_t)s * mn4 + i];
+    C[i] = D ? D[i] + acc : acc;
+  }
+}
+
 // ---- kernel table -----------------------------------------------------------
 struct TileCfg { int tm, tn; };
 constexpr TileCfg kTiles[] = {{2, 3}, {2, 2}, {2, 1}, {1, 2}, {1, 1}};
@@ -544,9 +566,18 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
   MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, v), dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch),
                             dim3(256), args, 0, s));
   if (nsplit > 1) {
-    size_t blocks = (mn + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    k_split_reduce<<<(unsigned)blocks, 256, 0, s>>>(dst, C, mn, nsplit, D);
+    const bool vec = mn % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(dst) & 15) == 0 && (reinterpret_cast<uintptr_t>(D) & 15) == 0;
+    if (vec) {
+      size_t blocks = (mn / 4 + 63) / 64;
+      if (blocks > 16384) blocks = 16384;
+      k_split_reduce4<<<(unsigned)blocks, 64, 0, s>>>(reinterpret_cast<const v4f_t*>(dst), reinterpret_cast<v4f_t*>(C),
+                                                     mn / 4, nsplit, reinterpret_cast<const v4f_t*>(D));
+    } else {
+      size_t blocks = (mn + 255) / 256;
+      if (blocks > 4096) blocks = 4096;
+      k_split_reduce<<<(unsigned)blocks, 256, 0, s>>>(dst, C, mn, nsplit, D);
+    }
     MALUS_HIP(hipGetLastError());
     pool_free(dst, bucket);
   }

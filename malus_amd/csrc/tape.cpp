@@ -83,7 +83,8 @@ bool slot_is(int32_t s, F fn) { return t_fuse_vjps && slot(s) == reinterpret_cas
 // whose epilogue adds `old` (the product is rounded first, exactly as the
 // GradAcc add of a separate result would round).  Accumulation order is the
 // reference's: dA into grads[a], then dB into grads[b].
-void accumulate_matmul(std::unordered_map<int64_t, int64_t>& grads, int64_t a, int64_t b, int64_t dout) {
+void accumulate_matmul(std::unordered_map<int64_t, int64_t>& grads, int64_t a, int64_t b, int64_t dout, bool need_a,
+                       bool need_b) {
   auto fold = [&](int64_t x, bool is_a) {
     auto it = grads.find(x);
     const TensorBuffer* old = it == grads.end() ? nullptr : T(it->second);
@@ -95,9 +96,57 @@ void accumulate_matmul(std::unordered_map<int64_t, int64_t>& grads, int64_t a, i
       it->second = g;
     }
   };
-  fold(a, true);
-  fold(b, false);
+  if (need_a) fold(a, true);
+  if (need_b) fold(b, false);
 }
+
+// A VJP that reads the values of a shape-only handle (the intermediate of a
+// fused forward kernel) has no data to read: stop before any launch.
+void need_values(int64_t h) {
+  const TensorBuffer* t = T(h);
+  if (t->len && (!t->st || !t->st->ptr))
+    fail("malus: backward needs the values of a fused intermediate %s that was never stored", shape_str(t).c_str());
+}
+
+bool binary_op(int32_t op) { return op == Matmul || op == Add || op == Sub || op == Mul || op == Div; }
+
+// Gradient liveness.  A gradient is computed only where it can reach a leaf
+// the program still holds.  A registered leaf whose only references are the
+// tape's own (the program released its handle before backward, like the
+// per-forward `variable(...)` scale and mask of the attention block) can never
+// be passed to tape_get_grad, and its registry entry is dropped by
+// tape_on_release as soon as tape_clear lets go of it, so the VJPs that would
+// only feed it are skipped.  Every gradient a live handle can observe is
+// computed by the same kernels in the same order as without the pruning.
+struct GradLiveness {
+  std::unordered_map<int64_t, int64_t> refs;  // tape references per handle
+  std::unordered_map<int64_t, bool> need;
+
+  explicit GradLiveness(const std::vector<TapeNode>& nodes) {
+    for (const TapeNode& n : nodes) {
+      for (int64_t h : n.saved) ++refs[h];
+      ++refs[n.output];
+    }
+    for (const TapeNode& n : nodes) {  // recording order: inputs precede the nodes that consume them
+      bool any = (*this)(n.saved[0]);
+      if (binary_op(n.op)) any = (*this)(n.saved[1]) || any;
+      bool& o = need[n.output];
+      o = o || any || live_leaf(n.output);
+    }
+  }
+  bool live_leaf(int64_t h) const {
+    if (!t_leaves.count(h)) return false;
+    auto it = refs.find(h);
+    return T(h)->rc.load() > (it == refs.end() ? 0 : it->second);
+  }
+  bool operator()(int64_t h) {
+    auto it = need.find(h);
+    if (it != need.end()) return it->second;
+    const bool v = live_leaf(h);
+    need.emplace(h, v);
+    return v;
+  }
+};
 
 // tape.rs:815-828: take ownership of new_grad, fold it into grads[input].
 void accumulate(std::unordered_map<int64_t, int64_t>& grads, int64_t input, int64_t new_grad) {
@@ -342,41 +391,43 @@ void backward(int64_t loss) {
     seed->write_seq = enqueue_mark("seed");
     grads.emplace(loss, H(seed));
   }
+  GradLiveness need(nodes);
   for (auto it = nodes.rbegin(); it != nodes.rend(); ++it) {
     const TapeNode& n = *it;
     auto g = grads.find(n.output);
     if (g == grads.end()) continue;
     const int64_t dout = g->second;
+    const bool na = need(n.saved[0]);
+    const bool nb = binary_op(n.op) && need(n.saved[1]);
+    if (!na && !nb) continue;
     switch (n.op) {
       case Matmul: {
         int64_t a = n.saved[0], b = n.saved[1];
+        if (na) need_values(b);
+        if (nb) need_values(a);
         if (slot_is(MatmulBwdA, &malus_std_matmul_bwd_a) && slot_is(MatmulBwdB, &malus_std_matmul_bwd_b) &&
             slot_is(GradAcc, &malus_std_broadcast_add_fwd)) {
-          accumulate_matmul(grads, a, b, dout);
+          accumulate_matmul(grads, a, b, dout, na, nb);
           break;
         }
-        int64_t da = slot_fn<Fn3>(MatmulBwdA)(a, b, dout);
-        int64_t db = slot_fn<Fn3>(MatmulBwdB)(a, b, dout);
-        accumulate(grads, a, da);
-        accumulate(grads, b, db);
+        if (na) accumulate(grads, a, slot_fn<Fn3>(MatmulBwdA)(a, b, dout));
+        if (nb) accumulate(grads, b, slot_fn<Fn3>(MatmulBwdB)(a, b, dout));
         break;
       }
       case Add: case Sub: {
         int64_t a = n.saved[0], b = n.saved[1];
         int32_t sa = n.op == Add ? AddBwdA : SubBwdA, sb = n.op == Add ? AddBwdB : SubBwdB;
-        int64_t da = slot_fn<Fn2>(sa)(dout, a);
-        int64_t db = slot_fn<Fn2>(sb)(dout, b);
-        accumulate(grads, a, da);
-        accumulate(grads, b, db);
+        if (na) accumulate(grads, a, slot_fn<Fn2>(sa)(dout, a));
+        if (nb) accumulate(grads, b, slot_fn<Fn2>(sb)(dout, b));
         break;
       }
       case Mul: case Div: {
         int64_t a = n.saved[0], b = n.saved[1];
         int32_t sa = n.op == Mul ? MulBwdA : DivBwdA, sb = n.op == Mul ? MulBwdB : DivBwdB;
-        int64_t da = slot_fn<Fn3>(sa)(dout, a, b);
-        int64_t db = slot_fn<Fn3>(sb)(dout, a, b);
-        accumulate(grads, a, da);
-        accumulate(grads, b, db);
+        if (na) need_values(b);
+        if (nb) { need_values(a); need_values(b); }
+        if (na) accumulate(grads, a, slot_fn<Fn3>(sa)(dout, a, b));
+        if (nb) accumulate(grads, b, slot_fn<Fn3>(sb)(dout, a, b));
         break;
       }
       case Sigmoid: accumulate(grads, n.saved[0], slot_fn<Fn2>(SigmoidBwd)(n.output, dout)); break;

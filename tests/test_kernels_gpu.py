@@ -356,6 +356,21 @@ def test_matmul_split_k_weight_grad_shape(rt):
     rt.free(hx, hd, hw)
 
 
+@pytest.mark.parametrize("m,n", [(41, 35), (64, 36)])
+def test_matmul_split_k_reduce_widths(rt, m, n):
+    # long K with few output tiles takes the split-K path; an output whose
+    # size is not a multiple of 4 uses the scalar partial reduction, the
+    # others the float4 one
+    x = rand(8192, m)
+    d = rand(8192, n)
+    w = rand(m, n)
+    hx, hd, hw = rt.tensor(x), rt.tensor(d), rt.tensor(w)
+    got = run(rt, rt.L.malus_std_matmul_bwd_b(hx, hw, hd))
+    want = O.matmul(O.permute(x, (1, 0)), d)
+    assert_normwise(got, want, 1e-5, "split-K dW")
+    rt.free(hx, hd, hw)
+
+
 # ---------------------------------------------------------------- optimizer
 def test_adam_l2_fused_bitexact(rt):
     n = 100003

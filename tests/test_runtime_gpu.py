@@ -281,6 +281,39 @@ def test_grad_accumulates_across_backwards_and_zero_grad(tape):
     assert lens[0] == 0 and lens[1] == 0  # releasing a leaf drops its registry entries
 
 
+def test_released_leaf_gradient_is_not_computed(tape):
+    # out = x * s with s a [1] leaf.  While the program holds s, backward
+    # computes ds = sum(dout * x) (tape.rs:460-469 computes both VJPs); once
+    # the program has released s (only the tape still references it, so its
+    # grad can never be queried) that VJP is skipped.  dx is the same either way.
+    rt = tape
+    xv = np.random.default_rng(5).uniform(-1, 1, (64, 32)).astype(np.float32)
+
+    def step(keep_s):
+        x = leaf(rt, *xv.ravel())
+        s = leaf(rt, 0.5)
+        out = rt.L.malus_std_broadcast_fwd(M.MUL, x, s)
+        rt.L.tape_record_binop(OP["Mul"], x, s, out)
+        if not keep_s:
+            rt.free(s)
+        rt.L.malus_rc_reset()
+        rt.L.backward(out)
+        c = (C.c_int64 * 3)()
+        rt.L.malus_rc_counts(c)
+        gx = grad(rt, x)
+        gs = grad(rt, s) if keep_s else None
+        rt.free(x, out, *([s] if keep_s else []))
+        rt.L.tape_reset()
+        return c[2], gx, gs
+
+    allocs_live, gx_live, gs = step(True)
+    allocs_dead, gx_dead, _ = step(False)
+    np.testing.assert_allclose(gs, [xv.astype(np.float64).sum()], rtol=1e-5, atol=1e-3)
+    assert_bitexact(gx_dead, gx_live, "dx")
+    assert np.all(gx_live == 0.5)
+    assert allocs_dead < allocs_live, (allocs_dead, allocs_live)
+
+
 def test_broadcast_add_backward_reduces_to_operand_shape(tape):
     # tests.rs:1130-1177: (1,3) + (2,3), loss = sum -> da = [[2,2,2]], db = ones
     rt = tape
