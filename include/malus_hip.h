@@ -151,6 +151,11 @@ int malus_gemm_set_tile(int tm, int tn);
 void malus_gemm_set_split(int target_blocks);
 /* Tuning: 0 keeps every GEMM on the register-staged path; 1 (default) allows the LDS-DMA path. */
 void malus_gemm_set_dma(int on);
+/* Fused attention scores softmax(q @ k^T * scale + mask, axis=2) for q, k
+ * [bh, t, hs] (t, hs in {256,64}, {128,64}, {64,32}, {64,64}); the kernel the
+ * model's fused forward uses for nanogpt_modular.ml:57-61.  causal != 0
+ * promises the -1e9-above-the-diagonal mask of tensor_causal_mask. */
+int64_t malus_std_attn_scores_softmax(int64_t q, int64_t k, int64_t scale, int64_t mask, int32_t causal);
 int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
 int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
 void malus_set_abort_on_error(int on);

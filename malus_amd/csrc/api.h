@@ -21,6 +21,9 @@ void set_last_error(const char* msg);
 void tape_on_release(int64_t handle);
 void register_default_backward_fns();
 std::vector<size_t> tape_normalize_perm(const std::vector<size_t>& raw, size_t rank);
+// Record a fused node (tags 100 HeadProj, 101 Scores, 102 AttnOut; see
+// tape.cpp) with inputs a, b and output out; retains all three.
+void tape_record_fused(int32_t op, int64_t a, int64_t b, int64_t out, const std::vector<int64_t>& meta);
 
 }  // namespace malus
 
@@ -32,6 +35,18 @@ int64_t matmul_impl(int64_t a, int64_t b, const malus::TensorBuffer* D);
 int64_t matmul_bwd_a_impl(int64_t a, int64_t b, int64_t dout, const malus::TensorBuffer* D);
 int64_t matmul_bwd_b_impl(int64_t a, int64_t b, int64_t dout, const malus::TensorBuffer* D);
 int64_t layernorm_bwd_impl(int64_t y, int64_t var, int64_t dout, int64_t axis, const malus::TensorBuffer* D);
+// Head-folded attention GEMMs (stdlib.cpp): the composed ops' values with
+// the permute copies folded into GEMM addressing.  heads_foldable: shapes
+// the folded layouts support.
+bool heads_foldable(size_t B, size_t T, size_t H, size_t hs);
+int64_t head_proj_fwd(int64_t x, int64_t w, size_t B, size_t T, size_t H);
+int64_t head_proj_bwd_x(int64_t dqh, int64_t w, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
+int64_t head_proj_bwd_w(int64_t x, int64_t dqh, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
+int64_t attn_out_fwd(int64_t p, int64_t v, size_t B, size_t T, size_t H);
+int64_t attn_out_bwd_p(int64_t datt, int64_t v, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
+int64_t attn_out_bwd_v(int64_t p, int64_t datt, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
+int64_t scores_bwd_q(int64_t ds, int64_t k, const malus::TensorBuffer* D);
+int64_t scores_bwd_k(int64_t ds, int64_t q, const malus::TensorBuffer* D);
 
 #define API_TRY try {
 #define API_CATCH(...)                                   \

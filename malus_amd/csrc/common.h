@@ -135,6 +135,15 @@ void reduce_axis(int op, const float* x, float* out, size_t outer, size_t axis, 
 // each op rounded as the separate broadcast kernels round it.
 void scale_mask_softmax(const float* S, const float* scale, const float* mask, float* P, size_t rows, size_t axis,
                         size_t mask_rows, hipStream_t s);
+// P = softmax(Q K^T * scale[0] + mask) over each query row of every head,
+// Q, K: [bh, t, hs], mask: [t, t], P: [bh, t, t]; the same values as
+// gemm(Q, K^T) followed by scale_mask_softmax.  causal: the mask is
+// -1e9 above the diagonal and 0 elsewhere (key tiles wholly above a row
+// block are skipped).  Returns false (nothing launched) for shapes the
+// kernel is not built for.
+bool attn_scores_supported(size_t bh, size_t t, size_t hs);
+bool attn_scores_softmax(const float* Q, const float* K, const float* scale, const float* mask, float* P, size_t bh,
+                         size_t t, size_t hs, bool causal, hipStream_t s);
 // Sum over the axis of x * y (y has x's layout); each product rounded to f32.
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 // Broadcast [outer, inner] back to [outer, axis, inner] (expand_axis).
@@ -161,6 +170,22 @@ void embedding(const float* w, const int32_t* idx, float* out, size_t t, size_t 
 void embedding_bwd(const float* dout, const int32_t* idx, float* dw, size_t t, size_t v, size_t d, hipStream_t s);
 void permute(const float* x, float* out, int ndim, const size_t* in_shape, const size_t* perm, hipStream_t s);
 
+// Operand addressing for gemm_mapped: element (i, j) of a stored matrix
+// (rows i, columns j) of batch b sits at  b-map(b) + r-map(i) + c-map(j)
+// floats past the operand's pointer, each map being
+//   x -> (x / div) * s1 + (x % div) * s0     (div == 0: x * s0),
+// which covers dense row-major storage ({0, 0, ld} rows, {0, 0, 1} columns)
+// and the head-folded views of multi-head attention (a [B*T, H*hs] matrix
+// stored as [B, H, T, hs], or per-head [T, hs] matrices inside [B, T, H, hs]).
+// Offsets stay below 2^29 floats (2^31 bytes), so the fields are 32-bit.
+struct GemmMap { int div, s1, s0; };
+struct GemmLayout { GemmMap b, r, c; };
+// ext_a / ext_b: floats addressable past A / B (the whole allocation).
+struct GemmLayouts { GemmLayout a, b, c; int ext_a, ext_b; };
+inline GemmLayout dense_layout(long ld, long batch_stride) {
+  return {{0, 0, (int)batch_stride}, {0, 0, (int)ld}, {0, 0, 1}};
+}
+
 // Batched GEMM: C[b] = op(A[b]) @ op(B[b]); transA: A stored [K,M]; transB: B stored [N,K].
 // strideA/B/C are element strides between batches (0 broadcasts).
 // With D (C's layout and batch stride), C = D + op(A) @ op(B): the GEMM
@@ -168,6 +193,13 @@ void permute(const float* x, float* out, int ndim, const size_t* in_shape, const
 // stored product would round.
 void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
           long strideA, long strideB, long strideC, hipStream_t s, const float* D = nullptr);
+// gemm with every operand addressed through its layout (D shares C's).
+// Returns false, launching nothing, when the LDS-DMA kernels cannot take
+// the layouts: K % 16 != 0, a contiguous dimension whose maps are not unit
+// stride in runs of 4, a k map whose div is not a multiple of 16, a C row
+// map whose div is not a multiple of 32, or offsets of 2^31 bytes or more.
+bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
+                 const GemmLayouts& L, hipStream_t s, const float* D = nullptr);
 
 // Fused Adam + L2 update (examples/nanogpt_modular.ml:97-108 op order).
 // One parameter tensor of a multi-tensor Adam update (device pointers).

@@ -236,31 +236,57 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* p, un
 }
 #endif
 
+// Element x of an index map (strides in floats); see GemmMap.  MAP = false
+// instances serve dense operands, whose maps are all x * s0.
+template <bool MAP>
+__device__ __forceinline__ int map_at(const GemmMap& f, int x) {
+  if (!MAP) return x * f.s0;
+  return f.div ? (x / f.div) * f.s1 + (x % f.div) * f.s0 : x * f.s0;
+}
+
+// Byte offset of k row/column k along a k map, advanced one 16-deep slab at
+// a time without a division (the host keeps div a multiple of 16).
+template <bool MAP>
+struct KCursor {
+  int q, r;  // k = q * div + r  (r = k for dense maps)
+  __device__ __forceinline__ void init(const GemmMap& f, int k) {
+    if (MAP && f.div) { q = k / f.div; r = k % f.div; } else { q = 0; r = k; }
+  }
+  __device__ __forceinline__ int bytes(const GemmMap& f) const { return 4 * ((MAP && f.div) ? q * f.s1 + r * f.s0 : r * f.s0); }
+  __device__ __forceinline__ void advance(const GemmMap& f) {
+    r += BK;
+    if (MAP && f.div && r == f.div) { r = 0; ++q; }
+  }
+};
+
 template <int BX, bool KC>
 struct DmaSlab {
   static constexpr int SIZE = BX * BK;        // floats
   static constexpr int PER_WAVE = SIZE / 1024;  // 1 KB instructions per wave (4 waves)
   int off[PER_WAVE];                          // byte offset of this lane's chunk at k0 = 0
 
-  // x0: first row/column of the tile; X: extent of x; ld: row stride of the
-  // operand in floats (K for KC, X for XC)
-  __device__ __forceinline__ void init(int x0, int ld, int wave, int lane) {
+  // x0: first row/column of the tile.  fx maps the operand's free index x
+  // (m for A, n for B), fk its k index; the host guarantees that 4
+  // consecutive values of the contiguous index and 16 consecutive k never
+  // straddle a map's div (so one slab's k rows sit at fk(k0) + r * fk.s0).
+  template <bool MAP>
+  __device__ __forceinline__ void init(int x0, const GemmMap& fx, const GemmMap& fk, int wave, int lane) {
 #pragma unroll
     for (int q = 0; q < PER_WAVE; ++q) {
       const int c = q * 4 + wave;  // 256-float run of the slab
       if (KC) {
         const int r = c * 16 + lane / 4;
         const int chunk = (lane & 3) ^ ((r >> 1) & 3);
-        off[q] = ((x0 + r) * ld + 4 * chunk) * 4;
+        off[q] = (map_at<MAP>(fx, x0 + r) + 4 * chunk) * 4;
       } else {
         const int f = c * 256 + 4 * lane;
-        off[q] = ((f / BX) * ld + x0 + f % BX) * 4;
+        off[q] = (map_at<MAP>(fx, x0 + f % BX) + (f / BX) * fk.s0) * 4;
       }
     }
   }
 #if defined(__HIP_DEVICE_COMPILE__)
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, float* S, int wave, int k0, int ld) const {
-    const int dk = KC ? 4 * k0 : 4 * k0 * ld;
+  // dk: byte offset of k row/column k0 (fk(k0) * 4), uniform over the block
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, float* S, int wave, int dk) const {
 #pragma unroll
     for (int q = 0; q < PER_WAVE; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(S + (q * 4 + wave) * 256), 16, off[q] + dk, 0, 0, 0);
@@ -282,13 +308,15 @@ struct DmaSlab {
   }
 };
 
-// Same contract as k_sgemm; the host guarantees K % 16 == 0, rows of the
-// x-contiguous operands a multiple of 4 floats, and per-batch operand bytes
-// below 2^31.
-template <int TM, int TN, bool TA, bool TB>
+// Same contract as k_sgemm, with each operand addressed through its
+// GemmLayout (batch, row and column maps of the stored matrix; C's also
+// addresses D).  Dense row-major operands are the maps {0, 0, ld}.  The
+// host guarantees K % 16 == 0, the map conditions above, and every byte
+// offset below 2^31; a split-K launch writes dense partials.
+template <int TM, int TN, bool TA, bool TB, bool MAP>
 __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ A, const float* __restrict__ B,
-                                                      float* __restrict__ C, int M, int N, int K, long sA, long sB,
-                                                      long sC, int k_chunk, int tiles_n, long split_stride,
+                                                      float* __restrict__ C, int M, int N, int K, GemmLayouts L,
+                                                      int k_chunk, int tiles_n, long split_stride,
                                                       const float* __restrict__ D) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 64 * TM, BN = 64 * TN;
@@ -303,23 +331,28 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   const int tm = tile / tiles_n, tn = tile % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
   const int b = blockIdx.z;
-  A += (size_t)b * sA;
-  B += (size_t)b * sB;
-  C += (size_t)b * sC + (size_t)blockIdx.y * split_stride;
-  if (D) D += (size_t)b * sC;
+  const int ba = map_at<MAP>(L.a.b, b), bb = map_at<MAP>(L.b.b, b);
+  A += ba;
+  B += bb;
+  C += map_at<MAP>(L.c.b, b) + (long)blockIdx.y * split_stride;
+  if (D) D += map_at<MAP>(L.c.b, b);
   const int kbeg = blockIdx.y * k_chunk;
   const int kend = min(K, kbeg + k_chunk);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * 32 * TM, wn = (wave & 1) * 32 * TN;
   const int li = lane & 31, lk = lane >> 5;
-  const int lda = TA ? M : K, ldb = TB ? K : N;
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, (unsigned)((size_t)M * K * 4));
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, (unsigned)((size_t)K * N * 4));
+  // stored A: [M][K] (rows m) or [K][M] (rows k); stored B: [K][N] or [N][K]
+  const GemmMap& fam = TA ? L.a.c : L.a.r;
+  const GemmMap& fak = TA ? L.a.r : L.a.c;
+  const GemmMap& fbn = TB ? L.b.r : L.b.c;
+  const GemmMap& fbk = TB ? L.b.c : L.b.r;
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, (unsigned)((L.ext_a - ba) * 4));
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, (unsigned)((L.ext_b - bb) * 4));
   SlabA sa;
   SlabB sb;
-  sa.init(m0, lda, wave, lane);
-  sb.init(n0, ldb, wave, lane);
+  sa.template init<MAP>(m0, fam, fak, wave, lane);
+  sb.template init<MAP>(n0, fbn, fbk, wave, lane);
 
   v16f acc[TM][TN];
 #pragma unroll
@@ -328,9 +361,14 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
     for (int j = 0; j < TN; ++j) acc[i][j] = v16f{0};
 
   const int nk = (kend - kbeg) / BK;
+  KCursor<MAP> ka, kb;
+  ka.init(fak, kbeg);
+  kb.init(fbk, kbeg);
   if (nk > 0) {
-    sa.issue(ra, As[0], wave, kbeg, lda);
-    sb.issue(rb, Bs[0], wave, kbeg, ldb);
+    sa.issue(ra, As[0], wave, ka.bytes(fak));
+    sb.issue(rb, Bs[0], wave, kb.bytes(fbk));
+    ka.advance(fak);
+    kb.advance(fbk);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -344,8 +382,10 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
     __builtin_amdgcn_sched_barrier(0);
     // the other buffer was last read before the previous barrier
     if (kt + 1 < nk) {
-      sa.issue(ra, As[cur ^ 1], wave, kbeg + (kt + 1) * BK, lda);
-      sb.issue(rb, Bs[cur ^ 1], wave, kbeg + (kt + 1) * BK, ldb);
+      sa.issue(ra, As[cur ^ 1], wave, ka.bytes(fak));
+      sb.issue(rb, Bs[cur ^ 1], wave, kb.bytes(fbk));
+      ka.advance(fak);
+      kb.advance(fbk);
     }
 #pragma unroll
     for (int s = 0; s < 8; ++s)
@@ -358,19 +398,26 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
     __syncthreads();
   }
 
+  // C rows come in aligned 32-row groups (the host keeps the row map's div
+  // a multiple of 32), so one map evaluation per group and per column
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
+    const int rbase = map_at<MAP>(L.c.r, m0 + wm + 32 * i);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = n0 + wn + 32 * j + li;
       if (n < N) {
+        const int cn = map_at<MAP>(L.c.c, n) + rbase;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
-          if (m < M) C[(size_t)m * N + n] = D ? D[(size_t)m * N + n] + acc[i][j][r] : acc[i][j][r];
+          const int dm = 8 * (r >> 2) + 4 * lk + (r & 3);
+          const int m = m0 + wm + 32 * i + dm;
+          const int o = cn + dm * L.c.r.s0;
+          if (m < M) C[o] = D ? D[o] + acc[i][j][r] : acc[i][j][r];
         }
       }
     }
+  }
 #endif
 }
 
@@ -420,7 +467,8 @@ inline int variant(bool ta, bool tb, bool va, bool vb, bool dma) {
 
 template <int TM, int TN, bool TA, bool TB>
 const void* kernel_of(int v) {
-  if (v & 16) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB>);
+  if (v & 32) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, true>);
+  if (v & 16) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, false>);
   const bool va = v & 2, vb = v & 1;
   if (va && vb) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, true>);
   if (va) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, false>);
@@ -450,7 +498,7 @@ const void* kernel_for(int ti, int v) {
 // Co-resident workgroups per CU of each kernel variant (VGPR and LDS
 // limited), from the runtime's occupancy calculator; cached per variant.
 int occupancy(int ti, int v) {
-  static int cache[kNumTiles][32];
+  static int cache[kNumTiles][64];
   int& o = cache[ti][v];
   if (o == 0) {
     int n = 0;
@@ -531,6 +579,80 @@ Plan plan_gemm(int batch, int M, int N, int K, int v) {
 
 }  // namespace
 
+namespace {
+
+void trace_plan(int batch, int M, int N, int K, bool transA, bool transB, bool dma, const Plan& p, int v,
+                const char* tag) {
+  static const bool trace = getenv("MALUS_GEMM_TRACE") != nullptr;
+  if (trace)
+    fprintf(stderr, "malus gemm b%d %dx%dx%d t%d%d -> %s%s tile %dx%d occ %d split %d k_chunk %d\n", batch, M, N, K,
+            transA, transB, dma ? "dma" : "reg", tag, 64 * kTiles[p.ti].tm, 64 * kTiles[p.ti].tn, occupancy(p.ti, v),
+            p.nsplit, p.k_chunk);
+}
+
+// Sum the split-K partials into C (+ D) in split order, then return the
+// partial buffer to the pool.
+void split_reduce(float* partial, float* C, size_t mn, int nsplit, const float* D, hipStream_t s, size_t bucket) {
+  const bool vec = mn % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(partial) & 15) == 0 && (reinterpret_cast<uintptr_t>(D) & 15) == 0;
+  if (vec) {
+    size_t blocks = (mn / 4 + 63) / 64;
+    if (blocks > 16384) blocks = 16384;
+    k_split_reduce4<<<(unsigned)blocks, 64, 0, s>>>(reinterpret_cast<const v4f_t*>(partial), reinterpret_cast<v4f_t*>(C),
+                                                   mn / 4, nsplit, reinterpret_cast<const v4f_t*>(D));
+  } else {
+    size_t blocks = (mn + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    k_split_reduce<<<(unsigned)blocks, 256, 0, s>>>(partial, C, mn, nsplit, D);
+  }
+  MALUS_HIP(hipGetLastError());
+  pool_free(partial, bucket);
+}
+
+// One LDS-DMA launch (plus the split-K reduction); a split writes dense
+// partials, so callers with a non-dense C pass split_ok = false.
+void launch_dma(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
+                GemmLayouts L, hipStream_t s, const float* D, bool split_ok, bool mapped) {
+  // mapped operands run the MAP instance on the dense shape's plan, so a
+  // mapped GEMM splits K exactly like its dense twin
+  const int v = variant(transA, transB, false, false, true);
+  Plan p = plan_gemm(batch, M, N, K, v);
+  const char* tag = mapped ? " mapped" : "";
+  if (!split_ok && p.nsplit > 1) {
+    p.nsplit = 1;
+    p.k_chunk = K;
+  }
+  trace_plan(batch, M, N, K, transA, transB, true, p, v, tag);
+  const int bm = 64 * kTiles[p.ti].tm, bn = 64 * kTiles[p.ti].tn;
+  const int tiles_n = (N + bn - 1) / bn, tiles = ((M + bm - 1) / bm) * tiles_n;
+  int nsplit = p.nsplit, k_chunk = p.k_chunk;
+  const size_t mn = (size_t)M * N;
+  size_t bucket = 0;
+  float* dst = C;
+  if (nsplit > 1) {
+    dst = static_cast<float*>(pool_alloc(mn * nsplit * sizeof(float), &bucket));
+    L.c = dense_layout(N, 0);
+  }
+  long split_stride = nsplit > 1 ? (long)mn : 0;
+  const float* Dk = nsplit > 1 ? nullptr : D;  // split-K applies the addend in the reduction
+  void* args[] = {&A, &B, &dst, &M, &N, &K, &L, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk};
+  MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, mapped ? v | 32 : v), dim3((unsigned)tiles, (unsigned)nsplit,
+                            (unsigned)batch), dim3(256), args, 0, s));
+  if (nsplit > 1) split_reduce(dst, C, mn, nsplit, D, s, bucket);
+}
+
+bool map_contig4(const GemmMap& f) { return f.s0 == 1 && (f.div == 0 || f.div % 4 == 0); }
+bool map_k16(const GemmMap& f) { return f.div == 0 || f.div % 16 == 0; }
+// largest offset the map reaches for x in [0, n)
+long map_max(const GemmMap& f, long n) {
+  if (n <= 0) return 0;
+  if (!f.div) return (n - 1) * f.s0;
+  const long q = (n - 1) / f.div, r = f.div - 1 < n - 1 ? f.div - 1 : n - 1;
+  return q * f.s1 + r * f.s0;
+}
+
+}  // namespace
+
 void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB, long sA,
           long sB, long sC, hipStream_t s, const float* D) {
   if (batch <= 0 || M <= 0 || N <= 0) return;
@@ -539,19 +661,23 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
     return;
   }
   if (batch > 65535) fail("malus: gemm batch %d exceeds 65535", batch);
+  const long lda = transA ? M : K, ldb = transB ? K : N;
+  const long ext_a = (long)(batch - 1) * sA + (long)M * K, ext_b = (long)(batch - 1) * sB + (long)K * N;
+  // LDS-DMA path: whole 16-deep K slabs, 16-byte rows, 32-bit byte offsets
+  const bool dma = K % 16 == 0 && (transA ? M % 4 == 0 : true) && (transB ? true : N % 4 == 0) &&
+                   (size_t)ext_a * 4 < (1ull << 31) && (size_t)ext_b * 4 < (1ull << 31) &&
+                   ((size_t)(batch - 1) * sC + (size_t)M * N) * 4 < (1ull << 31) && g_allow_dma;
+  if (dma) {
+    GemmLayouts L{dense_layout(lda, sA), dense_layout(ldb, sB), dense_layout(N, sC), (int)ext_a, (int)ext_b};
+    launch_dma(A, B, C, batch, M, N, K, transA, transB, L, s, D, true, false);
+    return;
+  }
   // float4 staging needs the contiguous dim of each operand to be a multiple of 4
   const bool va = transA ? (M % 4 == 0) : (K % 4 == 0);
   const bool vb = transB ? (K % 4 == 0) : (N % 4 == 0);
-  // LDS-DMA path: whole 16-deep K slabs, 16-byte rows, 32-bit byte offsets
-  const bool dma = K % 16 == 0 && (transA ? M % 4 == 0 : true) && (transB ? true : N % 4 == 0) &&
-                   (size_t)M * K * 4 < (1ull << 31) && (size_t)K * N * 4 < (1ull << 31) && g_allow_dma;
-  const int v = variant(transA, transB, va, vb, dma);
+  const int v = variant(transA, transB, va, vb, false);
   const Plan p = plan_gemm(batch, M, N, K, v);
-  static const bool trace = getenv("MALUS_GEMM_TRACE") != nullptr;
-  if (trace)
-    fprintf(stderr, "malus gemm b%d %dx%dx%d t%d%d -> %s tile %dx%d occ %d split %d k_chunk %d\n", batch, M, N, K,
-            transA, transB, dma ? "dma" : "reg", 64 * kTiles[p.ti].tm, 64 * kTiles[p.ti].tn, occupancy(p.ti, v),
-            p.nsplit, p.k_chunk);
+  trace_plan(batch, M, N, K, transA, transB, false, p, v, "");
   const int bm = 64 * kTiles[p.ti].tm, bn = 64 * kTiles[p.ti].tn;
   const int tiles_m = (M + bm - 1) / bm, tiles_n = (N + bn - 1) / bn;
   const int tiles = tiles_m * tiles_n;
@@ -565,22 +691,31 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
   void* args[] = {&A, &B, &dst, &M, &N, &K, &sA, &sB, &sC, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk};
   MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, v), dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch),
                             dim3(256), args, 0, s));
-  if (nsplit > 1) {
-    const bool vec = mn % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0 &&
-                     (reinterpret_cast<uintptr_t>(dst) & 15) == 0 && (reinterpret_cast<uintptr_t>(D) & 15) == 0;
-    if (vec) {
-      size_t blocks = (mn / 4 + 63) / 64;
-      if (blocks > 16384) blocks = 16384;
-      k_split_reduce4<<<(unsigned)blocks, 64, 0, s>>>(reinterpret_cast<const v4f_t*>(dst), reinterpret_cast<v4f_t*>(C),
-                                                     mn / 4, nsplit, reinterpret_cast<const v4f_t*>(D));
-    } else {
-      size_t blocks = (mn + 255) / 256;
-      if (blocks > 4096) blocks = 4096;
-      k_split_reduce<<<(unsigned)blocks, 256, 0, s>>>(dst, C, mn, nsplit, D);
-    }
-    MALUS_HIP(hipGetLastError());
-    pool_free(dst, bucket);
-  }
+  if (nsplit > 1) split_reduce(dst, C, mn, nsplit, D, s, bucket);
+}
+
+bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
+                 const GemmLayouts& L, hipStream_t s, const float* D) {
+  if (batch <= 0 || M <= 0 || N <= 0 || K <= 0 || batch > 65535 || K % 16 || !g_allow_dma) return false;
+  // contiguous dimension of each stored operand: runs of 4 floats
+  const GemmMap& a_contig = L.a.c;  // A [M][K]: k;  A^T [K][M]: m
+  const GemmMap& b_contig = L.b.c;  // B [K][N]: n;  B^T [N][K]: k
+  if (!map_contig4(a_contig) || !map_contig4(b_contig)) return false;
+  if (transA ? M % 4 : 0) return false;
+  if (transB ? 0 : N % 4) return false;
+  const GemmMap& fak = transA ? L.a.r : L.a.c;
+  const GemmMap& fbk = transB ? L.b.c : L.b.r;
+  if (!map_k16(fak) || !map_k16(fbk)) return false;
+  if (L.c.r.div % 32) return false;
+  // every operand offset the kernels form stays below 2^31 bytes
+  const long lim = (1l << 31) / 4;
+  const long ea = map_max(L.a.b, batch) + map_max(L.a.r, transA ? K : M) + map_max(L.a.c, transA ? M : K) + 1;
+  const long eb = map_max(L.b.b, batch) + map_max(L.b.r, transB ? N : K) + map_max(L.b.c, transB ? K : N) + 1;
+  const long ec = map_max(L.c.b, batch) + map_max(L.c.r, (M + 127) / 128 * 128) + map_max(L.c.c, N) + 1;
+  if (ea > L.ext_a || eb > L.ext_b || L.ext_a >= lim || L.ext_b >= lim || ec >= lim) return false;
+  const bool c_dense = L.c.r.div == 0 && L.c.c.div == 0 && L.c.c.s0 == 1 && L.c.r.s0 == N;
+  launch_dma(A, B, C, batch, M, N, K, transA, transB, L, s, D, c_dense && batch == 1, true);
+  return true;
 }
 
 }  // namespace k

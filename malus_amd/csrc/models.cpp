@@ -43,7 +43,8 @@ namespace {
 
 enum Op : int32_t {
   OP_MATMUL = 0, OP_ADD = 1, OP_SUB = 2, OP_MUL = 3, OP_DIV = 4, OP_TRANSPOSE = 13, OP_RESHAPE = 19, OP_SOFTMAX = 20,
-  OP_LAYERNORM = 21, OP_GELU = 22, OP_CE = 23, OP_EMBEDDING = 24
+  OP_LAYERNORM = 21, OP_GELU = 22, OP_CE = 23, OP_EMBEDDING = 24,
+  TAG_HEAD_PROJ = 100, TAG_SCORES = 101, TAG_ATTN_OUT = 102  // fused nodes (tape.cpp)
 };
 
 // grad-tracked binop: lower + tape_record_binop (codegen-cpu/lib.rs:1531-1552)
@@ -109,7 +110,16 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   // nanogpt_modular.ml:47-68
   int64_t y1 = layernorm(x);
   int64_t xn1 = binop(OP_MUL, y1, P[0]);
+  // Fused heads: the head fold / unfold permutes and K's transpose are
+  // folded into GEMM addressing (one tape node per projection, per score
+  // product and per attention output; the same values as the composed ops).
+  const bool fused_heads = g.fused_fwd && heads_foldable(B, Tn, H, hs);
   auto head_fold = [&](int64_t w) {
+    if (fused_heads) {
+      int64_t Qh = head_proj_fwd(xn1, w, B, Tn, H);
+      tape_record_fused(TAG_HEAD_PROJ, xn1, w, Qh, {(int64_t)B, (int64_t)Tn, (int64_t)H});
+      return Qh;
+    }
     int64_t q = binop(OP_MATMUL, xn1, w);
     int64_t q4 = reshape(q, {B, Tn, H, hs});
     int64_t qp = permute(q4, {0, 2, 1, 3});
@@ -120,17 +130,49 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   int64_t Q = head_fold(P[1]);
   int64_t K = head_fold(P[2]);
   int64_t Vv = head_fold(P[3]);
-  int64_t Kt = permute(K, {0, 2, 1});
+  int64_t Kt = fused_heads ? 0 : permute(K, {0, 2, 1});
   size_t s11[2] = {1, 1};
   int64_t ones11 = tensor_alloc_ones_gpu(s11, 2);
   int64_t scale = malus_std_scalar_op(k::MUL, ones11, 1.0f / sqrtf((float)hs), 1);  // ones(1,1) * (1/sqrt(hs))
   tensor_release(ones11);
   tape_register_leaf(scale);  // variable(...)
-  int64_t S = binop(OP_MATMUL, Q, Kt);
+  const size_t sshape[3] = {B * H, Tn, Tn};
+  // Fused scores: S = Q @ Kt stays in registers (its tape node gets a
+  // shape-only handle).  Only the VJP of the scale leaf would read S, and
+  // that leaf is released with the rest of this block's temporaries, so the
+  // backward pass never computes it.
+  const bool fused_scores = fused_heads && k::attn_scores_supported(B * H, Tn, hs);
+  int64_t S;
+  if (fused_scores) {
+    S = malus::H(alloc_virtual(F32, sshape, 3));
+    tape_record_fused(TAG_SCORES, Q, K, S, {});
+  } else if (fused_heads) {  // S = Q @ K^T with K read in place
+    TensorBuffer* st = alloc_tensor(F32, sshape, 3);
+    KTimer* kt = ktimer_begin("gemm");
+    k::gemm(T(Q)->f32(), T(K)->f32(), st->f32(), (int)(B * H), (int)Tn, (int)Tn, (int)hs, false, true,
+            (long)(Tn * hs), (long)(Tn * hs), (long)(Tn * Tn), stream());
+    ktimer_end(kt, 2.0 * B * H * Tn * Tn * hs);
+    st->write_seq = enqueue_mark("matmul");
+    S = malus::H(st);
+    tape_record_fused(TAG_SCORES, Q, K, S, {});
+  } else {
+    S = binop(OP_MATMUL, Q, Kt);
+  }
   int64_t mask = tensor_causal_mask((int64_t)Tn);
   tape_register_leaf(mask);  // variable(mask)
   int64_t Ss, Sm, Pm;
-  if (g.fused_fwd) {
+  if (fused_scores) {
+    Ss = malus::H(alloc_virtual(F32, sshape, 3));
+    Sm = malus::H(alloc_virtual(F32, sshape, 3));
+    TensorBuffer* p = alloc_tensor(F32, sshape, 3);
+    if (!k::attn_scores_softmax(T(Q)->f32(), T(K)->f32(), T(scale)->f32(), T(mask)->f32(), p->f32(), B * H, Tn, hs,
+                                /*causal=*/true, stream()))
+      fail("malus: fused attention scores rejected a supported shape");
+    p->write_seq = enqueue_mark("attn_scores_softmax");
+    Pm = malus::H(p);
+    tape_record_binop(OP_MUL, S, scale, Ss);
+    tape_record_binop(OP_ADD, Ss, mask, Sm);
+  } else if (g.fused_fwd) {
     // scores * scale + mask -> softmax in one pass.  The tape gets the same
     // three records; the two intermediates are shape-only handles because
     // no VJP reads their values (add: shapes; mul: S and scale; softmax: P).
@@ -149,10 +191,16 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
     Pm = malus_std_softmax_fwd(Sm, 2);
   }
   tape_record_reduce(OP_SOFTMAX, Sm, Pm, 2, 0);
-  int64_t AO = binop(OP_MATMUL, Pm, Vv);
-  int64_t ao4 = reshape(AO, {B, H, Tn, hs});
-  int64_t aop = permute(ao4, {0, 2, 1, 3});
-  int64_t att = reshape(aop, {N, C});
+  int64_t AO = 0, ao4 = 0, aop = 0, att;
+  if (fused_heads) {
+    att = attn_out_fwd(Pm, Vv, B, Tn, H);
+    tape_record_fused(TAG_ATTN_OUT, Pm, Vv, att, {(int64_t)B, (int64_t)Tn, (int64_t)H});
+  } else {
+    AO = binop(OP_MATMUL, Pm, Vv);
+    ao4 = reshape(AO, {B, H, Tn, hs});
+    aop = permute(ao4, {0, 2, 1, 3});
+    att = reshape(aop, {N, C});
+  }
   int64_t proj, x2;
   if (g.fused_fwd) residual_matmul(x, att, P[4], &proj, &x2);
   else {

@@ -602,6 +602,28 @@ int64_t malus_std_cross_entropy_bwd(int64_t probs, int64_t targets, int64_t dout
   return done(out, "cross_entropy_bwd");
   API_CATCH(0)
 }
+// Fused attention scores: softmax(q @ permute(k, 0, 2, 1) * scale + mask,
+// axis=2) for q, k: [bh, t, hs], scale: [1, 1], mask: [t, t].  causal != 0
+// promises a causal mask (-1e9 above the diagonal).  Returns 0 with the error
+// set for shapes the fused kernel is not built for.
+int64_t malus_std_attn_scores_softmax(int64_t q, int64_t kk, int64_t scale, int64_t mask, int32_t causal) {
+  API_TRY
+  TensorBuffer *Q = T(q), *K = T(kk), *sc = T(scale), *mk = T(mask);
+  if (Q->ndim != 3 || K->ndim != 3 || Q->shape[0] != K->shape[0] || Q->shape[1] != K->shape[1] ||
+      Q->shape[2] != K->shape[2] || sc->len != 1 || mk->ndim != 2 || mk->shape[0] != Q->shape[1] ||
+      mk->shape[1] != Q->shape[1])
+    fail("malus: attn_scores_softmax shape mismatch: q %s, k %s, scale %s, mask %s", shape_str(Q).c_str(),
+         shape_str(K).c_str(), shape_str(sc).c_str(), shape_str(mk).c_str());
+  const size_t bh = Q->shape[0], t = Q->shape[1], hs = Q->shape[2];
+  if (!k::attn_scores_supported(bh, t, hs))
+    fail("malus: attn_scores_softmax: no fused kernel for t=%zu hs=%zu", t, hs);
+  const size_t shape[3] = {bh, t, t};
+  TensorBuffer* out = alloc_tensor(F32, shape, 3);
+  if (!k::attn_scores_softmax(Q->f32(), K->f32(), sc->f32(), mk->f32(), out->f32(), bh, t, hs, causal != 0, stream()))
+    fail("malus: attn_scores_softmax: unaligned operand");
+  return done(out, "attn_scores_softmax");
+  API_CATCH(0)
+}
 int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout) {
   API_TRY
   TensorBuffer *w = T(weight), *idx = T(indices), *d = T(dout);
@@ -691,6 +713,117 @@ int64_t matmul_bwd_b_impl(int64_t ha, int64_t hb, int64_t hd, const TensorBuffer
   // A flattened to [rows, K] (2-D, or 3-D with B broadcast): A^T @ dout[rows, N]
   size_t k = a->shape[a->ndim - 1], rows = a->len / k, n = d->shape[d->ndim - 1];
   return gemm_out(a, d, true, false, 1, (int)k, (int)n, (int)rows, 0, 0, b->shape, b->ndim, D);
+}
+
+// ---- head-folded attention GEMMs (nanogpt_modular.ml:49-60) -----------------
+// The composed attention moves each [B*T, C] projection into heads with
+// reshape(permute(reshape(x @ W, B, T, H, hs), 0, 2, 1, 3), B*H, T, hs) and
+// back with the inverse chain; permute is an exact copy, so these GEMMs read
+// and write the folded layouts in place instead.  Values, and the order of
+// every sum, are those of the composed ops.
+using k::dense_layout;
+using k::GemmLayout;
+using k::GemmLayouts;
+namespace {
+TensorBuffer* T_(int64_t h) { return malus::T(h); }  // T is a sequence length below
+// [B*T, C] matrix stored as [B, H, T, hs] (row m = b T + t, column n = h hs + d)
+GemmLayout heads_as_rows(int T, int H, int hs) {
+  return {{0, 0, 0}, {T, T * H * hs, hs}, {hs, T * hs, 1}};
+}
+// per-head [T, hs] matrices of batch bh = b H + h stored inside [B, T, H, hs]
+GemmLayout rows_as_heads(int T, int H, int hs) {
+  return {{H, T * H * hs, hs}, {0, 0, H * hs}, {0, 0, 1}};
+}
+void check_addend(const TensorBuffer* D, const TensorBuffer* c) {
+  if (D && (D->dtype != F32 || D->len != c->len))
+    fail("malus: fused attention accumulate: addend %s does not match %s", shape_str(D).c_str(), shape_str(c).c_str());
+}
+int64_t mapped(TensorBuffer* a, TensorBuffer* b, TensorBuffer* c, bool ta, bool tb, int batch, int M, int N, int K,
+               const GemmLayouts& L, const TensorBuffer* D, const char* what) {
+  check_addend(D, c);
+  KTimer* kt = ktimer_begin("gemm");
+  if (!k::gemm_mapped(a->f32(), b->f32(), c->f32(), batch, M, N, K, ta, tb, L, stream(), D ? D->f32() : nullptr))
+    fail("malus: %s: head-folded GEMM layout rejected (T %% 32, hs %% 16 and sizes below 2 GiB are required)", what);
+  ktimer_end(kt, 2.0 * batch * (double)M * N * K);
+  return done(c, what);
+}
+}  // namespace
+
+bool heads_foldable(size_t B, size_t T, size_t H, size_t hs) {
+  const size_t n = B * T * H * hs;
+  return T % 32 == 0 && hs % 16 == 0 && B * H <= 65535 && n * 4 < (1ull << 31) && T * T * B * H * 4 < (1ull << 31);
+}
+
+// Qh = heads(x @ W): x [B*T, C], W [C, C] -> [B*H, T, hs]
+int64_t head_proj_fwd(int64_t hx, int64_t hw, size_t B, size_t T, size_t H) {
+  TensorBuffer *x = T_(hx), *w = T_(hw);
+  const size_t C = w->shape[1], hs = C / H, N = B * T;
+  const size_t sh[3] = {B * H, T, hs};
+  TensorBuffer* c = alloc_tensor(F32, sh, 3);
+  GemmLayouts L{dense_layout((long)x->shape[1], 0), dense_layout((long)C, 0), heads_as_rows(T, H, hs),
+                (int)x->len, (int)w->len};
+  return mapped(x, w, c, false, false, 1, (int)N, (int)C, (int)w->shape[0], L, nullptr, "head_proj");
+}
+// dx = unheads(dQh) @ W^T  (+ D)
+int64_t head_proj_bwd_x(int64_t hdq, int64_t hw, size_t B, size_t T, size_t H, const TensorBuffer* D) {
+  TensorBuffer *dq = T_(hdq), *w = T_(hw);
+  const size_t Cin = w->shape[0], C = w->shape[1], hs = C / H, N = B * T;
+  const size_t sh[2] = {N, Cin};
+  TensorBuffer* c = alloc_tensor(F32, sh, 2);
+  GemmLayouts L{heads_as_rows(T, H, hs), dense_layout((long)C, 0), dense_layout((long)Cin, 0), (int)dq->len,
+                (int)w->len};
+  return mapped(dq, w, c, false, true, 1, (int)N, (int)Cin, (int)C, L, D, "head_proj_bwd_x");
+}
+// dW = x^T @ unheads(dQh)  (+ D)
+int64_t head_proj_bwd_w(int64_t hx, int64_t hdq, size_t B, size_t T, size_t H, const TensorBuffer* D) {
+  TensorBuffer *x = T_(hx), *dq = T_(hdq);
+  const size_t Cin = x->shape[1], hs = dq->shape[2], C = H * hs, N = B * T;
+  const size_t sh[2] = {Cin, C};
+  TensorBuffer* c = alloc_tensor(F32, sh, 2);
+  GemmLayouts L{dense_layout((long)Cin, 0), heads_as_rows(T, H, hs), dense_layout((long)C, 0), (int)x->len,
+                (int)dq->len};
+  return mapped(x, dq, c, true, false, 1, (int)Cin, (int)C, (int)N, L, D, "head_proj_bwd_w");
+}
+// att = unheads(P @ V): P [B*H, T, T], V [B*H, T, hs] -> [B*T, H*hs]
+int64_t attn_out_fwd(int64_t hp, int64_t hv, size_t B, size_t T, size_t H) {
+  TensorBuffer *p = T_(hp), *v = T_(hv);
+  const size_t hs = v->shape[2], C = H * hs, N = B * T;
+  const size_t sh[2] = {N, C};
+  TensorBuffer* c = alloc_tensor(F32, sh, 2);
+  GemmLayouts L{dense_layout((long)T, (long)(T * T)), dense_layout((long)hs, (long)(T * hs)), rows_as_heads(T, H, hs),
+                (int)p->len, (int)v->len};
+  return mapped(p, v, c, false, false, (int)(B * H), (int)T, (int)hs, (int)T, L, nullptr, "attn_out");
+}
+// dP = heads(dAtt) @ V^T  (+ D)
+int64_t attn_out_bwd_p(int64_t hda, int64_t hv, size_t B, size_t T, size_t H, const TensorBuffer* D) {
+  TensorBuffer *da = T_(hda), *v = T_(hv);
+  const size_t hs = v->shape[2];
+  const size_t sh[3] = {B * H, T, T};
+  TensorBuffer* c = alloc_tensor(F32, sh, 3);
+  GemmLayouts L{rows_as_heads(T, H, hs), dense_layout((long)hs, (long)(T * hs)), dense_layout((long)T, (long)(T * T)),
+                (int)da->len, (int)v->len};
+  return mapped(da, v, c, false, true, (int)(B * H), (int)T, (int)T, (int)hs, L, D, "attn_out_bwd_p");
+}
+// dV = P^T @ heads(dAtt)  (+ D)
+int64_t attn_out_bwd_v(int64_t hp, int64_t hda, size_t B, size_t T, size_t H, const TensorBuffer* D) {
+  TensorBuffer *p = T_(hp), *da = T_(hda);
+  const size_t hs = da->shape[1] / H;
+  const size_t sh[3] = {B * H, T, hs};
+  TensorBuffer* c = alloc_tensor(F32, sh, 3);
+  GemmLayouts L{dense_layout((long)T, (long)(T * T)), rows_as_heads(T, H, hs), dense_layout((long)hs, (long)(T * hs)),
+                (int)p->len, (int)da->len};
+  return mapped(p, da, c, true, false, (int)(B * H), (int)T, (int)hs, (int)T, L, D, "attn_out_bwd_v");
+}
+// Scores S = Q @ K^T (the permute(K, 0, 2, 1) operand read in place): dQ = dS @ K, dK = dS^T @ Q  (+ D)
+int64_t scores_bwd_q(int64_t hds, int64_t hk, const TensorBuffer* D) {
+  TensorBuffer *ds = T_(hds), *kk = T_(hk);
+  const size_t bh = kk->shape[0], t = kk->shape[1], hs = kk->shape[2];
+  return gemm_out(ds, kk, false, false, (int)bh, (int)t, (int)hs, (int)t, (long)(t * t), (long)(t * hs), kk->shape, 3, D);
+}
+int64_t scores_bwd_k(int64_t hds, int64_t hq, const TensorBuffer* D) {
+  TensorBuffer *ds = T_(hds), *q = T_(hq);
+  const size_t bh = q->shape[0], t = q->shape[1], hs = q->shape[2];
+  return gemm_out(ds, q, true, false, (int)bh, (int)t, (int)hs, (int)t, (long)(t * t), (long)(t * hs), q->shape, 3, D);
 }
 
 extern "C" {

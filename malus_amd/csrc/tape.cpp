@@ -23,6 +23,16 @@ enum OpTag : int32_t {
   ReduceVarAxis = 18, Reshape = 19, Softmax = 20, Layernorm = 21, Gelu = 22, CrossEntropy = 23, Embedding = 24
 };
 
+// Fused nodes the library's own models record (never emitted by the JIT,
+// so outside the reference's numbering).  Each stands for a chain of
+// reference ops whose permutes are exact copies folded into GEMM
+// addressing; its VJP computes the chain's gradients with the same values.
+//   HeadProj (x, W) -> Qh:   reshape(permute(reshape(x @ W, B,T,H,hs), 0,2,1,3), B*H,T,hs)
+//   Scores   (Q, K) -> S:    Q @ permute(K, 0,2,1)
+//   AttnOut  (P, V) -> att:  reshape(permute(reshape(P @ V, B,H,T,hs), 0,2,1,3), B*T,C)
+// meta holds {B, T, H} for HeadProj and AttnOut.
+enum FusedTag : int32_t { HeadProj = 100, Scores = 101, AttnOut = 102 };
+
 enum BwdSlot : int32_t {
   AddBwdA = 0, AddBwdB, SubBwdA, SubBwdB, MulBwdA, MulBwdB, DivBwdA, DivBwdB, SigmoidBwd, ReluBwd, TanhBwd, ExpBwd,
   LogBwd, SqrtBwd, AbsBwd, NegBwd, SumBwd, PermuteNdFwd, ReduceSumAxisBwd, ReduceMeanAxisBwd, ReduceMaxAxisBwd,
@@ -108,7 +118,15 @@ void need_values(int64_t h) {
     fail("malus: backward needs the values of a fused intermediate %s that was never stored", shape_str(t).c_str());
 }
 
-bool binary_op(int32_t op) { return op == Matmul || op == Add || op == Sub || op == Mul || op == Div; }
+bool binary_op(int32_t op) {
+  return op == Matmul || op == Add || op == Sub || op == Mul || op == Div || op == HeadProj || op == Scores ||
+         op == AttnOut;
+}
+
+// grads[x] (+)= the VJP fn computes; with the library's GradAcc the old
+// gradient rides into fn's GEMM epilogue as an addend (same rounding).
+template <class F>
+void fold_grad(std::unordered_map<int64_t, int64_t>& grads, int64_t x, F fn);
 
 // Gradient liveness.  A gradient is computed only where it can reach a leaf
 // the program still holds.  A registered leaf whose only references are the
@@ -160,6 +178,22 @@ void accumulate(std::unordered_map<int64_t, int64_t>& grads, int64_t input, int6
   release(T(old));
   release(T(new_grad));
   it->second = summed;
+}
+
+template <class F>
+void fold_grad(std::unordered_map<int64_t, int64_t>& grads, int64_t x, F fn) {
+  auto it = grads.find(x);
+  if (!slot_is(GradAcc, &malus_std_broadcast_add_fwd)) {  // a JIT-registered GradAcc: call it
+    accumulate(grads, x, fn(nullptr));
+    return;
+  }
+  int64_t g = fn(it == grads.end() ? nullptr : T(it->second));
+  if (it == grads.end()) {
+    grads.emplace(x, g);
+  } else {
+    release(T(it->second));
+    it->second = g;
+  }
 }
 
 // normalize_perm / invert_perm (metal.rs:1275-1325)
@@ -257,6 +291,15 @@ void register_default_backward_fns() { ensure_slots(); }
 
 using namespace malus;
 
+namespace malus {
+void tape_record_fused(int32_t op, int64_t a, int64_t b, int64_t out, const std::vector<int64_t>& meta) {
+  if (!t_recording) return;
+  if (op != HeadProj && op != Scores && op != AttnOut) fail("malus: unknown fused op tag %d", op);
+  retain(T(a)); retain(T(b)); retain(T(out));
+  t_nodes.push_back({op, {a, b}, out, meta});
+}
+}  // namespace malus
+
 extern "C" {
 
 // 1 (default): fold gradient accumulation into the matmul and layernorm VJP
@@ -347,6 +390,7 @@ void tape_record_embedding(int32_t op, int64_t weight, int64_t indices, int64_t 
 }
 
 void tape_register_leaf(int64_t h) { t_leaves.insert(h); }
+
 void tape_pause(void) { t_recording = false; }
 void tape_resume(void) { t_recording = true; }
 
@@ -412,6 +456,24 @@ void backward(int64_t loss) {
         }
         if (na) accumulate(grads, a, slot_fn<Fn3>(MatmulBwdA)(a, b, dout));
         if (nb) accumulate(grads, b, slot_fn<Fn3>(MatmulBwdB)(a, b, dout));
+        break;
+      }
+      case HeadProj: case Scores: case AttnOut: {
+        const int64_t a = n.saved[0], b = n.saved[1];
+        if (na) need_values(b);
+        if (nb) need_values(a);
+        const size_t Bm = n.meta.empty() ? 0 : (size_t)n.meta[0], Tm = n.meta.empty() ? 0 : (size_t)n.meta[1],
+                     Hm = n.meta.empty() ? 0 : (size_t)n.meta[2];
+        if (n.op == HeadProj) {
+          if (na) fold_grad(grads, a, [&](const TensorBuffer* o) { return head_proj_bwd_x(dout, b, Bm, Tm, Hm, o); });
+          if (nb) fold_grad(grads, b, [&](const TensorBuffer* o) { return head_proj_bwd_w(a, dout, Bm, Tm, Hm, o); });
+        } else if (n.op == Scores) {
+          if (na) fold_grad(grads, a, [&](const TensorBuffer* o) { return scores_bwd_q(dout, b, o); });
+          if (nb) fold_grad(grads, b, [&](const TensorBuffer* o) { return scores_bwd_k(dout, a, o); });
+        } else {
+          if (na) fold_grad(grads, a, [&](const TensorBuffer* o) { return attn_out_bwd_p(dout, b, Bm, Tm, Hm, o); });
+          if (nb) fold_grad(grads, b, [&](const TensorBuffer* o) { return attn_out_bwd_v(a, dout, Bm, Tm, Hm, o); });
+        }
         break;
       }
       case Add: case Sub: {

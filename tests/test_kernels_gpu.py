@@ -180,6 +180,45 @@ def test_softmax_fwd_bwd(rt, shape, axis):
     rt.free(hx, hd, hy)
 
 
+@pytest.mark.parametrize("t,hs,causal", [(256, 64, 1), (256, 64, 0), (128, 64, 1), (64, 32, 1), (64, 32, 0),
+                                          (64, 64, 0)])
+def test_attn_scores_softmax_equals_composed_ops(rt, t, hs, causal):
+    # nanogpt_modular.ml:57-61: softmax((Q @ permute(K, 0, 2, 1)) * scale + mask, axis=2).
+    # The fused kernel reproduces the composed ops bit for bit; the causal
+    # form skips the key tiles above the diagonal, whose probabilities are +0.
+    bh = 7
+    q, kk = rand(bh, t, hs, lo=-2, hi=2), rand(bh, t, hs, lo=-2, hi=2)
+    mask = O.causal_mask(t) if causal else rand(t, t, lo=-3, hi=3)
+    sc = np.array([[1.0 / np.sqrt(hs)]], np.float32)
+    hq, hk, hsc, hm = rt.tensor(q), rt.tensor(kk), rt.tensor(sc), rt.tensor(mask)
+    fused = run(rt, rt.L.malus_std_attn_scores_softmax(hq, hk, hsc, hm, causal))
+    hkt = rt.L.tensor_permute(hk, M.sizes([0, 2, 1]), 3)
+    hS = rt.L.tensor_matmul(hq, hkt)
+    hSs = rt.L.malus_std_broadcast_fwd(M.MUL, hS, hsc)
+    hSm = rt.L.malus_std_broadcast_fwd(M.ADD, hSs, hm)
+    composed = run(rt, rt.L.malus_std_softmax_fwd(hSm, 2))
+    assert_bitexact(fused, composed, f"fused scores t={t} hs={hs} causal={causal}")
+    S = O.matmul(q, O.permute(kk, (0, 2, 1)))
+    want = O.softmax(O.broadcast(M.ADD, O.broadcast(M.MUL, S, sc), mask), 2)
+    assert_normwise(fused, want, 1e-5, "fused scores vs oracle")
+    if causal:
+        assert np.all(fused[:, np.triu_indices(t, 1)[0], np.triu_indices(t, 1)[1]] == 0)
+    rt.free(hq, hk, hsc, hm, hkt, hS, hSs, hSm)
+
+
+def test_attn_scores_softmax_rejects_unbuilt_shapes(rt):
+    hq = rt.tensor(rand(2, 48, 16))
+    hsc, hm = rt.tensor(np.ones((1, 1), np.float32)), rt.tensor(O.causal_mask(48))
+    rt.L.malus_set_abort_on_error(0)
+    try:
+        assert rt.L.malus_std_attn_scores_softmax(hq, hq, hsc, hm, 1) == 0
+        assert "no fused kernel" in rt.last_error()
+        rt.L.malus_clear_error()
+    finally:
+        rt.L.malus_set_abort_on_error(1)
+    rt.free(hq, hsc, hm)
+
+
 @pytest.mark.parametrize("shape,axis", [((65, 1024), 1), ((100, 384), 1), ((33, 128), 1), ((4, 70), 1),
                                         ((3, 5000), 1), ((6, 8, 5), 1)])
 def test_layernorm_fwd_bwd(rt, shape, axis):

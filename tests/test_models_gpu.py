@@ -143,13 +143,17 @@ def test_gpt_fused_optimizer_equals_op_by_op(rt):
         np.testing.assert_array_equal(u, v, err_msg=f"param {i}")
 
 
-def test_gpt_fusions_equal_separate_ops(rt):
-    """The forward fusions (scale + mask + softmax in one kernel, residual adds
-    in GEMM epilogues, shape-only intermediates on the tape) and the VJP
-    fusions (gradient accumulation inside the matmul / layernorm VJP kernels)
-    give the same loss, gradients and updated parameters as the separate
-    ops, bit for bit."""
-    cfg = dict(V=65, T=64, C=64, H=4, L=2, B=4)
+@pytest.mark.parametrize("cfg", [dict(V=65, T=64, C=64, H=4, L=2, B=4),     # hs 16: GEMM + fused softmax
+                                 dict(V=65, T=64, C=128, H=4, L=2, B=4),    # hs 32: fused scores kernel
+                                 dict(V=65, T=256, C=128, H=2, L=1, B=2)],  # hs 64, T 256: fused scores kernel
+                         ids=["t64hs16", "t64hs32", "t256hs64"])
+def test_gpt_fusions_equal_separate_ops(rt, cfg):
+    """The forward fusions (attention scores + scale + mask + softmax in one
+    kernel where the head size allows it, else scale + mask + softmax in one
+    kernel; residual adds in GEMM epilogues; shape-only intermediates on the
+    tape) and the VJP fusions (gradient accumulation inside the matmul /
+    layernorm VJP kernels) give the same loss, gradients and updated
+    parameters as the separate ops, bit for bit."""
     x, y = tokens(cfg, 6000)
     out = []
     for fa in (True, False):
