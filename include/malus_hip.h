@@ -156,6 +156,11 @@ void malus_gemm_set_dma(int on);
  * model's fused forward uses for nanogpt_modular.ml:57-61.  causal != 0
  * promises the -1e9-above-the-diagonal mask of tensor_causal_mask. */
 int64_t malus_std_attn_scores_softmax(int64_t q, int64_t k, int64_t scale, int64_t mask, int32_t causal);
+/* Its VJP fused with the score products' gradient input:
+ * softmax_bwd(p, dout @ v^T, axis=2) * scale for dout, v [bh, t, hs], p [bh, t, t]
+ * (the kernel the fused attention backward uses; transformer_bwd.ml:15-20 then the
+ * scale multiply's VJP). */
+int64_t malus_std_attn_scores_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, int32_t causal);
 int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
 int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
 void malus_set_abort_on_error(int on);

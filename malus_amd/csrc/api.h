@@ -21,9 +21,10 @@ void set_last_error(const char* msg);
 void tape_on_release(int64_t handle);
 void register_default_backward_fns();
 std::vector<size_t> tape_normalize_perm(const std::vector<size_t>& raw, size_t rank);
-// Record a fused node (tags 100 HeadProj, 101 Scores, 102 AttnOut; see
-// tape.cpp) with inputs a, b and output out; retains all three.
-void tape_record_fused(int32_t op, int64_t a, int64_t b, int64_t out, const std::vector<int64_t>& meta);
+// Record a fused node (tags 100 HeadProj, 101 Scores, 102 AttnOut,
+// 103 Attention; see tape.cpp) with its saved handles and output; retains
+// them all.
+void tape_record_fused(int32_t op, const std::vector<int64_t>& saved, int64_t out, const std::vector<int64_t>& meta);
 
 }  // namespace malus
 
@@ -45,6 +46,7 @@ int64_t head_proj_bwd_w(int64_t x, int64_t dqh, size_t B, size_t T, size_t H, co
 int64_t attn_out_fwd(int64_t p, int64_t v, size_t B, size_t T, size_t H);
 int64_t attn_out_bwd_p(int64_t datt, int64_t v, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
 int64_t attn_out_bwd_v(int64_t p, int64_t datt, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
+int64_t attn_scores_bwd_impl(int64_t datt, int64_t v, int64_t p, int64_t scale, size_t B, size_t T, size_t H);
 int64_t scores_bwd_q(int64_t ds, int64_t k, const malus::TensorBuffer* D);
 int64_t scores_bwd_k(int64_t ds, int64_t q, const malus::TensorBuffer* D);
 

@@ -139,11 +139,18 @@ void scale_mask_softmax(const float* S, const float* scale, const float* mask, f
 // Q, K: [bh, t, hs], mask: [t, t], P: [bh, t, t]; the same values as
 // gemm(Q, K^T) followed by scale_mask_softmax.  causal: the mask is
 // -1e9 above the diagonal and 0 elsewhere (key tiles wholly above a row
-// block are skipped).  Returns false (nothing launched) for shapes the
-// kernel is not built for.
+// block are skipped, and the mask is applied arithmetically: mask may be
+// null).  Returns false (nothing launched) for shapes the kernel is not
+// built for.
 bool attn_scores_supported(size_t bh, size_t t, size_t hs);
 bool attn_scores_softmax(const float* Q, const float* K, const float* scale, const float* mask, float* P, size_t bh,
                          size_t t, size_t hs, bool causal, hipStream_t s);
+// dS = softmax_bwd(P, dO @ V^T) * scale[0] per head (P, dS: [bh, t, t];
+// V: [bh, t, hs]); dO of head b is read at dO + (b / heads) * t * ldo +
+// (b % heads) * hs with row stride ldo (ldo = hs, heads = 1: dense
+// [bh, t, hs]).  Same values as gemm + softmax_bwd + the scalar multiply.
+bool attn_scores_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const float* P, const float* scale,
+                     float* dS, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s);
 // Sum over the axis of x * y (y has x's layout); each product rounded to f32.
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 // Broadcast [outer, inner] back to [outer, axis, inner] (expand_axis).

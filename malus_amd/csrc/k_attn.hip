@@ -188,6 +188,140 @@ void launch(const float* Q, const float* K, const float* scale, const float* mas
   else k_attn_scores_softmax<TT, HS, false><<<grid, 256, 0, s>>>(Q, K, scale, mask, P);
 }
 
+// Backward of the scores: dS = softmax_bwd(P, dP) * scale with dP = dO V^T,
+// for tape.rs:1150-1161 (dx = s * (dout - sum(dout * s))) followed by the
+// scale multiply's VJP (dout * scale).  The wave layout is the forward
+// kernel's (lane = query row, registers = keys), so dP^T = V dO^T runs on
+// MFMA with V staged in LDS, the row sum is one cross-lane step, and dP never
+// reaches memory.  Bit-identical to gemm(dO, V^T), softmax_bwd and the
+// scalar multiply: the same MFMA k pairing, per-group products summed from 0
+// in key order, the row kernel's xor tree, and the same f32 operations.
+// Causal: key tiles above a wave's rows hold P = 0, so their dS is 0 (the
+// composed ops give +-0 there) and neither dP nor P is read for them.
+// dO of head bh, row i, column d sits at dO + (bh / H) * T * ldo + (bh % H) * HS + i * ldo + d
+// (ldo = H * HS: the [B*T, C] attention output read in place).
+template <int TT, int HS, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void k_attn_scores_bwd(const float* __restrict__ dO, int ldo, int H,
+                                                           const float* __restrict__ V, const float* __restrict__ P,
+                                                           const float* __restrict__ scale, float* __restrict__ dS) {
+  constexpr int NT = TT / 32;
+  constexpr int NKB = HS / 16;
+  constexpr int LD = HS + 4;
+  __shared__ __attribute__((aligned(16))) float Vs[TT * LD];
+  const int bh = blockIdx.y;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const size_t head = (size_t)bh * TT * HS;
+
+  const int pair = 2 * blockIdx.x + (wave >> 1);
+  const int qt = (wave & 1) ? NT - 1 - pair : pair;
+  const bool idle = pair >= (NT + 1) / 2 || ((wave & 1) && qt == pair);
+  const int i0 = 32 * (idle ? 0 : qt);
+  const int x = lane & 31, lk = lane >> 5;
+  const int live = CAUSAL ? qt + 1 : NT;
+
+  // B operand: dO[i0 + x][16 kb + 8 lk + s]
+  const v4f* op = reinterpret_cast<const v4f*>(dO + (size_t)(bh / H) * TT * ldo + (size_t)(bh % H) * HS +
+                                               (size_t)(i0 + x) * ldo + 8 * lk);
+  v4f ov[2 * NKB];
+#pragma unroll
+  for (int e = 0; e < 2 * NKB; ++e) ov[e] = op[4 * (e >> 1) + (e & 1)];
+  {
+    constexpr int N4 = TT * HS / 4, PER = (N4 + 255) / 256;
+    const v4f* src = reinterpret_cast<const v4f*>(V + head);
+    v4f tmp[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int f = threadIdx.x + 256 * u;
+      if (f < N4) tmp[u] = src[f];
+    }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int f = threadIdx.x + 256 * u;
+      if (f < N4) *reinterpret_cast<v4f*>(Vs + (f / (HS / 4)) * LD + 4 * (f % (HS / 4))) = tmp[u];
+    }
+  }
+  __syncthreads();
+  if (idle) return;  // no barrier follows
+
+  v16f acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    acc[t] = v16f{0};
+    if (t < live) {
+      const float* vr = Vs + (32 * t + x) * LD + 8 * lk;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const v4f a = *reinterpret_cast<const v4f*>(vr + 16 * kb);
+        const v4f b = *reinterpret_cast<const v4f*>(vr + 16 * kb + 4);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], ov[2 * kb][s], acc[t], 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[s], ov[2 * kb + 1][s], acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // per-group sums of dP * P, then the row kernel's tree
+  const int i = i0 + x;
+  const v4f* prow = reinterpret_cast<const v4f*>(P + ((size_t)bh * TT + i) * TT);
+  float v[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float sum = 0.0f;
+      if (t < live) {
+        const v4f pv = prow[8 * t + 2 * g + lk];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float pr = acc[t][4 * g + c] * pv[c];
+          sum += pr;
+        }
+      }
+      v[t][g] = sum;
+    }
+#pragma unroll
+  for (int tb = NT / 2; tb >= 1; tb >>= 1)
+#pragma unroll
+    for (int t = 0; t < tb; ++t)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) v[t][g] = v[t][g] + v[t + tb][g];
+  float d = 0.0f;
+  {
+    const float d0 = v[0][0] + v[0][2], d1 = v[0][1] + v[0][3];
+    d = d0 + d1;
+  }
+  d = d + __shfl_xor(d, 32, 64);
+
+  const float sc = scale[0];
+  v4f* srow = reinterpret_cast<v4f*>(dS + ((size_t)bh * TT + i) * TT);
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      if (t < live) {
+        const v4f pv = prow[8 * t + 2 * g + lk];  // second read of the row (cache): dP stays in registers
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float diff = acc[t][4 * g + c] - d;
+          const float dx = pv[c] * diff;
+          o[c] = dx * sc;
+        }
+      }
+      srow[8 * t + 2 * g + lk] = o;
+    }
+}
+
+template <int TT, int HS>
+void launch_bwd(const float* dO, int ldo, int H, const float* V, const float* P, const float* scale, float* dS, int bh,
+                bool causal, hipStream_t s) {
+  const dim3 grid((TT / 32 + 3) / 4, (unsigned)bh);
+  if (causal) k_attn_scores_bwd<TT, HS, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS);
+  else k_attn_scores_bwd<TT, HS, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS);
+}
+
 }  // namespace
 
 bool attn_scores_supported(size_t bh, size_t t, size_t hs) {
@@ -199,12 +333,27 @@ bool attn_scores_softmax(const float* Q, const float* K, const float* scale, con
                          size_t t, size_t hs, bool causal, hipStream_t s) {
   if (!attn_scores_supported(bh, t, hs)) return false;
   const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  if (!aligned(Q) || !aligned(K) || !aligned(mask) || !aligned(P)) return false;
+  if (!aligned(Q) || !aligned(K) || !aligned(mask) || !aligned(P) || (!causal && !mask)) return false;
   const int b = (int)bh;
   if (t == 256 && hs == 64) launch<256, 64>(Q, K, scale, mask, P, b, causal, s);
   else if (t == 128 && hs == 64) launch<128, 64>(Q, K, scale, mask, P, b, causal, s);
   else if (t == 64 && hs == 32) launch<64, 32>(Q, K, scale, mask, P, b, causal, s);
   else if (t == 64 && hs == 64) launch<64, 64>(Q, K, scale, mask, P, b, causal, s);
+  else return false;
+  MALUS_HIP(hipGetLastError());
+  return true;
+}
+
+bool attn_scores_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const float* P, const float* scale,
+                     float* dS, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s) {
+  if (!attn_scores_supported(bh, t, hs) || heads == 0 || bh % heads || ldo < hs * heads) return false;
+  const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (!aligned(dO) || !aligned(V) || !aligned(P) || !aligned(dS) || ldo % 4) return false;
+  const int b = (int)bh, l = (int)ldo, H = (int)heads;
+  if (t == 256 && hs == 64) launch_bwd<256, 64>(dO, l, H, V, P, scale, dS, b, causal, s);
+  else if (t == 128 && hs == 64) launch_bwd<128, 64>(dO, l, H, V, P, scale, dS, b, causal, s);
+  else if (t == 64 && hs == 32) launch_bwd<64, 32>(dO, l, H, V, P, scale, dS, b, causal, s);
+  else if (t == 64 && hs == 64) launch_bwd<64, 64>(dO, l, H, V, P, scale, dS, b, causal, s);
   else return false;
   MALUS_HIP(hipGetLastError());
   return true;

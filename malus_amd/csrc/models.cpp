@@ -44,7 +44,7 @@ namespace {
 enum Op : int32_t {
   OP_MATMUL = 0, OP_ADD = 1, OP_SUB = 2, OP_MUL = 3, OP_DIV = 4, OP_TRANSPOSE = 13, OP_RESHAPE = 19, OP_SOFTMAX = 20,
   OP_LAYERNORM = 21, OP_GELU = 22, OP_CE = 23, OP_EMBEDDING = 24,
-  TAG_HEAD_PROJ = 100, TAG_SCORES = 101, TAG_ATTN_OUT = 102  // fused nodes (tape.cpp)
+  TAG_HEAD_PROJ = 100, TAG_SCORES = 101, TAG_ATTN_OUT = 102, TAG_ATTENTION = 103  // fused nodes (tape.cpp)
 };
 
 // grad-tracked binop: lower + tape_record_binop (codegen-cpu/lib.rs:1531-1552)
@@ -117,7 +117,7 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   auto head_fold = [&](int64_t w) {
     if (fused_heads) {
       int64_t Qh = head_proj_fwd(xn1, w, B, Tn, H);
-      tape_record_fused(TAG_HEAD_PROJ, xn1, w, Qh, {(int64_t)B, (int64_t)Tn, (int64_t)H});
+      tape_record_fused(TAG_HEAD_PROJ, {xn1, w}, Qh, {(int64_t)B, (int64_t)Tn, (int64_t)H});
       return Qh;
     }
     int64_t q = binop(OP_MATMUL, xn1, w);
@@ -137,69 +137,65 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   tensor_release(ones11);
   tape_register_leaf(scale);  // variable(...)
   const size_t sshape[3] = {B * H, Tn, Tn};
-  // Fused scores: S = Q @ Kt stays in registers (its tape node gets a
-  // shape-only handle).  Only the VJP of the scale leaf would read S, and
-  // that leaf is released with the rest of this block's temporaries, so the
-  // backward pass never computes it.
-  const bool fused_scores = fused_heads && k::attn_scores_supported(B * H, Tn, hs);
-  int64_t S;
-  if (fused_scores) {
-    S = malus::H(alloc_virtual(F32, sshape, 3));
-    tape_record_fused(TAG_SCORES, Q, K, S, {});
-  } else if (fused_heads) {  // S = Q @ K^T with K read in place
-    TensorBuffer* st = alloc_tensor(F32, sshape, 3);
-    KTimer* kt = ktimer_begin("gemm");
-    k::gemm(T(Q)->f32(), T(K)->f32(), st->f32(), (int)(B * H), (int)Tn, (int)Tn, (int)hs, false, true,
-            (long)(Tn * hs), (long)(Tn * hs), (long)(Tn * Tn), stream());
-    ktimer_end(kt, 2.0 * B * H * Tn * Tn * hs);
-    st->write_seq = enqueue_mark("matmul");
-    S = malus::H(st);
-    tape_record_fused(TAG_SCORES, Q, K, S, {});
-  } else {
-    S = binop(OP_MATMUL, Q, Kt);
-  }
-  int64_t mask = tensor_causal_mask((int64_t)Tn);
-  tape_register_leaf(mask);  // variable(mask)
-  int64_t Ss, Sm, Pm;
-  if (fused_scores) {
-    Ss = malus::H(alloc_virtual(F32, sshape, 3));
-    Sm = malus::H(alloc_virtual(F32, sshape, 3));
+  int64_t S = 0, mask = 0, Ss = 0, Sm = 0, Pm = 0, AO = 0, ao4 = 0, aop = 0, att;
+  if (fused_heads && k::attn_scores_supported(B * H, Tn, hs)) {
+    // Fused causal attention: S = Q @ K^T, scale, causal mask and softmax in
+    // one kernel (P stored), att = P @ V written straight into [B*T, C], and
+    // one tape node whose VJP runs the fused scores backward.  The causal
+    // mask is computed in the kernels, so its tensor is not built; the scale
+    // and mask leaves of the composed form are released before backward and
+    // never receive gradients.
     TensorBuffer* p = alloc_tensor(F32, sshape, 3);
-    if (!k::attn_scores_softmax(T(Q)->f32(), T(K)->f32(), T(scale)->f32(), T(mask)->f32(), p->f32(), B * H, Tn, hs,
+    if (!k::attn_scores_softmax(T(Q)->f32(), T(K)->f32(), T(scale)->f32(), nullptr, p->f32(), B * H, Tn, hs,
                                 /*causal=*/true, stream()))
       fail("malus: fused attention scores rejected a supported shape");
     p->write_seq = enqueue_mark("attn_scores_softmax");
     Pm = malus::H(p);
-    tape_record_binop(OP_MUL, S, scale, Ss);
-    tape_record_binop(OP_ADD, Ss, mask, Sm);
-  } else if (g.fused_fwd) {
-    // scores * scale + mask -> softmax in one pass.  The tape gets the same
-    // three records; the two intermediates are shape-only handles because
-    // no VJP reads their values (add: shapes; mul: S and scale; softmax: P).
-    TensorBuffer* st = T(S);
-    Ss = malus::H(alloc_virtual(F32, st->shape, st->ndim));
-    Sm = malus::H(alloc_virtual(F32, st->shape, st->ndim));
-    TensorBuffer* p = alloc_tensor(F32, st->shape, st->ndim);
-    k::scale_mask_softmax(st->f32(), T(scale)->f32(), T(mask)->f32(), p->f32(), st->len / Tn, Tn, Tn, stream());
-    p->write_seq = enqueue_mark("scale_mask_softmax");
-    Pm = malus::H(p);
-    tape_record_binop(OP_MUL, S, scale, Ss);
-    tape_record_binop(OP_ADD, Ss, mask, Sm);
-  } else {
-    Ss = binop(OP_MUL, S, scale);
-    Sm = binop(OP_ADD, Ss, mask);
-    Pm = malus_std_softmax_fwd(Sm, 2);
-  }
-  tape_record_reduce(OP_SOFTMAX, Sm, Pm, 2, 0);
-  int64_t AO = 0, ao4 = 0, aop = 0, att;
-  if (fused_heads) {
     att = attn_out_fwd(Pm, Vv, B, Tn, H);
-    tape_record_fused(TAG_ATTN_OUT, Pm, Vv, att, {(int64_t)B, (int64_t)Tn, (int64_t)H});
+    tape_record_fused(TAG_ATTENTION, {Q, K, Vv, Pm, scale}, att, {(int64_t)B, (int64_t)Tn, (int64_t)H});
   } else {
-    AO = binop(OP_MATMUL, Pm, Vv);
-    ao4 = reshape(AO, {B, H, Tn, hs});
-    aop = permute(ao4, {0, 2, 1, 3});
-    att = reshape(aop, {N, C});
+    if (fused_heads) {  // S = Q @ K^T with K read in place
+      TensorBuffer* st = alloc_tensor(F32, sshape, 3);
+      KTimer* kt = ktimer_begin("gemm");
+      k::gemm(T(Q)->f32(), T(K)->f32(), st->f32(), (int)(B * H), (int)Tn, (int)Tn, (int)hs, false, true,
+              (long)(Tn * hs), (long)(Tn * hs), (long)(Tn * Tn), stream());
+      ktimer_end(kt, 2.0 * B * H * Tn * Tn * hs);
+      st->write_seq = enqueue_mark("matmul");
+      S = malus::H(st);
+      tape_record_fused(TAG_SCORES, {Q, K}, S, {});
+    } else {
+      S = binop(OP_MATMUL, Q, Kt);
+    }
+    mask = tensor_causal_mask((int64_t)Tn);
+    tape_register_leaf(mask);  // variable(mask)
+    if (g.fused_fwd) {
+      // scores * scale + mask -> softmax in one pass.  The tape gets the same
+      // three records; the two intermediates are shape-only handles because
+      // no VJP reads their values (add: shapes; mul: S and scale; softmax: P).
+      TensorBuffer* st = T(S);
+      Ss = malus::H(alloc_virtual(F32, st->shape, st->ndim));
+      Sm = malus::H(alloc_virtual(F32, st->shape, st->ndim));
+      TensorBuffer* p = alloc_tensor(F32, st->shape, st->ndim);
+      k::scale_mask_softmax(st->f32(), T(scale)->f32(), T(mask)->f32(), p->f32(), st->len / Tn, Tn, Tn, stream());
+      p->write_seq = enqueue_mark("scale_mask_softmax");
+      Pm = malus::H(p);
+      tape_record_binop(OP_MUL, S, scale, Ss);
+      tape_record_binop(OP_ADD, Ss, mask, Sm);
+    } else {
+      Ss = binop(OP_MUL, S, scale);
+      Sm = binop(OP_ADD, Ss, mask);
+      Pm = malus_std_softmax_fwd(Sm, 2);
+    }
+    tape_record_reduce(OP_SOFTMAX, Sm, Pm, 2, 0);
+    if (fused_heads) {
+      att = attn_out_fwd(Pm, Vv, B, Tn, H);
+      tape_record_fused(TAG_ATTN_OUT, {Pm, Vv}, att, {(int64_t)B, (int64_t)Tn, (int64_t)H});
+    } else {
+      AO = binop(OP_MATMUL, Pm, Vv);
+      ao4 = reshape(AO, {B, H, Tn, hs});
+      aop = permute(ao4, {0, 2, 1, 3});
+      att = reshape(aop, {N, C});
+    }
   }
   int64_t proj, x2;
   if (g.fused_fwd) residual_matmul(x, att, P[4], &proj, &x2);

@@ -624,6 +624,25 @@ int64_t malus_std_attn_scores_softmax(int64_t q, int64_t kk, int64_t scale, int6
   return done(out, "attn_scores_softmax");
   API_CATCH(0)
 }
+// VJP of the fused scores for dout = d(attn) [bh, t, hs]-shaped heads:
+// softmax_bwd(p, dout @ permute(v, 0, 2, 1), axis=2) * scale.
+int64_t malus_std_attn_scores_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, int32_t causal) {
+  API_TRY
+  TensorBuffer *d = T(dout), *V = T(v), *Pt = T(p), *sc = T(scale);
+  if (d->ndim != 3 || V->ndim != 3 || Pt->ndim != 3 || d->shape[0] != V->shape[0] || d->shape[1] != V->shape[1] ||
+      d->shape[2] != V->shape[2] || Pt->shape[0] != d->shape[0] || Pt->shape[1] != d->shape[1] ||
+      Pt->shape[2] != d->shape[1] || sc->len != 1)
+    fail("malus: attn_scores_bwd shape mismatch: dout %s, v %s, p %s, scale %s", shape_str(d).c_str(),
+         shape_str(V).c_str(), shape_str(Pt).c_str(), shape_str(sc).c_str());
+  const size_t bh = d->shape[0], t = d->shape[1], hs = d->shape[2];
+  if (!k::attn_scores_supported(bh, t, hs)) fail("malus: attn_scores_bwd: no fused kernel for t=%zu hs=%zu", t, hs);
+  const size_t shape[3] = {bh, t, t};
+  TensorBuffer* out = alloc_tensor(F32, shape, 3);
+  if (!k::attn_scores_bwd(d->f32(), hs, 1, V->f32(), Pt->f32(), sc->f32(), out->f32(), bh, t, hs, causal != 0, stream()))
+    fail("malus: attn_scores_bwd: unaligned operand");
+  return done(out, "attn_scores_bwd");
+  API_CATCH(0)
+}
 int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout) {
   API_TRY
   TensorBuffer *w = T(weight), *idx = T(indices), *d = T(dout);
@@ -813,6 +832,16 @@ int64_t attn_out_bwd_v(int64_t hp, int64_t hda, size_t B, size_t T, size_t H, co
   GemmLayouts L{dense_layout((long)T, (long)(T * T)), rows_as_heads(T, H, hs), dense_layout((long)hs, (long)(T * hs)),
                 (int)p->len, (int)da->len};
   return mapped(p, da, c, true, false, (int)(B * H), (int)T, (int)hs, (int)T, L, D, "attn_out_bwd_v");
+}
+// dS of the fused causal attention: softmax_bwd(P, heads(dAtt) @ V^T) * scale
+int64_t attn_scores_bwd_impl(int64_t hda, int64_t hv, int64_t hp, int64_t hscale, size_t B, size_t T, size_t H) {
+  TensorBuffer *da = T_(hda), *v = T_(hv), *p = T_(hp), *sc = T_(hscale);
+  const size_t hs = v->shape[2], bh = B * H;
+  const size_t sh[3] = {bh, T, T};
+  TensorBuffer* out = alloc_tensor(F32, sh, 3);
+  if (!k::attn_scores_bwd(da->f32(), H * hs, H, v->f32(), p->f32(), sc->f32(), out->f32(), bh, T, hs, true, stream()))
+    fail("malus: attn_scores_bwd: no fused kernel for t=%zu hs=%zu", T, hs);
+  return done(out, "attn_scores_bwd");
 }
 // Scores S = Q @ K^T (the permute(K, 0, 2, 1) operand read in place): dQ = dS @ K, dK = dS^T @ Q  (+ D)
 int64_t scores_bwd_q(int64_t hds, int64_t hk, const TensorBuffer* D) {

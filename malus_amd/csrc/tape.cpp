@@ -30,8 +30,11 @@ enum OpTag : int32_t {
 //   HeadProj (x, W) -> Qh:   reshape(permute(reshape(x @ W, B,T,H,hs), 0,2,1,3), B*H,T,hs)
 //   Scores   (Q, K) -> S:    Q @ permute(K, 0,2,1)
 //   AttnOut  (P, V) -> att:  reshape(permute(reshape(P @ V, B,H,T,hs), 0,2,1,3), B*T,C)
-// meta holds {B, T, H} for HeadProj and AttnOut.
-enum FusedTag : int32_t { HeadProj = 100, Scores = 101, AttnOut = 102 };
+//   Attention (Q, K, V; P, scale) -> att: AttnOut(softmax(Scores(Q, K) * scale + causal mask), V),
+//            with P the saved probabilities; the per-forward scale and mask
+//            leaves are released before backward, so no gradient reaches them
+// meta holds {B, T, H} for HeadProj, AttnOut and Attention.
+enum FusedTag : int32_t { HeadProj = 100, Scores = 101, AttnOut = 102, Attention = 103 };
 
 enum BwdSlot : int32_t {
   AddBwdA = 0, AddBwdB, SubBwdA, SubBwdB, MulBwdA, MulBwdB, DivBwdA, DivBwdB, SigmoidBwd, ReluBwd, TanhBwd, ExpBwd,
@@ -118,9 +121,13 @@ void need_values(int64_t h) {
     fail("malus: backward needs the values of a fused intermediate %s that was never stored", shape_str(t).c_str());
 }
 
-bool binary_op(int32_t op) {
-  return op == Matmul || op == Add || op == Sub || op == Mul || op == Div || op == HeadProj || op == Scores ||
-         op == AttnOut;
+// Number of leading saved handles that are differentiable inputs.
+int diff_inputs(int32_t op) {
+  if (op == Attention) return 3;
+  if (op == Matmul || op == Add || op == Sub || op == Mul || op == Div || op == HeadProj || op == Scores ||
+      op == AttnOut)
+    return 2;
+  return 1;
 }
 
 // grads[x] (+)= the VJP fn computes; with the library's GradAcc the old
@@ -146,8 +153,8 @@ struct GradLiveness {
       ++refs[n.output];
     }
     for (const TapeNode& n : nodes) {  // recording order: inputs precede the nodes that consume them
-      bool any = (*this)(n.saved[0]);
-      if (binary_op(n.op)) any = (*this)(n.saved[1]) || any;
+      bool any = false;
+      for (int i = 0; i < diff_inputs(n.op); ++i) any = (*this)(n.saved[i]) || any;
       bool& o = need[n.output];
       o = o || any || live_leaf(n.output);
     }
@@ -292,11 +299,14 @@ void register_default_backward_fns() { ensure_slots(); }
 using namespace malus;
 
 namespace malus {
-void tape_record_fused(int32_t op, int64_t a, int64_t b, int64_t out, const std::vector<int64_t>& meta) {
+void tape_record_fused(int32_t op, const std::vector<int64_t>& saved, int64_t out, const std::vector<int64_t>& meta) {
   if (!t_recording) return;
-  if (op != HeadProj && op != Scores && op != AttnOut) fail("malus: unknown fused op tag %d", op);
-  retain(T(a)); retain(T(b)); retain(T(out));
-  t_nodes.push_back({op, {a, b}, out, meta});
+  const size_t want = op == Attention ? 5 : 2;
+  if (op < HeadProj || op > Attention) fail("malus: unknown fused op tag %d", op);
+  if (saved.size() != want) fail("malus: fused op %d takes %zu saved handles, got %zu", op, want, saved.size());
+  for (int64_t h : saved) retain(T(h));
+  retain(T(out));
+  t_nodes.push_back({op, saved, out, meta});
 }
 }  // namespace malus
 
@@ -441,9 +451,11 @@ void backward(int64_t loss) {
     auto g = grads.find(n.output);
     if (g == grads.end()) continue;
     const int64_t dout = g->second;
+    const int ni = diff_inputs(n.op);
     const bool na = need(n.saved[0]);
-    const bool nb = binary_op(n.op) && need(n.saved[1]);
-    if (!na && !nb) continue;
+    const bool nb = ni > 1 && need(n.saved[1]);
+    const bool nc = ni > 2 && need(n.saved[2]);
+    if (!na && !nb && !nc) continue;
     switch (n.op) {
       case Matmul: {
         int64_t a = n.saved[0], b = n.saved[1];
@@ -456,6 +468,20 @@ void backward(int64_t loss) {
         }
         if (na) accumulate(grads, a, slot_fn<Fn3>(MatmulBwdA)(a, b, dout));
         if (nb) accumulate(grads, b, slot_fn<Fn3>(MatmulBwdB)(a, b, dout));
+        break;
+      }
+      case Attention: {  // saved {Q, K, V, P, scale}
+        const int64_t q = n.saved[0], kk = n.saved[1], v = n.saved[2], pr = n.saved[3], sc = n.saved[4];
+        const size_t Bm = (size_t)n.meta[0], Tm = (size_t)n.meta[1], Hm = (size_t)n.meta[2];
+        for (int64_t h : n.saved) need_values(h);
+        // AttnOut's VJP (dP, dV), the softmax and scale VJPs, then Scores' (dQ, dK)
+        if (nc) fold_grad(grads, v, [&](const TensorBuffer* o) { return attn_out_bwd_v(pr, dout, Bm, Tm, Hm, o); });
+        if (na || nb) {
+          const int64_t ds = attn_scores_bwd_impl(dout, v, pr, sc, Bm, Tm, Hm);
+          if (na) fold_grad(grads, q, [&](const TensorBuffer* o) { return scores_bwd_q(ds, kk, o); });
+          if (nb) fold_grad(grads, kk, [&](const TensorBuffer* o) { return scores_bwd_k(ds, q, o); });
+          release(T(ds));
+        }
         break;
       }
       case HeadProj: case Scores: case AttnOut: {

@@ -206,6 +206,34 @@ def test_attn_scores_softmax_equals_composed_ops(rt, t, hs, causal):
     rt.free(hq, hk, hsc, hm, hkt, hS, hSs, hSm)
 
 
+@pytest.mark.parametrize("t,hs,causal", [(256, 64, 1), (256, 64, 0), (128, 64, 1), (64, 32, 1), (64, 64, 0)])
+def test_attn_scores_bwd_equals_composed_ops(rt, t, hs, causal):
+    # softmax VJP (transformer_bwd.ml:15-20) of dP = dout @ permute(V, 0, 2, 1),
+    # then the scale multiply's VJP (dout * scale): the fused kernel gives the
+    # composed ops' values (the causal form stores +0 above the diagonal,
+    # where the composed product P * (dP - sum) is +-0)
+    bh = 5
+    q, kk, v = (rand(bh, t, hs, lo=-2, hi=2) for _ in range(3))
+    d = rand(bh, t, hs)
+    mask = O.causal_mask(t) if causal else rand(t, t, lo=-3, hi=3)
+    sc = np.array([[1.0 / np.sqrt(hs)]], np.float32)
+    hq, hk, hv, hd, hsc, hm = (rt.tensor(a) for a in (q, kk, v, d, sc, mask))
+    hp = rt.L.malus_std_attn_scores_softmax(hq, hk, hsc, hm, causal)
+    fused = run(rt, rt.L.malus_std_attn_scores_bwd(hd, hv, hp, hsc, causal))
+    hvt = rt.L.tensor_permute(hv, M.sizes([0, 2, 1]), 3)
+    hdp = rt.L.tensor_matmul(hd, hvt)
+    hdx = rt.L.malus_std_softmax_bwd(hp, hdp, 2)
+    composed = run(rt, rt.L.malus_std_broadcast_fwd(M.MUL, hdx, hsc))
+    assert np.array_equal(fused, composed), f"fused scores bwd t={t} hs={hs} causal={causal}"
+    if not causal:
+        assert_bitexact(fused, composed, "fused scores bwd")
+    p = rt.numpy(hp)
+    dp = O.matmul(d, O.permute(v, (0, 2, 1)))
+    want = O.broadcast(M.MUL, O.softmax_bwd(p, dp, 2), sc)
+    assert_normwise(fused, want, 1e-5, "fused scores bwd vs oracle")
+    rt.free(hq, hk, hv, hd, hsc, hm, hp, hvt, hdp, hdx)
+
+
 def test_attn_scores_softmax_rejects_unbuilt_shapes(rt):
     hq = rt.tensor(rand(2, 48, 16))
     hsc, hm = rt.tensor(np.ones((1, 1), np.float32)), rt.tensor(O.causal_mask(48))
