@@ -43,12 +43,15 @@ bool heads_foldable(size_t B, size_t T, size_t H, size_t hs);
 int64_t head_proj_fwd(int64_t x, int64_t w, size_t B, size_t T, size_t H);
 int64_t head_proj_bwd_x(int64_t dqh, int64_t w, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
 int64_t head_proj_bwd_w(int64_t x, int64_t dqh, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
-int64_t attn_out_fwd(int64_t p, int64_t v, size_t B, size_t T, size_t H);
+// causal: P (and dS) are lower-triangular with exact zeros above the
+// diagonal, so the GEMMs skip those k slabs (same values).
+int64_t attn_out_fwd(int64_t p, int64_t v, size_t B, size_t T, size_t H, bool causal);
 int64_t attn_out_bwd_p(int64_t datt, int64_t v, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
-int64_t attn_out_bwd_v(int64_t p, int64_t datt, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
+int64_t attn_out_bwd_v(int64_t p, int64_t datt, size_t B, size_t T, size_t H, const malus::TensorBuffer* D,
+                       bool causal);
 int64_t attn_scores_bwd_impl(int64_t datt, int64_t v, int64_t p, int64_t scale, size_t B, size_t T, size_t H);
-int64_t scores_bwd_q(int64_t ds, int64_t k, const malus::TensorBuffer* D);
-int64_t scores_bwd_k(int64_t ds, int64_t q, const malus::TensorBuffer* D);
+int64_t scores_bwd_q(int64_t ds, int64_t k, const malus::TensorBuffer* D, bool causal);
+int64_t scores_bwd_k(int64_t ds, int64_t q, const malus::TensorBuffer* D, bool causal);
 
 #define API_TRY try {
 #define API_CATCH(...)                                   \

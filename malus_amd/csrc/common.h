@@ -188,7 +188,11 @@ void permute(const float* x, float* out, int ndim, const size_t* in_shape, const
 struct GemmMap { int div, s1, s0; };
 struct GemmLayout { GemmMap b, r, c; };
 // ext_a / ext_b: floats addressable past A / B (the whole allocation).
-struct GemmLayouts { GemmLayout a, b, c; int ext_a, ext_b; };
+// tri_a: every stored A matrix is square and lower-triangular, with exact
+// zeros above the diagonal (causal attention probabilities and their
+// gradients); a tile then skips the k slabs whose A values are all zero,
+// which leaves every sum's value unchanged.
+struct GemmLayouts { GemmLayout a, b, c; int ext_a, ext_b; int tri_a = 0; };
 inline GemmLayout dense_layout(long ld, long batch_stride) {
   return {{0, 0, (int)batch_stride}, {0, 0, (int)ld}, {0, 0, 1}};
 }
@@ -205,8 +209,10 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
 // the layouts: K % 16 != 0, a contiguous dimension whose maps are not unit
 // stride in runs of 4, a k map whose div is not a multiple of 16, a C row
 // map whose div is not a multiple of 32, or offsets of 2^31 bytes or more.
+// flops (optional): the multiply-add work launched (less than 2 M N K when
+// tri_a skips zero slabs).
 bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
-                 const GemmLayouts& L, hipStream_t s, const float* D = nullptr);
+                 const GemmLayouts& L, hipStream_t s, const float* D = nullptr, double* flops = nullptr);
 
 // Fused Adam + L2 update (examples/nanogpt_modular.ml:97-108 op order).
 // One parameter tensor of a multi-tensor Adam update (device pointers).

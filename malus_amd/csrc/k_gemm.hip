@@ -336,8 +336,12 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   B += bb;
   C += map_at<MAP>(L.c.b, b) + (long)blockIdx.y * split_stride;
   if (D) D += map_at<MAP>(L.c.b, b);
-  const int kbeg = blockIdx.y * k_chunk;
-  const int kend = min(K, kbeg + k_chunk);
+  int kbeg = blockIdx.y * k_chunk;
+  int kend = min(K, kbeg + k_chunk);
+  if (MAP && L.tri_a) {  // op(A) row m is zero past k = m (A) or before k = m (A^T stored lower-triangular)
+    if (TA) kbeg = max(kbeg, m0);
+    else kend = min(kend, m0 + BM);
+  }
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave >> 1) * 32 * TM, wn = (wave & 1) * 32 * TN;
@@ -360,7 +364,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = v16f{0};
 
-  const int nk = (kend - kbeg) / BK;
+  const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
   KCursor<MAP> ka, kb;
   ka.init(fak, kbeg);
   kb.init(fbk, kbeg);
@@ -534,7 +538,9 @@ bool g_allow_dma = true;   // LDS-DMA path where the shape allows it
 // tile's efficiency and the CU's concurrency), plus the split-K partials'
 // HBM round trip.  Long-K shapes with few output tiles (the weight-gradient
 // GEMMs, K = tokens) split K so the grid fills the chip's workgroup slots.
-Plan plan_gemm(int batch, int M, int N, int K, int v) {
+// tri: A lower-triangular (GemmLayouts::tri_a); a tile row then runs on
+// average (n + 1) / (2 n) of K for n tile rows, which favours short tiles.
+Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false) {
   if (g_forced_tile == -2) {  // MALUS_GEMM_TILE=TMxTN pins a tile (tuning sweeps)
     g_forced_tile = -1;
     if (const char* e = getenv("MALUS_GEMM_TILE"))
@@ -569,7 +575,9 @@ Plan plan_gemm(int batch, int M, int N, int K, int v) {
       const long blocks = tiles * ns;
       const long per_cu = (blocks + 255) / 256;
       const int conc = (int)(per_cu < occ ? per_cu : occ);
-      double t = per_cu * 2.0 * bm * bn * kc / (kCuRate * tile_base(ti, v & 16) * cu_util(conc));
+      const int nrow = (M + bm - 1) / bm;
+      const double kwork = tri ? kc * (nrow + 1.0) / (2.0 * nrow) : kc;
+      double t = per_cu * 2.0 * bm * bn * kwork / (kCuRate * tile_base(ti, v & 16) * cu_util(conc));
       if (ns > 1) t += (ns + 1.0) * M * N * 4.0 / kHbm + 3e-6;
       if (t < best_t * 0.999) { best_t = t; best = Plan{ti, ns, kc}; }
     }
@@ -611,12 +619,14 @@ void split_reduce(float* partial, float* C, size_t mn, int nsplit, const float* 
 
 // One LDS-DMA launch (plus the split-K reduction); a split writes dense
 // partials, so callers with a non-dense C pass split_ok = false.
-void launch_dma(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
-                GemmLayouts L, hipStream_t s, const float* D, bool split_ok, bool mapped) {
+// Returns the multiply-add work the launch runs (2 * rows * cols * k, with
+// the k ranges a triangular A leaves).
+double launch_dma(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
+                  GemmLayouts L, hipStream_t s, const float* D, bool split_ok, bool mapped) {
   // mapped operands run the MAP instance on the dense shape's plan, so a
   // mapped GEMM splits K exactly like its dense twin
   const int v = variant(transA, transB, false, false, true);
-  Plan p = plan_gemm(batch, M, N, K, v);
+  Plan p = plan_gemm(batch, M, N, K, v, mapped && L.tri_a);
   const char* tag = mapped ? " mapped" : "";
   if (!split_ok && p.nsplit > 1) {
     p.nsplit = 1;
@@ -639,6 +649,14 @@ void launch_dma(const float* A, const float* B, float* C, int batch, int M, int 
   MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, mapped ? v | 32 : v), dim3((unsigned)tiles, (unsigned)nsplit,
                             (unsigned)batch), dim3(256), args, 0, s));
   if (nsplit > 1) split_reduce(dst, C, mn, nsplit, D, s, bucket);
+  if (!(mapped && L.tri_a)) return 2.0 * batch * (double)M * N * K;
+  double rk = 0;  // sum over tile rows of rows * k range
+  for (int m0 = 0; m0 < M; m0 += bm) {
+    const int rows = M - m0 < bm ? M - m0 : bm;
+    const int klen = transA ? K - m0 : (m0 + bm < K ? m0 + bm : K);
+    rk += (double)rows * klen;
+  }
+  return 2.0 * batch * (double)N * rk;
 }
 
 bool map_contig4(const GemmMap& f) { return f.s0 == 1 && (f.div == 0 || f.div % 4 == 0); }
@@ -695,7 +713,7 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
 }
 
 bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
-                 const GemmLayouts& L, hipStream_t s, const float* D) {
+                 const GemmLayouts& L, hipStream_t s, const float* D, double* flops) {
   if (batch <= 0 || M <= 0 || N <= 0 || K <= 0 || batch > 65535 || K % 16 || !g_allow_dma) return false;
   // contiguous dimension of each stored operand: runs of 4 floats
   const GemmMap& a_contig = L.a.c;  // A [M][K]: k;  A^T [K][M]: m
@@ -713,8 +731,10 @@ bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int
   const long eb = map_max(L.b.b, batch) + map_max(L.b.r, transB ? N : K) + map_max(L.b.c, transB ? K : N) + 1;
   const long ec = map_max(L.c.b, batch) + map_max(L.c.r, (M + 127) / 128 * 128) + map_max(L.c.c, N) + 1;
   if (ea > L.ext_a || eb > L.ext_b || L.ext_a >= lim || L.ext_b >= lim || ec >= lim) return false;
+  if (L.tri_a && M != K) return false;
   const bool c_dense = L.c.r.div == 0 && L.c.c.div == 0 && L.c.c.s0 == 1 && L.c.r.s0 == N;
-  launch_dma(A, B, C, batch, M, N, K, transA, transB, L, s, D, c_dense && batch == 1, true);
+  const double f = launch_dma(A, B, C, batch, M, N, K, transA, transB, L, s, D, c_dense && batch == 1 && !L.tri_a, true);
+  if (flops) *flops = f;
   return true;
 }
 

@@ -151,7 +151,7 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
       fail("malus: fused attention scores rejected a supported shape");
     p->write_seq = enqueue_mark("attn_scores_softmax");
     Pm = malus::H(p);
-    att = attn_out_fwd(Pm, Vv, B, Tn, H);
+    att = attn_out_fwd(Pm, Vv, B, Tn, H, /*causal=*/true);
     tape_record_fused(TAG_ATTENTION, {Q, K, Vv, Pm, scale}, att, {(int64_t)B, (int64_t)Tn, (int64_t)H});
   } else {
     if (fused_heads) {  // S = Q @ K^T with K read in place
@@ -188,7 +188,7 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
     }
     tape_record_reduce(OP_SOFTMAX, Sm, Pm, 2, 0);
     if (fused_heads) {
-      att = attn_out_fwd(Pm, Vv, B, Tn, H);
+      att = attn_out_fwd(Pm, Vv, B, Tn, H, false);
       tape_record_fused(TAG_ATTN_OUT, {Pm, Vv}, att, {(int64_t)B, (int64_t)Tn, (int64_t)H});
     } else {
       AO = binop(OP_MATMUL, Pm, Vv);

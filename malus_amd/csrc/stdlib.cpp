@@ -761,9 +761,11 @@ int64_t mapped(TensorBuffer* a, TensorBuffer* b, TensorBuffer* c, bool ta, bool 
                const GemmLayouts& L, const TensorBuffer* D, const char* what) {
   check_addend(D, c);
   KTimer* kt = ktimer_begin("gemm");
-  if (!k::gemm_mapped(a->f32(), b->f32(), c->f32(), batch, M, N, K, ta, tb, L, stream(), D ? D->f32() : nullptr))
+  double flops = 0;
+  if (!k::gemm_mapped(a->f32(), b->f32(), c->f32(), batch, M, N, K, ta, tb, L, stream(), D ? D->f32() : nullptr,
+                      &flops))
     fail("malus: %s: head-folded GEMM layout rejected (T %% 32, hs %% 16 and sizes below 2 GiB are required)", what);
-  ktimer_end(kt, 2.0 * batch * (double)M * N * K);
+  ktimer_end(kt, flops);  // executed work: causal GEMMs skip the zero triangle
   return done(c, what);
 }
 }  // namespace
@@ -804,13 +806,13 @@ int64_t head_proj_bwd_w(int64_t hx, int64_t hdq, size_t B, size_t T, size_t H, c
   return mapped(x, dq, c, true, false, 1, (int)Cin, (int)C, (int)N, L, D, "head_proj_bwd_w");
 }
 // att = unheads(P @ V): P [B*H, T, T], V [B*H, T, hs] -> [B*T, H*hs]
-int64_t attn_out_fwd(int64_t hp, int64_t hv, size_t B, size_t T, size_t H) {
+int64_t attn_out_fwd(int64_t hp, int64_t hv, size_t B, size_t T, size_t H, bool causal) {
   TensorBuffer *p = T_(hp), *v = T_(hv);
   const size_t hs = v->shape[2], C = H * hs, N = B * T;
   const size_t sh[2] = {N, C};
   TensorBuffer* c = alloc_tensor(F32, sh, 2);
   GemmLayouts L{dense_layout((long)T, (long)(T * T)), dense_layout((long)hs, (long)(T * hs)), rows_as_heads(T, H, hs),
-                (int)p->len, (int)v->len};
+                (int)p->len, (int)v->len, causal ? 1 : 0};
   return mapped(p, v, c, false, false, (int)(B * H), (int)T, (int)hs, (int)T, L, nullptr, "attn_out");
 }
 // dP = heads(dAtt) @ V^T  (+ D)
@@ -824,13 +826,13 @@ int64_t attn_out_bwd_p(int64_t hda, int64_t hv, size_t B, size_t T, size_t H, co
   return mapped(da, v, c, false, true, (int)(B * H), (int)T, (int)T, (int)hs, L, D, "attn_out_bwd_p");
 }
 // dV = P^T @ heads(dAtt)  (+ D)
-int64_t attn_out_bwd_v(int64_t hp, int64_t hda, size_t B, size_t T, size_t H, const TensorBuffer* D) {
+int64_t attn_out_bwd_v(int64_t hp, int64_t hda, size_t B, size_t T, size_t H, const TensorBuffer* D, bool causal) {
   TensorBuffer *p = T_(hp), *da = T_(hda);
   const size_t hs = da->shape[1] / H;
   const size_t sh[3] = {B * H, T, hs};
   TensorBuffer* c = alloc_tensor(F32, sh, 3);
   GemmLayouts L{dense_layout((long)T, (long)(T * T)), rows_as_heads(T, H, hs), dense_layout((long)hs, (long)(T * hs)),
-                (int)p->len, (int)da->len};
+                (int)p->len, (int)da->len, causal ? 1 : 0};
   return mapped(p, da, c, true, false, (int)(B * H), (int)T, (int)hs, (int)T, L, D, "attn_out_bwd_v");
 }
 // dS of the fused causal attention: softmax_bwd(P, heads(dAtt) @ V^T) * scale
@@ -844,15 +846,25 @@ int64_t attn_scores_bwd_impl(int64_t hda, int64_t hv, int64_t hp, int64_t hscale
   return done(out, "attn_scores_bwd");
 }
 // Scores S = Q @ K^T (the permute(K, 0, 2, 1) operand read in place): dQ = dS @ K, dK = dS^T @ Q  (+ D)
-int64_t scores_bwd_q(int64_t hds, int64_t hk, const TensorBuffer* D) {
+int64_t scores_bwd_q(int64_t hds, int64_t hk, const TensorBuffer* D, bool causal) {
   TensorBuffer *ds = T_(hds), *kk = T_(hk);
   const size_t bh = kk->shape[0], t = kk->shape[1], hs = kk->shape[2];
-  return gemm_out(ds, kk, false, false, (int)bh, (int)t, (int)hs, (int)t, (long)(t * t), (long)(t * hs), kk->shape, 3, D);
+  if (!causal)
+    return gemm_out(ds, kk, false, false, (int)bh, (int)t, (int)hs, (int)t, (long)(t * t), (long)(t * hs), kk->shape, 3, D);
+  TensorBuffer* c = alloc_tensor(F32, kk->shape, 3);
+  GemmLayouts L{dense_layout((long)t, (long)(t * t)), dense_layout((long)hs, (long)(t * hs)),
+                dense_layout((long)hs, (long)(t * hs)), (int)ds->len, (int)kk->len, 1};
+  return mapped(ds, kk, c, false, false, (int)bh, (int)t, (int)hs, (int)t, L, D, "scores_bwd_q");
 }
-int64_t scores_bwd_k(int64_t hds, int64_t hq, const TensorBuffer* D) {
+int64_t scores_bwd_k(int64_t hds, int64_t hq, const TensorBuffer* D, bool causal) {
   TensorBuffer *ds = T_(hds), *q = T_(hq);
   const size_t bh = q->shape[0], t = q->shape[1], hs = q->shape[2];
-  return gemm_out(ds, q, true, false, (int)bh, (int)t, (int)hs, (int)t, (long)(t * t), (long)(t * hs), q->shape, 3, D);
+  if (!causal)
+    return gemm_out(ds, q, true, false, (int)bh, (int)t, (int)hs, (int)t, (long)(t * t), (long)(t * hs), q->shape, 3, D);
+  TensorBuffer* c = alloc_tensor(F32, q->shape, 3);
+  GemmLayouts L{dense_layout((long)t, (long)(t * t)), dense_layout((long)hs, (long)(t * hs)),
+                dense_layout((long)hs, (long)(t * hs)), (int)ds->len, (int)q->len, 1};
+  return mapped(ds, q, c, true, false, (int)bh, (int)t, (int)hs, (int)t, L, D, "scores_bwd_k");
 }
 
 extern "C" {

@@ -475,11 +475,11 @@ void backward(int64_t loss) {
         const size_t Bm = (size_t)n.meta[0], Tm = (size_t)n.meta[1], Hm = (size_t)n.meta[2];
         for (int64_t h : n.saved) need_values(h);
         // AttnOut's VJP (dP, dV), the softmax and scale VJPs, then Scores' (dQ, dK)
-        if (nc) fold_grad(grads, v, [&](const TensorBuffer* o) { return attn_out_bwd_v(pr, dout, Bm, Tm, Hm, o); });
+        if (nc) fold_grad(grads, v, [&](const TensorBuffer* o) { return attn_out_bwd_v(pr, dout, Bm, Tm, Hm, o, true); });
         if (na || nb) {
           const int64_t ds = attn_scores_bwd_impl(dout, v, pr, sc, Bm, Tm, Hm);
-          if (na) fold_grad(grads, q, [&](const TensorBuffer* o) { return scores_bwd_q(ds, kk, o); });
-          if (nb) fold_grad(grads, kk, [&](const TensorBuffer* o) { return scores_bwd_k(ds, q, o); });
+          if (na) fold_grad(grads, q, [&](const TensorBuffer* o) { return scores_bwd_q(ds, kk, o, true); });
+          if (nb) fold_grad(grads, kk, [&](const TensorBuffer* o) { return scores_bwd_k(ds, q, o, true); });
           release(T(ds));
         }
         break;
@@ -494,11 +494,11 @@ void backward(int64_t loss) {
           if (na) fold_grad(grads, a, [&](const TensorBuffer* o) { return head_proj_bwd_x(dout, b, Bm, Tm, Hm, o); });
           if (nb) fold_grad(grads, b, [&](const TensorBuffer* o) { return head_proj_bwd_w(a, dout, Bm, Tm, Hm, o); });
         } else if (n.op == Scores) {
-          if (na) fold_grad(grads, a, [&](const TensorBuffer* o) { return scores_bwd_q(dout, b, o); });
-          if (nb) fold_grad(grads, b, [&](const TensorBuffer* o) { return scores_bwd_k(dout, a, o); });
+          if (na) fold_grad(grads, a, [&](const TensorBuffer* o) { return scores_bwd_q(dout, b, o, false); });
+          if (nb) fold_grad(grads, b, [&](const TensorBuffer* o) { return scores_bwd_k(dout, a, o, false); });
         } else {
           if (na) fold_grad(grads, a, [&](const TensorBuffer* o) { return attn_out_bwd_p(dout, b, Bm, Tm, Hm, o); });
-          if (nb) fold_grad(grads, b, [&](const TensorBuffer* o) { return attn_out_bwd_v(a, dout, Bm, Tm, Hm, o); });
+          if (nb) fold_grad(grads, b, [&](const TensorBuffer* o) { return attn_out_bwd_v(a, dout, Bm, Tm, Hm, o, false); });
         }
         break;
       }
