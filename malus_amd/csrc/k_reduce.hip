@@ -13,6 +13,8 @@
 // multiply reduces dout * a without materializing the product; each product
 // is rounded to f32 exactly as the materialized tensor would be.
 // Every order is fixed, so results are run-to-run deterministic.
+#include <type_traits>
+
 #include "common.h"
 
 namespace malus {
@@ -161,13 +163,27 @@ __global__ __launch_bounds__(256) void k_col4(const float* __restrict__ x, const
     const float4* xp = reinterpret_cast<const float4*>(x + o * axis * inner) + i4;
     const float4* yp = OP == R_PROD ? reinterpret_cast<const float4*>(y + o * axis * inner) + i4 : nullptr;
     const size_t stride4 = inner / 4;
-    for (size_t a = beg + rt; a < end; a += RT) {
-      const float4 v = ld(xp + a * stride4, nt);
-      const float4 w = OP == R_PROD ? ld(yp + a * stride4, nt) : v;
+    auto fold = [&](float4 v, float4 w) {
       acc.x = rcomb<OP>(acc.x, rload<OP>(v.x, w.x, mu.x));
       acc.y = rcomb<OP>(acc.y, rload<OP>(v.y, w.y, mu.y));
       acc.z = rcomb<OP>(acc.z, rload<OP>(v.z, w.z, mu.z));
       acc.w = rcomb<OP>(acc.w, rload<OP>(v.w, w.w, mu.w));
+    };
+    size_t a = beg + rt;
+    // four rows' loads in flight before their (in-order) folds
+    for (; a + 3 * RT < end; a += 4 * RT) {
+      float4 v[4], w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v[u] = ld(xp + (a + u * RT) * stride4, nt);
+        w[u] = OP == R_PROD ? ld(yp + (a + u * RT) * stride4, nt) : v[u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) fold(v[u], w[u]);
+    }
+    for (; a < end; a += RT) {
+      const float4 v = ld(xp + a * stride4, nt);
+      fold(v, OP == R_PROD ? ld(yp + a * stride4, nt) : v);
     }
   }
   red[rt][ct] = acc;
@@ -220,32 +236,40 @@ __global__ __launch_bounds__(256) void k_col(const float* __restrict__ x, const 
   else dst[(o * nsplit + sp) * inner + i] = acc;
 }
 
-// Combine column partials.  Block (x, o) owns kCombCols consecutive columns;
-// its 256 threads form 16 split groups, group g summing splits g, g+16, ...
-// in order (each group's loads of one split row are contiguous), then the 16
-// group sums are folded in group order.
-constexpr int kCombCols = 16;
-template <int OP>
+// Combine the split partials of a column reduction: CC columns per block,
+// G = 256 / CC split groups each summing every G-th partial in split order
+// (four loads in flight), then a fixed pairwise tree over the groups.  CC is
+// picked so that every group sums a few partials; the order depends only on
+// the shape, so the result is deterministic.
+template <int OP, int CC>
 __global__ __launch_bounds__(256) void k_col_combine(const float* __restrict__ partial, float* __restrict__ out,
                                                      uint32_t nsplit, size_t inner, uint32_t count) {
-  constexpr int G = 256 / kCombCols;
-  __shared__ float red[G][kCombCols + 1];
-  const int lc = threadIdx.x % kCombCols, g = threadIdx.x / kCombCols;
+  constexpr int G = 256 / CC;
+  __shared__ float red[G][CC];
+  const int lc = threadIdx.x % CC, g = threadIdx.x / CC;
   const size_t o = blockIdx.y;
-  const size_t i = (size_t)blockIdx.x * kCombCols + lc;
+  const size_t i = (size_t)blockIdx.x * CC + lc;
   float acc = rinit<OP>();
   if (i < inner) {
     const float* p = partial + o * nsplit * inner + i;
-    for (uint32_t s = g; s < nsplit; s += G) acc = rcomb<OP>(acc, p[(size_t)s * inner]);
+    uint32_t sp = g;
+    for (; sp + 3 * G < nsplit; sp += 4 * G) {
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = p[(size_t)(sp + u * G) * inner];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc = rcomb<OP>(acc, v[u]);
+    }
+    for (; sp < nsplit; sp += G) acc = rcomb<OP>(acc, p[(size_t)sp * inner]);
   }
   red[g][lc] = acc;
   __syncthreads();
-  if (g == 0 && i < inner) {
-    float r = red[0][lc];
 #pragma unroll
-    for (int w = 1; w < G; ++w) r = rcomb<OP>(r, red[w][lc]);
-    out[o * inner + i] = rfinal<OP>(r, count);
+  for (int w = G / 2; w > 0; w >>= 1) {
+    if (g < w) red[g][lc] = rcomb<OP>(red[g][lc], red[g + w][lc]);
+    __syncthreads();
   }
+  if (g == 0 && i < inner) out[o * inner + i] = rfinal<OP>(red[0][lc], count);
 }
 
 __global__ __launch_bounds__(256) void k_expand_axis(const float* __restrict__ small, float* __restrict__ out,
@@ -360,10 +384,19 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
   MALUS_HIP(hipGetLastError());
   if (nsplit > 1) {
     // base_blocks < 2048 here, so outer fits gridDim.y
-    dim3 cgrid((unsigned)((inner + kCombCols - 1) / kCombCols), (unsigned)outer);
-    if (OP == R_MAX) k_col_combine<R_MAX><<<cgrid, 256, 0, s>>>(dst, out, nsplit, inner, (uint32_t)axis);
-    else if (OP == R_MEAN || OP == R_VAR) k_col_combine<R_MEAN><<<cgrid, 256, 0, s>>>(dst, out, nsplit, inner, (uint32_t)axis);
-    else k_col_combine<R_SUM><<<cgrid, 256, 0, s>>>(dst, out, nsplit, inner, (uint32_t)axis);
+    // columns per combine block: enough split groups to keep ~4+ partials each
+    const int cc = nsplit >= 256 ? 4 : nsplit >= 64 ? 16 : 64;
+    dim3 cgrid((unsigned)((inner + cc - 1) / cc), (unsigned)outer);
+    auto comb = [&](auto tag) {
+      constexpr int C = decltype(tag)::value;
+      const uint32_t cnt = (uint32_t)axis;
+      if (OP == R_MAX) k_col_combine<R_MAX, C><<<cgrid, 256, 0, s>>>(dst, out, nsplit, inner, cnt);
+      else if (OP == R_MEAN || OP == R_VAR) k_col_combine<R_MEAN, C><<<cgrid, 256, 0, s>>>(dst, out, nsplit, inner, cnt);
+      else k_col_combine<R_SUM, C><<<cgrid, 256, 0, s>>>(dst, out, nsplit, inner, cnt);
+    };
+    if (cc == 4) comb(std::integral_constant<int, 4>{});
+    else if (cc == 16) comb(std::integral_constant<int, 16>{});
+    else comb(std::integral_constant<int, 64>{});
     MALUS_HIP(hipGetLastError());
     pool_free(dst, bucket);
   }

@@ -231,6 +231,7 @@ __global__ __launch_bounds__(256) void k_ce_fwd_rows(const float* __restrict__ l
   const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
+  const int32_t tg = tgt[row];  // issued with the row's loads
   RowTile<NV, VM> t;
   t.load(logits + row * axis, axis, lane, -INFINITY);
   float m = -INFINITY;
@@ -248,14 +249,17 @@ __global__ __launch_bounds__(256) void k_ce_fwd_rows(const float* __restrict__ l
 #pragma unroll
   for (int e = 0; e < NV * 4; ++e) t.v[e] = t.v[e] / s;
   t.store(probs + row * axis, axis, lane);
-  const int32_t tg = tgt[row];
   if (tg < 0 || (uint32_t)tg >= axis) {
     if (lane == 0) { nll[row] = NAN; *err = 2; }
     return;
   }
+  // the lane holding column tg takes the one log (integer compare: exact)
+  float pt = 0.0f;
+  bool own = false;
 #pragma unroll
   for (int e = 0; e < NV * 4; ++e)
-    if (t.col(e, lane) == (uint32_t)tg) nll[row] = -logf(t.v[e]);
+    if (t.col(e, lane) == (uint32_t)tg) { pt = t.v[e]; own = true; }
+  if (own) nll[row] = -logf(pt);
 }
 
 // transformer_bwd.ml:57-65 / tape.rs:1200-1214: (p - 1{j == t}) * (dout[0] / N)
