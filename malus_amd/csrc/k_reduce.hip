@@ -324,14 +324,12 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
       float* partial = static_cast<float*>(pool_alloc(rows * nsplit * sizeof(float), &bucket));
       k_row_split<OP><<<(unsigned)(rows * nsplit), 256, 0, s>>>(x, y, mean, partial, axis, nsplit, chunk, nt);
       MALUS_HIP(hipGetLastError());
-      // combine partials of each row with one wave per row, then finalize
-      k_row_wave<COMB == R_MAX ? R_MAX : R_SUM, false>
-          <<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, rows, nsplit, nsplit, false, false);
+      // combine partials of each row with one wave per row; MEAN and VAR
+      // divide the combined sum by the axis length in the same kernel
+      constexpr int FIN = COMB == R_MAX ? R_MAX : (OP == R_MEAN || OP == R_VAR) ? R_MEAN : R_SUM;
+      k_row_wave<FIN, false><<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, rows, nsplit,
+                                                                       (uint32_t)axis, true, false);
       MALUS_HIP(hipGetLastError());
-      if (OP == R_MEAN || OP == R_VAR) {
-        // divide in place by the axis length
-        binary_scalar(DIV, out, nullptr, (float)axis, true, out, rows, s);
-      }
       pool_free(partial, bucket);
       return;
     }
