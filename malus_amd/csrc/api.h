@@ -22,8 +22,8 @@ void tape_on_release(int64_t handle);
 void register_default_backward_fns();
 std::vector<size_t> tape_normalize_perm(const std::vector<size_t>& raw, size_t rank);
 // Record a fused node (tags 100 HeadProj, 101 Scores, 102 AttnOut,
-// 103 Attention; see tape.cpp) with its saved handles and output; retains
-// them all.
+// 103 Attention, 104 LayerNormScale; see tape.cpp) with its saved handles
+// and output; retains them all.
 void tape_record_fused(int32_t op, const std::vector<int64_t>& saved, int64_t out, const std::vector<int64_t>& meta);
 
 }  // namespace malus
@@ -36,6 +36,10 @@ int64_t matmul_impl(int64_t a, int64_t b, const malus::TensorBuffer* D);
 int64_t matmul_bwd_a_impl(int64_t a, int64_t b, int64_t dout, const malus::TensorBuffer* D);
 int64_t matmul_bwd_b_impl(int64_t a, int64_t b, int64_t dout, const malus::TensorBuffer* D);
 int64_t layernorm_bwd_impl(int64_t y, int64_t var, int64_t dout, int64_t axis, const malus::TensorBuffer* D);
+// out = layernorm(x, axis=-1) * w in one kernel, and the VJP for x (the
+// layernorm VJP of dout * w, + D); the VJP for w is malus_std_mul_bwd_b(dout, y, w).
+int64_t ln_affine_fwd(int64_t x, int64_t w, int64_t* y_out, int64_t* var_out);
+int64_t ln_affine_bwd_x(int64_t y, int64_t var, int64_t w, int64_t dout, const malus::TensorBuffer* D);
 // Head-folded attention GEMMs (stdlib.cpp): the composed ops' values with
 // the permute copies folded into GEMM addressing.  heads_foldable: shapes
 // the folded layouts support.

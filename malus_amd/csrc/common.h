@@ -159,11 +159,15 @@ void expand_axis(const float* small, float* out, size_t outer, size_t axis, size
 // Row ops over [outer, axis, inner] (inner may be > 1).
 void softmax(const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
-void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s);
-// With addend: dx = addend + VJP (gradient accumulation folded in).
+// With w (last axis only): also out = y * w broadcast over rows.
+void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s,
+               const float* w = nullptr, float* out = nullptr);
+// With addend: dx = addend + VJP (gradient accumulation folded in).  With w
+// (last axis only): dout is the gradient of y * w, and dy = dout * w is formed
+// in the kernel.
 void layernorm_bwd(const float* y, const float* var, const float* dout, float* dx, size_t outer, size_t axis, size_t inner,
                    float eps, hipStream_t s,
-                   const float* addend = nullptr);
+                   const float* addend = nullptr, const float* w = nullptr);
 // probs = softmax(logits) rows; nll[i] = -log(probs[i, t_i]).
 void ce_fwd(const float* logits, const int32_t* tgt, float* probs, float* nll, size_t n, size_t v, int32_t* err, hipStream_t s);
 // scale = dout[0] / n when dout is given (read on the device), else scale_host.

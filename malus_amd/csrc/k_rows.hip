@@ -160,9 +160,12 @@ __global__ __launch_bounds__(256) void k_softmax_bwd_rows(const float* __restric
 }
 
 // tensor_layernorm_axis (metal.rs:1486-1533): y = (x - mu) / sqrt(var + eps)
+// With w: also out = y * w[col] (the `layernorm(x) * w` of nanogpt_modular.ml:47,
+// rounded like the separate broadcast multiply).
 template <int NV, int VM>
 __global__ __launch_bounds__(256) void k_layernorm_rows(const float* __restrict__ x, float* __restrict__ y,
-                                                        float* __restrict__ var, size_t rows, uint32_t axis, float eps) {
+                                                        float* __restrict__ var, size_t rows, uint32_t axis, float eps,
+                                                        const float* __restrict__ w, float* __restrict__ out) {
   const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
@@ -185,6 +188,13 @@ __global__ __launch_bounds__(256) void k_layernorm_rows(const float* __restrict_
   for (int e = 0; e < NV * 4; ++e) t.v[e] = (t.v[e] - mu) / sigma;
   t.store(y + row * axis, axis, lane);
   if (lane == 0 && var) var[row] = va;
+  if (w) {
+    RowTile<NV, VM == 2 ? 1 : VM> wt;  // w is re-read by every row: cached loads
+    wt.load(w, axis, lane, 0.0f);
+#pragma unroll
+    for (int e = 0; e < NV * 4; ++e) t.v[e] = t.v[e] * wt.v[e];
+    t.store(out + row * axis, axis, lane);
+  }
 }
 
 // tape.rs:1162-1186: dx = ((dy - mean(dy)) - y * mean(dy*y)) * (1 / sqrt(var + eps))
@@ -192,13 +202,20 @@ template <int NV, int VM>
 __global__ __launch_bounds__(256) void k_layernorm_bwd_rows(const float* __restrict__ y, const float* __restrict__ var,
                                                             const float* __restrict__ dout, float* __restrict__ dx,
                                                             size_t rows, uint32_t axis, float eps,
-                                                            const float* __restrict__ addend) {
+                                                            const float* __restrict__ addend,
+                                                            const float* __restrict__ w) {
   const size_t row = (size_t)blockIdx.x * kRowsPerBlock + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;
   RowTile<NV, VM> yt, dt;
   yt.load(y + row * axis, axis, lane, 0.0f);
   dt.load(dout + row * axis, axis, lane, 0.0f);
+  if (w) {  // dout is the gradient of y * w: dy = dout * w, rounded like the multiply's VJP
+    RowTile<NV, VM == 2 ? 1 : VM> wt;
+    wt.load(w, axis, lane, 0.0f);
+#pragma unroll
+    for (int e = 0; e < NV * 4; ++e) dt.v[e] = dt.v[e] * wt.v[e];
+  }
   float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
   for (int e = 0; e < NV * 4; ++e) { s1 += dt.v[e]; float p = dt.v[e] * yt.v[e]; s2 += p; }
@@ -466,26 +483,29 @@ void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, si
   MALUS_HIP(hipGetLastError());
 }
 
-void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s) {
+void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s,
+               const float* w, float* out) {
   if (!outer || !axis || !inner) return;
   if (inner == 1 && axis <= kMaxRowAxis) {
     row_dispatch<SelLN>((uint32_t)axis, [&](auto sel) {
-      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(x, y, var, outer, (uint32_t)axis, eps);
-    }, 2 * outer * (size_t)axis * sizeof(float));
+      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(x, y, var, outer, (uint32_t)axis, eps, w, out);
+    }, (w ? 3 : 2) * outer * (size_t)axis * sizeof(float));
   } else {
+    if (w) fail("malus: fused layernorm scale needs the normalized axis last");
     k_layernorm_seq<<<seq_grid(outer * inner), 256, 0, s>>>(x, y, var, outer, axis, inner, eps);
   }
   MALUS_HIP(hipGetLastError());
 }
 
 void layernorm_bwd(const float* y, const float* var, const float* dout, float* dx, size_t outer, size_t axis, size_t inner,
-                   float eps, hipStream_t s, const float* addend) {
+                   float eps, hipStream_t s, const float* addend, const float* w) {
   if (!outer || !axis || !inner) return;
   if (inner == 1 && axis <= kMaxRowAxis) {
     row_dispatch<SelLNBwd>((uint32_t)axis, [&](auto sel) {
-      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(y, var, dout, dx, outer, (uint32_t)axis, eps, addend);
+      decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(y, var, dout, dx, outer, (uint32_t)axis, eps, addend, w);
     }, 3 * outer * (size_t)axis * sizeof(float));
   } else {
+    if (w) fail("malus: fused layernorm scale needs the normalized axis last");
     k_layernorm_bwd_seq<<<seq_grid(outer * inner), 256, 0, s>>>(y, var, dout, dx, outer, axis, inner, eps);
     if (addend) binary_same(ADD, addend, dx, dx, outer * axis * inner, s);
   }

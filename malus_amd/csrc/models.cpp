@@ -44,7 +44,8 @@ namespace {
 enum Op : int32_t {
   OP_MATMUL = 0, OP_ADD = 1, OP_SUB = 2, OP_MUL = 3, OP_DIV = 4, OP_TRANSPOSE = 13, OP_RESHAPE = 19, OP_SOFTMAX = 20,
   OP_LAYERNORM = 21, OP_GELU = 22, OP_CE = 23, OP_EMBEDDING = 24,
-  TAG_HEAD_PROJ = 100, TAG_SCORES = 101, TAG_ATTN_OUT = 102, TAG_ATTENTION = 103  // fused nodes (tape.cpp)
+  TAG_HEAD_PROJ = 100, TAG_SCORES = 101, TAG_ATTN_OUT = 102, TAG_ATTENTION = 103,
+  TAG_LN_SCALE = 104  // fused nodes (tape.cpp)
 };
 
 // grad-tracked binop: lower + tape_record_binop (codegen-cpu/lib.rs:1531-1552)
@@ -75,6 +76,21 @@ int64_t layernorm(int64_t x) {
   int64_t y = malus_std_layernorm_fwd(x, 1, &var);
   tape_record_layernorm(OP_LAYERNORM, x, y, var, 1);
   return y;
+}
+
+// layernorm(x, axis=1) * w: one kernel and one LayerNormScale tape node when
+// fused (the same values; y and the variance are saved for the VJPs), else
+// the reference's LAYERNORM and MUL records.  *y gets the normalized rows.
+int64_t ln_scale(bool fused, int64_t x, int64_t w, int64_t* y) {
+  if (!fused) {
+    *y = layernorm(x);
+    return binop(OP_MUL, *y, w);
+  }
+  int64_t var;
+  int64_t out = ln_affine_fwd(x, w, y, &var);
+  tape_record_fused(TAG_LN_SCALE, {x, w, *y, var}, out, {});
+  tensor_release(var);  // the tape holds it
+  return out;
 }
 
 // out = x + a @ w with the add in the GEMM epilogue.  The tape gets the
@@ -108,8 +124,8 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   const size_t B = g.B, Tn = g.Tn, C = g.C, H = g.H, hs = C / H, N = B * Tn;
   int64_t* P = &g.p[8 * l];
   // nanogpt_modular.ml:47-68
-  int64_t y1 = layernorm(x);
-  int64_t xn1 = binop(OP_MUL, y1, P[0]);
+  int64_t y1;
+  int64_t xn1 = ln_scale(g.fused_fwd, x, P[0], &y1);
   // Fused heads: the head fold / unfold permutes and K's transpose are
   // folded into GEMM addressing (one tape node per projection, per score
   // product and per attention output; the same values as the composed ops).
@@ -203,8 +219,8 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
     proj = binop(OP_MATMUL, att, P[4]);
     x2 = binop(OP_ADD, x, proj);
   }
-  int64_t y2 = layernorm(x2);
-  int64_t xn2 = binop(OP_MUL, y2, P[5]);
+  int64_t y2;
+  int64_t xn2 = ln_scale(g.fused_fwd, x2, P[5], &y2);
   int64_t h = binop(OP_MATMUL, xn2, P[6]);
   int64_t ge = malus_std_gelu_fwd(h);
   tape_record_unary(OP_GELU, h, ge);
@@ -231,8 +247,8 @@ int64_t gpt_forward_loss(Gpt& g, int64_t toks, int64_t targets, int64_t* logits_
     tensor_release(x);
     x = nx;
   }
-  int64_t yf = layernorm(x);
-  int64_t xf = binop(OP_MUL, yf, g.top(2));
+  int64_t yf;
+  int64_t xf = ln_scale(g.fused_fwd, x, g.top(2), &yf);
   int64_t logits = binop(OP_MATMUL, xf, g.top(3));
   rel({x, yf, xf});
   if (!targets) {

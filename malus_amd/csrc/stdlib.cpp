@@ -710,6 +710,42 @@ int64_t layernorm_bwd_impl(int64_t y, int64_t var, int64_t dout, int64_t axis, c
   return done(out, "layernorm_bwd");
 }
 
+// out = layernorm(x, axis=-1) * w (nanogpt_modular.ml:47 and :62) from one
+// kernel; *y_out gets the normalized rows, *var_out the keepdim variance.
+int64_t ln_affine_fwd(int64_t hx, int64_t hw, int64_t* y_out, int64_t* var_out) {
+  TensorBuffer *t = T(hx), *w = T(hw);
+  need_f32(t, "layernorm");
+  const size_t a = t->shape[t->ndim - 1];
+  if (w->len != a || w->dtype != F32)
+    fail("malus: fused layernorm scale: weight %s does not match the last axis of %s", shape_str(w).c_str(),
+         shape_str(t).c_str());
+  TensorBuffer* y = alloc_like(t);
+  TensorBuffer* out = alloc_like(t);
+  size_t vsh[kMaxRank];
+  for (int i = 0; i < t->ndim; ++i) vsh[i] = i == t->ndim - 1 ? 1 : t->shape[i];
+  TensorBuffer* var = alloc_tensor(F32, vsh, t->ndim);
+  k::layernorm(t->f32(), y->f32(), var->f32(), t->len / a, a, 1, 1e-5f, stream(), w->f32(), out->f32());
+  uint64_t seq = enqueue_mark("layernorm_affine");
+  y->write_seq = var->write_seq = out->write_seq = seq;
+  *y_out = H(y);
+  *var_out = H(var);
+  return H(out);
+}
+// dx of out = layernorm(x) * w: the layernorm VJP of dout * w (+ D)
+int64_t ln_affine_bwd_x(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const TensorBuffer* D) {
+  TensorBuffer *ty = T(hy), *tv = T(hvar), *tw = T(hw), *td = T(hd);
+  const size_t a = ty->shape[ty->ndim - 1], o = ty->len / a;
+  if (tv->len != o || tw->len != a || td->len != ty->len)
+    fail("malus: fused layernorm scale VJP: y %s, var %s, w %s, dout %s", shape_str(ty).c_str(), shape_str(tv).c_str(),
+         shape_str(tw).c_str(), shape_str(td).c_str());
+  if (D && (D->dtype != F32 || D->len != ty->len))
+    fail("malus: layernorm VJP accumulate: addend %s does not match %s", shape_str(D).c_str(), shape_str(ty).c_str());
+  TensorBuffer* out = alloc_like(ty);
+  k::layernorm_bwd(ty->f32(), tv->f32(), td->f32(), out->f32(), o, a, 1, 1e-5f, stream(), D ? D->f32() : nullptr,
+                   tw->f32());
+  return done(out, "layernorm_affine_bwd");
+}
+
 // dA = dout @ op(B)^T
 int64_t matmul_bwd_a_impl(int64_t ha, int64_t hb, int64_t hd, const TensorBuffer* D) {
   TensorBuffer *a = T(ha), *b = T(hb), *d = T(hd);

@@ -33,8 +33,10 @@ enum OpTag : int32_t {
 //   Attention (Q, K, V; P, scale) -> att: AttnOut(softmax(Scores(Q, K) * scale + causal mask), V),
 //            with P the saved probabilities; the per-forward scale and mask
 //            leaves are released before backward, so no gradient reaches them
+//   LayerNormScale (x, w; y, var) -> out: layernorm(x, axis=-1) * w, with the
+//            normalized rows y and the keepdim variance saved
 // meta holds {B, T, H} for HeadProj, AttnOut and Attention.
-enum FusedTag : int32_t { HeadProj = 100, Scores = 101, AttnOut = 102, Attention = 103 };
+enum FusedTag : int32_t { HeadProj = 100, Scores = 101, AttnOut = 102, Attention = 103, LayerNormScale = 104 };
 
 enum BwdSlot : int32_t {
   AddBwdA = 0, AddBwdB, SubBwdA, SubBwdB, MulBwdA, MulBwdB, DivBwdA, DivBwdB, SigmoidBwd, ReluBwd, TanhBwd, ExpBwd,
@@ -125,7 +127,7 @@ void need_values(int64_t h) {
 int diff_inputs(int32_t op) {
   if (op == Attention) return 3;
   if (op == Matmul || op == Add || op == Sub || op == Mul || op == Div || op == HeadProj || op == Scores ||
-      op == AttnOut)
+      op == AttnOut || op == LayerNormScale)
     return 2;
   return 1;
 }
@@ -301,8 +303,8 @@ using namespace malus;
 namespace malus {
 void tape_record_fused(int32_t op, const std::vector<int64_t>& saved, int64_t out, const std::vector<int64_t>& meta) {
   if (!t_recording) return;
-  const size_t want = op == Attention ? 5 : 2;
-  if (op < HeadProj || op > Attention) fail("malus: unknown fused op tag %d", op);
+  const size_t want = op == Attention ? 5 : op == LayerNormScale ? 4 : 2;
+  if (op < HeadProj || op > LayerNormScale) fail("malus: unknown fused op tag %d", op);
   if (saved.size() != want) fail("malus: fused op %d takes %zu saved handles, got %zu", op, want, saved.size());
   for (int64_t h : saved) retain(T(h));
   retain(T(out));
@@ -482,6 +484,15 @@ void backward(int64_t loss) {
           if (nb) fold_grad(grads, kk, [&](const TensorBuffer* o) { return scores_bwd_k(ds, q, o, true); });
           release(T(ds));
         }
+        break;
+      }
+      case LayerNormScale: {  // saved {x, w, y, var}
+        const int64_t x = n.saved[0], w = n.saved[1], y = n.saved[2], var = n.saved[3];
+        need_values(w);
+        need_values(y);
+        // the multiply's VJPs (dy, then dw), then the layernorm VJP of dy
+        if (nb) accumulate(grads, w, slot_fn<Fn3>(MulBwdB)(dout, y, w));
+        if (na) fold_grad(grads, x, [&](const TensorBuffer* o) { return ln_affine_bwd_x(y, var, w, dout, o); });
         break;
       }
       case HeadProj: case Scores: case AttnOut: {
