@@ -22,7 +22,7 @@ void tape_on_release(int64_t handle);
 void register_default_backward_fns();
 std::vector<size_t> tape_normalize_perm(const std::vector<size_t>& raw, size_t rank);
 // Record a fused node (tags 100 HeadProj, 101 Scores, 102 AttnOut,
-// 103 Attention, 104 LayerNormScale; see tape.cpp) with its saved handles
+// 103 Attention, 104 LayerNormScale, 105 GeluMatmul; see tape.cpp) with its saved handles
 // and output; retains them all.
 void tape_record_fused(int32_t op, const std::vector<int64_t>& saved, int64_t out, const std::vector<int64_t>& meta);
 
@@ -40,6 +40,10 @@ int64_t layernorm_bwd_impl(int64_t y, int64_t var, int64_t dout, int64_t axis, c
 // layernorm VJP of dout * w, + D); the VJP for w is malus_std_mul_bwd_b(dout, y, w).
 int64_t ln_affine_fwd(int64_t x, int64_t w, int64_t* y_out, int64_t* var_out);
 int64_t ln_affine_bwd_x(int64_t y, int64_t var, int64_t w, int64_t dout, const malus::TensorBuffer* D);
+// The MLP's GELU in GEMM epilogues: h = x @ W1 with gelu(h) (returns h, 0
+// when the fused GEMM does not fit), and dh = gelu_bwd(h, dout @ W2^T) (+ D).
+int64_t matmul_gelu_fwd(int64_t x, int64_t w, int64_t* ge_out);
+int64_t gelu_matmul_bwd_h(int64_t dout, int64_t w, int64_t h, const malus::TensorBuffer* D);
 // Head-folded attention GEMMs (stdlib.cpp): the composed ops' values with
 // the permute copies folded into GEMM addressing.  heads_foldable: shapes
 // the folded layouts support.

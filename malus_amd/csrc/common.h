@@ -213,6 +213,14 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
 // the layouts: K % 16 != 0, a contiguous dimension whose maps are not unit
 // stride in runs of 4, a k map whose div is not a multiple of 16, a C row
 // map whose div is not a multiple of 32, or offsets of 2^31 bytes or more.
+// GEMMs with a fused GELU (dense, batch 1, LDS-DMA path; false, launching
+// nothing, when the shape does not fit it):
+//   forward  (backward = false): C = A @ B and E = gelu(C);
+//   backward (backward = true, transB): C = gelu_bwd(E, A @ B^T) (+ D), with E
+//   the GELU's input: the GELU VJP of the product, rounded as the separate
+//   kernels round it.
+bool gemm_gelu(const float* A, const float* B, float* C, float* E, int M, int N, int K, bool transB, bool backward,
+               hipStream_t s, const float* D = nullptr);
 // flops (optional): the multiply-add work launched (less than 2 M N K when
 // tri_a skips zero slabs).
 bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,

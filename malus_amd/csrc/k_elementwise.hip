@@ -6,6 +6,7 @@
 // with -ffp-contract=off so every expression rounds like the reference's
 // one-op-per-kernel f32 arithmetic.
 #include "common.h"
+#include "k_gelu.h"
 
 namespace malus {
 namespace k {
@@ -31,18 +32,6 @@ __device__ __forceinline__ float binop(float a, float b) {
   else return a / b;
 }
 
-// tanh for GELU's inner argument: 1 - 2 / (1 + 2^(2 y log2 e)) with the
-// hardware exp2 and reciprocal (each within 1 ulp).  Its absolute error is
-// at most 3 ulp(1) for every y (no cancellation issue: GELU adds the result
-// to 1, so only absolute error matters), and e -> inf / 0 give exactly
-// +1 / -1.  It replaces the library tanhf's ~35 instructions with ~5, which
-// keeps the GELU kernels memory-bound.
-__device__ __forceinline__ float gelu_tanh(float y) {
-  const float e = __builtin_amdgcn_exp2f(y * 2.8853900817779268f);  // 2 / ln 2
-  const float r = __builtin_amdgcn_rcpf(1.0f + e);
-  return __builtin_fmaf(-2.0f, r, 1.0f);
-}
-
 // Unary builtins: codegen-gpu/lib.rs:375-381; GELU: metal.rs:1535-1549.
 // exp / log / tanh are evaluated in f64 and rounded once to f32, so each is
 // within 0.5 ulp (+ a rare double-rounding step) of the exact value, like
@@ -58,11 +47,7 @@ __device__ __forceinline__ float unop(float x) {
   else if constexpr (OP == LOG) return (float)log((double)x);
   else if constexpr (OP == SQRT) return sqrtf(x);
   else if constexpr (OP == ABS) return fabsf(x);
-  else {  // GELU, tanh approximation
-    const float C0 = 0.7978845608f, C1 = 0.044715f;
-    float inner = C0 * (x + C1 * x * x * x);
-    return 0.5f * x * (1.0f + gelu_tanh(inner));
-  }
+  else return gelu_fwd(x);  // tanh approximation (k_gelu.h)
 }
 
 // Unary VJPs: tape.rs:1041-1083 and 1187-1199 (expression order kept).
@@ -75,14 +60,7 @@ __device__ __forceinline__ float unbwd(float v, float d) {
   else if constexpr (OP == B_ABS) return d * (v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f));
   else if constexpr (OP == B_EXP) return d * v;
   else if constexpr (OP == B_LOG) return d / v;
-  else {  // B_GELU
-    const float C0 = 0.7978845608f, C1 = 0.044715f;
-    float g = C0 * (v + C1 * v * v * v);
-    float t = gelu_tanh(g);
-    float gp = C0 * (1.0f + 3.0f * C1 * v * v);
-    float deriv = 0.5f * (1.0f + t) + 0.5f * v * (1.0f - t * t) * gp;
-    return d * deriv;
-  }
+  else return gelu_bwd(v, d);  // B_GELU (k_gelu.h)
 }
 
 typedef float v4f __attribute__((ext_vector_type(4)));

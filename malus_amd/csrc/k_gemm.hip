@@ -29,6 +29,7 @@
 #include <cstring>
 
 #include "common.h"
+#include "k_gelu.h"
 
 namespace malus {
 namespace k {
@@ -313,11 +314,14 @@ struct DmaSlab {
 // addresses D).  Dense row-major operands are the maps {0, 0, ld}.  The
 // host guarantees K % 16 == 0, the map conditions above, and every byte
 // offset below 2^31; a split-K launch writes dense partials.
-template <int TM, int TN, bool TA, bool TB, bool MAP>
+// EPI: 0 plain; 1 also E = gelu(C) (the GELU after a GEMM, no D); 2 C =
+// gelu_bwd(E, product) (+ D): the GELU VJP applied to the product, with E
+// the GELU input.  E shares C's layout.
+template <int TM, int TN, bool TA, bool TB, bool MAP, int EPI = 0>
 __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int M, int N, int K, GemmLayouts L,
                                                       int k_chunk, int tiles_n, long split_stride,
-                                                      const float* __restrict__ D) {
+                                                      const float* __restrict__ D, float* __restrict__ E) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 64 * TM, BN = 64 * TN;
   using SlabA = DmaSlab<BM, !TA>;  // A [M][K] is k-contiguous
@@ -336,6 +340,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   B += bb;
   C += map_at<MAP>(L.c.b, b) + (long)blockIdx.y * split_stride;
   if (D) D += map_at<MAP>(L.c.b, b);
+  if (EPI) E += map_at<MAP>(L.c.b, b);
   int kbeg = blockIdx.y * k_chunk;
   int kend = min(K, kbeg + k_chunk);
   if (MAP && L.tri_a) {  // op(A) row m is zero past k = m (A) or before k = m (A^T stored lower-triangular)
@@ -417,7 +422,12 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
           const int dm = 8 * (r >> 2) + 4 * lk + (r & 3);
           const int m = m0 + wm + 32 * i + dm;
           const int o = cn + dm * L.c.r.s0;
-          if (m < M) C[o] = D ? D[o] + acc[i][j][r] : acc[i][j][r];
+          if (m < M) {
+            float v = acc[i][j][r];
+            if (EPI == 2) v = gelu_bwd(E[o], v);
+            C[o] = D ? D[o] + v : v;
+            if (EPI == 1) E[o] = gelu_fwd(v);
+          }
         }
       }
     }
@@ -471,6 +481,11 @@ inline int variant(bool ta, bool tb, bool va, bool vb, bool dma) {
 
 template <int TM, int TN, bool TA, bool TB>
 const void* kernel_of(int v) {
+  if (v & 64) {  // GELU epilogues: dense NN (forward) and NT (the VJP's dA)
+    if constexpr (!TA && !TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, false, false, 1>);
+    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, false, 2>);
+    return nullptr;
+  }
   if (v & 32) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, true>);
   if (v & 16) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, false>);
   const bool va = v & 2, vb = v & 1;
@@ -502,7 +517,7 @@ const void* kernel_for(int ti, int v) {
 // Co-resident workgroups per CU of each kernel variant (VGPR and LDS
 // limited), from the runtime's occupancy calculator; cached per variant.
 int occupancy(int ti, int v) {
-  static int cache[kNumTiles][64];
+  static int cache[kNumTiles][128];
   int& o = cache[ti][v];
   if (o == 0) {
     int n = 0;
@@ -622,13 +637,14 @@ void split_reduce(float* partial, float* C, size_t mn, int nsplit, const float* 
 // Returns the multiply-add work the launch runs (2 * rows * cols * k, with
 // the k ranges a triangular A leaves).
 double launch_dma(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
-                  GemmLayouts L, hipStream_t s, const float* D, bool split_ok, bool mapped) {
+                  GemmLayouts L, hipStream_t s, const float* D, bool split_ok, bool mapped, float* E = nullptr,
+                  int epi = 0) {
   // mapped operands run the MAP instance on the dense shape's plan, so a
   // mapped GEMM splits K exactly like its dense twin
   const int v = variant(transA, transB, false, false, true);
   Plan p = plan_gemm(batch, M, N, K, v, mapped && L.tri_a);
   const char* tag = mapped ? " mapped" : "";
-  if (!split_ok && p.nsplit > 1) {
+  if ((!split_ok || epi) && p.nsplit > 1) {
     p.nsplit = 1;
     p.k_chunk = K;
   }
@@ -645,9 +661,10 @@ double launch_dma(const float* A, const float* B, float* C, int batch, int M, in
   }
   long split_stride = nsplit > 1 ? (long)mn : 0;
   const float* Dk = nsplit > 1 ? nullptr : D;  // split-K applies the addend in the reduction
-  void* args[] = {&A, &B, &dst, &M, &N, &K, &L, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk};
-  MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, mapped ? v | 32 : v), dim3((unsigned)tiles, (unsigned)nsplit,
-                            (unsigned)batch), dim3(256), args, 0, s));
+  void* args[] = {&A, &B, &dst, &M, &N, &K, &L, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk, &E};
+  const void* fn = kernel_for(p.ti, epi ? v | 64 : mapped ? v | 32 : v);
+  if (!fn) fail("malus: gemm: no kernel for epilogue %d with transA=%d transB=%d", epi, transA, transB);
+  MALUS_HIP(hipLaunchKernel(fn, dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch), dim3(256), args, 0, s));
   if (nsplit > 1) split_reduce(dst, C, mn, nsplit, D, s, bucket);
   if (!(mapped && L.tri_a)) return 2.0 * batch * (double)M * N * K;
   double rk = 0;  // sum over tile rows of rows * k range
@@ -710,6 +727,19 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
   MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, v), dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch),
                             dim3(256), args, 0, s));
   if (nsplit > 1) split_reduce(dst, C, mn, nsplit, D, s, bucket);
+}
+
+bool gemm_gelu(const float* A, const float* B, float* C, float* E, int M, int N, int K, bool transB, bool backward,
+               hipStream_t s, const float* D) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 16 || N % 4 || !g_allow_dma || (!backward && (D || transB)) ||
+      (backward && !transB))
+    return false;
+  const long ext_a = (long)M * K, ext_b = (long)K * N;
+  if ((size_t)ext_a * 4 >= (1ull << 31) || (size_t)ext_b * 4 >= (1ull << 31) || (size_t)M * N * 4 >= (1ull << 31))
+    return false;
+  GemmLayouts L{dense_layout(K, 0), dense_layout(transB ? K : N, 0), dense_layout(N, 0), (int)ext_a, (int)ext_b};
+  launch_dma(A, B, C, 1, M, N, K, false, transB, L, s, D, false, false, E, backward ? 2 : 1);
+  return true;
 }
 
 bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,

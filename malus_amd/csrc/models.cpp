@@ -45,7 +45,7 @@ enum Op : int32_t {
   OP_MATMUL = 0, OP_ADD = 1, OP_SUB = 2, OP_MUL = 3, OP_DIV = 4, OP_TRANSPOSE = 13, OP_RESHAPE = 19, OP_SOFTMAX = 20,
   OP_LAYERNORM = 21, OP_GELU = 22, OP_CE = 23, OP_EMBEDDING = 24,
   TAG_HEAD_PROJ = 100, TAG_SCORES = 101, TAG_ATTN_OUT = 102, TAG_ATTENTION = 103,
-  TAG_LN_SCALE = 104  // fused nodes (tape.cpp)
+  TAG_LN_SCALE = 104, TAG_GELU_MATMUL = 105  // fused nodes (tape.cpp)
 };
 
 // grad-tracked binop: lower + tape_record_binop (codegen-cpu/lib.rs:1531-1552)
@@ -221,14 +221,28 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   }
   int64_t y2;
   int64_t xn2 = ln_scale(g.fused_fwd, x2, P[5], &y2);
-  int64_t h = binop(OP_MATMUL, xn2, P[6]);
-  int64_t ge = malus_std_gelu_fwd(h);
-  tape_record_unary(OP_GELU, h, ge);
-  int64_t mo, x3;
-  if (g.fused_fwd) residual_matmul(x2, ge, P[7], &mo, &x3);
-  else {
-    mo = binop(OP_MATMUL, ge, P[7]);
-    x3 = binop(OP_ADD, x2, mo);
+  int64_t ge = 0, mo, x3;
+  int64_t h = g.fused_fwd ? matmul_gelu_fwd(xn2, P[6], &ge) : 0;
+  if (h) {
+    // MLP: gelu in the first GEMM's epilogue; out = x2 + ge @ W2 with the add
+    // in the second's.  Tape: MATMUL(xn2, W1 -> h), GeluMatmul(h, W2; ge ->
+    // prod) whose VJP applies the GELU VJP in the dA GEMM's epilogue, and
+    // ADD(x2, prod -> out); prod is shape-only.
+    tape_record_binop(OP_MATMUL, xn2, P[6], h);
+    x3 = matmul_impl(ge, P[7], T(x2));
+    TensorBuffer* o = T(x3);
+    mo = malus::H(alloc_virtual(F32, o->shape, o->ndim));
+    tape_record_fused(TAG_GELU_MATMUL, {h, P[7], ge}, mo, {});
+    tape_record_binop(OP_ADD, x2, mo, x3);
+  } else {
+    h = binop(OP_MATMUL, xn2, P[6]);
+    ge = malus_std_gelu_fwd(h);
+    tape_record_unary(OP_GELU, h, ge);
+    if (g.fused_fwd) residual_matmul(x2, ge, P[7], &mo, &x3);
+    else {
+      mo = binop(OP_MATMUL, ge, P[7]);
+      x3 = binop(OP_ADD, x2, mo);
+    }
   }
   rel({y1, xn1, Q, K, Vv, Kt, scale, S, Ss, mask, Sm, Pm, AO, ao4, aop, att, proj, x2, y2, xn2, h, ge, mo});
   return x3;

@@ -746,6 +746,45 @@ int64_t ln_affine_bwd_x(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const 
   return done(out, "layernorm_affine_bwd");
 }
 
+// h = x @ W1 and ge = gelu(h) from one GEMM (nanogpt_modular.ml:63);
+// returns h, *ge_out gets gelu(h).  0 when the shape does not fit the fused
+// epilogue (nothing launched).
+int64_t matmul_gelu_fwd(int64_t hx, int64_t hw, int64_t* ge_out) {
+  TensorBuffer *x = T(hx), *w = T(hw);
+  if (x->ndim != 2 || w->ndim != 2 || x->shape[1] != w->shape[0]) return 0;
+  const size_t M = x->shape[0], K = x->shape[1], N = w->shape[1];
+  const size_t sh[2] = {M, N};
+  TensorBuffer* h = alloc_tensor(F32, sh, 2);
+  TensorBuffer* ge = alloc_tensor(F32, sh, 2);
+  KTimer* kt = ktimer_begin("gemm");
+  if (!k::gemm_gelu(x->f32(), w->f32(), h->f32(), ge->f32(), (int)M, (int)N, (int)K, false, false, stream())) {
+    ktimer_end(kt, 0);
+    release(h);
+    release(ge);
+    return 0;
+  }
+  ktimer_end(kt, 2.0 * M * N * K);
+  h->write_seq = ge->write_seq = enqueue_mark("matmul_gelu");
+  *ge_out = H(ge);
+  return H(h);
+}
+// dh of mo = gelu(h) @ W2: gelu_bwd(h, dout @ W2^T) (+ D) from one GEMM
+int64_t gelu_matmul_bwd_h(int64_t hd, int64_t hw, int64_t hh, const TensorBuffer* D) {
+  TensorBuffer *d = T(hd), *w = T(hw), *h = T(hh);
+  const size_t N = w->shape[0], K = w->shape[1], M = d->len / K;
+  if (h->len != M * N || d->len != M * K) fail("malus: gelu matmul VJP: dout %s, w %s, h %s", shape_str(d).c_str(),
+                                               shape_str(w).c_str(), shape_str(h).c_str());
+  if (D && (D->dtype != F32 || D->len != h->len))
+    fail("malus: gelu matmul VJP accumulate: addend %s does not match %s", shape_str(D).c_str(), shape_str(h).c_str());
+  TensorBuffer* out = alloc_like(h);
+  KTimer* kt = ktimer_begin("gemm");
+  if (!k::gemm_gelu(d->f32(), w->f32(), out->f32(), h->f32(), (int)M, (int)N, (int)K, true, true, stream(),
+                    D ? D->f32() : nullptr))
+    fail("malus: gelu matmul VJP: no fused GEMM for %zux%zux%zu", M, N, K);
+  ktimer_end(kt, 2.0 * M * N * K);
+  return done(out, "gelu_matmul_bwd");
+}
+
 // dA = dout @ op(B)^T
 int64_t matmul_bwd_a_impl(int64_t ha, int64_t hb, int64_t hd, const TensorBuffer* D) {
   TensorBuffer *a = T(ha), *b = T(hb), *d = T(hd);

@@ -35,8 +35,11 @@ enum OpTag : int32_t {
 //            leaves are released before backward, so no gradient reaches them
 //   LayerNormScale (x, w; y, var) -> out: layernorm(x, axis=-1) * w, with the
 //            normalized rows y and the keepdim variance saved
+//   GeluMatmul (h, W; ge) -> out: gelu(h) @ W, with ge = gelu(h) saved
 // meta holds {B, T, H} for HeadProj, AttnOut and Attention.
-enum FusedTag : int32_t { HeadProj = 100, Scores = 101, AttnOut = 102, Attention = 103, LayerNormScale = 104 };
+enum FusedTag : int32_t {
+  HeadProj = 100, Scores = 101, AttnOut = 102, Attention = 103, LayerNormScale = 104, GeluMatmul = 105
+};
 
 enum BwdSlot : int32_t {
   AddBwdA = 0, AddBwdB, SubBwdA, SubBwdB, MulBwdA, MulBwdB, DivBwdA, DivBwdB, SigmoidBwd, ReluBwd, TanhBwd, ExpBwd,
@@ -127,7 +130,7 @@ void need_values(int64_t h) {
 int diff_inputs(int32_t op) {
   if (op == Attention) return 3;
   if (op == Matmul || op == Add || op == Sub || op == Mul || op == Div || op == HeadProj || op == Scores ||
-      op == AttnOut || op == LayerNormScale)
+      op == AttnOut || op == LayerNormScale || op == GeluMatmul)
     return 2;
   return 1;
 }
@@ -303,8 +306,8 @@ using namespace malus;
 namespace malus {
 void tape_record_fused(int32_t op, const std::vector<int64_t>& saved, int64_t out, const std::vector<int64_t>& meta) {
   if (!t_recording) return;
-  const size_t want = op == Attention ? 5 : op == LayerNormScale ? 4 : 2;
-  if (op < HeadProj || op > LayerNormScale) fail("malus: unknown fused op tag %d", op);
+  const size_t want = op == Attention ? 5 : op == LayerNormScale ? 4 : op == GeluMatmul ? 3 : 2;
+  if (op < HeadProj || op > GeluMatmul) fail("malus: unknown fused op tag %d", op);
   if (saved.size() != want) fail("malus: fused op %d takes %zu saved handles, got %zu", op, want, saved.size());
   for (int64_t h : saved) retain(T(h));
   retain(T(out));
@@ -484,6 +487,15 @@ void backward(int64_t loss) {
           if (nb) fold_grad(grads, kk, [&](const TensorBuffer* o) { return scores_bwd_k(ds, q, o, true); });
           release(T(ds));
         }
+        break;
+      }
+      case GeluMatmul: {  // saved {h, W, ge}: the matmul's VJPs (dge, then dW), then the GELU VJP of dge
+        const int64_t h = n.saved[0], w = n.saved[1], ge = n.saved[2];
+        need_values(h);
+        need_values(w);
+        need_values(ge);
+        if (na) fold_grad(grads, h, [&](const TensorBuffer* o) { return gelu_matmul_bwd_h(dout, w, h, o); });
+        if (nb) fold_grad(grads, w, [&](const TensorBuffer* o) { return matmul_bwd_b_impl(ge, w, dout, o); });
         break;
       }
       case LayerNormScale: {  // saved {x, w, y, var}
