@@ -58,14 +58,22 @@ __global__ __launch_bounds__(256) void k_adam_l2(const float* __restrict__ p, co
     adam_one(p[i], g[i], m[i], v[i], a, po[i], mo[i], vo[i]);
 }
 
-// Multi-tensor form: one launch updates every parameter tensor.  Block b
-// takes chunk[b] = (segment, first float) and covers 4096 floats of that
-// segment (1024 float4, four per thread); chunks never straddle segments.
-__global__ __launch_bounds__(256) void k_adam_l2_multi(const AdamSeg* __restrict__ segs, const uint2* __restrict__ chunks,
-                                                       AdamArgs a) {
-  const uint2 ch = chunks[blockIdx.x];
-  const AdamSeg sg = segs[ch.x];
-  const size_t first = ch.y, n = sg.n;
+// Multi-tensor form: one launch updates up to kAdamMaxSegs parameter
+// tensors.  The segment table travels by value in the kernel arguments (no
+// upload).  Block b covers 4096 floats (1024 float4, four per thread) of the
+// segment whose chunk range holds b; chunks never straddle segments.
+constexpr int kAdamMaxSegs = 16;
+struct AdamTable {
+  AdamSeg seg[kAdamMaxSegs];
+  uint32_t first_chunk[kAdamMaxSegs + 1];  // prefix sums of the segments' chunk counts
+  int count;
+};
+
+__global__ __launch_bounds__(256) void k_adam_l2_multi(const AdamTable t, AdamArgs a) {
+  int si = 0;
+  while (si + 1 < t.count && blockIdx.x >= t.first_chunk[si + 1]) ++si;
+  const AdamSeg& sg = t.seg[si];
+  const size_t first = (size_t)(blockIdx.x - t.first_chunk[si]) * kAdamChunk, n = sg.n;
   const size_t end = first + kAdamChunk < n ? first + kAdamChunk : n;
   if ((n & 3) == 0) {  // float4 path (segment bases are 256-byte aligned)
     for (size_t i = first / 4 + threadIdx.x; i < end / 4; i += blockDim.x) {
@@ -90,23 +98,22 @@ __global__ __launch_bounds__(256) void k_adam_l2_multi(const AdamSeg* __restrict
 
 void adam_l2_multi(const AdamSeg* segs_host, int count, float lr, float b1, float b2, float omb1, float omb2, float bc1,
                    float bc2, float eps, float wd, hipStream_t s) {
-  std::vector<uint2> chunks;
-  for (int i = 0; i < count; ++i)
-    for (size_t f = 0; f < segs_host[i].n; f += kAdamChunk) chunks.push_back(make_uint2((unsigned)i, (unsigned)f));
-  if (chunks.empty()) return;
-  if (chunks.size() > 0x7fffffffu) fail("malus: adam update: too many parameters");
-  // segment table and chunk table ride one device buffer
-  const size_t seg_bytes = (size_t)count * sizeof(AdamSeg), chunk_bytes = chunks.size() * sizeof(uint2);
-  const size_t off = (seg_bytes + 255) / 256 * 256;
-  size_t bucket;
-  char* dev = static_cast<char*>(pool_alloc(off + chunk_bytes, &bucket));
-  upload(dev, segs_host, seg_bytes);
-  upload(dev + off, chunks.data(), chunk_bytes);
-  AdamArgs a{lr, b1, b2, omb1, omb2, bc1, bc2, eps, wd};
-  k_adam_l2_multi<<<(unsigned)chunks.size(), 256, 0, s>>>(reinterpret_cast<const AdamSeg*>(dev),
-                                                          reinterpret_cast<const uint2*>(dev + off), a);
-  MALUS_HIP(hipGetLastError());
-  pool_free(dev, bucket);  // stream order keeps it alive until the kernel has read it
+  const AdamArgs a{lr, b1, b2, omb1, omb2, bc1, bc2, eps, wd};
+  for (int base = 0; base < count; base += kAdamMaxSegs) {
+    AdamTable t{};
+    t.count = count - base < kAdamMaxSegs ? count - base : kAdamMaxSegs;
+    size_t chunks = 0;
+    for (int i = 0; i < t.count; ++i) {
+      t.seg[i] = segs_host[base + i];
+      t.first_chunk[i] = (uint32_t)chunks;
+      chunks += (t.seg[i].n + kAdamChunk - 1) / kAdamChunk;
+    }
+    t.first_chunk[t.count] = (uint32_t)chunks;
+    if (chunks == 0) continue;
+    if (chunks > 0x7fffffffu) fail("malus: adam update: too many parameters");
+    k_adam_l2_multi<<<(unsigned)chunks, 256, 0, s>>>(t, a);
+    MALUS_HIP(hipGetLastError());
+  }
 }
 
 void adam_l2(const float* p, const float* g, const float* m, const float* v, float* p_out, float* m_out, float* v_out,

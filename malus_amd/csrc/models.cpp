@@ -115,6 +115,7 @@ struct Gpt {
   bool fused_fwd = true;  // forward fusions: scale+mask+softmax, residual adds in GEMM epilogues (same values, same tape)
   std::vector<int64_t> p, m, v;  // block l params at 8l..8l+7, then wte, wpe, ln_f, lm_head
   int64_t pos = 0;               // [B*T] i32 position ids
+  int64_t attn_scale = 0;        // [1,1] 1/sqrt(hs) of the fused attention (built on first use)
 
   int np() const { return 8 * L + 4; }
   int64_t& top(int j) { return p[8 * L + j]; }
@@ -147,14 +148,29 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   int64_t K = head_fold(P[2]);
   int64_t Vv = head_fold(P[3]);
   int64_t Kt = fused_heads ? 0 : permute(K, {0, 2, 1});
-  size_t s11[2] = {1, 1};
-  int64_t ones11 = tensor_alloc_ones_gpu(s11, 2);
-  int64_t scale = malus_std_scalar_op(k::MUL, ones11, 1.0f / sqrtf((float)hs), 1);  // ones(1,1) * (1/sqrt(hs))
-  tensor_release(ones11);
-  tape_register_leaf(scale);  // variable(...)
+  const bool fused_attention = fused_heads && k::attn_scores_supported(B * H, Tn, hs);
+  int64_t scale;
+  if (fused_attention) {
+    // variable(ones(1,1) * (1/sqrt(hs))) is the same value every forward and
+    // receives no gradient in the fused form: build it once per model
+    if (!g.attn_scale) {
+      size_t s11[2] = {1, 1};
+      int64_t ones11 = tensor_alloc_ones_gpu(s11, 2);
+      g.attn_scale = malus_std_scalar_op(k::MUL, ones11, 1.0f / sqrtf((float)hs), 1);
+      tensor_release(ones11);
+    }
+    scale = g.attn_scale;
+    tensor_retain(scale);
+  } else {
+    size_t s11[2] = {1, 1};
+    int64_t ones11 = tensor_alloc_ones_gpu(s11, 2);
+    scale = malus_std_scalar_op(k::MUL, ones11, 1.0f / sqrtf((float)hs), 1);  // ones(1,1) * (1/sqrt(hs))
+    tensor_release(ones11);
+    tape_register_leaf(scale);  // variable(...)
+  }
   const size_t sshape[3] = {B * H, Tn, Tn};
   int64_t S = 0, mask = 0, Ss = 0, Sm = 0, Pm = 0, AO = 0, ao4 = 0, aop = 0, att;
-  if (fused_heads && k::attn_scores_supported(B * H, Tn, hs)) {
+  if (fused_attention) {
     // Fused causal attention: S = Q @ K^T, scale, causal mask and softmax in
     // one kernel (P stored), att = P @ V written straight into [B*T, C], and
     // one tape node whose VJP runs the fused scores backward.  The causal
@@ -411,6 +427,7 @@ void malus_gpt_free(void* gp) {
   if (!g) return;
   for (size_t i = 0; i < g->p.size(); ++i) rel({g->p[i], g->m[i], g->v[i]});
   tensor_release(g->pos);
+  tensor_release(g->attn_scale);
   delete g;
   API_CATCH()
 }

@@ -203,6 +203,8 @@ void sync_all() {
 uint64_t enqueue_mark(const char* op_name) {
   Context& c = ctx();
   uint64_t s = ++c.seq;
+  static const bool trace = getenv("MALUS_OP_TRACE") != nullptr;  // one line per enqueued op (instrumentation)
+  if (trace) fprintf(stderr, "malus op %s\n", op_name);
   if (c.sync_dispatch) {
     hipError_t e = hipStreamSynchronize(c.stream);
     if (e != hipSuccess) fail("malus: GPU op '%s' failed: %s", op_name, hipGetErrorString(e));
