@@ -196,7 +196,17 @@ struct GemmLayout { GemmMap b, r, c; };
 // zeros above the diagonal (causal attention probabilities and their
 // gradients); a tile then skips the k slabs whose A values are all zero,
 // which leaves every sum's value unchanged.
-struct GemmLayouts { GemmLayout a, b, c; int ext_a, ext_b; int tri_a = 0; };
+// ngroup > 1 (gemm_grouped): up to 3 products with this one shape and
+// layout, group g reading ga[g] / gb[g] and writing gc[g].
+struct GemmLayouts {
+  GemmLayout a, b, c;
+  int ext_a, ext_b;
+  int tri_a = 0;
+  int ngroup = 1;
+  const float* ga[3] = {nullptr, nullptr, nullptr};
+  const float* gb[3] = {nullptr, nullptr, nullptr};
+  float* gc[3] = {nullptr, nullptr, nullptr};
+};
 inline GemmLayout dense_layout(long ld, long batch_stride) {
   return {{0, 0, (int)batch_stride}, {0, 0, (int)ld}, {0, 0, 1}};
 }
@@ -221,6 +231,16 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
 //   kernels round it.
 bool gemm_gelu(const float* A, const float* B, float* C, float* E, int M, int N, int K, bool transB, bool backward,
                hipStream_t s, const float* D = nullptr);
+// Grouped GEMMs on the mapped LDS-DMA kernel (batch 1): L.ngroup products
+// of one shape and layout, operands L.ga / L.gb.
+//   accumulate = false: L.gc[g] = op(A_g) @ op(B_g), all groups in one
+//     launch (split-K as for a single product of the shape);
+//   accumulate = true: C = ((D + op(A_0) @ op(B_0)) + op(A_1) @ op(B_1)) + ...,
+//     each product rounded to f32 before its add, as one GEMM per group with
+//     chained addends would round (no split).
+// Returns false, launching nothing, where gemm_mapped would.
+bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayouts& L, float* C, bool accumulate,
+                  hipStream_t s, const float* D = nullptr, double* flops = nullptr);
 // flops (optional): the multiply-add work launched (less than 2 M N K when
 // tri_a skips zero slabs).
 bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,

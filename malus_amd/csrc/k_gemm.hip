@@ -316,7 +316,11 @@ struct DmaSlab {
 // offset below 2^31; a split-K launch writes dense partials.
 // EPI: 0 plain; 1 also E = gelu(C) (the GELU after a GEMM, no D); 2 C =
 // gelu_bwd(E, product) (+ D): the GELU VJP applied to the product, with E
-// the GELU input.  E shares C's layout.
+// the GELU input; 3 accumulate L.ngroup products in group order,
+// C = ((D + A0 op B0) + A1 op B1) + ..., each product rounded to f32 before
+// its add (the rounding of one GEMM per group with its addend chained).
+// E shares C's layout.  Grouped launches (L.ngroup > 1, MAP only): with
+// EPI != 3, workgroup z runs group z (its own A, B, C); the batch index is 0.
 template <int TM, int TN, bool TA, bool TB, bool MAP, int EPI = 0>
 __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int M, int N, int K, GemmLayouts L,
@@ -334,13 +338,17 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   if ((nt & 7) == 0) tile = (tile & 7) * (nt >> 3) + (tile >> 3);  // XCD-contiguous tile ranges
   const int tm = tile / tiles_n, tn = tile % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
-  const int b = blockIdx.z;
+  const bool grouped = MAP && L.ngroup > 1;
+  const int b = grouped ? 0 : blockIdx.z;
+  if (grouped && EPI != 3) {
+    A = L.ga[blockIdx.z];
+    B = L.gb[blockIdx.z];
+    C = L.gc[blockIdx.z];
+  }
   const int ba = map_at<MAP>(L.a.b, b), bb = map_at<MAP>(L.b.b, b);
-  A += ba;
-  B += bb;
   C += map_at<MAP>(L.c.b, b) + (long)blockIdx.y * split_stride;
   if (D) D += map_at<MAP>(L.c.b, b);
-  if (EPI) E += map_at<MAP>(L.c.b, b);
+  if (EPI == 1 || EPI == 2) E += map_at<MAP>(L.c.b, b);
   int kbeg = blockIdx.y * k_chunk;
   int kend = min(K, kbeg + k_chunk);
   if (MAP && L.tri_a) {  // op(A) row m is zero past k = m (A) or before k = m (A^T stored lower-triangular)
@@ -356,81 +364,112 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   const GemmMap& fak = TA ? L.a.r : L.a.c;
   const GemmMap& fbn = TB ? L.b.r : L.b.c;
   const GemmMap& fbk = TB ? L.b.c : L.b.r;
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, (unsigned)((L.ext_a - ba) * 4));
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(B, (unsigned)((L.ext_b - bb) * 4));
   SlabA sa;
   SlabB sb;
   sa.template init<MAP>(m0, fam, fak, wave, lane);
   sb.template init<MAP>(n0, fbn, fbk, wave, lane);
 
   v16f acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = v16f{0};
-
   const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
-  KCursor<MAP> ka, kb;
-  ka.init(fak, kbeg);
-  kb.init(fbk, kbeg);
-  if (nk > 0) {
-    sa.issue(ra, As[0], wave, ka.bytes(fak));
-    sb.issue(rb, Bs[0], wave, kb.bytes(fbk));
-    ka.advance(fak);
-    kb.advance(fbk);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    float fa[TM][8], fb[TN][8];
+  // acc = op(A) @ op(B) over [kbeg, kend) for operands Ap, Bp
+  auto run_k = [&](const float* Ap, const float* Bp) {
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(Ap + ba, (unsigned)((L.ext_a - ba) * 4));
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(Bp + bb, (unsigned)((L.ext_b - bb) * 4));
 #pragma unroll
-    for (int i = 0; i < TM; ++i) SlabA::frag(As[cur], wm + 32 * i, fa[i]);
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur], wn + 32 * j, fb[j]);
-    __builtin_amdgcn_sched_barrier(0);
-    // the other buffer was last read before the previous barrier
-    if (kt + 1 < nk) {
-      sa.issue(ra, As[cur ^ 1], wave, ka.bytes(fak));
-      sb.issue(rb, Bs[cur ^ 1], wave, kb.bytes(fbk));
+      for (int j = 0; j < TN; ++j) acc[i][j] = v16f{0};
+    KCursor<MAP> ka, kb;
+    ka.init(fak, kbeg);
+    kb.init(fbk, kbeg);
+    if (nk > 0) {
+      sa.issue(ra, As[0], wave, ka.bytes(fak));
+      sb.issue(rb, Bs[0], wave, kb.bytes(fbk));
       ka.advance(fak);
       kb.advance(fbk);
     }
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs ahead of the wait below
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-  }
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      float fa[TM][8], fb[TN][8];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) SlabA::frag(As[cur], wm + 32 * i, fa[i]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur], wn + 32 * j, fb[j]);
+      __builtin_amdgcn_sched_barrier(0);
+      // the other buffer was last read before the previous barrier
+      if (kt + 1 < nk) {
+        sa.issue(ra, As[cur ^ 1], wave, ka.bytes(fak));
+        sb.issue(rb, Bs[cur ^ 1], wave, kb.bytes(fbk));
+        ka.advance(fak);
+        kb.advance(fbk);
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs ahead of the wait below
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+  };
 
-  // C rows come in aligned 32-row groups (the host keeps the row map's div
-  // a multiple of 32), so one map evaluation per group and per column
+  // Element (i, j, r) of the wave's accumulators is C at offset
+  // cn(i, j) + dm(r) * row stride; C rows come in aligned 32-row groups (the
+  // host keeps the row map's div a multiple of 32), so one map evaluation
+  // per group and per column.
+  auto for_each = [&](auto&& f) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int rbase = map_at<MAP>(L.c.r, m0 + wm + 32 * i);
+    for (int i = 0; i < TM; ++i) {
+      const int rbase = map_at<MAP>(L.c.r, m0 + wm + 32 * i);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn + 32 * j + li;
-      if (n < N) {
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wn + 32 * j + li;
         const int cn = map_at<MAP>(L.c.c, n) + rbase;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int dm = 8 * (r >> 2) + 4 * lk + (r & 3);
           const int m = m0 + wm + 32 * i + dm;
-          const int o = cn + dm * L.c.r.s0;
-          if (m < M) {
-            float v = acc[i][j][r];
-            if (EPI == 2) v = gelu_bwd(E[o], v);
-            C[o] = D ? D[o] + v : v;
-            if (EPI == 1) E[o] = gelu_fwd(v);
-          }
+          f(i, j, r, n < N && m < M, cn + dm * L.c.r.s0);
         }
       }
     }
+  };
+
+  if constexpr (EPI == 3) {
+    v16f tot[TM][TN];
+    for (int g = 0; g < L.ngroup; ++g) {
+      run_k(L.ga[g], L.gb[g]);
+      if (g == 0) {
+        for_each([&](int i, int j, int r, bool live, int o) {
+          tot[i][j][r] = D && live ? D[o] + acc[i][j][r] : acc[i][j][r];
+        });
+      } else {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tot[i][j][r] = tot[i][j][r] + acc[i][j][r];
+      }
+    }
+    for_each([&](int i, int j, int r, bool live, int o) {
+      if (live) C[o] = tot[i][j][r];
+    });
+  } else {
+    run_k(A, B);
+    for_each([&](int i, int j, int r, bool live, int o) {
+      if (live) {
+        float v = acc[i][j][r];
+        if (EPI == 2) v = gelu_bwd(E[o], v);
+        C[o] = D ? D[o] + v : v;
+        if (EPI == 1) E[o] = gelu_fwd(v);
+      }
+    });
   }
 #endif
 }
@@ -481,6 +520,10 @@ inline int variant(bool ta, bool tb, bool va, bool vb, bool dma) {
 
 template <int TM, int TN, bool TA, bool TB>
 const void* kernel_of(int v) {
+  if (v & 128) {  // grouped accumulation: mapped NT (the head projections' dA)
+    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, true, 3>);
+    return nullptr;
+  }
   if (v & 64) {  // GELU epilogues: dense NN (forward) and NT (the VJP's dA)
     if constexpr (!TA && !TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, false, false, 1>);
     if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, false, 2>);
@@ -517,7 +560,7 @@ const void* kernel_for(int ti, int v) {
 // Co-resident workgroups per CU of each kernel variant (VGPR and LDS
 // limited), from the runtime's occupancy calculator; cached per variant.
 int occupancy(int ti, int v) {
-  static int cache[kNumTiles][128];
+  static int cache[kNumTiles][256];
   int& o = cache[ti][v];
   if (o == 0) {
     int n = 0;
@@ -621,7 +664,8 @@ void trace_plan(int batch, int M, int N, int K, bool transA, bool transB, bool d
 
 // Sum the split-K partials into C (+ D) in split order, then return the
 // partial buffer to the pool.
-void split_reduce(float* partial, float* C, size_t mn, int nsplit, const float* D, hipStream_t s, size_t bucket) {
+void split_reduce(float* partial, float* C, size_t mn, int nsplit, const float* D, hipStream_t s, size_t bucket,
+                  bool release = true) {
   const bool vec = mn % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(partial) & 15) == 0 && (reinterpret_cast<uintptr_t>(D) & 15) == 0;
   if (vec) {
@@ -635,7 +679,7 @@ void split_reduce(float* partial, float* C, size_t mn, int nsplit, const float* 
     k_split_reduce<<<(unsigned)blocks, 256, 0, s>>>(partial, C, mn, nsplit, D);
   }
   MALUS_HIP(hipGetLastError());
-  pool_free(partial, bucket);
+  if (release) pool_free(partial, bucket);
 }
 
 // One LDS-DMA launch (plus the split-K reduction); a split writes dense
@@ -748,8 +792,72 @@ bool gemm_gelu(const float* A, const float* B, float* C, float* E, int M, int N,
   return true;
 }
 
+namespace {
+bool mapped_ok(int batch, int M, int N, int K, bool transA, bool transB, const GemmLayouts& L);
+}
+
+bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayouts& Lin, float* C, bool accumulate,
+                  hipStream_t s, const float* D, double* flops) {
+  if (Lin.ngroup < 1 || Lin.ngroup > 3 || Lin.tri_a || !mapped_ok(1, M, N, K, transA, transB, Lin)) return false;
+  if (accumulate && !(!transA && transB)) return false;  // built for the projections' dA (NT) only
+  GemmLayouts L = Lin;
+  const int v = variant(transA, transB, false, false, true);
+  Plan p = plan_gemm(1, M, N, K, v);
+  const bool c_dense = L.c.r.div == 0 && L.c.c.div == 0 && L.c.c.s0 == 1 && L.c.r.s0 == N;
+  if (accumulate || !c_dense) {
+    p.nsplit = 1;
+    p.k_chunk = K;
+  }
+  static const bool trace = getenv("MALUS_GEMM_TRACE") != nullptr;
+  if (trace)
+    fprintf(stderr, "malus gemm b1 %dx%dx%d t%d%d -> dma grouped%d%s tile %dx%d occ %d split %d k_chunk %d\n", M, N, K,
+            transA, transB, L.ngroup, accumulate ? " acc" : "", 64 * kTiles[p.ti].tm, 64 * kTiles[p.ti].tn,
+            occupancy(p.ti, v), p.nsplit, p.k_chunk);
+  const int bm = 64 * kTiles[p.ti].tm, bn = 64 * kTiles[p.ti].tn;
+  const int tiles_n = (N + bn - 1) / bn, tiles = ((M + bm - 1) / bm) * tiles_n;
+  int nsplit = p.nsplit, k_chunk = p.k_chunk;
+  const size_t mn = (size_t)M * N;
+  size_t bucket = 0;
+  float* partial = nullptr;
+  float* outs[3] = {L.gc[0], L.gc[1], L.gc[2]};
+  if (nsplit > 1) {
+    partial = static_cast<float*>(pool_alloc(mn * nsplit * L.ngroup * sizeof(float), &bucket));
+    for (int g = 0; g < L.ngroup; ++g) L.gc[g] = partial + (size_t)g * nsplit * mn;
+    L.c = dense_layout(N, 0);
+  }
+  long split_stride = nsplit > 1 ? (long)mn : 0;
+  const float* Dk = accumulate ? D : nullptr;
+  float* E = nullptr;
+  float* Cp = accumulate ? C : L.gc[0];
+  const float *A0 = L.ga[0], *B0 = L.gb[0];
+  void* args[] = {&A0, &B0, &Cp, &M, &N, &K, &L, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk, &E};
+  const void* fn = kernel_for(p.ti, accumulate ? v | 128 : v | 32);
+  if (!fn) fail("malus: gemm_grouped: no kernel for transA=%d transB=%d", transA, transB);
+  MALUS_HIP(hipLaunchKernel(fn, dim3((unsigned)tiles, (unsigned)nsplit, accumulate ? 1u : (unsigned)L.ngroup), dim3(256),
+                            args, 0, s));
+  if (nsplit > 1) {
+    for (int g = 0; g < L.ngroup; ++g) {
+      size_t none = 0;
+      split_reduce(L.gc[g], outs[g], mn, nsplit, nullptr, s, none, false);
+    }
+    pool_free(partial, bucket);
+  }
+  if (flops) *flops = 2.0 * L.ngroup * (double)M * N * K;
+  return true;
+}
+
 bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
                  const GemmLayouts& L, hipStream_t s, const float* D, double* flops) {
+  if (!mapped_ok(batch, M, N, K, transA, transB, L)) return false;
+  if (L.tri_a && M != K) return false;
+  const bool c_dense = L.c.r.div == 0 && L.c.c.div == 0 && L.c.c.s0 == 1 && L.c.r.s0 == N;
+  const double f = launch_dma(A, B, C, batch, M, N, K, transA, transB, L, s, D, c_dense && batch == 1 && !L.tri_a, true);
+  if (flops) *flops = f;
+  return true;
+}
+
+namespace {
+bool mapped_ok(int batch, int M, int N, int K, bool transA, bool transB, const GemmLayouts& L) {
   if (batch <= 0 || M <= 0 || N <= 0 || K <= 0 || batch > 65535 || K % 16 || !g_allow_dma) return false;
   // contiguous dimension of each stored operand: runs of 4 floats
   const GemmMap& a_contig = L.a.c;  // A [M][K]: k;  A^T [K][M]: m
@@ -767,12 +875,9 @@ bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int
   const long eb = map_max(L.b.b, batch) + map_max(L.b.r, transB ? N : K) + map_max(L.b.c, transB ? K : N) + 1;
   const long ec = map_max(L.c.b, batch) + map_max(L.c.r, (M + 127) / 128 * 128) + map_max(L.c.c, N) + 1;
   if (ea > L.ext_a || eb > L.ext_b || L.ext_a >= lim || L.ext_b >= lim || ec >= lim) return false;
-  if (L.tri_a && M != K) return false;
-  const bool c_dense = L.c.r.div == 0 && L.c.c.div == 0 && L.c.c.s0 == 1 && L.c.r.s0 == N;
-  const double f = launch_dma(A, B, C, batch, M, N, K, transA, transB, L, s, D, c_dense && batch == 1 && !L.tri_a, true);
-  if (flops) *flops = f;
   return true;
 }
+}  // namespace
 
 }  // namespace k
 }  // namespace malus

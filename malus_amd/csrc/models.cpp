@@ -144,9 +144,20 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
     rel({q, q4, qp});
     return Q;
   };
-  int64_t Q = head_fold(P[1]);
-  int64_t K = head_fold(P[2]);
-  int64_t Vv = head_fold(P[3]);
+  int64_t Q, K, Vv;
+  if (fused_heads) {  // the three projections in one grouped launch, three tape nodes
+    const int64_t w[3] = {P[1], P[2], P[3]};
+    int64_t qkv[3];
+    head_proj_fwd3(xn1, w, B, Tn, H, qkv);
+    for (int i = 0; i < 3; ++i) tape_record_fused(TAG_HEAD_PROJ, {xn1, w[i]}, qkv[i], {(int64_t)B, (int64_t)Tn, (int64_t)H});
+    Q = qkv[0];
+    K = qkv[1];
+    Vv = qkv[2];
+  } else {
+    Q = head_fold(P[1]);
+    K = head_fold(P[2]);
+    Vv = head_fold(P[3]);
+  }
   int64_t Kt = fused_heads ? 0 : permute(K, {0, 2, 1});
   const bool fused_attention = fused_heads && k::attn_scores_supported(B * H, Tn, hs);
   int64_t scale;

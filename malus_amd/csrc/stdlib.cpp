@@ -880,6 +880,85 @@ int64_t head_proj_bwd_w(int64_t hx, int64_t hdq, size_t B, size_t T, size_t H, c
                 (int)dq->len};
   return mapped(x, dq, c, true, false, 1, (int)Cin, (int)C, (int)N, L, D, "head_proj_bwd_w");
 }
+// Qh_g = heads(x @ W_g) for three weights in one launch.
+void head_proj_fwd3(int64_t hx, const int64_t* hw, size_t B, size_t T, size_t H, int64_t* out) {
+  TensorBuffer* x = T_(hx);
+  TensorBuffer* w0 = T_(hw[0]);
+  const size_t C = w0->shape[1], hs = C / H, N = B * T;
+  const size_t sh[3] = {B * H, T, hs};
+  GemmLayouts L{dense_layout((long)x->shape[1], 0), dense_layout((long)C, 0), heads_as_rows(T, H, hs), (int)x->len,
+                (int)w0->len};
+  L.ngroup = 3;
+  TensorBuffer* o[3];
+  for (int g = 0; g < 3; ++g) {
+    if (T_(hw[g])->len != w0->len) fail("malus: head_proj_fwd3: weights differ in shape");
+    o[g] = alloc_tensor(F32, sh, 3);
+    L.ga[g] = x->f32();
+    L.gb[g] = T_(hw[g])->f32();
+    L.gc[g] = o[g]->f32();
+  }
+  KTimer* kt = ktimer_begin("gemm");
+  double flops = 0;
+  if (!k::gemm_grouped((int)N, (int)C, (int)w0->shape[0], false, false, L, nullptr, false, stream(), nullptr, &flops))
+    fail("malus: head_proj_fwd3: grouped GEMM rejected");
+  ktimer_end(kt, flops);
+  const uint64_t seq = enqueue_mark("head_proj3");
+  for (int g = 0; g < 3; ++g) {
+    o[g]->write_seq = seq;
+    out[g] = malus::H(o[g]);
+  }
+}
+
+// The three projections of one input (q, k, v) in one launch each:
+// dx = ((D + unheads(dQh_0) @ W_0^T) + unheads(dQh_1) @ W_1^T) + unheads(dQh_2) @ W_2^T,
+// in the given group order (the tape's order), and dW_g = x^T @ unheads(dQh_g).
+int64_t head_proj_bwd_x3(const int64_t* hdq, const int64_t* hw, size_t B, size_t T, size_t H, const TensorBuffer* D) {
+  TensorBuffer* w0 = T_(hw[0]);
+  const size_t Cin = w0->shape[0], C = w0->shape[1], hs = C / H, N = B * T;
+  const size_t sh[2] = {N, Cin};
+  TensorBuffer* c = alloc_tensor(F32, sh, 2);
+  check_addend(D, c);
+  GemmLayouts L{heads_as_rows(T, H, hs), dense_layout((long)C, 0), dense_layout((long)Cin, 0), (int)T_(hdq[0])->len,
+                (int)w0->len};
+  L.ngroup = 3;
+  for (int g = 0; g < 3; ++g) {
+    L.ga[g] = T_(hdq[g])->f32();
+    L.gb[g] = T_(hw[g])->f32();
+  }
+  KTimer* kt = ktimer_begin("gemm");
+  double flops = 0;
+  if (!k::gemm_grouped((int)N, (int)Cin, (int)C, false, true, L, c->f32(), true, stream(), D ? D->f32() : nullptr,
+                       &flops))
+    fail("malus: head_proj_bwd_x3: grouped GEMM rejected");
+  ktimer_end(kt, flops);
+  return done(c, "head_proj_bwd_x3");
+}
+void head_proj_bwd_w3(int64_t hx, const int64_t* hdq, size_t B, size_t T, size_t H, int64_t* out) {
+  TensorBuffer* x = T_(hx);
+  const size_t Cin = x->shape[1], hs = T_(hdq[0])->shape[2], C = H * hs, N = B * T;
+  const size_t sh[2] = {Cin, C};
+  GemmLayouts L{dense_layout((long)Cin, 0), heads_as_rows(T, H, hs), dense_layout((long)C, 0), (int)x->len,
+                (int)T_(hdq[0])->len};
+  L.ngroup = 3;
+  TensorBuffer* o[3];
+  for (int g = 0; g < 3; ++g) {
+    o[g] = alloc_tensor(F32, sh, 2);
+    L.ga[g] = x->f32();
+    L.gb[g] = T_(hdq[g])->f32();
+    L.gc[g] = o[g]->f32();
+  }
+  KTimer* kt = ktimer_begin("gemm");
+  double flops = 0;
+  if (!k::gemm_grouped((int)Cin, (int)C, (int)N, true, false, L, nullptr, false, stream(), nullptr, &flops))
+    fail("malus: head_proj_bwd_w3: grouped GEMM rejected");
+  ktimer_end(kt, flops);
+  const uint64_t seq = enqueue_mark("head_proj_bwd_w3");
+  for (int g = 0; g < 3; ++g) {
+    o[g]->write_seq = seq;
+    out[g] = malus::H(o[g]);
+  }
+}
+
 // att = unheads(P @ V): P [B*H, T, T], V [B*H, T, hs] -> [B*T, H*hs]
 int64_t attn_out_fwd(int64_t hp, int64_t hv, size_t B, size_t T, size_t H, bool causal) {
   TensorBuffer *p = T_(hp), *v = T_(hv);

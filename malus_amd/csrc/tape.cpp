@@ -7,6 +7,7 @@
 // library's stdlib host functions, and a JIT can overwrite them through
 // tape_register_backward_fn exactly as compile_and_run does.
 #include <cstdint>
+#include <iterator>
 #include <unordered_map>
 #include <unordered_set>
 #include <vector>
@@ -461,6 +462,33 @@ void backward(int64_t loss) {
     const bool nb = ni > 1 && need(n.saved[1]);
     const bool nc = ni > 2 && need(n.saved[2]);
     if (!na && !nb && !nc) continue;
+    if (n.op == HeadProj && std::distance(it, nodes.rend()) >= 3) {
+      // The q, k, v projections of one input sit back to back on the tape:
+      // run their three VJPs as one grouped launch each for dx (accumulated
+      // in this same order) and for the three dW (same values as one node
+      // at a time).
+      const TapeNode &n1 = *(it + 1), &n2 = *(it + 2);
+      const int64_t x = n.saved[0];
+      auto g1 = grads.find(n1.output), g2 = grads.find(n2.output);
+      const bool grouped = n1.op == HeadProj && n2.op == HeadProj && n1.saved[0] == x && n2.saved[0] == x &&
+                           n1.meta == n.meta && n2.meta == n.meta && g1 != grads.end() && g2 != grads.end() && na &&
+                           need(n.saved[1]) && need(n1.saved[1]) && need(n2.saved[1]) && !grads.count(n.saved[1]) &&
+                           !grads.count(n1.saved[1]) && !grads.count(n2.saved[1]) &&
+                           slot_is(GradAcc, &malus_std_broadcast_add_fwd);
+      if (grouped) {
+        const int64_t dq[3] = {dout, g1->second, g2->second};
+        const int64_t w[3] = {n.saved[1], n1.saved[1], n2.saved[1]};
+        for (int64_t h : w) need_values(h);
+        need_values(x);
+        const size_t Bm = (size_t)n.meta[0], Tm = (size_t)n.meta[1], Hm = (size_t)n.meta[2];
+        fold_grad(grads, x, [&](const TensorBuffer* o) { return head_proj_bwd_x3(dq, w, Bm, Tm, Hm, o); });
+        int64_t dw[3];
+        head_proj_bwd_w3(x, dq, Bm, Tm, Hm, dw);
+        for (int i = 0; i < 3; ++i) grads.emplace(w[i], dw[i]);
+        it += 2;
+        continue;
+      }
+    }
     switch (n.op) {
       case Matmul: {
         int64_t a = n.saved[0], b = n.saved[1];
