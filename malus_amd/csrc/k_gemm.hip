@@ -230,6 +230,9 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
 // Buffer loads past the descriptor's byte count return 0; other reads past a
 // matrix edge only feed output rows/columns that are never stored.
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) const float lds_float;
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
 #if defined(__HIP_DEVICE_COMPILE__)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* p, unsigned bytes) {
@@ -259,6 +262,14 @@ struct KCursor {
     if (MAP && f.div && r == f.div) { r = 0; ++q; }
   }
 };
+
+// s_waitcnt with vmcnt = N and no wait on the other counters (gfx9
+// encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
+template <int N>
+__device__ __forceinline__ void waitcnt_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 template <int BX, bool KC>
 struct DmaSlab {
@@ -294,18 +305,35 @@ struct DmaSlab {
   }
 #endif
   // The 8 MFMA-step values (k = 8h .. 8h + 7) of lane (i, h) for tile rows xw ..
+  // The reads are inline asm: the compiler treats any LDS read after an
+  // LDS-DMA load as a possible alias of it and would wait for every DMA in
+  // flight, including the slabs prefetched into other stages.  The caller
+  // waits (lgkmcnt) before the values are used.
   __device__ __forceinline__ static void frag(const float* __restrict__ S, int xw, float f[8]) {
+#if defined(__HIP_DEVICE_COMPILE__)
     const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+    const unsigned base = (unsigned)(uintptr_t)(const lds_float*)S;
     if (KC) {
       const int r = xw + i, sw = (r >> 1) & 3;
-      const float4 a = *reinterpret_cast<const float4*>(S + r * BK + 4 * ((2 * h) ^ sw));
-      const float4 b = *reinterpret_cast<const float4*>(S + r * BK + 4 * ((2 * h + 1) ^ sw));
+      v4f a, b;
+      asm volatile("ds_read_b128 %0, %1" : "=v"(a) : "v"(base + 4u * (r * BK + 4 * ((2 * h) ^ sw))));
+      asm volatile("ds_read_b128 %0, %1" : "=v"(b) : "v"(base + 4u * (r * BK + 4 * ((2 * h + 1) ^ sw))));
       f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
       f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
     } else {
-#pragma unroll
-      for (int s = 0; s < 8; ++s) f[s] = S[(8 * h + s) * BX + xw + i];
+      // rows 8h + s, s = 0..7, are BX floats apart: pairs via the 64-dword stride form
+      static_assert(BX % 64 == 0, "x-contiguous slab rows are whole 64-dword strides");
+      constexpr int ST = BX / 64;
+      const unsigned a0 = base + 4u * (8 * h * BX + xw + i);
+      v2f p0, p1, p2, p3;
+      asm volatile("ds_read2st64_b32 %0, %1 offset1:%2" : "=v"(p0) : "v"(a0), "i"(ST));
+      asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(p1) : "v"(a0), "i"(2 * ST), "i"(3 * ST));
+      asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(p2) : "v"(a0), "i"(4 * ST), "i"(5 * ST));
+      asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(p3) : "v"(a0), "i"(6 * ST), "i"(7 * ST));
+      f[0] = p0.x; f[1] = p0.y; f[2] = p1.x; f[3] = p1.y;
+      f[4] = p2.x; f[5] = p2.y; f[6] = p3.x; f[7] = p3.y;
     }
+#endif
   }
 };
 
@@ -330,8 +358,10 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   constexpr int BM = 64 * TM, BN = 64 * TN;
   using SlabA = DmaSlab<BM, !TA>;  // A [M][K] is k-contiguous
   using SlabB = DmaSlab<BN, TB>;   // B^T [N][K] is k-contiguous
-  __shared__ __attribute__((aligned(1024))) float As[2][SlabA::SIZE];
-  __shared__ __attribute__((aligned(1024))) float Bs[2][SlabB::SIZE];
+  // NS-stage ring: slab kt + NS - 1 is in flight while slab kt is consumed
+  constexpr int NS = 2, PER_SLAB = SlabA::PER_WAVE + SlabB::PER_WAVE;
+  __shared__ __attribute__((aligned(1024))) float As[NS][SlabA::SIZE];
+  __shared__ __attribute__((aligned(1024))) float Bs[NS][SlabB::SIZE];
 
   const int nt = gridDim.x;
   int tile = blockIdx.x;
@@ -382,29 +412,38 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
     KCursor<MAP> ka, kb;
     ka.init(fak, kbeg);
     kb.init(fbk, kbeg);
-    if (nk > 0) {
-      sa.issue(ra, As[0], wave, ka.bytes(fak));
-      sb.issue(rb, Bs[0], wave, kb.bytes(fbk));
-      ka.advance(fak);
-      kb.advance(fbk);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p)
+      if (p < nk) {
+        sa.issue(ra, As[p], wave, ka.bytes(fak));
+        sb.issue(rb, Bs[p], wave, kb.bytes(fbk));
+        ka.advance(fak);
+        kb.advance(fbk);
+      }
+    int cur = 0;
     for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
+      // slab kt has landed once at most the slabs issued after it are in
+      // flight (this wave's loads complete in order); the barrier makes
+      // every wave's part visible and retires the reads of stage kt - 1
+      if (kt + NS - 2 < nk) waitcnt_vm<(NS - 2) * PER_SLAB>();
+      else waitcnt_vm<0>();
+      __builtin_amdgcn_s_barrier();
       float fa[TM][8], fb[TN][8];
 #pragma unroll
       for (int i = 0; i < TM; ++i) SlabA::frag(As[cur], wm + 32 * i, fa[i]);
 #pragma unroll
       for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur], wn + 32 * j, fb[j]);
       __builtin_amdgcn_sched_barrier(0);
-      // the other buffer was last read before the previous barrier
-      if (kt + 1 < nk) {
-        sa.issue(ra, As[cur ^ 1], wave, ka.bytes(fak));
-        sb.issue(rb, Bs[cur ^ 1], wave, kb.bytes(fbk));
+      // stage kt - 1 (= kt + NS - 1 mod NS) was last read before the barrier
+      const int nxt = cur == 0 ? NS - 1 : cur - 1;
+      if (kt + NS - 1 < nk) {
+        sa.issue(ra, As[nxt], wave, ka.bytes(fak));
+        sb.issue(rb, Bs[nxt], wave, kb.bytes(fbk));
         ka.advance(fak);
         kb.advance(fbk);
       }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the fragment reads above
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int s = 0; s < 8; ++s)
 #pragma unroll
@@ -412,10 +451,10 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);  // keep the MFMAs ahead of the wait below
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      cur = cur == NS - 1 ? 0 : cur + 1;
     }
+    __syncthreads();  // every wave is done with the stages before they are reused
   };
 
   // Element (i, j, r) of the wave's accumulators is C at offset
