@@ -479,13 +479,31 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
     }
   };
 
+  // The epilogue's operand read (the addend D, or E for the GELU VJP) is
+  // issued before the K loop, so its latency hides under the MFMAs instead
+  // of stalling every workgroup's epilogue at once.  Small wave tiles only:
+  // it holds another TM * TN * 16 registers, so only instances that read
+  // one (the dense GEMMs that take an addend, the GELU VJP, the grouped
+  // accumulation) carry it.
+  constexpr bool PF = TM * TN <= 2 && ((EPI == 0 && !MAP) || EPI == 2 || EPI == 3);
+  const float* pre_src = EPI == 2 ? E : D;
+  v16f pre[PF ? TM : 1][PF ? TN : 1];
+  if (PF && pre_src)
+    for_each([&](int i, int j, int r, bool live, int o) {
+      if (PF) pre[i][j][r] = live ? pre_src[o] : 0.0f;
+    });
+  auto pre_at = [&](int i, int j, int r, int o) -> float {
+    if constexpr (PF) return pre[i][j][r];
+    else return pre_src[o];
+  };
+
   if constexpr (EPI == 3) {
     v16f tot[TM][TN];
     for (int g = 0; g < L.ngroup; ++g) {
       run_k(L.ga[g], L.gb[g]);
       if (g == 0) {
         for_each([&](int i, int j, int r, bool live, int o) {
-          tot[i][j][r] = D && live ? D[o] + acc[i][j][r] : acc[i][j][r];
+          tot[i][j][r] = D && live ? pre_at(i, j, r, o) + acc[i][j][r] : acc[i][j][r];
         });
       } else {
 #pragma unroll
@@ -504,8 +522,8 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
     for_each([&](int i, int j, int r, bool live, int o) {
       if (live) {
         float v = acc[i][j][r];
-        if (EPI == 2) v = gelu_bwd(E[o], v);
-        C[o] = D ? D[o] + v : v;
+        if (EPI == 2) v = gelu_bwd(pre_at(i, j, r, o), v);
+        C[o] = D ? (EPI == 2 ? D[o] : pre_at(i, j, r, o)) + v : v;
         if (EPI == 1) E[o] = gelu_fwd(v);
       }
     });
