@@ -43,9 +43,9 @@ def gemm_flops_per_step(cfg) -> float:
 def gemm_bytes_per_step(cfg) -> float:
     """Algorithmic HBM bytes of the step's GEMM launches (the k_sgemm class):
     each launch reads both operands once and writes its output once (4 bytes
-    per element).  The score product Q K^T and its dP = dO V^T VJP run inside
-    the fused attention kernels, so the attention GEMMs here are P @ V and
-    its dV VJP, and the two score VJPs dQ = dS K and dK = dS^T Q."""
+    per element).  Q K^T, P @ V, the dP = dO V^T VJP and dQ = dS K run inside
+    the fused attention kernels, so the attention GEMMs here are the two key
+    side VJPs, dV = P^T dO and dK = dS^T Q."""
     B, T, Cn, H, L, V = cfg["B"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["V"]
     N, hs, F, BH = B * T, Cn // H, 4 * cfg["C"], B * H
 
@@ -55,7 +55,7 @@ def gemm_bytes_per_step(cfg) -> float:
     def mm(m, n, k, batch=1):  # a forward GEMM and its two VJP GEMMs (dA: m x k, dB: k x n)
         return 3 * one(m, n, k, batch)
 
-    attn = 4 * one(T, hs, T, BH)
+    attn = 2 * one(T, hs, T, BH)
     layer = 4 * mm(N, Cn, Cn) + mm(N, F, Cn) + mm(N, Cn, F) + attn
     return L * layer + mm(N, V, Cn)
 

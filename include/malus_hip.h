@@ -161,6 +161,16 @@ int64_t malus_std_attn_scores_softmax(int64_t q, int64_t k, int64_t scale, int64
  * (the kernel the fused attention backward uses; transformer_bwd.ml:15-20 then the
  * scale multiply's VJP). */
 int64_t malus_std_attn_scores_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, int32_t causal);
+/* The whole fused attention forward: returns attn @ v [bh, t, hs] for
+ * attn = malus_std_attn_scores_softmax(q, k, scale, mask, causal), written
+ * with attn from one kernel (nanogpt_modular.ml:57-62); *p_out (if non-null)
+ * receives attn. */
+int64_t malus_std_attn_fwd(int64_t q, int64_t k, int64_t v, int64_t scale, int64_t mask, int32_t causal,
+                           int64_t* p_out);
+/* malus_std_attn_scores_bwd, and dq = ds @ k [bh, t, hs] (the scores
+ * product's VJP for q) from the same kernel into *dq_out (if non-null). */
+int64_t malus_std_attn_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, int64_t k, int32_t causal,
+                           int64_t* dq_out);
 int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
 int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
 void malus_set_abort_on_error(int on);

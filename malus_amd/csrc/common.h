@@ -151,6 +151,16 @@ bool attn_scores_softmax(const float* Q, const float* K, const float* scale, con
 // [bh, t, hs]).  Same values as gemm + softmax_bwd + the scalar multiply.
 bool attn_scores_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const float* P, const float* scale,
                      float* dS, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s);
+// attn_scores_softmax, and with O non-null also O = P @ V (V [bh, t, hs])
+// from the same kernel: head b's row i, column d at O + (b / heads) * t * ldo
+// + (b % heads) * hs + i * ldo + d.  Same values as gemm(P, V).
+bool attn_fwd(const float* Q, const float* K, const float* V, const float* scale, const float* mask, float* P, float* O,
+              size_t ldo, size_t heads, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s);
+// attn_scores_bwd, and with dQ non-null also dQ = Dq + dS @ K (K, dQ, Dq
+// dense [bh, t, hs]; Dq may be null) from the same kernel.  Same values as
+// gemm(dS, K) with the addend.
+bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const float* P, const float* scale, float* dS,
+              const float* K, float* dQ, const float* Dq, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s);
 // Sum over the axis of x * y (y has x's layout); each product rounded to f32.
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 // Broadcast [outer, inner] back to [outer, axis, inner] (expand_axis).

@@ -182,19 +182,13 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   const size_t sshape[3] = {B * H, Tn, Tn};
   int64_t S = 0, mask = 0, Ss = 0, Sm = 0, Pm = 0, AO = 0, ao4 = 0, aop = 0, att;
   if (fused_attention) {
-    // Fused causal attention: S = Q @ K^T, scale, causal mask and softmax in
-    // one kernel (P stored), att = P @ V written straight into [B*T, C], and
-    // one tape node whose VJP runs the fused scores backward.  The causal
-    // mask is computed in the kernels, so its tensor is not built; the scale
-    // and mask leaves of the composed form are released before backward and
-    // never receive gradients.
-    TensorBuffer* p = alloc_tensor(F32, sshape, 3);
-    if (!k::attn_scores_softmax(T(Q)->f32(), T(K)->f32(), T(scale)->f32(), nullptr, p->f32(), B * H, Tn, hs,
-                                /*causal=*/true, stream()))
-      fail("malus: fused attention scores rejected a supported shape");
-    p->write_seq = enqueue_mark("attn_scores_softmax");
-    Pm = malus::H(p);
-    att = attn_out_fwd(Pm, Vv, B, Tn, H, /*causal=*/true);
+    // Fused causal attention: S = Q @ K^T, scale, causal mask, softmax (P
+    // stored) and att = P @ V written straight into [B*T, C], all in one
+    // kernel, and one tape node whose VJP runs the fused scores backward.
+    // The causal mask is computed in the kernels, so its tensor is not built;
+    // the scale and mask leaves of the composed form are released before
+    // backward and never receive gradients.
+    att = attn_fwd_impl(Q, K, Vv, scale, B, Tn, H, &Pm);
     tape_record_fused(TAG_ATTENTION, {Q, K, Vv, Pm, scale}, att, {(int64_t)B, (int64_t)Tn, (int64_t)H});
   } else {
     if (fused_heads) {  // S = Q @ K^T with K read in place

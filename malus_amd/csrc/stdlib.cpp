@@ -643,6 +643,59 @@ int64_t malus_std_attn_scores_bwd(int64_t dout, int64_t v, int64_t p, int64_t sc
   return done(out, "attn_scores_bwd");
   API_CATCH(0)
 }
+int64_t malus_std_attn_fwd(int64_t q, int64_t kk, int64_t v, int64_t scale, int64_t mask, int32_t causal,
+                           int64_t* p_out) {
+  API_TRY
+  TensorBuffer *Q = T(q), *K = T(kk), *V = T(v), *sc = T(scale), *mk = T(mask);
+  if (Q->ndim != 3 || K->ndim != 3 || V->ndim != 3 || Q->shape[0] != K->shape[0] || Q->shape[1] != K->shape[1] ||
+      Q->shape[2] != K->shape[2] || V->shape[0] != Q->shape[0] || V->shape[1] != Q->shape[1] ||
+      V->shape[2] != Q->shape[2] || sc->len != 1 || mk->ndim != 2 || mk->shape[0] != Q->shape[1] ||
+      mk->shape[1] != Q->shape[1])
+    fail("malus: attn_fwd shape mismatch: q %s, k %s, v %s, scale %s, mask %s", shape_str(Q).c_str(),
+         shape_str(K).c_str(), shape_str(V).c_str(), shape_str(sc).c_str(), shape_str(mk).c_str());
+  const size_t bh = Q->shape[0], t = Q->shape[1], hs = Q->shape[2];
+  if (!k::attn_scores_supported(bh, t, hs)) fail("malus: attn_fwd: no fused kernel for t=%zu hs=%zu", t, hs);
+  const size_t pshape[3] = {bh, t, t};
+  TensorBuffer* p = alloc_tensor(F32, pshape, 3);
+  TensorBuffer* out = alloc_tensor(F32, Q->shape, 3);
+  if (!k::attn_fwd(Q->f32(), K->f32(), V->f32(), sc->f32(), mk->f32(), p->f32(), out->f32(), hs, 1, bh, t, hs,
+                   causal != 0, stream()))
+    fail("malus: attn_fwd: unaligned operand");
+  const uint64_t seq = enqueue_mark("attn_fwd");
+  p->write_seq = seq;
+  out->write_seq = seq;
+  if (p_out) *p_out = malus::H(p);
+  else release(p);
+  return malus::H(out);
+  API_CATCH(0)
+}
+int64_t malus_std_attn_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, int64_t kk, int32_t causal,
+                           int64_t* dq_out) {
+  API_TRY
+  TensorBuffer *d = T(dout), *V = T(v), *Pt = T(p), *sc = T(scale), *K = T(kk);
+  if (d->ndim != 3 || V->ndim != 3 || Pt->ndim != 3 || K->ndim != 3 || d->shape[0] != V->shape[0] ||
+      d->shape[1] != V->shape[1] || d->shape[2] != V->shape[2] || Pt->shape[0] != d->shape[0] ||
+      Pt->shape[1] != d->shape[1] || Pt->shape[2] != d->shape[1] || sc->len != 1 || K->shape[0] != V->shape[0] ||
+      K->shape[1] != V->shape[1] || K->shape[2] != V->shape[2])
+    fail("malus: attn_bwd shape mismatch: dout %s, v %s, p %s, scale %s, k %s", shape_str(d).c_str(),
+         shape_str(V).c_str(), shape_str(Pt).c_str(), shape_str(sc).c_str(), shape_str(K).c_str());
+  const size_t bh = d->shape[0], t = d->shape[1], hs = d->shape[2];
+  if (!k::attn_scores_supported(bh, t, hs)) fail("malus: attn_bwd: no fused kernel for t=%zu hs=%zu", t, hs);
+  const size_t shape[3] = {bh, t, t};
+  TensorBuffer* out = alloc_tensor(F32, shape, 3);
+  TensorBuffer* dq = dq_out ? alloc_tensor(F32, K->shape, 3) : nullptr;
+  if (!k::attn_bwd(d->f32(), hs, 1, V->f32(), Pt->f32(), sc->f32(), out->f32(), K->f32(), dq ? dq->f32() : nullptr,
+                   nullptr, bh, t, hs, causal != 0, stream()))
+    fail("malus: attn_bwd: unaligned operand");
+  const uint64_t seq = enqueue_mark("attn_bwd");
+  out->write_seq = seq;
+  if (dq) {
+    dq->write_seq = seq;
+    *dq_out = malus::H(dq);
+  }
+  return malus::H(out);
+  API_CATCH(0)
+}
 int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout) {
   API_TRY
   TensorBuffer *w = T(weight), *idx = T(indices), *d = T(dout);
@@ -998,6 +1051,40 @@ int64_t attn_scores_bwd_impl(int64_t hda, int64_t hv, int64_t hp, int64_t hscale
   if (!k::attn_scores_bwd(da->f32(), H * hs, H, v->f32(), p->f32(), sc->f32(), out->f32(), bh, T, hs, true, stream()))
     fail("malus: attn_scores_bwd: no fused kernel for t=%zu hs=%zu", T, hs);
   return done(out, "attn_scores_bwd");
+}
+// The fused causal attention forward: P = softmax(Q K^T * scale + mask) and
+// att = unheads(P @ V) [B*T, H*hs] from one kernel; *p_out receives P.
+int64_t attn_fwd_impl(int64_t hq, int64_t hk, int64_t hv, int64_t hscale, size_t B, size_t T, size_t H, int64_t* p_out) {
+  TensorBuffer *q = T_(hq), *kk = T_(hk), *v = T_(hv), *sc = T_(hscale);
+  const size_t hs = q->shape[2], bh = B * H, C = H * hs;
+  const size_t psh[3] = {bh, T, T}, osh[2] = {B * T, C};
+  TensorBuffer* p = alloc_tensor(F32, psh, 3);
+  TensorBuffer* out = alloc_tensor(F32, osh, 2);
+  if (!k::attn_fwd(q->f32(), kk->f32(), v->f32(), sc->f32(), nullptr, p->f32(), out->f32(), C, H, bh, T, hs, true,
+                   stream()))
+    fail("malus: attn_fwd: no fused kernel for t=%zu hs=%zu", T, hs);
+  const uint64_t seq = enqueue_mark("attn_fwd");
+  p->write_seq = seq;
+  out->write_seq = seq;
+  *p_out = malus::H(p);
+  return malus::H(out);
+}
+// dS of the fused causal attention and dQ = D + dS @ K from one kernel; *dq receives dQ.
+int64_t attn_bwd_impl(int64_t hda, int64_t hv, int64_t hp, int64_t hscale, int64_t hk, const TensorBuffer* D,
+                      int64_t* dq, size_t B, size_t T, size_t H) {
+  TensorBuffer *da = T_(hda), *v = T_(hv), *p = T_(hp), *sc = T_(hscale), *kk = T_(hk);
+  const size_t hs = v->shape[2], bh = B * H;
+  const size_t sh[3] = {bh, T, T};
+  TensorBuffer* out = alloc_tensor(F32, sh, 3);
+  TensorBuffer* q = alloc_tensor(F32, kk->shape, 3);
+  if (!k::attn_bwd(da->f32(), H * hs, H, v->f32(), p->f32(), sc->f32(), out->f32(), kk->f32(), q->f32(),
+                   D ? D->f32() : nullptr, bh, T, hs, true, stream()))
+    fail("malus: attn_bwd: no fused kernel for t=%zu hs=%zu", T, hs);
+  const uint64_t seq = enqueue_mark("attn_bwd");
+  out->write_seq = seq;
+  q->write_seq = seq;
+  *dq = malus::H(q);
+  return malus::H(out);
 }
 // Scores S = Q @ K^T (the permute(K, 0, 2, 1) operand read in place): dQ = dS @ K, dK = dS^T @ Q  (+ D)
 int64_t scores_bwd_q(int64_t hds, int64_t hk, const TensorBuffer* D, bool causal) {

@@ -510,8 +510,16 @@ void backward(int64_t loss) {
         // AttnOut's VJP (dP, dV), the softmax and scale VJPs, then Scores' (dQ, dK)
         if (nc) fold_grad(grads, v, [&](const TensorBuffer* o) { return attn_out_bwd_v(pr, dout, Bm, Tm, Hm, o, true); });
         if (na || nb) {
-          const int64_t ds = attn_scores_bwd_impl(dout, v, pr, sc, Bm, Tm, Hm);
-          if (na) fold_grad(grads, q, [&](const TensorBuffer* o) { return scores_bwd_q(ds, kk, o, true); });
+          int64_t ds = 0;
+          if (na) {  // dS and dQ = dS @ K from one kernel
+            fold_grad(grads, q, [&](const TensorBuffer* o) {
+              int64_t dq = 0;
+              ds = attn_bwd_impl(dout, v, pr, sc, kk, o, &dq, Bm, Tm, Hm);
+              return dq;
+            });
+          } else {
+            ds = attn_scores_bwd_impl(dout, v, pr, sc, Bm, Tm, Hm);
+          }
           if (nb) fold_grad(grads, kk, [&](const TensorBuffer* o) { return scores_bwd_k(ds, q, o, true); });
           release(T(ds));
         }

@@ -234,6 +234,52 @@ def test_attn_scores_bwd_equals_composed_ops(rt, t, hs, causal):
     rt.free(hq, hk, hv, hd, hsc, hm, hp, hvt, hdp, hdx)
 
 
+@pytest.mark.parametrize("t,hs,causal", [(256, 64, 1), (256, 64, 0), (128, 64, 1), (64, 32, 1), (64, 32, 0),
+                                          (64, 64, 0)])
+def test_attn_fwd_equals_composed_ops(rt, t, hs, causal):
+    # nanogpt_modular.ml:57-62: attn @ V with attn the fused scores softmax.
+    # P @ V runs from the scores kernel's registers; it equals the batched
+    # matmul of the stored P with V bit for bit (a causal P's zeros above the
+    # diagonal add exact zeros in the matmul)
+    bh = 6
+    q, kk, v = (rand(bh, t, hs, lo=-2, hi=2) for _ in range(3))
+    mask = O.causal_mask(t) if causal else rand(t, t, lo=-3, hi=3)
+    sc = np.array([[1.0 / np.sqrt(hs)]], np.float32)
+    hq, hk, hv, hsc, hm = (rt.tensor(a) for a in (q, kk, v, sc, mask))
+    hp = C.c_int64()
+    fused = run(rt, rt.L.malus_std_attn_fwd(hq, hk, hv, hsc, hm, causal, C.byref(hp)))
+    p_fused = run(rt, hp.value)
+    hp2 = rt.L.malus_std_attn_scores_softmax(hq, hk, hsc, hm, causal)
+    assert_bitexact(p_fused, rt.numpy(hp2), f"attn_fwd P t={t} hs={hs} causal={causal}")
+    composed = run(rt, rt.L.tensor_matmul(hp2, hv))
+    assert_bitexact(fused, composed, f"attn_fwd P@V t={t} hs={hs} causal={causal}")
+    assert_normwise(fused, O.matmul(p_fused, v), 1e-5, "attn_fwd vs oracle matmul")
+    rt.free(hq, hk, hv, hsc, hm, hp2)
+
+
+@pytest.mark.parametrize("t,hs,causal", [(256, 64, 1), (256, 64, 0), (128, 64, 1), (64, 32, 1), (64, 64, 0)])
+def test_attn_bwd_dq_equals_composed_ops(rt, t, hs, causal):
+    # The scores backward with the Q gradient of the scores product
+    # (dQ = dS @ K) run from the same kernel's registers: dS equals the
+    # scores backward alone and dQ the batched matmul of that dS with K
+    bh = 5
+    q, kk, v = (rand(bh, t, hs, lo=-2, hi=2) for _ in range(3))
+    d = rand(bh, t, hs)
+    mask = O.causal_mask(t) if causal else rand(t, t, lo=-3, hi=3)
+    sc = np.array([[1.0 / np.sqrt(hs)]], np.float32)
+    hq, hk, hv, hd, hsc, hm = (rt.tensor(a) for a in (q, kk, v, d, sc, mask))
+    hp = rt.L.malus_std_attn_scores_softmax(hq, hk, hsc, hm, causal)
+    hdq = C.c_int64()
+    ds = run(rt, rt.L.malus_std_attn_bwd(hd, hv, hp, hsc, hk, causal, C.byref(hdq)))
+    dq = run(rt, hdq.value)
+    hds2 = rt.L.malus_std_attn_scores_bwd(hd, hv, hp, hsc, causal)
+    assert_bitexact(ds, rt.numpy(hds2), f"attn_bwd dS t={t} hs={hs} causal={causal}")
+    composed = run(rt, rt.L.tensor_matmul(hds2, hk))
+    assert_bitexact(dq, composed, f"attn_bwd dQ t={t} hs={hs} causal={causal}")
+    assert_normwise(dq, O.matmul(ds, kk), 1e-5, "attn_bwd dQ vs oracle matmul")
+    rt.free(hq, hk, hv, hd, hsc, hm, hp, hds2)
+
+
 def test_attn_scores_softmax_rejects_unbuilt_shapes(rt):
     hq = rt.tensor(rand(2, 48, 16))
     hsc, hm = rt.tensor(np.ones((1, 1), np.float32)), rt.tensor(O.causal_mask(48))
