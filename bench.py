@@ -42,8 +42,8 @@ def gemm_flops_per_step(cfg) -> float:
 
 def gemm_bytes_per_step(cfg) -> float:
     """Algorithmic HBM bytes of the step's GEMM launches (the k_sgemm class):
-    each launch reads both operands once and writes its output once (4 bytes
-    per element).  Q K^T, P @ V, the dP = dO V^T VJP and dQ = dS K run inside
+    each launch reads both operands and its epilogue operand once and writes
+    its outputs once (4 bytes per element).  Q K^T, P @ V, the dP = dO V^T VJP and dQ = dS K run inside
     the fused attention kernels, so the attention GEMMs here are the two key
     side VJPs, dV = P^T dO and dK = dS^T Q."""
     B, T, Cn, H, L, V = cfg["B"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["V"]
@@ -56,7 +56,10 @@ def gemm_bytes_per_step(cfg) -> float:
         return 3 * one(m, n, k, batch)
 
     attn = 2 * one(T, hs, T, BH)
-    layer = 4 * mm(N, Cn, Cn) + mm(N, F, Cn) + mm(N, Cn, F) + attn
+    # epilogue operands: the GELU epilogue writes gelu(h) beside h and the
+    # GELU VJP epilogue reads h; the two residual adds read their addend
+    epi = 4.0 * (2 * N * F + 2 * N * Cn)
+    layer = 4 * mm(N, Cn, Cn) + mm(N, F, Cn) + mm(N, Cn, F) + attn + epi
     return L * layer + mm(N, V, Cn)
 
 
