@@ -865,6 +865,20 @@ bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayou
     p.nsplit = 1;
     p.k_chunk = K;
   }
+  if (!accumulate && !c_dense && g_forced_tile < 0) {
+    // Separate groups without a split multiply the tile count by ngroup:
+    // take the widest tile that still gives every CU three workgroups (the
+    // q/k/v projections, 16384 x 384 x 384 x 3: 128 x 192 tiles run 9 %
+    // faster than the single GEMM's 128 x 64).
+    for (int ti = 0; ti < kNumTiles; ++ti) {
+      const long tiles = (long)((M + 64 * kTiles[ti].tm - 1) / (64 * kTiles[ti].tm)) *
+                         ((N + 64 * kTiles[ti].tn - 1) / (64 * kTiles[ti].tn)) * L.ngroup;
+      if (N % (64 * kTiles[ti].tn) == 0 && tiles >= 3 * 256) {
+        p.ti = ti;
+        break;
+      }
+    }
+  }
   static const bool trace = getenv("MALUS_GEMM_TRACE") != nullptr;
   if (trace)
     fprintf(stderr, "malus gemm b1 %dx%dx%d t%d%d -> dma grouped%d%s tile %dx%d occ %d split %d k_chunk %d\n", M, N, K,
