@@ -100,6 +100,98 @@ __global__ __launch_bounds__(256) void k_emb_accum(const float* __restrict__ dou
   dw[(size_t)row * d + c] = acc;
 }
 
+// Two-launch form for small vocabularies (v * t list slots fit the pool).
+// k_emb_list: block per vocab row v writes the positions of its tokens, in
+// increasing order, at pos[v * t ..] and their count.  Thread i owns the
+// contiguous tokens [i * per, (i + 1) * per) (per a multiple of 4, read as
+// int4 with VEC); a block exclusive scan of the per-thread hit counts
+// (thread order = token order) places them.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_emb_list(const int32_t* __restrict__ idx, size_t t, uint32_t* __restrict__ pos,
+                                                  uint32_t* __restrict__ count) {
+  __shared__ uint32_t wave_tot[4];
+  const int32_t v = (int32_t)blockIdx.x;
+  const size_t per = ((t + 255) / 256 + 3) / 4 * 4;
+  const size_t beg = min(t, (size_t)threadIdx.x * per), end = min(t, beg + per);
+  const int4* idx4 = reinterpret_cast<const int4*>(idx);
+  uint32_t c = 0;
+  if (VEC) {  // t % 4 == 0, so [beg, end) is whole int4s
+#pragma unroll 4
+    for (size_t q = beg / 4; q < end / 4; ++q) {
+      const int4 x = idx4[q];
+      c += (x.x == v ? 1u : 0u) + (x.y == v ? 1u : 0u) + (x.z == v ? 1u : 0u) + (x.w == v ? 1u : 0u);
+    }
+  } else {
+#pragma unroll 4
+    for (size_t i = beg; i < end; ++i) c += idx[i] == v ? 1u : 0u;
+  }
+  // inclusive scan over the wave, then over the four waves
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  uint32_t inc = c;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += o;
+  }
+  if (lane == 63) wave_tot[wave] = inc;
+  __syncthreads();
+  uint32_t base = inc - c;
+  for (int q = 0; q < wave; ++q) base += wave_tot[q];
+  uint32_t* out = pos + (size_t)blockIdx.x * t;
+  if (c) {
+    if (VEC) {
+#pragma unroll 4
+      for (size_t q = beg / 4; q < end / 4; ++q) {
+        const int4 x = idx4[q];
+        const uint32_t i = (uint32_t)(4 * q);
+        if (x.x == v) out[base++] = i;
+        if (x.y == v) out[base++] = i + 1;
+        if (x.z == v) out[base++] = i + 2;
+        if (x.w == v) out[base++] = i + 3;
+      }
+    } else {
+      for (size_t i = beg; i < end; ++i)
+        if (idx[i] == v) out[base++] = (uint32_t)i;
+    }
+  }
+  if (threadIdx.x == 255) count[blockIdx.x] = base;
+}
+
+// k_emb_rows: dw[v, 4c .. 4c + 3] = the sum of dout[t, 4c ..] over row v's
+// token list, in list order (the same adds as k_emb_accum); sixteen rows'
+// loads are in flight before their adds.
+__global__ __launch_bounds__(64) void k_emb_rows(const float4* __restrict__ dout, const uint32_t* __restrict__ pos,
+                                                 const uint32_t* __restrict__ count, float4* __restrict__ dw, size_t t,
+                                                 uint32_t d4, uint32_t col_blocks) {
+  const uint32_t row = blockIdx.x / col_blocks;
+  const uint32_t c = (blockIdx.x % col_blocks) * 64 + threadIdx.x;
+  if (c >= d4) return;
+  const uint32_t n = count[row];
+  const uint32_t* p = pos + (size_t)row * t;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  uint32_t k = 0;
+  for (; k + 16 <= n; k += 16) {
+    float4 a[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) a[u] = dout[(size_t)p[k + u] * d4 + c];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      acc.x += a[u].x;
+      acc.y += a[u].y;
+      acc.z += a[u].z;
+      acc.w += a[u].w;
+    }
+  }
+  for (; k < n; ++k) {
+    const float4 a = dout[(size_t)p[k] * d4 + c];
+    acc.x += a.x;
+    acc.y += a.y;
+    acc.z += a.z;
+    acc.w += a.w;
+  }
+  dw[(size_t)row * d4 + c] = acc;
+}
+
 struct PermDesc {
   int ndim;
   uint32_t out_shape[kMaxRank];
@@ -172,6 +264,21 @@ void embedding_bwd(const float* dout, const int32_t* idx, float* dw, size_t t, s
   if (!v || !d) return;
   if (!t) { fill(dw, 0.0f, v * d, s); return; }
   size_t b_count, b_offs, b_pos;
+  const auto aligned = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  if (d % 4 == 0 && v * t <= ((size_t)1 << 24) && aligned(dout) && aligned(dw)) {
+    uint32_t* count = static_cast<uint32_t*>(pool_alloc(v * sizeof(uint32_t), &b_count));
+    uint32_t* pos = static_cast<uint32_t*>(pool_alloc(v * t * sizeof(uint32_t), &b_pos));
+    if (t % 4 == 0 && aligned(idx)) k_emb_list<true><<<(unsigned)v, 256, 0, s>>>(idx, t, pos, count);
+    else k_emb_list<false><<<(unsigned)v, 256, 0, s>>>(idx, t, pos, count);
+    MALUS_HIP(hipGetLastError());
+    const uint32_t d4 = (uint32_t)(d / 4), col_blocks = (d4 + 63) / 64;
+    k_emb_rows<<<(unsigned)(v * col_blocks), 64, 0, s>>>(reinterpret_cast<const float4*>(dout), pos, count,
+                                                         reinterpret_cast<float4*>(dw), t, d4, col_blocks);
+    MALUS_HIP(hipGetLastError());
+    pool_free(count, b_count);
+    pool_free(pos, b_pos);
+    return;
+  }
   uint32_t* count = static_cast<uint32_t*>(pool_alloc(v * sizeof(uint32_t), &b_count));
   uint32_t* offs = static_cast<uint32_t*>(pool_alloc((v + 1) * sizeof(uint32_t), &b_offs));
   uint32_t* pos = static_cast<uint32_t*>(pool_alloc(t * sizeof(uint32_t), &b_pos));
