@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void k_adam_l2(const float* __restrict__ p, co
 // tensors.  The segment table travels by value in the kernel arguments (no
 // upload).  Block b covers 4096 floats (1024 float4, four per thread) of the
 // segment whose chunk range holds b; chunks never straddle segments.
-constexpr int kAdamMaxSegs = 16;
+constexpr int kAdamMaxSegs = 48;  // 3.3 KB of kernel arguments
 struct AdamTable {
   AdamSeg seg[kAdamMaxSegs];
   uint32_t first_chunk[kAdamMaxSegs + 1];  // prefix sums of the segments' chunk counts

@@ -478,8 +478,10 @@ void malus_gpt_zero_grad(void* gp) {
 void malus_gpt_optimizer_step(void* gp, int64_t t) {
   API_TRY
   auto* g = static_cast<Gpt*>(gp);
-  for (int l = 0; l < g->L; ++l) adamw_range(*g, 8 * l, 8 * l + 8, t);  // lines 186-187
-  adamw_range(*g, 8 * g->L, 8 * g->L + 4, t);                        // line 188
+  // lines 186-187 (each block's params), then line 188 (the rest): every
+  // update is elementwise on its own tensors, so the whole list is one range
+  // (the fused form then takes two multi-tensor launches)
+  adamw_range(*g, 0, 8 * g->L + 4, t);
   API_CATCH()
 }
 
