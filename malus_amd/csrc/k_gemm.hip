@@ -547,9 +547,14 @@ __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ 
 // loads are in flight before their adds, and 64-thread workgroups spread the
 // few thousand float4 columns of a weight gradient over every CU.
 typedef float v4f_t __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(64) void k_split_reduce4(const v4f_t* __restrict__ partial, v4f_t* __restrict__ C,
-                                                      size_t mn4, int nsplit, const v4f_t* __restrict__ D) {
+// blockIdx.y = group g of a grouped launch: its partials follow group
+// g - 1's (nsplit * mn4 each) and it writes out.c[g].
+struct SplitOut { v4f_t* c[3]; };
+__global__ __launch_bounds__(64) void k_split_reduce4(const v4f_t* __restrict__ partial, SplitOut out, size_t mn4,
+                                                      int nsplit, const v4f_t* __restrict__ D) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
+  partial += (size_t)blockIdx.y * nsplit * mn4;
+  v4f_t* __restrict__ C = out.c[blockIdx.y];
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn4; i += stride) {
     v4f_t acc = partial[i];
     int s = 1;
@@ -728,8 +733,9 @@ void split_reduce(float* partial, float* C, size_t mn, int nsplit, const float* 
   if (vec) {
     size_t blocks = (mn / 4 + 63) / 64;
     if (blocks > 16384) blocks = 16384;
-    k_split_reduce4<<<(unsigned)blocks, 64, 0, s>>>(reinterpret_cast<const v4f_t*>(partial), reinterpret_cast<v4f_t*>(C),
-                                                   mn / 4, nsplit, reinterpret_cast<const v4f_t*>(D));
+    const SplitOut out{{reinterpret_cast<v4f_t*>(C), nullptr, nullptr}};
+    k_split_reduce4<<<(unsigned)blocks, 64, 0, s>>>(reinterpret_cast<const v4f_t*>(partial), out, mn / 4, nsplit,
+                                                   reinterpret_cast<const v4f_t*>(D));
   } else {
     size_t blocks = (mn + 255) / 256;
     if (blocks > 4096) blocks = 4096;
@@ -907,9 +913,21 @@ bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayou
   MALUS_HIP(hipLaunchKernel(fn, dim3((unsigned)tiles, (unsigned)nsplit, accumulate ? 1u : (unsigned)L.ngroup), dim3(256),
                             args, 0, s));
   if (nsplit > 1) {
-    for (int g = 0; g < L.ngroup; ++g) {
-      size_t none = 0;
-      split_reduce(L.gc[g], outs[g], mn, nsplit, nullptr, s, none, false);
+    bool vec = mn % 4 == 0;
+    for (int g = 0; g < L.ngroup; ++g) vec = vec && (reinterpret_cast<uintptr_t>(outs[g]) & 15) == 0;
+    if (vec) {  // one launch for every group's reduction
+      SplitOut out{};
+      for (int g = 0; g < L.ngroup; ++g) out.c[g] = reinterpret_cast<v4f_t*>(outs[g]);
+      size_t blocks = (mn / 4 + 63) / 64;
+      if (blocks > 16384) blocks = 16384;
+      k_split_reduce4<<<dim3((unsigned)blocks, (unsigned)L.ngroup), 64, 0, s>>>(reinterpret_cast<const v4f_t*>(partial),
+                                                                               out, mn / 4, nsplit, nullptr);
+      MALUS_HIP(hipGetLastError());
+    } else {
+      for (int g = 0; g < L.ngroup; ++g) {
+        size_t none = 0;
+        split_reduce(L.gc[g], outs[g], mn, nsplit, nullptr, s, none, false);
+      }
     }
     pool_free(partial, bucket);
   }
