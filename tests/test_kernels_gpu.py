@@ -288,6 +288,18 @@ def test_attn_scores_softmax_rejects_unbuilt_shapes(rt):
         assert rt.L.malus_std_attn_scores_softmax(hq, hq, hsc, hm, 1) == 0
         assert "no fused kernel" in rt.last_error()
         rt.L.malus_clear_error()
+        assert rt.L.malus_std_attn_fwd(hq, hq, hq, hsc, hm, 1, None) == 0
+        assert "no fused kernel" in rt.last_error()
+        rt.L.malus_clear_error()
+        hp = rt.tensor(rand(2, 48, 48))
+        assert rt.L.malus_std_attn_bwd(hq, hq, hp, hsc, hq, 1, None) == 0
+        assert "no fused kernel" in rt.last_error()
+        rt.L.malus_clear_error()
+        hv = rt.tensor(rand(2, 48, 32))  # v of another head size
+        assert rt.L.malus_std_attn_fwd(hq, hq, hv, hsc, hm, 1, None) == 0
+        assert "attn_fwd shape mismatch" in rt.last_error()
+        rt.L.malus_clear_error()
+        rt.free(hp, hv)
     finally:
         rt.L.malus_set_abort_on_error(1)
     rt.free(hq, hsc, hm)
