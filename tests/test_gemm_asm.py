@@ -1,7 +1,7 @@
-"""The GEMM's LDS fragment reads are inline asm (k_gemm.hip, DmaSlab::frag):
-the compiler does not know they are pending, so nothing may read or
-overwrite their destination registers before the kernel's own
-``s_waitcnt lgkmcnt(0)``.  This test compiles k_gemm.hip for gfx950 to
+"""The GEMM's LDS fragment reads are inline asm (k_gemm.hip,
+DmaSlab::frag): the compiler does not know they are pending, so
+nothing may read or overwrite their destination registers before the
+kernel's own ``s_waitcnt lgkmcnt(N)`` has retired them.  This test compiles k_gemm.hip for gfx950 to
 assembly and follows every control-flow path from each such read to the
 wait.  CPU only (hipcc cross-compiles); about a minute."""
 import os
@@ -36,7 +36,17 @@ def _functions(asm):
     return funcs
 
 
+def _lgkm_wait(t):
+    m = re.search(r"lgkmcnt\((\d+)\)", t)
+    return int(m.group(1)) if m else None
+
+
 def _hazards(name, body):
+    """Walk every path from each inline-asm ds_read.  LDS operations retire
+    in issue order, so ``s_waitcnt lgkmcnt(N)`` retires all but the last N
+    outstanding ones; the read is done once it is retired.  Scalar memory
+    loads also count against lgkmcnt but return out of order, so one issued
+    while the read is outstanding is reported too."""
     insts, labels, in_asm = [], {}, False
     for line in body:
         t = line.strip()
@@ -61,26 +71,44 @@ def _hazards(name, body):
             continue
         reads += 1
         pend = _regs(t.split()[1].rstrip(","))
-        stack, seen = [k + 1], set()
+        # state: number of LDS operations issued after this read
+        stack, seen = [(k + 1, 0)], set()
         while stack:
-            j = stack.pop()
-            while j < len(insts) and j not in seen:
-                seen.add(j)
+            j, after = stack.pop()
+            while j < len(insts) and (j, after) not in seen:
+                seen.add((j, after))
                 tt, aa = insts[j]
                 op = tt.split()[0]
-                if (op == "s_waitcnt" and "lgkmcnt(0)" in tt) or op == "s_endpgm":
+                if op == "s_endpgm":
+                    break
+                if op == "s_waitcnt":
+                    n = _lgkm_wait(tt)
+                    if n is not None and after + 1 > n:  # this read is among the retired ones
+                        break
+                    j += 1
+                    continue
+                if op.startswith(("s_load", "s_buffer_load")):
+                    found.append(f"{name}: scalar load while an LDS read is pending: {tt}")
                     break
                 ops = [x for x in re.split(r",\s*", tt[len(op):].strip()) if x]
                 used = set().union(*(_regs(x) for x in ops)) if ops else set()
-                other_read = aa and op.startswith("ds_read") and not (used & pend)
-                if used & pend and not other_read:
+                if op.startswith("ds_"):
+                    if aa and op.startswith("ds_read") and not (used & pend):
+                        after += 1
+                        j += 1
+                        continue
+                    if not (used & pend):
+                        after += 1
+                        j += 1
+                        continue
+                if used & pend:
                     found.append(f"{name}: {tt}")
                     break
                 if op == "s_branch":
                     j = labels[ops[0]]
                     continue
                 if op.startswith("s_cbranch"):
-                    stack.append(labels[ops[0]])
+                    stack.append((labels[ops[0]], after))
                 j += 1
     return reads, found
 
