@@ -114,143 +114,186 @@ __device__ __forceinline__ void product_from_registers(const v16f (&a)[NT], int 
     }
 }
 
+// Query tiles are dealt to the waves in pairs (p, NT-1-p): wave w runs both
+// tiles of pair w, one after the other, so every wave has NT + 1 key tiles
+// of unmasked work under a causal mask and the workgroup (one head) is
+// balanced across its SIMDs.  NT <= 8: at most four pairs per head.
+template <int NT>
+__device__ __forceinline__ int pair_tile(int w, int which) {
+  return which ? NT - 1 - w : w;
+}
+
+// One wave's query tile qt (rows 32 qt ..): S^T = K Q^T from K staged in LDS
+// (rows in key_row order), scale, mask, the row softmax, and the store of the
+// P rows.  Leaves P in acc (zeros in the skipped key tiles).
+template <int TT, int HS, bool CAUSAL>
+__device__ __forceinline__ void softmax_tile(const float* __restrict__ Qh, const float* Ks, const float* __restrict__ scale,
+                                             const float* __restrict__ mask, float* __restrict__ Ph, int qt,
+                                             v16f (&acc)[TT / 32]) {
+  constexpr int NT = TT / 32;   // key tiles per row (= 32-row query tiles per head)
+  constexpr int NKB = HS / 16;  // 16-deep k slabs
+  constexpr int LD = HS + 4;
+  const int lane = threadIdx.x & 63, x = lane & 31, lk = lane >> 5;
+  const int i0 = 32 * qt, i = i0 + x;
+  const int live = CAUSAL ? qt + 1 : NT;  // key tiles holding an unmasked key
+
+  // B operand: Q[i0 + x][16 kb + 8 lk + s] for step s of slab kb
+  const v4f* qp = reinterpret_cast<const v4f*>(Qh + (size_t)i * HS + 8 * lk);
+  v4f qv[2 * NKB];
+#pragma unroll
+  for (int e = 0; e < 2 * NKB; ++e) qv[e] = qp[4 * (e >> 1) + (e & 1)];
+
+  // A operand: K[32 t + key_row(x)][16 kb + 8 lk + s] from LDS
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    acc[t] = v16f{0};
+    if (t < live) {
+      const float* kr = Ks + (32 * t + key_row(x)) * LD + 8 * lk;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const v4f a = *reinterpret_cast<const v4f*>(kr + 16 * kb);
+        const v4f b = *reinterpret_cast<const v4f*>(kr + 16 * kb + 4);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], qv[2 * kb][s], acc[t], 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[s], qv[2 * kb + 1][s], acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // x = S * scale + mask[i][j]; row max.  The causal mask is the one
+  // tensor_causal_mask fills: -1e9 where j > i, else 0.
+  const float sc = scale[0];
+  const v4f* mrow = reinterpret_cast<const v4f*>(mask + (size_t)i * TT);
+  float m = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (t < live) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int gi = key_group(t, g, lk);
+        v4f mk;
+        if (CAUSAL) {  // only the diagonal tile (t == qt) mixes masked and unmasked keys
+#pragma unroll
+          for (int c = 0; c < 4; ++c) mk[c] = t == qt && 4 * gi + c > i ? -1e9f : 0.0f;
+        } else {
+          mk = mrow[gi];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float ss = acc[t][4 * g + c] * sc;
+          const float xv = ss + mk[c];
+          acc[t][4 * g + c] = xv;
+          m = fmaxf(m, xv);
+        }
+      }
+    }
+  }
+  m = fmaxf(m, __shfl_xor(m, 32, 64));
+
+  // probabilities and the per-group partial sums v[t][g] (4 keys each)
+  float v[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float s = 0.0f;
+      if (t < live) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float ex = expf(acc[t][4 * g + c] - m);
+          acc[t][4 * g + c] = ex;
+          s += ex;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[t][4 * g + c] = 0.0f;
+      }
+      v[t][g] = s;
+    }
+  }
+  const float s = row_tree<NT>(v);
+
+  v4f* prow = reinterpret_cast<v4f*>(Ph + (size_t)i * TT);
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};  // +0 / s = +0 for the skipped tiles
+      if (t < live) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = acc[t][4 * g + c] = acc[t][4 * g + c] / s;
+      }
+      prow[key_group(t, g, lk)] = o;
+    }
+}
+
+// Reload a wave's [32, TT] rows (P or dS of query tile qt, stored by
+// softmax_tile / dscores_tile) into the key-tile register layout; the
+// skipped key tiles are zero.
+template <int TT>
+__device__ __forceinline__ void load_tile(const float* __restrict__ Xh, int qt, int live, v16f (&acc)[TT / 32]) {
+  constexpr int NT = TT / 32;
+  const int lane = threadIdx.x & 63, x = lane & 31, lk = lane >> 5;
+  const v4f* row = reinterpret_cast<const v4f*>(Xh + (size_t)(32 * qt + x) * TT);
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const v4f q = t < live ? row[key_group(t, g, lk)] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[t][4 * g + c] = q[c];
+    }
+}
+
 // PV: also att = P @ V, written at O + (bh / H) * TT * ldo + (bh % H) * HS
 // + i * ldo + d (ldo = H * HS: the [B*T, C] layout the output projection
-// reads; ldo = HS, H = 1: dense heads).
+// reads; ldo = HS, H = 1: dense heads).  One workgroup per head; wave w
+// runs query tiles w and NT-1-w: both score tiles while K is staged (the
+// first one's P goes to memory, the second stays in registers), then, with V
+// staged where K was, P @ V for the second tile from the registers and for
+// the first from its reloaded rows.
 template <int TT, int HS, bool CAUSAL, bool PV>
 __global__ __launch_bounds__(256, 2) void k_attn_fwd(const float* __restrict__ Q, const float* __restrict__ Kh,
                                                     const float* __restrict__ V, const float* __restrict__ scale,
                                                     const float* __restrict__ mask, float* __restrict__ P,
                                                     float* __restrict__ O, int ldo, int H) {
-  constexpr int NT = TT / 32;   // key tiles per row (= 32-row query tiles per head)
-  constexpr int NKB = HS / 16;  // 16-deep k slabs
+  constexpr int NT = TT / 32;
   constexpr int LD = HS + 4;
+  static_assert(NT % 2 == 0 && NT <= 8, "one pair of query tiles per wave");
   __shared__ __attribute__((aligned(16))) float S[TT * LD];  // K, then V
   const int bh = blockIdx.y;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const size_t head = (size_t)bh * TT * HS;
+  const bool active = wave < NT / 2;
+  const int qa = pair_tile<NT>(wave, 0), qb = pair_tile<NT>(wave, 1);
+  float* Ph = P + (size_t)bh * TT * TT;
 
-  // Query tiles are dealt in pairs (p, NT-1-p) so that every workgroup gets
-  // the same number of unmasked key tiles under a causal mask.
-  const int pair = 2 * blockIdx.x + (wave >> 1);
-  const int qt = (wave & 1) ? NT - 1 - pair : pair;
-  const bool idle = pair >= (NT + 1) / 2 || ((wave & 1) && qt == pair);  // odd NT: the middle tile has no partner
-  const int i0 = 32 * (idle ? 0 : qt);
-  const int x = lane & 31, lk = lane >> 5;
-  const int live = CAUSAL ? qt + 1 : NT;  // key tiles holding an unmasked key
-
-  // B operand: Q[i0 + x][16 kb + 8 lk + s] for step s of slab kb (loaded
-  // while K is staged; an idle wave reads tile 0 and discards it)
-  const v4f* qp = reinterpret_cast<const v4f*>(Q + head + (size_t)(i0 + x) * HS + 8 * lk);
-  v4f qv[2 * NKB];
-#pragma unroll
-  for (int e = 0; e < 2 * NKB; ++e) qv[e] = qp[4 * (e >> 1) + (e & 1)];
   stage_head<TT, HS>(Kh + head, S);
   __syncthreads();
-
   v16f acc[NT];
-  if (!idle) {
-    // A operand: K[32 t + key_row(x)][16 kb + 8 lk + s] from LDS
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      acc[t] = v16f{0};
-      if (t < live) {
-        const float* kr = S + (32 * t + key_row(x)) * LD + 8 * lk;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-          const v4f a = *reinterpret_cast<const v4f*>(kr + 16 * kb);
-          const v4f b = *reinterpret_cast<const v4f*>(kr + 16 * kb + 4);
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], qv[2 * kb][s], acc[t], 0, 0, 0);
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[s], qv[2 * kb + 1][s], acc[t], 0, 0, 0);
-        }
-      }
-    }
-
-    // x = S * scale + mask[i][j]; row max.  The causal mask is the one
-    // tensor_causal_mask fills: -1e9 where j > i, else 0.
-    const int i = i0 + x;
-    const float sc = scale[0];
-    const v4f* mrow = reinterpret_cast<const v4f*>(mask + (size_t)i * TT);
-    float m = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      if (t < live) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int gi = key_group(t, g, lk);
-          v4f mk;
-          if (CAUSAL) {  // only the diagonal tile (t == qt) mixes masked and unmasked keys
-#pragma unroll
-            for (int c = 0; c < 4; ++c) mk[c] = t == qt && 4 * gi + c > i ? -1e9f : 0.0f;
-          } else {
-            mk = mrow[gi];
-          }
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const float ss = acc[t][4 * g + c] * sc;
-            const float xv = ss + mk[c];
-            acc[t][4 * g + c] = xv;
-            m = fmaxf(m, xv);
-          }
-        }
-      }
-    }
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
-
-    // probabilities and the per-group partial sums v[t][g] (4 keys each)
-    float v[NT][4];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float s = 0.0f;
-        if (t < live) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const float ex = expf(acc[t][4 * g + c] - m);
-            acc[t][4 * g + c] = ex;
-            s += ex;
-          }
-        } else {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[t][4 * g + c] = 0.0f;
-        }
-        v[t][g] = s;
-      }
-    }
-    const float s = row_tree<NT>(v);
-
-    v4f* prow = reinterpret_cast<v4f*>(P + ((size_t)bh * TT + i) * TT);
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};  // +0 / s = +0 for the skipped tiles
-        if (t < live) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) o[c] = acc[t][4 * g + c] = acc[t][4 * g + c] / s;
-        }
-        prow[key_group(t, g, lk)] = o;
-      }
+  if (active) {
+    softmax_tile<TT, HS, CAUSAL>(Q + head, S, scale, mask, Ph, qa, acc);
+    softmax_tile<TT, HS, CAUSAL>(Q + head, S, scale, mask, Ph, qb, acc);
   }
   if constexpr (PV) {
     __syncthreads();  // every wave is done with K
     stage_head<TT, HS>(V + head, S);
     __syncthreads();
-    if (!idle)
-      product_from_registers<NT, HS>(acc, live, S, i0, O + (size_t)(bh / H) * TT * ldo + (size_t)(bh % H) * HS, nullptr,
-                                     ldo);
+    if (active) {
+      float* Oh = O + (size_t)(bh / H) * TT * ldo + (size_t)(bh % H) * HS;
+      product_from_registers<NT, HS>(acc, CAUSAL ? qb + 1 : NT, S, 32 * qb, Oh, nullptr, ldo);
+      load_tile<TT>(Ph, qa, CAUSAL ? qa + 1 : NT, acc);
+      product_from_registers<NT, HS>(acc, CAUSAL ? qa + 1 : NT, S, 32 * qa, Oh, nullptr, ldo);
+    }
   }
 }
 
 template <int TT, int HS>
 void launch(const float* Q, const float* K, const float* V, const float* scale, const float* mask, float* P, float* O,
             int ldo, int H, int bh, bool causal, hipStream_t s) {
-  const dim3 grid((TT / 32 + 3) / 4, (unsigned)bh);  // two query-tile pairs per workgroup
+  const dim3 grid(1, (unsigned)bh);  // one workgroup per head
   if (O) {
     if (causal) k_attn_fwd<TT, HS, true, true><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H);
     else k_attn_fwd<TT, HS, false, true><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H);
@@ -260,17 +303,98 @@ void launch(const float* Q, const float* K, const float* V, const float* scale, 
   }
 }
 
+// One wave's query tile qt of the scores backward: dP^T = V dO^T from V
+// staged in LDS, dS = P * (dP - sum(dP * P)) * scale, and the store of the dS
+// rows.  Leaves dS in acc.
+template <int TT, int HS, bool CAUSAL>
+__device__ __forceinline__ void dscores_tile(const float* __restrict__ dOh, int ldo, const float* Vs,
+                                             const float* __restrict__ Ph, const float* __restrict__ scale,
+                                             float* __restrict__ dSh, int qt, v16f (&acc)[TT / 32]) {
+  constexpr int NT = TT / 32;
+  constexpr int NKB = HS / 16;
+  constexpr int LD = HS + 4;
+  const int lane = threadIdx.x & 63, x = lane & 31, lk = lane >> 5;
+  const int i0 = 32 * qt, i = i0 + x;
+  const int live = CAUSAL ? qt + 1 : NT;
+
+  // B operand: dO[i0 + x][16 kb + 8 lk + s]
+  const v4f* op = reinterpret_cast<const v4f*>(dOh + (size_t)i * ldo + 8 * lk);
+  v4f ov[2 * NKB];
+#pragma unroll
+  for (int e = 0; e < 2 * NKB; ++e) ov[e] = op[4 * (e >> 1) + (e & 1)];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    acc[t] = v16f{0};
+    if (t < live) {
+      const float* vr = Vs + (32 * t + key_row(x)) * LD + 8 * lk;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const v4f a = *reinterpret_cast<const v4f*>(vr + 16 * kb);
+        const v4f b = *reinterpret_cast<const v4f*>(vr + 16 * kb + 4);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], ov[2 * kb][s], acc[t], 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[s], ov[2 * kb + 1][s], acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // per-group sums of dP * P, then the row kernel's tree
+  const v4f* prow = reinterpret_cast<const v4f*>(Ph + (size_t)i * TT);
+  float v[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float sum = 0.0f;
+      if (t < live) {
+        const v4f pv = prow[key_group(t, g, lk)];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float pr = acc[t][4 * g + c] * pv[c];
+          sum += pr;
+        }
+      }
+      v[t][g] = sum;
+    }
+  const float d = row_tree<NT>(v);
+
+  const float sc = scale[0];
+  v4f* srow = reinterpret_cast<v4f*>(dSh + (size_t)i * TT);
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      if (t < live) {
+        const v4f pv = prow[key_group(t, g, lk)];  // second read of the row (cache): dP stays in registers
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float diff = acc[t][4 * g + c] - d;
+          const float dx = pv[c] * diff;
+          o[c] = acc[t][4 * g + c] = dx * sc;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[t][4 * g + c] = 0.0f;
+      }
+      srow[key_group(t, g, lk)] = o;
+    }
+}
+
 // Backward of the scores: dS = softmax_bwd(P, dP) * scale with dP = dO V^T,
 // for tape.rs:1150-1161 (dx = s * (dout - sum(dout * s))) followed by the
 // scale multiply's VJP (dout * scale); DQ: also dQ = dS @ K (+ Dq), the
 // scores product's VJP for Q.  The wave layout is the forward kernel's
-// (lane = query row, registers = keys in the key_row order), so
-// dP^T = V dO^T runs on MFMA with V staged in LDS, the row sum is one
-// cross-lane step, dP never reaches memory, and dS feeds dS @ K from the
-// registers with K staged in LDS after V.  Bit-identical to gemm(dO, V^T),
-// softmax_bwd, the scalar multiply and gemm(dS, K): the same MFMA k pairing,
-// per-group products summed from 0 in key order, the row kernel's xor tree,
-// and the same f32 operations.
+// (lane = query row, registers = keys in the key_row order, one pair of
+// query tiles per wave), so dP^T = V dO^T runs on MFMA with V staged in LDS,
+// the row sum is one cross-lane step, dP never reaches memory, and dS feeds
+// dS @ K from the registers (the pair's second tile) or from its reloaded
+// rows (the first) with K staged in LDS after V.  Bit-identical to
+// gemm(dO, V^T), softmax_bwd, the scalar multiply and gemm(dS, K): the same
+// MFMA k pairing, per-group products summed from 0 in key order, the row
+// kernel's xor tree, and the same f32 operations.
 // Causal: key tiles above a wave's rows hold P = 0, so their dS is 0 (the
 // composed ops give +-0 there) and neither dP nor P is read for them.
 // dO of head bh, row i, column d sits at dO + (bh / H) * T * ldo + (bh % H) * HS + i * ldo + d
@@ -282,102 +406,42 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ d
                                                     const float* __restrict__ Kh, float* __restrict__ dQ,
                                                     const float* __restrict__ Dq) {
   constexpr int NT = TT / 32;
-  constexpr int NKB = HS / 16;
   constexpr int LD = HS + 4;
+  static_assert(NT % 2 == 0 && NT <= 8, "one pair of query tiles per wave");
   __shared__ __attribute__((aligned(16))) float S[TT * LD];  // V, then K
   const int bh = blockIdx.y;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const size_t head = (size_t)bh * TT * HS;
+  const bool active = wave < NT / 2;
+  const int qa = pair_tile<NT>(wave, 0), qb = pair_tile<NT>(wave, 1);
+  const float* dOh = dO + (size_t)(bh / H) * TT * ldo + (size_t)(bh % H) * HS;
+  const float* Ph = P + (size_t)bh * TT * TT;
+  float* dSh = dS + (size_t)bh * TT * TT;
 
-  const int pair = 2 * blockIdx.x + (wave >> 1);
-  const int qt = (wave & 1) ? NT - 1 - pair : pair;
-  const bool idle = pair >= (NT + 1) / 2 || ((wave & 1) && qt == pair);
-  const int i0 = 32 * (idle ? 0 : qt);
-  const int x = lane & 31, lk = lane >> 5;
-  const int live = CAUSAL ? qt + 1 : NT;
-
-  // B operand: dO[i0 + x][16 kb + 8 lk + s]
-  const v4f* op = reinterpret_cast<const v4f*>(dO + (size_t)(bh / H) * TT * ldo + (size_t)(bh % H) * HS +
-                                               (size_t)(i0 + x) * ldo + 8 * lk);
-  v4f ov[2 * NKB];
-#pragma unroll
-  for (int e = 0; e < 2 * NKB; ++e) ov[e] = op[4 * (e >> 1) + (e & 1)];
   stage_head<TT, HS>(V + head, S);
   __syncthreads();
-
   v16f acc[NT];
-  if (!idle) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      acc[t] = v16f{0};
-      if (t < live) {
-        const float* vr = S + (32 * t + key_row(x)) * LD + 8 * lk;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-          const v4f a = *reinterpret_cast<const v4f*>(vr + 16 * kb);
-          const v4f b = *reinterpret_cast<const v4f*>(vr + 16 * kb + 4);
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], ov[2 * kb][s], acc[t], 0, 0, 0);
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[s], ov[2 * kb + 1][s], acc[t], 0, 0, 0);
-        }
-      }
-    }
-
-    // per-group sums of dP * P, then the row kernel's tree
-    const int i = i0 + x;
-    const v4f* prow = reinterpret_cast<const v4f*>(P + ((size_t)bh * TT + i) * TT);
-    float v[NT][4];
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float sum = 0.0f;
-        if (t < live) {
-          const v4f pv = prow[key_group(t, g, lk)];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const float pr = acc[t][4 * g + c] * pv[c];
-            sum += pr;
-          }
-        }
-        v[t][g] = sum;
-      }
-    const float d = row_tree<NT>(v);
-
-    const float sc = scale[0];
-    v4f* srow = reinterpret_cast<v4f*>(dS + ((size_t)bh * TT + i) * TT);
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        v4f o = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        if (t < live) {
-          const v4f pv = prow[key_group(t, g, lk)];  // second read of the row (cache): dP stays in registers
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const float diff = acc[t][4 * g + c] - d;
-            const float dx = pv[c] * diff;
-            o[c] = acc[t][4 * g + c] = dx * sc;
-          }
-        }
-        srow[key_group(t, g, lk)] = o;
-      }
+  if (active) {
+    dscores_tile<TT, HS, CAUSAL>(dOh, ldo, S, Ph, scale, dSh, qa, acc);
+    dscores_tile<TT, HS, CAUSAL>(dOh, ldo, S, Ph, scale, dSh, qb, acc);
   }
   if constexpr (DQ) {
     __syncthreads();  // every wave is done with V
     stage_head<TT, HS>(Kh + head, S);
     __syncthreads();
-    if (!idle) product_from_registers<NT, HS>(acc, live, S, i0, dQ + head, Dq ? Dq + head : nullptr, HS);
+    if (active) {
+      const float* Dh = Dq ? Dq + head : nullptr;
+      product_from_registers<NT, HS>(acc, CAUSAL ? qb + 1 : NT, S, 32 * qb, dQ + head, Dh, HS);
+      load_tile<TT>(dSh, qa, CAUSAL ? qa + 1 : NT, acc);
+      product_from_registers<NT, HS>(acc, CAUSAL ? qa + 1 : NT, S, 32 * qa, dQ + head, Dh, HS);
+    }
   }
 }
 
 template <int TT, int HS>
 void launch_bwd(const float* dO, int ldo, int H, const float* V, const float* P, const float* scale, float* dS,
                 const float* K, float* dQ, const float* Dq, int bh, bool causal, hipStream_t s) {
-  const dim3 grid((TT / 32 + 3) / 4, (unsigned)bh);
+  const dim3 grid(1, (unsigned)bh);  // one workgroup per head
   if (dQ) {
     if (causal) k_attn_bwd<TT, HS, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq);
     else k_attn_bwd<TT, HS, false, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq);
