@@ -239,6 +239,116 @@ __global__ __launch_bounds__(256) void k_layernorm_bwd_rows(const float* __restr
   yt.store(dx + row * axis, axis, lane);
 }
 
+// Half-wave forms of the two layernorm kernels for rows of 128 * NV floats
+// (NV <= 4: the C = 128 .. 512 models): 32 lanes per row, NV float4 per lane
+// with no idle lanes, eight rows per workgroup.  Same arithmetic as the
+// full-wave kernels above; the sums run over 32 lanes instead of 64.
+__device__ __forceinline__ float hsum(float v) {
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) v += __shfl_xor(v, off, 32);
+  return v;
+}
+constexpr int kHalfRowsPerBlock = 8;
+
+template <int NV>
+__global__ __launch_bounds__(256) void k_layernorm_rows32(const float* __restrict__ x, float* __restrict__ y,
+                                                          float* __restrict__ var, size_t rows, float eps,
+                                                          const float* __restrict__ w, float* __restrict__ out) {
+  constexpr uint32_t axis = 128 * NV;
+  const size_t row = (size_t)blockIdx.x * kHalfRowsPerBlock + threadIdx.x / 32;
+  const int hl = threadIdx.x % 32;
+  if (row >= rows) return;  // whole half-waves leave together
+  const float4* xr = reinterpret_cast<const float4*>(x + row * axis);
+  float v[4 * NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const float4 t = xr[hl + 32 * j];
+    v[4 * j] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4 * NV; ++e) s += v[e];
+  s = hsum(s);
+  const float mu = s / (float)axis;
+  float q = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4 * NV; ++e) { float dd = v[e] - mu; q += dd * dd; }
+  q = hsum(q);
+  const float va = q / (float)axis;
+  const float sigma = sqrtf(va + eps);
+#pragma unroll
+  for (int e = 0; e < 4 * NV; ++e) v[e] = (v[e] - mu) / sigma;
+  float4* yr = reinterpret_cast<float4*>(y + row * axis);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) yr[hl + 32 * j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+  if (hl == 0 && var) var[row] = va;
+  if (w) {
+    const float4* wr = reinterpret_cast<const float4*>(w);
+    float4* orow = reinterpret_cast<float4*>(out + row * axis);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const float4 g = wr[hl + 32 * j];
+      orow[hl + 32 * j] = make_float4(v[4 * j] * g.x, v[4 * j + 1] * g.y, v[4 * j + 2] * g.z, v[4 * j + 3] * g.w);
+    }
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void k_layernorm_bwd_rows32(const float* __restrict__ y, const float* __restrict__ var,
+                                                              const float* __restrict__ dout, float* __restrict__ dx,
+                                                              size_t rows, float eps, const float* __restrict__ addend,
+                                                              const float* __restrict__ w) {
+  constexpr uint32_t axis = 128 * NV;
+  const size_t row = (size_t)blockIdx.x * kHalfRowsPerBlock + threadIdx.x / 32;
+  const int hl = threadIdx.x % 32;
+  if (row >= rows) return;
+  const float4* yr = reinterpret_cast<const float4*>(y + row * axis);
+  const float4* dr = reinterpret_cast<const float4*>(dout + row * axis);
+  float yv[4 * NV], dv[4 * NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const float4 a = yr[hl + 32 * j], b = dr[hl + 32 * j];
+    yv[4 * j] = a.x; yv[4 * j + 1] = a.y; yv[4 * j + 2] = a.z; yv[4 * j + 3] = a.w;
+    dv[4 * j] = b.x; dv[4 * j + 1] = b.y; dv[4 * j + 2] = b.z; dv[4 * j + 3] = b.w;
+  }
+  if (w) {  // dout is the gradient of y * w: dy = dout * w, rounded like the multiply's VJP
+    const float4* wr = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const float4 g = wr[hl + 32 * j];
+      dv[4 * j] = dv[4 * j] * g.x; dv[4 * j + 1] = dv[4 * j + 1] * g.y;
+      dv[4 * j + 2] = dv[4 * j + 2] * g.z; dv[4 * j + 3] = dv[4 * j + 3] * g.w;
+    }
+  }
+  float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4 * NV; ++e) { s1 += dv[e]; float p = dv[e] * yv[e]; s2 += p; }
+  s1 = hsum(s1);
+  s2 = hsum(s2);
+  const float dy_mean = s1 / (float)axis;
+  const float dyy_mean = s2 / (float)axis;
+  const float inv_sigma = 1.0f / sqrtf(var[row] + eps);
+#pragma unroll
+  for (int e = 0; e < 4 * NV; ++e) {
+    float y_term = yv[e] * dyy_mean;
+    float tmp = dv[e] - dy_mean;
+    float numer = tmp - y_term;
+    yv[e] = numer * inv_sigma;
+  }
+  if (addend) {  // gradient accumulation: old + this VJP's value
+    const float4* ar = reinterpret_cast<const float4*>(addend + row * axis);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const float4 a = ar[hl + 32 * j];
+      yv[4 * j] = a.x + yv[4 * j]; yv[4 * j + 1] = a.y + yv[4 * j + 1];
+      yv[4 * j + 2] = a.z + yv[4 * j + 2]; yv[4 * j + 3] = a.w + yv[4 * j + 3];
+    }
+  }
+  float4* xr = reinterpret_cast<float4*>(dx + row * axis);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) xr[hl + 32 * j] = make_float4(yv[4 * j], yv[4 * j + 1], yv[4 * j + 2], yv[4 * j + 3]);
+}
+
 // cross_entropy.ml:18-28 / metal.rs:1555-1598: probs = softmax(logits, 1),
 // nll[i] = -log(probs[i, t_i]) read back from the rounded probability.
 template <int NV, int VM>
@@ -486,7 +596,16 @@ void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, si
 void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s,
                const float* w, float* out) {
   if (!outer || !axis || !inner) return;
-  if (inner == 1 && axis <= kMaxRowAxis) {
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (inner == 1 && axis % 128 == 0 && axis <= 512 && a16(x) && a16(y) && a16(w) && a16(out)) {
+    const unsigned grid = (unsigned)((outer + kHalfRowsPerBlock - 1) / kHalfRowsPerBlock);
+    switch (axis / 128) {
+      case 1: k_layernorm_rows32<1><<<grid, 256, 0, s>>>(x, y, var, outer, eps, w, out); break;
+      case 2: k_layernorm_rows32<2><<<grid, 256, 0, s>>>(x, y, var, outer, eps, w, out); break;
+      case 3: k_layernorm_rows32<3><<<grid, 256, 0, s>>>(x, y, var, outer, eps, w, out); break;
+      default: k_layernorm_rows32<4><<<grid, 256, 0, s>>>(x, y, var, outer, eps, w, out); break;
+    }
+  } else if (inner == 1 && axis <= kMaxRowAxis) {
     row_dispatch<SelLN>((uint32_t)axis, [&](auto sel) {
       decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(x, y, var, outer, (uint32_t)axis, eps, w, out);
     }, (w ? 3 : 2) * outer * (size_t)axis * sizeof(float));
@@ -500,7 +619,16 @@ void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, 
 void layernorm_bwd(const float* y, const float* var, const float* dout, float* dx, size_t outer, size_t axis, size_t inner,
                    float eps, hipStream_t s, const float* addend, const float* w) {
   if (!outer || !axis || !inner) return;
-  if (inner == 1 && axis <= kMaxRowAxis) {
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (inner == 1 && axis % 128 == 0 && axis <= 512 && a16(y) && a16(dout) && a16(dx) && a16(addend) && a16(w)) {
+    const unsigned grid = (unsigned)((outer + kHalfRowsPerBlock - 1) / kHalfRowsPerBlock);
+    switch (axis / 128) {
+      case 1: k_layernorm_bwd_rows32<1><<<grid, 256, 0, s>>>(y, var, dout, dx, outer, eps, addend, w); break;
+      case 2: k_layernorm_bwd_rows32<2><<<grid, 256, 0, s>>>(y, var, dout, dx, outer, eps, addend, w); break;
+      case 3: k_layernorm_bwd_rows32<3><<<grid, 256, 0, s>>>(y, var, dout, dx, outer, eps, addend, w); break;
+      default: k_layernorm_bwd_rows32<4><<<grid, 256, 0, s>>>(y, var, dout, dx, outer, eps, addend, w); break;
+    }
+  } else if (inner == 1 && axis <= kMaxRowAxis) {
     row_dispatch<SelLNBwd>((uint32_t)axis, [&](auto sel) {
       decltype(sel)::fn<<<row_grid(outer), 256, 0, s>>>(y, var, dout, dx, outer, (uint32_t)axis, eps, addend, w);
     }, 3 * outer * (size_t)axis * sizeof(float));
