@@ -92,6 +92,7 @@ __device__ __forceinline__ void product_from_registers(const v16f (&a)[NT], int 
   v16f o[NN];
 #pragma unroll
   for (int n = 0; n < NN; ++n) o[n] = v16f{0};
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if (t < live) {
@@ -105,6 +106,7 @@ __device__ __forceinline__ void product_from_registers(const v16f (&a)[NT], int 
         }
     }
   }
+  __builtin_amdgcn_s_setprio(0);
 #pragma unroll
   for (int n = 0; n < NN; ++n)
 #pragma unroll
@@ -144,6 +146,7 @@ __device__ __forceinline__ void softmax_tile(const float* __restrict__ Qh, const
   for (int e = 0; e < 2 * NKB; ++e) qv[e] = qp[4 * (e >> 1) + (e & 1)];
 
   // A operand: K[32 t + key_row(x)][16 kb + 8 lk + s] from LDS
+  __builtin_amdgcn_s_setprio(1);  // MFMA issue ahead of the CU's other waves
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     acc[t] = v16f{0};
@@ -161,6 +164,8 @@ __device__ __forceinline__ void softmax_tile(const float* __restrict__ Qh, const
       }
     }
   }
+
+  __builtin_amdgcn_s_setprio(0);
 
   // x = S * scale + mask[i][j]; row max.  The causal mask is the one
   // tensor_causal_mask fills: -1e9 where j > i, else 0.
@@ -322,6 +327,7 @@ __device__ __forceinline__ void dscores_tile(const float* __restrict__ dOh, int 
   v4f ov[2 * NKB];
 #pragma unroll
   for (int e = 0; e < 2 * NKB; ++e) ov[e] = op[4 * (e >> 1) + (e & 1)];
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     acc[t] = v16f{0};
@@ -339,6 +345,8 @@ __device__ __forceinline__ void dscores_tile(const float* __restrict__ dOh, int 
       }
     }
   }
+
+  __builtin_amdgcn_s_setprio(0);
 
   // per-group sums of dP * P, then the row kernel's tree
   const v4f* prow = reinterpret_cast<const v4f*>(Ph + (size_t)i * TT);
