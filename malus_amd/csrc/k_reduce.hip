@@ -143,7 +143,8 @@ __global__ __launch_bounds__(256) void k_row_split(const float* __restrict__ x, 
 // columns 4 * (cb * CT + ct) .. +3 and rows beg + rt, beg + rt + RT, ... of
 // the axis chunk [beg, end).  The RT partial sums of a column are folded in
 // rt order through LDS.  nsplit == 1 writes the finalized value; otherwise
-// partial[(o * nsplit + sp) * inner + i].
+// partial[(o * inner + i) * nsplit + sp], so that a column's partials form
+// one contiguous row for the combining row reduction.
 template <int OP, int CT>
 __global__ __launch_bounds__(256) void k_col4(const float* __restrict__ x, const float* __restrict__ y,
                                               const float* __restrict__ mean, float* __restrict__ dst, size_t axis,
@@ -206,8 +207,12 @@ __global__ __launch_bounds__(256) void k_col4(const float* __restrict__ x, const
         r.w = rfinal<OP>(r.w, (uint32_t)axis);
       }
       reinterpret_cast<float4*>(dst + o * inner)[i4] = r;
-    } else {
-      reinterpret_cast<float4*>(dst + (o * nsplit + sp) * inner)[i4] = r;
+    } else {  // split partials column-major: column c's nsplit partials are contiguous
+      float* pc = dst + (o * inner + 4 * i4) * nsplit + sp;
+      pc[0] = r.x;
+      pc[nsplit] = r.y;
+      pc[2 * (size_t)nsplit] = r.z;
+      pc[3 * (size_t)nsplit] = r.w;
     }
   }
 }
@@ -380,7 +385,20 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
                                                                 (uint32_t)col_blocks, nsplit == 1);
   }
   MALUS_HIP(hipGetLastError());
-  if (nsplit > 1) {
+  if (nsplit > 1 && vec) {
+    // one wave per column over its contiguous partials (MEAN and VAR divide
+    // the combined sum by the axis length in the same kernel)
+    constexpr int FIN = COMB == R_MAX ? R_MAX : (OP == R_MEAN || OP == R_VAR) ? R_MEAN : R_SUM;
+    const size_t cols = outer * inner;
+    if (nsplit % 4 == 0)
+      k_row_wave<FIN, true><<<(unsigned)((cols + 3) / 4), 256, 0, s>>>(dst, nullptr, nullptr, out, cols, nsplit,
+                                                                        (uint32_t)axis, true, false);
+    else
+      k_row_wave<FIN, false><<<(unsigned)((cols + 3) / 4), 256, 0, s>>>(dst, nullptr, nullptr, out, cols, nsplit,
+                                                                         (uint32_t)axis, true, false);
+    MALUS_HIP(hipGetLastError());
+    pool_free(dst, bucket);
+  } else if (nsplit > 1) {
     // base_blocks < 2048 here, so outer fits gridDim.y
     // columns per combine block: enough split groups to keep ~4+ partials each
     const int cc = nsplit >= 256 ? 4 : nsplit >= 64 ? 16 : 64;
