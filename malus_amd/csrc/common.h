@@ -163,6 +163,12 @@ bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const f
               const float* K, float* dQ, const float* Dq, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s);
 // Sum over the axis of x * y (y has x's layout); each product rounded to f32.
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
+// The split of reduce_axis_prod's column reduction over [axis, inner]
+// (outer = 1): nsplit chunks of `chunk` rows, row_threads rows interleaved
+// per chunk.  False when it does not split on the float4 path.
+bool col_prod_split(size_t axis, size_t inner, uint32_t* nsplit, size_t* chunk, int* row_threads);
+// out[c] = the sum of partial[c * nsplit ..], as that reduction combines them.
+void col_combine_sum(const float* partial, float* out, size_t cols, uint32_t nsplit, size_t axis, hipStream_t s);
 // Broadcast [outer, inner] back to [outer, axis, inner] (expand_axis).
 void expand_axis(const float* small, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 
@@ -175,6 +181,11 @@ void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, 
 // With addend: dx = addend + VJP (gradient accumulation folded in).  With w
 // (last axis only): dout is the gradient of y * w, and dy = dout * w is formed
 // in the kernel.
+// layernorm_bwd with the scale w, plus dw = reduce_axis_prod(dout, y) over
+// the rows, from one row kernel and the combine (bit-identical to the two
+// separate calls).  False (nothing launched) when the shape has no such form.
+bool layernorm_bwd_scale(const float* y, const float* var, const float* dout, float* dx, float* dw, size_t rows,
+                         size_t axis, float eps, hipStream_t s, const float* addend, const float* w);
 void layernorm_bwd(const float* y, const float* var, const float* dout, float* dx, size_t outer, size_t axis, size_t inner,
                    float eps, hipStream_t s,
                    const float* addend = nullptr, const float* w = nullptr);

@@ -303,6 +303,44 @@ void launch_col4(int ct, dim3 grid, const float* x, const float* y, const float*
   }
 }
 
+// The column reduction's launch plan for [outer, axis, inner] (inner > 1):
+// float4 path (vec) with CT column-threads x 256/CT row-threads per block, or
+// the scalar path; the axis split into nsplit chunks of `chunk` rows until
+// the grid holds ~2048 workgroups, keeping >= 4 rows per row-thread (vec) or
+// >= 16 rows per thread (scalar).
+struct ColPlan {
+  bool vec;
+  int ct;
+  size_t col_blocks;
+  uint32_t nsplit;
+  size_t chunk;
+};
+ColPlan col_plan(size_t outer, size_t axis, size_t inner, bool aligned) {
+  ColPlan p{};
+  p.vec = inner % 4 == 0 && outer <= 65535 && aligned;
+  p.ct = 64;
+  if (p.vec) {
+    const size_t groups = inner / 4;  // float4 columns
+    while (p.ct > 8 && groups % p.ct != 0) p.ct >>= 1;
+    if (groups % p.ct != 0) p.ct = 64;
+    p.col_blocks = (groups + p.ct - 1) / p.ct;
+  } else {
+    p.col_blocks = (inner + 255) / 256;
+  }
+  const size_t base_blocks = outer * p.col_blocks;
+  const size_t rows_per_block = p.vec ? (size_t)(256 / p.ct) * 4 : 16;
+  p.nsplit = 1;
+  if (base_blocks < 2048) {
+    size_t want = (2048 + base_blocks - 1) / base_blocks;
+    size_t cap = axis / rows_per_block > 0 ? axis / rows_per_block : 1;
+    p.nsplit = (uint32_t)(want < cap ? want : cap);
+    if (p.nsplit > 65535) p.nsplit = 65535;
+  }
+  p.chunk = (axis + p.nsplit - 1) / p.nsplit;
+  p.nsplit = (uint32_t)((axis + p.chunk - 1) / p.chunk);
+  return p;
+}
+
 template <int OP>
 void reduce_impl(const float* x, const float* y, const float* mean, float* out, size_t outer, size_t axis, size_t inner,
                  hipStream_t s) {
@@ -347,33 +385,11 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
   }
   // column reduction
   const bool aligned = ((uintptr_t)x | (uintptr_t)y | (uintptr_t)mean | (uintptr_t)out) % 16 == 0;
-  const bool vec = inner % 4 == 0 && outer <= 65535 && aligned;
-  size_t col_blocks, per_block_cols;
-  int ct = 64;
-  if (vec) {
-    const size_t groups = inner / 4;  // float4 columns
-    while (ct > 8 && groups % ct != 0) ct >>= 1;
-    if (groups % ct != 0) ct = 64;
-    per_block_cols = 4 * (size_t)ct;
-    col_blocks = (groups + ct - 1) / ct;
-  } else {
-    per_block_cols = 256;
-    col_blocks = (inner + 255) / 256;
-  }
-  const size_t base_blocks = outer * col_blocks;
-  // split the axis until the grid holds ~2048 workgroups, keeping >= 4 rows
-  // per row-thread (vec) or >= 16 rows per thread (scalar)
-  const size_t rows_per_block = vec ? (size_t)(256 / ct) * 4 : 16;
-  uint32_t nsplit = 1;
-  if (base_blocks < 2048) {
-    size_t want = (2048 + base_blocks - 1) / base_blocks;
-    size_t cap = axis / rows_per_block > 0 ? axis / rows_per_block : 1;
-    nsplit = (uint32_t)(want < cap ? want : cap);
-    if (nsplit > 65535) nsplit = 65535;
-  }
-  size_t chunk = (axis + nsplit - 1) / nsplit;
-  nsplit = (uint32_t)((axis + chunk - 1) / chunk);
-  (void)per_block_cols;
+  const ColPlan cp = col_plan(outer, axis, inner, aligned);
+  const bool vec = cp.vec;
+  const int ct = cp.ct;
+  const size_t col_blocks = cp.col_blocks, base_blocks = outer * col_blocks, chunk = cp.chunk;
+  const uint32_t nsplit = cp.nsplit;
   float* dst = out;
   size_t bucket = 0;
   if (nsplit > 1) dst = static_cast<float*>(pool_alloc(outer * nsplit * inner * sizeof(float), &bucket));
@@ -440,6 +456,26 @@ void reduce_axis(int op, const float* x, float* out, size_t outer, size_t axis, 
 
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {
   reduce_impl<R_PROD>(x, y, nullptr, out, outer, axis, inner, s);
+}
+
+bool col_prod_split(size_t axis, size_t inner, uint32_t* nsplit, size_t* chunk, int* row_threads) {
+  if (inner <= 1) return false;
+  const ColPlan p = col_plan(1, axis, inner, true);
+  if (!p.vec || p.nsplit < 2) return false;
+  *nsplit = p.nsplit;
+  *chunk = p.chunk;
+  *row_threads = 256 / p.ct;
+  return true;
+}
+
+void col_combine_sum(const float* partial, float* out, size_t cols, uint32_t nsplit, size_t axis, hipStream_t s) {
+  if (nsplit % 4 == 0)
+    k_row_wave<R_SUM, true><<<(unsigned)((cols + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, cols, nsplit,
+                                                                        (uint32_t)axis, true, false);
+  else
+    k_row_wave<R_SUM, false><<<(unsigned)((cols + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, cols, nsplit,
+                                                                         (uint32_t)axis, true, false);
+  MALUS_HIP(hipGetLastError());
 }
 
 void expand_axis(const float* small, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {

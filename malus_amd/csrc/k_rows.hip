@@ -349,6 +349,94 @@ __global__ __launch_bounds__(256) void k_layernorm_bwd_rows32(const float* __res
   for (int j = 0; j < NV; ++j) xr[hl + 32 * j] = make_float4(yv[4 * j], yv[4 * j + 1], yv[4 * j + 2], yv[4 * j + 3]);
 }
 
+// k_layernorm_bwd_rows32 for the rows of one 32-row chunk per workgroup
+// (half-wave h takes rows beg + h + 8 k, k = 0..3), which also forms the
+// chunk's column partial of dw = sum over rows of dout * y (the scale's
+// VJP): each half-wave sums its rows' products in k order, then the eight
+// half-waves' sums are added in order.  That is exactly the partial the
+// column reduction (k_col4 with 8 row-threads over 32-row chunks) writes,
+// so the combined dw is the separate reduction's, bit for bit.  Partials go
+// column-major: partial[c * nsplit + chunk].
+template <int NV>
+__global__ __launch_bounds__(256) void k_layernorm_bwd_scale_rows32(const float* __restrict__ y,
+                                                                    const float* __restrict__ var,
+                                                                    const float* __restrict__ dout,
+                                                                    float* __restrict__ dx, size_t rows, float eps,
+                                                                    const float* __restrict__ addend,
+                                                                    const float* __restrict__ w,
+                                                                    float* __restrict__ partial, uint32_t nsplit) {
+  constexpr uint32_t axis = 128 * NV;
+  __shared__ float red[8][axis];
+  const int hw = threadIdx.x / 32, hl = threadIdx.x % 32;
+  float pacc[4 * NV];
+#pragma unroll
+  for (int e = 0; e < 4 * NV; ++e) pacc[e] = 0.0f;
+#pragma unroll 1
+  for (int k = 0; k < 4; ++k) {
+    const size_t row = (size_t)blockIdx.x * 32 + hw + 8 * k;
+    if (row >= rows) break;  // uniform over the half-wave
+    const float4* yr = reinterpret_cast<const float4*>(y + row * axis);
+    const float4* dr = reinterpret_cast<const float4*>(dout + row * axis);
+    float yv[4 * NV], dv[4 * NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const float4 a = yr[hl + 32 * j], b = dr[hl + 32 * j];
+      yv[4 * j] = a.x; yv[4 * j + 1] = a.y; yv[4 * j + 2] = a.z; yv[4 * j + 3] = a.w;
+      dv[4 * j] = b.x; dv[4 * j + 1] = b.y; dv[4 * j + 2] = b.z; dv[4 * j + 3] = b.w;
+    }
+#pragma unroll
+    for (int e = 0; e < 4 * NV; ++e) {
+      const float p = dv[e] * yv[e];  // dout * y, rounded like the reduction's product
+      pacc[e] = pacc[e] + p;
+    }
+    const float4* wr = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const float4 g = wr[hl + 32 * j];
+      dv[4 * j] = dv[4 * j] * g.x; dv[4 * j + 1] = dv[4 * j + 1] * g.y;
+      dv[4 * j + 2] = dv[4 * j + 2] * g.z; dv[4 * j + 3] = dv[4 * j + 3] * g.w;
+    }
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4 * NV; ++e) { s1 += dv[e]; float p = dv[e] * yv[e]; s2 += p; }
+    s1 = hsum(s1);
+    s2 = hsum(s2);
+    const float dy_mean = s1 / (float)axis;
+    const float dyy_mean = s2 / (float)axis;
+    const float inv_sigma = 1.0f / sqrtf(var[row] + eps);
+#pragma unroll
+    for (int e = 0; e < 4 * NV; ++e) {
+      float y_term = yv[e] * dyy_mean;
+      float tmp = dv[e] - dy_mean;
+      float numer = tmp - y_term;
+      yv[e] = numer * inv_sigma;
+    }
+    if (addend) {
+      const float4* ar = reinterpret_cast<const float4*>(addend + row * axis);
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const float4 a = ar[hl + 32 * j];
+        yv[4 * j] = a.x + yv[4 * j]; yv[4 * j + 1] = a.y + yv[4 * j + 1];
+        yv[4 * j + 2] = a.z + yv[4 * j + 2]; yv[4 * j + 3] = a.w + yv[4 * j + 3];
+      }
+    }
+    float4* xr = reinterpret_cast<float4*>(dx + row * axis);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) xr[hl + 32 * j] = make_float4(yv[4 * j], yv[4 * j + 1], yv[4 * j + 2], yv[4 * j + 3]);
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[hw][4 * (hl + 32 * j) + c] = pacc[4 * j + c];
+  __syncthreads();
+  for (uint32_t col = threadIdx.x; col < axis; col += 256) {
+    float r = red[0][col];
+#pragma unroll
+    for (int h = 1; h < 8; ++h) r = r + red[h][col];
+    partial[(size_t)col * nsplit + blockIdx.x] = r;
+  }
+}
+
 // cross_entropy.ml:18-28 / metal.rs:1555-1598: probs = softmax(logits, 1),
 // nll[i] = -log(probs[i, t_i]) read back from the rounded probability.
 template <int NV, int VM>
@@ -638,6 +726,30 @@ void layernorm_bwd(const float* y, const float* var, const float* dout, float* d
     if (addend) binary_same(ADD, addend, dx, dx, outer * axis * inner, s);
   }
   MALUS_HIP(hipGetLastError());
+}
+
+bool layernorm_bwd_scale(const float* y, const float* var, const float* dout, float* dx, float* dw, size_t rows,
+                         size_t axis, float eps, hipStream_t s, const float* addend, const float* w) {
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (!rows || axis % 128 != 0 || axis > 512 || !w || !a16(y) || !a16(dout) || !a16(dx) || !a16(addend) || !a16(w))
+    return false;
+  uint32_t nsplit = 0;
+  size_t chunk = 0;
+  int rt = 0;
+  // the chunking must be the one the separate column reduction uses
+  if (!col_prod_split(rows, axis, &nsplit, &chunk, &rt) || chunk != 32 || rt != 8) return false;
+  size_t bucket;
+  float* partial = static_cast<float*>(pool_alloc(axis * nsplit * sizeof(float), &bucket));
+  switch (axis / 128) {
+    case 1: k_layernorm_bwd_scale_rows32<1><<<nsplit, 256, 0, s>>>(y, var, dout, dx, rows, eps, addend, w, partial, nsplit); break;
+    case 2: k_layernorm_bwd_scale_rows32<2><<<nsplit, 256, 0, s>>>(y, var, dout, dx, rows, eps, addend, w, partial, nsplit); break;
+    case 3: k_layernorm_bwd_scale_rows32<3><<<nsplit, 256, 0, s>>>(y, var, dout, dx, rows, eps, addend, w, partial, nsplit); break;
+    default: k_layernorm_bwd_scale_rows32<4><<<nsplit, 256, 0, s>>>(y, var, dout, dx, rows, eps, addend, w, partial, nsplit); break;
+  }
+  MALUS_HIP(hipGetLastError());
+  col_combine_sum(partial, dw, axis, nsplit, rows, s);
+  pool_free(partial, bucket);
+  return true;
 }
 
 void ce_fwd(const float* logits, const int32_t* tgt, float* probs, float* nll, size_t n, size_t v, int32_t* err,

@@ -799,6 +799,30 @@ int64_t ln_affine_bwd_x(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const 
   return done(out, "layernorm_affine_bwd");
 }
 
+// ln_affine_bwd_x and the scale's gradient mul_bwd_b(dout, y, w) from one
+// row kernel (bit-identical to the two calls); *dw_out gets dw.  0 when the
+// shape has no fused form (nothing launched).
+int64_t ln_affine_bwd_xw(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const TensorBuffer* D, int64_t* dw_out) {
+  TensorBuffer *ty = T(hy), *tv = T(hvar), *tw = T(hw), *td = T(hd);
+  const size_t a = ty->shape[ty->ndim - 1], o = ty->len / a;
+  if (tv->len != o || tw->len != a || td->len != ty->len || tw->ndim != 1) return 0;
+  if (D && (D->dtype != F32 || D->len != ty->len))
+    fail("malus: layernorm VJP accumulate: addend %s does not match %s", shape_str(D).c_str(), shape_str(ty).c_str());
+  TensorBuffer* out = alloc_like(ty);
+  TensorBuffer* dw = alloc_tensor(F32, tw->shape, tw->ndim);
+  if (!k::layernorm_bwd_scale(ty->f32(), tv->f32(), td->f32(), out->f32(), dw->f32(), o, a, 1e-5f, stream(),
+                              D ? D->f32() : nullptr, tw->f32())) {
+    release(out);
+    release(dw);
+    return 0;
+  }
+  const uint64_t seq = enqueue_mark("layernorm_affine_bwd_xw");
+  out->write_seq = seq;
+  dw->write_seq = seq;
+  *dw_out = malus::H(dw);
+  return malus::H(out);
+}
+
 // h = x @ W1 and ge = gelu(h) from one GEMM (nanogpt_modular.ml:63);
 // returns h, *ge_out gets gelu(h).  0 when the shape does not fit the fused
 // epilogue (nothing launched).

@@ -539,6 +539,15 @@ void backward(int64_t loss) {
         need_values(w);
         need_values(y);
         // the multiply's VJPs (dy, then dw), then the layernorm VJP of dy
+        if (na && nb && slot_is(MulBwdB, &malus_std_mul_bwd_b)) {  // both from one row kernel where it applies
+          int64_t dw = 0;
+          fold_grad(grads, x, [&](const TensorBuffer* o) {
+            const int64_t dx = ln_affine_bwd_xw(y, var, w, dout, o, &dw);
+            return dx ? dx : ln_affine_bwd_x(y, var, w, dout, o);
+          });
+          accumulate(grads, w, dw ? dw : slot_fn<Fn3>(MulBwdB)(dout, y, w));
+          break;
+        }
         if (nb) accumulate(grads, w, slot_fn<Fn3>(MulBwdB)(dout, y, w));
         if (na) fold_grad(grads, x, [&](const TensorBuffer* o) { return ln_affine_bwd_x(y, var, w, dout, o); });
         break;
