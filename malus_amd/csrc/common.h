@@ -199,6 +199,10 @@ void nll_gather(const float* probs, const int32_t* tgt, float* nll, size_t n, si
 
 // Gathers / index ops.
 void embedding(const float* w, const int32_t* idx, float* out, size_t t, size_t v, size_t d, int32_t* err, hipStream_t s);
+// out = embedding(wa, ia) + embedding(wb, ib) in one pass (d % 4 == 0;
+// 16-byte aligned tables and output).
+void embedding2(const float* wa, const int32_t* ia, size_t va, const float* wb, const int32_t* ib, size_t vb, float* out,
+                size_t t, size_t d, int32_t* err, hipStream_t s);
 void embedding_bwd(const float* dout, const int32_t* idx, float* dw, size_t t, size_t v, size_t d, hipStream_t s);
 void permute(const float* x, float* out, int ndim, const size_t* in_shape, const size_t* perm, hipStream_t s);
 

@@ -254,6 +254,40 @@ __global__ __launch_bounds__(256) void k_transpose_last2(const float* __restrict
 
 }  // namespace
 
+// The token and position embeddings and their sum in one pass:
+// out[t, c] = wa[ia[t], c] + wb[ib[t], c] (embedding.ml:11-16 twice, then the
+// broadcast add: the same f32 add).  Out-of-range rows count as zero rows
+// and set the error flag, as in k_embedding.
+__global__ __launch_bounds__(256) void k_embedding2(const float* __restrict__ wa, const int32_t* __restrict__ ia,
+                                                    uint32_t va, const float* __restrict__ wb,
+                                                    const int32_t* __restrict__ ib, uint32_t vb,
+                                                    float* __restrict__ out, size_t t, uint32_t d,
+                                                    int32_t* __restrict__ err) {
+  const size_t row = (size_t)blockIdx.x * 4 + threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  if (row >= t) return;
+  const int32_t ra = ia[row], rb = ib[row];
+  const bool oka = ra >= 0 && (uint32_t)ra < va, okb = rb >= 0 && (uint32_t)rb < vb;
+  if ((!oka || !okb) && lane == 0) *err = 1;
+  const float* pa = wa + (size_t)(oka ? ra : 0) * d;
+  const float* pb = wb + (size_t)(okb ? rb : 0) * d;
+  float* o = out + row * d;
+  for (uint32_t c = lane; c < d / 4; c += 64) {
+    const float4 a = oka ? reinterpret_cast<const float4*>(pa)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 b = okb ? reinterpret_cast<const float4*>(pb)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    reinterpret_cast<float4*>(o)[c] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+  }
+}
+
+void embedding2(const float* wa, const int32_t* ia, size_t va, const float* wb, const int32_t* ib, size_t vb, float* out,
+                size_t t, size_t d, int32_t* err, hipStream_t s) {
+  if (!t || !d) return;
+  if (d % 4) fail("malus: embedding2: row length %zu is not a multiple of 4", d);
+  k_embedding2<<<(unsigned)((t + 3) / 4), 256, 0, s>>>(wa, ia, (uint32_t)va, wb, ib, (uint32_t)vb, out, t, (uint32_t)d,
+                                                       err);
+  MALUS_HIP(hipGetLastError());
+}
+
 void embedding(const float* w, const int32_t* idx, float* out, size_t t, size_t v, size_t d, int32_t* err, hipStream_t s) {
   if (!t || !d) return;
   k_embedding<<<(unsigned)((t + 3) / 4), 256, 0, s>>>(w, idx, out, t, (uint32_t)v, (uint32_t)d, err);

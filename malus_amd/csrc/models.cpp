@@ -271,11 +271,31 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
 
 // GPT.forward (nanogpt_modular.ml:75-91) + cross_entropy (lib.rs:2945-2972)
 int64_t gpt_forward_loss(Gpt& g, int64_t toks, int64_t targets, int64_t* logits_out) {
-  int64_t te = malus_std_embedding_fwd(g.top(0), toks);
-  tape_record_embedding(OP_EMBEDDING, g.top(0), toks, te);
-  int64_t pe = malus_std_embedding_fwd(g.top(1), g.pos);
-  tape_record_embedding(OP_EMBEDDING, g.top(1), g.pos, pe);
-  int64_t x = binop(OP_ADD, te, pe);
+  int64_t te, pe, x;
+  TensorBuffer *wte = T(g.top(0)), *wpe = T(g.top(1)), *tk = T(toks), *ps = T(g.pos);
+  if (g.fused_fwd && tk->dtype == I32 && ps->dtype == I32 && tk->ndim == 1 && tk->len == ps->len &&
+      wte->shape[1] == wpe->shape[1] && wte->shape[1] % 4 == 0) {
+    // tok_emb + pos_emb in one pass; the tape gets the same three records,
+    // with the two embeddings as shape-only handles (their VJPs read the
+    // indices and the gradient, the add's reads shapes)
+    const size_t d = wte->shape[1], sh[2] = {tk->len, d};
+    TensorBuffer* xo = alloc_tensor(F32, sh, 2);
+    k::embedding2(wte->f32(), tk->i32(), wte->shape[0], wpe->f32(), ps->i32(), wpe->shape[0], xo->f32(), tk->len, d,
+                  device_error_flag(), stream());
+    xo->write_seq = enqueue_mark("embedding2");
+    te = malus::H(alloc_virtual(F32, sh, 2));
+    pe = malus::H(alloc_virtual(F32, sh, 2));
+    x = malus::H(xo);
+    tape_record_embedding(OP_EMBEDDING, g.top(0), toks, te);
+    tape_record_embedding(OP_EMBEDDING, g.top(1), g.pos, pe);
+    tape_record_binop(OP_ADD, te, pe, x);
+  } else {
+    te = malus_std_embedding_fwd(g.top(0), toks);
+    tape_record_embedding(OP_EMBEDDING, g.top(0), toks, te);
+    pe = malus_std_embedding_fwd(g.top(1), g.pos);
+    tape_record_embedding(OP_EMBEDDING, g.top(1), g.pos, pe);
+    x = binop(OP_ADD, te, pe);
+  }
   rel({te, pe});
   for (int l = 0; l < g.L; ++l) {
     int64_t nx = block_forward(g, l, x);
