@@ -261,6 +261,33 @@ def test_backward_neg_sum_transpose_matmul(tape):
     rt.free(A, B, Cm, T, TT)
 
 
+def test_matmul_vjps_with_both_operands_watched(tape):
+    """A @ B with both operands watched (dA and dB from the two VJP GEMMs),
+    then X @ X, whose two VJPs add into the one gradient.  Gradients against
+    float64 products of the same inputs."""
+    rt = tape
+    rng = np.random.default_rng(11)
+    av = rng.uniform(-1, 1, (300, 200)).astype(np.float32)
+    bv = rng.uniform(-1, 1, (200, 96)).astype(np.float32)
+    xv = rng.uniform(-1, 1, (96, 96)).astype(np.float32)
+    A, B, X = rt.tensor(av), rt.tensor(bv), rt.tensor(xv)
+    for h in (A, B, X):
+        rt.L.tape_register_leaf(h)
+    Cm = rt.L.tensor_matmul(A, B)
+    rt.L.tape_record_binop(OP["Matmul"], A, B, Cm)
+    rt.L.backward(Cm)
+    ones = np.ones((300, 96))
+    np.testing.assert_allclose(grad(rt, A), ones @ bv.T.astype(np.float64), rtol=1e-5, atol=1e-4)
+    np.testing.assert_allclose(grad(rt, B), av.T.astype(np.float64) @ ones, rtol=1e-5, atol=1e-4)
+    Xm = rt.L.tensor_matmul(X, X)
+    rt.L.tape_record_binop(OP["Matmul"], X, X, Xm)
+    rt.L.backward(Xm)
+    o2 = np.ones((96, 96))
+    want = o2 @ xv.T.astype(np.float64) + xv.T.astype(np.float64) @ o2
+    np.testing.assert_allclose(grad(rt, X), want, rtol=1e-5, atol=1e-4)
+    rt.free(A, B, X, Cm, Xm)
+
+
 def test_grad_accumulates_across_backwards_and_zero_grad(tape):
     rt = tape
     a = leaf(rt, 2)
