@@ -165,7 +165,8 @@ bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const f
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 // The split of reduce_axis_prod's column reduction over [axis, inner]
 // (outer = 1): nsplit chunks of `chunk` rows, row_threads rows interleaved
-// per chunk.  False when it does not split on the float4 path.
+// per chunk.  False when it does not split on the float4 path or walks
+// contiguous runs of rows instead.
 bool col_prod_split(size_t axis, size_t inner, uint32_t* nsplit, size_t* chunk, int* row_threads);
 // out[c] = the sum of partial[c * nsplit ..], as that reduction combines them.
 void col_combine_sum(const float* partial, float* out, size_t cols, uint32_t nsplit, size_t axis, hipStream_t s);
