@@ -171,6 +171,11 @@ int64_t malus_std_attn_fwd(int64_t q, int64_t k, int64_t v, int64_t scale, int64
  * product's VJP for q) from the same kernel into *dq_out (if non-null). */
 int64_t malus_std_attn_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, int64_t k, int32_t causal,
                            int64_t* dq_out);
+/* The whole attention VJP from one kernel: returns ds as malus_std_attn_bwd,
+ * with dq = ds @ k, dk = ds^T @ q and dv = p^T @ dout [bh, t, hs] into
+ * *dq_out, *dk_out, *dv_out (all required). */
+int64_t malus_std_attn_bwd_all(int64_t dout, int64_t q, int64_t k, int64_t v, int64_t p, int64_t scale,
+                               int32_t causal, int64_t* dq_out, int64_t* dk_out, int64_t* dv_out);
 int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
 int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
 void malus_set_abort_on_error(int on);

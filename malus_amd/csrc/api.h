@@ -69,6 +69,9 @@ int64_t ln_affine_bwd_xw(int64_t y, int64_t var, int64_t w, int64_t dout, const 
 int64_t attn_fwd_impl(int64_t q, int64_t k, int64_t v, int64_t scale, size_t B, size_t T, size_t H, int64_t* p_out);
 int64_t attn_bwd_impl(int64_t datt, int64_t v, int64_t p, int64_t scale, int64_t k, const malus::TensorBuffer* D, int64_t* dq,
                       size_t B, size_t T, size_t H);
+void attn_bwd_all_impl(int64_t datt, int64_t q, int64_t k, int64_t v, int64_t p, int64_t scale,
+                       const malus::TensorBuffer* Dq, const malus::TensorBuffer* Dk, const malus::TensorBuffer* Dv,
+                       int64_t* dq, int64_t* dk, int64_t* dv, size_t B, size_t T, size_t H);
 int64_t scores_bwd_q(int64_t ds, int64_t k, const malus::TensorBuffer* D, bool causal);
 int64_t scores_bwd_k(int64_t ds, int64_t q, const malus::TensorBuffer* D, bool causal);
 

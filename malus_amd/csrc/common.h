@@ -159,8 +159,19 @@ bool attn_fwd(const float* Q, const float* K, const float* V, const float* scale
 // attn_scores_bwd, and with dQ non-null also dQ = Dq + dS @ K (K, dQ, Dq
 // dense [bh, t, hs]; Dq may be null) from the same kernel.  Same values as
 // gemm(dS, K) with the addend.
+// With kv non-null (needs dQ) the same kernel also forms, per head,
+// dK = Dk + dS^T @ Q and dV = Dv + P^T @ dO (Q, dK, dV, Dk, Dv dense
+// [bh, t, hs]; the addends may be null): the same values as the two GEMMs.
+struct AttnKV {
+  const float* Q;
+  float* dK;
+  const float* Dk;
+  float* dV;
+  const float* Dv;
+};
 bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const float* P, const float* scale, float* dS,
-              const float* K, float* dQ, const float* Dq, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s);
+              const float* K, float* dQ, const float* Dq, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s,
+              const AttnKV* kv = nullptr);
 // Sum over the axis of x * y (y has x's layout); each product rounded to f32.
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 // The split of reduce_axis_prod's column reduction over [axis, inner]

@@ -116,6 +116,78 @@ __device__ __forceinline__ void product_from_registers(const v16f (&a)[NT], int 
     }
 }
 
+// Stage one head's [TT, HS] rows that sit ld floats apart (the [B*T, C]
+// layout read in place) in LDS with padded rows, as stage_head does.
+template <int TT, int HS>
+__device__ __forceinline__ void stage_rows(const float* __restrict__ src_head, int ld, float* S) {
+  constexpr int LD = HS + 4, N4 = TT * HS / 4, PER = (N4 + 255) / 256;
+  v4f tmp[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int f = threadIdx.x + 256 * u;
+    if (f < N4) tmp[u] = *reinterpret_cast<const v4f*>(src_head + (size_t)(f / (HS / 4)) * ld + 4 * (f % (HS / 4)));
+  }
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int f = threadIdx.x + 256 * u;
+    if (f < N4) *reinterpret_cast<v4f*>(S + (f / (HS / 4)) * LD + 4 * (f % (HS / 4))) = tmp[u];
+  }
+}
+
+// out[32 j + i][d] (+ D) = sum over queries q of A[q][32 j + i] M[q][d]: the
+// product A^T M for key tile j, A a head's [TT, TT] matrix in global memory
+// (P or dS) and M [TT, HS] staged in LDS (padded rows).  The queries run in
+// 16-deep slabs in ascending order and MFMA step s of a slab pairs queries
+// k0 + s (lane half 0) and k0 + 8 + s (lane half 1), exactly as the GEMM's
+// fragments of a transposed A operand do, so the values are the GEMM's.
+// Causal: the slabs before query 32 j are skipped; there A holds +0 or -0
+// (P = 0 above the diagonal), and the GEMM either skips them too or adds
+// those zero products to a +0 accumulator.  A's slab pairs are loaded one
+// pair ahead of their MFMAs.  out/D rows are HS floats apart.
+template <int TT, int HS, bool CAUSAL>
+__device__ __forceinline__ void transposed_product(const float* __restrict__ Ah, int j, const float* Ms,
+                                                   float* __restrict__ out, const float* __restrict__ D) {
+  constexpr int LD = HS + 4, NN = HS / 32, NSL = TT / 16;
+  const int lane = threadIdx.x & 63, x = lane & 31, lk = lane >> 5;
+  const int s0 = CAUSAL ? 2 * j : 0;  // a key tile spans two slabs, so the slab count is even
+  const float* ap = Ah + 32 * j + x + (size_t)(8 * lk) * TT;
+  auto load = [&](int sl, float (&r)[16]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int s = 0; s < 8; ++s) r[8 * u + s] = ap[(size_t)(16 * (sl + u) + s) * TT];
+  };
+  v16f o[NN];
+#pragma unroll
+  for (int n = 0; n < NN; ++n) o[n] = v16f{0};
+  float a[16], nx[16];
+  load(s0, a);
+  for (int sl = s0; sl < NSL; sl += 2) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) nx[e] = 0.0f;
+    if (sl + 2 < NSL) load(sl + 2, nx);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float* mr = Ms + (16 * (sl + u) + 8 * lk + s) * LD + x;
+#pragma unroll
+        for (int n = 0; n < NN; ++n) o[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[8 * u + s], mr[32 * n], o[n], 0, 0, 0);
+      }
+    __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) a[e] = nx[e];
+  }
+#pragma unroll
+  for (int n = 0; n < NN; ++n)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const size_t off = (size_t)(32 * j + 8 * (r >> 2) + 4 * lk + (r & 3)) * HS + 32 * n + x;
+      out[off] = D ? D[off] + o[n][r] : o[n][r];
+    }
+}
+
 // Query tiles are dealt to the waves in pairs (p, NT-1-p): wave w runs both
 // tiles of pair w, one after the other, so every wave has NT + 1 key tiles
 // of unmasked work under a causal mask and the workgroup (one head) is
@@ -407,12 +479,16 @@ __device__ __forceinline__ void dscores_tile(const float* __restrict__ dOh, int 
 // composed ops give +-0 there) and neither dP nor P is read for them.
 // dO of head bh, row i, column d sits at dO + (bh / H) * T * ldo + (bh % H) * HS + i * ldo + d
 // (ldo = H * HS: the [B*T, C] attention output read in place).
-template <int TT, int HS, bool CAUSAL, bool DQ>
+// KV: then also dV = P^T dO (dO staged in LDS) and dK = dS^T Q (Q staged),
+// each wave taking the key tiles of its pair (the same balance as the query
+// tiles: under a causal mask key tile j meets the NT - j query tiles from j
+// on).  The dS rows other waves stored are read back after a barrier.
+template <int TT, int HS, bool CAUSAL, bool DQ, bool KV>
 __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ dO, int ldo, int H,
                                                     const float* __restrict__ V, const float* __restrict__ P,
                                                     const float* __restrict__ scale, float* __restrict__ dS,
                                                     const float* __restrict__ Kh, float* __restrict__ dQ,
-                                                    const float* __restrict__ Dq) {
+                                                    const float* __restrict__ Dq, AttnKV kv) {
   constexpr int NT = TT / 32;
   constexpr int LD = HS + 4;
   static_assert(NT % 2 == 0 && NT <= 8, "one pair of query tiles per wave");
@@ -444,18 +520,40 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ d
       product_from_registers<NT, HS>(acc, CAUSAL ? qa + 1 : NT, S, 32 * qa, dQ + head, Dh, HS);
     }
   }
+  if constexpr (KV) {
+    __syncthreads();  // every wave is done with K and has stored its dS rows
+    stage_rows<TT, HS>(dOh, ldo, S);
+    __syncthreads();
+    if (active) {
+      const float* Dv = kv.Dv ? kv.Dv + head : nullptr;
+      transposed_product<TT, HS, CAUSAL>(Ph, qa, S, kv.dV + head, Dv);
+      transposed_product<TT, HS, CAUSAL>(Ph, qb, S, kv.dV + head, Dv);
+    }
+    __syncthreads();  // every wave is done with dO
+    stage_head<TT, HS>(kv.Q + head, S);
+    __syncthreads();
+    if (active) {
+      const float* Dk = kv.Dk ? kv.Dk + head : nullptr;
+      transposed_product<TT, HS, CAUSAL>(dSh, qa, S, kv.dK + head, Dk);
+      transposed_product<TT, HS, CAUSAL>(dSh, qb, S, kv.dK + head, Dk);
+    }
+  }
 }
 
 template <int TT, int HS>
 void launch_bwd(const float* dO, int ldo, int H, const float* V, const float* P, const float* scale, float* dS,
-                const float* K, float* dQ, const float* Dq, int bh, bool causal, hipStream_t s) {
+                const float* K, float* dQ, const float* Dq, int bh, bool causal, const AttnKV* kv, hipStream_t s) {
   const dim3 grid(1, (unsigned)bh);  // one workgroup per head
-  if (dQ) {
-    if (causal) k_attn_bwd<TT, HS, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq);
-    else k_attn_bwd<TT, HS, false, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq);
+  const AttnKV a = kv ? *kv : AttnKV{};
+  if (kv) {
+    if (causal) k_attn_bwd<TT, HS, true, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
+    else k_attn_bwd<TT, HS, false, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
+  } else if (dQ) {
+    if (causal) k_attn_bwd<TT, HS, true, true, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
+    else k_attn_bwd<TT, HS, false, true, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
   } else {
-    if (causal) k_attn_bwd<TT, HS, true, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq);
-    else k_attn_bwd<TT, HS, false, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq);
+    if (causal) k_attn_bwd<TT, HS, true, false, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
+    else k_attn_bwd<TT, HS, false, false, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
   }
 }
 
@@ -488,16 +586,18 @@ bool attn_scores_softmax(const float* Q, const float* K, const float* scale, con
 }
 
 bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const float* P, const float* scale, float* dS,
-              const float* K, float* dQ, const float* Dq, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s) {
+              const float* K, float* dQ, const float* Dq, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s,
+              const AttnKV* kv) {
   if (!attn_scores_supported(bh, t, hs) || heads == 0 || bh % heads || ldo < hs * heads) return false;
   const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!aligned(dO) || !aligned(V) || !aligned(P) || !aligned(dS) || ldo % 4) return false;
   if (dQ && !K) return false;
+  if (kv && (!dQ || !kv->Q || !kv->dK || !kv->dV || !aligned(kv->Q))) return false;
   const int b = (int)bh, l = (int)ldo, H = (int)heads;
-  if (t == 256 && hs == 64) launch_bwd<256, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, s);
-  else if (t == 128 && hs == 64) launch_bwd<128, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, s);
-  else if (t == 64 && hs == 32) launch_bwd<64, 32>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, s);
-  else if (t == 64 && hs == 64) launch_bwd<64, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, s);
+  if (t == 256 && hs == 64) launch_bwd<256, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);
+  else if (t == 128 && hs == 64) launch_bwd<128, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);
+  else if (t == 64 && hs == 32) launch_bwd<64, 32>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);
+  else if (t == 64 && hs == 64) launch_bwd<64, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);
   else return false;
   MALUS_HIP(hipGetLastError());
   return true;

@@ -696,6 +696,35 @@ int64_t malus_std_attn_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, in
   return malus::H(out);
   API_CATCH(0)
 }
+int64_t malus_std_attn_bwd_all(int64_t dout, int64_t q, int64_t kk, int64_t v, int64_t p, int64_t scale, int32_t causal,
+                               int64_t* dq_out, int64_t* dk_out, int64_t* dv_out) {
+  API_TRY
+  TensorBuffer *d = T(dout), *Q = T(q), *K = T(kk), *V = T(v), *Pt = T(p), *sc = T(scale);
+  auto same3 = [&](const TensorBuffer* x) {
+    return x->ndim == 3 && x->shape[0] == d->shape[0] && x->shape[1] == d->shape[1] && x->shape[2] == d->shape[2];
+  };
+  if (d->ndim != 3 || !same3(Q) || !same3(K) || !same3(V) || Pt->ndim != 3 || Pt->shape[0] != d->shape[0] ||
+      Pt->shape[1] != d->shape[1] || Pt->shape[2] != d->shape[1] || sc->len != 1 || !dq_out || !dk_out || !dv_out)
+    fail("malus: attn_bwd_all shape mismatch: dout %s, q %s, k %s, v %s, p %s, scale %s", shape_str(d).c_str(),
+         shape_str(Q).c_str(), shape_str(K).c_str(), shape_str(V).c_str(), shape_str(Pt).c_str(),
+         shape_str(sc).c_str());
+  const size_t bh = d->shape[0], t = d->shape[1], hs = d->shape[2];
+  if (!k::attn_scores_supported(bh, t, hs)) fail("malus: attn_bwd_all: no fused kernel for t=%zu hs=%zu", t, hs);
+  const size_t shape[3] = {bh, t, t};
+  TensorBuffer* out = alloc_tensor(F32, shape, 3);
+  TensorBuffer *dq = alloc_like(Q), *dk = alloc_like(K), *dv = alloc_like(V);
+  const k::AttnKV kv{Q->f32(), dk->f32(), nullptr, dv->f32(), nullptr};
+  if (!k::attn_bwd(d->f32(), hs, 1, V->f32(), Pt->f32(), sc->f32(), out->f32(), K->f32(), dq->f32(), nullptr, bh, t,
+                   hs, causal != 0, stream(), &kv))
+    fail("malus: attn_bwd_all: unaligned operand");
+  const uint64_t seq = enqueue_mark("attn_bwd_all");
+  for (TensorBuffer* x : {out, dq, dk, dv}) x->write_seq = seq;
+  *dq_out = malus::H(dq);
+  *dk_out = malus::H(dk);
+  *dv_out = malus::H(dv);
+  return malus::H(out);
+  API_CATCH(0)
+}
 int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout) {
   API_TRY
   TensorBuffer *w = T(weight), *idx = T(indices), *d = T(dout);
@@ -1109,6 +1138,28 @@ int64_t attn_bwd_impl(int64_t hda, int64_t hv, int64_t hp, int64_t hscale, int64
   q->write_seq = seq;
   *dq = malus::H(q);
   return malus::H(out);
+}
+// The whole attention VJP from one kernel: dS (scratch), dQ = Dq + dS @ K,
+// dK = Dk + dS^T @ Q and dV = Dv + P^T @ dAtt, with dAtt [B*T, H*hs] read in
+// place and Q, K, V, dQ, dK, dV [B*H, T, hs].
+void attn_bwd_all_impl(int64_t hda, int64_t hq, int64_t hk, int64_t hv, int64_t hp, int64_t hscale,
+                       const TensorBuffer* Dq, const TensorBuffer* Dk, const TensorBuffer* Dv, int64_t* dq, int64_t* dk,
+                       int64_t* dv, size_t B, size_t T, size_t H) {
+  TensorBuffer *da = T_(hda), *q = T_(hq), *kk = T_(hk), *v = T_(hv), *p = T_(hp), *sc = T_(hscale);
+  const size_t hs = v->shape[2], bh = B * H;
+  size_t bucket;
+  float* ds = static_cast<float*>(pool_alloc(bh * T * T * sizeof(float), &bucket));
+  TensorBuffer *oq = alloc_like(q), *ok = alloc_like(kk), *ov = alloc_like(v);
+  const k::AttnKV kv{q->f32(), ok->f32(), Dk ? Dk->f32() : nullptr, ov->f32(), Dv ? Dv->f32() : nullptr};
+  if (!k::attn_bwd(da->f32(), H * hs, H, v->f32(), p->f32(), sc->f32(), ds, kk->f32(), oq->f32(),
+                   Dq ? Dq->f32() : nullptr, bh, T, hs, true, stream(), &kv))
+    fail("malus: attn_bwd_all: no fused kernel for t=%zu hs=%zu", T, hs);
+  pool_free(ds, bucket);  // stream order: later users of the buffer run after the kernel
+  const uint64_t seq = enqueue_mark("attn_bwd_all");
+  for (TensorBuffer* x : {oq, ok, ov}) x->write_seq = seq;
+  *dq = malus::H(oq);
+  *dk = malus::H(ok);
+  *dv = malus::H(ov);
 }
 // Scores S = Q @ K^T (the permute(K, 0, 2, 1) operand read in place): dQ = dS @ K, dK = dS^T @ Q  (+ D)
 int64_t scores_bwd_q(int64_t hds, int64_t hk, const TensorBuffer* D, bool causal) {

@@ -507,6 +507,26 @@ void backward(int64_t loss) {
         const int64_t q = n.saved[0], kk = n.saved[1], v = n.saved[2], pr = n.saved[3], sc = n.saved[4];
         const size_t Bm = (size_t)n.meta[0], Tm = (size_t)n.meta[1], Hm = (size_t)n.meta[2];
         for (int64_t h : n.saved) need_values(h);
+        if (na && nb && nc && q != kk && q != v && kk != v && slot_is(GradAcc, &malus_std_broadcast_add_fwd)) {
+          // all four products from one kernel; each gradient folds into its
+          // own entry, in the order below (dV, dQ, dK)
+          auto old = [&](int64_t x) -> const TensorBuffer* {
+            auto f = grads.find(x);
+            return f == grads.end() ? nullptr : T(f->second);
+          };
+          int64_t dq = 0, dk = 0, dv = 0;
+          attn_bwd_all_impl(dout, q, kk, v, pr, sc, old(q), old(kk), old(v), &dq, &dk, &dv, Bm, Tm, Hm);
+          for (auto [x, g] : {std::pair{v, dv}, std::pair{q, dq}, std::pair{kk, dk}}) {
+            auto f = grads.find(x);
+            if (f == grads.end()) {
+              grads.emplace(x, g);
+            } else {
+              release(T(f->second));
+              f->second = g;
+            }
+          }
+          break;
+        }
         // AttnOut's VJP (dP, dV), the softmax and scale VJPs, then Scores' (dQ, dK)
         if (nc) fold_grad(grads, v, [&](const TensorBuffer* o) { return attn_out_bwd_v(pr, dout, Bm, Tm, Hm, o, true); });
         if (na || nb) {

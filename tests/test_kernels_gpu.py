@@ -280,6 +280,36 @@ def test_attn_bwd_dq_equals_composed_ops(rt, t, hs, causal):
     rt.free(hq, hk, hv, hd, hsc, hm, hp, hds2)
 
 
+@pytest.mark.parametrize("t,hs,causal", [(256, 64, 1), (256, 64, 0), (128, 64, 1), (64, 32, 1), (64, 64, 0)])
+def test_attn_bwd_all_equals_composed_ops(rt, t, hs, causal):
+    # The whole attention VJP from one kernel: dS and dQ as the kernel
+    # without the key-side products, dK = dS^T @ Q and dV = P^T @ dO as the
+    # batched matmuls of the transposed operands (every output bit-exact)
+    bh = 5
+    q, kk, v = (rand(bh, t, hs, lo=-2, hi=2) for _ in range(3))
+    d = rand(bh, t, hs)
+    mask = O.causal_mask(t) if causal else rand(t, t, lo=-3, hi=3)
+    sc = np.array([[1.0 / np.sqrt(hs)]], np.float32)
+    hq, hk, hv, hd, hsc, hm = (rt.tensor(a) for a in (q, kk, v, d, sc, mask))
+    hp = rt.L.malus_std_attn_scores_softmax(hq, hk, hsc, hm, causal)
+    hdq, hdk, hdv = C.c_int64(), C.c_int64(), C.c_int64()
+    ds = run(rt, rt.L.malus_std_attn_bwd_all(hd, hq, hk, hv, hp, hsc, causal, C.byref(hdq), C.byref(hdk), C.byref(hdv)))
+    dq, dk, dv = (run(rt, h.value) for h in (hdq, hdk, hdv))
+    hdq2 = C.c_int64()
+    hds2 = rt.L.malus_std_attn_bwd(hd, hv, hp, hsc, hk, causal, C.byref(hdq2))
+    tag = f"t={t} hs={hs} causal={causal}"
+    assert_bitexact(ds, rt.numpy(hds2), f"attn_bwd_all dS {tag}")
+    assert_bitexact(dq, run(rt, hdq2.value), f"attn_bwd_all dQ {tag}")
+    hdst = rt.L.tensor_permute(hds2, M.sizes([0, 2, 1]), 3)
+    hpt = rt.L.tensor_permute(hp, M.sizes([0, 2, 1]), 3)
+    assert_bitexact(dk, run(rt, rt.L.tensor_matmul(hdst, hq)), f"attn_bwd_all dK {tag}")
+    assert_bitexact(dv, run(rt, rt.L.tensor_matmul(hpt, hd)), f"attn_bwd_all dV {tag}")
+    p = rt.numpy(hp)
+    assert_normwise(dk, O.matmul(np.ascontiguousarray(ds.transpose(0, 2, 1)), q), 1e-5, "dK vs oracle matmul")
+    assert_normwise(dv, O.matmul(np.ascontiguousarray(p.transpose(0, 2, 1)), d), 1e-5, "dV vs oracle matmul")
+    rt.free(hq, hk, hv, hd, hsc, hm, hp, hds2, hdst, hpt)
+
+
 def test_attn_scores_softmax_rejects_unbuilt_shapes(rt):
     hq = rt.tensor(rand(2, 48, 16))
     hsc, hm = rt.tensor(np.ones((1, 1), np.float32)), rt.tensor(O.causal_mask(48))
