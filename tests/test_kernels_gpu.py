@@ -280,12 +280,13 @@ def test_attn_bwd_dq_equals_composed_ops(rt, t, hs, causal):
     rt.free(hq, hk, hv, hd, hsc, hm, hp, hds2)
 
 
-@pytest.mark.parametrize("t,hs,causal", [(256, 64, 1), (256, 64, 0), (128, 64, 1), (64, 32, 1), (64, 64, 0)])
-def test_attn_bwd_all_equals_composed_ops(rt, t, hs, causal):
+@pytest.mark.parametrize("t,hs,causal,bh", [(256, 64, 1, 5), (256, 64, 0, 5), (128, 64, 1, 5), (64, 32, 1, 5),
+                                             (64, 64, 0, 5), (256, 64, 1, 300), (64, 32, 0, 600)])
+def test_attn_bwd_all_equals_composed_ops(rt, t, hs, causal, bh):
     # The whole attention VJP from one kernel: dS and dQ as the kernel
     # without the key-side products, dK = dS^T @ Q and dV = P^T @ dO as the
-    # batched matmuls of the transposed operands (every output bit-exact)
-    bh = 5
+    # batched matmuls of the transposed operands (every output bit-exact).
+    # Up to 600 heads: more workgroups than CUs.
     q, kk, v = (rand(bh, t, hs, lo=-2, hi=2) for _ in range(3))
     d = rand(bh, t, hs)
     mask = O.causal_mask(t) if causal else rand(t, t, lo=-3, hi=3)
