@@ -43,11 +43,11 @@ def gemm_flops_per_step(cfg) -> float:
 def gemm_bytes_per_step(cfg) -> float:
     """Algorithmic HBM bytes of the step's GEMM launches (the k_sgemm class):
     each launch reads both operands and its epilogue operand once and writes
-    its outputs once (4 bytes per element).  Q K^T, P @ V, the dP = dO V^T VJP and dQ = dS K run inside
-    the fused attention kernels, so the attention GEMMs here are the two key
-    side VJPs, dV = P^T dO and dK = dS^T Q."""
+    its outputs once (4 bytes per element).  Every attention product (Q K^T,
+    P @ V, dP = dO V^T, dQ = dS K, dK = dS^T Q and dV = P^T dO) runs inside
+    the fused attention kernels, so none is counted here."""
     B, T, Cn, H, L, V = cfg["B"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["V"]
-    N, hs, F, BH = B * T, Cn // H, 4 * cfg["C"], B * H
+    N, F = B * T, 4 * cfg["C"]
 
     def one(m, n, k, batch=1):  # one GEMM launch
         return 4.0 * batch * (m * k + k * n + m * n)
@@ -55,11 +55,10 @@ def gemm_bytes_per_step(cfg) -> float:
     def mm(m, n, k, batch=1):  # a forward GEMM and its two VJP GEMMs (dA: m x k, dB: k x n)
         return 3 * one(m, n, k, batch)
 
-    attn = 2 * one(T, hs, T, BH)
     # epilogue operands: the GELU epilogue writes gelu(h) beside h and the
     # GELU VJP epilogue reads h; the two residual adds read their addend
     epi = 4.0 * (2 * N * F + 2 * N * Cn)
-    layer = 4 * mm(N, Cn, Cn) + mm(N, F, Cn) + mm(N, Cn, F) + attn + epi
+    layer = 4 * mm(N, Cn, Cn) + mm(N, F, Cn) + mm(N, Cn, F) + epi
     return L * layer + mm(N, V, Cn)
 
 
