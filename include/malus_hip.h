@@ -172,10 +172,12 @@ int64_t malus_std_attn_fwd(int64_t q, int64_t k, int64_t v, int64_t scale, int64
 int64_t malus_std_attn_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, int64_t k, int32_t causal,
                            int64_t* dq_out);
 /* The whole attention VJP from one kernel: returns ds as malus_std_attn_bwd,
- * with dq = ds @ k, dk = ds^T @ q and dv = p^T @ dout [bh, t, hs] into
- * *dq_out, *dk_out, *dv_out (all required). */
+ * with dq = dq_add + ds @ k, dk = dk_add + ds^T @ q and dv = dv_add + p^T @ dout
+ * [bh, t, hs] into *dq_out, *dk_out, *dv_out (all required); an addend handle
+ * of 0 adds nothing (the gradient accumulation the tape folds in). */
 int64_t malus_std_attn_bwd_all(int64_t dout, int64_t q, int64_t k, int64_t v, int64_t p, int64_t scale,
-                               int32_t causal, int64_t* dq_out, int64_t* dk_out, int64_t* dv_out);
+                               int32_t causal, int64_t dq_add, int64_t dk_add, int64_t dv_add, int64_t* dq_out,
+                               int64_t* dk_out, int64_t* dv_out);
 int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
 int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
 void malus_set_abort_on_error(int on);

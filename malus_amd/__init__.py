@@ -117,7 +117,8 @@ SIGNATURES = {
     "malus_std_attn_scores_bwd": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "malus_std_attn_fwd": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32, _P(_i64)]),
     "malus_std_attn_bwd": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32, _P(_i64)]),
-    "malus_std_attn_bwd_all": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i32, _P(_i64), _P(_i64), _P(_i64)]),
+    "malus_std_attn_bwd_all": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _P(_i64), _P(_i64),
+                                      _P(_i64)]),
     "malus_ktimer_collect": (_i64, [C.c_char_p, _P(C.c_double), _P(C.c_double)]),
     "malus_device_info": (C.c_int, [C.c_char_p, _sz, _P(C.c_int), _P(C.c_int)]),
     "malus_set_abort_on_error": (None, [C.c_int]),

@@ -697,14 +697,17 @@ int64_t malus_std_attn_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, in
   API_CATCH(0)
 }
 int64_t malus_std_attn_bwd_all(int64_t dout, int64_t q, int64_t kk, int64_t v, int64_t p, int64_t scale, int32_t causal,
-                               int64_t* dq_out, int64_t* dk_out, int64_t* dv_out) {
+                               int64_t dq_add, int64_t dk_add, int64_t dv_add, int64_t* dq_out, int64_t* dk_out,
+                               int64_t* dv_out) {
   API_TRY
   TensorBuffer *d = T(dout), *Q = T(q), *K = T(kk), *V = T(v), *Pt = T(p), *sc = T(scale);
+  TensorBuffer *Aq = dq_add ? T(dq_add) : nullptr, *Ak = dk_add ? T(dk_add) : nullptr, *Av = dv_add ? T(dv_add) : nullptr;
   auto same3 = [&](const TensorBuffer* x) {
     return x->ndim == 3 && x->shape[0] == d->shape[0] && x->shape[1] == d->shape[1] && x->shape[2] == d->shape[2];
   };
   if (d->ndim != 3 || !same3(Q) || !same3(K) || !same3(V) || Pt->ndim != 3 || Pt->shape[0] != d->shape[0] ||
-      Pt->shape[1] != d->shape[1] || Pt->shape[2] != d->shape[1] || sc->len != 1 || !dq_out || !dk_out || !dv_out)
+      Pt->shape[1] != d->shape[1] || Pt->shape[2] != d->shape[1] || sc->len != 1 || !dq_out || !dk_out || !dv_out ||
+      (Aq && !same3(Aq)) || (Ak && !same3(Ak)) || (Av && !same3(Av)))
     fail("malus: attn_bwd_all shape mismatch: dout %s, q %s, k %s, v %s, p %s, scale %s", shape_str(d).c_str(),
          shape_str(Q).c_str(), shape_str(K).c_str(), shape_str(V).c_str(), shape_str(Pt).c_str(),
          shape_str(sc).c_str());
@@ -713,9 +716,9 @@ int64_t malus_std_attn_bwd_all(int64_t dout, int64_t q, int64_t kk, int64_t v, i
   const size_t shape[3] = {bh, t, t};
   TensorBuffer* out = alloc_tensor(F32, shape, 3);
   TensorBuffer *dq = alloc_like(Q), *dk = alloc_like(K), *dv = alloc_like(V);
-  const k::AttnKV kv{Q->f32(), dk->f32(), nullptr, dv->f32(), nullptr};
-  if (!k::attn_bwd(d->f32(), hs, 1, V->f32(), Pt->f32(), sc->f32(), out->f32(), K->f32(), dq->f32(), nullptr, bh, t,
-                   hs, causal != 0, stream(), &kv))
+  const k::AttnKV kv{Q->f32(), dk->f32(), Ak ? Ak->f32() : nullptr, dv->f32(), Av ? Av->f32() : nullptr};
+  if (!k::attn_bwd(d->f32(), hs, 1, V->f32(), Pt->f32(), sc->f32(), out->f32(), K->f32(), dq->f32(),
+                   Aq ? Aq->f32() : nullptr, bh, t, hs, causal != 0, stream(), &kv))
     fail("malus: attn_bwd_all: unaligned operand");
   const uint64_t seq = enqueue_mark("attn_bwd_all");
   for (TensorBuffer* x : {out, dq, dk, dv}) x->write_seq = seq;

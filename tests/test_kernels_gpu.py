@@ -294,8 +294,18 @@ def test_attn_bwd_all_equals_composed_ops(rt, t, hs, causal, bh):
     hq, hk, hv, hd, hsc, hm = (rt.tensor(a) for a in (q, kk, v, d, sc, mask))
     hp = rt.L.malus_std_attn_scores_softmax(hq, hk, hsc, hm, causal)
     hdq, hdk, hdv = C.c_int64(), C.c_int64(), C.c_int64()
-    ds = run(rt, rt.L.malus_std_attn_bwd_all(hd, hq, hk, hv, hp, hsc, causal, C.byref(hdq), C.byref(hdk), C.byref(hdv)))
+    ds = run(rt, rt.L.malus_std_attn_bwd_all(hd, hq, hk, hv, hp, hsc, causal, 0, 0, 0, C.byref(hdq), C.byref(hdk),
+                                             C.byref(hdv)))
     dq, dk, dv = (run(rt, h.value) for h in (hdq, hdk, hdv))
+    # with addends (an existing gradient of each input): each output is the
+    # f32 sum of the addend and the product
+    adds = [rand(bh, t, hs) for _ in range(3)]
+    ha = [rt.tensor(a) for a in adds]
+    run(rt, rt.L.malus_std_attn_bwd_all(hd, hq, hk, hv, hp, hsc, causal, ha[0], ha[1], ha[2], C.byref(hdq),
+                                        C.byref(hdk), C.byref(hdv)))
+    for name, h, a, base in zip("QKV", (hdq, hdk, hdv), adds, (dq, dk, dv)):
+        assert_bitexact(run(rt, h.value), a + base, f"attn_bwd_all d{name} with addend")
+    rt.free(*ha)
     hdq2 = C.c_int64()
     hds2 = rt.L.malus_std_attn_bwd(hd, hv, hp, hsc, hk, causal, C.byref(hdq2))
     tag = f"t={t} hs={hs} causal={causal}"
