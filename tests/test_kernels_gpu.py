@@ -43,7 +43,8 @@ def test_broadcast_binop(rt, op, shapes):
 
 
 @pytest.mark.parametrize("big,small", [((64, 384), (384,)), ((64, 384), (1, 384)), ((6, 40, 52), (1, 1)),
-                                       ((3, 5, 7), (5, 1)), ((4, 8, 16), (1, 8, 1)), ((1, 5), (5,)), ((33, 70001), (1, 1))])
+                                       ((3, 5, 7), (5, 1)), ((4, 8, 16), (1, 8, 1)), ((1, 5), (5,)), ((33, 70001), (1, 1)),
+                                       ((5000, 8192), (1, 8192))])
 def test_mul_vjp_fused_reduction_matches_materialized(rt, big, small):
     """The broadcast-multiply VJP reduces dout * a without materializing the
     product; it must equal broadcast_mul then sum_to_shape bit for bit, and
@@ -128,6 +129,9 @@ def test_unary_vjp_bitexact(rt, fn, op):
 @pytest.mark.parametrize("shape,axis", [((65, 1024), 1), ((65, 1024), 0), ((3, 70001), 1), ((70001, 3), 0),
                                         ((4, 5, 6), 1), ((4, 5, 6), 2), ((4, 5, 6), 0), ((2, 300, 50), -2), ((4096, 384), 0),
                                         ((3, 999, 40), 1),
+                                        # wide rows: the column reduction's contiguous row runs (split into
+                                        # chunks with a short last one, and unsplit over many columns)
+                                        ((5000, 8192), 0), ((2, 9000, 4096), 1), ((40, 160, 8192), 1),
                                         ((1, 1), 0), ((17,), 0)])
 @pytest.mark.parametrize("op", [M.R_SUM, M.R_MEAN, M.R_MAX, M.R_VAR])
 def test_reduce_axis(rt, shape, axis, op):
