@@ -174,7 +174,9 @@ int64_t malus_std_attn_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, in
 /* The whole attention VJP from one kernel: returns ds as malus_std_attn_bwd,
  * with dq = dq_add + ds @ k, dk = dk_add + ds^T @ q and dv = dv_add + p^T @ dout
  * [bh, t, hs] into *dq_out, *dk_out, *dv_out (all required); an addend handle
- * of 0 adds nothing (the gradient accumulation the tape folds in). */
+ * of 0 adds nothing (the gradient accumulation the tape folds in).  These are
+ * the matmul VJPs (tape.rs:460-469) of the two products of the composed
+ * attention (nanogpt_modular.ml:57-62). */
 int64_t malus_std_attn_bwd_all(int64_t dout, int64_t q, int64_t k, int64_t v, int64_t p, int64_t scale,
                                int32_t causal, int64_t dq_add, int64_t dk_add, int64_t dv_add, int64_t* dq_out,
                                int64_t* dk_out, int64_t* dv_out);
