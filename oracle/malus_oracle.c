@@ -385,21 +385,6 @@ void or_sum_to_shape(const float* g, const size_t* gsh, int gnd, const size_t* t
     }
 }
 
-void or_broadcast_to_shape(const float* x, const size_t* xsh, int xnd, const size_t* osh, int ond, float* out) {
-    /* broadcast_to_shape, metal.rs:1779-1806 */
-    size_t padded[8];
-    for (int i = 0; i < ond - xnd; ++i) padded[i] = 1;
-    for (int i = 0; i < xnd; ++i) padded[ond - xnd + i] = xsh[i];
-    size_t total = prod(osh, ond);
-    for (size_t flat = 0; flat < total; ++flat) {
-        size_t rem = flat, idx[8];
-        for (int d = ond - 1; d >= 0; --d) { idx[d] = rem % osh[d]; rem /= osh[d]; }
-        size_t f = 0;
-        for (int d = 0; d < ond; ++d) f = f * padded[d] + (idx[d] % padded[d]);
-        out[flat] = x[f];
-    }
-}
-
 /* Unary VJPs, tape.rs:1041-1083.  x_or_y is the forward output for
  * sigmoid/tanh/exp/sqrt and the forward input for relu/log/abs/gelu. */
 void or_unary_bwd(int op, const float* xy, const float* dout, size_t n, float* out) {

@@ -59,7 +59,6 @@ void or_matmul(const float* a, const size_t* ash, int and_, const float* b, cons
 
 /* ---- VJPs (tape.rs:971-1260) -------------------------------------------- */
 void or_sum_to_shape(const float* g, const size_t* gsh, int gnd, const size_t* tsh, int tnd, float* out);
-void or_broadcast_to_shape(const float* x, const size_t* xsh, int xnd, const size_t* osh, int ond, float* out);
 void or_unary_bwd(int op, const float* x_or_y, const float* dout, size_t n, float* out);
 void or_softmax_bwd(const float* s, const float* dout, const size_t* shape, int ndim, int axis, float* out);
 void or_layernorm_bwd(const float* y, const float* var, const float* dout, const size_t* shape, int ndim, int axis, float* out);

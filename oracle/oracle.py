@@ -57,7 +57,6 @@ def lib():
             "or_permute": (None, [_f, _szp, C.c_int, _szp, _f]),
             "or_matmul": (None, [_f, _szp, C.c_int, _f, _szp, C.c_int, _f]),
             "or_sum_to_shape": (None, [_f, _szp, C.c_int, _szp, C.c_int, _f]),
-            "or_broadcast_to_shape": (None, [_f, _szp, C.c_int, _szp, C.c_int, _f]),
             "or_unary_bwd": (None, [C.c_int, _f, _f, C.c_size_t, _f]),
             "or_softmax_bwd": (None, [_f, _f, _szp, C.c_int, C.c_int, _f]),
             "or_layernorm_bwd": (None, [_f, _f, _f, _szp, C.c_int, C.c_int, _f]),
