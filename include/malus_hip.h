@@ -41,6 +41,11 @@ void malus_init(void);
  * other sources are HIP C++ compiled with hipRTC (cached by source text). */
 void malus_runtime_init(const uint64_t* ids, const char* const* sources, size_t n);
 int malus_kernel_is_builtin(uint64_t id);
+/* No reference counterpart: compile HIP source for `arch` with the options
+ * malus_runtime_init uses for user kernels (no device needed).  Returns the
+ * code object size, 0 on failure (compiler log in `log`); copies the object
+ * into `code` when `cap` is large enough. */
+size_t malus_rtc_compile(const char* src, const char* arch, void* code, size_t cap, char* log, size_t log_cap);
 
 /* ---- tensor creation and lifetime (metal.rs:340-558) -------------------- */
 int64_t tensor_alloc_gpu(int32_t dtype, const size_t* shape, size_t ndim, const void* data); /* metal.rs:341-348 */

@@ -63,6 +63,7 @@ SIGNATURES = {
     "kernel_dispatch_v2": (_i64, [_u64, _P(_i64), _sz, _P(_sz), _P(_sz), _P(_sz), _sz, _i32, _vp, _sz]),
     "malus_runtime_init": (None, [_P(_u64), _P(C.c_char_p), _sz]),
     "malus_kernel_is_builtin": (C.c_int, [_u64]),
+    "malus_rtc_compile": (C.c_size_t, [C.c_char_p, C.c_char_p, C.c_void_p, C.c_size_t, C.c_char_p, C.c_size_t]),
     # buffers (buffer.rs)
     "malus_buffer_i32": (_i64, [_i64]),
     "malus_buffer_get_i32": (_i64, [_i64, _i64]),
@@ -143,6 +144,10 @@ SIGNATURES = {
     "malus_std_fill_like_fwd": (_i64, [_i64, _f32]),
     "malus_std_eq_fwd": (_i64, [_i64, _i64]),
     "malus_std_expand_axis_fwd": (_i64, [_i64, _i64, _i64]),
+    "malus_std_reduce_sum_axis_bwd": (_i64, [_i64, _i64, _i64]),
+    "malus_std_reduce_mean_axis_bwd": (_i64, [_i64, _i64, _i64]),
+    "malus_std_reduce_max_axis_bwd": (_i64, [_i64, _i64, _i64, _i64]),
+    "malus_std_reduce_var_axis_bwd": (_i64, [_i64, _i64, _i64]),
     "malus_std_sum_to_shape_bwd": (_i64, [_i64, _i64]),
     "malus_std_mul_bwd_a": (_i64, [_i64, _i64, _i64]),
     "malus_std_mul_bwd_b": (_i64, [_i64, _i64, _i64]),

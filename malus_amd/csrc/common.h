@@ -29,6 +29,9 @@ struct Storage {
   void* ptr = nullptr;
   size_t bytes = 0;              // bucketed allocation size
   std::atomic<int> aliases{0};   // TensorBuffers referencing this storage
+  // t > 0: holds attention probabilities [.., t, t] written by a causal
+  // attention forward (zero above the diagonal); reset by any host write.
+  uint32_t causal_t = 0;
 };
 
 // One tensor handle (metal.rs:280-296 TensorBuffer).  The i64 handle the ABI

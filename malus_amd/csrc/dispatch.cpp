@@ -110,28 +110,52 @@ std::string normalize(uint64_t id, const std::string& src) {
   return s;
 }
 
-hipModule_t compile_hiprtc(uint64_t id, const std::string& src) {
+// Options for every runtime-compiled kernel: the same code generation rules as
+// the library's own translation units (no FMA contraction, denormals kept, and
+// no packed-FP32 instruction selection).
+std::vector<std::string> rtc_options(const std::string& arch) {
+  return {"--offload-arch=" + arch, "-O3", "-std=c++17", "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+}
+
+// hipRTC: source -> code object for `arch`.  Needs no device.  On failure the
+// log goes to *log and an empty vector is returned.
+std::vector<char> rtc_compile(const std::string& src, const std::string& name, const std::string& arch,
+                              std::string* log) {
   hiprtcProgram prog;
-  std::string name = "malus_kernel_" + std::to_string(id) + ".hip";
-  if (hiprtcCreateProgram(&prog, src.c_str(), name.c_str(), 0, nullptr, nullptr) != HIPRTC_SUCCESS)
-    fail("malus: hiprtcCreateProgram failed for kernel %llu", (unsigned long long)id);
-  std::string arch = "--offload-arch=" + device_arch();
-  const char* opts[] = {arch.c_str(), "-O3", "-ffp-contract=off", "-std=c++17"};
-  hiprtcResult r = hiprtcCompileProgram(prog, 4, opts);
+  if (hiprtcCreateProgram(&prog, src.c_str(), name.c_str(), 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
+    if (log) *log = "hiprtcCreateProgram failed";
+    return {};
+  }
+  std::vector<std::string> opts = rtc_options(arch);
+  std::vector<const char*> argv;
+  for (const std::string& o : opts) argv.push_back(o.c_str());
+  hiprtcResult r = hiprtcCompileProgram(prog, (int)argv.size(), argv.data());
+  size_t log_size = 0;
+  hiprtcGetProgramLogSize(prog, &log_size);
+  std::string text(log_size, '\0');
+  if (log_size) hiprtcGetProgramLog(prog, &text[0]);
+  while (!text.empty() && text.back() == '\0') text.pop_back();
   if (r != HIPRTC_SUCCESS) {
-    size_t log_size = 0;
-    hiprtcGetProgramLogSize(prog, &log_size);
-    std::string log(log_size + 1, '\0');
-    hiprtcGetProgramLog(prog, &log[0]);
     hiprtcDestroyProgram(&prog);
-    fail("malus: HIP compilation failed for kernel %llu: %s\n%s", (unsigned long long)id, hiprtcGetErrorString(r),
-         log.c_str());
+    if (log) *log = std::string(hiprtcGetErrorString(r)) + "\n" + text;
+    return {};
   }
   size_t code_size = 0;
   hiprtcGetCodeSize(prog, &code_size);
   std::vector<char> code(code_size);
   hiprtcGetCode(prog, code.data());
   hiprtcDestroyProgram(&prog);
+  if (log) *log = text;
+  return code;
+}
+
+hipModule_t compile_hiprtc(uint64_t id, const std::string& src) {
+  std::string name = "malus_kernel_" + std::to_string(id) + ".hip";
+  std::string log;
+  std::vector<char> code = rtc_compile(src, name, device_arch(), &log);
+  if (code.empty())
+    fail("malus: HIP compilation failed for kernel %llu: %s", (unsigned long long)id, log.c_str());
   hipModule_t mod;
   MALUS_HIP(hipModuleLoadData(&mod, code.data()));
   return mod;
@@ -420,6 +444,21 @@ void malus_runtime_init(const uint64_t* ids, const char* const* sources, size_t 
     reg().by_id[ids[i]] = e;
   }
   API_CATCH()
+}
+
+// Compile HIP source for `arch` (e.g. "gfx950") with the options runtime_init
+// uses, without a device.  Returns the code object's size (0 on failure, with
+// the compiler log in `log`); the object is copied to `code` when cap allows.
+size_t malus_rtc_compile(const char* src, const char* arch, void* code, size_t cap, char* log, size_t log_cap) {
+  std::string text;
+  std::vector<char> obj = rtc_compile(src ? src : "", "malus_rtc.hip", arch ? arch : "gfx950", &text);
+  if (log && log_cap) {
+    size_t n = std::min(text.size(), log_cap - 1);
+    memcpy(log, text.data(), n);
+    log[n] = '\0';
+  }
+  if (code && cap >= obj.size()) memcpy(code, obj.data(), obj.size());
+  return obj.size();
 }
 
 int malus_kernel_is_builtin(uint64_t id) {

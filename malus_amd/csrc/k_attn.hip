@@ -569,7 +569,7 @@ bool attn_fwd(const float* Q, const float* K, const float* V, const float* scale
   if (!attn_scores_supported(bh, t, hs)) return false;
   const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!aligned(Q) || !aligned(K) || !aligned(mask) || !aligned(P) || (!causal && !mask)) return false;
-  if (O && (!V || heads == 0 || bh % heads || ldo < hs * heads)) return false;
+  if (O && (!V || !aligned(V) || !aligned(O) || ldo % 4 || heads == 0 || bh % heads || ldo < hs * heads)) return false;
   const int b = (int)bh, l = (int)ldo, H = (int)heads;
   if (t == 256 && hs == 64) launch<256, 64>(Q, K, V, scale, mask, P, O, l, H, b, causal, s);
   else if (t == 128 && hs == 64) launch<128, 64>(Q, K, V, scale, mask, P, O, l, H, b, causal, s);
@@ -591,8 +591,10 @@ bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const f
   if (!attn_scores_supported(bh, t, hs) || heads == 0 || bh % heads || ldo < hs * heads) return false;
   const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!aligned(dO) || !aligned(V) || !aligned(P) || !aligned(dS) || ldo % 4) return false;
-  if (dQ && !K) return false;
-  if (kv && (!dQ || !kv->Q || !kv->dK || !kv->dV || !aligned(kv->Q))) return false;
+  if (dQ && (!K || !aligned(K) || !aligned(dQ) || (Dq && !aligned(Dq)))) return false;
+  if (kv && (!dQ || !kv->Q || !kv->dK || !kv->dV || !aligned(kv->Q) || !aligned(kv->dK) || !aligned(kv->dV) ||
+             (kv->Dk && !aligned(kv->Dk)) || (kv->Dv && !aligned(kv->Dv))))
+    return false;
   const int b = (int)bh, l = (int)ldo, H = (int)heads;
   if (t == 256 && hs == 64) launch_bwd<256, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);
   else if (t == 128 && hs == 64) launch_bwd<128, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);

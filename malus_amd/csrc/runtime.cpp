@@ -606,6 +606,7 @@ void malus_tensor_write(int64_t h, const void* src, size_t bytes) {
   TensorBuffer* t = T(h);
   if (bytes > t->bytes()) fail("malus: tensor_write of %zu bytes into a %zu-byte tensor", bytes, t->bytes());
   upload(t->data(), src, bytes);
+  t->st->causal_t = 0;
   t->write_seq = enqueue_mark("tensor_write");
   API_CATCH()
 }

@@ -606,6 +606,30 @@ int64_t malus_std_cross_entropy_bwd(int64_t probs, int64_t targets, int64_t dout
 // axis=2) for q, k: [bh, t, hs], scale: [1, 1], mask: [t, t].  causal != 0
 // promises a causal mask (-1e9 above the diagonal).  Returns 0 with the error
 // set for shapes the fused kernel is not built for.
+// Checks of the public attention entries.  Every operand is f32.  causal=1
+// lets the kernels skip the key tiles above the diagonal, which is only valid
+// for the mask tensor_causal_mask builds (0 on and below the diagonal, -1e9
+// above; checked here on the host) and, in the VJPs, for probabilities that a
+// causal forward wrote (marked on their storage).
+static void attn_need_f32(const char* what, std::initializer_list<const TensorBuffer*> ts) {
+  for (const TensorBuffer* t : ts)
+    if (t && t->dtype != F32) fail("malus: %s: every operand must be f32, got dtype tag %d", what, (int)t->dtype);
+}
+static void attn_need_causal_mask(const char* what, const TensorBuffer* mk, size_t t) {
+  if (!mk->st) fail("malus: %s: the mask has no device storage", what);
+  std::vector<float> m(t * t);
+  download(m.data(), mk, m.size() * sizeof(float));
+  for (size_t i = 0; i < t; ++i)
+    for (size_t j = 0; j < t; ++j)
+      if (m[i * t + j] != (j > i ? -1e9f : 0.0f))
+        fail("malus: %s: causal=1 needs the causal mask (0 on/below the diagonal, -1e9 above); element [%zu,%zu] is %g",
+             what, i, j, (double)m[i * t + j]);
+}
+static void attn_need_causal_probs(const char* what, const TensorBuffer* p, size_t t) {
+  if (!p->st || p->st->causal_t != (uint32_t)t)
+    fail("malus: %s: causal=1 needs probabilities written by a causal attention forward", what);
+}
+
 int64_t malus_std_attn_scores_softmax(int64_t q, int64_t kk, int64_t scale, int64_t mask, int32_t causal) {
   API_TRY
   TensorBuffer *Q = T(q), *K = T(kk), *sc = T(scale), *mk = T(mask);
@@ -617,10 +641,13 @@ int64_t malus_std_attn_scores_softmax(int64_t q, int64_t kk, int64_t scale, int6
   const size_t bh = Q->shape[0], t = Q->shape[1], hs = Q->shape[2];
   if (!k::attn_scores_supported(bh, t, hs))
     fail("malus: attn_scores_softmax: no fused kernel for t=%zu hs=%zu", t, hs);
+  attn_need_f32("attn_scores_softmax", {Q, K, sc, mk});
+  if (causal) attn_need_causal_mask("attn_scores_softmax", mk, t);
   const size_t shape[3] = {bh, t, t};
   TensorBuffer* out = alloc_tensor(F32, shape, 3);
   if (!k::attn_scores_softmax(Q->f32(), K->f32(), sc->f32(), mk->f32(), out->f32(), bh, t, hs, causal != 0, stream()))
     fail("malus: attn_scores_softmax: unaligned operand");
+  out->st->causal_t = causal ? (uint32_t)t : 0;
   return done(out, "attn_scores_softmax");
   API_CATCH(0)
 }
@@ -636,6 +663,8 @@ int64_t malus_std_attn_scores_bwd(int64_t dout, int64_t v, int64_t p, int64_t sc
          shape_str(V).c_str(), shape_str(Pt).c_str(), shape_str(sc).c_str());
   const size_t bh = d->shape[0], t = d->shape[1], hs = d->shape[2];
   if (!k::attn_scores_supported(bh, t, hs)) fail("malus: attn_scores_bwd: no fused kernel for t=%zu hs=%zu", t, hs);
+  attn_need_f32("attn_scores_bwd", {d, V, Pt, sc});
+  if (causal) attn_need_causal_probs("attn_scores_bwd", Pt, t);
   const size_t shape[3] = {bh, t, t};
   TensorBuffer* out = alloc_tensor(F32, shape, 3);
   if (!k::attn_scores_bwd(d->f32(), hs, 1, V->f32(), Pt->f32(), sc->f32(), out->f32(), bh, t, hs, causal != 0, stream()))
@@ -655,6 +684,8 @@ int64_t malus_std_attn_fwd(int64_t q, int64_t kk, int64_t v, int64_t scale, int6
          shape_str(K).c_str(), shape_str(V).c_str(), shape_str(sc).c_str(), shape_str(mk).c_str());
   const size_t bh = Q->shape[0], t = Q->shape[1], hs = Q->shape[2];
   if (!k::attn_scores_supported(bh, t, hs)) fail("malus: attn_fwd: no fused kernel for t=%zu hs=%zu", t, hs);
+  attn_need_f32("attn_fwd", {Q, K, V, sc, mk});
+  if (causal) attn_need_causal_mask("attn_fwd", mk, t);
   const size_t pshape[3] = {bh, t, t};
   TensorBuffer* p = alloc_tensor(F32, pshape, 3);
   TensorBuffer* out = alloc_tensor(F32, Q->shape, 3);
@@ -662,6 +693,7 @@ int64_t malus_std_attn_fwd(int64_t q, int64_t kk, int64_t v, int64_t scale, int6
                    causal != 0, stream()))
     fail("malus: attn_fwd: unaligned operand");
   const uint64_t seq = enqueue_mark("attn_fwd");
+  p->st->causal_t = causal ? (uint32_t)t : 0;
   p->write_seq = seq;
   out->write_seq = seq;
   if (p_out) *p_out = malus::H(p);
@@ -681,6 +713,8 @@ int64_t malus_std_attn_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, in
          shape_str(V).c_str(), shape_str(Pt).c_str(), shape_str(sc).c_str(), shape_str(K).c_str());
   const size_t bh = d->shape[0], t = d->shape[1], hs = d->shape[2];
   if (!k::attn_scores_supported(bh, t, hs)) fail("malus: attn_bwd: no fused kernel for t=%zu hs=%zu", t, hs);
+  attn_need_f32("attn_bwd", {d, V, Pt, sc, K});
+  if (causal) attn_need_causal_probs("attn_bwd", Pt, t);
   const size_t shape[3] = {bh, t, t};
   TensorBuffer* out = alloc_tensor(F32, shape, 3);
   TensorBuffer* dq = dq_out ? alloc_tensor(F32, K->shape, 3) : nullptr;
@@ -713,6 +747,8 @@ int64_t malus_std_attn_bwd_all(int64_t dout, int64_t q, int64_t kk, int64_t v, i
          shape_str(sc).c_str());
   const size_t bh = d->shape[0], t = d->shape[1], hs = d->shape[2];
   if (!k::attn_scores_supported(bh, t, hs)) fail("malus: attn_bwd_all: no fused kernel for t=%zu hs=%zu", t, hs);
+  attn_need_f32("attn_bwd_all", {d, Q, K, V, Pt, sc, Aq, Ak, Av});
+  if (causal) attn_need_causal_probs("attn_bwd_all", Pt, t);
   const size_t shape[3] = {bh, t, t};
   TensorBuffer* out = alloc_tensor(F32, shape, 3);
   TensorBuffer *dq = alloc_like(Q), *dk = alloc_like(K), *dv = alloc_like(V);

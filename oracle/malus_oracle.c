@@ -224,6 +224,39 @@ void or_reduce_axis(int op, const float* x, const size_t* shape, int ndim, int a
         }
 }
 
+/* VJPs of the axis reductions: tape.rs:1085-1145, composed the same way by
+ * reduce_bwd.ml:40-71.  y is the forward output (used by max only); dout
+ * has outer*inner elements.
+ *   sum:  dx = expand(dout)
+ *   mean: dx = expand(dout * (1/n))                    (scalar_mul, 1.0/n)
+ *   max:  dx = expand(dout) * (x == expand(y))         (every tied max gets it)
+ *   var:  dx = expand(dout) * ((x - expand(mean)) * (2/n)), mean keepdim     */
+void or_reduce_axis_bwd(int op, const float* x, const float* y, const float* dout, const size_t* shape, int ndim,
+                        int axis, float* out) {
+    size_t O, A, I;
+    outer_axis_inner(shape, ndim, axis, &O, &A, &I);
+    float* mean = NULL;
+    if (op == OR_RVAR) {
+        mean = (float*)malloc(O * I * sizeof(float));
+        or_reduce_axis(OR_RMEAN, x, shape, ndim, axis, mean);
+    }
+    const float inv_n = 1.0f / (float)A, two_n = 2.0f / (float)A;
+    for (size_t o = 0; o < O; ++o)
+        for (size_t k = 0; k < A; ++k)
+            for (size_t i = 0; i < I; ++i) {
+                size_t f = (o * A + k) * I + i, s = o * I + i;
+                float r;
+                switch (op) {
+                case OR_RSUM: r = dout[s]; break;
+                case OR_RMEAN: r = dout[s] * inv_n; break;
+                case OR_RMAX: r = dout[s] * (x[f] == y[s] ? 1.0f : 0.0f); break;
+                default: r = dout[s] * ((x[f] - mean[s]) * two_n); break;
+                }
+                out[f] = r;
+            }
+    free(mean);
+}
+
 float or_sum_all(const float* x, size_t n) {
     float s = 0.0f;
     for (size_t i = 0; i < n; ++i) s += x[i];

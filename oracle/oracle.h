@@ -47,6 +47,9 @@ enum { OR_RSUM = 0, OR_RMEAN = 1, OR_RMAX = 2, OR_RVAR = 3 };
 /* Output element count = outer*inner; layout identical for keepdim 0/1. */
 void or_reduce_axis(int op, const float* x, const size_t* shape, int ndim, int axis, float* out);
 float or_sum_all(const float* x, size_t n); /* tensor_sum metal.rs:996-1006 */
+/* VJPs of the axis reductions (tape.rs:1085-1145, reduce_bwd.ml:40-71); y used by max only. */
+void or_reduce_axis_bwd(int op, const float* x, const float* y, const float* dout, const size_t* shape, int ndim,
+                        int axis, float* out);
 
 /* ---- transformer ops (metal.rs:1437-1688) ------------------------------- */
 void or_softmax_axis(const float* x, const size_t* shape, int ndim, int axis, float* out);

@@ -49,6 +49,7 @@ def lib():
             "or_unary": (None, [C.c_int, _f, C.c_size_t, _f]),
             "or_reduce_axis": (None, [C.c_int, _f, _szp, C.c_int, C.c_int, _f]),
             "or_sum_all": (C.c_float, [_f, C.c_size_t]),
+            "or_reduce_axis_bwd": (None, [C.c_int, _f, _f, _f, _szp, C.c_int, C.c_int, _f]),
             "or_softmax_axis": (None, [_f, _szp, C.c_int, C.c_int, _f]),
             "or_layernorm_axis": (None, [_f, _szp, C.c_int, C.c_int, _f, _f]),
             "or_cross_entropy": (C.c_float, [_f, C.c_size_t, C.c_size_t, _i32p, _f]),
@@ -162,6 +163,17 @@ def reduce_axis(op, x, axis, keepdim=False):
     out = np.empty(int(np.prod(out_shape)) if out_shape else 1, np.float32)
     lib().or_reduce_axis(op, _fp(x), _sz(x.shape), x.ndim, axis, _fp(out))
     return out.reshape(out_shape) if out_shape else out
+
+
+def reduce_axis_bwd(op, x, dout, axis, y=None):
+    """VJP of reduce_axis (tape.rs:1085-1145); y = the forward output (max only)."""
+    x = f32(x)
+    ax = axis % x.ndim
+    dout = f32(dout).ravel()
+    y = f32(y).ravel() if y is not None else np.zeros(dout.size, np.float32)
+    out = np.empty(x.shape, np.float32)
+    lib().or_reduce_axis_bwd(op, _fp(x), _fp(y), _fp(dout), _sz(x.shape), x.ndim, ax, _fp(out))
+    return out
 
 
 def sum_all(x):

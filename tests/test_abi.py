@@ -77,3 +77,49 @@ def test_no_device_fails_loudly_without_cpu_fallback():
         assert lib.tensor_alloc_zeros_gpu(shape, 1) == 0  # no silent host allocation either
     finally:
         lib.malus_set_abort_on_error(1)
+
+
+FLOAT2_KERNEL = r"""
+extern "C" __global__ void malus_kernel_7(const float2* a, const float2* b, float2* out, unsigned n) {
+  unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float2 x = a[i], y = b[i];
+  out[i] = make_float2(x.x * y.x + 1.0f, x.y * y.y + 1.0f);
+}
+"""
+
+
+def rtc_compile(src, arch=b"gfx950"):
+    import malus_amd as M
+
+    lib = M.lib()
+    log = C.create_string_buffer(1 << 16)
+    n = lib.malus_rtc_compile(src.encode(), arch, None, 0, log, len(log))
+    assert n > 0, log.value.decode()
+    buf = C.create_string_buffer(n)
+    assert lib.malus_rtc_compile(src.encode(), arch, buf, n, log, len(log)) == n
+    return buf.raw
+
+
+def test_runtime_compiled_kernels_use_no_packed_fp32(tmp_path):
+    """User kernels go through hipRTC with the library's option list, which
+    disables packed-FP32 instruction selection: a float2 multiply-add that
+    would otherwise become v_pk_mul_f32 / v_pk_add_f32 must not (checked in
+    the AMD disassembly of the code object compiled here)."""
+    co = tmp_path / "k.co"
+    co.write_bytes(rtc_compile(FLOAT2_KERNEL))
+    objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    if not os.path.exists(objdump):
+        pytest.skip("llvm-objdump not available")
+    asm = subprocess.run([objdump, "-d", str(co)], capture_output=True, text=True, check=True).stdout
+    assert "v_mul_f32" in asm or "v_fma" in asm or "v_add_f32" in asm, "kernel body not found in the disassembly"
+    assert not re.search(r"v_pk_(add|mul|fma)_f32", asm), "packed FP32 instructions in a runtime-compiled kernel"
+
+
+def test_runtime_compile_reports_errors():
+    import malus_amd as M
+
+    log = C.create_string_buffer(1 << 14)
+    n = M.lib().malus_rtc_compile(b"extern \"C\" __global__ void k() { undefined_name(); }", b"gfx950", None, 0, log,
+                                  len(log))
+    assert n == 0 and b"undefined_name" in log.value

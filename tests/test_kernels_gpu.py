@@ -150,6 +150,44 @@ def test_reduce_axis(rt, shape, axis, op):
     rt.free(hx)
 
 
+@pytest.mark.parametrize("shape,axis,keep", [((5, 24), 1, 1), ((6, 40, 5), 1, 0), ((3000, 7), 0, 1), ((4, 1500), 1, 0),
+                                            ((2, 3, 4), 2, 1), ((17,), 0, 0), ((64, 2048), 0, 0)])
+@pytest.mark.parametrize("op", [M.R_SUM, M.R_MEAN, M.R_MAX, M.R_VAR])
+def test_reduce_axis_vjps(rt, shape, axis, keep, op):
+    """malus_std_reduce_{sum,mean,max,var}_axis_bwd (reduce_bwd.ml:40-71) vs
+    the oracle: sum, mean and max are single roundings per element
+    (bit-exact; max with ties, every tied maximum gets dout); var goes
+    through the device mean, so it meets the reduction bar."""
+    x = rand(*shape, lo=-2, hi=2)
+    if op == M.R_MAX:
+        # every reduced line holds its maximum at least twice (first and last position)
+        xv = np.moveaxis(x, axis, -1)
+        m = xv.max(axis=-1)
+        xv[..., 0] = m
+        xv[..., -1] = m
+        x = np.ascontiguousarray(np.moveaxis(xv, -1, axis))
+    hx = rt.tensor(x)
+    hy = rt.L.malus_std_reduce_fwd(op, hx, axis, keep)
+    y = rt.numpy(hy)
+    dout = rand(*y.shape) if y.ndim else rand(1)
+    hd = rt.tensor(dout)
+    fn = {M.R_SUM: lambda: rt.L.malus_std_reduce_sum_axis_bwd(hx, hd, axis),
+          M.R_MEAN: lambda: rt.L.malus_std_reduce_mean_axis_bwd(hx, hd, axis),
+          M.R_MAX: lambda: rt.L.malus_std_reduce_max_axis_bwd(hx, hy, hd, axis),
+          M.R_VAR: lambda: rt.L.malus_std_reduce_var_axis_bwd(hx, hd, axis)}[op]
+    h = fn()
+    assert rt.shape(h) == shape
+    got = run(rt, h)
+    want = O.reduce_axis_bwd(op, x, dout, axis, y if op == M.R_MAX else None)
+    if op == M.R_VAR:
+        assert_normwise(got, want, 1e-5, f"var VJP {shape} {axis}")
+    else:
+        assert_bitexact(got, want, f"reduce VJP {op} {shape} {axis}")
+    if op == M.R_MAX:
+        assert np.count_nonzero(got) > got.size // shape[axis], "the tie case must be exercised"
+    rt.free(hx, hy, hd)
+
+
 def test_reduce_keepdim_shapes(rt):
     x = rand(2, 3)
     hx = rt.tensor(x)
@@ -348,6 +386,44 @@ def test_attn_scores_softmax_rejects_unbuilt_shapes(rt):
     finally:
         rt.L.malus_set_abort_on_error(1)
     rt.free(hq, hsc, hm)
+
+
+def test_attn_causal_flag_requires_causal_operands(rt):
+    # causal=1 skips the key tiles above the diagonal: valid only for the
+    # causal mask itself and, in the VJPs, for P written by a causal forward.
+    # Anything else is an error, never a silently wrong result.
+    t, hs = 64, 32
+    hq = rt.tensor(rand(3, t, hs))
+    hsc = rt.tensor(np.ones((1, 1), np.float32))
+    hm_bad = rt.tensor(rand(t, t))
+    hm_ok = rt.L.tensor_causal_mask(t)
+    hi = rt.tensor(np.zeros((3, t, hs), np.int32))
+    rt.L.malus_set_abort_on_error(0)
+    try:
+        assert rt.L.malus_std_attn_scores_softmax(hq, hq, hsc, hm_bad, 1) == 0
+        assert "causal=1 needs the causal mask" in rt.last_error()
+        rt.L.malus_clear_error()
+        assert rt.L.malus_std_attn_fwd(hq, hq, hq, hsc, hm_bad, 1, None) == 0
+        assert "causal=1 needs the causal mask" in rt.last_error()
+        rt.L.malus_clear_error()
+        hp_dense = rt.L.malus_std_attn_scores_softmax(hq, hq, hsc, hm_bad, 0)
+        assert hp_dense != 0
+        assert rt.L.malus_std_attn_bwd(hq, hq, hp_dense, hsc, hq, 1, None) == 0
+        assert "written by a causal attention forward" in rt.last_error()
+        rt.L.malus_clear_error()
+        assert rt.L.malus_std_attn_scores_bwd(hq, hq, hp_dense, hsc, 1) == 0
+        assert "written by a causal attention forward" in rt.last_error()
+        rt.L.malus_clear_error()
+        assert rt.L.malus_std_attn_fwd(hi, hq, hq, hsc, hm_ok, 1, None) == 0
+        assert "must be f32" in rt.last_error()
+        rt.L.malus_clear_error()
+        hp_causal = rt.L.malus_std_attn_scores_softmax(hq, hq, hsc, hm_ok, 1)
+        hds = rt.L.malus_std_attn_scores_bwd(hq, hq, hp_causal, hsc, 1)
+        assert hds != 0, rt.last_error()
+        rt.free(hp_dense, hp_causal, hds)
+    finally:
+        rt.L.malus_set_abort_on_error(1)
+    rt.free(hq, hsc, hm_bad, hm_ok, hi)
 
 
 @pytest.mark.parametrize("shape,axis", [((65, 1024), 1), ((100, 384), 1), ((33, 128), 1), ((4, 70), 1),

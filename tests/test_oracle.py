@@ -347,3 +347,28 @@ def test_gpt_oracle_gradients_finite_differences():
         num = (vals[0] - vals[1]) / (2 * eps)
         ana = float(gp @ d)
         assert abs(num - ana) <= 3e-2 * abs(ana) + 2e-5, (pi, num, ana)
+
+
+@pytest.mark.parametrize("op", [O.R_SUM, O.R_MEAN, O.R_VAR])
+@pytest.mark.parametrize("shape,axis", [((5, 24), 1), ((6, 4, 5), 1), ((7, 3), 0)])
+def test_reduce_axis_vjps_finite_differences(op, shape, axis):
+    x = r(*shape, lo=-2, hi=2)
+    ysh = list(shape)
+    ysh[axis] = 1
+    w = r(*ysh).astype(np.float64)
+    g = O.reduce_axis_bwd(op, x, w.astype(np.float32), axis)
+    fd_check(lambda z: wsum(w, O.reduce_axis(op, z, axis, keepdim=True)), x, g, eps=5e-3)
+
+
+def test_reduce_axis_vjps_closed_forms_and_max_ties():
+    # mean: dout/N broadcast; var: dout * 2(x - mean)/N; max: every tied
+    # maximum receives dout (reduce_bwd.ml:54-58), the others 0.
+    x = np.array([[1, 3, 3, 2], [0, 5, -1, 5], [-4, -4, -4, -4]], np.float32)
+    d = np.array([2, 3, 0.5], np.float32)
+    np.testing.assert_array_equal(O.reduce_axis_bwd(O.R_MEAN, x, d, 1), np.repeat(d[:, None] * np.float32(0.25), 4, 1))
+    y = O.reduce_axis(O.R_MAX, x, 1)
+    np.testing.assert_array_equal(O.reduce_axis_bwd(O.R_MAX, x, d, 1, y),
+                                  [[0, 2, 2, 0], [0, 3, 0, 3], [0.5, 0.5, 0.5, 0.5]])
+    want_var = d[:, None].astype(np.float64) * 2 * (x - x.astype(np.float64).mean(1, keepdims=True)) / 4
+    np.testing.assert_allclose(O.reduce_axis_bwd(O.R_VAR, x, d, 1), want_var, rtol=0, atol=1e-6)
+    np.testing.assert_array_equal(O.reduce_axis_bwd(O.R_SUM, x, d, 0 + 1), np.repeat(d[:, None], 4, 1))

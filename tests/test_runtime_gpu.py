@@ -459,6 +459,33 @@ def test_v2_index_and_vjp_kernels(rt, kid):
     rt.free(hw, hi, he, hb, hp, hn, hg, h4, hp4)
 
 
+def test_v2_unary_bwd_helper_kernels(rt, kid):
+    # __scale_kernel, __fill_like_kernel, __eq_kernel (unary_bwd.ml:6-34) and
+    # __rsqrt_eps_kernel (transformer_bwd.ml:6-12) by tag, at the host fns'
+    # launch shape grid=[n], tg=[1], with the output shaped like input 0.
+    n = 70001
+    x = RNG.standard_normal((7, n // 7)).astype(np.float32)
+    y = np.where(RNG.random(x.shape) < 0.3, x, RNG.standard_normal(x.shape)).astype(np.float32)
+    hx, hy = rt.tensor(x), rt.tensor(y)
+    hs = v2(rt, kid, "__scale_kernel", [hx], [n, 1, 1], [1, 1, 1], uniforms=u("f", -0.375))
+    assert rt.shape(hs) == x.shape
+    assert_bitexact(rt.numpy(hs), O.scalar_op(O.MUL, x, -0.375), "scale via v2")
+    hf = v2(rt, kid, "__fill_like_kernel", [hx], [n, 1, 1], [1, 1, 1], uniforms=u("f", 2.5))
+    assert_bitexact(rt.numpy(hf), np.full(x.shape, 2.5, np.float32), "fill_like via v2")
+    he = v2(rt, kid, "__eq_kernel", [hx, hy], [n, 1, 1], [1, 1, 1])
+    eq = rt.numpy(he)
+    assert_bitexact(eq, (x == y).astype(np.float32), "eq via v2")
+    assert 0.2 < eq.mean() < 0.4
+    v = RNG.uniform(0, 4, x.shape).astype(np.float32)
+    v.flat[:3] = [0.0, 1e-30, 3.0]
+    hv = rt.tensor(v)
+    hr = v2(rt, kid, "__rsqrt_eps_kernel", [hv], [n, 1, 1], [1, 1, 1], uniforms=u("f", 1e-5))
+    # 1/sqrt(v + eps) in f32: an IEEE add, square root and division
+    want = np.float32(1) / np.sqrt(v + np.float32(1e-5))
+    assert_bitexact(rt.numpy(hr), want, "rsqrt_eps via v2")
+    rt.free(hx, hy, hs, hf, he, hv, hr)
+
+
 def test_v1_builtins(rt, kid):
     a = RNG.uniform(0.5, 2, 1001).astype(np.float32)
     b = RNG.uniform(0.5, 2, 1001).astype(np.float32)
