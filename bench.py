@@ -1,11 +1,15 @@
 """Headline benchmark: warm-median ms/step of the Karpathy char-nanoGPT f32
 training step on one MI355X.
 
-A step = zero_grad -> forward -> cross_entropy -> backward -> "AdamW"
-(examples/nanogpt_modular.ml:167-189) through libmalus_hip's C ABI, with a
-device flush inside the timed step (docs/adr/0038-benchmark-methodology.md).
-Token batches are synthetic (int32 i.i.d. uniform in [0, 65) from a fixed
-seed) and resident in HBM before timing starts.  Prints ONE JSON line.
+A step = token upload (the `freeze` of buffer.rs:39-50) -> zero_grad ->
+forward -> cross_entropy -> backward -> "AdamW" (examples/nanogpt_modular.ml:
+167-189) through libmalus_hip's C ABI, with a device flush inside the timed
+step (docs/adr/0038-benchmark-methodology.md).  Token batches are synthetic
+(int32 i.i.d. uniform in [0, 65) from a fixed seed), built on the host before
+timing and uploaded inside each timed step.  Prints ONE JSON line.
+
+--config c4 runs the toy char-nanoGPT the same
+way; --config c1 runs the XOR MLP's 10,000 steps.
 """
 from __future__ import annotations
 
@@ -20,7 +24,11 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-CFG = dict(V=65, T=256, C=384, H=6, L=6, B=64)
+CONFIGS = {
+    "c5": dict(V=65, T=256, C=384, H=6, L=6, B=64),
+    "c4": dict(V=65, T=64, C=128, H=4, L=4, B=32),
+}
+CFG = CONFIGS["c5"]
 OPT = dict(lr=1e-3, b1=0.9, b2=0.99, eps=1e-8, wd=0.1)
 METRIC = "warm-median ms/step, char-nanoGPT f32 train step; HBM GB/s & MFMA % of peak"
 PEAK_FP32_MFMA_TFLOPS = 157.3
@@ -181,111 +189,190 @@ def kernel_suite(rt, M, reps: int):
     return rows
 
 
-def cpu_baseline(sample_batch: int, threads: int):
+def host_cpu():
+    """The host the CPU baseline ran on: usable cores and the CPU model."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count()
+    return avail, model
+
+
+def cpu_baseline(cfg, batches, threads: int):
     """The oracle (plain-C restatement of the reference CPU path) on a
-    bounded sample: one full step at batch `sample_batch`, scaled to the
-    configured batch (every cost in the step is linear in the batch)."""
+    bounded sample.  One full training step costs a + b*B: the forward and
+    backward scale with the batch B, the optimizer and the batch-independent
+    parts (AdamW over every parameter, the LN-weight and embedding-table
+    sizes) do not.  Time one step at each of two small batches, fit a and b,
+    and report the step at the configured batch."""
     from oracle import oracle as O
     import numpy as np
 
-    cfg = dict(CFG, B=sample_batch)
     O.set_threads(threads)
-    g = O.Gpt(**cfg, rng_call_idx=0, **OPT)
     rng = np.random.default_rng(7)
-    n = cfg["B"] * cfg["T"]
-    x = rng.integers(0, cfg["V"], n).astype(np.int32)
-    y = rng.integers(0, cfg["V"], n).astype(np.int32)
+    pts = []
+    for b in batches:
+        c = dict(cfg, B=b)
+        g = O.Gpt(**c, rng_call_idx=0, **OPT)
+        n = b * c["T"]
+        x = rng.integers(0, c["V"], n).astype(np.int32)
+        y = rng.integers(0, c["V"], n).astype(np.int32)
+        t0 = time.perf_counter()
+        g.step(x, y, 1)
+        pts.append((b, time.perf_counter() - t0))
+        del g
+    (b0, t0_), (b1, t1_) = pts
+    per_b = (t1_ - t0_) / (b1 - b0)
+    fixed = t0_ - per_b * b0
+    est = fixed + per_b * cfg["B"]
+    avail, model = host_cpu()
+    return dict(value=round(est * 1e3, 1), unit="ms/step", cores=threads, kind="port",
+                cores_available=avail, cpu_model=model,
+                method=f"one oracle step at batch {b0} ({t0_:.2f} s) and at batch {b1} ({t1_:.2f} s); "
+                       f"fit a + b*B (a = {fixed:.3f} s, b = {per_b:.3f} s per sequence), evaluated at B={cfg['B']}",
+                sample=f"2 full steps (batches {b0} and {b1}) of the {cfg['B']}-sequence workload")
+
+
+def cpu_baseline_xor(steps: int):
+    """The oracle's XOR training (examples/xor.ml), all `steps` steps, 1 thread."""
+    from oracle import oracle as O
+
     t0 = time.perf_counter()
-    g.step(x, y, 1)
+    O.xor_train(steps, 1.5)
     dt = time.perf_counter() - t0
-    scale = CFG["B"] / sample_batch
-    return dict(value=round(dt * 1e3 * scale, 1), unit="ms/step", cores=threads, kind="port",
-                sample=f"1 full step at batch {sample_batch} of {CFG['B']} ({dt:.1f} s), scaled x{scale:g}")
+    avail, model = host_cpu()
+    return dict(value=round(dt * 1e3 / steps, 5), unit="ms/step", cores=1, kind="port", cores_available=avail,
+                cpu_model=model, total_s=round(dt, 4), method=f"the full {steps}-step run, timed once",
+                sample=f"all {steps} steps")
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-batch", type=int, default=1)
-    ap.add_argument("--cpu-threads", type=int, default=1)
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="run only a plain 256 MiB copy (counter calibration for the traffic figure)")
-    ap.add_argument("--suite", choices=["kernels"],
-                    help="kernels: the C2/C3 elementwise and row-op kernels' HBM bandwidth (one JSON line)")
-    a = ap.parse_args()
-    if a.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
-              "multi-GPU data parallelism is designed but not built", file=sys.stderr)
-        sys.exit(2)
+# examples/xor.ml:1-2 `sigmoid_backward`, the one user kernel on the C1 path,
+# lowered to the v1 kernel ABI (implicit form: out[tid] = expr).
+SIGMOID_BACKWARD_ML = """kernel sigmoid_backward(grad_out: Tensor<f32>, sig_z: Tensor<f32>) -> Tensor<f32>:
+    return grad_out * sig_z * (1.0 - sig_z)
+"""
 
-    import numpy as np
 
+def xor_kernel_id(rt):
+    """Lower xor.ml's user kernel with the library's HIP emitter and register
+    it through malus_runtime_init; returns its kernel id."""
     import malus_amd as M
 
-    rt = M.Runtime()
+    reg = M.compile_kernels(SIGMOID_BACKWARD_ML)
+    rt.L.malus_runtime_init(*reg.init_args())
+    return reg.ids["sigmoid_backward"]
+
+
+def run_xor(rt, a):
+    """C1: the XOR MLP's 10,000 training steps (examples/xor.ml) through the
+    C ABI; every step is ~37 runtime ops on [4,8]-sized tensors, so the
+    figure is launch and latency bound (no roofline applies)."""
     L = rt.L
-    if a.copy_calibration:
-        copy_calibration(rt, M.sizes)
-        return
-    if a.suite == "kernels":
-        rows = kernel_suite(rt, M, reps=10)
-        print(json.dumps({"suite": "kernels", "unit": "GB/s", "peak_hbm_GBs": PEAK_HBM_GBS, "rows": rows}), flush=True)
-        return
+    kid = xor_kernel_id(rt)
+    steps = 10000
+    loss_at, preds, params = (C.c_float * 6)(), (C.c_float * 4)(), (C.c_float * 33)()
+    for _ in range(a.warmup):
+        L.malus_xor_run(100, 1.5, kid, None, None, None)
+    L.gpu_barrier()
+    runs = []
+    for _ in range(max(1, min(a.steps, 5))):
+        t0 = time.perf_counter()
+        loss = L.malus_xor_run(steps, 1.5, kid, loss_at, preds, params)
+        L.gpu_barrier()
+        runs.append(time.perf_counter() - t0)
+    total = statistics.median(runs)
+    log(f"xor: {len(runs)} runs of {steps} steps, median {total:.3f} s ({total * 1e3 / steps:.4f} ms/step), "
+        f"final loss {loss:.8g}, predictions {[round(v, 6) for v in preds]}")
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = cpu_baseline_xor(steps)
+        log(f"cpu baseline: {cpu}")
+    return {
+        "metric": METRIC, "value": round(total * 1e3 / steps, 5), "unit": "ms/step", "n_gpus": 1,
+        "steps": steps, "warmup": a.warmup, "ms_per_step": round(total * 1e3 / steps, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "the fixed tensors of examples/xor.ml (no RNG)",
+        "config": {"workload": "C1 XOR MLP 2-8-1, 10,000 SGD steps (lr 1.5)", "total_s": round(total, 4),
+                   "runs": len(runs), "final_loss": loss, "parallelism": "single GPU"},
+        "roofline": None,
+        "cpu_baseline": cpu,
+    }
+
+
+def run_gpt(rt, a, cfg):
+    L = rt.L
+    import numpy as np
+
     name = C.create_string_buffer(64)
     cus, clk = C.c_int(), C.c_int()
     L.malus_device_info(name, 64, C.byref(cus), C.byref(clk))
     log(f"device {name.value.decode()} CUs {cus.value} clock {clk.value / 1e6:.2f} GHz")
 
     L.malus_rng_set_counter(0)
-    g = L.malus_gpt_create(CFG["V"], CFG["T"], CFG["C"], CFG["H"], CFG["L"], CFG["B"], OPT["lr"], OPT["b1"],
+    g = L.malus_gpt_create(cfg["V"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["B"], OPT["lr"], OPT["b1"],
                            OPT["b2"], OPT["eps"], OPT["wd"])
-    n = CFG["B"] * CFG["T"]
+    n = cfg["B"] * cfg["T"]
     rng = np.random.default_rng(2024)
-    batches = []
-    for _ in range(a.warmup + a.steps):
-        x = rng.integers(0, CFG["V"], n).astype(np.int32)
-        y = rng.integers(0, CFG["V"], n).astype(np.int32)
-        batches.append((rt.tensor(x), rt.tensor(y)))
-    L.gpu_barrier()
+    gemm_steps = min(a.steps, 20)
+    host = [(rng.integers(0, cfg["V"], n).astype(np.int32), rng.integers(0, cfg["V"], n).astype(np.int32))
+            for _ in range(a.warmup + a.steps + gemm_steps)]
 
     t = 0
+
+    def step(i):
+        # the step's own token upload (buffer.rs:39-50 freeze), then the step
+        nonlocal t
+        t += 1
+        x, y = rt.tensor(host[i][0]), rt.tensor(host[i][1])
+        hl = L.malus_gpt_step(g, x, y, t)
+        return hl, x, y
+
     first_loss = last_loss = None
     for i in range(a.warmup):
-        t += 1
-        hl = L.malus_gpt_step(g, batches[i][0], batches[i][1], t)
+        hl, x, y = step(i)
         L.gpu_barrier()
         if first_loss is None:
             first_loss = L.malus_tensor_get_f32(hl, 0)
-        rt.free(hl)
-
-    L.malus_ktimer_collect(None, C.byref(C.c_double()), C.byref(C.c_double()))  # drop warmup records
-    L.malus_ktimer_enable(1)
+        rt.free(hl, x, y)
     L.gpu_barrier()
-    times = []
-    enq = []
+
+    # headline: the kernel timer is off
+    times, enq = [], []
     t_all = time.perf_counter()
     for i in range(a.steps):
-        t += 1
-        x, y = batches[a.warmup + i]
         t0 = time.perf_counter()
-        hl = L.malus_gpt_step(g, x, y, t)
+        hl, x, y = step(a.warmup + i)
         enq.append((time.perf_counter() - t0) * 1e3)
         L.gpu_barrier()  # flush inside the timed step
         times.append((time.perf_counter() - t0) * 1e3)
         if i == a.steps - 1:
             last_loss = L.malus_tensor_get_f32(hl, 0)
-        rt.free(hl)
+        rt.free(hl, x, y)
     L.gpu_barrier()
     wall = time.perf_counter() - t_all
+
+    # a separate pass for the GEMM class: HIP events around every GEMM launch
+    L.malus_ktimer_collect(None, C.byref(C.c_double()), C.byref(C.c_double()))  # drop stale records
+    L.malus_ktimer_enable(1)
+    for i in range(gemm_steps):
+        hl, x, y = step(a.warmup + a.steps + i)
+        L.gpu_barrier()
+        rt.free(hl, x, y)
     L.malus_ktimer_enable(0)
     gms, gflop = C.c_double(), C.c_double()
     ng = L.malus_ktimer_collect(b"gemm", C.byref(gms), C.byref(gflop))
 
     med = statistics.median(times)
-    step_flops = gemm_flops_per_step(CFG)
+    step_flops = gemm_flops_per_step(cfg)
     gemm_tflops = gflop.value / (gms.value * 1e-3) / 1e12 if gms.value > 0 else 0.0
     log(f"steps {a.steps}: median {med:.3f} ms  min {min(times):.3f}  max {max(times):.3f}  wall {wall:.2f} s  "
         f"(host enqueue median {statistics.median(enq):.3f} ms)")
@@ -293,23 +380,23 @@ def main():
     ps = (C.c_int64 * 4)()
     L.malus_pool_stats(ps)
     log(f"pool: hits {ps[0]} misses {ps[1]} peak device bytes {ps[3] / 1e9:.2f} GB")
-    log(f"gemm: {ng} launches, {gms.value / a.steps:.3f} ms/step, {gemm_tflops:.1f} TFLOP/s "
-        f"({gflop.value / a.steps / 1e9:.1f} GFLOP/step; algorithmic {step_flops / 1e9:.1f})")
+    log(f"gemm ({gemm_steps} separate steps): {ng} launches, {gms.value / gemm_steps:.3f} ms/step, "
+        f"{gemm_tflops:.1f} TFLOP/s ({gflop.value / gemm_steps / 1e9:.1f} GFLOP/step; "
+        f"algorithmic {step_flops / 1e9:.1f})")
 
     cpu = None
     if not a.no_cpu_baseline:
         try:
-            cpu = cpu_baseline(a.cpu_sample_batch, a.cpu_threads)
+            cpu = cpu_baseline(cfg, (1, 2) if cfg["B"] >= 16 else (1, cfg["B"]), a.cpu_threads)
             log(f"cpu baseline: {cpu}")
         except Exception as e:  # the CPU leg is a reported baseline only
             log(f"cpu baseline failed: {e!r}")
-
-    for x, y in batches:
-        rt.free(x, y)
     L.malus_gpt_free(g)
 
-    traffic = measured_traffic()
-    out = {
+    c5 = cfg == CONFIGS["c5"]
+    traffic = measured_traffic() if c5 else None
+    tag = "C5 Karpathy" if c5 else "C4 toy"
+    return {
         "metric": METRIC,
         "value": round(med, 3),
         "unit": "ms/step",
@@ -321,19 +408,54 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic int32 tokens i.i.d. uniform in [0,65) (seed 2024); weights randn*0.02 (Philox, call 0)",
-        "config": {"workload": "C5 Karpathy char-nanoGPT train step (fwd+bwd+AdamW)", "vocab": CFG["V"],
-                   "block_size": CFG["T"], "n_embd": CFG["C"], "n_head": CFG["H"], "n_layer": CFG["L"],
-                   "batch": CFG["B"], "tokens_per_step": n, "parallelism": "single GPU"},
+        "data": "synthetic int32 tokens i.i.d. uniform in [0,65) (seed 2024), uploaded inside each timed step; "
+                "weights randn*0.02 (Philox, call 0)",
+        "config": {"workload": f"{tag} char-nanoGPT train step (token upload+fwd+bwd+AdamW)", "vocab": cfg["V"],
+                   "block_size": cfg["T"], "n_embd": cfg["C"], "n_head": cfg["H"], "n_layer": cfg["L"],
+                   "batch": cfg["B"], "tokens_per_step": n, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "k_sgemm (all GEMM launches of the step)",
                      "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic,
                      "traffic_unit": "HBM bytes per step, all GEMM launches (rocprofv3 FETCH_SIZE+WRITE_SIZE)",
-                     "algorithmic_bytes": gemm_bytes_per_step(CFG),
-                     "gemm_ms_per_step": round(gms.value / a.steps, 3),
-                     "gemm_gflop_per_step": round(gflop.value / a.steps / 1e9, 1)},
+                     "algorithmic_bytes": gemm_bytes_per_step(cfg),
+                     "timing": f"HIP events around each GEMM launch over {gemm_steps} steps run after the "
+                               "headline steps (the headline runs with the event timer off)",
+                     "gemm_ms_per_step": round(gms.value / gemm_steps, 3),
+                     "gemm_gflop_per_step": round(gflop.value / gemm_steps / 1e9, 1)},
         "cpu_baseline": cpu,
     }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", choices=["c5", "c4", "c1"], default="c5",
+                    help="c5 (default): Karpathy char-nanoGPT; c4: toy char-nanoGPT; c1: XOR MLP, 10,000 steps")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=1)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 256 MiB copy (counter calibration for the traffic figure)")
+    ap.add_argument("--suite", choices=["kernels"],
+                    help="kernels: the C2/C3 elementwise and row-op kernels' HBM bandwidth (one JSON line)")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
+              "multi-GPU data parallelism is designed but not built", file=sys.stderr)
+        sys.exit(2)
+
+    import malus_amd as M
+
+    rt = M.Runtime()
+    if a.copy_calibration:
+        copy_calibration(rt, M.sizes)
+        return
+    if a.suite == "kernels":
+        rows = kernel_suite(rt, M, reps=10)
+        print(json.dumps({"suite": "kernels", "unit": "GB/s", "peak_hbm_GBs": PEAK_HBM_GBS, "rows": rows}), flush=True)
+        return
+    out = run_xor(rt, a) if a.config == "c1" else run_gpt(rt, a, CONFIGS[a.config])
     print(json.dumps(out), flush=True)
 
 

@@ -47,6 +47,29 @@ int malus_kernel_is_builtin(uint64_t id);
  * into `code` when `cap` is large enough. */
 size_t malus_rtc_compile(const char* src, const char* arch, void* code, size_t cap, char* log, size_t log_cap);
 
+/* ---- HIP emitter (crates/malus-codegen-gpu/src/lib.rs) -------------------- */
+/* compile_kernels (codegen-gpu/lib.rs:95-155) as a C ABI.  `program` is malus
+ * source; each top-level `kernel` item is parsed, type-checked with the
+ * reference sema's kernel-body rules and lowered to HIP C++ for hipRTC
+ * (implicit-map bodies to the v1 ABI, lib.rs:432-562; explicit bodies to the
+ * v2 ABI, lib.rs:564-1006); other items are skipped.  `builtins` names the
+ * synthesized kernels the program's fn bodies use ("malus_add" ...
+ * "malus_rdiv_scalar", "relu" ... "abs"; lib.rs:373-418), which sema collects
+ * from typed fn bodies.  Ids are process-global and increase in the
+ * reference's order: user kernels, tensor-tensor, scalar-broadcast, unary.
+ * flags bit 0: prefix the sources of kernels the runtime implements by hand
+ * (the stdlib kernels and builtins) with "//@malus-builtin <name>", so
+ * malus_runtime_init binds the hand-written kernel.  Returns NULL on error
+ * (malus_last_error() in return mode). */
+typedef struct malus_registry malus_registry;
+malus_registry* malus_compile_kernels(const char* program, const char* const* builtins, size_t nbuiltins, int flags);
+size_t malus_registry_len(const malus_registry* r);
+uint64_t malus_registry_id(const malus_registry* r, size_t i);
+const char* malus_registry_name(const malus_registry* r, size_t i);
+const char* malus_registry_source(const malus_registry* r, size_t i);
+int malus_registry_lookup(const malus_registry* r, const char* name, uint64_t* id);
+void malus_registry_free(malus_registry* r);
+
 /* ---- tensor creation and lifetime (metal.rs:340-558) -------------------- */
 int64_t tensor_alloc_gpu(int32_t dtype, const size_t* shape, size_t ndim, const void* data); /* metal.rs:341-348 */
 int64_t tensor_alloc_zeros_gpu(const size_t* shape, size_t ndim);                          /* metal.rs:458-484 */

@@ -180,6 +180,13 @@ SIGNATURES = {
     "malus_gpt_optimizer_step": (None, [_vp, _i64]),
     "malus_gpt_step": (_i64, [_vp, _i64, _i64, _i64]),
     "malus_xor_run": (_f32, [C.c_int, _f32, _u64, _P(_f32), _P(_f32), _P(_f32)]),
+    "malus_compile_kernels": (_vp, [C.c_char_p, _P(C.c_char_p), _sz, C.c_int]),
+    "malus_registry_len": (_sz, [_vp]),
+    "malus_registry_id": (_u64, [_vp, _sz]),
+    "malus_registry_name": (C.c_char_p, [_vp, _sz]),
+    "malus_registry_source": (C.c_char_p, [_vp, _sz]),
+    "malus_registry_lookup": (C.c_int, [_vp, C.c_char_p, _P(_u64)]),
+    "malus_registry_free": (None, [_vp]),
 }
 
 _lib = None
@@ -248,6 +255,47 @@ class Runtime:
     def last_error(self) -> str:
         e = self.L.malus_last_error()
         return e.decode() if e else ""
+
+
+class KernelRegistry:
+    """compile_kernels' output (the emitter's id -> HIP source map, plus name
+    -> id), read out of the library's registry."""
+
+    def __init__(self, entries):
+        self.entries = entries  # [(name, id, source)] in id order
+        self.ids = {n: i for n, i, _ in entries}
+        self.sources = {n: s for n, _, s in entries}
+
+    def init_args(self):
+        """(ids, sources, n) for malus_runtime_init."""
+        n = len(self.entries)
+        ids = (_u64 * max(1, n))(*[i for _, i, _ in self.entries])
+        srcs = (C.c_char_p * max(1, n))(*[s.encode() for _, _, s in self.entries])
+        return ids, srcs, n
+
+
+def compile_kernels(program: str, builtins=(), tags: bool = False) -> KernelRegistry:
+    """Lower the `kernel` items of malus source `program` (and the named
+    synthesized builtins) to HIP with the library's emitter.  Raises
+    RuntimeError with the emitter's message on a bad program.  Needs no GPU."""
+    L = lib()
+    names = [b.encode() for b in builtins]
+    arr = (C.c_char_p * max(1, len(names)))(*names)
+    L.malus_set_abort_on_error(0)
+    try:
+        r = L.malus_compile_kernels(program.encode(), arr, len(names), 1 if tags else 0)
+        if not r:
+            msg = L.malus_last_error()
+            L.malus_clear_error()
+            raise RuntimeError(msg.decode() if msg else "malus_compile_kernels failed")
+    finally:
+        L.malus_set_abort_on_error(1)
+    try:
+        entries = [(L.malus_registry_name(r, i).decode(), int(L.malus_registry_id(r, i)),
+                    L.malus_registry_source(r, i).decode()) for i in range(L.malus_registry_len(r))]
+    finally:
+        L.malus_registry_free(r)
+    return KernelRegistry(entries)
 
 
 def device_count_hint() -> int:

@@ -79,7 +79,20 @@ struct KernelEntry {
   Builtin builtin = Builtin::None;
   hipModule_t module = nullptr;
   hipFunction_t fn = nullptr;
+  // From the emitter's annotations: v1 inputs read only at [0] (bit i =
+  // input i), and the v2 uniforms blob size (-1: unknown).
+  uint32_t scalar_inputs = 0;
+  long uniform_bytes = -1;
 };
+
+// The emitter's "//@malus-<key> <value>" annotation lines.
+bool annotation(const std::string& src, const char* key, long* value) {
+  std::string tag = std::string("//@malus-") + key + " ";
+  size_t p = src.find(tag);
+  if (p == std::string::npos) return false;
+  *value = strtol(src.c_str() + p + tag.size(), nullptr, 10);
+  return true;
+}
 
 struct Registry {
   std::mutex mu;
@@ -102,11 +115,19 @@ std::string device_arch() {
   return c == std::string::npos ? a : a.substr(0, c);
 }
 
+// Source-cache key: the text with the kernel id taken out of every name the
+// emitter derives from it (malus_kernel_<id>, Uniforms_<id>), so identical
+// bodies registered under different ids share one module (metal.rs:304-336).
 std::string normalize(uint64_t id, const std::string& src) {
-  std::string needle = "malus_kernel_" + std::to_string(id);
   std::string s = src;
-  size_t pos = s.find(needle);
-  if (pos != std::string::npos) s.replace(pos, needle.size(), "malus_kernel_X");
+  for (const std::string& prefix : {std::string("malus_kernel_"), std::string("Uniforms_")}) {
+    const std::string needle = prefix + std::to_string(id);
+    for (size_t pos = s.find(needle); pos != std::string::npos; pos = s.find(needle, pos + prefix.size() + 1)) {
+      const size_t end = pos + needle.size();
+      if (end < s.size() && isdigit((unsigned char)s[end])) continue;  // a longer id
+      s.replace(pos, needle.size(), prefix + "X");
+    }
+  }
   return s;
 }
 
@@ -405,6 +426,10 @@ KernelEntry lookup(uint64_t id, const char* api) {
 
 }  // namespace
 
+namespace malus {
+bool dispatch_has_builtin(const std::string& name) { return builtin_names().count(name) != 0; }
+}  // namespace malus
+
 extern "C" {
 
 // runtime_init(&HashMap<u64, String>) as a C ABI (metal.rs:304-336).
@@ -439,6 +464,9 @@ void malus_runtime_init(const uint64_t* ids, const char* const* sources, size_t 
       }
       if (hipModuleGetFunction(&e.fn, e.module, fname.c_str()) != hipSuccess)
         fail("malus: kernel function '%s' not found", fname.c_str());
+      long v;
+      if (annotation(src, "v1-scalar-inputs", &v) && v >= 0 && v < 32) e.scalar_inputs |= 1u << v;
+      if (annotation(src, "v2-uniform-bytes", &v)) e.uniform_bytes = v;
     }
     std::lock_guard<std::mutex> lk(reg().mu);
     reg().by_id[ids[i]] = e;
@@ -480,9 +508,13 @@ int64_t kernel_dispatch(uint64_t id, const int64_t* handles, size_t count) {
     run_builtin_v1(e.builtin, in, out);
   } else {
     // an emitted implicit-map kernel reads in_i[tid] for every tid < out.len
-    for (auto* t : in)
-      if (t->len < out->len)
-        fail("malus: kernel_dispatch input of %zu elements is shorter than the %zu-element output", t->len, out->len);
+    // (a scalar-broadcast builtin reads its scalar input at [0] only)
+    for (size_t i = 0; i < in.size(); ++i) {
+      const size_t need = (i < 32 && (e.scalar_inputs >> i) & 1u) ? 1 : out->len;
+      if (in[i]->len < need)
+        fail("malus: kernel_dispatch input of %zu elements is shorter than the %zu elements the kernel reads",
+             in[i]->len, need);
+    }
     std::vector<void*> ptrs;
     for (auto* t : in) ptrs.push_back(t->data());
     ptrs.push_back(out->data());
@@ -524,6 +556,9 @@ int64_t kernel_dispatch_v2(uint64_t id, const int64_t* handles, size_t hc, const
     std::vector<TensorMeta> metas;
     for (auto* t : in) metas.push_back(meta_of(t));
     metas.push_back(meta_of(out));
+    if (e.uniform_bytes >= 0 && (size_t)e.uniform_bytes != ubytes)
+      fail("malus: kernel_dispatch_v2: kernel %llu takes %ld bytes of uniforms, got %zu", (unsigned long long)id,
+           e.uniform_bytes, ubytes);
     std::vector<uint8_t> ublob(ubytes);
     if (ubytes && uniforms) memcpy(ublob.data(), uniforms, ubytes);
     std::vector<void*> args;

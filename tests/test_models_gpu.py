@@ -11,17 +11,10 @@ import pytest
 
 import malus_amd as M
 from oracle import oracle as O
+from tests.emit_programs import SIGMOID_BACKWARD
 from tests.helpers import normwise_err
 
 pytestmark = pytest.mark.gpu
-
-SIGMOID_BACKWARD_HIP = """
-extern "C" __global__ void malus_kernel_{id}(const float* grad_out, const float* sig_z, float* out, unsigned n) {{
-  unsigned tid = blockIdx.x * blockDim.x + threadIdx.x;
-  if (tid >= n) return;
-  out[tid] = ((grad_out[tid] * sig_z[tid]) * (1.0f - sig_z[tid]));
-}}
-"""
 
 C4 = dict(V=65, T=64, C=128, H=4, L=4, B=32)
 C5 = dict(V=65, T=256, C=384, H=6, L=6, B=64)
@@ -33,8 +26,11 @@ def oracle_threads():
 
 
 def test_xor_10000_steps_vs_oracle(rt):
-    kid = 9100
-    rt.L.malus_runtime_init((C.c_uint64 * 1)(kid), (C.c_char_p * 1)(SIGMOID_BACKWARD_HIP.format(id=kid).encode()), 1)
+    # xor.ml's user kernel, lowered by the library's HIP emitter and compiled with hipRTC
+    reg = M.compile_kernels(SIGMOID_BACKWARD)
+    rt.L.malus_runtime_init(*reg.init_args())
+    kid = reg.ids["sigmoid_backward"]
+    assert not rt.L.malus_kernel_is_builtin(kid)
     loss_at = np.zeros(6, np.float32)
     preds = np.zeros(4, np.float32)
     params = np.zeros(33, np.float32)
