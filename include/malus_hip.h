@@ -89,6 +89,9 @@ int32_t malus_tensor_dtype(int64_t h);
 void malus_tensor_shape(int64_t h, size_t* out /* [8] */);
 void malus_tensor_read(int64_t h, void* dst, size_t bytes);
 void malus_tensor_write(int64_t h, const void* src, size_t bytes);
+/* The device address of a tensor's storage; NULL for a shape-only handle.
+ * Writes made through it are not tracked by tensor_is_pending. */
+void* malus_tensor_device_ptr(int64_t h);
 size_t malus_format_f32(float v, char* buf, size_t cap);
 
 /* ---- synchronization (metal.rs:201-259, 677-694) ------------------------ */

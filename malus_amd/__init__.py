@@ -46,6 +46,7 @@ SIGNATURES = {
     "malus_tensor_get_f32": (_f32, [_i64, _i64]),
     "malus_tensor_read": (None, [_i64, _vp, _sz]),
     "malus_tensor_write": (None, [_i64, _vp, _sz]),
+    "malus_tensor_device_ptr": (_vp, [_i64]),
     "malus_format_f32": (_sz, [_f32, C.c_char_p, _sz]),
     "gpu_barrier": (None, []),
     "malus_flush_if_pending": (None, [_i64]),

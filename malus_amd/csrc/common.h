@@ -134,6 +134,13 @@ void iota_rows(int32_t* out, size_t rows, size_t t, hipStream_t s);
 // Axis reductions over a contiguous [outer, axis, inner] view.
 enum RedOp : int { R_SUM = 0, R_MEAN = 1, R_MAX = 2, R_VAR = 3 };
 void reduce_axis(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
+// reduce_axis with its temporaries (split partials; the variance's mean) in
+// a caller's device buffer of `scratch_floats` floats instead of the pool;
+// the same plan and kernels, so the same values.  reduce_axis_scratch_floats
+// is the size that call needs (0: none).
+size_t reduce_axis_scratch_floats(int op, const float* x, const float* out, size_t outer, size_t axis, size_t inner);
+void reduce_axis_scratch(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, float* scratch,
+                         size_t scratch_floats, hipStream_t s);
 // P = softmax over the last axis of (S * scale[0]) + mask[row % mask_rows],
 // each op rounded as the separate broadcast kernels round it.
 void scale_mask_softmax(const float* S, const float* scale, const float* mask, float* P, size_t rows, size_t axis,

@@ -14,6 +14,8 @@
 // is rounded to f32 exactly as the materialized tensor would be.
 // Every order is fixed, so results are run-to-run deterministic.
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 #include "common.h"
 
@@ -359,9 +361,61 @@ ColPlan col_plan(size_t outer, size_t axis, size_t inner, bool aligned) {
   return p;
 }
 
+// Where a reduction's temporaries (split partials, the variance's mean) come
+// from: the device pool by default, or a caller's fixed buffer (`base`, `cap`
+// floats), carved in 256-byte-aligned pieces.  Buffers taken from the pool
+// go back to it in release(): stream order keeps every later user behind the
+// kernels that read them.
+struct Arena {
+  float* base = nullptr;
+  size_t cap = 0, used = 0;
+  std::vector<std::pair<void*, size_t>> pooled;
+  float* get(size_t n) {
+    if (!base) {
+      size_t bucket;
+      void* p = pool_alloc(n * sizeof(float), &bucket);
+      pooled.emplace_back(p, bucket);
+      return static_cast<float*>(p);
+    }
+    if (used + n > cap) fail("malus: reduction scratch overflow (%zu + %zu floats > %zu)", used, n, cap);
+    float* p = base + used;
+    used += (n + 63) / 64 * 64;
+    return p;
+  }
+  void release() {
+    for (auto& q : pooled) pool_free(q.first, q.second);
+    pooled.clear();
+  }
+};
+
+// The split plan of a long-row reduction (rows of `axis` elements): 0 when
+// the rows are reduced without splitting.
+uint32_t row_split(size_t rows, size_t axis, size_t* chunk_out) {
+  if (!(axis >= 16384 && rows < 2048)) return 0;
+  size_t want_blocks = 2048;
+  uint32_t nsplit = (uint32_t)((want_blocks + rows - 1) / rows);
+  size_t chunk = (axis + nsplit - 1) / nsplit;
+  chunk = (chunk + 1023) / 1024 * 1024;  // multiple of 4, float4-friendly
+  nsplit = (uint32_t)((axis + chunk - 1) / chunk);
+  *chunk_out = chunk;
+  return nsplit;
+}
+
+// Floats of partials one reduce_impl call takes from its arena.
+size_t partial_floats(size_t outer, size_t axis, size_t inner, bool aligned) {
+  if (outer * inner == 0 || axis == 0) return 0;
+  if (inner == 1) {
+    size_t chunk;
+    const uint32_t nsplit = row_split(outer, axis, &chunk);
+    return nsplit ? outer * nsplit : 0;
+  }
+  const ColPlan cp = col_plan(outer, axis, inner, aligned);
+  return cp.nsplit > 1 ? (outer * cp.nsplit * inner + 63) / 64 * 64 : 0;
+}
+
 template <int OP>
 void reduce_impl(const float* x, const float* y, const float* mean, float* out, size_t outer, size_t axis, size_t inner,
-                 hipStream_t s) {
+                 hipStream_t s, Arena& arena) {
   constexpr int COMB = combine_op<OP>();
   const size_t n_out = outer * inner;
   const bool nt = outer * axis * inner * sizeof(float) * (OP == R_PROD ? 2 : 1) >= kStreamBytes;
@@ -375,14 +429,9 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
   if (inner == 1) {
     const size_t rows = outer;
     // Long rows with few of them: split each row across blocks.
-    if (axis >= 16384 && rows < 2048) {
-      size_t want_blocks = 2048;
-      uint32_t nsplit = (uint32_t)((want_blocks + rows - 1) / rows);
-      size_t chunk = (axis + nsplit - 1) / nsplit;
-      chunk = (chunk + 1023) / 1024 * 1024;  // multiple of 4, float4-friendly
-      nsplit = (uint32_t)((axis + chunk - 1) / chunk);
-      size_t bucket;
-      float* partial = static_cast<float*>(pool_alloc(rows * nsplit * sizeof(float), &bucket));
+    size_t chunk;
+    if (const uint32_t nsplit = row_split(rows, axis, &chunk)) {
+      float* partial = arena.get(rows * nsplit);
       k_row_split<OP><<<(unsigned)(rows * nsplit), 256, 0, s>>>(x, y, mean, partial, axis, nsplit, chunk, nt);
       MALUS_HIP(hipGetLastError());
       // combine partials of each row with one wave per row; MEAN and VAR
@@ -391,7 +440,6 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
       k_row_wave<FIN, false><<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, rows, nsplit,
                                                                        (uint32_t)axis, true, false);
       MALUS_HIP(hipGetLastError());
-      pool_free(partial, bucket);
       return;
     }
     const bool vec = (axis % 4) == 0;
@@ -409,8 +457,7 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
   const size_t col_blocks = cp.col_blocks, base_blocks = outer * col_blocks, chunk = cp.chunk;
   const uint32_t nsplit = cp.nsplit;
   float* dst = out;
-  size_t bucket = 0;
-  if (nsplit > 1) dst = static_cast<float*>(pool_alloc(outer * nsplit * inner * sizeof(float), &bucket));
+  if (nsplit > 1) dst = arena.get(outer * nsplit * inner);
   if (vec) {
     launch_col4<OP>(ct, dim3((unsigned)col_blocks, nsplit, (unsigned)outer), x, y, mean, dst, axis, inner, nsplit, chunk,
                     nsplit == 1, nt, cp.contig, s);
@@ -431,7 +478,6 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
       k_row_wave<FIN, false><<<(unsigned)((cols + 3) / 4), 256, 0, s>>>(dst, nullptr, nullptr, out, cols, nsplit,
                                                                          (uint32_t)axis, true, false);
     MALUS_HIP(hipGetLastError());
-    pool_free(dst, bucket);
   } else if (nsplit > 1) {
     // base_blocks < 2048 here, so outer fits gridDim.y
     // columns per combine block: enough split groups to keep ~4+ partials each
@@ -448,32 +494,56 @@ void reduce_impl(const float* x, const float* y, const float* mean, float* out, 
     else if (cc == 16) comb(std::integral_constant<int, 16>{});
     else comb(std::integral_constant<int, 64>{});
     MALUS_HIP(hipGetLastError());
-    pool_free(dst, bucket);
   }
 }
 
 }  // namespace
 
-void reduce_axis(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {
+static void reduce_axis_in(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s,
+                           Arena& arena) {
   switch (op) {
-    case R_SUM: reduce_impl<R_SUM>(x, nullptr, nullptr, out, outer, axis, inner, s); break;
-    case R_MEAN: reduce_impl<R_MEAN>(x, nullptr, nullptr, out, outer, axis, inner, s); break;
-    case R_MAX: reduce_impl<R_MAX>(x, nullptr, nullptr, out, outer, axis, inner, s); break;
+    case R_SUM: reduce_impl<R_SUM>(x, nullptr, nullptr, out, outer, axis, inner, s, arena); break;
+    case R_MEAN: reduce_impl<R_MEAN>(x, nullptr, nullptr, out, outer, axis, inner, s, arena); break;
+    case R_MAX: reduce_impl<R_MAX>(x, nullptr, nullptr, out, outer, axis, inner, s, arena); break;
     case R_VAR: {
-      // two-pass population variance (reduce_var.ml:11-22)
-      size_t bucket;
-      float* mean = static_cast<float*>(pool_alloc(outer * inner * sizeof(float), &bucket));
-      reduce_impl<R_MEAN>(x, nullptr, nullptr, mean, outer, axis, inner, s);
-      reduce_impl<R_VAR>(x, nullptr, mean, out, outer, axis, inner, s);
-      pool_free(mean, bucket);
+      // two-pass population variance (reduce_var.ml:11-22); the mean pass's
+      // partials are consumed before the variance pass starts (stream order),
+      // so both passes carve the same region after the mean
+      float* mean = arena.get(outer * inner);
+      const size_t mark = arena.used;
+      reduce_impl<R_MEAN>(x, nullptr, nullptr, mean, outer, axis, inner, s, arena);
+      arena.used = mark;
+      reduce_impl<R_VAR>(x, nullptr, mean, out, outer, axis, inner, s, arena);
       break;
     }
     default: fail("malus: bad reduction op %d", op);
   }
 }
 
+void reduce_axis(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {
+  Arena arena;
+  reduce_axis_in(op, x, out, outer, axis, inner, s, arena);
+  arena.release();
+}
+
+size_t reduce_axis_scratch_floats(int op, const float* x, const float* out, size_t outer, size_t axis, size_t inner) {
+  const bool aligned = ((uintptr_t)x | (uintptr_t)out) % 16 == 0;
+  const size_t part = partial_floats(outer, axis, inner, aligned);
+  return op == R_VAR ? (outer * inner + 63) / 64 * 64 + part : part;
+}
+
+void reduce_axis_scratch(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, float* scratch,
+                         size_t scratch_floats, hipStream_t s) {
+  Arena arena;
+  arena.base = scratch;
+  arena.cap = scratch_floats;
+  reduce_axis_in(op, x, out, outer, axis, inner, s, arena);
+}
+
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {
-  reduce_impl<R_PROD>(x, y, nullptr, out, outer, axis, inner, s);
+  Arena arena;
+  reduce_impl<R_PROD>(x, y, nullptr, out, outer, axis, inner, s, arena);
+  arena.release();
 }
 
 bool col_prod_split(size_t axis, size_t inner, uint32_t* nsplit, size_t* chunk, int* row_threads) {

@@ -601,6 +601,12 @@ void malus_tensor_read(int64_t h, void* dst, size_t bytes) {
 }
 
 // Overwrite a tensor's contents from host memory (stream-ordered).
+// The device address of a tensor's storage (NULL for a shape-only handle).
+void* malus_tensor_device_ptr(int64_t h) {
+  TensorBuffer* t = T(h);
+  return t && t->st ? t->st->ptr : nullptr;
+}
+
 void malus_tensor_write(int64_t h, const void* src, size_t bytes) {
   API_TRY
   TensorBuffer* t = T(h);
