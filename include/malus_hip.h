@@ -47,6 +47,23 @@ int malus_kernel_is_builtin(uint64_t id);
  * into `code` when `cap` is large enough. */
 size_t malus_rtc_compile(const char* src, const char* arch, void* code, size_t cap, char* log, size_t log_cap);
 
+/* ---- allocation-free reduction ------------------------------------------ */
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The values of malus_std_reduce_fwd(op, x, axis, keepdim)
+ * (op: 0 sum, 1 mean, 2 max, 3 population variance) for a contiguous f32
+ * tensor of `shape` at device address `x`, written to the caller's device
+ * buffer `out` (outer * inner floats; keepdim only changes the shape), with
+ * the same kernels and plan.  Its split partials and the variance's mean
+ * live in a fixed 4 MiB device array of the library (one per GPU, held until
+ * the process ends, set up by malus_init); a reduction needing more is
+ * rejected with an error.  No hipMalloc/hipFree is called.  The work is
+ * enqueued on the library's stream (gpu_barrier() waits for it); calls on one
+ * GPU share the array, so calls that overlap (several host threads) race.
+ * With 16-byte-aligned x and out the values equal malus_std_reduce_fwd's.
+ * Returns 0, or -1 in return-error mode. */
+int malus_std_reduce_noalloc(int32_t op, const float* x, const size_t* shape, size_t ndim, int64_t axis, float* out);
+
 /* ---- HIP emitter (crates/malus-codegen-gpu/src/lib.rs) -------------------- */
 /* compile_kernels (codegen-gpu/lib.rs:95-155) as a C ABI.  `program` is malus
  * source; each top-level `kernel` item is parsed, type-checked with the

@@ -62,6 +62,9 @@ std::string shape_str(const TensorBuffer* t);
 
 // ---- context ---------------------------------------------------------------
 void ensure_init();
+// Set-up of the allocation-free entry point's scratch array on `device`
+// (noalloc.hip); called once by ensure_init with that device current.
+void noalloc_init_device(int device);
 hipStream_t stream();
 // Marks one enqueued GPU operation; returns its sequence number.  Every op
 // that writes a tensor stamps that tensor's write_seq with it.

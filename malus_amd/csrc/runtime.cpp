@@ -172,6 +172,7 @@ void ensure_init() {
     const char* hg = getenv("MALUS_ALLOC_HISTOGRAM");
     c->histogram = hg && std::string(hg) == "1";
     g_ctx = c;
+    noalloc_init_device(c->device);
     register_default_backward_fns();
   });
 }
