@@ -327,11 +327,22 @@ def run_gpt(rt, a, cfg):
             for _ in range(a.warmup + a.steps + gemm_steps)]
 
     t = 0
+    I32P = C.POINTER(C.c_int32)
+    graph = None
 
     def step(i):
         # the step's own token upload (buffer.rs:39-50 freeze), then the step
-        nonlocal t
+        nonlocal t, graph
         t += 1
+        if a.graph:
+            x, y = host[i]
+            if graph is None:  # step 1 runs eagerly inside create, which then captures the step
+                hl = C.c_int64()
+                graph = L.malus_gpt_graph_create(g, x.ctypes.data_as(I32P), y.ctypes.data_as(I32P), t, C.byref(hl))
+                if not graph:
+                    raise RuntimeError("malus_gpt_graph_create failed")
+                return hl.value, 0, 0
+            return L.malus_gpt_graph_step(graph, x.ctypes.data_as(I32P), y.ctypes.data_as(I32P), t), 0, 0
         x, y = rt.tensor(host[i][0]), rt.tensor(host[i][1])
         hl = L.malus_gpt_step(g, x, y, t)
         return hl, x, y
@@ -359,6 +370,13 @@ def run_gpt(rt, a, cfg):
         rt.free(hl, x, y)
     L.gpu_barrier()
     wall = time.perf_counter() - t_all
+    nodes = 0
+    if graph is not None:
+        nodes = L.malus_gpt_graph_nodes(graph)
+        L.malus_gpt_graph_free(graph)
+        graph = None
+        log(f"graph: one hipGraphLaunch per step, {nodes} nodes (kernels + 3 input copies)")
+    a_graph, a.graph = a.graph, False  # the GEMM pass below runs eagerly (event timers are not graph nodes)
 
     # a separate pass for the GEMM class: HIP events around every GEMM launch
     L.malus_ktimer_collect(None, C.byref(C.c_double()), C.byref(C.c_double()))  # drop stale records
@@ -410,6 +428,9 @@ def run_gpt(rt, a, cfg):
         "dtype": "f32",
         "data": "synthetic int32 tokens i.i.d. uniform in [0,65) (seed 2024), uploaded inside each timed step; "
                 "weights randn*0.02 (Philox, call 0)",
+        "execution": ("hipGraph replay of the captured step (token/target ids and AdamW bias corrections copied from "
+                      f"pinned host memory by the graph's nodes; {nodes} nodes)") if a_graph else
+                     "eager: every kernel launched from the host each step",
         "config": {"workload": f"{tag} char-nanoGPT train step (token upload+fwd+bwd+AdamW)", "vocab": cfg["V"],
                    "block_size": cfg["T"], "n_embd": cfg["C"], "n_head": cfg["H"], "n_layer": cfg["L"],
                    "batch": cfg["B"], "tokens_per_step": n, "parallelism": "single GPU"},
@@ -433,6 +454,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", choices=["c5", "c4", "c1"], default="c5",
                     help="c5 (default): Karpathy char-nanoGPT; c4: toy char-nanoGPT; c1: XOR MLP, 10,000 steps")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the step as a replayed hipGraph (malus_gpt_graph_*) instead of eager launches")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",

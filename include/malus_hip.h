@@ -307,6 +307,17 @@ int64_t malus_gpt_logits(void* g, int64_t toks);
 void malus_gpt_zero_grad(void* g);
 void malus_gpt_optimizer_step(void* g, int64_t t);    /* nanogpt_modular.ml:186-188 */
 int64_t malus_gpt_step(void* g, int64_t toks, int64_t targets, int64_t t); /* nanogpt_modular.ml:167-189 */
+/* No reference counterpart: the whole training step as a HIP graph (the
+ * "optionally hipGraph-captured train steps" of the north star).  create runs
+ * step t eagerly (its loss in *loss_out) and captures the step; each
+ * graph_step replays it for step t on new token/target ids (copied from
+ * pinned host memory by the graph's own nodes) and returns the loss tensor
+ * (the same device buffer every step).  Parameters are updated in place; the
+ * values equal malus_gpt_step's.  Free the graph before the model. */
+void* malus_gpt_graph_create(void* gpt, const int32_t* x, const int32_t* y, int64_t t, int64_t* loss_out);
+int64_t malus_gpt_graph_step(void* graph, const int32_t* x, const int32_t* y, int64_t t);
+void malus_gpt_graph_free(void* graph);
+size_t malus_gpt_graph_nodes(void* graph);
 float malus_xor_run(int steps, float lr, uint64_t sigmoid_backward_id, float* loss_at, float* preds,
                     float* params); /* examples/xor.ml */
 

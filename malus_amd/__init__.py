@@ -181,6 +181,10 @@ SIGNATURES = {
     "malus_gpt_optimizer_step": (None, [_vp, _i64]),
     "malus_gpt_step": (_i64, [_vp, _i64, _i64, _i64]),
     "malus_xor_run": (_f32, [C.c_int, _f32, _u64, _P(_f32), _P(_f32), _P(_f32)]),
+    "malus_gpt_graph_create": (_vp, [_vp, _P(_i32), _P(_i32), _i64, _P(_i64)]),
+    "malus_gpt_graph_step": (_i64, [_vp, _P(_i32), _P(_i32), _i64]),
+    "malus_gpt_graph_free": (None, [_vp]),
+    "malus_gpt_graph_nodes": (_sz, [_vp]),
     "malus_std_reduce_noalloc": (C.c_int, [_i32, _vp, _P(_sz), _sz, _i64, _vp]),
     "malus_compile_kernels": (_vp, [C.c_char_p, _P(C.c_char_p), _sz, C.c_int]),
     "malus_registry_len": (_sz, [_vp]),

@@ -87,6 +87,12 @@ void retain(TensorBuffer* t);
 // Scratch device memory from the same pool, released with pool_free.
 void* pool_alloc(size_t bytes, size_t* bucket_out);
 void pool_free(void* p, size_t bucket);
+// HIP graph capture: buffers handed out between pool_capture_begin(g) and
+// pool_capture_end(g) stay reserved for graph g (never reused by others)
+// until pool_release_graph(g).
+void pool_capture_begin(int graph);
+void pool_capture_end(int graph);
+void pool_release_graph(int graph);
 
 // Host -> device copy on the runtime stream via pinned staging.
 void upload(void* dst, const void* src, size_t bytes);
@@ -306,7 +312,7 @@ struct AdamSeg {
 constexpr size_t kAdamChunk = 4096;  // floats per workgroup
 // Every tensor of `segs` in one launch; same per-element expression as adam_l2.
 void adam_l2_multi(const AdamSeg* segs_host, int count, float lr, float b1, float b2, float omb1, float omb2, float bc1,
-                   float bc2, float eps, float wd, hipStream_t s);
+                   float bc2, float eps, float wd, hipStream_t s, const float* bc_dev = nullptr);
 void adam_l2(const float* p, const float* g, const float* m, const float* v, float* p_out, float* m_out, float* v_out,
              size_t n, float lr, float b1, float b2, float omb1, float omb2, float bc1, float bc2, float eps, float wd,
              hipStream_t s);

@@ -69,7 +69,14 @@ struct AdamTable {
   int count;
 };
 
-__global__ __launch_bounds__(256) void k_adam_l2_multi(const AdamTable t, AdamArgs a) {
+// bc (optional): the two bias corrections read from device memory instead of
+// the arguments, so a captured step can take each step's values from a
+// buffer the host refills before every replay.
+__global__ __launch_bounds__(256) void k_adam_l2_multi(const AdamTable t, AdamArgs a, const float* __restrict__ bc) {
+  if (bc) {
+    a.bc1 = bc[0];
+    a.bc2 = bc[1];
+  }
   int si = 0;
   while (si + 1 < t.count && blockIdx.x >= t.first_chunk[si + 1]) ++si;
   const AdamSeg& sg = t.seg[si];
@@ -97,7 +104,7 @@ __global__ __launch_bounds__(256) void k_adam_l2_multi(const AdamTable t, AdamAr
 }  // namespace
 
 void adam_l2_multi(const AdamSeg* segs_host, int count, float lr, float b1, float b2, float omb1, float omb2, float bc1,
-                   float bc2, float eps, float wd, hipStream_t s) {
+                   float bc2, float eps, float wd, hipStream_t s, const float* bc_dev) {
   const AdamArgs a{lr, b1, b2, omb1, omb2, bc1, bc2, eps, wd};
   for (int base = 0; base < count; base += kAdamMaxSegs) {
     AdamTable t{};
@@ -111,7 +118,7 @@ void adam_l2_multi(const AdamSeg* segs_host, int count, float lr, float b1, floa
     t.first_chunk[t.count] = (uint32_t)chunks;
     if (chunks == 0) continue;
     if (chunks > 0x7fffffffu) fail("malus: adam update: too many parameters");
-    k_adam_l2_multi<<<(unsigned)chunks, 256, 0, s>>>(t, a);
+    k_adam_l2_multi<<<(unsigned)chunks, 256, 0, s>>>(t, a, bc_dev);
     MALUS_HIP(hipGetLastError());
   }
 }

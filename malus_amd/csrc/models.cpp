@@ -5,8 +5,10 @@
 // follow codegen-cpu's lowering (lib.rs:1525-1850, 2765-3082); the
 // nanoGPT driver is generalized to L blocks and H heads for the C4/C5
 // configurations.
+#include <atomic>
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <vector>
 
 #include "api.h"
@@ -113,6 +115,12 @@ struct Gpt {
   float lr, b1, b2, eps, wd;
   bool fused_opt = true;
   bool fused_fwd = true;  // forward fusions: scale+mask+softmax, residual adds in GEMM epilogues (same values, same tape)
+  // Parameters and moments updated in place (the same values as the
+  // reference's `ps[i] = variable(new)`; the handles stay fixed, as a
+  // captured step needs).  bc_dev: the bias corrections read from device
+  // memory instead of kernel arguments.
+  bool inplace_opt = false;
+  const float* bc_dev = nullptr;
   std::vector<int64_t> p, m, v;  // block l params at 8l..8l+7, then wte, wpe, ln_f, lm_head
   int64_t pos = 0;               // [B*T] i32 position ids
   int64_t attn_scale = 0;        // [1,1] 1/sqrt(hs) of the fused attention (built on first use)
@@ -323,6 +331,26 @@ int64_t gpt_forward_loss(Gpt& g, int64_t toks, int64_t targets, int64_t* logits_
 // expression tree as the op-by-op sequence the JIT emits.
 void adamw_range(Gpt& g, int beg, int end, int64_t t) {
   const float bc1 = 1.0f - powf(g.b1, (float)t), bc2 = 1.0f - powf(g.b2, (float)t);
+  if (g.inplace_opt) {
+    std::vector<k::AdamSeg> segs;
+    std::vector<int64_t> grads;
+    for (int i = beg; i < end; ++i) {
+      int64_t grad = tape_get_grad(g.p[i]);
+      grads.push_back(grad);
+      TensorBuffer *tp = T(g.p[i]), *tg = T(grad), *tm = T(g.m[i]), *tv = T(g.v[i]);
+      if (tg->len != tp->len || tm->len != tp->len || tv->len != tp->len) fail("malus: adam update: length mismatch");
+      // each element is read before the same thread writes it back
+      segs.push_back(k::AdamSeg{tp->f32(), tg->f32(), tm->f32(), tv->f32(), tp->f32(), tm->f32(), tv->f32(), tp->len});
+    }
+    k::adam_l2_multi(segs.data(), (int)segs.size(), g.lr, g.b1, g.b2, 1.0f - g.b1, 1.0f - g.b2, bc1, bc2, g.eps, g.wd,
+                     stream(), g.bc_dev);
+    const uint64_t seq = enqueue_mark("adam");
+    for (int i = beg; i < end; ++i) {
+      T(g.p[i])->write_seq = T(g.m[i])->write_seq = T(g.v[i])->write_seq = seq;
+      tensor_release(grads[i - beg]);
+    }
+    return;
+  }
   if (g.fused_opt) {
     std::vector<k::AdamSeg> segs;
     std::vector<int64_t> grads, np_(end - beg), nm(end - beg), nv(end - beg);
@@ -595,6 +623,163 @@ float malus_xor_run(int steps, float lr, uint64_t sigmoid_backward_id, float* lo
   if (out) tensor_release(out);
   return loss_v;
   API_CATCH(0.0f)
+}
+
+// ---- the training step as a HIP graph ---------------------------------------
+// One step (token upload, zero_grad, forward, cross_entropy, backward, AdamW)
+// captured once and replayed: one hipGraphLaunch per step instead of ~180
+// kernel launches.  Whatever changes between steps comes from pinned host
+// memory through the graph's own copy nodes: the token and target ids, and
+// AdamW's two bias corrections (1 - b^t, computed on the host as in the
+// eager step and read by the kernel from device memory).  Parameters and
+// moments are updated in place, so every address the graph uses stays fixed;
+// the pool keeps the buffers the captured step allocated for the graph alone
+// (pool_capture_begin/end).  Values are those of the eager step.
+
+}  // extern "C"
+
+namespace {
+
+struct GptGraph {
+  Gpt* g = nullptr;
+  int id = 0;
+  size_t n = 0;                  // tokens per step (B * T)
+  char* pinned = nullptr;        // [n] i32 tokens, [n] i32 targets, [2] f32 bias corrections
+  int64_t toks = 0, tgts = 0;    // fixed device inputs [n] i32
+  TensorBuffer* bc = nullptr;    // [2] f32 on the device
+  int64_t loss = 0;              // written by every replay
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipEvent_t done = nullptr;     // after the last launch: the pinned inputs may be rewritten once it completes
+  bool launched = false;
+};
+
+std::atomic<int> g_graph_ids{0};
+
+void graph_set_inputs(GptGraph& gr, const int32_t* x, const int32_t* y, int64_t t) {
+  if (gr.launched) MALUS_HIP(hipEventSynchronize(gr.done));  // the previous step's copies have read the buffer
+  int32_t* ids = reinterpret_cast<int32_t*>(gr.pinned);
+  memcpy(ids, x, gr.n * sizeof(int32_t));
+  memcpy(ids + gr.n, y, gr.n * sizeof(int32_t));
+  float* bc = reinterpret_cast<float*>(ids + 2 * gr.n);
+  bc[0] = 1.0f - powf(gr.g->b1, (float)t);  // nanogpt_modular.ml:99-100, as adamw_range computes them
+  bc[1] = 1.0f - powf(gr.g->b2, (float)t);
+}
+
+// The step's work on the stream; the same calls eagerly and under capture.
+int64_t graph_step_body(GptGraph& gr, int64_t t) {
+  Gpt& g = *gr.g;
+  const int32_t* ids = reinterpret_cast<const int32_t*>(gr.pinned);
+  MALUS_HIP(hipMemcpyAsync(T(gr.toks)->data(), ids, gr.n * sizeof(int32_t), hipMemcpyHostToDevice, stream()));
+  MALUS_HIP(hipMemcpyAsync(T(gr.tgts)->data(), ids + gr.n, gr.n * sizeof(int32_t), hipMemcpyHostToDevice, stream()));
+  MALUS_HIP(hipMemcpyAsync(gr.bc->data(), ids + 2 * gr.n, 2 * sizeof(float), hipMemcpyHostToDevice, stream()));
+  const uint64_t seq = enqueue_mark("graph inputs");
+  T(gr.toks)->write_seq = T(gr.tgts)->write_seq = gr.bc->write_seq = seq;
+  malus_gpt_zero_grad(&g);
+  int64_t loss = gpt_forward_loss(g, gr.toks, gr.tgts, nullptr);
+  backward(loss);
+  adamw_range(g, 0, 8 * g.L + 4, t);
+  return loss;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Runs step t eagerly through the graph's input buffers (it warms the pool
+// and returns that step's loss in *loss_out), then captures the step.  The
+// model switches to in-place parameter updates; free the graph before the
+// model, and leave the tape alone while the graph exists.
+void* malus_gpt_graph_create(void* gp, const int32_t* x, const int32_t* y, int64_t t, int64_t* loss_out) {
+  API_TRY
+  auto* g = static_cast<Gpt*>(gp);
+  if (!g || !x || !y) fail("malus: gpt_graph_create: null model or token ids");
+  auto gr = std::make_unique<GptGraph>();
+  gr->g = g;
+  gr->id = ++g_graph_ids;
+  gr->n = (size_t)g->B * g->Tn;
+  MALUS_HIP(hipHostMalloc(reinterpret_cast<void**>(&gr->pinned), 2 * gr->n * sizeof(int32_t) + 2 * sizeof(float),
+                          hipHostMallocDefault));
+  const size_t sh[1] = {gr->n}, sh2[1] = {2};
+  gr->toks = H(alloc_tensor(I32, sh, 1));
+  gr->tgts = H(alloc_tensor(I32, sh, 1));
+  gr->bc = alloc_tensor(F32, sh2, 1);
+  MALUS_HIP(hipEventCreateWithFlags(&gr->done, hipEventDisableTiming));
+  g->inplace_opt = true;
+  g->bc_dev = gr->bc->f32();
+  // eager step t
+  graph_set_inputs(*gr, x, y, t);
+  int64_t loss = graph_step_body(*gr, t);
+  MALUS_HIP(hipEventRecord(gr->done, stream()));
+  gr->launched = true;
+  if (loss_out) *loss_out = loss;
+  else tensor_release(loss);
+  // capture one step (recorded, not run)
+  pool_capture_begin(gr->id);
+  MALUS_HIP(hipStreamBeginCapture(stream(), hipStreamCaptureModeRelaxed));
+  int64_t cap_loss = 0;
+  try {
+    cap_loss = graph_step_body(*gr, t + 1);
+  } catch (...) {
+    hipGraph_t broken = nullptr;
+    (void)hipStreamEndCapture(stream(), &broken);
+    if (broken) (void)hipGraphDestroy(broken);
+    pool_capture_end(gr->id);
+    throw;
+  }
+  MALUS_HIP(hipStreamEndCapture(stream(), &gr->graph));
+  pool_capture_end(gr->id);
+  gr->loss = cap_loss;
+  MALUS_HIP(hipGraphInstantiate(&gr->exec, gr->graph, nullptr, nullptr, 0));
+  return gr.release();
+  API_CATCH(nullptr)
+}
+
+// One replay: step t on the given token and target ids.  Returns the loss
+// tensor (the same device buffer every step; a new reference the caller
+// releases).  Nothing is read back to the host.
+int64_t malus_gpt_graph_step(void* gh, const int32_t* x, const int32_t* y, int64_t t) {
+  API_TRY
+  auto* gr = static_cast<GptGraph*>(gh);
+  if (!gr || !x || !y) fail("malus: gpt_graph_step: null graph or token ids");
+  graph_set_inputs(*gr, x, y, t);
+  MALUS_HIP(hipGraphLaunch(gr->exec, stream()));
+  MALUS_HIP(hipEventRecord(gr->done, stream()));
+  gr->launched = true;
+  const uint64_t seq = enqueue_mark("graph step");
+  Gpt& g = *gr->g;
+  for (size_t i = 0; i < g.p.size(); ++i) T(g.p[i])->write_seq = T(g.m[i])->write_seq = T(g.v[i])->write_seq = seq;
+  T(gr->loss)->write_seq = seq;
+  tensor_retain(gr->loss);
+  return gr->loss;
+  API_CATCH(0)
+}
+
+void malus_gpt_graph_free(void* gh) {
+  API_TRY
+  auto* gr = static_cast<GptGraph*>(gh);
+  if (!gr) return;
+  MALUS_HIP(hipStreamSynchronize(stream()));
+  if (gr->exec) MALUS_HIP(hipGraphExecDestroy(gr->exec));
+  if (gr->graph) MALUS_HIP(hipGraphDestroy(gr->graph));
+  MALUS_HIP(hipEventDestroy(gr->done));
+  MALUS_HIP(hipHostFree(gr->pinned));
+  tensor_release(gr->loss);
+  tensor_release(gr->toks);
+  tensor_release(gr->tgts);
+  release(gr->bc);
+  gr->g->bc_dev = nullptr;
+  pool_release_graph(gr->id);
+  delete gr;
+  API_CATCH()
+}
+
+// Kernel nodes of the captured step (the launches one replay stands for).
+size_t malus_gpt_graph_nodes(void* gh) {
+  auto* gr = static_cast<GptGraph*>(gh);
+  size_t n = 0;
+  if (gr && gr->graph) MALUS_HIP(hipGraphGetNodes(gr->graph, nullptr, &n));
+  return n;
 }
 
 }  // extern "C"

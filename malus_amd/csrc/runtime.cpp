@@ -100,6 +100,13 @@ struct Pool {
   std::unordered_map<size_t, std::vector<void*>> free_lists;
   int64_t hits = 0, misses = 0, pooled_bytes = 0, live_bytes = 0, peak_bytes = 0;
   std::map<size_t, uint64_t> histogram;
+  // HIP graph capture: every buffer handed out while a capture is recorded
+  // (capture_owner != 0) belongs to that graph afterwards.  A graph's buffer
+  // that is freed goes to the graph's own list, never back to the free
+  // lists, so no later allocation can share memory the graph's replays write.
+  int capture_owner = 0;
+  std::unordered_map<void*, std::pair<int, size_t>> reserved;       // ptr -> (graph, bucket)
+  std::unordered_map<int, std::vector<std::pair<void*, size_t>>> reserved_free;  // graph -> its freed buffers
 };
 
 struct Context {
@@ -235,6 +242,7 @@ void* pool_alloc(size_t bytes, size_t* bucket_out) {
     c.pool.hits++;
     c.pool.pooled_bytes -= (int64_t)b;
     c.pool.live_bytes += (int64_t)b;
+    if (c.pool.capture_owner) c.pool.reserved[p] = {c.pool.capture_owner, b};
     *bucket_out = b;
     return p;
   }
@@ -250,6 +258,7 @@ void* pool_alloc(size_t bytes, size_t* bucket_out) {
   }
   c.pool.live_bytes += (int64_t)b;
   c.pool.peak_bytes = std::max(c.pool.peak_bytes, c.pool.live_bytes + c.pool.pooled_bytes);
+  if (c.pool.capture_owner) c.pool.reserved[p] = {c.pool.capture_owner, b};
   *bucket_out = b;
   return p;
 }
@@ -258,9 +267,63 @@ void pool_free(void* p, size_t bucket) {
   if (!p) return;
   Context& c = ctx();
   std::lock_guard<std::mutex> lk(c.pool.mu);
-  c.pool.free_lists[bucket].push_back(p);
+  auto r = c.pool.reserved.find(p);
+  if (r != c.pool.reserved.end() && r->second.first != c.pool.capture_owner) {
+    // a graph's buffer, freed outside that graph's capture: kept for the
+    // graph (it stays counted as live)
+    c.pool.reserved_free[r->second.first].emplace_back(p, bucket);
+    return;
+  }
   c.pool.live_bytes -= (int64_t)bucket;
   c.pool.pooled_bytes += (int64_t)bucket;
+  c.pool.free_lists[bucket].push_back(p);
+}
+
+void pool_capture_begin(int graph) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.pool.mu);
+  if (c.pool.capture_owner) fail("malus: a graph capture is already being recorded");
+  c.pool.capture_owner = graph;
+}
+
+void pool_capture_end(int graph) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.pool.mu);
+  if (c.pool.capture_owner != graph) fail("malus: pool_capture_end for a graph that is not capturing");
+  c.pool.capture_owner = 0;
+  // buffers the capture freed sit in the free lists: move them to the graph
+  for (auto& fl : c.pool.free_lists) {
+    auto& v = fl.second;
+    for (size_t i = 0; i < v.size();) {
+      auto r = c.pool.reserved.find(v[i]);
+      if (r != c.pool.reserved.end() && r->second.first == graph) {
+        c.pool.reserved_free[graph].emplace_back(v[i], fl.first);
+        c.pool.pooled_bytes -= (int64_t)fl.first;
+        c.pool.live_bytes += (int64_t)fl.first;
+        v[i] = v.back();
+        v.pop_back();
+      } else {
+        ++i;
+      }
+    }
+  }
+}
+
+// The graph is gone: its freed buffers return to the free lists, and its
+// live ones return there when their tensors are released.
+void pool_release_graph(int graph) {
+  Context& c = ctx();
+  std::lock_guard<std::mutex> lk(c.pool.mu);
+  for (auto& q : c.pool.reserved_free[graph]) {
+    c.pool.free_lists[q.second].push_back(q.first);
+    c.pool.live_bytes -= (int64_t)q.second;
+    c.pool.pooled_bytes += (int64_t)q.second;
+  }
+  c.pool.reserved_free.erase(graph);
+  for (auto it = c.pool.reserved.begin(); it != c.pool.reserved.end();) {
+    if (it->second.first == graph) it = c.pool.reserved.erase(it);
+    else ++it;
+  }
 }
 
 // ============================================================================
@@ -469,6 +532,9 @@ static std::mutex g_ktimer_mu;
 
 KTimer* ktimer_begin(const char* cls) {
   if (!g_ktimer_on.load()) return nullptr;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  MALUS_HIP(hipStreamIsCapturing(stream(), &cap));
+  if (cap != hipStreamCaptureStatusNone) return nullptr;  // no event nodes in a captured step
   std::lock_guard<std::mutex> lk(g_ktimer_mu);
   KTimer* t;
   if (g_ktimer_spare.empty()) {
