@@ -132,6 +132,15 @@ int64_t tensor_randn(const size_t* shape, size_t ndim);                 /* metal
 float malus_rand_uniform(void);                                         /* metal.rs:1744-1750 */
 int64_t malus_rand_int(int64_t n);                                      /* metal.rs:1752-1759 */
 /* No reference counterpart: read/set the per-thread RNG call counter. */
+/* No reference counterpart: the device-side data path.  randn with the
+ * stream of tensor_randn (metal.rs:1720-1740: the same Philox words and the
+ * same f64 Box-Muller), generated on the device.  batch_windows builds the
+ * nanogpt_modular.ml:170-177 batch from a device-resident 1-D i32 token
+ * stream: B sequence starts rand_int(len - T - 1) (B RNG calls, as the host
+ * loop makes them) and x/y windows of T tokens (y shifted by one), as new
+ * [B*T] i32 tensors; starts_out (host int32[B], optional) gets the starts. */
+int64_t malus_randn_device(const size_t* shape, size_t ndim);
+void malus_batch_windows(int64_t data, int64_t B, int64_t T, int64_t* x_out, int64_t* y_out, int32_t* starts_out);
 uint64_t malus_rng_get_counter(void);
 void malus_rng_set_counter(uint64_t v);
 
@@ -318,6 +327,13 @@ void* malus_gpt_graph_create(void* gpt, const int32_t* x, const int32_t* y, int6
 int64_t malus_gpt_graph_step(void* graph, const int32_t* x, const int32_t* y, int64_t t);
 void malus_gpt_graph_free(void* graph);
 size_t malus_gpt_graph_nodes(void* graph);
+/* No reference counterpart (a checkpoint format is deferred in the
+ * reference, CLAUDE.md:70): the model's parameters and AdamW moments as a
+ * SafeTensors file, with the step in its metadata.  save returns 0; load
+ * checks names, dtypes and shapes against the model and returns the step
+ * (both -1 in return-error mode). */
+int malus_gpt_save(void* gpt, const char* path, int64_t step);
+int64_t malus_gpt_load(void* gpt, const char* path);
 float malus_xor_run(int steps, float lr, uint64_t sigmoid_backward_id, float* loss_at, float* preds,
                     float* params); /* examples/xor.ml */
 

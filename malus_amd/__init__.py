@@ -185,6 +185,10 @@ SIGNATURES = {
     "malus_gpt_graph_step": (_i64, [_vp, _P(_i32), _P(_i32), _i64]),
     "malus_gpt_graph_free": (None, [_vp]),
     "malus_gpt_graph_nodes": (_sz, [_vp]),
+    "malus_gpt_save": (C.c_int, [_vp, C.c_char_p, _i64]),
+    "malus_gpt_load": (_i64, [_vp, C.c_char_p]),
+    "malus_randn_device": (_i64, [_P(_sz), _sz]),
+    "malus_batch_windows": (None, [_i64, _i64, _i64, _P(_i64), _P(_i64), _P(C.c_int32)]),
     "malus_std_reduce_noalloc": (C.c_int, [_i32, _vp, _P(_sz), _sz, _i64, _vp]),
     "malus_compile_kernels": (_vp, [C.c_char_p, _P(C.c_char_p), _sz, C.c_int]),
     "malus_registry_len": (_sz, [_vp]),

@@ -108,6 +108,13 @@ uint64_t rng_next_call();
 
 // ---- kernel launch wrappers (k_*.hip) --------------------------------------
 namespace k {
+// k_rng.hip: Philox4x32-10 on the device (the host generator's words).
+// randn: Box-Muller of pair k (counter [k, 0, 0, 0], key = call) in f64.
+void randn(float* out, size_t n, uint64_t call, hipStream_t s);
+// batch_windows: B sequences of T tokens at starts rand_int(range) drawn with
+// call indices call0 .. call0 + B - 1; y is x shifted by one token.
+void batch_windows(const int32_t* data, int32_t* x, int32_t* y, size_t B, size_t T, uint64_t call0, uint64_t range,
+                   int32_t* starts, hipStream_t s);
 enum BinOp : int { ADD = 0, SUB = 1, MUL = 2, DIV = 3 };
 enum UnOp : int { RELU = 0, SIGMOID, TANH, EXP, LOG, SQRT, ABS, GELU, NEG_UNUSED };
 enum UnBwd : int { B_SIGMOID = 0, B_RELU, B_TANH, B_SQRT, B_ABS, B_GELU, B_EXP, B_LOG };

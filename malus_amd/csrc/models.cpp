@@ -782,4 +782,220 @@ size_t malus_gpt_graph_nodes(void* gh) {
   return n;
 }
 
+// ---- checkpoints (SafeTensors) ------------------------------------------------
+// The model's parameters and AdamW moments in the SafeTensors layout: an
+// 8-byte little-endian header length, a JSON header (name -> dtype, shape,
+// data_offsets; "__metadata__" holds the step and the configuration), then
+// the raw little-endian f32 data in header order.  Names follow the program's
+// structure: blocks.<l>.{ln1_w,wq,wk,wv,wo,ln2_w,w1,w2}, wte, wpe, ln_f,
+// lm_head, and adam_m.<name> / adam_v.<name> for the moments.
+
+}  // extern "C"
+
+namespace {
+
+const char* const kBlockNames[8] = {"ln1_w", "wq", "wk", "wv", "wo", "ln2_w", "w1", "w2"};
+const char* const kTopNames[4] = {"wte", "wpe", "ln_f", "lm_head"};
+
+std::string param_name(const Gpt& g, int i) {
+  if (i < 8 * g.L) return "blocks." + std::to_string(i / 8) + "." + kBlockNames[i % 8];
+  return kTopNames[i - 8 * g.L];
+}
+
+// A minimal JSON reader for SafeTensors headers: objects, arrays, strings,
+// integers (the values a header holds).
+struct Json {
+  enum K { Null, Num, Str, Arr, Obj } k = Null;
+  long long num = 0;
+  std::string str;
+  std::vector<Json> arr;
+  std::vector<std::pair<std::string, Json>> obj;
+  const Json* get(const std::string& key) const {
+    for (auto& kv : obj)
+      if (kv.first == key) return &kv.second;
+    return nullptr;
+  }
+};
+
+struct JsonParser {
+  const std::string& s;
+  size_t p = 0;
+  [[noreturn]] void bad() { fail("malus: checkpoint header is not valid JSON (at byte %zu)", p); }
+  void ws() { while (p < s.size() && isspace((unsigned char)s[p])) ++p; }
+  Json value() {
+    ws();
+    if (p >= s.size()) bad();
+    Json j;
+    if (s[p] == '{') {
+      j.k = Json::Obj;
+      ++p;
+      ws();
+      if (p < s.size() && s[p] == '}') { ++p; return j; }
+      while (true) {
+        ws();
+        Json key = value();
+        if (key.k != Json::Str) bad();
+        ws();
+        if (p >= s.size() || s[p] != ':') bad();
+        ++p;
+        j.obj.emplace_back(key.str, value());
+        ws();
+        if (p < s.size() && s[p] == ',') { ++p; continue; }
+        if (p < s.size() && s[p] == '}') { ++p; return j; }
+        bad();
+      }
+    }
+    if (s[p] == '[') {
+      j.k = Json::Arr;
+      ++p;
+      ws();
+      if (p < s.size() && s[p] == ']') { ++p; return j; }
+      while (true) {
+        j.arr.push_back(value());
+        ws();
+        if (p < s.size() && s[p] == ',') { ++p; continue; }
+        if (p < s.size() && s[p] == ']') { ++p; return j; }
+        bad();
+      }
+    }
+    if (s[p] == '"') {
+      j.k = Json::Str;
+      ++p;
+      while (p < s.size() && s[p] != '"') {
+        if (s[p] == '\\' && p + 1 < s.size()) ++p;
+        j.str += s[p++];
+      }
+      if (p >= s.size()) bad();
+      ++p;
+      return j;
+    }
+    if (s[p] == '-' || isdigit((unsigned char)s[p])) {
+      j.k = Json::Num;
+      size_t e = p + 1;
+      while (e < s.size() && (isdigit((unsigned char)s[e]) || s[e] == '.' || s[e] == 'e' || s[e] == 'E' ||
+                              s[e] == '+' || s[e] == '-'))
+        ++e;
+      j.num = strtoll(s.c_str() + p, nullptr, 10);
+      p = e;
+      return j;
+    }
+    if (s.compare(p, 4, "null") == 0) { p += 4; return j; }
+    if (s.compare(p, 4, "true") == 0) { p += 4; j.k = Json::Num; j.num = 1; return j; }
+    if (s.compare(p, 5, "false") == 0) { p += 5; j.k = Json::Num; return j; }
+    bad();
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+// Writes the model (parameters and moments) and `step` to `path`.
+// Returns 0, or -1 in return-error mode.
+int malus_gpt_save(void* gp, const char* path, int64_t step) {
+  API_TRY
+  auto* g = static_cast<Gpt*>(gp);
+  if (!g || !path) fail("malus: gpt_save: null model or path");
+  struct Item { std::string name; int64_t h; };
+  std::vector<Item> items;
+  for (int i = 0; i < g->np(); ++i) items.push_back({param_name(*g, i), g->p[(size_t)i]});
+  for (int i = 0; i < g->np(); ++i) items.push_back({"adam_m." + param_name(*g, i), g->m[(size_t)i]});
+  for (int i = 0; i < g->np(); ++i) items.push_back({"adam_v." + param_name(*g, i), g->v[(size_t)i]});
+  std::string hdr = "{\"__metadata__\":{\"format\":\"malus\",\"step\":\"" + std::to_string(step) + "\",\"config\":\"V=" +
+                    std::to_string(g->V) + ",T=" + std::to_string(g->Tn) + ",C=" + std::to_string(g->C) + ",H=" +
+                    std::to_string(g->H) + ",L=" + std::to_string(g->L) + "\"}";
+  size_t off = 0;
+  for (auto& it : items) {
+    TensorBuffer* t = T(it.h);
+    hdr += ",\"" + it.name + "\":{\"dtype\":\"F32\",\"shape\":[";
+    for (int d = 0; d < t->ndim; ++d) hdr += (d ? "," : "") + std::to_string(t->shape[d]);
+    hdr += "],\"data_offsets\":[" + std::to_string(off) + "," + std::to_string(off + t->bytes()) + "]}";
+    off += t->bytes();
+  }
+  hdr += "}";
+  while (hdr.size() % 8) hdr += ' ';
+  FILE* f = fopen(path, "wb");
+  if (!f) fail("malus: gpt_save: cannot open %s for writing", path);
+  uint64_t n = hdr.size();
+  unsigned char len[8];
+  for (int b = 0; b < 8; ++b) len[b] = (unsigned char)(n >> (8 * b));
+  bool ok = fwrite(len, 1, 8, f) == 8 && fwrite(hdr.data(), 1, hdr.size(), f) == hdr.size();
+  std::vector<char> buf;
+  for (auto& it : items) {
+    TensorBuffer* t = T(it.h);
+    buf.resize(t->bytes());
+    download(buf.data(), t, t->bytes());
+    ok = ok && fwrite(buf.data(), 1, buf.size(), f) == buf.size();
+  }
+  ok = (fclose(f) == 0) && ok;
+  if (!ok) fail("malus: gpt_save: write to %s failed", path);
+  return 0;
+  API_CATCH(-1)
+}
+
+// Reads parameters and moments from `path` into the model (names, dtypes and
+// shapes must match) and returns the stored step (-1 in return-error mode).
+int64_t malus_gpt_load(void* gp, const char* path) {
+  API_TRY
+  auto* g = static_cast<Gpt*>(gp);
+  if (!g || !path) fail("malus: gpt_load: null model or path");
+  FILE* f = fopen(path, "rb");
+  if (!f) fail("malus: gpt_load: cannot open %s", path);
+  unsigned char len[8];
+  if (fread(len, 1, 8, f) != 8) { fclose(f); fail("malus: gpt_load: %s is too short", path); }
+  uint64_t n = 0;
+  for (int b = 0; b < 8; ++b) n |= (uint64_t)len[b] << (8 * b);
+  if (n > (uint64_t)1 << 30) { fclose(f); fail("malus: gpt_load: header of %llu bytes", (unsigned long long)n); }
+  std::string hdr(n, '\0');
+  if (fread(&hdr[0], 1, n, f) != n) { fclose(f); fail("malus: gpt_load: truncated header in %s", path); }
+  fseek(f, 0, SEEK_END);
+  const long total = ftell(f);
+  const uint64_t data0 = 8 + n;
+  Json root;
+  try {
+    JsonParser jp{hdr};
+    root = jp.value();
+  } catch (...) {
+    fclose(f);
+    throw;
+  }
+  auto load_one = [&](const std::string& name, int64_t h) {
+    const Json* e = root.get(name);
+    if (!e) fail("malus: gpt_load: %s has no tensor named %s", path, name.c_str());
+    const Json* dt = e->get("dtype");
+    const Json* sh = e->get("shape");
+    const Json* of = e->get("data_offsets");
+    if (!dt || dt->str != "F32") fail("malus: gpt_load: %s is not F32", name.c_str());
+    TensorBuffer* t = T(h);
+    if (!sh || sh->k != Json::Arr || (int)sh->arr.size() != t->ndim) fail("malus: gpt_load: %s has the wrong rank", name.c_str());
+    for (int d = 0; d < t->ndim; ++d)
+      if ((size_t)sh->arr[(size_t)d].num != t->shape[d])
+        fail("malus: gpt_load: %s has shape mismatching the model's %s", name.c_str(), shape_str(t).c_str());
+    if (!of || of->arr.size() != 2 || (uint64_t)(of->arr[1].num - of->arr[0].num) != t->bytes() ||
+        data0 + (uint64_t)of->arr[1].num > (uint64_t)total)
+      fail("malus: gpt_load: %s has bad data offsets", name.c_str());
+    std::vector<char> buf(t->bytes());
+    fseek(f, (long)(data0 + (uint64_t)of->arr[0].num), SEEK_SET);
+    if (fread(buf.data(), 1, buf.size(), f) != buf.size()) fail("malus: gpt_load: short read of %s", name.c_str());
+    upload(t->data(), buf.data(), buf.size());
+    t->write_seq = enqueue_mark("checkpoint load");
+  };
+  try {
+    for (int i = 0; i < g->np(); ++i) {
+      load_one(param_name(*g, i), g->p[(size_t)i]);
+      load_one("adam_m." + param_name(*g, i), g->m[(size_t)i]);
+      load_one("adam_v." + param_name(*g, i), g->v[(size_t)i]);
+    }
+  } catch (...) {
+    fclose(f);
+    throw;
+  }
+  fclose(f);
+  int64_t step = 0;
+  if (const Json* md = root.get("__metadata__"))
+    if (const Json* st = md->get("step")) step = strtoll(st->str.c_str(), nullptr, 10);
+  return step;
+  API_CATCH(-1)
+}
+
 }  // extern "C"

@@ -755,6 +755,51 @@ int64_t malus_rand_int(int64_t n) {
   API_CATCH(0)
 }
 
+// ---- the device-side data path (no reference counterpart) ------------------
+// randn with the reference's stream (metal.rs:1720-1740), generated on the
+// device: the same Philox words; the same f64 Box-Muller.
+int64_t malus_randn_device(const size_t* shape, size_t ndim) {
+  API_TRY
+  TensorBuffer* t = alloc_tensor(F32, shape, (int)ndim);
+  const uint64_t call = rng_next_call();
+  k::randn(t->f32(), t->len, call, stream());
+  t->write_seq = enqueue_mark("randn_device");
+  return H(t);
+  API_CATCH(0)
+}
+
+// The batch of nanogpt_modular.ml:170-177 built on the device from a
+// device-resident i32 token stream `data`: for b in 0..B, start =
+// rand_int(len(data) - T - 1) (one RNG call each, as the host loop makes
+// them), x[b*T + t] = data[start + t], y[b*T + t] = data[start + t + 1].
+// x and y are new [B*T] i32 tensors.  starts_out (optional, host int32[B])
+// receives the starts, which costs a device read.
+void malus_batch_windows(int64_t data, int64_t B, int64_t Tn, int64_t* x_out, int64_t* y_out, int32_t* starts_out) {
+  API_TRY
+  TensorBuffer* d = T(data);
+  if (d->dtype != I32 || d->ndim != 1) fail("malus: batch_windows: data must be a 1-D i32 tensor, got %s", shape_str(d).c_str());
+  if (B <= 0 || Tn <= 0 || B > 65535) fail("malus: batch_windows: bad batch %lld x %lld", (long long)B, (long long)Tn);
+  if ((int64_t)d->len < Tn + 2) fail("malus: batch_windows: %zu tokens cannot hold a window of %lld + 1", d->len, (long long)Tn);
+  if (!x_out || !y_out) fail("malus: batch_windows: null output");
+  const uint64_t range = (uint64_t)(d->len - (size_t)Tn - 1);
+  const uint64_t call0 = t_rng_calls;
+  t_rng_calls += (uint64_t)B;
+  const size_t sh[1] = {(size_t)(B * Tn)};
+  TensorBuffer *x = alloc_tensor(I32, sh, 1), *y = alloc_tensor(I32, sh, 1);
+  size_t bucket = 0;
+  int32_t* starts = starts_out ? static_cast<int32_t*>(pool_alloc((size_t)B * sizeof(int32_t), &bucket)) : nullptr;
+  k::batch_windows(d->i32(), x->i32(), y->i32(), (size_t)B, (size_t)Tn, call0, range, starts, stream());
+  x->write_seq = y->write_seq = enqueue_mark("batch_windows");
+  if (starts) {
+    MALUS_HIP(hipMemcpyAsync(starts_out, starts, (size_t)B * sizeof(int32_t), hipMemcpyDeviceToHost, stream()));
+    MALUS_HIP(hipStreamSynchronize(stream()));
+    pool_free(starts, bucket);
+  }
+  *x_out = H(x);
+  *y_out = H(y);
+  API_CATCH()
+}
+
 uint64_t malus_rng_get_counter(void) { return t_rng_calls; }
 void malus_rng_set_counter(uint64_t v) { t_rng_calls = v; }
 
