@@ -32,6 +32,7 @@ CFG = CONFIGS["c5"]
 OPT = dict(lr=1e-3, b1=0.9, b2=0.99, eps=1e-8, wd=0.1)
 METRIC = "warm-median ms/step, char-nanoGPT f32 train step; HBM GB/s & MFMA % of peak"
 PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_BF16_MFMA_TFLOPS = 2500.0  # dense bf16 MFMA (no sparsity)
 PEAK_HBM_GBS = 8000.0
 
 
@@ -320,6 +321,8 @@ def run_gpt(rt, a, cfg):
     L.malus_rng_set_counter(0)
     g = L.malus_gpt_create(cfg["V"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["B"], OPT["lr"], OPT["b1"],
                            OPT["b2"], OPT["eps"], OPT["wd"])
+    # docs/adr/0037-bf16-autocast.md:5-12: the whole step inside `with autocast:`
+    L.malus_autocast(1 if a.autocast else 0)
     n = cfg["B"] * cfg["T"]
     rng = np.random.default_rng(2024)
     gemm_steps = min(a.steps, 20)
@@ -410,9 +413,11 @@ def run_gpt(rt, a, cfg):
         except Exception as e:  # the CPU leg is a reported baseline only
             log(f"cpu baseline failed: {e!r}")
     L.malus_gpt_free(g)
+    L.malus_autocast(0)
 
     c5 = cfg == CONFIGS["c5"]
-    traffic = measured_traffic() if c5 else None
+    traffic = measured_traffic() if c5 and not a.autocast else None
+    peak = PEAK_BF16_MFMA_TFLOPS if a.autocast else PEAK_FP32_MFMA_TFLOPS
     tag = "C5 Karpathy" if c5 else "C4 toy"
     return {
         "metric": METRIC,
@@ -425,7 +430,7 @@ def run_gpt(rt, a, cfg):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16 GEMM operands, f32 accumulation and everything else f32 (autocast)" if a.autocast else "f32",
         "data": "synthetic int32 tokens i.i.d. uniform in [0,65) (seed 2024), uploaded inside each timed step; "
                 "weights randn*0.02 (Philox, call 0)",
         "execution": ("hipGraph replay of the captured step (token/target ids and AdamW bias corrections copied from "
@@ -435,8 +440,8 @@ def run_gpt(rt, a, cfg):
                    "block_size": cfg["T"], "n_embd": cfg["C"], "n_head": cfg["H"], "n_layer": cfg["L"],
                    "batch": cfg["B"], "tokens_per_step": n, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "k_sgemm (all GEMM launches of the step)",
-                     "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic,
+                     "achieved": round(gemm_tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(gemm_tflops / peak, 4), "traffic": traffic,
                      "traffic_unit": "HBM bytes per step, all GEMM launches (rocprofv3 FETCH_SIZE+WRITE_SIZE)",
                      "algorithmic_bytes": gemm_bytes_per_step(cfg),
                      "timing": f"HIP events around each GEMM launch over {gemm_steps} steps run after the "
@@ -456,6 +461,9 @@ def main():
                     help="c5 (default): Karpathy char-nanoGPT; c4: toy char-nanoGPT; c1: XOR MLP, 10,000 steps")
     ap.add_argument("--graph", action="store_true",
                     help="time the step as a replayed hipGraph (malus_gpt_graph_*) instead of eager launches")
+    ap.add_argument("--autocast", action="store_true",
+                    help="run the step in the bf16 autocast scope (bf16 GEMMs, f32 accumulation, f32 master state); "
+                         "reported alongside the f32 headline, never in its place")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",

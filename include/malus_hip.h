@@ -208,6 +208,14 @@ int malus_gemm_set_tile(int tm, int tn);
 void malus_gemm_set_split(int target_blocks);
 /* Tuning: 0 keeps every GEMM on the register-staged path; 1 (default) allows the LDS-DMA path. */
 void malus_gemm_set_dma(int on);
+/* The `with autocast:` scope of docs/adr/0037-bf16-autocast.md:5-12 (the
+ * reference fixes the policy, not yet an entry point): while on, every GEMM
+ * (tensor_matmul, the model's projections and their VJPs) rounds its f32
+ * operands to bf16 (nearest even) and accumulates in f32 on the bf16 MFMA;
+ * tensors, parameters, gradients, optimizer state, reductions and the fused
+ * attention stay f32.  Returns the previous state, which the scope's exit
+ * passes back.  A captured step keeps the precision it was captured with. */
+int malus_autocast(int on);
 /* Fused attention scores softmax(q @ k^T * scale + mask, axis=2) for q, k
  * [bh, t, hs] (t, hs in {256,64}, {128,64}, {64,32}, {64,64}); the kernel the
  * model's fused forward uses for nanogpt_modular.ml:57-61.  causal != 0

@@ -115,6 +115,7 @@ SIGNATURES = {
     "malus_gemm_set_tile": (C.c_int, [C.c_int, C.c_int]),
     "malus_gemm_set_split": (None, [C.c_int]),
     "malus_gemm_set_dma": (None, [C.c_int]),
+    "malus_autocast": (C.c_int, [C.c_int]),
     "malus_std_attn_scores_softmax": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "malus_std_attn_scores_bwd": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "malus_std_attn_fwd": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32, _P(_i64)]),
@@ -306,6 +307,24 @@ def compile_kernels(program: str, builtins=(), tags: bool = False) -> KernelRegi
     finally:
         L.malus_registry_free(r)
     return KernelRegistry(entries)
+
+
+class autocast:
+    """`with autocast():` -- the scope of docs/adr/0037-bf16-autocast.md:5-12
+    over malus_autocast: GEMMs in bf16 with f32 accumulation inside the
+    block, the previous state restored on exit (nested blocks compose)."""
+
+    def __init__(self, enabled: bool = True):
+        self.enabled = enabled
+        self._prev = 0
+
+    def __enter__(self):
+        self._prev = lib().malus_autocast(1 if self.enabled else 0)
+        return self
+
+    def __exit__(self, *exc):
+        lib().malus_autocast(self._prev)
+        return False
 
 
 def device_count_hint() -> int:

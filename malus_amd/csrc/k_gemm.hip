@@ -36,8 +36,42 @@ namespace k {
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int BK = 16;
+
+// The MFMA work of one 16-deep K step from each lane's 8 fragment values
+// (k = 8h + s for lane half h, the same k slots in A and B): eight FP32
+// 32x32x2 steps, or under autocast (BF) one 32x32x16 bf16 MFMA over the same
+// 16 k values, with both operands rounded to bf16 (round to nearest even,
+// v_cvt_pk_bf16_f32).  A bf16 product is exact in f32, so BF differs from
+// the f32 product only in the operands' rounding and the order of the f32
+// accumulation.
+template <int TM, int TN, bool BF>
+__device__ __forceinline__ void mfma_kstep(const float (&fa)[TM][8], const float (&fb)[TN][8], v16f (&acc)[TM][TN]) {
+  if constexpr (BF) {
+    bf16x8 a[TM], b[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[i][e] = (__bf16)fa[i][e];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) b[j][e] = (__bf16)fb[j][e];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st], fb[j][st], acc[i][j], 0, 0, 0);
+  }
+}
 
 // One operand's tile: BX rows of its free dimension x (m for A, n for B) by
 // BK of k, staged in LDS in the operand's global orientation, so staging
@@ -128,7 +162,7 @@ struct Tile {
 
 // grid: x = output tiles (XCD-remapped), y = K splits, z = batch.
 // Split s writes its partial tile to C + s * split_stride.
-template <int TM, int TN, bool TA, bool TB, bool VA, bool VB>
+template <int TM, int TN, bool TA, bool TB, bool VA, bool VB, bool BF = false>
 __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, const float* __restrict__ B,
                                                   float* __restrict__ C, int M, int N, int K, long sA, long sB, long sC,
                                                   int k_chunk, int tiles_n, long split_stride,
@@ -186,12 +220,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
 #pragma unroll
     for (int j = 0; j < TN; ++j) TileB::frag(Bs[cur], wn + 32 * j, fb[j]);
     __builtin_amdgcn_sched_barrier(0);  // keep every fragment read ahead of the MFMA chain
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+    mfma_kstep<TM, TN, BF>(fa, fb, acc);
     if (more) {
       la.store(As[cur ^ 1]);
       lb.store(Bs[cur ^ 1]);
@@ -349,7 +378,7 @@ struct DmaSlab {
 // its add (the rounding of one GEMM per group with its addend chained).
 // E shares C's layout.  Grouped launches (L.ngroup > 1, MAP only): with
 // EPI != 3, workgroup z runs group z (its own A, B, C); the batch index is 0.
-template <int TM, int TN, bool TA, bool TB, bool MAP, int EPI = 0>
+template <int TM, int TN, bool TA, bool TB, bool MAP, int EPI = 0, bool BF = false>
 __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int M, int N, int K, GemmLayouts L,
                                                       int k_chunk, int tiles_n, long split_stride,
@@ -447,13 +476,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
       // a wave with MFMAs to issue goes ahead of the CU's other waves (measured
       // 1 % on the C5 step; raising it from the barrier on instead lost 2 %)
       __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int s = 0; s < 8; ++s)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+      mfma_kstep<TM, TN, BF>(fa, fb, acc);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       cur = cur == NS - 1 ? 0 : cur + 1;
@@ -579,54 +602,62 @@ struct TileCfg { int tm, tn; };
 constexpr TileCfg kTiles[] = {{2, 3}, {2, 2}, {2, 1}, {1, 2}, {1, 1}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-// Variant code: bit 4 = LDS-DMA path, bits 3..0 = transA, transB, vecA, vecB.
+// Variant code: bit 8 = bf16 MFMA (autocast), bit 7 = grouped accumulation,
+// bit 6 = GELU epilogues, bit 5 = mapped operands, bit 4 = LDS-DMA path,
+// bits 3..0 = transA, transB, vecA, vecB.
+constexpr int kVarBf16 = 256;
 inline int variant(bool ta, bool tb, bool va, bool vb, bool dma) {
   return (dma << 4) | (ta << 3) | (tb << 2) | (va << 1) | (int)vb;
 }
 
-template <int TM, int TN, bool TA, bool TB>
+template <int TM, int TN, bool TA, bool TB, bool BF>
 const void* kernel_of(int v) {
   if (v & 128) {  // grouped accumulation: mapped NT (the head projections' dA)
-    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, true, 3>);
+    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, true, 3, BF>);
     return nullptr;
   }
   if (v & 64) {  // GELU epilogues: dense NN (forward) and NT (the VJP's dA)
-    if constexpr (!TA && !TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, false, false, 1>);
-    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, false, 2>);
+    if constexpr (!TA && !TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, false, false, 1, BF>);
+    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, false, 2, BF>);
     return nullptr;
   }
-  if (v & 32) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, true>);
-  if (v & 16) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, false>);
+  if (v & 32) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, true, 0, BF>);
+  if (v & 16) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, false, 0, BF>);
   const bool va = v & 2, vb = v & 1;
-  if (va && vb) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, true>);
-  if (va) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, false>);
-  if (vb) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, false, true>);
-  return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, false, false>);
+  if (va && vb) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, true, BF>);
+  if (va) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, false, BF>);
+  if (vb) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, false, true, BF>);
+  return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, false, false, BF>);
 }
 
-template <int TM, int TN>
+template <int TM, int TN, bool BF>
 const void* kernel_of_layout(int v) {
   const bool ta = v & 8, tb = v & 4;
-  if (!ta && !tb) return kernel_of<TM, TN, false, false>(v);
-  if (!ta && tb) return kernel_of<TM, TN, false, true>(v);
-  if (ta && !tb) return kernel_of<TM, TN, true, false>(v);
-  return kernel_of<TM, TN, true, true>(v);
+  if (!ta && !tb) return kernel_of<TM, TN, false, false, BF>(v);
+  if (!ta && tb) return kernel_of<TM, TN, false, true, BF>(v);
+  if (ta && !tb) return kernel_of<TM, TN, true, false, BF>(v);
+  return kernel_of<TM, TN, true, true, BF>(v);
+}
+
+template <bool BF>
+const void* kernel_for_prec(int ti, int v) {
+  switch (ti) {
+    case 0: return kernel_of_layout<2, 3, BF>(v);
+    case 1: return kernel_of_layout<2, 2, BF>(v);
+    case 2: return kernel_of_layout<2, 1, BF>(v);
+    case 3: return kernel_of_layout<1, 2, BF>(v);
+    default: return kernel_of_layout<1, 1, BF>(v);
+  }
 }
 
 const void* kernel_for(int ti, int v) {
-  switch (ti) {
-    case 0: return kernel_of_layout<2, 3>(v);
-    case 1: return kernel_of_layout<2, 2>(v);
-    case 2: return kernel_of_layout<2, 1>(v);
-    case 3: return kernel_of_layout<1, 2>(v);
-    default: return kernel_of_layout<1, 1>(v);
-  }
+  return (v & kVarBf16) ? kernel_for_prec<true>(ti, v) : kernel_for_prec<false>(ti, v);
 }
 
 // Co-resident workgroups per CU of each kernel variant (VGPR and LDS
 // limited), from the runtime's occupancy calculator; cached per variant.
 int occupancy(int ti, int v) {
-  static int cache[kNumTiles][256];
+  static int cache[kNumTiles][512];
   int& o = cache[ti][v];
   if (o == 0) {
     int n = 0;
@@ -654,6 +685,7 @@ inline double cu_util(int conc) { return conc <= 1 ? 0.75 : conc == 2 ? 0.92 : 1
 struct Plan { int ti, nsplit, k_chunk; };
 
 int g_forced_tile = -2;    // -2: read MALUS_GEMM_TILE once; -1: automatic
+bool g_autocast = false;   // GEMM products in bf16 with f32 accumulation (autocast scope)
 int g_split_target = 0;    // workgroups a split-K launch aims for; 0: model
 bool g_allow_dma = true;   // LDS-DMA path where the shape allows it
 
@@ -779,7 +811,8 @@ double launch_dma(const float* A, const float* B, float* C, int batch, int M, in
   long split_stride = nsplit > 1 ? (long)mn : 0;
   const float* Dk = nsplit > 1 ? nullptr : D;  // split-K applies the addend in the reduction
   void* args[] = {&A, &B, &dst, &M, &N, &K, &L, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk, &E};
-  const void* fn = kernel_for(p.ti, epi ? v | 64 : mapped ? v | 32 : v);
+  const int vb = (epi ? v | 64 : mapped ? v | 32 : v) | (g_autocast ? kVarBf16 : 0);
+  const void* fn = kernel_for(p.ti, vb);
   if (!fn) fail("malus: gemm: no kernel for epilogue %d with transA=%d transB=%d", epi, transA, transB);
   MALUS_HIP(hipLaunchKernel(fn, dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch), dim3(256), args, 0, s));
   if (nsplit > 1) split_reduce(dst, C, mn, nsplit, D, s, bucket);
@@ -841,8 +874,8 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
   long split_stride = nsplit > 1 ? (long)mn : 0;
   const float* Dk = nsplit > 1 ? nullptr : D;  // split-K applies the addend in the reduction
   void* args[] = {&A, &B, &dst, &M, &N, &K, &sA, &sB, &sC, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk};
-  MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, v), dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch),
-                            dim3(256), args, 0, s));
+  MALUS_HIP(hipLaunchKernel(kernel_for(p.ti, v | (g_autocast ? kVarBf16 : 0)),
+                            dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch), dim3(256), args, 0, s));
   if (nsplit > 1) split_reduce(dst, C, mn, nsplit, D, s, bucket);
 }
 
@@ -912,7 +945,7 @@ bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayou
   float* Cp = accumulate ? C : L.gc[0];
   const float *A0 = L.ga[0], *B0 = L.gb[0];
   void* args[] = {&A0, &B0, &Cp, &M, &N, &K, &L, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk, &E};
-  const void* fn = kernel_for(p.ti, accumulate ? v | 128 : v | 32);
+  const void* fn = kernel_for(p.ti, (accumulate ? v | 128 : v | 32) | (g_autocast ? kVarBf16 : 0));
   if (!fn) fail("malus: gemm_grouped: no kernel for transA=%d transB=%d", transA, transB);
   MALUS_HIP(hipLaunchKernel(fn, dim3((unsigned)tiles, (unsigned)nsplit, accumulate ? 1u : (unsigned)L.ngroup), dim3(256),
                             args, 0, s));
@@ -983,6 +1016,17 @@ extern "C" int malus_gemm_set_tile(int tm, int tn) {
   for (int i = 0; i < kNumTiles; ++i)
     if (kTiles[i].tm == tm && kTiles[i].tn == tn) { g_forced_tile = i; return 1; }
   return 0;
+}
+
+// The autocast scope (docs/adr/0037-bf16-autocast.md:5-12: matmuls in bf16
+// with f32 accumulation; parameters, gradients, optimizer state and
+// reductions stay f32): while on, every GEMM launch rounds its operands to
+// bf16 and runs the bf16 MFMA.  A `with autocast:` block turns it on at entry
+// and restores the returned previous state at exit.
+extern "C" int malus_autocast(int on) {
+  const bool prev = malus::k::g_autocast;
+  malus::k::g_autocast = on != 0;
+  return prev ? 1 : 0;
 }
 
 // Tuning knob: 0 keeps every GEMM on the register-staged path (for A/B

@@ -240,6 +240,16 @@ def matmul(a, b):
     return out
 
 
+def bf16_round(a):
+    """f32 -> nearest bf16 (ties to even), returned as f32: the operand
+    rounding of the autocast matmul policy (docs/adr/0037-bf16-autocast.md:5-12,
+    "matmuls ... compute in bfloat").  bf16 keeps the top 16 bits of the f32
+    pattern; finite inputs only."""
+    u = f32(a).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return r.astype(np.uint32).view(np.float32)
+
+
 def sum_to_shape(g, target_shape):
     g = f32(g)
     out = np.empty(target_shape, np.float32)

@@ -157,6 +157,28 @@ def test_matmul_within_sequential_error_bound():
     assert np.allclose(O.matmul(A, B[0]), A.astype(np.float64) @ B[0], rtol=1e-5, atol=1e-6)
 
 
+def test_bf16_round_is_torchs_bfloat16_conversion():
+    # torch's f32 -> bfloat16 conversion rounds to nearest, ties to even
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 100000),
+                        np.array([0.0, -0.0, 1.0, -2.5, 3e38, -3e38, 1e-40, 65504.0], np.float32)])
+    # exact ties: the dropped 16 bits are 0x8000, with an even and an odd kept part
+    tie_even = (np.arange(1000, dtype=np.uint32) * 2 << 16 | 0x8000) + 0x3F800000
+    tie_odd = tie_even + 0x10000
+    x = np.concatenate([x, tie_even.view(np.float32), tie_odd.view(np.float32), -tie_odd.view(np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    got = O.bf16_round(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # ties went to the even kept part: down for even, up for odd
+    assert np.array_equal(O.bf16_round(tie_even.view(np.float32)).view(np.uint32), tie_even & 0xFFFF0000)
+    assert np.array_equal(O.bf16_round(tie_odd.view(np.float32)).view(np.uint32), (tie_odd & 0xFFFF0000) + 0x10000)
+    # idempotent, and within half a bf16 ulp (2^-9 relative)
+    assert np.array_equal(O.bf16_round(got), got)
+    nz = np.abs(x) > 1e-30
+    assert np.all(np.abs(got[nz] - x[nz]) <= np.abs(x[nz]) * 2.0 ** -8)
+
+
 def test_reductions_within_bound_and_shapes():
     x = r(13, 1000, 3)
     for axis in range(3):
