@@ -34,6 +34,7 @@ METRIC = "warm-median ms/step, char-nanoGPT f32 train step; HBM GB/s & MFMA % of
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_BF16_MFMA_TFLOPS = 2500.0  # dense bf16 MFMA (no sparsity)
 PEAK_HBM_GBS = 8000.0
+ATTN_MODES = {"auto": 0, "flash": 1, "rows": 2, "composed": 3}
 
 
 def log(*a):
@@ -321,6 +322,7 @@ def run_gpt(rt, a, cfg):
     L.malus_rng_set_counter(0)
     g = L.malus_gpt_create(cfg["V"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["B"], OPT["lr"], OPT["b1"],
                            OPT["b2"], OPT["eps"], OPT["wd"])
+    L.malus_gpt_set_attention(g, ATTN_MODES[a.attention])
     # docs/adr/0037-bf16-autocast.md:5-12: the whole step inside `with autocast:`
     L.malus_autocast(1 if a.autocast else 0)
     n = cfg["B"] * cfg["T"]
@@ -433,6 +435,7 @@ def run_gpt(rt, a, cfg):
         "dtype": "bf16 GEMM operands, f32 accumulation and everything else f32 (autocast)" if a.autocast else "f32",
         "data": "synthetic int32 tokens i.i.d. uniform in [0,65) (seed 2024), uploaded inside each timed step; "
                 "weights randn*0.02 (Philox, call 0)",
+        "attention": a.attention,
         "execution": ("hipGraph replay of the captured step (token/target ids and AdamW bias corrections copied from "
                       f"pinned host memory by the graph's nodes; {nodes} nodes)") if a_graph else
                      "eager: every kernel launched from the host each step",
@@ -464,6 +467,9 @@ def main():
     ap.add_argument("--autocast", action="store_true",
                     help="run the step in the bf16 autocast scope (bf16 GEMMs, f32 accumulation, f32 master state); "
                          "reported alongside the f32 headline, never in its place")
+    ap.add_argument("--attention", choices=list(ATTN_MODES), default="auto",
+                    help="attention kernel of the model: auto, flash (online softmax), rows (the row-register "
+                         "fused kernel), composed (matmul + softmax ops)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",

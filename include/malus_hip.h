@@ -245,6 +245,21 @@ int64_t malus_std_attn_bwd(int64_t dout, int64_t v, int64_t p, int64_t scale, in
 int64_t malus_std_attn_bwd_all(int64_t dout, int64_t q, int64_t k, int64_t v, int64_t p, int64_t scale,
                                int32_t causal, int64_t dq_add, int64_t dk_add, int64_t dv_add, int64_t* dq_out,
                                int64_t* dk_out, int64_t* dv_out);
+/* Flash attention (online softmax; docs/adr/0029-composed-attention.md:23-33,
+ * the fused attention the reference reserves): returns softmax(q @ k^T *
+ * scale + causal mask) @ v [bh, t, hs] without forming the [bh, t, t]
+ * scores or probabilities (causal 0: no mask); *lse_out (if non-null)
+ * receives the row log-sum-exp [bh, t] the backward needs.  t is any
+ * multiple of 32, hs 32 or 64; under malus_autocast the products run on
+ * the bf16 MFMA.  No reference counterpart as an entry point: the reference
+ * composes the same value from matmul and softmax (nanogpt_modular.ml:57-62). */
+int64_t malus_std_flash_attn_fwd(int64_t q, int64_t k, int64_t v, int64_t scale, int32_t causal, int64_t* lse_out);
+/* Its VJP: dq = dq_add + ..., dk = dk_add + ..., dv = dv_add + ... (the
+ * addends may be 0) from dout [bh, t, hs], the forward's inputs, output and
+ * lse; P is recomputed.  Returns 0, or -1 with the error set. */
+int32_t malus_std_flash_attn_bwd(int64_t dout, int64_t q, int64_t k, int64_t v, int64_t out, int64_t lse,
+                                 int64_t scale, int32_t causal, int64_t dq_add, int64_t dk_add, int64_t dv_add,
+                                 int64_t* dq_out, int64_t* dk_out, int64_t* dv_out);
 int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
 int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
 void malus_set_abort_on_error(int on);
@@ -317,6 +332,11 @@ int malus_gpt_nparams(void* g);
 int64_t malus_gpt_param(void* g, int i);              /* borrowed */
 int64_t malus_gpt_moment(void* g, int i, int which);  /* borrowed; which 0 = m, 1 = v */
 void malus_gpt_set_fused_optimizer(void* g, int on);
+/* Attention of the model: 0 automatic (under malus_autocast flash
+ * attention; else the row-register fused kernel where its shapes are built,
+ * else flash, else composed), 1 flash attention, 2 the row-register kernel,
+ * 3 the composed ops.  Returns 0 or -1. */
+int malus_gpt_set_attention(void* gpt, int mode);
 /* 1 (default): forward fusions (attention scale+mask+softmax, residual adds in GEMM epilogues); 0: separate ops (same values and tape). */
 void malus_gpt_set_fused_forward(void* g, int on);
 int64_t malus_gpt_forward_loss(void* g, int64_t toks, int64_t targets); /* nanogpt_modular.ml:75-91 + cross_entropy */

@@ -122,6 +122,9 @@ SIGNATURES = {
     "malus_std_attn_bwd": (_i64, [_i64, _i64, _i64, _i64, _i64, _i32, _P(_i64)]),
     "malus_std_attn_bwd_all": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64, _i64, _i64, _P(_i64), _P(_i64),
                                       _P(_i64)]),
+    "malus_std_flash_attn_fwd": (_i64, [_i64, _i64, _i64, _i64, _i32, _P(_i64)]),
+    "malus_std_flash_attn_bwd": (_i32, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64, _i64, _i64,
+                                             _P(_i64), _P(_i64), _P(_i64)]),
     "malus_ktimer_collect": (_i64, [C.c_char_p, _P(C.c_double), _P(C.c_double)]),
     "malus_device_info": (C.c_int, [C.c_char_p, _sz, _P(C.c_int), _P(C.c_int)]),
     "malus_set_abort_on_error": (None, [C.c_int]),
@@ -174,6 +177,7 @@ SIGNATURES = {
     "malus_gpt_param": (_i64, [_vp, C.c_int]),
     "malus_gpt_moment": (_i64, [_vp, C.c_int, C.c_int]),
     "malus_gpt_set_fused_optimizer": (None, [_vp, C.c_int]),
+    "malus_gpt_set_attention": (C.c_int, [_vp, C.c_int]),
     "malus_gpt_set_fused_forward": (None, [_vp, C.c_int]),
     "malus_tape_set_fused_vjps": (None, [C.c_int]),
     "malus_gpt_forward_loss": (_i64, [_vp, _i64, _i64]),

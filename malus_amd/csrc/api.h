@@ -72,6 +72,10 @@ int64_t attn_bwd_impl(int64_t datt, int64_t v, int64_t p, int64_t scale, int64_t
 void attn_bwd_all_impl(int64_t datt, int64_t q, int64_t k, int64_t v, int64_t p, int64_t scale,
                        const malus::TensorBuffer* Dq, const malus::TensorBuffer* Dk, const malus::TensorBuffer* Dv,
                        int64_t* dq, int64_t* dk, int64_t* dv, size_t B, size_t T, size_t H);
+int64_t flash_fwd_impl(int64_t q, int64_t k, int64_t v, int64_t scale, size_t B, size_t T, size_t H, int64_t* lse_out);
+void flash_bwd_impl(int64_t datt, int64_t q, int64_t k, int64_t v, int64_t o, int64_t lse, int64_t scale,
+                    const malus::TensorBuffer* Dq, const malus::TensorBuffer* Dk, const malus::TensorBuffer* Dv,
+                    int64_t* dq, int64_t* dk, int64_t* dv, size_t B, size_t T, size_t H);
 int64_t scores_bwd_q(int64_t ds, int64_t k, const malus::TensorBuffer* D, bool causal);
 int64_t scores_bwd_k(int64_t ds, int64_t q, const malus::TensorBuffer* D, bool causal);
 

@@ -198,6 +198,29 @@ struct AttnKV {
 bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const float* P, const float* scale, float* dS,
               const float* K, float* dQ, const float* Dq, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s,
               const AttnKV* kv = nullptr);
+// Flash attention (online softmax, no [bh, t, t] buffers): t any multiple
+// of 32, hs 32 or 64.  Forward: O = softmax(Q K^T * scale[0] (+ causal
+// mask)) @ V written at O + (b / heads) * t * ldo + (b % heads) * hs +
+// i * ldo (ldo = heads * hs: the [B*T, C] layout; ldo = hs, heads = 1:
+// dense), and lse[b * t + i] = row max + log(row sum).  bf16: products on
+// the bf16 MFMA (autocast).  False (nothing launched) when the shape or an
+// alignment does not fit.
+bool flash_supported(size_t bh, size_t t, size_t hs);
+bool flash_fwd(const float* Q, const float* K, const float* V, const float* scale, float* O, size_t ldo, size_t heads,
+               float* lse, size_t bh, size_t t, size_t hs, bool causal, bool bf16, hipStream_t s);
+// Backward: dQ = Dq + dS K, dK = Dk + dS^T Q, dV = Dv + P^T dO with P
+// recomputed from lse and dS = P (dP - rowsum(dO O)) scale; O and dO use the
+// forward's O addressing, Q K V dQ dK dV (and the optional addends) are
+// dense [bh, t, hs]; dsum is [bh, t] scratch.
+struct FlashBwd {
+  const float *Q, *K, *V, *O, *dO, *lse, *scale;
+  float *dQ, *dK, *dV, *dsum;
+  const float *Dq, *Dk, *Dv;
+};
+bool flash_bwd(const FlashBwd& a, size_t ldo, size_t heads, size_t bh, size_t t, size_t hs, bool causal, bool bf16,
+               hipStream_t s);
+// The autocast scope's state (GEMMs and flash attention on the bf16 MFMA).
+bool autocast_on();
 // Sum over the axis of x * y (y has x's layout); each product rounded to f32.
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 // The split of reduce_axis_prod's column reduction over [axis, inner]

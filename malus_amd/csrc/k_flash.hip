@@ -1,0 +1,435 @@
+// Flash attention: causal (or unmasked) softmax(Q K^T * scale) @ V with an
+// online softmax (Dao et al.), the post-composed attention that
+// docs/adr/0029-composed-attention.md:23-33 reserves: the [B*H, T, T]
+// scores and probabilities are never written; the forward keeps one f32 per
+// query row (lse = max + log(sum)), and the backward recomputes P from it.
+// T is any multiple of 32 (no softmax-row cap); head sizes 32 and 64.
+//
+// Work split: one wave per (head, 32-row tile); the grid runs the longest
+// tiles first (under a causal mask query tile q meets q + 1 key tiles, key
+// tile k meets NT - k query tiles), so the scheduler balances the CUs with
+// 64-thread workgroups and no LDS.  Operands come straight from L2 into MFMA
+// registers: of each product one operand is held for the whole pass (Q,
+// dO of the query tile; K, V of the key tile) and the other streams.
+//
+// MFMA layout (v_mfma_f32_32x32x2f32, or under autocast one
+// v_mfma_f32_32x32x16_bf16 per 16-deep slab): lane l = x + 32 lk supplies
+// row / column x of its operand; in each 16-deep slab lane half lk supplies
+// the 8 consecutive k values 8 lk .. 8 lk + 7.  The accumulator of lane l
+// holds column x and rows 8 (r >> 2) + 4 lk + (r & 3), r = 0..15.  A row
+// operand loaded through perm_row (bits 2 and 3 of the row swapped) leaves
+// register r holding row perm_index(r, lk) = 16 (r >> 3) + 8 lk + (r & 7):
+// registers 8 h .. 8 h + 7 are then a slab's k values for the next product,
+// so P and dS feed the P V, dS K, dO^T P and Q^T dS products from registers.
+//
+// Backward: dS = P * (dP - D) * scale with D = rowsum(dO * O) (equal to the
+// composed softmax VJP's rowsum(dP * P) in exact arithmetic); dQ from a
+// query-centric pass (S^T, dP^T, dQ += dS K), dK and dV from a key-centric
+// pass (S, dP, dV^T += dO^T P, dK^T += Q^T dS).  Each gradient element is
+// written by one wave: no atomics, and the results are deterministic.
+#include "common.h"
+
+namespace malus {
+namespace k {
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ int perm_row(int x) { return x ^ ((((x >> 2) ^ (x >> 3)) & 1) * 12); }
+__device__ __forceinline__ int perm_index(int r, int lk) { return 16 * (r >> 3) + 8 * lk + (r & 7); }
+
+// One 16-deep slab: acc += A B over the 8 k values of each lane half.
+template <bool BF>
+__device__ __forceinline__ v16f slab(const float (&a)[8], const float (&b)[8], v16f c) {
+  if constexpr (BF) {
+    bf16x8 x, y;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = (__bf16)a[e];
+      y[e] = (__bf16)b[e];
+    }
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, y, c, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], c, 0, 0, 0);
+    return c;
+  }
+}
+
+// 8 consecutive floats (16-byte aligned)
+__device__ __forceinline__ void load8(const float* __restrict__ p, float (&v)[8]) {
+  const v4f a = *reinterpret_cast<const v4f*>(p), b = *reinterpret_cast<const v4f*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = a[e];
+    v[4 + e] = b[e];
+  }
+}
+
+// A head's row `row` of a [B*T, H*HS] tensor (O, dO) or of [B*H, T, HS].
+__device__ __forceinline__ const float* head_row(const float* base, int bh, int H, int T, int ld, int hs, int row) {
+  return base + (size_t)(bh / H) * T * ld + (size_t)(bh % H) * hs + (size_t)row * ld;
+}
+
+// Forward: query tile qt of head bh.  O^T = V^T P^T keeps the output with
+// lane = query, so the online rescale is a per-lane factor.
+template <int HS, bool CAUSAL, bool BF>
+__global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q, const float* __restrict__ K,
+                                                  const float* __restrict__ V, const float* __restrict__ scale,
+                                                  float* __restrict__ O, int ldo, int H, float* __restrict__ lse, int T,
+                                                  int BH) {
+  constexpr int NKB = HS / 16, NN = HS / 32;
+  const int NT = T / 32;
+  const int qt = NT - 1 - (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
+  const int lane = threadIdx.x, x = lane & 31, lk = lane >> 5;
+  const size_t head = (size_t)bh * T * HS;
+  const float *Qh = Q + head, *Kh = K + head, *Vh = V + head;
+  const int i0 = 32 * qt;
+  const float sc = scale[0];
+
+  float qb[NKB][8];  // B of S^T = K Q^T: Q[i0 + x][16 kb + 8 lk + e]
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) load8(Qh + (size_t)(i0 + x) * HS + 16 * kb + 8 * lk, qb[kb]);
+  float ka[NKB][8];  // A of S^T: K[32 j + perm_row(x)][16 kb + 8 lk + e]
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) load8(Kh + (size_t)perm_row(x) * HS + 16 * kb + 8 * lk, ka[kb]);
+
+  v16f o[NN];
+#pragma unroll
+  for (int n = 0; n < NN; ++n) o[n] = v16f{0};
+  float m = -INFINITY, l = 0.0f;
+  const int last = CAUSAL ? qt : NT - 1;
+  for (int j = 0; j <= last; ++j) {
+    float va[NN][2][8];  // A of O^T = V^T P^T: V[32 j + 16 h + 8 lk + e][32 n + x]
+#pragma unroll
+    for (int n = 0; n < NN; ++n)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) va[n][h][e] = Vh[(size_t)(32 * j + 16 * h + 8 * lk + e) * HS + 32 * n + x];
+    v16f st = v16f{0};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) st = slab<BF>(ka[kb], qb[kb], st);
+    if (j < last) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        load8(Kh + (size_t)(32 * (j + 1) + perm_row(x)) * HS + 16 * kb + 8 * lk, ka[kb]);
+    }
+    // lane = query i0 + x, register r = key 32 j + perm_index(r, lk)
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = st[r] * sc;
+      if (CAUSAL && j == qt && perm_index(r, lk) > x) v = -INFINITY;
+      st[r] = v;
+      mt = fmaxf(mt, v);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m, mt);
+    const float alpha = expf(m - mn);  // 0 on the first tile (m = -inf)
+    float ls = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = expf(st[r] - mn);
+      st[r] = p;
+      ls += p;
+    }
+    ls += __shfl_xor(ls, 32, 64);
+    l = l * alpha + ls;
+    m = mn;
+#pragma unroll
+    for (int n = 0; n < NN; ++n) o[n] *= alpha;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float pb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[e] = st[8 * h + e];
+#pragma unroll
+      for (int n = 0; n < NN; ++n) o[n] = slab<BF>(va[n][h], pb, o[n]);
+    }
+  }
+  // O[i0 + x][32 n + 8 g + 4 lk + c] = o[n][4 g + c] / l
+  float* orow = O + (size_t)(bh / H) * T * ldo + (size_t)(bh % H) * HS + (size_t)(i0 + x) * ldo;
+#pragma unroll
+  for (int n = 0; n < NN; ++n)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      v4f w;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) w[c] = o[n][4 * g + c] / l;
+      *reinterpret_cast<v4f*>(orow + 32 * n + 8 * g + 4 * lk) = w;
+    }
+  if (lk == 0) lse[(size_t)bh * T + i0 + x] = m + logf(l);
+}
+
+// Backward, query-centric: dQ (+ Dq) of query tile qt, and D = rowsum(dO*O)
+// of its rows into dsum for the key-centric pass.
+template <int HS, bool CAUSAL, bool BF>
+__global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict__ Q, const float* __restrict__ K,
+                                                     const float* __restrict__ V, const float* __restrict__ O,
+                                                     const float* __restrict__ dO, int ldo, int H,
+                                                     const float* __restrict__ lse, const float* __restrict__ scale,
+                                                     float* __restrict__ dQ, const float* __restrict__ Dq,
+                                                     float* __restrict__ dsum, int T, int BH) {
+  constexpr int NKB = HS / 16, NN = HS / 32;
+  const int NT = T / 32;
+  const int qt = NT - 1 - (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
+  const int lane = threadIdx.x, x = lane & 31, lk = lane >> 5;
+  const size_t head = (size_t)bh * T * HS;
+  const float *Qh = Q + head, *Kh = K + head, *Vh = V + head;
+  const int i0 = 32 * qt, i = i0 + x;
+  const float sc = scale[0];
+
+  float qb[NKB][8], ob[NKB][8];  // B of S^T = K Q^T and of dP^T = V dO^T
+  const float* dorow = head_row(dO, bh, H, T, ldo, HS, i);
+  const float* orow = head_row(O, bh, H, T, ldo, HS, i);
+  float d = 0.0f;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    load8(Qh + (size_t)i * HS + 16 * kb + 8 * lk, qb[kb]);
+    load8(dorow + 16 * kb + 8 * lk, ob[kb]);
+    float ov[8];
+    load8(orow + 16 * kb + 8 * lk, ov);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d += ob[kb][e] * ov[e];
+  }
+  d += __shfl_xor(d, 32, 64);
+  if (lk == 0) dsum[(size_t)bh * T + i] = d;
+  const float L = lse[(size_t)bh * T + i];
+
+  v16f dq[NN];
+#pragma unroll
+  for (int n = 0; n < NN; ++n) dq[n] = v16f{0};
+  const int last = CAUSAL ? qt : NT - 1;
+  for (int j = 0; j <= last; ++j) {
+    float ka[NKB][8], vr[NKB][8];  // A of S^T and dP^T: rows perm_row(x) of K_j, V_j
+    const int krow = 32 * j + perm_row(x);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      load8(Kh + (size_t)krow * HS + 16 * kb + 8 * lk, ka[kb]);
+      load8(Vh + (size_t)krow * HS + 16 * kb + 8 * lk, vr[kb]);
+    }
+    v16f st = v16f{0}, dp = v16f{0};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      st = slab<BF>(ka[kb], qb[kb], st);
+      dp = slab<BF>(vr[kb], ob[kb], dp);
+    }
+    float kc[NN][2][8];  // B of dQ = dS K: K[32 j + 16 h + 8 lk + e][32 n + x]
+#pragma unroll
+    for (int n = 0; n < NN; ++n)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kc[n][h][e] = Kh[(size_t)(32 * j + 16 * h + 8 * lk + e) * HS + 32 * n + x];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const bool masked = CAUSAL && j == qt && perm_index(r, lk) > x;
+      const float p = masked ? 0.0f : expf(st[r] * sc - L);
+      const float diff = dp[r] - d;
+      const float dx = p * diff;
+      st[r] = dx * sc;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float ab[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ab[e] = st[8 * h + e];
+#pragma unroll
+      for (int n = 0; n < NN; ++n) dq[n] = slab<BF>(ab, kc[n][h], dq[n]);
+    }
+  }
+  // dQ[i0 + 8 (r >> 2) + 4 lk + (r & 3)][32 n + x]
+  float* dqh = dQ + head;
+#pragma unroll
+  for (int n = 0; n < NN; ++n)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const size_t off = (size_t)(i0 + 8 * (r >> 2) + 4 * lk + (r & 3)) * HS + 32 * n + x;
+      dqh[off] = Dq ? Dq[head + off] + dq[n][r] : dq[n][r];
+    }
+}
+
+// Backward, key-centric: dK (+ Dk) and dV (+ Dv) of key tile kt.
+template <int HS, bool CAUSAL, bool BF>
+__global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict__ Q, const float* __restrict__ K,
+                                                      const float* __restrict__ V, const float* __restrict__ dO, int ldo,
+                                                      int H, const float* __restrict__ lse,
+                                                      const float* __restrict__ dsum, const float* __restrict__ scale,
+                                                      float* __restrict__ dK, const float* __restrict__ Dk,
+                                                      float* __restrict__ dV, const float* __restrict__ Dv, int T,
+                                                      int BH) {
+  constexpr int NKB = HS / 16, NN = HS / 32;
+  const int NT = T / 32;
+  const int kt = (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
+  const int lane = threadIdx.x, x = lane & 31, lk = lane >> 5;
+  const size_t head = (size_t)bh * T * HS;
+  const float *Qh = Q + head, *Kh = K + head, *Vh = V + head;
+  const int j0 = 32 * kt, key = j0 + x;
+  const float sc = scale[0];
+  const float* lseh = lse + (size_t)bh * T;
+  const float* dsh = dsum + (size_t)bh * T;
+
+  float kb_[NKB][8], vb[NKB][8];  // B of S = Q K^T and of dP = dO V^T: rows j0 + x of K, V
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    load8(Kh + (size_t)key * HS + 16 * kb + 8 * lk, kb_[kb]);
+    load8(Vh + (size_t)key * HS + 16 * kb + 8 * lk, vb[kb]);
+  }
+  v16f dvt[NN], dkt[NN];  // dV^T, dK^T: lane = key, rows = head dims
+#pragma unroll
+  for (int n = 0; n < NN; ++n) {
+    dvt[n] = v16f{0};
+    dkt[n] = v16f{0};
+  }
+  const int first = CAUSAL ? kt : 0;
+  for (int it = first; it < NT; ++it) {
+    const int i0 = 32 * it;
+    v16f s = v16f{0}, dp = v16f{0};
+    {
+      const int qrow = i0 + perm_row(x);
+      const float* dorow = head_row(dO, bh, H, T, ldo, HS, qrow);
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        float qa[8], oa[8];  // A: rows perm_row(x) of Q_i, dO_i
+        load8(Qh + (size_t)qrow * HS + 16 * kb + 8 * lk, qa);
+        load8(dorow + 16 * kb + 8 * lk, oa);
+        s = slab<BF>(qa, kb_[kb], s);
+        dp = slab<BF>(oa, vb[kb], dp);
+      }
+    }
+    // lane = key j0 + x, register r = query i0 + perm_index(r, lk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float Lq[8], Dq_[8];
+      load8(lseh + i0 + 16 * h + 8 * lk, Lq);
+      load8(dsh + i0 + 16 * h + 8 * lk, Dq_);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int r = 8 * h + e;
+        const bool masked = CAUSAL && key > i0 + perm_index(r, lk);
+        const float p = masked ? 0.0f : expf(s[r] * sc - Lq[e]);
+        const float diff = dp[r] - Dq_[e];
+        const float dx = p * diff;
+        s[r] = p;
+        dp[r] = dx * sc;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float pb[8], db[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pb[e] = s[8 * h + e];
+        db[e] = dp[8 * h + e];
+      }
+#pragma unroll
+      for (int n = 0; n < NN; ++n) {
+        float oa[8], qa[8];  // A of dV^T = dO^T P and dK^T = Q^T dS: [i0 + 16 h + 8 lk + e][32 n + x]
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int q = i0 + 16 * h + 8 * lk + e;
+          oa[e] = head_row(dO, bh, H, T, ldo, HS, q)[32 * n + x];
+          qa[e] = Qh[(size_t)q * HS + 32 * n + x];
+        }
+        dvt[n] = slab<BF>(oa, pb, dvt[n]);
+        dkt[n] = slab<BF>(qa, db, dkt[n]);
+      }
+    }
+  }
+  // dV[j0 + x][32 n + 8 g + 4 lk + c] = dvt[n][4 g + c] (+ Dv), dK likewise
+#pragma unroll
+  for (int n = 0; n < NN; ++n)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const size_t off = head + (size_t)key * HS + 32 * n + 8 * g + 4 * lk;
+      v4f wv, wk;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        wv[c] = dvt[n][4 * g + c];
+        wk[c] = dkt[n][4 * g + c];
+      }
+      if (Dv) wv = *reinterpret_cast<const v4f*>(Dv + off) + wv;
+      if (Dk) wk = *reinterpret_cast<const v4f*>(Dk + off) + wk;
+      *reinterpret_cast<v4f*>(dV + off) = wv;
+      *reinterpret_cast<v4f*>(dK + off) = wk;
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <int HS, bool CAUSAL, bool BF>
+void fwd_launch(const float* Q, const float* K, const float* V, const float* scale, float* O, int ldo, int H,
+                float* lse, int T, int BH, hipStream_t s) {
+  k_flash_fwd<HS, CAUSAL, BF><<<(unsigned)(T / 32 * BH), 64, 0, s>>>(Q, K, V, scale, O, ldo, H, lse, T, BH);
+}
+
+template <int HS, bool CAUSAL, bool BF>
+void bwd_launch(const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
+  const unsigned grid = (unsigned)(T / 32 * BH);
+  k_flash_bwd_dq<HS, CAUSAL, BF><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.O, a.dO, ldo, H, a.lse, a.scale, a.dQ, a.Dq,
+                                                      a.dsum, T, BH);
+  k_flash_bwd_dkv<HS, CAUSAL, BF><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.dO, ldo, H, a.lse, a.dsum, a.scale, a.dK, a.Dk,
+                                                       a.dV, a.Dv, T, BH);
+}
+
+template <bool CAUSAL, bool BF>
+void fwd_hs(size_t hs, const float* Q, const float* K, const float* V, const float* scale, float* O, int ldo, int H,
+            float* lse, int T, int BH, hipStream_t s) {
+  if (hs == 64) fwd_launch<64, CAUSAL, BF>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
+  else fwd_launch<32, CAUSAL, BF>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
+}
+
+template <bool CAUSAL, bool BF>
+void bwd_hs(size_t hs, const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
+  if (hs == 64) bwd_launch<64, CAUSAL, BF>(a, ldo, H, T, BH, s);
+  else bwd_launch<32, CAUSAL, BF>(a, ldo, H, T, BH, s);
+}
+
+}  // namespace
+
+bool flash_supported(size_t bh, size_t t, size_t hs) {
+  return bh > 0 && t >= 32 && t % 32 == 0 && (hs == 32 || hs == 64) && (t / 32) * bh <= 0x7fffffffu &&
+         bh * t * hs < (1ull << 40);
+}
+
+bool flash_fwd(const float* Q, const float* K, const float* V, const float* scale, float* O, size_t ldo, size_t heads,
+               float* lse, size_t bh, size_t t, size_t hs, bool causal, bool bf16, hipStream_t s) {
+  if (!flash_supported(bh, t, hs) || heads == 0 || bh % heads || ldo < hs * heads || ldo % 4) return false;
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O) || !lse || !scale) return false;
+  const int T = (int)t, BH = (int)bh, l = (int)ldo, H = (int)heads;
+  if (causal) {
+    if (bf16) fwd_hs<true, true>(hs, Q, K, V, scale, O, l, H, lse, T, BH, s);
+    else fwd_hs<true, false>(hs, Q, K, V, scale, O, l, H, lse, T, BH, s);
+  } else {
+    if (bf16) fwd_hs<false, true>(hs, Q, K, V, scale, O, l, H, lse, T, BH, s);
+    else fwd_hs<false, false>(hs, Q, K, V, scale, O, l, H, lse, T, BH, s);
+  }
+  MALUS_HIP(hipGetLastError());
+  return true;
+}
+
+bool flash_bwd(const FlashBwd& a, size_t ldo, size_t heads, size_t bh, size_t t, size_t hs, bool causal, bool bf16,
+               hipStream_t s) {
+  if (!flash_supported(bh, t, hs) || heads == 0 || bh % heads || ldo < hs * heads || ldo % 4) return false;
+  for (const void* p : {(const void*)a.Q, (const void*)a.K, (const void*)a.V, (const void*)a.O, (const void*)a.dO,
+                        (const void*)a.dQ, (const void*)a.dK, (const void*)a.dV, (const void*)a.lse,
+                        (const void*)a.dsum})
+    if (!p || !aligned16(p)) return false;
+  if ((a.Dk && !aligned16(a.Dk)) || (a.Dv && !aligned16(a.Dv)) || !a.scale) return false;
+  const int T = (int)t, BH = (int)bh, l = (int)ldo, H = (int)heads;
+  if (causal) {
+    if (bf16) bwd_hs<true, true>(hs, a, l, H, T, BH, s);
+    else bwd_hs<true, false>(hs, a, l, H, T, BH, s);
+  } else {
+    if (bf16) bwd_hs<false, true>(hs, a, l, H, T, BH, s);
+    else bwd_hs<false, false>(hs, a, l, H, T, BH, s);
+  }
+  MALUS_HIP(hipGetLastError());
+  return true;
+}
+
+}  // namespace k
+}  // namespace malus

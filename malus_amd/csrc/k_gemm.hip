@@ -1023,6 +1023,12 @@ extern "C" int malus_gemm_set_tile(int tm, int tn) {
 // reductions stay f32): while on, every GEMM launch rounds its operands to
 // bf16 and runs the bf16 MFMA.  A `with autocast:` block turns it on at entry
 // and restores the returned previous state at exit.
+namespace malus {
+namespace k {
+bool autocast_on() { return g_autocast; }
+}  // namespace k
+}  // namespace malus
+
 extern "C" int malus_autocast(int on) {
   const bool prev = malus::k::g_autocast;
   malus::k::g_autocast = on != 0;

@@ -47,8 +47,13 @@ enum Op : int32_t {
   OP_MATMUL = 0, OP_ADD = 1, OP_SUB = 2, OP_MUL = 3, OP_DIV = 4, OP_TRANSPOSE = 13, OP_RESHAPE = 19, OP_SOFTMAX = 20,
   OP_LAYERNORM = 21, OP_GELU = 22, OP_CE = 23, OP_EMBEDDING = 24,
   TAG_HEAD_PROJ = 100, TAG_SCORES = 101, TAG_ATTN_OUT = 102, TAG_ATTENTION = 103,
-  TAG_LN_SCALE = 104, TAG_GELU_MATMUL = 105  // fused nodes (tape.cpp)
+  TAG_LN_SCALE = 104, TAG_GELU_MATMUL = 105, TAG_FLASH = 106  // fused nodes (tape.cpp)
 };
+
+// Attention kernel choice: AUTO takes flash attention under autocast, else
+// the row-register kernel where its shapes are built, else flash attention,
+// else the composed ops.
+enum AttnMode : int { ATTN_AUTO = 0, ATTN_FLASH = 1, ATTN_ROWS = 2, ATTN_COMPOSED = 3 };
 
 // grad-tracked binop: lower + tape_record_binop (codegen-cpu/lib.rs:1531-1552)
 int64_t binop(int32_t op, int64_t a, int64_t b) {
@@ -121,6 +126,7 @@ struct Gpt {
   // memory instead of kernel arguments.
   bool inplace_opt = false;
   const float* bc_dev = nullptr;
+  int attn_mode = ATTN_AUTO;
   std::vector<int64_t> p, m, v;  // block l params at 8l..8l+7, then wte, wpe, ln_f, lm_head
   int64_t pos = 0;               // [B*T] i32 position ids
   int64_t attn_scale = 0;        // [1,1] 1/sqrt(hs) of the fused attention (built on first use)
@@ -167,9 +173,16 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
     Vv = head_fold(P[3]);
   }
   int64_t Kt = fused_heads ? 0 : permute(K, {0, 2, 1});
-  const bool fused_attention = fused_heads && k::attn_scores_supported(B * H, Tn, hs);
+  const bool rows_ok = fused_heads && k::attn_scores_supported(B * H, Tn, hs);
+  const bool flash_ok = fused_heads && k::flash_supported(B * H, Tn, hs);
+  // AUTO: in f32 the row-register kernel where it is built (at T = 256 its
+  // backward reads the stored P instead of recomputing it, and is faster);
+  // under autocast flash attention, whose products run on the bf16 MFMA
+  const bool flash = flash_ok && (g.attn_mode == ATTN_FLASH ||
+                                  (g.attn_mode == ATTN_AUTO && (!rows_ok || k::autocast_on())));
+  const bool fused_attention = !flash && rows_ok && (g.attn_mode == ATTN_AUTO || g.attn_mode == ATTN_ROWS);
   int64_t scale;
-  if (fused_attention) {
+  if (fused_attention || flash) {
     // variable(ones(1,1) * (1/sqrt(hs))) is the same value every forward and
     // receives no gradient in the fused form: build it once per model
     if (!g.attn_scale) {
@@ -189,7 +202,15 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   }
   const size_t sshape[3] = {B * H, Tn, Tn};
   int64_t S = 0, mask = 0, Ss = 0, Sm = 0, Pm = 0, AO = 0, ao4 = 0, aop = 0, att;
-  if (fused_attention) {
+  if (flash) {
+    // Flash attention: the same value with an online softmax; neither the
+    // scores nor the probabilities exist, the VJP recomputes them from the
+    // saved row log-sum-exp.
+    int64_t lse = 0;
+    att = flash_fwd_impl(Q, K, Vv, scale, B, Tn, H, &lse);
+    tape_record_fused(TAG_FLASH, {Q, K, Vv, att, lse, scale}, att, {(int64_t)B, (int64_t)Tn, (int64_t)H});
+    tensor_release(lse);
+  } else if (fused_attention) {
     // Fused causal attention: S = Q @ K^T, scale, causal mask, softmax (P
     // stored) and att = P @ V written straight into [B*T, C], all in one
     // kernel, and one tape node whose VJP runs the fused scores backward.
@@ -497,6 +518,14 @@ int64_t malus_gpt_moment(void* gp, int i, int which) {
 void malus_gpt_set_fused_forward(void* gp, int on) { static_cast<Gpt*>(gp)->fused_fwd = on != 0; }
 
 void malus_gpt_set_fused_optimizer(void* gp, int on) { static_cast<Gpt*>(gp)->fused_opt = on != 0; }
+// 0: automatic, 1: flash attention, 2: the row-register fused kernel, 3: composed ops
+int malus_gpt_set_attention(void* gp, int mode) {
+  API_TRY
+  if (mode < ATTN_AUTO || mode > ATTN_COMPOSED) fail("malus: attention mode %d is not 0..3", mode);
+  static_cast<Gpt*>(gp)->attn_mode = mode;
+  return 0;
+  API_CATCH(-1)
+}
 
 // Forward + cross-entropy (recorded on the tape); returns the loss [1].
 int64_t malus_gpt_forward_loss(void* gp, int64_t toks, int64_t targets) {

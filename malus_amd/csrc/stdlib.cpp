@@ -764,6 +764,69 @@ int64_t malus_std_attn_bwd_all(int64_t dout, int64_t q, int64_t kk, int64_t v, i
   return malus::H(out);
   API_CATCH(0)
 }
+// Flash attention (k_flash.hip): q, k, v and the output dense [bh, t, hs],
+// lse [bh, t]; causal 0 means no mask.
+int64_t malus_std_flash_attn_fwd(int64_t q, int64_t kk, int64_t v, int64_t scale, int32_t causal, int64_t* lse_out) {
+  API_TRY
+  TensorBuffer *Q = T(q), *K = T(kk), *V = T(v), *sc = T(scale);
+  auto same3 = [&](const TensorBuffer* x) {
+    return x->ndim == 3 && x->shape[0] == Q->shape[0] && x->shape[1] == Q->shape[1] && x->shape[2] == Q->shape[2];
+  };
+  if (Q->ndim != 3 || !same3(K) || !same3(V) || sc->len != 1)
+    fail("malus: flash_attn_fwd shape mismatch: q %s, k %s, v %s, scale %s", shape_str(Q).c_str(),
+         shape_str(K).c_str(), shape_str(V).c_str(), shape_str(sc).c_str());
+  const size_t bh = Q->shape[0], t = Q->shape[1], hs = Q->shape[2];
+  if (!k::flash_supported(bh, t, hs))
+    fail("malus: flash_attn_fwd: t=%zu hs=%zu (needs t a multiple of 32 and hs 32 or 64)", t, hs);
+  attn_need_f32("flash_attn_fwd", {Q, K, V, sc});
+  const size_t lsh[2] = {bh, t};
+  TensorBuffer* lse = alloc_tensor(F32, lsh, 2);
+  TensorBuffer* out = alloc_tensor(F32, Q->shape, 3);
+  if (!k::flash_fwd(Q->f32(), K->f32(), V->f32(), sc->f32(), out->f32(), hs, 1, lse->f32(), bh, t, hs, causal != 0,
+                    k::autocast_on(), stream()))
+    fail("malus: flash_attn_fwd: unaligned operand");
+  const uint64_t seq = enqueue_mark("flash_attn_fwd");
+  out->write_seq = seq;
+  lse->write_seq = seq;
+  if (lse_out) *lse_out = malus::H(lse);
+  else release(lse);
+  return malus::H(out);
+  API_CATCH(0)
+}
+int32_t malus_std_flash_attn_bwd(int64_t dout, int64_t q, int64_t kk, int64_t v, int64_t out, int64_t lse,
+                                 int64_t scale, int32_t causal, int64_t dq_add, int64_t dk_add, int64_t dv_add,
+                                 int64_t* dq_out, int64_t* dk_out, int64_t* dv_out) {
+  API_TRY
+  TensorBuffer *d = T(dout), *Q = T(q), *K = T(kk), *V = T(v), *O = T(out), *L = T(lse), *sc = T(scale);
+  TensorBuffer *Aq = dq_add ? T(dq_add) : nullptr, *Ak = dk_add ? T(dk_add) : nullptr, *Av = dv_add ? T(dv_add) : nullptr;
+  auto same3 = [&](const TensorBuffer* x) {
+    return x->ndim == 3 && x->shape[0] == d->shape[0] && x->shape[1] == d->shape[1] && x->shape[2] == d->shape[2];
+  };
+  if (d->ndim != 3 || !same3(Q) || !same3(K) || !same3(V) || !same3(O) || L->len != d->shape[0] * d->shape[1] ||
+      sc->len != 1 || !dq_out || !dk_out || !dv_out || (Aq && !same3(Aq)) || (Ak && !same3(Ak)) || (Av && !same3(Av)))
+    fail("malus: flash_attn_bwd shape mismatch: dout %s, q %s, k %s, v %s, out %s, lse %s", shape_str(d).c_str(),
+         shape_str(Q).c_str(), shape_str(K).c_str(), shape_str(V).c_str(), shape_str(O).c_str(), shape_str(L).c_str());
+  const size_t bh = d->shape[0], t = d->shape[1], hs = d->shape[2];
+  if (!k::flash_supported(bh, t, hs))
+    fail("malus: flash_attn_bwd: t=%zu hs=%zu (needs t a multiple of 32 and hs 32 or 64)", t, hs);
+  attn_need_f32("flash_attn_bwd", {d, Q, K, V, O, L, sc, Aq, Ak, Av});
+  TensorBuffer *dq = alloc_like(Q), *dk = alloc_like(K), *dv = alloc_like(V);
+  size_t bucket;
+  float* dsum = static_cast<float*>(pool_alloc(bh * t * sizeof(float), &bucket));
+  const k::FlashBwd a{Q->f32(), K->f32(), V->f32(), O->f32(), d->f32(), L->f32(), sc->f32(),
+                      dq->f32(), dk->f32(), dv->f32(), dsum,
+                      Aq ? Aq->f32() : nullptr, Ak ? Ak->f32() : nullptr, Av ? Av->f32() : nullptr};
+  if (!k::flash_bwd(a, hs, 1, bh, t, hs, causal != 0, k::autocast_on(), stream()))
+    fail("malus: flash_attn_bwd: unaligned operand");
+  pool_free(dsum, bucket);  // stream order: later users of the buffer run after the kernels
+  const uint64_t seq = enqueue_mark("flash_attn_bwd");
+  for (TensorBuffer* x : {dq, dk, dv}) x->write_seq = seq;
+  *dq_out = malus::H(dq);
+  *dk_out = malus::H(dk);
+  *dv_out = malus::H(dv);
+  return 0;
+  API_CATCH(-1)
+}
 int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout) {
   API_TRY
   TensorBuffer *w = T(weight), *idx = T(indices), *d = T(dout);
@@ -1195,6 +1258,45 @@ void attn_bwd_all_impl(int64_t hda, int64_t hq, int64_t hk, int64_t hv, int64_t 
     fail("malus: attn_bwd_all: no fused kernel for t=%zu hs=%zu", T, hs);
   pool_free(ds, bucket);  // stream order: later users of the buffer run after the kernel
   const uint64_t seq = enqueue_mark("attn_bwd_all");
+  for (TensorBuffer* x : {oq, ok, ov}) x->write_seq = seq;
+  *dq = malus::H(oq);
+  *dk = malus::H(ok);
+  *dv = malus::H(ov);
+}
+// Flash attention of the model: Q, K, V [B*H, T, hs] -> att [B*T, H*hs]
+// (causal); *lse_out [B*H, T].
+int64_t flash_fwd_impl(int64_t hq, int64_t hk, int64_t hv, int64_t hscale, size_t B, size_t T, size_t H,
+                       int64_t* lse_out) {
+  TensorBuffer *q = T_(hq), *kk = T_(hk), *v = T_(hv), *sc = T_(hscale);
+  const size_t hs = q->shape[2], bh = B * H, C = H * hs;
+  const size_t lsh[2] = {bh, T}, osh[2] = {B * T, C};
+  TensorBuffer* lse = alloc_tensor(F32, lsh, 2);
+  TensorBuffer* out = alloc_tensor(F32, osh, 2);
+  if (!k::flash_fwd(q->f32(), kk->f32(), v->f32(), sc->f32(), out->f32(), C, H, lse->f32(), bh, T, hs, true,
+                    k::autocast_on(), stream()))
+    fail("malus: flash attention: no kernel for t=%zu hs=%zu", T, hs);
+  const uint64_t seq = enqueue_mark("flash_attn_fwd");
+  lse->write_seq = seq;
+  out->write_seq = seq;
+  *lse_out = malus::H(lse);
+  return malus::H(out);
+}
+// Its VJP: dQ = Dq + ..., dK = Dk + ..., dV = Dv + ... from dAtt [B*T, H*hs].
+void flash_bwd_impl(int64_t hda, int64_t hq, int64_t hk, int64_t hv, int64_t ho, int64_t hlse, int64_t hscale,
+                    const TensorBuffer* Dq, const TensorBuffer* Dk, const TensorBuffer* Dv, int64_t* dq, int64_t* dk,
+                    int64_t* dv, size_t B, size_t T, size_t H) {
+  TensorBuffer *da = T_(hda), *q = T_(hq), *kk = T_(hk), *v = T_(hv), *o = T_(ho), *lse = T_(hlse), *sc = T_(hscale);
+  const size_t hs = q->shape[2], bh = B * H, C = H * hs;
+  TensorBuffer *oq = alloc_like(q), *ok = alloc_like(kk), *ov = alloc_like(v);
+  size_t bucket;
+  float* dsum = static_cast<float*>(pool_alloc(bh * T * sizeof(float), &bucket));
+  const k::FlashBwd a{q->f32(), kk->f32(), v->f32(), o->f32(), da->f32(), lse->f32(), sc->f32(),
+                      oq->f32(), ok->f32(), ov->f32(), dsum,
+                      Dq ? Dq->f32() : nullptr, Dk ? Dk->f32() : nullptr, Dv ? Dv->f32() : nullptr};
+  if (!k::flash_bwd(a, C, H, bh, T, hs, true, k::autocast_on(), stream()))
+    fail("malus: flash attention VJP: no kernel for t=%zu hs=%zu", T, hs);
+  pool_free(dsum, bucket);
+  const uint64_t seq = enqueue_mark("flash_attn_bwd");
   for (TensorBuffer* x : {oq, ok, ov}) x->write_seq = seq;
   *dq = malus::H(oq);
   *dk = malus::H(ok);

@@ -8,6 +8,7 @@
 // tape_register_backward_fn exactly as compile_and_run does.
 #include <cstdint>
 #include <iterator>
+#include <tuple>
 #include <unordered_map>
 #include <unordered_set>
 #include <vector>
@@ -37,9 +38,13 @@ enum OpTag : int32_t {
 //   LayerNormScale (x, w; y, var) -> out: layernorm(x, axis=-1) * w, with the
 //            normalized rows y and the keepdim variance saved
 //   GeluMatmul (h, W; ge) -> out: gelu(h) @ W, with ge = gelu(h) saved
-// meta holds {B, T, H} for HeadProj, AttnOut and Attention.
+//   FlashAttention (Q, K, V; att, lse, scale) -> att: Attention's value with an
+//            online softmax (no P); the output and the row log-sum-exp are
+//            saved for the VJP, which recomputes P
+// meta holds {B, T, H} for HeadProj, AttnOut, Attention and FlashAttention.
 enum FusedTag : int32_t {
-  HeadProj = 100, Scores = 101, AttnOut = 102, Attention = 103, LayerNormScale = 104, GeluMatmul = 105
+  HeadProj = 100, Scores = 101, AttnOut = 102, Attention = 103, LayerNormScale = 104, GeluMatmul = 105,
+  FlashAttention = 106
 };
 
 enum BwdSlot : int32_t {
@@ -129,7 +134,7 @@ void need_values(int64_t h) {
 
 // Number of leading saved handles that are differentiable inputs.
 int diff_inputs(int32_t op) {
-  if (op == Attention) return 3;
+  if (op == Attention || op == FlashAttention) return 3;
   if (op == Matmul || op == Add || op == Sub || op == Mul || op == Div || op == HeadProj || op == Scores ||
       op == AttnOut || op == LayerNormScale || op == GeluMatmul)
     return 2;
@@ -307,8 +312,9 @@ using namespace malus;
 namespace malus {
 void tape_record_fused(int32_t op, const std::vector<int64_t>& saved, int64_t out, const std::vector<int64_t>& meta) {
   if (!t_recording) return;
-  const size_t want = op == Attention ? 5 : op == LayerNormScale ? 4 : op == GeluMatmul ? 3 : 2;
-  if (op < HeadProj || op > GeluMatmul) fail("malus: unknown fused op tag %d", op);
+  const size_t want = op == FlashAttention ? 6 : op == Attention ? 5 : op == LayerNormScale ? 4
+                                               : op == GeluMatmul ? 3 : 2;
+  if (op < HeadProj || op > FlashAttention) fail("malus: unknown fused op tag %d", op);
   if (saved.size() != want) fail("malus: fused op %d takes %zu saved handles, got %zu", op, want, saved.size());
   for (int64_t h : saved) retain(T(h));
   retain(T(out));
@@ -542,6 +548,33 @@ void backward(int64_t loss) {
           }
           if (nb) fold_grad(grads, kk, [&](const TensorBuffer* o) { return scores_bwd_k(ds, q, o, true); });
           release(T(ds));
+        }
+        break;
+      }
+      case FlashAttention: {  // saved {Q, K, V, att, lse, scale}: the three gradients from two kernels
+        const int64_t q = n.saved[0], kk = n.saved[1], v = n.saved[2], o = n.saved[3], lse = n.saved[4],
+                      sc = n.saved[5];
+        const size_t Bm = (size_t)n.meta[0], Tm = (size_t)n.meta[1], Hm = (size_t)n.meta[2];
+        for (int64_t h : n.saved) need_values(h);
+        // with the library's GradAcc an existing gradient rides into the
+        // kernels as an addend and the result replaces it (same rounding)
+        const bool fold = q != kk && q != v && kk != v && slot_is(GradAcc, &malus_std_broadcast_add_fwd);
+        auto old = [&](int64_t x) -> const TensorBuffer* {
+          auto f = grads.find(x);
+          return fold && f != grads.end() ? T(f->second) : nullptr;
+        };
+        int64_t dq = 0, dk = 0, dv = 0;
+        flash_bwd_impl(dout, q, kk, v, o, lse, sc, old(q), old(kk), old(v), &dq, &dk, &dv, Bm, Tm, Hm);
+        for (auto [x, gr, needed] : {std::tuple{v, dv, nc}, std::tuple{q, dq, na}, std::tuple{kk, dk, nb}}) {
+          auto f = grads.find(x);
+          if (!needed) {
+            release(T(gr));
+          } else if (fold && f != grads.end()) {
+            release(T(f->second));
+            f->second = gr;
+          } else {
+            accumulate(grads, x, gr);
+          }
         }
         break;
       }
