@@ -191,6 +191,88 @@ def kernel_suite(rt, M, reps: int):
     return rows
 
 
+def attention_suite(rt, M, reps: int):
+    """Causal attention forward and backward per call: the row-register
+    fused kernels (T <= 256) and flash attention (any T multiple of 32), in
+    f32 and under autocast, at C5's shape (B*H = 384, T = 256, hs = 64) and
+    at longer T with the same tokens per call.  Rate: algorithmic FLOP
+    (forward: Q K^T and P V; backward: dP, dQ, dK, dV; causal pairs only,
+    2 * hs per query-key pair per product) / time."""
+    import numpy as np
+
+    L = rt.L
+    rng = np.random.default_rng(5)
+    rows = []
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        L.gpu_barrier()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        L.gpu_barrier()
+        return (time.perf_counter() - t0) / reps
+
+    for bh, t, hs in [(384, 256, 64), (96, 1024, 64), (48, 2048, 64), (24, 4096, 64)]:
+        q, k, v, d = (rt.tensor(rng.uniform(-1, 1, (bh, t, hs)).astype(np.float32)) for _ in range(4))
+        sc = rt.tensor(np.array([[1.0 / np.sqrt(hs)]], np.float32))
+        pairs = bh * t * (t + 1) / 2
+        f_fwd, f_bwd = 2 * 2.0 * hs * pairs, 4 * 2.0 * hs * pairs
+        for ac in (0, 1):
+            prev = L.malus_autocast(ac)
+            lse = C.c_int64()
+            out = L.malus_std_flash_attn_fwd(q, k, v, sc, 1, C.byref(lse))
+
+            def flash_fwd():
+                h = L.malus_std_flash_attn_fwd(q, k, v, sc, 1, None)
+                L.tensor_free(h)
+
+            def flash_bwd():
+                g = [C.c_int64() for _ in range(3)]
+                L.malus_std_flash_attn_bwd(d, q, k, v, out, lse.value, sc, 1, 0, 0, 0, *[C.byref(x) for x in g])
+                for x in g:
+                    L.tensor_free(x.value)
+
+            tf, tb = timed(flash_fwd), timed(flash_bwd)
+            rows.append({"kernel": "flash", "bh": bh, "t": t, "hs": hs, "autocast": bool(ac),
+                         "fwd_us": round(tf * 1e6, 1), "bwd_us": round(tb * 1e6, 1),
+                         "fwd_TFLOPs": round(f_fwd / tf / 1e12, 1), "bwd_TFLOPs": round(f_bwd / tb / 1e12, 1)})
+            L.tensor_free(out)
+            L.tensor_free(lse.value)
+            if t <= 256 and not ac:
+                mask = L.tensor_causal_mask(t)
+                p = C.c_int64()
+                o2 = L.malus_std_attn_fwd(q, k, v, sc, mask, 1, C.byref(p))
+
+                def rows_fwd():
+                    pp = C.c_int64()
+                    h = L.malus_std_attn_fwd(q, k, v, sc, mask, 1, C.byref(pp))
+                    L.tensor_free(h)
+                    L.tensor_free(pp.value)
+
+                def rows_bwd():
+                    g = [C.c_int64() for _ in range(3)]
+                    ds = L.malus_std_attn_bwd_all(d, q, k, v, p.value, sc, 1, 0, 0, 0, *[C.byref(x) for x in g])
+                    L.tensor_free(ds)
+                    for x in g:
+                        L.tensor_free(x.value)
+
+                tf, tb = timed(rows_fwd), timed(rows_bwd)
+                rows.append({"kernel": "rows", "bh": bh, "t": t, "hs": hs, "autocast": False,
+                             "fwd_us": round(tf * 1e6, 1), "bwd_us": round(tb * 1e6, 1),
+                             "fwd_TFLOPs": round(f_fwd / tf / 1e12, 1), "bwd_TFLOPs": round(f_bwd / tb / 1e12, 1)})
+                for h in (mask, p.value, o2):
+                    L.tensor_free(h)
+            L.malus_autocast(prev)
+        for h in (q, k, v, d, sc):
+            L.tensor_free(h)
+    for r in rows:
+        log(f"  {r['kernel']:5s} bh {r['bh']:4d} t {r['t']:5d} hs {r['hs']} {'bf16' if r['autocast'] else 'f32 '}  "
+            f"fwd {r['fwd_us']:8.1f} us {r['fwd_TFLOPs']:6.1f} TF/s   bwd {r['bwd_us']:8.1f} us {r['bwd_TFLOPs']:6.1f} TF/s")
+    return rows
+
+
 def host_cpu():
     """The host the CPU baseline ran on: usable cores and the CPU model."""
     model = "unknown"
@@ -462,8 +544,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", choices=["c5", "c4", "c1"], default="c5",
                     help="c5 (default): Karpathy char-nanoGPT; c4: toy char-nanoGPT; c1: XOR MLP, 10,000 steps")
-    ap.add_argument("--graph", action="store_true",
-                    help="time the step as a replayed hipGraph (malus_gpt_graph_*) instead of eager launches")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every kernel of the step from the host (default: the step captured once as a "
+                         "hipGraph and replayed, malus_gpt_graph_*, with each step's tokens copied in by its nodes)")
     ap.add_argument("--autocast", action="store_true",
                     help="run the step in the bf16 autocast scope (bf16 GEMMs, f32 accumulation, f32 master state); "
                          "reported alongside the f32 headline, never in its place")
@@ -474,9 +557,11 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB copy (counter calibration for the traffic figure)")
-    ap.add_argument("--suite", choices=["kernels"],
-                    help="kernels: the C2/C3 elementwise and row-op kernels' HBM bandwidth (one JSON line)")
+    ap.add_argument("--suite", choices=["kernels", "attention"],
+                    help="kernels: the C2/C3 elementwise and row-op kernels' HBM bandwidth; attention: the causal "
+                         "attention kernels' forward and backward times (one JSON line each)")
     a = ap.parse_args()
+    a.graph = not a.eager
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
               "multi-GPU data parallelism is designed but not built", file=sys.stderr)
@@ -491,6 +576,11 @@ def main():
     if a.suite == "kernels":
         rows = kernel_suite(rt, M, reps=10)
         print(json.dumps({"suite": "kernels", "unit": "GB/s", "peak_hbm_GBs": PEAK_HBM_GBS, "rows": rows}), flush=True)
+        return
+    if a.suite == "attention":
+        rows = attention_suite(rt, M, reps=10)
+        print(json.dumps({"suite": "attention", "peak_fp32_TFLOPs": PEAK_FP32_MFMA_TFLOPS,
+                          "peak_bf16_TFLOPs": PEAK_BF16_MFMA_TFLOPS, "rows": rows}), flush=True)
         return
     out = run_xor(rt, a) if a.config == "c1" else run_gpt(rt, a, CONFIGS[a.config])
     print(json.dumps(out), flush=True)

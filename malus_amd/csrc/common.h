@@ -30,8 +30,12 @@ struct Storage {
   size_t bytes = 0;              // bucketed allocation size
   std::atomic<int> aliases{0};   // TensorBuffers referencing this storage
   // t > 0: holds attention probabilities [.., t, t] written by a causal
-  // attention forward (zero above the diagonal); reset by any host write.
+  // attention forward (zero above the diagonal); reset by any host write
+  // and by a kernel_dispatch_v2 that receives the tensor.
   uint32_t causal_t = 0;
+  // t > 0: holds tensor_causal_mask(t) (0 on and below the diagonal, -1e9
+  // above), as built by it or verified once; reset like causal_t.
+  uint32_t causal_mask_t = 0;
 };
 
 // One tensor handle (metal.rs:280-296 TensorBuffer).  The i64 handle the ABI

@@ -680,6 +680,7 @@ void malus_tensor_write(int64_t h, const void* src, size_t bytes) {
   if (bytes > t->bytes()) fail("malus: tensor_write of %zu bytes into a %zu-byte tensor", bytes, t->bytes());
   upload(t->data(), src, bytes);
   t->st->causal_t = 0;
+  t->st->causal_mask_t = 0;
   t->write_seq = enqueue_mark("tensor_write");
   API_CATCH()
 }
@@ -710,6 +711,7 @@ int64_t tensor_causal_mask(int64_t tsz) {
   size_t sh[2] = {(size_t)tsz, (size_t)tsz};
   TensorBuffer* t = alloc_tensor(F32, sh, 2);
   k::causal_mask(t->f32(), (size_t)tsz, stream());
+  t->st->causal_mask_t = (uint32_t)tsz;
   t->write_seq = enqueue_mark("causal_mask");
   return H(t);
   API_CATCH(0)

@@ -617,6 +617,7 @@ static void attn_need_f32(const char* what, std::initializer_list<const TensorBu
 }
 static void attn_need_causal_mask(const char* what, const TensorBuffer* mk, size_t t) {
   if (!mk->st) fail("malus: %s: the mask has no device storage", what);
+  if (mk->st->causal_mask_t == (uint32_t)t && mk->len == t * t) return;  // built by tensor_causal_mask(t)
   std::vector<float> m(t * t);
   download(m.data(), mk, m.size() * sizeof(float));
   for (size_t i = 0; i < t; ++i)
@@ -624,6 +625,7 @@ static void attn_need_causal_mask(const char* what, const TensorBuffer* mk, size
       if (m[i * t + j] != (j > i ? -1e9f : 0.0f))
         fail("malus: %s: causal=1 needs the causal mask (0 on/below the diagonal, -1e9 above); element [%zu,%zu] is %g",
              what, i, j, (double)m[i * t + j]);
+  mk->st->causal_mask_t = (uint32_t)t;  // verified: later calls skip the download
 }
 static void attn_need_causal_probs(const char* what, const TensorBuffer* p, size_t t) {
   if (!p->st || p->st->causal_t != (uint32_t)t)
