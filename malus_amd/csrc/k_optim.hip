@@ -62,12 +62,15 @@ __global__ __launch_bounds__(256) void k_adam_l2(const float* __restrict__ p, co
 // tensors.  The segment table travels by value in the kernel arguments (no
 // upload).  Block b covers 4096 floats (1024 float4, four per thread) of the
 // segment whose chunk range holds b; chunks never straddle segments.
-constexpr int kAdamMaxSegs = 48;  // 3.3 KB of kernel arguments
+// 56 segments: the C5 model's 52 parameter tensors in one launch (one
+// ramp-up and drain instead of two), 3.8 KB of kernel arguments.
+constexpr int kAdamMaxSegs = 56;
 struct AdamTable {
   AdamSeg seg[kAdamMaxSegs];
   uint32_t first_chunk[kAdamMaxSegs + 1];  // prefix sums of the segments' chunk counts
   int count;
 };
+static_assert(sizeof(AdamTable) + 64 <= 4096, "the segment table travels in the 4 KB of kernel arguments");
 
 // bc (optional): the two bias corrections read from device memory instead of
 // the arguments, so a captured step can take each step's values from a
