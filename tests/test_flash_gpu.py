@@ -182,7 +182,7 @@ def test_gpt_flash_attention_vs_oracle(rt, cfg):
     worst = max(normwise_err(grads[i], og.grad(i)) for i in range(og.nparams))
     print(f"flash {cfg}: loss {loss:.7f} oracle {wloss:.7f}, worst gradient error {worst:.2e}")
     assert abs(loss - wloss) <= 1e-5 * abs(wloss)
-    assert worst <= 1e-4
+    assert worst <= 3e-5  # the model tests' gradient bar (measured 1.7e-6 .. 5.2e-6)
 
 
 def test_gpt_flash_steps_deterministic_and_graph_equal(rt):

@@ -1,8 +1,8 @@
 """End-to-end parity of the workload drivers against the CPU oracle:
 examples/xor.ml (C1), the toy char-nanoGPT (C4) and the Karpathy
 char-nanoGPT (C5).  Loss trajectories: within 1e-3 relative (north star);
-single-step gradients: normwise 1e-4 (per-op 1e-5 errors compound through
-~40 dependent ops per block)."""
+single-step gradients: normwise 3e-5 (per-op 1e-5 errors compound through
+~40 dependent ops per block; measured worst 2.5e-6 at C4, 7.0e-6 at C5)."""
 import ctypes as C
 import os
 
@@ -112,9 +112,10 @@ def test_gpt_c4_loss_and_grads_vs_oracle(rt):
     try:
         loss = g.loss_and_grads(x, y)
         wloss = og.loss_and_grads(x, y)
-        assert abs(loss - wloss) <= 1e-5 * abs(wloss), (loss, wloss)
         worst = max(normwise_err(g.grad(i), og.grad(i)) for i in range(og.nparams))
-        assert worst <= 1e-4, f"worst normwise gradient error {worst:.2e}"
+        print(f"loss rel {abs(loss - wloss) / abs(wloss):.2e}, worst normwise gradient error {worst:.2e}")
+        assert abs(loss - wloss) <= 1e-5 * abs(wloss), (loss, wloss)
+        assert worst <= 3e-5, f"worst normwise gradient error {worst:.2e}"
     finally:
         g.close()
 
@@ -200,8 +201,9 @@ def test_gpt_c5_one_step_vs_oracle(rt):
     try:
         loss = g.loss_and_grads(x, y)
         wloss = og.loss_and_grads(x, y)
-        assert abs(loss - wloss) <= 1e-5 * abs(wloss), (loss, wloss)
         worst = max(normwise_err(g.grad(i), og.grad(i)) for i in range(og.nparams))
-        assert worst <= 1e-4, f"worst normwise gradient error {worst:.2e}"
+        print(f"loss rel {abs(loss - wloss) / abs(wloss):.2e}, worst normwise gradient error {worst:.2e}")
+        assert abs(loss - wloss) <= 1e-5 * abs(wloss), (loss, wloss)
+        assert worst <= 3e-5, f"worst normwise gradient error {worst:.2e}"
     finally:
         g.close()
