@@ -304,6 +304,7 @@ template <int BX, bool KC>
 struct DmaSlab {
   static constexpr int SIZE = BX * BK;        // floats
   static constexpr int PER_WAVE = SIZE / 1024;  // 1 KB instructions per wave (4 waves)
+  static constexpr int READS = KC ? 2 : 4;    // LDS read instructions of one 32-row fragment
   int off[PER_WAVE];                          // byte offset of this lane's chunk at k0 = 0
 
   // x0: first row/column of the tile.  fx maps the operand's free index x
@@ -387,10 +388,17 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   constexpr int BM = 64 * TM, BN = 64 * TN;
   using SlabA = DmaSlab<BM, !TA>;  // A [M][K] is k-contiguous
   using SlabB = DmaSlab<BN, TB>;   // B^T [N][K] is k-contiguous
-  // NS-stage ring: slab kt + NS - 1 is in flight while slab kt is consumed
-  constexpr int NS = 2, PER_SLAB = SlabA::PER_WAVE + SlabB::PER_WAVE;
-  __shared__ __attribute__((aligned(1024))) float As[NS][SlabA::SIZE];
-  __shared__ __attribute__((aligned(1024))) float Bs[NS][SlabB::SIZE];
+  // Two-stage ring of KS 16-deep slabs per stage: stage st + 1 is in
+  // flight while stage st is consumed.  Under autocast (BF) a slab's MFMA
+  // work is one bf16 instruction per accumulator, so the barrier and the
+  // fragment reads dominate; two slabs per stage halve the barriers and let
+  // the second slab's reads overlap the first slab's MFMAs (f32 K steps are
+  // long enough that one slab per stage measured faster).
+  constexpr int NS = 2, KS = BF && (BM + BN <= 256) ? 2 : 1;
+  // LDS reads of one slab's fragments (lgkmcnt is 4 bits)
+  constexpr int READS = TM * SlabA::READS + TN * SlabB::READS;
+  __shared__ __attribute__((aligned(1024))) float As[NS][KS][SlabA::SIZE];
+  __shared__ __attribute__((aligned(1024))) float Bs[NS][KS][SlabB::SIZE];
 
   const int nt = gridDim.x;
   int tile = blockIdx.x;
@@ -441,45 +449,68 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
     KCursor<MAP> ka, kb;
     ka.init(fak, kbeg);
     kb.init(fbk, kbeg);
+    const int nst = (nk + KS - 1) / KS;
+    auto issue_stage = [&](int st, int buf) {
 #pragma unroll
-    for (int p = 0; p < NS - 1; ++p)
-      if (p < nk) {
-        sa.issue(ra, As[p], wave, ka.bytes(fak));
-        sb.issue(rb, Bs[p], wave, kb.bytes(fbk));
-        ka.advance(fak);
-        kb.advance(fbk);
-      }
+      for (int u = 0; u < KS; ++u)
+        if (st * KS + u < nk) {
+          sa.issue(ra, As[buf][u], wave, ka.bytes(fak));
+          sb.issue(rb, Bs[buf][u], wave, kb.bytes(fbk));
+          ka.advance(fak);
+          kb.advance(fbk);
+        }
+    };
+    if (nst > 0) issue_stage(0, 0);
     int cur = 0;
-    for (int kt = 0; kt < nk; ++kt) {
-      // slab kt has landed once at most the slabs issued after it are in
-      // flight (this wave's loads complete in order); the barrier makes
-      // every wave's part visible and retires the reads of stage kt - 1
-      if (kt + NS - 2 < nk) waitcnt_vm<(NS - 2) * PER_SLAB>();
-      else waitcnt_vm<0>();
+    for (int st = 0; st < nst; ++st) {
+      // only stage st is in flight (this wave's loads complete in order); the
+      // barrier makes every wave's part visible and retires the reads of
+      // stage st - 1
+      waitcnt_vm<0>();
       __builtin_amdgcn_s_barrier();
-      float fa[TM][8], fb[TN][8];
+      const bool two = KS == 2 && st * KS + 1 < nk;
+      float fa[KS][TM][8], fb[KS][TN][8];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) SlabA::frag(As[cur], wm + 32 * i, fa[i]);
+      for (int i = 0; i < TM; ++i) SlabA::frag(As[cur][0], wm + 32 * i, fa[0][i]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur], wn + 32 * j, fb[j]);
+      for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][0], wn + 32 * j, fb[0][j]);
       __builtin_amdgcn_sched_barrier(0);
-      // stage kt - 1 (= kt + NS - 1 mod NS) was last read before the barrier
-      const int nxt = cur == 0 ? NS - 1 : cur - 1;
-      if (kt + NS - 1 < nk) {
-        sa.issue(ra, As[nxt], wave, ka.bytes(fak));
-        sb.issue(rb, Bs[nxt], wave, kb.bytes(fbk));
-        ka.advance(fak);
-        kb.advance(fbk);
+      // stage st - 1 (the other buffer) was last read before the barrier
+      if (st + 1 < nst) issue_stage(st + 1, cur ^ 1);
+      if constexpr (KS == 2) {
+        if (two) {
+#pragma unroll
+          for (int i = 0; i < TM; ++i) SlabA::frag(As[cur][KS - 1], wm + 32 * i, fa[KS - 1][i]);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][KS - 1], wn + 32 * j, fb[KS - 1][j]);
+          // LDS reads complete in order: the first slab's are done when at
+          // most the second slab's READS are outstanding
+          if constexpr (READS <= 15) asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(READS) : "memory");
+          else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        } else {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+      } else {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the fragment reads above
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the fragment reads above
       __builtin_amdgcn_sched_barrier(0);
       // a wave with MFMAs to issue goes ahead of the CU's other waves (measured
       // 1 % on the C5 step; raising it from the barrier on instead lost 2 %)
       __builtin_amdgcn_s_setprio(1);
-      mfma_kstep<TM, TN, BF>(fa, fb, acc);
+      mfma_kstep<TM, TN, BF>(fa[0], fb[0], acc);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
-      cur = cur == NS - 1 ? 0 : cur + 1;
+      if constexpr (KS == 2) {
+        if (two) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_s_setprio(1);
+          mfma_kstep<TM, TN, BF>(fa[KS - 1], fb[KS - 1], acc);
+          __builtin_amdgcn_s_setprio(0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      cur ^= 1;
     }
     __syncthreads();  // every wave is done with the stages before they are reused
   };
