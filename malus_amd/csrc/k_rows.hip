@@ -378,9 +378,11 @@ __global__ __launch_bounds__(256) void k_layernorm_bwd_scale_rows32(const float*
     const float4* yr = reinterpret_cast<const float4*>(y + row * axis);
     const float4* dr = reinterpret_cast<const float4*>(dout + row * axis);
     float yv[4 * NV], dv[4 * NV];
+    float4 av[NV];  // the addend row, loaded with y and dout (one memory round trip per row)
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const float4 a = yr[hl + 32 * j], b = dr[hl + 32 * j];
+      if (addend) av[j] = reinterpret_cast<const float4*>(addend + row * axis)[hl + 32 * j];
       yv[4 * j] = a.x; yv[4 * j + 1] = a.y; yv[4 * j + 2] = a.z; yv[4 * j + 3] = a.w;
       dv[4 * j] = b.x; dv[4 * j + 1] = b.y; dv[4 * j + 2] = b.z; dv[4 * j + 3] = b.w;
     }
@@ -412,10 +414,9 @@ __global__ __launch_bounds__(256) void k_layernorm_bwd_scale_rows32(const float*
       yv[e] = numer * inv_sigma;
     }
     if (addend) {
-      const float4* ar = reinterpret_cast<const float4*>(addend + row * axis);
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
-        const float4 a = ar[hl + 32 * j];
+        const float4 a = av[j];
         yv[4 * j] = a.x + yv[4 * j]; yv[4 * j + 1] = a.y + yv[4 * j + 1];
         yv[4 * j + 2] = a.z + yv[4 * j + 2]; yv[4 * j + 3] = a.w + yv[4 * j + 3];
       }
