@@ -394,7 +394,10 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   // fragment reads dominate; two slabs per stage halve the barriers and let
   // the second slab's reads overlap the first slab's MFMAs (f32 K steps are
   // long enough that one slab per stage measured faster).
-  constexpr int NS = 2, KS = BF && (BM + BN <= 256) ? 2 : 1;
+  // (Three- and four-stage rings measured no faster for either precision.)
+  constexpr bool BFS = BF && (BM + BN <= 256);
+  constexpr int NS = 2, KS = BFS ? 2 : 1;
+  constexpr int PER_SLAB = SlabA::PER_WAVE + SlabB::PER_WAVE;  // DMA instructions per slab and wave
   // LDS reads of one slab's fragments (lgkmcnt is 4 bits)
   constexpr int READS = TM * SlabA::READS + TN * SlabB::READS;
   __shared__ __attribute__((aligned(1024))) float As[NS][KS][SlabA::SIZE];
@@ -477,13 +480,16 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
           kb.advance(fbk);
         }
     };
-    if (nst > 0) issue_stage(0, 0);
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p)
+      if (p < nst) issue_stage(p, p);
     int cur = 0;
     for (int st = 0; st < nst; ++st) {
-      // only stage st is in flight (this wave's loads complete in order); the
-      // barrier makes every wave's part visible and retires the reads of
-      // stage st - 1
-      waitcnt_vm<0>();
+      // stage st has landed once at most the NS - 2 full stages issued after
+      // it are in flight (this wave's loads complete in order); the barrier
+      // makes every wave's part visible and retires the reads of stage st - 1
+      if (st + NS - 2 < nst - 1) waitcnt_vm<(NS - 2) * KS * PER_SLAB>();
+      else waitcnt_vm<0>();
       __builtin_amdgcn_s_barrier();
       const bool two = KS == 2 && st * KS + 1 < nk;
       float fa[KS][TM][8], fb[KS][TN][8];
@@ -492,8 +498,9 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
 #pragma unroll
       for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][0], wn + 32 * j, fb[0][j]);
       __builtin_amdgcn_sched_barrier(0);
-      // stage st - 1 (the other buffer) was last read before the barrier
-      if (st + 1 < nst) issue_stage(st + 1, cur ^ 1);
+      // stage st - 1 (= st + NS - 1 mod NS) was last read before the barrier
+      const int nxt = cur == 0 ? NS - 1 : cur - 1;
+      if (st + NS - 1 < nst) issue_stage(st + NS - 1, nxt);
       if constexpr (KS == 2) {
         if (two) {
 #pragma unroll
@@ -527,7 +534,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      cur ^= 1;
+      cur = cur == NS - 1 ? 0 : cur + 1;
     }
     __syncthreads();  // every wave is done with the stages before they are reused
   };
