@@ -85,7 +85,38 @@ __global__ __launch_bounds__(256) void k_adam_l2_multi(const AdamTable t, AdamAr
   const AdamSeg& sg = t.seg[si];
   const size_t first = (size_t)(blockIdx.x - t.first_chunk[si]) * kAdamChunk, n = sg.n;
   const size_t end = first + kAdamChunk < n ? first + kAdamChunk : n;
-  if ((n & 3) == 0) {  // float4 path (segment bases are 256-byte aligned)
+  constexpr int PER = (int)(kAdamChunk / 4 / 256);  // float4 per thread in a whole chunk
+  if ((n & 3) == 0 && end - first == kAdamChunk && blockDim.x == 256) {
+    // Whole chunk: every load is issued before the first store (the outputs
+    // may alias the inputs, in place, so the compiler cannot hoist the next
+    // iteration's loads above this one's stores by itself).
+    const float4* P4 = reinterpret_cast<const float4*>(sg.p) + first / 4 + threadIdx.x;
+    const float4* G4 = reinterpret_cast<const float4*>(sg.g) + first / 4 + threadIdx.x;
+    const float4* M4 = reinterpret_cast<const float4*>(sg.m) + first / 4 + threadIdx.x;
+    const float4* V4 = reinterpret_cast<const float4*>(sg.v) + first / 4 + threadIdx.x;
+    float4 P[PER], G[PER], Mv[PER], V[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      P[j] = P4[256 * j];
+      G[j] = G4[256 * j];
+      Mv[j] = M4[256 * j];
+      V[j] = V4[256 * j];
+    }
+    float4* Po4 = reinterpret_cast<float4*>(sg.po) + first / 4 + threadIdx.x;
+    float4* Mo4 = reinterpret_cast<float4*>(sg.mo) + first / 4 + threadIdx.x;
+    float4* Vo4 = reinterpret_cast<float4*>(sg.vo) + first / 4 + threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      float4 Po, Mo, Vo;
+      adam_one(P[j].x, G[j].x, Mv[j].x, V[j].x, a, Po.x, Mo.x, Vo.x);
+      adam_one(P[j].y, G[j].y, Mv[j].y, V[j].y, a, Po.y, Mo.y, Vo.y);
+      adam_one(P[j].z, G[j].z, Mv[j].z, V[j].z, a, Po.z, Mo.z, Vo.z);
+      adam_one(P[j].w, G[j].w, Mv[j].w, V[j].w, a, Po.w, Mo.w, Vo.w);
+      Po4[256 * j] = Po;
+      Mo4[256 * j] = Mo;
+      Vo4[256 * j] = Vo;
+    }
+  } else if ((n & 3) == 0) {  // float4 path (segment bases are 256-byte aligned)
     for (size_t i = first / 4 + threadIdx.x; i < end / 4; i += blockDim.x) {
       const float4 P = reinterpret_cast<const float4*>(sg.p)[i], G = reinterpret_cast<const float4*>(sg.g)[i];
       const float4 Mv = reinterpret_cast<const float4*>(sg.m)[i], V = reinterpret_cast<const float4*>(sg.v)[i];
