@@ -36,6 +36,10 @@ struct Storage {
   // t > 0: holds tensor_causal_mask(t) (0 on and below the diagonal, -1e9
   // above), as built by it or verified once; reset like causal_t.
   uint32_t causal_mask_t = 0;
+  // t > 0: causal attention probabilities [.., t, t] whose 32 x 32 tiles
+  // wholly above the diagonal were never written (the fused backward reads
+  // only the tiles on and below it); attn_zero_upper_tiles fills them.
+  uint32_t upper_unwritten_t = 0;
 };
 
 // One tensor handle (metal.rs:280-296 TensorBuffer).  The i64 handle the ABI
@@ -102,6 +106,10 @@ void pool_release_graph(int graph);
 void upload(void* dst, const void* src, size_t bytes);
 // Device -> host copy after waiting for the producing work.
 void download(void* dst, const TensorBuffer* t, size_t bytes);
+// Fill the tiles a causal attention forward left unwritten
+// (Storage::upper_unwritten_t) before anything other than the fused
+// backward reads the tensor; no-op otherwise.
+void materialize_upper_tiles(TensorBuffer* t);
 
 // Device-side error flag (index out of range in gathers); checked at flush.
 int32_t* device_error_flag();
@@ -184,8 +192,12 @@ bool attn_scores_bwd(const float* dO, size_t ldo, size_t heads, const float* V, 
 // attn_scores_softmax, and with O non-null also O = P @ V (V [bh, t, hs])
 // from the same kernel: head b's row i, column d at O + (b / heads) * t * ldo
 // + (b % heads) * hs + i * ldo + d.  Same values as gemm(P, V).
+// causal && !full: the 32 x 32 tiles of P wholly above the diagonal are
+// not written (no reader of this P looks at them).
 bool attn_fwd(const float* Q, const float* K, const float* V, const float* scale, const float* mask, float* P, float* O,
-              size_t ldo, size_t heads, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s);
+              size_t ldo, size_t heads, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s, bool full = true);
+// The zero tiles attn_fwd(full = false) left unwritten: P [bh, t, t].
+void attn_zero_upper_tiles(float* P, size_t bh, size_t t, hipStream_t s);
 // attn_scores_bwd, and with dQ non-null also dQ = Dq + dS @ K (K, dQ, Dq
 // dense [bh, t, hs]; Dq may be null) from the same kernel.  Same values as
 // gemm(dS, K) with the addend.
@@ -199,9 +211,11 @@ struct AttnKV {
   float* dV;
   const float* Dv;
 };
+// causal && !full: dS's tiles wholly above the diagonal are not written (a
+// scratch dS that only this kernel reads).
 bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const float* P, const float* scale, float* dS,
               const float* K, float* dQ, const float* Dq, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s,
-              const AttnKV* kv = nullptr);
+              const AttnKV* kv = nullptr, bool full = true);
 // Flash attention (online softmax, no [bh, t, t] buffers): t any multiple
 // of 32, hs 32 or 64.  Forward: O = softmax(Q K^T * scale[0] (+ causal
 // mask)) @ V written at O + (b / heads) * t * ldo + (b % heads) * hs +

@@ -501,6 +501,7 @@ int64_t kernel_dispatch(uint64_t id, const int64_t* handles, size_t count) {
   KernelEntry e = lookup(id, "kernel_dispatch");
   std::vector<TensorBuffer*> in;
   for (size_t i = 0; i < count; ++i) in.push_back(T(handles[i]));
+  for (TensorBuffer* t : in) materialize_upper_tiles(t);
   // output: dtype and shape of inputs[0] (metal.rs:1878-1888)
   TensorBuffer* out = alloc_tensor(in[0]->dtype, in[0]->shape, in[0]->ndim);
   if (out->len == 0) return H(out);
@@ -539,8 +540,10 @@ int64_t kernel_dispatch_v2(uint64_t id, const int64_t* handles, size_t hc, const
   KernelEntry e = lookup(id, "kernel_dispatch_v2");
   std::vector<TensorBuffer*> in;
   for (size_t i = 0; i < hc; ++i) in.push_back(T(handles[i]));
-  for (TensorBuffer* t : in)  // an explicit kernel may write its tensor arguments
+  for (TensorBuffer* t : in) {  // an explicit kernel may write its tensor arguments
+    materialize_upper_tiles(t);
     if (t->st) t->st->causal_t = t->st->causal_mask_t = 0;
+  }
   TensorBuffer* out;
   if (out_ndim == 0) {  // inherit input 0's shape; dtype from the tag or input 0 (metal.rs:1973-1981)
     if (in.empty()) fail("malus: kernel_dispatch_v2: out_ndim==0 but no tensor inputs");

@@ -222,7 +222,7 @@ __device__ __forceinline__ int pair_tile(int w, int which) {
 template <int TT, int HS, bool CAUSAL>
 __device__ __forceinline__ void softmax_tile(const float* __restrict__ Qh, const float* Ks, const float* __restrict__ scale,
                                              const float* __restrict__ mask, float* __restrict__ Ph, int qt,
-                                             v16f (&acc)[TT / 32]) {
+                                             v16f (&acc)[TT / 32], bool full) {
   constexpr int NT = TT / 32;   // key tiles per row (= 32-row query tiles per head)
   constexpr int NKB = HS / 16;  // 16-deep k slabs
   constexpr int LD = HS + 4;
@@ -321,7 +321,7 @@ __device__ __forceinline__ void softmax_tile(const float* __restrict__ Qh, const
 #pragma unroll
         for (int c = 0; c < 4; ++c) o[c] = acc[t][4 * g + c] = acc[t][4 * g + c] / s;
       }
-      prow[key_group(t, g, lk)] = o;
+      if (t < live || full) prow[key_group(t, g, lk)] = o;
     }
 }
 
@@ -354,7 +354,7 @@ template <int TT, int HS, bool CAUSAL, bool PV>
 __global__ __launch_bounds__(256, 2) void k_attn_fwd(const float* __restrict__ Q, const float* __restrict__ Kh,
                                                     const float* __restrict__ V, const float* __restrict__ scale,
                                                     const float* __restrict__ mask, float* __restrict__ P,
-                                                    float* __restrict__ O, int ldo, int H) {
+                                                    float* __restrict__ O, int ldo, int H, bool full) {
   constexpr int NT = TT / 32;
   constexpr int LD = HS + 4;
   static_assert(NT % 2 == 0 && NT <= 8, "one pair of query tiles per wave");
@@ -370,8 +370,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const float* __restrict__ Q
   __syncthreads();
   v16f acc[NT];
   if (active) {
-    softmax_tile<TT, HS, CAUSAL>(Q + head, S, scale, mask, Ph, qa, acc);
-    softmax_tile<TT, HS, CAUSAL>(Q + head, S, scale, mask, Ph, qb, acc);
+    softmax_tile<TT, HS, CAUSAL>(Q + head, S, scale, mask, Ph, qa, acc, full);
+    softmax_tile<TT, HS, CAUSAL>(Q + head, S, scale, mask, Ph, qb, acc, full);
   }
   if constexpr (PV) {
     __syncthreads();  // every wave is done with K
@@ -388,15 +388,26 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const float* __restrict__ Q
 
 template <int TT, int HS>
 void launch(const float* Q, const float* K, const float* V, const float* scale, const float* mask, float* P, float* O,
-            int ldo, int H, int bh, bool causal, hipStream_t s) {
+            int ldo, int H, int bh, bool causal, bool full, hipStream_t s) {
   const dim3 grid(1, (unsigned)bh);  // one workgroup per head
   if (O) {
-    if (causal) k_attn_fwd<TT, HS, true, true><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H);
-    else k_attn_fwd<TT, HS, false, true><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H);
+    if (causal) k_attn_fwd<TT, HS, true, true><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, full);
+    else k_attn_fwd<TT, HS, false, true><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, true);
   } else {
-    if (causal) k_attn_fwd<TT, HS, true, false><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H);
-    else k_attn_fwd<TT, HS, false, false><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H);
+    if (causal) k_attn_fwd<TT, HS, true, false><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, full);
+    else k_attn_fwd<TT, HS, false, false><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, true);
   }
+}
+
+// Zero the 32 x 32 tiles of P [bh, TT, TT] wholly above the diagonal: one
+// 256-thread workgroup per (head, query tile), float4 stores.
+__global__ __launch_bounds__(256) void k_attn_zero_upper(float* __restrict__ P, int TT) {
+  const int NT = TT / 32, qt = (int)blockIdx.x % NT;
+  const size_t bh = blockIdx.x / NT;
+  const int first = 32 * (qt + 1), n4 = (TT - first) / 4;  // float4s per row right of the diagonal tile
+  float* rows = P + (bh * TT + 32 * (size_t)qt) * TT + first;
+  for (int f = threadIdx.x; f < 32 * n4; f += 256)
+    reinterpret_cast<v4f*>(rows + (size_t)(f / n4) * TT)[f % n4] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 }
 
 // One wave's query tile qt of the scores backward: dP^T = V dO^T from V
@@ -405,7 +416,7 @@ void launch(const float* Q, const float* K, const float* V, const float* scale, 
 template <int TT, int HS, bool CAUSAL>
 __device__ __forceinline__ void dscores_tile(const float* __restrict__ dOh, int ldo, const float* Vs,
                                              const float* __restrict__ Ph, const float* __restrict__ scale,
-                                             float* __restrict__ dSh, int qt, v16f (&acc)[TT / 32]) {
+                                             float* __restrict__ dSh, int qt, v16f (&acc)[TT / 32], bool full) {
   constexpr int NT = TT / 32;
   constexpr int NKB = HS / 16;
   constexpr int LD = HS + 4;
@@ -478,7 +489,7 @@ __device__ __forceinline__ void dscores_tile(const float* __restrict__ dOh, int 
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[t][4 * g + c] = 0.0f;
       }
-      srow[key_group(t, g, lk)] = o;
+      if (t < live || full) srow[key_group(t, g, lk)] = o;
     }
 }
 
@@ -507,7 +518,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ d
                                                     const float* __restrict__ V, const float* __restrict__ P,
                                                     const float* __restrict__ scale, float* __restrict__ dS,
                                                     const float* __restrict__ Kh, float* __restrict__ dQ,
-                                                    const float* __restrict__ Dq, AttnKV kv) {
+                                                    const float* __restrict__ Dq, AttnKV kv, bool full) {
   constexpr int NT = TT / 32;
   constexpr int LD = HS + 4;
   static_assert(NT % 2 == 0 && NT <= 8, "one pair of query tiles per wave");
@@ -525,8 +536,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ d
   __syncthreads();
   v16f acc[NT];
   if (active) {
-    dscores_tile<TT, HS, CAUSAL>(dOh, ldo, S, Ph, scale, dSh, qa, acc);
-    dscores_tile<TT, HS, CAUSAL>(dOh, ldo, S, Ph, scale, dSh, qb, acc);
+    dscores_tile<TT, HS, CAUSAL>(dOh, ldo, S, Ph, scale, dSh, qa, acc, full);
+    dscores_tile<TT, HS, CAUSAL>(dOh, ldo, S, Ph, scale, dSh, qb, acc, full);
   }
   if constexpr (DQ) {
     __syncthreads();  // every wave is done with V
@@ -561,18 +572,19 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ d
 
 template <int TT, int HS>
 void launch_bwd(const float* dO, int ldo, int H, const float* V, const float* P, const float* scale, float* dS,
-                const float* K, float* dQ, const float* Dq, int bh, bool causal, const AttnKV* kv, hipStream_t s) {
+                const float* K, float* dQ, const float* Dq, int bh, bool causal, const AttnKV* kv, bool full,
+                hipStream_t s) {
   const dim3 grid(1, (unsigned)bh);  // one workgroup per head
   const AttnKV a = kv ? *kv : AttnKV{};
   if (kv) {
-    if (causal) k_attn_bwd<TT, HS, true, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
-    else k_attn_bwd<TT, HS, false, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
+    if (causal) k_attn_bwd<TT, HS, true, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, full);
+    else k_attn_bwd<TT, HS, false, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, true);
   } else if (dQ) {
-    if (causal) k_attn_bwd<TT, HS, true, true, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
-    else k_attn_bwd<TT, HS, false, true, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
+    if (causal) k_attn_bwd<TT, HS, true, true, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, full);
+    else k_attn_bwd<TT, HS, false, true, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, true);
   } else {
-    if (causal) k_attn_bwd<TT, HS, true, false, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
-    else k_attn_bwd<TT, HS, false, false, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a);
+    if (causal) k_attn_bwd<TT, HS, true, false, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, full);
+    else k_attn_bwd<TT, HS, false, false, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, true);
   }
 }
 
@@ -584,19 +596,25 @@ bool attn_scores_supported(size_t bh, size_t t, size_t hs) {
 }
 
 bool attn_fwd(const float* Q, const float* K, const float* V, const float* scale, const float* mask, float* P, float* O,
-              size_t ldo, size_t heads, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s) {
+              size_t ldo, size_t heads, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s, bool full) {
   if (!attn_scores_supported(bh, t, hs)) return false;
   const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!aligned(Q) || !aligned(K) || !aligned(mask) || !aligned(P) || (!causal && !mask)) return false;
   if (O && (!V || !aligned(V) || !aligned(O) || ldo % 4 || heads == 0 || bh % heads || ldo < hs * heads)) return false;
   const int b = (int)bh, l = (int)ldo, H = (int)heads;
-  if (t == 256 && hs == 64) launch<256, 64>(Q, K, V, scale, mask, P, O, l, H, b, causal, s);
-  else if (t == 128 && hs == 64) launch<128, 64>(Q, K, V, scale, mask, P, O, l, H, b, causal, s);
-  else if (t == 64 && hs == 32) launch<64, 32>(Q, K, V, scale, mask, P, O, l, H, b, causal, s);
-  else if (t == 64 && hs == 64) launch<64, 64>(Q, K, V, scale, mask, P, O, l, H, b, causal, s);
+  if (t == 256 && hs == 64) launch<256, 64>(Q, K, V, scale, mask, P, O, l, H, b, causal, full, s);
+  else if (t == 128 && hs == 64) launch<128, 64>(Q, K, V, scale, mask, P, O, l, H, b, causal, full, s);
+  else if (t == 64 && hs == 32) launch<64, 32>(Q, K, V, scale, mask, P, O, l, H, b, causal, full, s);
+  else if (t == 64 && hs == 64) launch<64, 64>(Q, K, V, scale, mask, P, O, l, H, b, causal, full, s);
   else return false;
   MALUS_HIP(hipGetLastError());
   return true;
+}
+
+void attn_zero_upper_tiles(float* P, size_t bh, size_t t, hipStream_t s) {
+  if (!bh || t < 64 || t % 32 || bh * (t / 32) > 0x7fffffffu) return;
+  k_attn_zero_upper<<<(unsigned)(bh * (t / 32)), 256, 0, s>>>(P, (int)t);
+  MALUS_HIP(hipGetLastError());
 }
 
 bool attn_scores_softmax(const float* Q, const float* K, const float* scale, const float* mask, float* P, size_t bh,
@@ -606,7 +624,7 @@ bool attn_scores_softmax(const float* Q, const float* K, const float* scale, con
 
 bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const float* P, const float* scale, float* dS,
               const float* K, float* dQ, const float* Dq, size_t bh, size_t t, size_t hs, bool causal, hipStream_t s,
-              const AttnKV* kv) {
+              const AttnKV* kv, bool full) {
   if (!attn_scores_supported(bh, t, hs) || heads == 0 || bh % heads || ldo < hs * heads) return false;
   const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!aligned(dO) || !aligned(V) || !aligned(P) || !aligned(dS) || ldo % 4) return false;
@@ -615,10 +633,10 @@ bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const f
              (kv->Dk && !aligned(kv->Dk)) || (kv->Dv && !aligned(kv->Dv))))
     return false;
   const int b = (int)bh, l = (int)ldo, H = (int)heads;
-  if (t == 256 && hs == 64) launch_bwd<256, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);
-  else if (t == 128 && hs == 64) launch_bwd<128, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);
-  else if (t == 64 && hs == 32) launch_bwd<64, 32>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);
-  else if (t == 64 && hs == 64) launch_bwd<64, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, s);
+  if (t == 256 && hs == 64) launch_bwd<256, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, full, s);
+  else if (t == 128 && hs == 64) launch_bwd<128, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, full, s);
+  else if (t == 64 && hs == 32) launch_bwd<64, 32>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, full, s);
+  else if (t == 64 && hs == 64) launch_bwd<64, 64>(dO, l, H, V, P, scale, dS, K, dQ, Dq, b, causal, kv, full, s);
   else return false;
   MALUS_HIP(hipGetLastError());
   return true;

@@ -502,18 +502,17 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
       const int nxt = cur == 0 ? NS - 1 : cur - 1;
       if (st + NS - 1 < nst) issue_stage(st + NS - 1, nxt);
       if constexpr (KS == 2) {
-        if (two) {
+        // The second slab's fragments are read on every path, also in a last
+        // stage that holds one slab (an odd slab count; the values then go
+        // unused), so the waits below do not depend on a branch.
 #pragma unroll
-          for (int i = 0; i < TM; ++i) SlabA::frag(As[cur][KS - 1], wm + 32 * i, fa[KS - 1][i]);
+        for (int i = 0; i < TM; ++i) SlabA::frag(As[cur][KS - 1], wm + 32 * i, fa[KS - 1][i]);
 #pragma unroll
-          for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][KS - 1], wn + 32 * j, fb[KS - 1][j]);
-          // LDS reads complete in order: the first slab's are done when at
-          // most the second slab's READS are outstanding
-          if constexpr (READS <= 15) asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(READS) : "memory");
-          else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        } else {
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        }
+        for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][KS - 1], wn + 32 * j, fb[KS - 1][j]);
+        // LDS reads complete in order: the first slab's are done when at
+        // most the second slab's READS are outstanding
+        if constexpr (READS <= 15) asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(READS) : "memory");
+        else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       } else {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the fragment reads above
       }
@@ -525,14 +524,14 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (KS == 2) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
         if (two) {
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          __builtin_amdgcn_sched_barrier(0);
           __builtin_amdgcn_s_setprio(1);
           mfma_kstep<TM, TN, BF>(fa[KS - 1], fb[KS - 1], acc);
           __builtin_amdgcn_s_setprio(0);
-          __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
       cur = cur == NS - 1 ? 0 : cur + 1;
     }

@@ -443,7 +443,16 @@ void upload(void* dst, const void* src, size_t bytes) {
   sg.head += need;
 }
 
+void materialize_upper_tiles(TensorBuffer* t) {
+  if (!t || !t->st || !t->st->upper_unwritten_t) return;
+  const size_t tt = t->st->upper_unwritten_t;
+  k::attn_zero_upper_tiles(t->f32(), t->len / (tt * tt), tt, stream());
+  t->st->upper_unwritten_t = 0;
+  t->write_seq = enqueue_mark("attn_zero_upper");
+}
+
 void download(void* dst, const TensorBuffer* t, size_t bytes) {
+  materialize_upper_tiles(const_cast<TensorBuffer*>(t));
   flush_if_pending(const_cast<TensorBuffer*>(t));
   if (!bytes) return;
   if (!t->st->ptr) fail("malus: tensor %s has no device storage (an intermediate of a fused kernel)", shape_str(t).c_str());
@@ -650,6 +659,7 @@ float malus_tensor_get_f32(int64_t h, int64_t idx) {
   API_TRY
   TensorBuffer* t = T(h);
   if (idx < 0 || (size_t)idx >= t->len) fail("malus: tensor_get_f32 index %lld out of range for len %zu", (long long)idx, t->len);
+  materialize_upper_tiles(t);
   flush_if_pending(t);
   float v;
   MALUS_HIP(hipMemcpyAsync(&v, t->f32() + idx, sizeof(float), hipMemcpyDeviceToHost, stream()));
@@ -678,6 +688,7 @@ void malus_tensor_write(int64_t h, const void* src, size_t bytes) {
   API_TRY
   TensorBuffer* t = T(h);
   if (bytes > t->bytes()) fail("malus: tensor_write of %zu bytes into a %zu-byte tensor", bytes, t->bytes());
+  materialize_upper_tiles(t);  // a partial write keeps the rest
   upload(t->data(), src, bytes);
   t->st->causal_t = 0;
   t->st->causal_mask_t = 0;

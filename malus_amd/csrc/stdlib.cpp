@@ -1217,9 +1217,12 @@ int64_t attn_fwd_impl(int64_t hq, int64_t hk, int64_t hv, int64_t hscale, size_t
   const size_t psh[3] = {bh, T, T}, osh[2] = {B * T, C};
   TensorBuffer* p = alloc_tensor(F32, psh, 3);
   TensorBuffer* out = alloc_tensor(F32, osh, 2);
+  // P's tiles wholly above the diagonal stay unwritten: the fused VJP reads
+  // only the others, and any other reader first has them filled with zeros
   if (!k::attn_fwd(q->f32(), kk->f32(), v->f32(), sc->f32(), nullptr, p->f32(), out->f32(), C, H, bh, T, hs, true,
-                   stream()))
+                   stream(), /*full=*/false))
     fail("malus: attn_fwd: no fused kernel for t=%zu hs=%zu", T, hs);
+  p->st->upper_unwritten_t = (uint32_t)T;
   const uint64_t seq = enqueue_mark("attn_fwd");
   p->write_seq = seq;
   out->write_seq = seq;
@@ -1256,7 +1259,7 @@ void attn_bwd_all_impl(int64_t hda, int64_t hq, int64_t hk, int64_t hv, int64_t 
   TensorBuffer *oq = alloc_like(q), *ok = alloc_like(kk), *ov = alloc_like(v);
   const k::AttnKV kv{q->f32(), ok->f32(), Dk ? Dk->f32() : nullptr, ov->f32(), Dv ? Dv->f32() : nullptr};
   if (!k::attn_bwd(da->f32(), H * hs, H, v->f32(), p->f32(), sc->f32(), ds, kk->f32(), oq->f32(),
-                   Dq ? Dq->f32() : nullptr, bh, T, hs, true, stream(), &kv))
+                   Dq ? Dq->f32() : nullptr, bh, T, hs, true, stream(), &kv, /*full=*/false))  // ds: scratch
     fail("malus: attn_bwd_all: no fused kernel for t=%zu hs=%zu", T, hs);
   pool_free(ds, bucket);  // stream order: later users of the buffer run after the kernel
   const uint64_t seq = enqueue_mark("attn_bwd_all");

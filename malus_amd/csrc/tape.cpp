@@ -533,7 +533,9 @@ void backward(int64_t loss) {
           }
           break;
         }
-        // AttnOut's VJP (dP, dV), the softmax and scale VJPs, then Scores' (dQ, dK)
+        // AttnOut's VJP (dP, dV), the softmax and scale VJPs, then Scores' (dQ, dK);
+        // the GEMMs read P whole
+        materialize_upper_tiles(T(pr));
         if (nc) fold_grad(grads, v, [&](const TensorBuffer* o) { return attn_out_bwd_v(pr, dout, Bm, Tm, Hm, o, true); });
         if (na || nb) {
           int64_t ds = 0;

@@ -65,6 +65,10 @@ def _hazards(name, body):
         insts.append((t, in_asm))
         if t.startswith("s_endpgm"):
             break
+    # lgkmcnt is 4 bits: with 16 LDS operations issued after a read, any
+    # lgkmcnt wait retires it, so counts past 16 are the same state (this
+    # also bounds the walk around loops)
+    cap = 16
     reads, found = 0, []
     for k, (t, a) in enumerate(insts):
         if not (a and t.startswith("ds_read")):
@@ -94,11 +98,11 @@ def _hazards(name, body):
                 used = set().union(*(_regs(x) for x in ops)) if ops else set()
                 if op.startswith("ds_"):
                     if aa and op.startswith("ds_read") and not (used & pend):
-                        after += 1
+                        after = min(after + 1, cap)
                         j += 1
                         continue
                     if not (used & pend):
-                        after += 1
+                        after = min(after + 1, cap)
                         j += 1
                         continue
                 if used & pend:

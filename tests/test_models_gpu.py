@@ -176,6 +176,36 @@ def test_gpt_fusions_equal_separate_ops(rt, cfg):
         np.testing.assert_array_equal(pa[i], pb[i], err_msg=f"param {i}")
 
 
+@pytest.mark.parametrize("cfg", [dict(V=65, T=256, C=128, H=2, L=2, B=2),
+                                 dict(V=65, T=128, C=256, H=4, L=1, B=3)], ids=["t256hs64", "t128hs64"])
+def test_fused_attention_unwritten_tiles(rt, cfg):
+    """The fused attention forward leaves P's 32 x 32 tiles wholly above the
+    diagonal unwritten.  With the pool's buffers of P's size poisoned with
+    NaN, the fused VJP (which reads only the other tiles) and the composed
+    VJPs (GEMMs over P after the runtime fills those tiles with zeros) must
+    give the same gradients, bit for bit, and finite."""
+    x, y = tokens(cfg, 7000)
+    nbytes = cfg["B"] * cfg["H"] * cfg["T"] * cfg["T"]
+    out = []
+    for fv in (True, False):
+        poison = [rt.tensor(np.full(nbytes, np.nan, np.float32)) for _ in range(2 * cfg["L"])]
+        rt.free(*poison)
+        rt.L.malus_tape_set_fused_vjps(int(fv))
+        g = GpuGpt(rt, cfg, fused_forward=True)
+        try:
+            loss = g.loss_and_grads(x, y)
+            grads = [g.grad(i) for i in range(8 * cfg["L"] + 4)]
+        finally:
+            g.close()
+            rt.L.malus_tape_set_fused_vjps(1)
+        out.append((loss, grads))
+    (la, ga), (lb, gb) = out
+    assert np.isfinite(la) and la == lb
+    for i in range(len(ga)):
+        assert np.all(np.isfinite(ga[i])), f"grad {i}"
+        np.testing.assert_array_equal(ga[i], gb[i], err_msg=f"grad {i}")
+
+
 def test_gpt_c4_200_step_loss_trajectory(rt):
     g = GpuGpt(rt, C4)
     og = O.Gpt(**C4)
