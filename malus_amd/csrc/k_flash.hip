@@ -203,13 +203,34 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
 #pragma unroll
   for (int n = 0; n < NN; ++n) dq[n] = v16f{0};
   const int last = CAUSAL ? qt : NT - 1;
+  // Key tile j of K and V goes through LDS (rows padded to HS + 4 floats):
+  // one 16-byte global load per 4 floats, and both of K's orientations (the
+  // rows for S^T, the columns for dQ = dS K) read back from LDS.  (Fetching
+  // tile j + 1 into registers during tile j measured no faster and spilled.)
+  constexpr int LD = HS + 4, Q4 = HS / 4, PER = 32 * Q4 / 64;
+  __shared__ __attribute__((aligned(16))) float Ks[32 * LD], Vs[32 * LD];
+  v4f kn[PER], vn[PER];
+  auto fetch = [&](int j) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int f = lane + 64 * u;
+      kn[u] = *reinterpret_cast<const v4f*>(Kh + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
+      vn[u] = *reinterpret_cast<const v4f*>(Vh + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
+    }
+  };
   for (int j = 0; j <= last; ++j) {
+    fetch(j);
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {  // LDS ops of one wave run in order: the last tile's reads are done
+      const int f = lane + 64 * u;
+      *reinterpret_cast<v4f*>(Ks + (f / Q4) * LD + 4 * (f % Q4)) = kn[u];
+      *reinterpret_cast<v4f*>(Vs + (f / Q4) * LD + 4 * (f % Q4)) = vn[u];
+    }
     float ka[NKB][8], vr[NKB][8];  // A of S^T and dP^T: rows perm_row(x) of K_j, V_j
-    const int krow = 32 * j + perm_row(x);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      load8(Kh + (size_t)krow * HS + 16 * kb + 8 * lk, ka[kb]);
-      load8(Vh + (size_t)krow * HS + 16 * kb + 8 * lk, vr[kb]);
+      load8(Ks + perm_row(x) * LD + 16 * kb + 8 * lk, ka[kb]);
+      load8(Vs + perm_row(x) * LD + 16 * kb + 8 * lk, vr[kb]);
     }
     v16f st = v16f{0}, dp = v16f{0};
 #pragma unroll
@@ -223,7 +244,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) kc[n][h][e] = Kh[(size_t)(32 * j + 16 * h + 8 * lk + e) * HS + 32 * n + x];
+        for (int e = 0; e < 8; ++e) kc[n][h][e] = Ks[(16 * h + 8 * lk + e) * LD + 32 * n + x];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const bool masked = CAUSAL && j == qt && perm_index(r, lk) > x;
@@ -285,10 +306,41 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
     dkt[n] = v16f{0};
   }
   const int first = CAUSAL ? kt : 0;
+  // f32: query tile it of Q and dO goes through LDS (rows padded to HS + 4
+  // floats): one 16-byte global load per 4 floats, and both orientations
+  // (rows for S and dP, columns for dV^T = dO^T P and dK^T = Q^T dS) read
+  // back from LDS.  Under bf16 the products are too short to hide the
+  // staging's round trip: there the operands come straight from L2 (the LDS
+  // form measured 3 % faster at T = 256 but 3-20 % slower at T = 1024-4096).
+  constexpr bool STAGE = !BF;
+  constexpr int LD = HS + 4, Q4 = HS / 4, PER = 32 * Q4 / 64;
+  __shared__ __attribute__((aligned(16))) float Qs[STAGE ? 32 * LD : 1], Os[STAGE ? 32 * LD : 1];
   for (int it = first; it < NT; ++it) {
     const int i0 = 32 * it;
     v16f s = v16f{0}, dp = v16f{0};
-    {
+    if constexpr (STAGE) {
+      v4f qn[PER], on[PER];
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int f = lane + 64 * u;
+        qn[u] = *reinterpret_cast<const v4f*>(Qh + (size_t)(i0 + f / Q4) * HS + 4 * (f % Q4));
+        on[u] = *reinterpret_cast<const v4f*>(head_row(dO, bh, H, T, ldo, HS, i0 + f / Q4) + 4 * (f % Q4));
+      }
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {  // LDS ops of one wave run in order: the last tile's reads are done
+        const int f = lane + 64 * u;
+        *reinterpret_cast<v4f*>(Qs + (f / Q4) * LD + 4 * (f % Q4)) = qn[u];
+        *reinterpret_cast<v4f*>(Os + (f / Q4) * LD + 4 * (f % Q4)) = on[u];
+      }
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        float qa[8], oa[8];  // A: rows perm_row(x) of Q_i, dO_i
+        load8(Qs + perm_row(x) * LD + 16 * kb + 8 * lk, qa);
+        load8(Os + perm_row(x) * LD + 16 * kb + 8 * lk, oa);
+        s = slab<BF>(qa, kb_[kb], s);
+        dp = slab<BF>(oa, vb[kb], dp);
+      }
+    } else {
       const int qrow = i0 + perm_row(x);
       const float* dorow = head_row(dO, bh, H, T, ldo, HS, qrow);
 #pragma unroll
@@ -330,9 +382,15 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
         float oa[8], qa[8];  // A of dV^T = dO^T P and dK^T = Q^T dS: [i0 + 16 h + 8 lk + e][32 n + x]
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int q = i0 + 16 * h + 8 * lk + e;
-          oa[e] = head_row(dO, bh, H, T, ldo, HS, q)[32 * n + x];
-          qa[e] = Qh[(size_t)q * HS + 32 * n + x];
+          if constexpr (STAGE) {
+            const int q = 16 * h + 8 * lk + e;
+            oa[e] = Os[q * LD + 32 * n + x];
+            qa[e] = Qs[q * LD + 32 * n + x];
+          } else {
+            const int q = i0 + 16 * h + 8 * lk + e;
+            oa[e] = head_row(dO, bh, H, T, ldo, HS, q)[32 * n + x];
+            qa[e] = Qh[(size_t)q * HS + 32 * n + x];
+          }
         }
         dvt[n] = slab<BF>(oa, pb, dvt[n]);
         dkt[n] = slab<BF>(qa, db, dkt[n]);
