@@ -262,15 +262,25 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
       for (int n = 0; n < NN; ++n) dq[n] = slab<BF>(ab, kc[n][h], dq[n]);
     }
   }
-  // dQ[i0 + 8 (r >> 2) + 4 lk + (r & 3)][32 n + x]
+  // dQ[i0 + 8 (r >> 2) + 4 lk + (r & 3)][32 n + x] (+ Dq: every addend loaded before the first add)
   float* dqh = dQ + head;
+  auto off = [&](int n, int r) { return (size_t)(i0 + 8 * (r >> 2) + 4 * lk + (r & 3)) * HS + 32 * n + x; };
+  if (Dq) {
+    float a[NN][16];
 #pragma unroll
-  for (int n = 0; n < NN; ++n)
+    for (int n = 0; n < NN; ++n)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const size_t off = (size_t)(i0 + 8 * (r >> 2) + 4 * lk + (r & 3)) * HS + 32 * n + x;
-      dqh[off] = Dq ? Dq[head + off] + dq[n][r] : dq[n][r];
-    }
+      for (int r = 0; r < 16; ++r) a[n][r] = Dq[head + off(n, r)];
+#pragma unroll
+    for (int n = 0; n < NN; ++n)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dqh[off(n, r)] = a[n][r] + dq[n][r];
+  } else {
+#pragma unroll
+    for (int n = 0; n < NN; ++n)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dqh[off(n, r)] = dq[n][r];
+  }
 }
 
 // Backward, key-centric: dK (+ Dk) and dV (+ Dv) of key tile kt.
@@ -398,6 +408,16 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
     }
   }
   // dV[j0 + x][32 n + 8 g + 4 lk + c] = dvt[n][4 g + c] (+ Dv), dK likewise
+  // (the addends, where given, are all loaded before the first add)
+  v4f av[NN][4], ak[NN][4];
+#pragma unroll
+  for (int n = 0; n < NN; ++n)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const size_t off = head + (size_t)key * HS + 32 * n + 8 * g + 4 * lk;
+      if (Dv) av[n][g] = *reinterpret_cast<const v4f*>(Dv + off);
+      if (Dk) ak[n][g] = *reinterpret_cast<const v4f*>(Dk + off);
+    }
 #pragma unroll
   for (int n = 0; n < NN; ++n)
 #pragma unroll
@@ -409,8 +429,8 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
         wv[c] = dvt[n][4 * g + c];
         wk[c] = dkt[n][4 * g + c];
       }
-      if (Dv) wv = *reinterpret_cast<const v4f*>(Dv + off) + wv;
-      if (Dk) wk = *reinterpret_cast<const v4f*>(Dk + off) + wk;
+      if (Dv) wv = av[n][g] + wv;
+      if (Dk) wk = ak[n][g] + wk;
       *reinterpret_cast<v4f*>(dV + off) = wv;
       *reinterpret_cast<v4f*>(dK + off) = wk;
     }
