@@ -357,7 +357,7 @@ struct AdamSeg {
   float *po, *mo, *vo;
   size_t n;
 };
-constexpr size_t kAdamChunk = 4096;  // floats per workgroup
+constexpr size_t kAdamChunk = 1024;  // floats per workgroup
 // Every tensor of `segs` in one launch; same per-element expression as adam_l2.
 void adam_l2_multi(const AdamSeg* segs_host, int count, float lr, float b1, float b2, float omb1, float omb2, float bc1,
                    float bc2, float eps, float wd, hipStream_t s, const float* bc_dev = nullptr);
