@@ -246,7 +246,7 @@ void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, 
 // per chunk.  False when it does not split on the float4 path or walks
 // contiguous runs of rows instead.
 bool col_prod_split(size_t axis, size_t inner, uint32_t* nsplit, size_t* chunk, int* row_threads);
-// out[c] = the sum of partial[c * nsplit ..], as that reduction combines them.
+// out[c] = the sum over s of partial[s * cols + c], as that reduction combines them.
 void col_combine_sum(const float* partial, float* out, size_t cols, uint32_t nsplit, size_t axis, hipStream_t s);
 // Broadcast [outer, inner] back to [outer, axis, inner] (expand_axis).
 void expand_axis(const float* small, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);

@@ -151,7 +151,8 @@ __global__ __launch_bounds__(256) void k_row_split(const float* __restrict__ x, 
 // of a column are folded in rt order through LDS.  nsplit == 1 writes the
 // finalized value; otherwise partial[(o * inner + i) * nsplit + sp], so
 // that a column's partials form one contiguous row for the combining row
-// reduction.
+// reduction (row-major partials with k_col_combine_tree measured 3-6 %
+// slower on [65536, 1024]).
 template <int OP, int CT>
 __global__ __launch_bounds__(256) void k_col4(const float* __restrict__ x, const float* __restrict__ y,
                                               const float* __restrict__ mean, float* __restrict__ dst, size_t axis,
@@ -289,6 +290,77 @@ __global__ __launch_bounds__(256) void k_col_combine(const float* __restrict__ p
     __syncthreads();
   }
   if (g == 0 && i < inner) out[o * inner + i] = rfinal<OP>(red[0][lc], count);
+}
+
+// Combine split partials stored row-major ([o][sp][inner]: the layernorm
+// VJP's column partials, one contiguous row per split) in the order
+// k_row_wave<OP, VEC> reduces the same values stored column-major (a
+// column's nsplit partials contiguous, as k_col4 writes them): lane slot l
+// (0..63) folds, from rinit, the partials l, l + 64, ... (VEC: the runs of
+// four 4l .. 4l + 3, 4 (l + 64) .., one float4 per lane step) in order, then
+// the 64 slot sums go through wave_reduce's butterfly as lane 0 sees it
+// (level w: slot l += slot l + w for l < w, w = 32 .. 1).  So both layouts
+// give the same sums, bit for bit.  CC columns per block, G = 256 / CC slot
+// groups, 64 / G slots per thread.
+template <int OP, bool VEC, int CC>
+__global__ __launch_bounds__(256) void k_col_combine_tree(const float* __restrict__ partial, float* __restrict__ out,
+                                                          uint32_t nsplit, size_t inner, uint32_t count) {
+  constexpr int G = 256 / CC, LPT = kWave / G;
+  static_assert(kWave % G == 0, "whole lane slots per thread");
+  __shared__ float red[kWave][CC];
+  const int lc = threadIdx.x % CC, g = threadIdx.x / CC;
+  const size_t o = blockIdx.y;
+  const size_t i = (size_t)blockIdx.x * CC + lc;
+  const float* p = partial + o * nsplit * inner + i;
+  // step k reads, for every slot of the thread, its k-th run (VEC: four
+  // partials, else one) before folding any of them: one memory round trip
+  // per step
+  constexpr int RUN = VEC ? 4 : 1;
+  const uint32_t runs = VEC ? nsplit / 4 : nsplit;
+  float acc[LPT];
+#pragma unroll
+  for (int u = 0; u < LPT; ++u) acc[u] = rinit<OP>();
+  if (i < inner) {
+    for (uint32_t q0 = 0; q0 < runs; q0 += kWave) {
+      float v[LPT][RUN];
+#pragma unroll
+      for (int u = 0; u < LPT; ++u) {
+        const uint32_t q = q0 + g + u * G;
+#pragma unroll
+        for (int e = 0; e < RUN; ++e) v[u][e] = q < runs ? p[(size_t)(RUN * q + e) * inner] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < LPT; ++u) {
+        if (q0 + g + u * G < runs) {
+#pragma unroll
+          for (int e = 0; e < RUN; ++e) acc[u] = rcomb<OP>(acc[u], v[u][e]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < LPT; ++u) red[g + u * G][lc] = acc[u];
+  __syncthreads();
+#pragma unroll
+  for (int w = kWave / 2; w > 0; w >>= 1) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int l = g + u * G;
+      if (l < w) red[l][lc] = rcomb<OP>(red[l][lc], red[l + w][lc]);
+    }
+    __syncthreads();
+  }
+  if (g == 0 && i < inner) out[o * inner + i] = rfinal<OP>(red[0][lc], count);
+}
+
+// Launch k_col_combine_tree over [outer][nsplit][inner] partials.
+template <int OP>
+void launch_col_combine_tree(const float* partial, float* out, size_t outer, uint32_t nsplit, size_t inner,
+                             uint32_t count, hipStream_t s) {
+  constexpr int CC = 8;  // 4.4 us for the C5 layernorm scale (384 columns, 512 splits); 16: 5.5 us
+  const dim3 grid((unsigned)((inner + CC - 1) / CC), (unsigned)outer);
+  if (nsplit % 4 == 0) k_col_combine_tree<OP, true, CC><<<grid, 256, 0, s>>>(partial, out, nsplit, inner, count);
+  else k_col_combine_tree<OP, false, CC><<<grid, 256, 0, s>>>(partial, out, nsplit, inner, count);
 }
 
 __global__ __launch_bounds__(256) void k_expand_axis(const float* __restrict__ small, float* __restrict__ out,
@@ -557,12 +629,7 @@ bool col_prod_split(size_t axis, size_t inner, uint32_t* nsplit, size_t* chunk, 
 }
 
 void col_combine_sum(const float* partial, float* out, size_t cols, uint32_t nsplit, size_t axis, hipStream_t s) {
-  if (nsplit % 4 == 0)
-    k_row_wave<R_SUM, true><<<(unsigned)((cols + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, cols, nsplit,
-                                                                        (uint32_t)axis, true, false);
-  else
-    k_row_wave<R_SUM, false><<<(unsigned)((cols + 3) / 4), 256, 0, s>>>(partial, nullptr, nullptr, out, cols, nsplit,
-                                                                         (uint32_t)axis, true, false);
+  launch_col_combine_tree<R_SUM>(partial, out, 1, nsplit, cols, (uint32_t)axis, s);
   MALUS_HIP(hipGetLastError());
 }
 

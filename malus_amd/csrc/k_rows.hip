@@ -355,8 +355,11 @@ __global__ __launch_bounds__(256) void k_layernorm_bwd_rows32(const float* __res
 // VJP): each half-wave sums its rows' products in k order, then the eight
 // half-waves' sums are added in order.  That is exactly the partial the
 // column reduction (k_col4 with 8 row-threads over 32-row chunks) writes,
-// so the combined dw is the separate reduction's, bit for bit.  Partials go
-// column-major: partial[c * nsplit + chunk].
+// so the combined dw is the separate reduction's, bit for bit.  The
+// partials go row-major, partial[chunk * axis + c] (one contiguous row per
+// workgroup; the reduction's column-major layout, a 4-byte store per column
+// at the stride of the chunk count, made this kernel 9 % slower at C5), and
+// col_combine_sum adds them in the order the reduction's combine uses.
 template <int NV>
 __global__ __launch_bounds__(256) void k_layernorm_bwd_scale_rows32(const float* __restrict__ y,
                                                                     const float* __restrict__ var,
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(256) void k_layernorm_bwd_scale_rows32(const float*
     float r = red[0][col];
 #pragma unroll
     for (int h = 1; h < 8; ++h) r = r + red[h][col];
-    partial[(size_t)col * nsplit + blockIdx.x] = r;
+    partial[(size_t)blockIdx.x * axis + col] = r;
   }
 }
 

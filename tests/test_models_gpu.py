@@ -146,8 +146,13 @@ def test_gpt_fused_optimizer_equals_op_by_op(rt):
                                  dict(V=65, T=128, C=256, H=4, L=2, B=3),   # hs 64, T 128
                                  dict(V=65, T=64, C=384, H=6, L=1, B=16),   # C5 width: LN-scale VJP at 384 columns
                                  dict(V=65, T=20, C=384, H=6, L=1, B=3),    # 60 rows: a ragged last row block
-                                 dict(V=65, T=16, C=512, H=8, L=1, B=6)],   # 512 columns
-                         ids=["t64hs16", "t64hs32", "t256hs64", "t128hs64", "c384", "c384ragged", "c512"])
+                                 dict(V=65, T=16, C=512, H=8, L=1, B=6),    # 512 columns
+                                 # the LN-scale VJP's column partials over 198 and 300 row chunks: combined in
+                                 # two lane steps, singly (198) and in runs of four (300)
+                                 dict(V=65, T=64, C=384, H=6, L=1, B=99),
+                                 dict(V=65, T=64, C=384, H=6, L=1, B=150)],
+                         ids=["t64hs16", "t64hs32", "t256hs64", "t128hs64", "c384", "c384ragged", "c512", "c384s198",
+                              "c384s300"])
 def test_gpt_fusions_equal_separate_ops(rt, cfg):
     """The forward fusions (attention scores + scale + mask + softmax in one
     kernel where the head size allows it, else scale + mask + softmax in one
