@@ -204,3 +204,38 @@ def test_reference_kernel_corpus_lowers_and_compiles():
             rtc(src)
             count += 1
     assert count >= 36  # 30 stdlib kernels + the examples' user kernels
+
+
+def test_mutated_programs_lower_or_fail_cleanly():
+    """Malformed input: seeded truncations, deletions, insertions and byte
+    substitutions of the test programs either lower to kernels or raise the
+    emitter's error (a RuntimeError with the library's message); none ends
+    the process, and the emitter keeps working afterwards."""
+    import random
+
+    rng = random.Random(2024)
+    alphabet = " \n\t:()[]<>,.=+-*/%!&|^~#\"'abcxyz019_"
+    bases = [PROGRAM, SIGMOID_BACKWARD]
+    lowered = rejected = 0
+    for _ in range(3000):
+        q = rng.choice(bases)
+        at = rng.randrange(len(q))
+        kind = rng.randrange(4)
+        if kind == 0:
+            q = q[:at]
+        elif kind == 1:
+            q = q[:at] + rng.choice(alphabet) + q[at + 1:]
+        elif kind == 2:
+            q = q[:at] + q[at + 1 + rng.randrange(8):]
+        else:
+            q = q[:at] + rng.choice(alphabet) * (1 + rng.randrange(4)) + q[at:]
+        try:
+            r = M.compile_kernels(q, BUILTINS if rng.random() < 0.5 else ())
+            assert all(src for _, _, src in r.entries)
+            lowered += 1
+        except RuntimeError as e:
+            assert str(e), "an emitter error carries a message"
+            rejected += 1
+    assert lowered and rejected
+    (name, _, _), = M.compile_kernels(SIGMOID_BACKWARD).entries
+    assert name == "sigmoid_backward"
