@@ -646,7 +646,15 @@ __global__ __launch_bounds__(64) void k_split_reduce4(const v4f_t* __restrict__ 
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc += t[u];
     }
-    for (; s < nsplit; ++s) acc += partial[(size_t)s * mn4 + i];
+    if (s < nsplit) {  // the last (at most 7) partials, also loaded before their adds
+      v4f_t t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s + u < nsplit) t[u] = partial[(size_t)(s + u) * mn4 + i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s + u < nsplit) acc += t[u];
+    }
     C[i] = D ? D[i] + acc : acc;
   }
 }
