@@ -565,7 +565,9 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   // of stalling every workgroup's epilogue at once.  Small wave tiles only:
   // it holds another TM * TN * 16 registers, so only instances that read
   // one (the dense GEMMs that take an addend, the GELU VJP, the grouped
-  // accumulation) carry it.
+  // accumulation) carry it.  Without it (4 -> 6 workgroups per CU on the
+  // 128x64 tiles) the C5 step measured 0.7 % slower for the GELU VJP alone
+  // and 1.7 % slower for the dense forms.
   constexpr bool PF = TM * TN <= 2 && ((EPI == 0 && !MAP) || EPI == 2 || EPI == 3);
   const float* pre_src = EPI == 2 ? E : D;
   v16f pre[PF ? TM : 1][PF ? TN : 1];
