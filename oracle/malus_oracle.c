@@ -150,6 +150,7 @@ void or_broadcast_fwd(int op, const float* a, const size_t* ash, int and_,
 
 /* codegen-gpu/lib.rs:400-418 synthesize_scalar_builtin */
 void or_scalar_op(int op, int scalar_on_right, const float* a, size_t n, float s, float* out) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < n; ++i)
         out[i] = scalar_on_right ? apply_op(op, a[i], s) : apply_op(op, s, a[i]);
 }
@@ -169,6 +170,8 @@ static float gelu_f(float x) {
  * amplifies that last-bit choice (1 + e rounds at e's spacing), so the
  * platform-independent correctly rounded functions are the restatement. */
 void or_unary(int op, const float* a, size_t n, float* out) {
+    if (op < OR_RELU || op > OR_GELU) die("bad unary op");
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < n; ++i) {
         float x = a[i];
         switch (op) {
@@ -179,8 +182,7 @@ void or_unary(int op, const float* a, size_t n, float* out) {
         case OR_LOG: out[i] = (float)log((double)x); break;
         case OR_SQRT: out[i] = sqrtf(x); break;
         case OR_ABS: out[i] = fabsf(x); break;
-        case OR_GELU: out[i] = gelu_f(x); break;
-        default: die("bad unary op");
+        default: out[i] = gelu_f(x); break; /* OR_GELU */
         }
     }
 }
@@ -336,38 +338,104 @@ void or_causal_mask(size_t t, float* out) {
 }
 
 void or_permute(const float* x, const size_t* shape, int ndim, const size_t* perm, float* out) {
-    /* permute_by_perm, metal.rs:1346-1382 */
+    /* permute_by_perm, metal.rs:1346-1382: out[flat] = x[source index of
+     * flat].  A pure copy, so visiting the output rows in parallel, with the
+     * source offset computed once per row, gives the same result. */
+    if (ndim <= 0) { out[0] = x[0]; return; }
     size_t in_st[8], os[8];
     in_st[ndim - 1] = 1;
     for (int i = ndim - 2; i >= 0; --i) in_st[i] = in_st[i + 1] * shape[i + 1];
     for (int d = 0; d < ndim; ++d) os[d] = shape[perm[d]];
     size_t total = prod(os, ndim);
-    for (size_t flat = 0; flat < total; ++flat) {
-        size_t rem = flat, in_flat = 0;
-        for (int d = ndim - 1; d >= 0; --d) {
+    size_t inner = os[ndim - 1], step = in_st[perm[ndim - 1]];
+    if (total == 0) return;
+    size_t rows = total / inner;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (size_t row = 0; row < rows; ++row) {
+        size_t rem = row, in_flat = 0;
+        for (int d = ndim - 2; d >= 0; --d) {
             size_t id = rem % os[d];
             rem /= os[d];
             in_flat += id * in_st[perm[d]];
         }
-        out[flat] = x[in_flat];
+        float* o = out + row * inner;
+        for (size_t j = 0; j < inner; ++j) o[j] = x[in_flat + j * step];
     }
 }
 
 /* tensor_matmul_cpu, metal.rs:698-800: out[i,j] accumulates a[i,k]*b[k,j]
- * in k order from 0.0.  The k-outer/j-inner loop below gives every output
- * element the identical addition sequence while vectorizing over j. */
-static void mm_rows(const float* a, const float* b, float* c, size_t m, size_t k, size_t n) {
-#pragma omp parallel for num_threads(g_threads) schedule(static)
-    for (size_t i = 0; i < m; ++i) {
-        float* crow = c + i * n;
-        for (size_t j = 0; j < n; ++j) crow[j] = 0.0f;
-        const float* arow = a + i * k;
-        for (size_t kk = 0; kk < k; ++kk) {
-            float av = arow[kk];
-            const float* brow = b + kk * n;
-            for (size_t j = 0; j < n; ++j) crow[j] += av * brow[j];
+ * in k order from 0.0, each product and each sum rounded to f32.
+ *
+ * The loops below keep that per-element sequence exactly and only change
+ * which elements are in flight together: a 4-row x 32-column tile of out is
+ * held in 16 eight-float vectors while k runs 0..K-1 (GCC vector extensions:
+ * a vector multiply and a vector add are eight independent f32 roundings,
+ * and -ffp-contract=off keeps them unfused).  Rows and columns that do not
+ * fill a tile take the scalar loop with the same order.  Tiles are split
+ * over OpenMP threads by column panel, so a K x 32 panel of b stays in the
+ * core's cache while its row tiles pass. */
+typedef float v8f __attribute__((vector_size(32)));
+#define MM_TR 6
+#define MM_TC 16
+
+static void mm_scalar(const float* a, const float* b, float* c, size_t k, size_t n,
+                      size_t i0, size_t i1, size_t j0, size_t j1) {
+    for (size_t i = i0; i < i1; ++i)
+        for (size_t j = j0; j < j1; ++j) {
+            float acc = 0.0f;
+            for (size_t kk = 0; kk < k; ++kk) acc += a[i * k + kk] * b[kk * n + j];
+            c[i * n + j] = acc;
+        }
+}
+
+static void mm_tile(const float* a, const float* b, float* c, size_t k, size_t n, size_t i0, size_t j0) {
+    v8f acc[MM_TR][MM_TC / 8];
+#pragma GCC unroll 8
+    for (int r = 0; r < MM_TR; ++r)
+#pragma GCC unroll 4
+        for (int q = 0; q < MM_TC / 8; ++q) acc[r][q] = (v8f){0, 0, 0, 0, 0, 0, 0, 0};
+    const float* a0 = a + i0 * k;
+    for (size_t kk = 0; kk < k; ++kk) {
+        v8f bv[MM_TC / 8];
+#pragma GCC unroll 4
+        for (int q = 0; q < MM_TC / 8; ++q) memcpy(&bv[q], b + kk * n + j0 + 8 * q, sizeof(v8f));
+#pragma GCC unroll 8
+        for (int r = 0; r < MM_TR; ++r) {
+            float s = a0[r * k + kk];
+            v8f av = {s, s, s, s, s, s, s, s};
+#pragma GCC unroll 4
+            for (int q = 0; q < MM_TC / 8; ++q) acc[r][q] += av * bv[q];
         }
     }
+#pragma GCC unroll 8
+    for (int r = 0; r < MM_TR; ++r)
+#pragma GCC unroll 4
+        for (int q = 0; q < MM_TC / 8; ++q) memcpy(c + (i0 + r) * n + j0 + 8 * q, &acc[r][q], sizeof(v8f));
+}
+
+/* One [m,k] @ [k,n] product, as tasks of (column panel, 512-row chunk);
+ * `par` splits them over threads (callers that already run batches in
+ * parallel pass 0). */
+static void mm_seq(const float* a, const float* b, float* c, size_t m, size_t k, size_t n, int par) {
+    const size_t rc = 512;
+    size_t nt = n / MM_TC * MM_TC, npan = nt / MM_TC;
+    size_t nrc = (m + rc - 1) / rc, ntask = nrc * (npan + 1);
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic, 1) if (par)
+    for (size_t t = 0; t < ntask; ++t) {
+        size_t p = t / nrc, i0 = t % nrc * rc;
+        size_t i1 = i0 + rc < m ? i0 + rc : m;
+        size_t it = i0 + (i1 - i0) / MM_TR * MM_TR;
+        if (p < npan) {
+            for (size_t i = i0; i < it; i += MM_TR) mm_tile(a, b, c, k, n, i, p * MM_TC);
+            mm_scalar(a, b, c, k, n, it, i1, p * MM_TC, (p + 1) * MM_TC);
+        } else if (nt < n) {
+            mm_scalar(a, b, c, k, n, i0, i1, nt, n);
+        }
+    }
+}
+
+static void mm_rows(const float* a, const float* b, float* c, size_t m, size_t k, size_t n) {
+    mm_seq(a, b, c, m, k, n, g_threads > 1);
 }
 
 void or_matmul(const float* a, const size_t* ash, int and_, const float* b, const size_t* bsh, int bnd, float* out) {
@@ -377,20 +445,9 @@ void or_matmul(const float* a, const size_t* ash, int and_, const float* b, cons
     } else if (and_ == 3 && bnd == 3) {
         if (ash[0] != bsh[0] || ash[2] != bsh[1]) die("batched matmul shape mismatch");
         size_t B = ash[0], m = ash[1], k = ash[2], n = bsh[2];
-        /* batches are independent; flatten batch x rows for the worker split */
-#pragma omp parallel for num_threads(g_threads) schedule(static)
-        for (size_t br = 0; br < B * m; ++br) {
-            size_t bx = br / m, i = br % m;
-            float* crow = out + bx * m * n + i * n;
-            for (size_t j = 0; j < n; ++j) crow[j] = 0.0f;
-            const float* arow = a + bx * m * k + i * k;
-            const float* bb = b + bx * k * n;
-            for (size_t kk = 0; kk < k; ++kk) {
-                float av = arow[kk];
-                const float* brow = bb + kk * n;
-                for (size_t j = 0; j < n; ++j) crow[j] += av * brow[j];
-            }
-        }
+        /* batches are independent: one batch per worker */
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic, 1)
+        for (size_t bx = 0; bx < B; ++bx) mm_seq(a + bx * m * k, b + bx * k * n, out + bx * m * n, m, k, n, 0);
     } else if (and_ == 3 && bnd == 2) {
         if (ash[2] != bsh[0]) die("matmul shape mismatch");
         mm_rows(a, b, out, ash[0] * ash[1], ash[2], bsh[1]);
@@ -403,18 +460,30 @@ void or_matmul(const float* a, const size_t* ash, int and_, const float* b, cons
  * VJP helpers — metal.rs:1779-1856 and tape.rs cpu_fallback (971-1260)
  * ====================================================================== */
 void or_sum_to_shape(const float* g, const size_t* gsh, int gnd, const size_t* tsh, int tnd, float* out) {
-    /* sum_to_shape, metal.rs:1812-1842: flat-order accumulation */
-    size_t padded[8];
+    /* sum_to_shape, metal.rs:1812-1842: flat-order accumulation.  Each output
+     * element starts at 0.0 and adds its input elements in increasing flat
+     * order; here every output element walks its own inputs in that order
+     * (the reduced dimensions as an odometer), so elements run in parallel. */
+    size_t padded[8], gst[8];
+    int rd[8], nr = 0;
     for (int i = 0; i < gnd - tnd; ++i) padded[i] = 1;
     for (int i = 0; i < tnd; ++i) padded[gnd - tnd + i] = tsh[i];
-    size_t outn = prod(tsh, tnd), total = prod(gsh, gnd);
-    for (size_t i = 0; i < outn; ++i) out[i] = 0.0f;
-    for (size_t flat = 0; flat < total; ++flat) {
-        size_t rem = flat, idx[8];
-        for (int d = gnd - 1; d >= 0; --d) { idx[d] = rem % gsh[d]; rem /= gsh[d]; }
-        size_t of = 0;
-        for (int d = 0; d < gnd; ++d) of = of * padded[d] + (idx[d] % padded[d]);
-        out[of] += g[flat];
+    for (int d = gnd - 1; d >= 0; --d) gst[d] = d == gnd - 1 ? 1 : gst[d + 1] * gsh[d + 1];
+    size_t rcount = 1;
+    for (int d = 0; d < gnd; ++d)
+        if (padded[d] == 1 && gsh[d] > 1) { rd[nr++] = d; rcount *= gsh[d]; }
+    size_t outn = prod(tsh, tnd);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (size_t o = 0; o < outn; ++o) {
+        size_t rem = o, base = 0;
+        for (int d = gnd - 1; d >= 0; --d) { base += (rem % padded[d]) * gst[d]; rem /= padded[d]; }
+        float acc = 0.0f;
+        for (size_t r = 0; r < rcount; ++r) {
+            size_t rr = r, off = base;
+            for (int q = nr - 1; q >= 0; --q) { off += (rr % gsh[rd[q]]) * gst[rd[q]]; rr /= gsh[rd[q]]; }
+            acc += g[off];
+        }
+        out[o] = acc;
     }
 }
 
@@ -422,6 +491,8 @@ void or_sum_to_shape(const float* g, const size_t* gsh, int gnd, const size_t* t
  * sigmoid/tanh/exp/sqrt and the forward input for relu/log/abs/gelu. */
 void or_unary_bwd(int op, const float* xy, const float* dout, size_t n, float* out) {
     const float C0 = 0.7978845608f, C1 = 0.044715f;
+    if (op < OR_RELU || op > OR_GELU) die("bad unary bwd op");
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < n; ++i) {
         float v = xy[i], d = dout[i];
         switch (op) {
@@ -432,7 +503,7 @@ void or_unary_bwd(int op, const float* xy, const float* dout, size_t n, float* o
         case OR_LOG: out[i] = d / v; break;                                               /* 1062 */
         case OR_SQRT: { float two_s = v * 2.0f; out[i] = d / two_s; break; }              /* 1063-1068 */
         case OR_ABS: out[i] = d * (v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f)); break;   /* 1069-1074 */
-        case OR_GELU: {                                                                   /* 1187-1199 */
+        default: {                                                                        /* GELU, 1187-1199 */
             float g = C0 * (v + C1 * v * v * v);
             float t = tanhf(g);
             float gp = C0 * (1.0f + 3.0f * C1 * v * v);
@@ -440,7 +511,6 @@ void or_unary_bwd(int op, const float* xy, const float* dout, size_t n, float* o
             out[i] = d * deriv;
             break;
         }
-        default: die("bad unary bwd op");
         }
     }
 }
@@ -491,6 +561,7 @@ void or_cross_entropy_bwd(const float* probs, size_t n, size_t c, const int32_t*
     float scale = dout0 / (float)n;
     memcpy(out, probs, n * c * sizeof(float));
     for (size_t i = 0; i < n; ++i) out[i * c + (size_t)targets[i]] -= 1.0f;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < n * c; ++i) out[i] *= scale;
 }
 
@@ -631,6 +702,7 @@ static T mm_bwd_a(const T* b, const T* dout) { T bt = transpose_last2(b); T r = 
 static T mm_bwd_b(const T* a, const T* dout) { T at = transpose_last2(a); T r = mm(&at, dout); tfree(&at); return r; }
 
 static void add_into(T* acc, const T* x) { /* grad_acc = __broadcast_add_fwd(old, new) */
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < acc->n; ++i) acc->d[i] = acc->d[i] + x->d[i];
 }
 
@@ -699,6 +771,12 @@ int or_gpt_nparams(const or_gpt* g) { return g->np; }
 size_t or_gpt_param_len(const or_gpt* g, int i) { return g->p[i].n; }
 void or_gpt_get_param(const or_gpt* g, int i, float* out) { memcpy(out, g->p[i].d, g->p[i].n * sizeof(float)); }
 void or_gpt_set_param(or_gpt* g, int i, const float* in) { memcpy(g->p[i].d, in, g->p[i].n * sizeof(float)); }
+void or_gpt_get_moment(const or_gpt* g, int i, int which, float* out) {
+    memcpy(out, (which ? g->v : g->m)[i].d, g->p[i].n * sizeof(float));
+}
+void or_gpt_set_moment(or_gpt* g, int i, int which, const float* in) {
+    memcpy((which ? g->v : g->m)[i].d, in, g->p[i].n * sizeof(float));
+}
 void or_gpt_get_grad(const or_gpt* g, int i, float* out) {
     if (g->g[i].d) memcpy(out, g->g[i].d, g->g[i].n * sizeof(float));
     else memset(out, 0, g->p[i].n * sizeof(float));
@@ -733,6 +811,7 @@ static void ln_fwd(const T* x, T* y, T* var) {
 static T mul_row(const T* y, const T* w) { /* [N,C] * [C] broadcast */
     T o = tnew(y->nd, y->sh);
     size_t C = y->sh[1];
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < y->n; ++i) o.d[i] = y->d[i] * w->d[i % C];
     return o;
 }
@@ -741,6 +820,7 @@ static void mul_row_bwd(const T* y, const T* w, const T* dout, T* dy, T* dw) {
     size_t C = y->sh[1];
     *dy = tnew(y->nd, y->sh);
     T full = tnew(y->nd, y->sh);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < y->n; ++i) { dy->d[i] = dout->d[i] * w->d[i % C]; full.d[i] = y->d[i] * dout->d[i]; }
     *dw = tnew1(C);
     size_t tsh[1] = {C};
@@ -768,6 +848,7 @@ float or_gpt_loss_and_grads(or_gpt* g, const int32_t* xt, const int32_t* yt, flo
     or_embedding(g->p[PT(g, 0)].d, (size_t)V, (size_t)C, xt, N, te.d);
     or_embedding(g->p[PT(g, 1)].d, (size_t)Tn, (size_t)C, g->pos, N, pe.d);
     T x = tnew2(N, (size_t)C);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (size_t i = 0; i < x.n; ++i) x.d[i] = te.d[i] + pe.d[i];
     tfree(&te); tfree(&pe);
     BlockCache* cache = (BlockCache*)calloc((size_t)L, sizeof(BlockCache));
@@ -786,8 +867,10 @@ float or_gpt_loss_and_grads(or_gpt* g, const int32_t* xt, const int32_t* yt, flo
         c->V = head_fold(&v, B, Tn, H, hs); tfree(&v);
         c->Kt = transpose_last2(&c->K);
         T S = mm(&c->Q, &c->Kt);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
         for (size_t i = 0; i < S.n; ++i) S.d[i] = S.d[i] * scale;                 /* scores * scale */
         size_t TT = (size_t)Tn * Tn;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
         for (size_t i = 0; i < S.n; ++i) S.d[i] = S.d[i] + mask.d[i % TT];       /* + vmask */
         c->P = tnew(S.nd, S.sh);
         or_softmax_axis(S.d, S.sh, 3, 2, c->P.d);
@@ -796,6 +879,7 @@ float or_gpt_loss_and_grads(or_gpt* g, const int32_t* xt, const int32_t* yt, flo
         c->att_out = head_unfold(&ao, B, Tn, H, hs); tfree(&ao);
         T proj = mm(&c->att_out, &g->p[PB(l, 4)]);
         c->x2 = tnew2(N, (size_t)C);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
         for (size_t i = 0; i < proj.n; ++i) c->x2.d[i] = x.d[i] + proj.d[i];
         tfree(&proj);
         ln_fwd(&c->x2, &c->y2, &c->var2);
@@ -805,6 +889,7 @@ float or_gpt_loss_and_grads(or_gpt* g, const int32_t* xt, const int32_t* yt, flo
         or_unary(OR_GELU, c->h.d, c->h.n, c->ge.d);
         T mo = mm(&c->ge, &g->p[PB(l, 7)]);
         T xn = tnew2(N, (size_t)C);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
         for (size_t i = 0; i < xn.n; ++i) xn.d[i] = c->x2.d[i] + mo.d[i];
         tfree(&mo);
         x = xn;
@@ -873,6 +958,7 @@ float or_gpt_loss_and_grads(or_gpt* g, const int32_t* xt, const int32_t* yt, flo
         or_softmax_bwd(c->P.d, dP.d, dP.sh, 3, 2, dS.d);
         tfree(&dP);
         /* masked = scores + vmask: dscores = dS; scores = QKt * scale: dQKt = dS * scale */
+#pragma omp parallel for num_threads(g_threads) schedule(static)
         for (size_t i = 0; i < dS.n; ++i) dS.d[i] = dS.d[i] * scale;
         T dQ = mm_bwd_a(&c->Kt, &dS);
         T dKt = mm_bwd_b(&c->Q, &dS);

@@ -86,6 +86,9 @@ size_t or_gpt_param_len(const or_gpt* g, int i);
 void or_gpt_get_param(const or_gpt* g, int i, float* out);
 void or_gpt_get_grad(const or_gpt* g, int i, float* out);
 void or_gpt_set_param(or_gpt* g, int i, const float* in);
+/* AdamW moments of parameter i (which = 0: m, 1: v), to save and resume a run. */
+void or_gpt_get_moment(const or_gpt* g, int i, int which, float* out);
+void or_gpt_set_moment(or_gpt* g, int i, int which, const float* in);
 /* forward + cross-entropy + backward; grads kept for or_gpt_get_grad. */
 float or_gpt_loss_and_grads(or_gpt* g, const int32_t* x, const int32_t* y, float* logits_out);
 /* full training step (forward, backward, Adam+L2 update with bias-correction step t). */

@@ -72,6 +72,8 @@ def lib():
             "or_gpt_get_param": (None, [C.c_void_p, C.c_int, _f]),
             "or_gpt_get_grad": (None, [C.c_void_p, C.c_int, _f]),
             "or_gpt_set_param": (None, [C.c_void_p, C.c_int, _f]),
+            "or_gpt_get_moment": (None, [C.c_void_p, C.c_int, C.c_int, _f]),
+            "or_gpt_set_moment": (None, [C.c_void_p, C.c_int, C.c_int, _f]),
             "or_gpt_loss_and_grads": (C.c_float, [C.c_void_p, _i32p, _i32p, _f]),
             "or_gpt_step": (C.c_float, [C.c_void_p, _i32p, _i32p, C.c_int64]),
             "or_set_threads": (None, [C.c_int]),
@@ -331,6 +333,16 @@ class Gpt:
         v = f32(values).ravel()
         assert v.size == lib().or_gpt_param_len(self.h, i)
         lib().or_gpt_set_param(self.h, i, _fp(v))
+
+    def moment(self, i, which):
+        out = np.empty(lib().or_gpt_param_len(self.h, i), np.float32)
+        lib().or_gpt_get_moment(self.h, i, which, _fp(out))
+        return out
+
+    def set_moment(self, i, which, values):
+        v = f32(values).ravel()
+        assert v.size == lib().or_gpt_param_len(self.h, i)
+        lib().or_gpt_set_moment(self.h, i, which, _fp(v))
 
     def loss_and_grads(self, x, y, want_logits=False):
         x = np.ascontiguousarray(x, np.int32)

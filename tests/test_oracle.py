@@ -11,7 +11,7 @@ import pytest
 
 from oracle import oracle as O
 
-from tests.helpers import KATS
+from tests.helpers import KATS, assert_bitexact
 
 RNG = np.random.default_rng(7)
 
@@ -155,6 +155,30 @@ def test_matmul_within_sequential_error_bound():
     A, B = r(3, 5, 7), r(3, 7, 4)
     assert np.allclose(O.matmul(A, B), np.einsum("bmk,bkn->bmn", A.astype(np.float64), B), rtol=1e-5, atol=1e-6)
     assert np.allclose(O.matmul(A, B[0]), A.astype(np.float64) @ B[0], rtol=1e-5, atol=1e-6)
+
+
+def _matmul_k_sequential(a, b):
+    """metal.rs:698-800's summation, written as numpy float32 steps: every
+    out[i,j] starts at 0.0 and adds the rounded product a[i,k]*b[k,j] for k
+    ascending, each step rounded to f32 (separate multiply and add ufuncs)."""
+    acc = np.zeros(a.shape[:-1] + (b.shape[-1],), np.float32)
+    for kk in range(a.shape[-1]):
+        acc = acc + a[..., kk:kk + 1] * b[..., kk:kk + 1, :]
+    return acc
+
+
+@pytest.mark.parametrize("m,k,n", [(13, 37, 70), (4, 5, 32), (1, 1, 1), (600, 9, 97), (8, 64, 31), (515, 3, 64)])
+def test_matmul_is_the_k_sequential_sum_bit_for_bit(m, k, n):
+    # the oracle's register tiles (4 x 32) and thread split (512-row chunks)
+    # cover ragged rows and columns on both sides of every boundary
+    a, b = r(m, k), r(k, n)
+    for threads in (1, 8):
+        O.set_threads(threads)
+        assert_bitexact(O.matmul(a, b), _matmul_k_sequential(a, b), f"{m}x{k}x{n}, {threads} threads")
+    A, B = r(3, m % 40 + 1, k), r(3, k, n)
+    assert_bitexact(O.matmul(A, B), _matmul_k_sequential(A, B), "batched")
+    assert_bitexact(O.matmul(A, B[1]), _matmul_k_sequential(A, B[1]), "3-D by 2-D")
+    O.set_threads(1)
 
 
 def test_bf16_round_is_torchs_bfloat16_conversion():
