@@ -405,32 +405,40 @@ def run_gpt(rt, a, cfg):
     g = L.malus_gpt_create(cfg["V"], cfg["T"], cfg["C"], cfg["H"], cfg["L"], cfg["B"], OPT["lr"], OPT["b1"],
                            OPT["b2"], OPT["eps"], OPT["wd"])
     L.malus_gpt_set_attention(g, ATTN_MODES[a.attention])
+    if a.composed:
+        # the op sequence an unchanged nanogpt_modular.ml issues through the C ABI:
+        # no forward fusions, the tape's plain VJPs, op-by-op AdamW
+        L.malus_gpt_set_fused_forward(g, 0)
+        L.malus_gpt_set_fused_optimizer(g, 0)
+        L.malus_tape_set_fused_vjps(0)
     # docs/adr/0037-bf16-autocast.md:5-12: the whole step inside `with autocast:`
     L.malus_autocast(1 if a.autocast else 0)
     n = cfg["B"] * cfg["T"]
-    rng = np.random.default_rng(2024)
     gemm_steps = min(a.steps, 20)
-    host = [(rng.integers(0, cfg["V"], n).astype(np.int32), rng.integers(0, cfg["V"], n).astype(np.int32))
-            for _ in range(a.warmup + a.steps + gemm_steps)]
 
     t = 0
-    I32P = C.POINTER(C.c_int32)
     graph = None
 
+    def calls(i):
+        # step i's token and target ids: rand_int(V) per token with call
+        # indices base + j and base + n + j (i.i.d. uniform in [0, V))
+        base = (1 << 33) + 2 * n * i
+        return base, base + n
+
     def step(i):
-        # the step's own token upload (buffer.rs:39-50 freeze), then the step
+        # batch construction (the ids drawn on the device), then the step
         nonlocal t, graph
         t += 1
+        cx, cy = calls(i)
         if a.graph:
-            x, y = host[i]
             if graph is None:  # step 1 runs eagerly inside create, which then captures the step
                 hl = C.c_int64()
-                graph = L.malus_gpt_graph_create(g, x.ctypes.data_as(I32P), y.ctypes.data_as(I32P), t, C.byref(hl))
+                graph = L.malus_gpt_graph_create_drawn(g, cx, cy, t, C.byref(hl))
                 if not graph:
-                    raise RuntimeError("malus_gpt_graph_create failed")
+                    raise RuntimeError("malus_gpt_graph_create_drawn failed")
                 return hl.value, 0, 0
-            return L.malus_gpt_graph_step(graph, x.ctypes.data_as(I32P), y.ctypes.data_as(I32P), t), 0, 0
-        x, y = rt.tensor(host[i][0]), rt.tensor(host[i][1])
+            return L.malus_gpt_graph_step_drawn(graph, cx, cy, t), 0, 0
+        x, y = L.malus_rand_tokens_device(cx, n, cfg["V"]), L.malus_rand_tokens_device(cy, n, cfg["V"])
         hl = L.malus_gpt_step(g, x, y, t)
         return hl, x, y
 
@@ -462,7 +470,7 @@ def run_gpt(rt, a, cfg):
         nodes = L.malus_gpt_graph_nodes(graph)
         L.malus_gpt_graph_free(graph)
         graph = None
-        log(f"graph: one hipGraphLaunch per step, {nodes} nodes (kernels + 3 input copies)")
+        log(f"graph: one hipGraphLaunch per step, {nodes} nodes (kernels, the token draw and 2 input copies)")
     a_graph, a.graph = a.graph, False  # the GEMM pass below runs eagerly (event timers are not graph nodes)
 
     # a separate pass for the GEMM class: HIP events around every GEMM launch
@@ -498,6 +506,7 @@ def run_gpt(rt, a, cfg):
             log(f"cpu baseline failed: {e!r}")
     L.malus_gpt_free(g)
     L.malus_autocast(0)
+    L.malus_tape_set_fused_vjps(1)
 
     c5 = cfg == CONFIGS["c5"]
     traffic = measured_traffic() if c5 and not a.autocast else None
@@ -515,13 +524,15 @@ def run_gpt(rt, a, cfg):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16 GEMM operands, f32 accumulation and everything else f32 (autocast)" if a.autocast else "f32",
-        "data": "synthetic int32 tokens i.i.d. uniform in [0,65) (seed 2024), uploaded inside each timed step; "
-                "weights randn*0.02 (Philox, call 0)",
+        "data": "synthetic int32 tokens i.i.d. uniform in [0,65), drawn on the device inside each timed step "
+                "(rand_int per token, Philox keyed by call index); weights randn*0.02 (Philox, call 0)",
         "attention": a.attention,
-        "execution": ("hipGraph replay of the captured step (token/target ids and AdamW bias corrections copied from "
-                      f"pinned host memory by the graph's nodes; {nodes} nodes)") if a_graph else
+        "execution": ("hipGraph replay of the captured step (the id draw, the step's call indices and AdamW bias "
+                      f"corrections from pinned host memory by the graph's nodes; {nodes} nodes)") if a_graph else
                      "eager: every kernel launched from the host each step",
-        "config": {"workload": f"{tag} char-nanoGPT train step (token upload+fwd+bwd+AdamW)", "vocab": cfg["V"],
+        "ops": ("composed: nanogpt_modular.ml's op sequence through the C ABI (no forward fusions, plain tape VJPs, "
+                "op-by-op AdamW)") if a.composed else "fused forward, fused VJPs, multi-tensor AdamW",
+        "config": {"workload": f"{tag} char-nanoGPT train step (batch draw+fwd+bwd+AdamW)", "vocab": cfg["V"],
                    "block_size": cfg["T"], "n_embd": cfg["C"], "n_head": cfg["H"], "n_layer": cfg["L"],
                    "batch": cfg["B"], "tokens_per_step": n, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "k_sgemm (all GEMM launches of the step)",
@@ -553,6 +564,10 @@ def main():
     ap.add_argument("--attention", choices=list(ATTN_MODES), default="auto",
                     help="attention kernel of the model: auto, flash (online softmax), rows (the row-register "
                          "fused kernel), composed (matmul + softmax ops)")
+    ap.add_argument("--composed", action="store_true",
+                    help="the op sequence an unchanged nanogpt_modular.ml issues through the C ABI: forward fusions, "
+                         "fused VJPs and the fused optimizer off, composed attention, eager launches; reported "
+                         "beside the headline, never in its place")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -561,6 +576,8 @@ def main():
                     help="kernels: the C2/C3 elementwise and row-op kernels' HBM bandwidth; attention: the causal "
                          "attention kernels' forward and backward times (one JSON line each)")
     a = ap.parse_args()
+    if a.composed:
+        a.eager, a.attention = True, "composed"
     a.graph = not a.eager
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "

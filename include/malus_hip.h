@@ -141,6 +141,10 @@ int64_t malus_rand_int(int64_t n);                                      /* metal
  * [B*T] i32 tensors; starts_out (host int32[B], optional) gets the starts. */
 int64_t malus_randn_device(const size_t* shape, size_t ndim);
 void malus_batch_windows(int64_t data, int64_t B, int64_t T, int64_t* x_out, int64_t* y_out, int32_t* starts_out);
+/* No reference counterpart (device-side data path): n i.i.d. token ids,
+ * out[i] = rand_int(vocab) with call index call + i, the ids of the host
+ * builtin's loop (metal.rs:1752-1759), drawn on the device; a new [n] i32. */
+int64_t malus_rand_tokens_device(uint64_t call, size_t n, int64_t vocab);
 uint64_t malus_rng_get_counter(void);
 void malus_rng_set_counter(uint64_t v);
 
@@ -198,6 +202,11 @@ int64_t malus_pool_live_bytes(void);
 size_t malus_pool_buckets(size_t* sizes, size_t* counts, size_t cap);
 void malus_pool_reset(void);
 void malus_set_mem_budget(int64_t bytes);
+/* Fault injection for tests of error paths (no reference counterpart): the
+ * pool allocation after the next n fails with a malus error, once; n < 0
+ * turns it off.  The failure is raised on the host before the buffer's
+ * first use, so no kernel sees it. */
+void malus_fail_alloc_after(int64_t n);
 size_t malus_alloc_histogram(size_t* sizes, uint64_t* counts, size_t cap);
 
 /* ---- instrumentation and errors (no reference counterparts) ------------- */
@@ -262,7 +271,7 @@ int32_t malus_std_flash_attn_bwd(int64_t dout, int64_t q, int64_t k, int64_t v, 
                                  int64_t* dq_out, int64_t* dk_out, int64_t* dv_out);
 int64_t malus_ktimer_collect(const char* cls, double* total_ms, double* total_units);
 int malus_device_info(char* name, size_t cap, int* cus, int* clock_khz);
-void malus_set_abort_on_error(int on);
+int malus_set_abort_on_error(int on); /* returns the previous setting */
 const char* malus_last_error(void);
 void malus_clear_error(void);
 
@@ -353,6 +362,12 @@ int64_t malus_gpt_step(void* g, int64_t toks, int64_t targets, int64_t t); /* na
  * values equal malus_gpt_step's.  Free the graph before the model. */
 void* malus_gpt_graph_create(void* gpt, const int32_t* x, const int32_t* y, int64_t t, int64_t* loss_out);
 int64_t malus_gpt_graph_step(void* graph, const int32_t* x, const int32_t* y, int64_t t);
+/* The same graph with each step's ids drawn on the device by a kernel node
+ * of the step itself: x[i] = rand_int(V) with call index x_call + i, y[i]
+ * with y_call + i (the ids malus_rand_tokens_device draws), so batch
+ * construction is part of the replayed step. */
+void* malus_gpt_graph_create_drawn(void* gpt, uint64_t x_call, uint64_t y_call, int64_t t, int64_t* loss_out);
+int64_t malus_gpt_graph_step_drawn(void* graph, uint64_t x_call, uint64_t y_call, int64_t t);
 void malus_gpt_graph_free(void* graph);
 size_t malus_gpt_graph_nodes(void* graph);
 /* No reference counterpart (a checkpoint format is deferred in the

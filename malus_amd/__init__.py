@@ -8,7 +8,6 @@ is missing or no HIP device is present, calls fail loudly.
 from __future__ import annotations
 
 import ctypes as C
-import os
 from pathlib import Path
 
 import numpy as np
@@ -110,6 +109,7 @@ SIGNATURES = {
     "malus_pool_buckets": (_sz, [_P(_sz), _P(_sz), _sz]),
     "malus_pool_reset": (None, []),
     "malus_set_mem_budget": (None, [_i64]),
+    "malus_fail_alloc_after": (None, [_i64]),
     "malus_alloc_histogram": (_sz, [_P(_sz), _P(_u64), _sz]),
     "malus_ktimer_enable": (None, [C.c_int]),
     "malus_gemm_set_tile": (C.c_int, [C.c_int, C.c_int]),
@@ -127,7 +127,7 @@ SIGNATURES = {
                                              _P(_i64), _P(_i64), _P(_i64)]),
     "malus_ktimer_collect": (_i64, [C.c_char_p, _P(C.c_double), _P(C.c_double)]),
     "malus_device_info": (C.c_int, [C.c_char_p, _sz, _P(C.c_int), _P(C.c_int)]),
-    "malus_set_abort_on_error": (None, [C.c_int]),
+    "malus_set_abort_on_error": (C.c_int, [C.c_int]),
     "malus_last_error": (C.c_char_p, []),
     "malus_clear_error": (None, []),
     # stdlib host fns
@@ -188,12 +188,15 @@ SIGNATURES = {
     "malus_xor_run": (_f32, [C.c_int, _f32, _u64, _P(_f32), _P(_f32), _P(_f32)]),
     "malus_gpt_graph_create": (_vp, [_vp, _P(_i32), _P(_i32), _i64, _P(_i64)]),
     "malus_gpt_graph_step": (_i64, [_vp, _P(_i32), _P(_i32), _i64]),
+    "malus_gpt_graph_create_drawn": (_vp, [_vp, _u64, _u64, _i64, _P(_i64)]),
+    "malus_gpt_graph_step_drawn": (_i64, [_vp, _u64, _u64, _i64]),
     "malus_gpt_graph_free": (None, [_vp]),
     "malus_gpt_graph_nodes": (_sz, [_vp]),
     "malus_gpt_save": (C.c_int, [_vp, C.c_char_p, _i64]),
     "malus_gpt_load": (_i64, [_vp, C.c_char_p]),
     "malus_randn_device": (_i64, [_P(_sz), _sz]),
     "malus_batch_windows": (None, [_i64, _i64, _i64, _P(_i64), _P(_i64), _P(C.c_int32)]),
+    "malus_rand_tokens_device": (_i64, [C.c_uint64, _sz, _i64]),
     "malus_std_reduce_noalloc": (C.c_int, [_i32, _vp, _P(_sz), _sz, _i64, _vp]),
     "malus_compile_kernels": (_vp, [C.c_char_p, _P(C.c_char_p), _sz, C.c_int]),
     "malus_registry_len": (_sz, [_vp]),
@@ -296,7 +299,7 @@ def compile_kernels(program: str, builtins=(), tags: bool = False) -> KernelRegi
     L = lib()
     names = [b.encode() for b in builtins]
     arr = (C.c_char_p * max(1, len(names)))(*names)
-    L.malus_set_abort_on_error(0)
+    prev = L.malus_set_abort_on_error(0)
     try:
         r = L.malus_compile_kernels(program.encode(), arr, len(names), 1 if tags else 0)
         if not r:
@@ -304,7 +307,7 @@ def compile_kernels(program: str, builtins=(), tags: bool = False) -> KernelRegi
             L.malus_clear_error()
             raise RuntimeError(msg.decode() if msg else "malus_compile_kernels failed")
     finally:
-        L.malus_set_abort_on_error(1)
+        L.malus_set_abort_on_error(prev)
     try:
         entries = [(L.malus_registry_name(r, i).decode(), int(L.malus_registry_id(r, i)),
                     L.malus_registry_source(r, i).decode()) for i in range(L.malus_registry_len(r))]
@@ -330,12 +333,3 @@ class autocast:
         lib().malus_autocast(self._prev)
         return False
 
-
-def device_count_hint() -> int:
-    """Number of visible GPUs without initializing HIP (for test gating)."""
-    try:
-        import torch  # noqa: F401  (torch.cuda.device_count does not initialize HIP on this image)
-
-        return int(torch.cuda.device_count())
-    except Exception:
-        return 1 if os.path.exists("/dev/kfd") else 0

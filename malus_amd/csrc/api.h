@@ -79,12 +79,29 @@ void flash_bwd_impl(int64_t datt, int64_t q, int64_t k, int64_t v, int64_t o, in
 int64_t scores_bwd_q(int64_t ds, int64_t k, const malus::TensorBuffer* D, bool causal);
 int64_t scores_bwd_k(int64_t ds, int64_t q, const malus::TensorBuffer* D, bool causal);
 
-#define API_TRY try {
-#define API_CATCH(...)                                   \
-  }                                                      \
-  catch (const ::malus::MalusError& e) {                 \
-    ::malus::set_last_error(e.what());                   \
-    return __VA_ARGS__;                                  \
+// C-ABI entry points wrap their bodies in API_TRY ... API_CATCH(value).  In
+// return-error mode the outermost entry point on the thread's stack turns a
+// malus error into `value` and malus_last_error(); an entry point that
+// another one called passes the error on, so the caller stops where the
+// error arose instead of going on with a null handle.
+namespace malus {
+extern thread_local int g_api_depth;
+struct ApiDepth {
+  ApiDepth() { ++g_api_depth; }
+  ~ApiDepth() { --g_api_depth; }
+};
+}  // namespace malus
+#define API_TRY                        \
+  {                                    \
+    ::malus::ApiDepth api_depth_guard_; \
+    try {
+#define API_CATCH(...)                                 \
+  }                                                    \
+  catch (const ::malus::MalusError& e) {               \
+    if (::malus::g_api_depth > 1) throw;               \
+    ::malus::set_last_error(e.what());                 \
+    return __VA_ARGS__;                                \
+  }                                                    \
   }
 
 // Stdlib host functions (stdlib.cpp), exported with a malus_std_ prefix.

@@ -123,6 +123,10 @@ namespace k {
 // k_rng.hip: Philox4x32-10 on the device (the host generator's words).
 // randn: Box-Muller of pair k (counter [k, 0, 0, 0], key = call) in f64.
 void randn(float* out, size_t n, uint64_t call, hipStream_t s);
+// rand_tokens: x[i] = rand_int(vocab) with call index cx + i, y[i] with cy + i
+// (vocab >= 1); `calls` (device, 2 words), when given, supplies cx and cy.
+void rand_tokens(int32_t* x, int32_t* y, size_t n, const uint64_t* calls, uint64_t cx, uint64_t cy, uint32_t vocab,
+                 hipStream_t s);
 // batch_windows: B sequences of T tokens at starts rand_int(range) drawn with
 // call indices call0 .. call0 + B - 1; y is x shifted by one token.
 void batch_windows(const int32_t* data, int32_t* x, int32_t* y, size_t B, size_t T, uint64_t call0, uint64_t range,

@@ -83,9 +83,29 @@ struct KernelEntry {
   // input i), and the v2 uniforms blob size (-1: unknown).
   uint32_t scalar_inputs = 0;
   long uniform_bytes = -1;
+  // v1: element bytes of the output, then of each input, as the kernel
+  // declares them (empty: not annotated).
+  std::vector<long> elem_bytes;
 };
 
 // The emitter's "//@malus-<key> <value>" annotation lines.
+// A list annotation "//@malus-<key> v0 v1 ...": the numbers up to the line's end.
+std::vector<long> annotation_list(const std::string& src, const char* key) {
+  std::vector<long> out;
+  std::string tag = std::string("//@malus-") + key + " ";
+  size_t p = src.find(tag);
+  if (p == std::string::npos) return out;
+  const char* c = src.c_str() + p + tag.size();
+  while (*c && *c != '\n') {
+    char* end = nullptr;
+    long v = strtol(c, &end, 10);
+    if (end == c) break;
+    out.push_back(v);
+    c = end;
+  }
+  return out;
+}
+
 bool annotation(const std::string& src, const char* key, long* value) {
   std::string tag = std::string("//@malus-") + key + " ";
   size_t p = src.find(tag);
@@ -385,6 +405,9 @@ void run_builtin_v2(Builtin b, std::vector<TensorBuffer*>& in, TensorBuffer* out
 void run_builtin_v1(Builtin b, std::vector<TensorBuffer*>& in, TensorBuffer* out) {
   hipStream_t s = stream();
   const size_t n = out->len;
+  // the synthesized builtins are f32 kernels (codegen-gpu/lib.rs:373-418)
+  for (TensorBuffer* t : in)
+    if (t->dtype != F32) fail("malus: kernel_dispatch: the builtin kernels take f32 tensors (got dtype tag %d)", t->dtype);
   auto same = [&](int op) {
     need_inputs(in, 2, "elementwise builtin");
     need_len(in[1], n, "elementwise builtin");
@@ -467,6 +490,7 @@ void malus_runtime_init(const uint64_t* ids, const char* const* sources, size_t 
       long v;
       if (annotation(src, "v1-scalar-inputs", &v) && v >= 0 && v < 32) e.scalar_inputs |= 1u << v;
       if (annotation(src, "v2-uniform-bytes", &v)) e.uniform_bytes = v;
+      e.elem_bytes = annotation_list(src, "v1-elem-bytes");
     }
     std::lock_guard<std::mutex> lk(reg().mu);
     reg().by_id[ids[i]] = e;
@@ -508,6 +532,20 @@ int64_t kernel_dispatch(uint64_t id, const int64_t* handles, size_t count) {
   if (e.builtin != Builtin::None) {
     run_builtin_v1(e.builtin, in, out);
   } else {
+    // The output takes input 0's dtype (metal.rs:1878-1888); the kernel
+    // reads and writes the element widths it declares, so they must agree.
+    if (!e.elem_bytes.empty()) {
+      if (e.elem_bytes.size() != in.size() + 1)
+        fail("malus: kernel_dispatch: kernel %llu takes %zu tensor inputs, got %zu", (unsigned long long)id,
+             e.elem_bytes.size() - 1, in.size());
+      if ((long)dtype_size(out->dtype) != e.elem_bytes[0])
+        fail("malus: kernel_dispatch: kernel %llu writes %ld-byte elements, but its output takes input 0's dtype "
+             "(%zu-byte elements)", (unsigned long long)id, e.elem_bytes[0], dtype_size(out->dtype));
+      for (size_t i = 0; i < in.size(); ++i)
+        if ((long)dtype_size(in[i]->dtype) != e.elem_bytes[i + 1])
+          fail("malus: kernel_dispatch: kernel %llu reads input %zu as %ld-byte elements, got %zu-byte elements",
+               (unsigned long long)id, i, e.elem_bytes[i + 1], dtype_size(in[i]->dtype));
+    }
     // an emitted implicit-map kernel reads in_i[tid] for every tid < out.len
     // (a scalar-broadcast builtin reads its scalar input at [0] only)
     for (size_t i = 0; i < in.size(); ++i) {

@@ -66,6 +66,10 @@ const char* sc_name(Sc s) {
   static const char* n[] = {"f32", "f16", "bf16", "i8", "i16", "i32", "i64", "u8", "u16", "u32", "u64"};
   return n[(int)s];
 }
+int sc_bytes(Sc s) {
+  static const int n[] = {4, 2, 2, 1, 2, 4, 8, 1, 2, 4, 8};
+  return n[(int)s];
+}
 // dtype_to_msl (codegen-gpu/lib.rs:1060-1074), mapped to HIP C++ types.
 const char* sc_hip(Sc s) {
   static const char* n[] = {"float",      "_Float16",       "__bf16",         "signed char",
@@ -1055,7 +1059,9 @@ class Lower {
       }
     }
     o << "}\n";
-    *notes = "";
+    *notes = "//@malus-v1-elem-bytes " + std::to_string(sc_bytes(k_.ret.s));
+    for (auto& p : k_.params) *notes += " " + std::to_string(sc_bytes(p.ty.s));
+    *notes += "\n";
     return "// malus kernel " + k_.name + " (implicit map, v1 ABI)\n" + prelude_for(o.str()) + o.str();
   }
 
@@ -1257,7 +1263,9 @@ class Lower {
 
 std::string v1_header(const std::string& name, uint64_t id, const std::vector<std::string>& ins) {
   std::ostringstream o;
-  o << "// malus builtin " << name << " (v1 ABI)\n";
+  o << "//@malus-v1-elem-bytes 4";
+  for (size_t i = 0; i < ins.size(); ++i) o << " 4";
+  o << "\n// malus builtin " << name << " (v1 ABI)\n";
   o << "extern \"C\" __global__ void malus_kernel_" << id << "(";
   for (auto& i : ins) o << "const float* __restrict__ " << i << ", ";
   o << "float* __restrict__ out, unsigned int n) {\n";

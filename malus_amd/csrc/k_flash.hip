@@ -74,6 +74,18 @@ __device__ __forceinline__ const float* head_row(const float* base, int bh, int 
   return base + (size_t)(bh / H) * T * ld + (size_t)(bh % H) * hs + (size_t)row * ld;
 }
 
+// Orders one wave's LDS traffic between its lanes: the stores before it are
+// visible to every lane's loads after it, and every lane's loads before it
+// are done before the stores after it.  Wavefront-scope fences around the
+// wave barrier keep the compiler from moving LDS accesses across it; the
+// hardware already runs one wave's LDS operations in order, so in these
+// one-wave workgroups it costs no instruction.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Forward: query tile qt of head bh.  O^T = V^T P^T keeps the output with
 // lane = query, so the online rescale is a per-lane factor.
 template <int HS, bool CAUSAL, bool BF>
@@ -116,11 +128,13 @@ __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q
         const int f = lane + 64 * u;
         vn[u] = *reinterpret_cast<const v4f*>(Vh + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
       }
+      wave_lds_sync();  // the last tile's reads of Vs are done
 #pragma unroll
-      for (int u = 0; u < PER; ++u) {  // LDS ops of one wave run in order: the last tile's reads are done
+      for (int u = 0; u < PER; ++u) {
         const int f = lane + 64 * u;
         *reinterpret_cast<v4f*>(Vs + (f / Q4) * LD + 4 * (f % Q4)) = vn[u];
       }
+      wave_lds_sync();  // this tile's stores are visible to every lane
 #pragma unroll
       for (int n = 0; n < NN; ++n)
 #pragma unroll
@@ -239,12 +253,14 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
   };
   for (int j = 0; j <= last; ++j) {
     fetch(j);
+    wave_lds_sync();  // the last tile's reads of Ks and Vs are done
 #pragma unroll
-    for (int u = 0; u < PER; ++u) {  // LDS ops of one wave run in order: the last tile's reads are done
+    for (int u = 0; u < PER; ++u) {
       const int f = lane + 64 * u;
       *reinterpret_cast<v4f*>(Ks + (f / Q4) * LD + 4 * (f % Q4)) = kn[u];
       *reinterpret_cast<v4f*>(Vs + (f / Q4) * LD + 4 * (f % Q4)) = vn[u];
     }
+    wave_lds_sync();  // this tile's stores are visible to every lane
     float ka[NKB][8], vr[NKB][8];  // A of S^T and dP^T: rows perm_row(x) of K_j, V_j
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
@@ -355,12 +371,14 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
         qn[u] = *reinterpret_cast<const v4f*>(Qh + (size_t)(i0 + f / Q4) * HS + 4 * (f % Q4));
         on[u] = *reinterpret_cast<const v4f*>(head_row(dO, bh, H, T, ldo, HS, i0 + f / Q4) + 4 * (f % Q4));
       }
+      wave_lds_sync();  // the last tile's reads of Qs and Os are done
 #pragma unroll
-      for (int u = 0; u < PER; ++u) {  // LDS ops of one wave run in order: the last tile's reads are done
+      for (int u = 0; u < PER; ++u) {
         const int f = lane + 64 * u;
         *reinterpret_cast<v4f*>(Qs + (f / Q4) * LD + 4 * (f % Q4)) = qn[u];
         *reinterpret_cast<v4f*>(Os + (f / Q4) * LD + 4 * (f % Q4)) = on[u];
       }
+      wave_lds_sync();  // this tile's stores are visible to every lane
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
         float qa[8], oa[8];  // A: rows perm_row(x) of Q_i, dO_i

@@ -599,9 +599,14 @@ void reduce_axis(int op, const float* x, float* out, size_t outer, size_t axis, 
 }
 
 size_t reduce_axis_scratch_floats(int op, const float* x, const float* out, size_t outer, size_t axis, size_t inner) {
+  // each pass plans with the pointers it is given (reduce_impl): a plain
+  // reduction with x and out; the variance's mean pass with x and the
+  // 256-byte-aligned mean, its second pass with x, the mean and out
   const bool aligned = ((uintptr_t)x | (uintptr_t)out) % 16 == 0;
   const size_t part = partial_floats(outer, axis, inner, aligned);
-  return op == R_VAR ? (outer * inner + 63) / 64 * 64 + part : part;
+  if (op != R_VAR) return part;
+  const size_t mean_part = partial_floats(outer, axis, inner, (uintptr_t)x % 16 == 0);
+  return (outer * inner + 63) / 64 * 64 + (part > mean_part ? part : mean_part);
 }
 
 void reduce_axis_scratch(int op, const float* x, float* out, size_t outer, size_t axis, size_t inner, float* scratch,

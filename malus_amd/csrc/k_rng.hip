@@ -70,7 +70,38 @@ __global__ __launch_bounds__(256) void k_batch_windows(const int32_t* __restrict
   }
 }
 
+// i.i.d. token ids: x[i] = rand_int(vocab) with call index cx + i, y[i]
+// the same with cy + i (the `rand_int` builtin: counter [1, 0, 0, 0], key =
+// the call index; the word's remainder by vocab).  The two call indices come
+// from `calls` in device memory when it is given (a captured step reads each
+// replay's own), else from cx and cy.  y may be null (x only).
+__global__ __launch_bounds__(256) void k_rand_tokens(int32_t* __restrict__ x, int32_t* __restrict__ y, size_t n,
+                                                     const uint64_t* __restrict__ calls, uint64_t cx, uint64_t cy,
+                                                     uint32_t vocab) {
+  if (calls) {
+    cx = calls[0];
+    cy = calls[1];
+  }
+  const size_t stride = (size_t)gridDim.x * blockDim.x, total = y ? 2 * n : n;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const bool second = i >= n;
+    const uint64_t call = (second ? cy : cx) + (second ? i - n : i);
+    uint32_t r[4];
+    philox(1u, 0u, 0u, 0u, (uint32_t)call, (uint32_t)(call >> 32), r);
+    (second ? y : x)[second ? i - n : i] = (int32_t)(r[0] % vocab);
+  }
+}
+
 }  // namespace
+
+void rand_tokens(int32_t* x, int32_t* y, size_t n, const uint64_t* calls, uint64_t cx, uint64_t cy, uint32_t vocab,
+                 hipStream_t s) {
+  if (!n) return;
+  size_t blocks = ((y ? 2 * n : n) + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  k_rand_tokens<<<(unsigned)blocks, 256, 0, s>>>(x, y, n, calls, cx, cy, vocab);
+  MALUS_HIP(hipGetLastError());
+}
 
 void randn(float* out, size_t n, uint64_t call, hipStream_t s) {
   if (!n) return;

@@ -5,6 +5,7 @@
 // follow codegen-cpu's lowering (lib.rs:1525-1850, 2765-3082); the
 // nanoGPT driver is generalized to L blocks and H heads for the C4/C5
 // configurations.
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstring>
@@ -34,6 +35,7 @@ void tape_register_leaf(int64_t h);
 void tape_zero_grad(const int64_t* handles, size_t count);
 int64_t tape_get_grad(int64_t h);
 void backward(int64_t loss);
+void tape_clear(void);
 void tape_pause(void);
 void tape_resume(void);
 int64_t kernel_dispatch(uint64_t id, const int64_t* handles, size_t count);
@@ -673,8 +675,15 @@ struct GptGraph {
   Gpt* g = nullptr;
   int id = 0;
   size_t n = 0;                  // tokens per step (B * T)
-  char* pinned = nullptr;        // [n] i32 tokens, [n] i32 targets, [2] f32 bias corrections
+  // Where a step's token and target ids come from: copied from host arrays
+  // (`pinned` holds [n] i32 tokens, [n] i32 targets, [2] f32 bias
+  // corrections), or drawn on the device (`drawn`: `pinned` holds the two
+  // [2] u64 call indices, then the [2] f32 bias corrections, and a kernel node
+  // draws the ids).
+  bool drawn = false;
+  char* pinned = nullptr;
   int64_t toks = 0, tgts = 0;    // fixed device inputs [n] i32
+  int64_t calls = 0;             // drawn: [2] i64 call indices on the device
   TensorBuffer* bc = nullptr;    // [2] f32 on the device
   int64_t loss = 0;              // written by every replay
   hipGraph_t graph = nullptr;
@@ -685,12 +694,25 @@ struct GptGraph {
 
 std::atomic<int> g_graph_ids{0};
 
-void graph_set_inputs(GptGraph& gr, const int32_t* x, const int32_t* y, int64_t t) {
+size_t pinned_bytes(const GptGraph& gr) {
+  return (gr.drawn ? 2 * sizeof(uint64_t) : 2 * gr.n * sizeof(int32_t)) + 2 * sizeof(float);
+}
+
+// Step t's inputs into the pinned block, once the last launch has read it.
+void graph_set_inputs(GptGraph& gr, const int32_t* x, const int32_t* y, uint64_t cx, uint64_t cy, int64_t t) {
   if (gr.launched) MALUS_HIP(hipEventSynchronize(gr.done));  // the previous step's copies have read the buffer
-  int32_t* ids = reinterpret_cast<int32_t*>(gr.pinned);
-  memcpy(ids, x, gr.n * sizeof(int32_t));
-  memcpy(ids + gr.n, y, gr.n * sizeof(int32_t));
-  float* bc = reinterpret_cast<float*>(ids + 2 * gr.n);
+  float* bc;
+  if (gr.drawn) {
+    uint64_t* calls = reinterpret_cast<uint64_t*>(gr.pinned);
+    calls[0] = cx;
+    calls[1] = cy;
+    bc = reinterpret_cast<float*>(calls + 2);
+  } else {
+    int32_t* ids = reinterpret_cast<int32_t*>(gr.pinned);
+    memcpy(ids, x, gr.n * sizeof(int32_t));
+    memcpy(ids + gr.n, y, gr.n * sizeof(int32_t));
+    bc = reinterpret_cast<float*>(ids + 2 * gr.n);
+  }
   bc[0] = 1.0f - powf(gr.g->b1, (float)t);  // nanogpt_modular.ml:99-100, as adamw_range computes them
   bc[1] = 1.0f - powf(gr.g->b2, (float)t);
 }
@@ -698,10 +720,18 @@ void graph_set_inputs(GptGraph& gr, const int32_t* x, const int32_t* y, int64_t 
 // The step's work on the stream; the same calls eagerly and under capture.
 int64_t graph_step_body(GptGraph& gr, int64_t t) {
   Gpt& g = *gr.g;
-  const int32_t* ids = reinterpret_cast<const int32_t*>(gr.pinned);
-  MALUS_HIP(hipMemcpyAsync(T(gr.toks)->data(), ids, gr.n * sizeof(int32_t), hipMemcpyHostToDevice, stream()));
-  MALUS_HIP(hipMemcpyAsync(T(gr.tgts)->data(), ids + gr.n, gr.n * sizeof(int32_t), hipMemcpyHostToDevice, stream()));
-  MALUS_HIP(hipMemcpyAsync(gr.bc->data(), ids + 2 * gr.n, 2 * sizeof(float), hipMemcpyHostToDevice, stream()));
+  if (gr.drawn) {
+    const uint64_t* calls = reinterpret_cast<const uint64_t*>(gr.pinned);
+    MALUS_HIP(hipMemcpyAsync(T(gr.calls)->data(), calls, 2 * sizeof(uint64_t), hipMemcpyHostToDevice, stream()));
+    MALUS_HIP(hipMemcpyAsync(gr.bc->data(), calls + 2, 2 * sizeof(float), hipMemcpyHostToDevice, stream()));
+    k::rand_tokens(T(gr.toks)->i32(), T(gr.tgts)->i32(), gr.n, static_cast<const uint64_t*>(T(gr.calls)->data()), 0,
+                   0, (uint32_t)g.V, stream());
+  } else {
+    const int32_t* ids = reinterpret_cast<const int32_t*>(gr.pinned);
+    MALUS_HIP(hipMemcpyAsync(T(gr.toks)->data(), ids, gr.n * sizeof(int32_t), hipMemcpyHostToDevice, stream()));
+    MALUS_HIP(hipMemcpyAsync(T(gr.tgts)->data(), ids + gr.n, gr.n * sizeof(int32_t), hipMemcpyHostToDevice, stream()));
+    MALUS_HIP(hipMemcpyAsync(gr.bc->data(), ids + 2 * gr.n, 2 * sizeof(float), hipMemcpyHostToDevice, stream()));
+  }
   const uint64_t seq = enqueue_mark("graph inputs");
   T(gr.toks)->write_seq = T(gr.tgts)->write_seq = gr.bc->write_seq = seq;
   malus_gpt_zero_grad(&g);
@@ -709,6 +739,97 @@ int64_t graph_step_body(GptGraph& gr, int64_t t) {
   backward(loss);
   adamw_range(g, 0, 8 * g.L + 4, t);
   return loss;
+}
+
+// Launches the replay of the inputs just set; returns the loss handle (a
+// new reference).
+int64_t graph_launch(GptGraph& gr) {
+  MALUS_HIP(hipGraphLaunch(gr.exec, stream()));
+  MALUS_HIP(hipEventRecord(gr.done, stream()));
+  gr.launched = true;
+  const uint64_t seq = enqueue_mark("graph step");
+  Gpt& g = *gr.g;
+  for (size_t i = 0; i < g.p.size(); ++i) T(g.p[i])->write_seq = T(g.m[i])->write_seq = T(g.v[i])->write_seq = seq;
+  T(gr.loss)->write_seq = seq;
+  tensor_retain(gr.loss);
+  return gr.loss;
+}
+
+// Releases what a graph holds (any part may still be unset) and detaches
+// it from its model.  `prev_inplace` is the model's update mode to restore.
+void graph_destroy(GptGraph* gr, bool prev_inplace) {
+  (void)hipStreamSynchronize(stream());
+  if (gr->exec) (void)hipGraphExecDestroy(gr->exec);
+  if (gr->graph) (void)hipGraphDestroy(gr->graph);
+  if (gr->done) (void)hipEventDestroy(gr->done);
+  if (gr->pinned) (void)hipHostFree(gr->pinned);
+  if (gr->loss) tensor_release(gr->loss);
+  if (gr->toks) tensor_release(gr->toks);
+  if (gr->tgts) tensor_release(gr->tgts);
+  if (gr->calls) tensor_release(gr->calls);
+  if (gr->bc) release(gr->bc);
+  if (gr->g) {
+    gr->g->bc_dev = nullptr;
+    gr->g->inplace_opt = prev_inplace;
+  }
+  pool_release_graph(gr->id);
+  delete gr;
+}
+
+GptGraph* graph_create(Gpt* g, bool drawn, const int32_t* x, const int32_t* y, uint64_t cx, uint64_t cy, int64_t t,
+                       int64_t* loss_out) {
+  if (g->bc_dev) fail("malus: gpt_graph_create: the model already has a graph");
+  const bool prev_inplace = g->inplace_opt;
+  auto* gr = new GptGraph();
+  gr->id = ++g_graph_ids;
+  gr->n = (size_t)g->B * g->Tn;
+  gr->drawn = drawn;
+  int64_t eager_loss = 0;
+  try {
+    MALUS_HIP(hipHostMalloc(reinterpret_cast<void**>(&gr->pinned), pinned_bytes(*gr), hipHostMallocDefault));
+    const size_t sh[1] = {gr->n}, sh2[1] = {2};
+    gr->toks = H(alloc_tensor(I32, sh, 1));
+    gr->tgts = H(alloc_tensor(I32, sh, 1));
+    if (drawn) gr->calls = H(alloc_tensor(I64, sh2, 1));
+    gr->bc = alloc_tensor(F32, sh2, 1);
+    MALUS_HIP(hipEventCreateWithFlags(&gr->done, hipEventDisableTiming));
+    gr->g = g;
+    g->inplace_opt = true;
+    g->bc_dev = gr->bc->f32();
+    // eager step t
+    graph_set_inputs(*gr, x, y, cx, cy, t);
+    eager_loss = graph_step_body(*gr, t);
+    MALUS_HIP(hipEventRecord(gr->done, stream()));
+    gr->launched = true;
+    // capture one step (recorded, not run)
+    pool_capture_begin(gr->id);
+    MALUS_HIP(hipStreamBeginCapture(stream(), hipStreamCaptureModeRelaxed));
+    int64_t cap_loss = 0;
+    try {
+      cap_loss = graph_step_body(*gr, t + 1);
+    } catch (...) {
+      hipGraph_t broken = nullptr;
+      (void)hipStreamEndCapture(stream(), &broken);
+      if (broken) (void)hipGraphDestroy(broken);
+      pool_capture_end(gr->id);
+      throw;
+    }
+    MALUS_HIP(hipStreamEndCapture(stream(), &gr->graph));
+    pool_capture_end(gr->id);
+    gr->loss = cap_loss;
+    MALUS_HIP(hipGraphInstantiate(&gr->exec, gr->graph, nullptr, nullptr, 0));
+  } catch (...) {
+    // The eager step may have run: its in-place update stands (as any
+    // eager step's would), and later eager steps use their own bias
+    // corrections again.
+    if (eager_loss) tensor_release(eager_loss);
+    tape_clear();  // the records of a step cut short
+    graph_destroy(gr, prev_inplace);
+    throw;
+  }
+  if (loss_out) *loss_out = eager_loss;
+  else tensor_release(eager_loss);
+  return gr;
 }
 
 }  // namespace
@@ -723,44 +844,18 @@ void* malus_gpt_graph_create(void* gp, const int32_t* x, const int32_t* y, int64
   API_TRY
   auto* g = static_cast<Gpt*>(gp);
   if (!g || !x || !y) fail("malus: gpt_graph_create: null model or token ids");
-  auto gr = std::make_unique<GptGraph>();
-  gr->g = g;
-  gr->id = ++g_graph_ids;
-  gr->n = (size_t)g->B * g->Tn;
-  MALUS_HIP(hipHostMalloc(reinterpret_cast<void**>(&gr->pinned), 2 * gr->n * sizeof(int32_t) + 2 * sizeof(float),
-                          hipHostMallocDefault));
-  const size_t sh[1] = {gr->n}, sh2[1] = {2};
-  gr->toks = H(alloc_tensor(I32, sh, 1));
-  gr->tgts = H(alloc_tensor(I32, sh, 1));
-  gr->bc = alloc_tensor(F32, sh2, 1);
-  MALUS_HIP(hipEventCreateWithFlags(&gr->done, hipEventDisableTiming));
-  g->inplace_opt = true;
-  g->bc_dev = gr->bc->f32();
-  // eager step t
-  graph_set_inputs(*gr, x, y, t);
-  int64_t loss = graph_step_body(*gr, t);
-  MALUS_HIP(hipEventRecord(gr->done, stream()));
-  gr->launched = true;
-  if (loss_out) *loss_out = loss;
-  else tensor_release(loss);
-  // capture one step (recorded, not run)
-  pool_capture_begin(gr->id);
-  MALUS_HIP(hipStreamBeginCapture(stream(), hipStreamCaptureModeRelaxed));
-  int64_t cap_loss = 0;
-  try {
-    cap_loss = graph_step_body(*gr, t + 1);
-  } catch (...) {
-    hipGraph_t broken = nullptr;
-    (void)hipStreamEndCapture(stream(), &broken);
-    if (broken) (void)hipGraphDestroy(broken);
-    pool_capture_end(gr->id);
-    throw;
-  }
-  MALUS_HIP(hipStreamEndCapture(stream(), &gr->graph));
-  pool_capture_end(gr->id);
-  gr->loss = cap_loss;
-  MALUS_HIP(hipGraphInstantiate(&gr->exec, gr->graph, nullptr, nullptr, 0));
-  return gr.release();
+  return graph_create(g, false, x, y, 0, 0, t, loss_out);
+  API_CATCH(nullptr)
+}
+
+// The same with each step's token and target ids drawn on the device by the
+// step's own kernel node: x[i] = rand_int(V) with call index x_call + i, y[i]
+// with y_call + i (the ids malus_rand_tokens_device returns).
+void* malus_gpt_graph_create_drawn(void* gp, uint64_t x_call, uint64_t y_call, int64_t t, int64_t* loss_out) {
+  API_TRY
+  auto* g = static_cast<Gpt*>(gp);
+  if (!g) fail("malus: gpt_graph_create_drawn: null model");
+  return graph_create(g, true, nullptr, nullptr, x_call, y_call, t, loss_out);
   API_CATCH(nullptr)
 }
 
@@ -771,16 +866,21 @@ int64_t malus_gpt_graph_step(void* gh, const int32_t* x, const int32_t* y, int64
   API_TRY
   auto* gr = static_cast<GptGraph*>(gh);
   if (!gr || !x || !y) fail("malus: gpt_graph_step: null graph or token ids");
-  graph_set_inputs(*gr, x, y, t);
-  MALUS_HIP(hipGraphLaunch(gr->exec, stream()));
-  MALUS_HIP(hipEventRecord(gr->done, stream()));
-  gr->launched = true;
-  const uint64_t seq = enqueue_mark("graph step");
-  Gpt& g = *gr->g;
-  for (size_t i = 0; i < g.p.size(); ++i) T(g.p[i])->write_seq = T(g.m[i])->write_seq = T(g.v[i])->write_seq = seq;
-  T(gr->loss)->write_seq = seq;
-  tensor_retain(gr->loss);
-  return gr->loss;
+  if (gr->drawn) fail("malus: gpt_graph_step: this graph draws its ids (use malus_gpt_graph_step_drawn)");
+  graph_set_inputs(*gr, x, y, 0, 0, t);
+  return graph_launch(*gr);
+  API_CATCH(0)
+}
+
+// One replay of a graph made by malus_gpt_graph_create_drawn: step t on the
+// ids drawn from call indices x_call and y_call.
+int64_t malus_gpt_graph_step_drawn(void* gh, uint64_t x_call, uint64_t y_call, int64_t t) {
+  API_TRY
+  auto* gr = static_cast<GptGraph*>(gh);
+  if (!gr) fail("malus: gpt_graph_step_drawn: null graph");
+  if (!gr->drawn) fail("malus: gpt_graph_step_drawn: this graph copies its ids (use malus_gpt_graph_step)");
+  graph_set_inputs(*gr, nullptr, nullptr, x_call, y_call, t);
+  return graph_launch(*gr);
   API_CATCH(0)
 }
 
@@ -789,17 +889,7 @@ void malus_gpt_graph_free(void* gh) {
   auto* gr = static_cast<GptGraph*>(gh);
   if (!gr) return;
   MALUS_HIP(hipStreamSynchronize(stream()));
-  if (gr->exec) MALUS_HIP(hipGraphExecDestroy(gr->exec));
-  if (gr->graph) MALUS_HIP(hipGraphDestroy(gr->graph));
-  MALUS_HIP(hipEventDestroy(gr->done));
-  MALUS_HIP(hipHostFree(gr->pinned));
-  tensor_release(gr->loss);
-  tensor_release(gr->toks);
-  tensor_release(gr->tgts);
-  release(gr->bc);
-  gr->g->bc_dev = nullptr;
-  pool_release_graph(gr->id);
-  delete gr;
+  graph_destroy(gr, true);  // the model keeps its in-place updates
   API_CATCH()
 }
 
@@ -988,7 +1078,16 @@ int64_t malus_gpt_load(void* gp, const char* path) {
     fclose(f);
     throw;
   }
-  auto load_one = [&](const std::string& name, int64_t h) {
+  // Every entry is checked before any is read: F32, the model's shape, and
+  // data offsets [begin, end) with 0 <= begin <= end <= the data section's
+  // size, end - begin = the tensor's bytes, and no two ranges overlapping.
+  struct Item {
+    int64_t h;
+    uint64_t begin, end;
+    std::string name;
+  };
+  std::vector<Item> items;
+  auto check_one = [&](const std::string& name, int64_t h) {
     const Json* e = root.get(name);
     if (!e) fail("malus: gpt_load: %s has no tensor named %s", path, name.c_str());
     const Json* dt = e->get("dtype");
@@ -998,22 +1097,37 @@ int64_t malus_gpt_load(void* gp, const char* path) {
     TensorBuffer* t = T(h);
     if (!sh || sh->k != Json::Arr || (int)sh->arr.size() != t->ndim) fail("malus: gpt_load: %s has the wrong rank", name.c_str());
     for (int d = 0; d < t->ndim; ++d)
-      if ((size_t)sh->arr[(size_t)d].num != t->shape[d])
+      if (sh->arr[(size_t)d].k != Json::Num || sh->arr[(size_t)d].num < 0 ||
+          (size_t)sh->arr[(size_t)d].num != t->shape[d])
         fail("malus: gpt_load: %s has shape mismatching the model's %s", name.c_str(), shape_str(t).c_str());
-    if (!of || of->arr.size() != 2 || (uint64_t)(of->arr[1].num - of->arr[0].num) != t->bytes() ||
-        data0 + (uint64_t)of->arr[1].num > (uint64_t)total)
-      fail("malus: gpt_load: %s has bad data offsets", name.c_str());
-    std::vector<char> buf(t->bytes());
-    fseek(f, (long)(data0 + (uint64_t)of->arr[0].num), SEEK_SET);
-    if (fread(buf.data(), 1, buf.size(), f) != buf.size()) fail("malus: gpt_load: short read of %s", name.c_str());
-    upload(t->data(), buf.data(), buf.size());
-    t->write_seq = enqueue_mark("checkpoint load");
+    if (!of || of->k != Json::Arr || of->arr.size() != 2 || of->arr[0].k != Json::Num || of->arr[1].k != Json::Num)
+      fail("malus: gpt_load: %s has no [begin, end] data offsets", name.c_str());
+    const long long b0 = of->arr[0].num, e0 = of->arr[1].num;
+    const uint64_t data_bytes = (uint64_t)total > data0 ? (uint64_t)total - data0 : 0;
+    if (b0 < 0 || e0 < b0 || (uint64_t)e0 > data_bytes || (uint64_t)(e0 - b0) != t->bytes())
+      fail("malus: gpt_load: %s has bad data offsets [%lld, %lld) for %zu bytes in a %llu-byte data section",
+           name.c_str(), b0, e0, t->bytes(), (unsigned long long)data_bytes);
+    items.push_back({h, (uint64_t)b0, (uint64_t)e0, name});
   };
   try {
     for (int i = 0; i < g->np(); ++i) {
-      load_one(param_name(*g, i), g->p[(size_t)i]);
-      load_one("adam_m." + param_name(*g, i), g->m[(size_t)i]);
-      load_one("adam_v." + param_name(*g, i), g->v[(size_t)i]);
+      check_one(param_name(*g, i), g->p[(size_t)i]);
+      check_one("adam_m." + param_name(*g, i), g->m[(size_t)i]);
+      check_one("adam_v." + param_name(*g, i), g->v[(size_t)i]);
+    }
+    std::vector<const Item*> order;
+    for (auto& it : items) order.push_back(&it);
+    std::sort(order.begin(), order.end(), [](const Item* x, const Item* y) { return x->begin < y->begin; });
+    for (size_t i = 1; i < order.size(); ++i)
+      if (order[i]->begin < order[i - 1]->end)
+        fail("malus: gpt_load: the data of %s and %s overlap", order[i - 1]->name.c_str(), order[i]->name.c_str());
+    for (auto& it : items) {
+      TensorBuffer* t = T(it.h);
+      std::vector<char> buf(t->bytes());
+      fseek(f, (long)(data0 + it.begin), SEEK_SET);
+      if (fread(buf.data(), 1, buf.size(), f) != buf.size()) fail("malus: gpt_load: short read of %s", it.name.c_str());
+      upload(t->data(), buf.data(), buf.size());
+      t->write_seq = enqueue_mark("checkpoint load");
     }
   } catch (...) {
     fclose(f);

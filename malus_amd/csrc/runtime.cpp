@@ -35,6 +35,7 @@ namespace malus {
 // errors
 // ============================================================================
 static std::atomic<int> g_abort_on_error{1};
+thread_local int g_api_depth = 0;
 static thread_local std::string g_last_error;
 
 size_t dtype_size(int32_t tag) {
@@ -119,6 +120,7 @@ struct Context {
   bool sync_dispatch = false;
   bool histogram = false;
   int64_t budget = -1;  // -1: derive from env
+  int64_t fail_alloc_after = -1;  // fault injection for error-path tests: -1 off
 };
 
 Context* g_ctx = nullptr;
@@ -234,6 +236,7 @@ void* pool_alloc(size_t bytes, size_t* bucket_out) {
   Context& c = ctx();
   size_t b = bucket_size(bytes);
   std::lock_guard<std::mutex> lk(c.pool.mu);
+  if (c.fail_alloc_after >= 0 && c.fail_alloc_after-- == 0) fail("malus: injected allocation failure (%zu bytes)", b);
   if (c.histogram) c.pool.histogram[b]++;
   auto it = c.pool.free_lists.find(b);
   if (it != c.pool.free_lists.end() && !it->second.empty()) {
@@ -576,7 +579,7 @@ using namespace malus;
 // ============================================================================
 extern "C" {
 
-void malus_set_abort_on_error(int on) { g_abort_on_error.store(on ? 1 : 0); }
+int malus_set_abort_on_error(int on) { return g_abort_on_error.exchange(on ? 1 : 0); }
 const char* malus_last_error(void) { return g_last_error.c_str(); }
 void malus_clear_error(void) { g_last_error.clear(); }
 
@@ -781,6 +784,20 @@ int64_t malus_randn_device(const size_t* shape, size_t ndim) {
   API_CATCH(0)
 }
 
+// i.i.d. token ids on the device: out[i] = rand_int(vocab) with call index
+// call + i, the ids the host builtin's loop draws (metal.rs:1741-1759).  A new
+// [n] i32 tensor.
+int64_t malus_rand_tokens_device(uint64_t call, size_t n, int64_t vocab) {
+  API_TRY
+  if (vocab < 1 || vocab > INT32_MAX) fail("malus: rand_tokens: vocab %lld out of range", (long long)vocab);
+  const size_t sh[1] = {n};
+  TensorBuffer* t = alloc_tensor(I32, sh, 1);
+  k::rand_tokens(t->i32(), nullptr, n, nullptr, call, 0, (uint32_t)vocab, stream());
+  t->write_seq = enqueue_mark("rand_tokens");
+  return H(t);
+  API_CATCH(0)
+}
+
 // The batch of nanogpt_modular.ml:170-177 built on the device from a
 // device-resident i32 token stream `data`: for b in 0..B, start =
 // rand_int(len(data) - T - 1) (one RNG call each, as the host loop makes
@@ -947,6 +964,7 @@ void malus_pool_reset(void) {
   API_CATCH()
 }
 void malus_set_mem_budget(int64_t bytes) { ctx().budget = bytes < 0 ? -1 : bytes; }
+void malus_fail_alloc_after(int64_t n) { ctx().fail_alloc_after = n < 0 ? -1 : n; }
 size_t malus_alloc_histogram(size_t* sizes, uint64_t* counts, size_t cap) {
   Context& c = ctx();
   std::lock_guard<std::mutex> lk(c.pool.mu);

@@ -6,10 +6,15 @@ broadcast, forward and backward.  The tensor-scalar product `0.5*c` records
 no tape node (codegen-cpu/src/lib.rs:1556-1580), so c receives no gradient;
 the other gradients are sums of +-1, b and a and come out bit-exact.
 
-C3: layernorm with gamma = 1 and beta = 0 perturbed by
-N(0, 0.02) (nanogpt_modular.ml:38-45 applies the weight as a broadcast mul),
-through the tape with a random upstream gradient: normwise 1e-5 against the
-oracle's composition of the same VJPs.
+Both run at the configuration's own [8192, 8192] and at 1/64 of it.
+
+C3 (configs[2]), at [65536, 1024]: layernorm with gamma = 1 and beta = 0
+perturbed by N(0, 0.02) (nanogpt_modular.ml:38-45 applies the weight as a
+broadcast mul), through the tape with a random upstream gradient: normwise
+1e-5 against the oracle's composition of the same VJPs (also at 4,096 rows);
+softmax, GELU and cross-entropy (logits ~ N(0, 2), int32 targets in
+[0, 1024)) forward and backward, and the axis-0 and axis-1 sums, against the
+oracle at the bars of tests/helpers.py.
 
 C5 (configs[4]): three training steps (loss within 1e-5 relative each step;
 after the third, at most 0.1% of the parameters more than 1e-5 apart)."""
@@ -21,7 +26,7 @@ import pytest
 
 import malus_amd as M
 from oracle import oracle as O
-from tests.helpers import assert_bitexact, assert_normwise, normwise_err
+from tests.helpers import assert_bitexact, assert_normwise, assert_reduction, normwise_err
 
 pytestmark = pytest.mark.gpu
 
@@ -52,10 +57,10 @@ def grad(rt, h):
     return out
 
 
-def test_c2_chain_through_the_tape(tape):
+@pytest.mark.parametrize("R,Cc", [(1024, 1024), (8192, 8192)], ids=["1_64th", "full_2pow26"])
+def test_c2_chain_through_the_tape(tape, R, Cc):
     rt = tape
     rng = np.random.default_rng(2)
-    R, Cc = 1024, 1024  # the C2 shapes at 1/64 of the elements
     a, b, c = (rng.uniform(-1, 1, (R, Cc)).astype(np.float32) for _ in range(3))
     bias = rng.uniform(-1, 1, (1, Cc)).astype(np.float32)
     ha, hb, hc, hbias = leaf(rt, a), leaf(rt, b), leaf(rt, c), leaf(rt, bias)
@@ -86,10 +91,11 @@ def test_c2_chain_through_the_tape(tape):
     rt.free(ha, hb, hc, hbias, ab, half_c, s1, r, z, y)
 
 
-def test_c3_affine_layernorm_through_the_tape(tape):
+@pytest.mark.parametrize("R", [4096, 65536], ids=["1_16th", "full_65536"])
+def test_c3_affine_layernorm_through_the_tape(tape, R):
     rt = tape
     rng = np.random.default_rng(3)
-    R, Cc = 4096, 1024  # the C3 row length at 1/16 of the rows
+    Cc = 1024
     x = rng.standard_normal((R, Cc)).astype(np.float32)
     gamma = (1.0 + 0.02 * rng.standard_normal(Cc)).astype(np.float32)
     beta = (0.02 * rng.standard_normal(Cc)).astype(np.float32)
@@ -120,6 +126,74 @@ def test_c3_affine_layernorm_through_the_tape(tape):
     assert_normwise(grad(rt, hg), dgamma, 1e-5, "dgamma")
     assert_normwise(grad(rt, hx), dx, 1e-5, "dx")
     rt.free(hx, hg, hbeta, hup, hy, hs, ho, hl)
+
+
+C3_ROWS, C3_COLS = 65536, 1024
+
+
+def run(rt, h):
+    assert h, rt.last_error()
+    out = rt.numpy(h)
+    rt.free(h)
+    return out
+
+
+def test_c3_softmax_at_full_size(rt):
+    rng = np.random.default_rng(31)
+    x = rng.uniform(-4, 4, (C3_ROWS, C3_COLS)).astype(np.float32)
+    d = rng.uniform(-1, 1, (C3_ROWS, C3_COLS)).astype(np.float32)
+    hx, hd = rt.tensor(x), rt.tensor(d)
+    hy = rt.L.malus_std_softmax_fwd(hx, 1)
+    y = rt.numpy(hy)
+    assert_normwise(y, O.softmax(x, 1), 1e-5, "softmax [65536,1024]")
+    assert_normwise(run(rt, rt.L.malus_std_softmax_bwd(hy, hd, 1)), O.softmax_bwd(y, d, 1), 1e-5, "softmax bwd")
+    rt.free(hx, hd, hy)
+
+
+def test_c3_gelu_at_full_size(rt):
+    rng = np.random.default_rng(32)
+    x = rng.uniform(-8, 8, (C3_ROWS, C3_COLS)).astype(np.float32)
+    d = rng.uniform(-1, 1, (C3_ROWS, C3_COLS)).astype(np.float32)
+    hx, hd = rt.tensor(x), rt.tensor(d)
+    got = run(rt, rt.L.malus_std_gelu_fwd(hx))
+    want = O.unary(O.GELU, x)
+    # 2 ulp of the result plus the propagated 2-ulp tanh uncertainty 0.5|x| * 2 ulp(1)
+    bound = 2 * np.spacing(np.abs(want)) + 0.5 * np.abs(x) * 2 * np.spacing(np.float32(1.0)) * 2
+    assert np.all(np.abs(got - want) <= bound), "gelu [65536,1024] beyond the derived bound"
+    del got, want, bound
+    assert_normwise(run(rt, rt.L.malus_std_gelu_bwd(hx, hd)), O.unary_bwd(O.GELU, x, d), 1e-5, "gelu bwd")
+    rt.free(hx, hd)
+
+
+def test_c3_cross_entropy_at_full_size(rt):
+    rng = np.random.default_rng(33)
+    logits = (rng.standard_normal((C3_ROWS, C3_COLS)) * 2).astype(np.float32)
+    t = rng.integers(0, C3_COLS, C3_ROWS).astype(np.int32)
+    hl, ht = rt.tensor(logits), rt.tensor(t)
+    hp = C.c_int64()
+    hloss = rt.L.malus_std_cross_entropy_fwd(hl, ht, C.byref(hp))
+    loss, probs = rt.numpy(hloss), rt.numpy(hp.value)
+    wl, wp = O.cross_entropy(logits, t)
+    assert_normwise(probs, wp, 1e-5, "probs [65536,1024]")
+    # the loss is a mean over 65,536 rows: within 1e-5 of the float64 mean of
+    # -log p[target], or no farther from it than the oracle's sequential sum
+    exact = -np.mean(np.log(wp[np.arange(C3_ROWS), t].astype(np.float64)))
+    assert_reduction(loss, np.array([wl]), np.array([exact]), 1e-5, "ce loss")
+    hd = rt.tensor(np.array([1.0], np.float32))
+    got = run(rt, rt.L.malus_std_cross_entropy_bwd(hp.value, ht, hd))
+    assert_normwise(got, O.cross_entropy_bwd(probs, t, 1.0), 1e-6, "ce bwd")
+    rt.free(hl, ht, hloss, hp.value, hd)
+
+
+@pytest.mark.parametrize("axis", [0, 1])
+def test_c3_axis_sums_at_full_size(rt, axis):
+    rng = np.random.default_rng(34 + axis)
+    x = rng.uniform(-2, 2, (C3_ROWS, C3_COLS)).astype(np.float32)
+    hx = rt.tensor(x)
+    got = run(rt, rt.L.malus_std_reduce_fwd(M.R_SUM, hx, axis, 0))
+    exact = x.astype(np.float64).sum(axis=axis)
+    assert_reduction(got, O.reduce_axis(O.R_SUM, x, axis), exact, 1e-5, f"sum over axis {axis} of [65536,1024]")
+    rt.free(hx)
 
 
 def test_c5_three_step_trajectory(rt):

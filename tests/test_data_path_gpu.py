@@ -61,6 +61,19 @@ def test_batch_windows_are_the_host_loop(rt):
     rt.free(hdata, hx.value, hy.value)
 
 
+@pytest.mark.parametrize("call,n,vocab", [(0, 16384, 65), ((1 << 32) - 100, 1000, 65), (7, 1, 1), (123, 777, 1024),
+                                         ((5 << 40) + 3, 70000, 50257)])
+def test_rand_tokens_device_is_the_host_draw(rt, call, n, vocab):
+    # the device draw equals the host builtin's loop (rand_int per token with
+    # call index call + i), key words crossing 2^32 included
+    h = rt.L.malus_rand_tokens_device(call, n, vocab)
+    assert h, rt.last_error()
+    got = rt.numpy(h)
+    rt.free(h)
+    assert got.dtype == np.int32
+    assert_bitexact(got, O.rand_tokens(call, n, vocab), f"rand_tokens call {call} n {n} vocab {vocab}")
+
+
 def test_batch_windows_rejects_short_data(rt):
     hdata = rt.tensor(np.arange(10, dtype=np.int32))
     hx, hy = C.c_int64(), C.c_int64()
@@ -136,4 +149,53 @@ def test_checkpoint_resume_is_bit_identical_and_readable(rt, tmp_path):
         rt.L.malus_set_abort_on_error(1)
     rt.L.malus_gpt_free(g2)
     rt.L.malus_gpt_free(g3)
+    rt.L.tape_reset()
+
+
+def test_checkpoint_with_malformed_offsets_is_refused(rt, tmp_path):
+    import json
+    import struct
+
+    cfg = dict(V=65, T=16, C=32, H=4, L=1, B=2)
+    path = tmp_path / "gpt.safetensors"
+    g = _gpt(rt, cfg, 0)
+    assert rt.L.malus_gpt_save(g, str(path).encode(), 1) == 0
+    raw = path.read_bytes()
+    n = struct.unpack("<Q", raw[:8])[0]
+    hdr, data = json.loads(raw[8:8 + n]), raw[8 + n:]
+    before = [rt.numpy(rt.L.malus_gpt_param(g, i)) for i in range(rt.L.malus_gpt_nparams(g))]
+
+    def write(h):
+        b = json.dumps(h).encode()
+        p = tmp_path / "bad.safetensors"
+        p.write_bytes(struct.pack("<Q", len(b)) + b + data)
+        return str(p).encode()
+
+    wq, wk = hdr["blocks.0.wq"]["data_offsets"], hdr["blocks.0.wk"]["data_offsets"]
+    cases = []
+    h = json.loads(json.dumps(hdr))
+    h["blocks.0.wq"]["data_offsets"] = [-8, wq[1] - wq[0] - 8]  # header bytes as data
+    cases.append((h, "bad data offsets"))
+    h = json.loads(json.dumps(hdr))
+    h["blocks.0.wq"]["data_offsets"] = list(wk)  # two tensors on the same bytes
+    cases.append((h, "overlap"))
+    h = json.loads(json.dumps(hdr))
+    h["blocks.0.wq"]["data_offsets"] = [len(data) - 4, len(data) - 4 + wq[1] - wq[0]]  # past the end
+    cases.append((h, "bad data offsets"))
+    h = json.loads(json.dumps(hdr))
+    h["blocks.0.wq"]["data_offsets"] = ["0", str(wq[1] - wq[0])]  # not numbers
+    cases.append((h, "data offsets"))
+    rt.L.malus_set_abort_on_error(0)
+    try:
+        for h, msg in cases:
+            assert rt.L.malus_gpt_load(g, write(h)) == -1
+            assert msg in rt.last_error(), rt.last_error()
+            rt.L.malus_clear_error()
+    finally:
+        rt.L.malus_set_abort_on_error(1)
+    # nothing was read into the model
+    for i, p in enumerate(before):
+        np.testing.assert_array_equal(rt.numpy(rt.L.malus_gpt_param(g, i)), p)
+    assert rt.L.malus_gpt_load(g, write(hdr)) == 1
+    rt.L.malus_gpt_free(g)
     rt.L.tape_reset()

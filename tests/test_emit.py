@@ -239,3 +239,20 @@ def test_mutated_programs_lower_or_fail_cleanly():
     assert lowered and rejected
     (name, _, _), = M.compile_kernels(SIGMOID_BACKWARD).entries
     assert name == "sigmoid_backward"
+
+
+def test_implicit_kernels_declare_their_element_widths():
+    # kernel_dispatch allocates the v1 output with input 0's dtype
+    # (metal.rs:1878-1888); the emitted kernel states the widths it reads and
+    # writes, and the runtime refuses a launch where they disagree (an f16
+    # input 0 would give a 2-byte output that an f32 kernel overruns).
+    prog = "kernel widen(a: Tensor<f16>, b: Tensor<f32>) -> Tensor<f32>:\n    return b\n"
+    (name, kid, src), = M.compile_kernels(prog).entries
+    assert "//@malus-v1-elem-bytes 4 2 4\n" in src
+    rtc(src)
+    (_, _, src), = M.compile_kernels(SIGMOID_BACKWARD).entries
+    assert "//@malus-v1-elem-bytes 4 4 4\n" in src
+    r = M.compile_kernels("", ["malus_add", "malus_mul_scalar", "exp"])
+    for name, _, src in r.entries:
+        want = "4 4" if name == "exp" else "4 4 4"
+        assert f"//@malus-v1-elem-bytes {want}\n" in src, name

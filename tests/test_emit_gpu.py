@@ -179,6 +179,9 @@ def test_emitted_math_builtins_pow_and_logic(rt, kid):
 def test_emitted_kernel_abi_checks(rt, kid):
     x = RNG.uniform(-1, 1, 64).astype(np.float32)
     hx, hshort = rt.tensor(x), rt.tensor(x[:10])
+    reg = M.compile_kernels("kernel widen(a: Tensor<i64>, b: Tensor<f32>) -> Tensor<f32>:\n    return b\n")
+    rt.L.malus_runtime_init(*reg.init_args())
+    wid = reg.ids["widen"]
     rt.L.malus_set_abort_on_error(0)
     try:
         # the uniforms blob must be the size the emitted kernel declares
@@ -189,6 +192,19 @@ def test_emitted_kernel_abi_checks(rt, kid):
         assert v1(rt, kid, "malus_add", [hx, hshort]) == 0
         assert "shorter than" in rt.last_error()
         rt.L.malus_clear_error()
+        # the element widths the kernel declares must be the tensors' (the
+        # output takes input 0's dtype, metal.rs:1878-1888)
+        h64 = rt.tensor(np.arange(64, dtype=np.int64))
+        assert v1(rt, kid, "malus_add", [h64, hx]) == 0
+        assert "writes 4-byte elements" in rt.last_error()
+        rt.L.malus_clear_error()
+        assert rt.L.kernel_dispatch(wid, M.handles([h64, hx]), 2) == 0
+        assert "writes 4-byte elements, but its output takes input 0's dtype (8-byte elements)" in rt.last_error()
+        rt.L.malus_clear_error()
+        assert rt.L.kernel_dispatch(wid, M.handles([hx, hx]), 2) == 0
+        assert "reads input 0 as 8-byte elements" in rt.last_error()
+        rt.L.malus_clear_error()
+        rt.free(h64)
     finally:
         rt.L.malus_set_abort_on_error(1)
     rt.free(hx, hshort)

@@ -85,3 +85,26 @@ def test_noalloc_rejects_reductions_past_the_scratch_array(rt):
     h = rt.L.malus_std_reduce_fwd(M.R_VAR, hx, 0, 0)
     assert np.all(rt.numpy(h) == 0.0)
     rt.free(h, hx, hout)
+
+
+@pytest.mark.parametrize("shape,axis", [((65536, 64), 0), ((3, 4000, 96), 1)])
+def test_noalloc_variance_with_unaligned_output(rt, shape, axis):
+    # x 16-byte aligned, out 4 bytes past an aligned address: the variance's
+    # mean pass plans with x and its own aligned mean, the second pass with
+    # x, the mean and out, so the two passes take different column plans
+    x = RNG.uniform(-2, 2, shape).astype(np.float32)
+    hx = rt.tensor(x)
+    osh = out_shape(shape, axis)
+    n = int(np.prod(osh))
+    hout = rt.L.tensor_alloc_gpu(M.F32, M.sizes((n + 1,)), 1, None)
+    rc = rt.L.malus_std_reduce_noalloc(M.R_VAR, rt.L.malus_tensor_device_ptr(hx), M.sizes(shape), len(shape), axis,
+                                       rt.L.malus_tensor_device_ptr(hout) + 4)
+    assert rc == 0, rt.last_error()
+    rt.L.gpu_barrier()
+    got = rt.numpy(hout).ravel()[1:]
+    want_h = rt.L.malus_std_reduce_fwd(M.R_VAR, hx, axis, 0)
+    want = rt.numpy(want_h).ravel()
+    rt.free(want_h, hout, hx)
+    exact = x.astype(np.float64).var(axis=axis).ravel()
+    assert_reduction(got, O.reduce_axis(M.R_VAR, x, axis).ravel(), exact, 1e-5, "unaligned-out variance vs oracle")
+    assert_reduction(want, O.reduce_axis(M.R_VAR, x, axis).ravel(), exact, 1e-5, "reduce_fwd variance vs oracle")
