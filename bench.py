@@ -414,7 +414,7 @@ def run_gpt(rt, a, cfg):
     # docs/adr/0037-bf16-autocast.md:5-12: the whole step inside `with autocast:`
     L.malus_autocast(1 if a.autocast else 0)
     n = cfg["B"] * cfg["T"]
-    gemm_steps = min(a.steps, 20)
+    gemm_steps = 0 if a.no_gemm_pass else min(a.steps, 20)
 
     t = 0
     graph = None
@@ -487,14 +487,15 @@ def run_gpt(rt, a, cfg):
     med = statistics.median(times)
     step_flops = gemm_flops_per_step(cfg)
     gemm_tflops = gflop.value / (gms.value * 1e-3) / 1e12 if gms.value > 0 else 0.0
+    gsteps = max(gemm_steps, 1)
     log(f"steps {a.steps}: median {med:.3f} ms  min {min(times):.3f}  max {max(times):.3f}  wall {wall:.2f} s  "
         f"(host enqueue median {statistics.median(enq):.3f} ms)")
     log(f"loss first {first_loss:.4f} last {last_loss:.4f}")
     ps = (C.c_int64 * 4)()
     L.malus_pool_stats(ps)
     log(f"pool: hits {ps[0]} misses {ps[1]} peak device bytes {ps[3] / 1e9:.2f} GB")
-    log(f"gemm ({gemm_steps} separate steps): {ng} launches, {gms.value / gemm_steps:.3f} ms/step, "
-        f"{gemm_tflops:.1f} TFLOP/s ({gflop.value / gemm_steps / 1e9:.1f} GFLOP/step; "
+    log(f"gemm ({gemm_steps} separate steps): {ng} launches, {gms.value / gsteps:.3f} ms/step, "
+        f"{gemm_tflops:.1f} TFLOP/s ({gflop.value / gsteps / 1e9:.1f} GFLOP/step; "
         f"algorithmic {step_flops / 1e9:.1f})")
 
     cpu = None
@@ -542,8 +543,8 @@ def run_gpt(rt, a, cfg):
                      "algorithmic_bytes": gemm_bytes_per_step(cfg),
                      "timing": f"HIP events around each GEMM launch over {gemm_steps} steps run after the "
                                "headline steps (the headline runs with the event timer off)",
-                     "gemm_ms_per_step": round(gms.value / gemm_steps, 3),
-                     "gemm_gflop_per_step": round(gflop.value / gemm_steps / 1e9, 1)},
+                     "gemm_ms_per_step": round(gms.value / gsteps, 3),
+                     "gemm_gflop_per_step": round(gflop.value / gsteps / 1e9, 1)},
         "cpu_baseline": cpu,
     }
 
@@ -569,6 +570,9 @@ def main():
                          "fused VJPs and the fused optimizer off, composed attention, eager launches; reported "
                          "beside the headline, never in its place")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-gemm-pass", action="store_true",
+                    help="skip the event-timed eager GEMM pass after the headline steps (for a kernel trace of the "
+                         "headline steps alone; the roofline figures are then empty)")
     ap.add_argument("--cpu-threads", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB copy (counter calibration for the traffic figure)")

@@ -158,24 +158,58 @@ __global__ __launch_bounds__(256) void k_emb_list(const int32_t* __restrict__ id
 }
 
 // k_emb_rows: dw[v, 4c .. 4c + 3] = the sum of dout[t, 4c ..] over row v's
-// token list, in list order (the same adds as k_emb_accum); sixteen rows'
-// loads are in flight before their adds.
+// token list, in list order (the same adds as k_emb_accum).  One lane per
+// (row, 4-column group), lanes packed across rows.  Each chain is a run of
+// dependent adds over its list, so the list is walked in batches of R
+// float4 loads that are all in flight before their adds, with the next
+// batch's positions loaded meanwhile (a chain of ~250 tokens then costs a
+// handful of memory round trips instead of one per 16 tokens).
+template <int R>
 __global__ __launch_bounds__(64) void k_emb_rows(const float4* __restrict__ dout, const uint32_t* __restrict__ pos,
                                                  const uint32_t* __restrict__ count, float4* __restrict__ dw, size_t t,
-                                                 uint32_t d4, uint32_t col_blocks) {
-  const uint32_t row = blockIdx.x / col_blocks;
-  const uint32_t c = (blockIdx.x % col_blocks) * 64 + threadIdx.x;
-  if (c >= d4) return;
+                                                 uint32_t d4, uint32_t chains) {
+  static_assert(R % 4 == 0, "positions are loaded four at a time");
+  const uint32_t g = blockIdx.x * 64 + threadIdx.x;
+  if (g >= chains) return;
+  const uint32_t row = g / d4, c = g % d4;
   const uint32_t n = count[row];
-  const uint32_t* p = pos + (size_t)row * t;
+  const uint32_t* p = pos + (size_t)row * t;  // R > 0: 16-byte aligned (the host takes this form for t % 4 == 0)
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   uint32_t k = 0;
-  for (; k + 16 <= n; k += 16) {
-    float4 a[16];
+  if constexpr (R > 0) {
+    uint4 ix[R / 4];
+    if (R <= n) {
 #pragma unroll
-    for (int u = 0; u < 16; ++u) a[u] = dout[(size_t)p[k + u] * d4 + c];
+      for (int u = 0; u < R / 4; ++u) ix[u] = reinterpret_cast<const uint4*>(p)[u];
+    }
+    for (; k + R <= n; k += R) {
+      float4 a[R];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
+      for (int u = 0; u < R / 4; ++u) {
+        a[4 * u] = dout[(size_t)ix[u].x * d4 + c];
+        a[4 * u + 1] = dout[(size_t)ix[u].y * d4 + c];
+        a[4 * u + 2] = dout[(size_t)ix[u].z * d4 + c];
+        a[4 * u + 3] = dout[(size_t)ix[u].w * d4 + c];
+      }
+      if (k + 2 * R <= n) {
+#pragma unroll
+        for (int u = 0; u < R / 4; ++u) ix[u] = reinterpret_cast<const uint4*>(p + k + R)[u];
+      }
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        acc.x += a[u].x;
+        acc.y += a[u].y;
+        acc.z += a[u].z;
+        acc.w += a[u].w;
+      }
+    }
+  }
+  for (; k + 8 <= n; k += 8) {
+    float4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = dout[(size_t)p[k + u] * d4 + c];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
       acc.x += a[u].x;
       acc.y += a[u].y;
       acc.z += a[u].z;
@@ -299,15 +333,19 @@ void embedding_bwd(const float* dout, const int32_t* idx, float* dw, size_t t, s
   if (!t) { fill(dw, 0.0f, v * d, s); return; }
   size_t b_count, b_offs, b_pos;
   const auto aligned = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  if (d % 4 == 0 && v * t <= ((size_t)1 << 24) && aligned(dout) && aligned(dw)) {
+  if (d % 4 == 0 && v * t <= ((size_t)1 << 24) && v * (d / 4) < ((size_t)1 << 31) && aligned(dout) && aligned(dw)) {
     uint32_t* count = static_cast<uint32_t*>(pool_alloc(v * sizeof(uint32_t), &b_count));
     uint32_t* pos = static_cast<uint32_t*>(pool_alloc(v * t * sizeof(uint32_t), &b_pos));
     if (t % 4 == 0 && aligned(idx)) k_emb_list<true><<<(unsigned)v, 256, 0, s>>>(idx, t, pos, count);
     else k_emb_list<false><<<(unsigned)v, 256, 0, s>>>(idx, t, pos, count);
     MALUS_HIP(hipGetLastError());
-    const uint32_t d4 = (uint32_t)(d / 4), col_blocks = (d4 + 63) / 64;
-    k_emb_rows<<<(unsigned)(v * col_blocks), 64, 0, s>>>(reinterpret_cast<const float4*>(dout), pos, count,
-                                                         reinterpret_cast<float4*>(dw), t, d4, col_blocks);
+    const uint32_t d4 = (uint32_t)(d / 4), chains = (uint32_t)(v * d4);
+    if (t % 4 == 0)
+      k_emb_rows<48><<<(chains + 63) / 64, 64, 0, s>>>(reinterpret_cast<const float4*>(dout), pos, count,
+                                                        reinterpret_cast<float4*>(dw), t, d4, chains);
+    else
+      k_emb_rows<0><<<(chains + 63) / 64, 64, 0, s>>>(reinterpret_cast<const float4*>(dout), pos, count,
+                                                       reinterpret_cast<float4*>(dw), t, d4, chains);
     MALUS_HIP(hipGetLastError());
     pool_free(count, b_count);
     pool_free(pos, b_pos);
