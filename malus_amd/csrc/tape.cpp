@@ -16,6 +16,8 @@
 #include "api.h"
 #include "common.h"
 
+extern "C" const char* malus_last_error(void);
+
 namespace malus {
 namespace {
 
@@ -83,9 +85,36 @@ size_t slot(int32_t s) {
   return p;
 }
 
+// A registered slot may be foreign code (the JIT's own VJP functions), and
+// no C++ exception may cross it: the slot runs as an outermost call (any
+// entry point it calls turns an error into a null handle and the last
+// error), and a null result is raised here, in the tape's own frame.
+struct SlotDepth {
+  int saved;
+  SlotDepth() : saved(g_api_depth) { g_api_depth = 0; }
+  ~SlotDepth() { g_api_depth = saved; }
+};
+
 template <class F>
-F slot_fn(int32_t s) {
-  return reinterpret_cast<F>(slot(s));
+struct SlotCall;
+template <class... A>
+struct SlotCall<int64_t (*)(A...)> {
+  int32_t s;
+  int64_t (*f)(A...);
+  int64_t operator()(A... a) const {
+    int64_t r;
+    {
+      SlotDepth isolate;
+      r = f(a...);
+    }
+    if (!r) fail("malus: the function in backward slot %d failed: %s", s, malus_last_error());
+    return r;
+  }
+};
+
+template <class F>
+SlotCall<F> slot_fn(int32_t s) {
+  return SlotCall<F>{s, reinterpret_cast<F>(slot(s))};
 }
 
 using Fn1 = int64_t (*)(int64_t);

@@ -550,3 +550,43 @@ def test_hiprtc_user_kernels_v1_and_v2(rt):
                                  0, struct.pack("<i", 8), 4)
     assert_normwise(rt.numpy(ho), O.softmax(x, 1), 1e-5, "user softmax")
     rt.free(hg, hs, hx, ho)
+
+
+def test_foreign_backward_slot_error_comes_back_as_a_value(rt):
+    """A registered backward function may be foreign code (the JIT's own
+    VJPs, here a ctypes callback): no exception may cross it.  An entry point
+    it calls that fails returns a null handle to it, and backward reports the
+    slot's failure with the inner message (return-error mode)."""
+    L = rt.L
+    RELU_BWD = 9  # BwdSlot numbering, tape.rs:92-175
+    FN2 = C.CFUNCTYPE(C.c_int64, C.c_int64, C.c_int64)
+    a, b = rt.tensor(np.ones((2, 3), np.float32)), rt.tensor(np.ones((4, 5), np.float32))
+    seen = []
+
+    def foreign(dout, x):
+        seen.append((dout, x))
+        return L.tensor_matmul(a, b)  # fails: inner dims 3 != 4
+
+    cb = FN2(foreign)
+    prev = L.malus_tape_backward_fn(RELU_BWD)
+    L.tape_reset()
+    x = rt.tensor(np.array([-1.0, 2.0, 3.0], np.float32))
+    L.tape_register_leaf(x)
+    r = L.malus_std_unary(M.RELU, x)
+    L.tape_record_unary(OP["Relu"], x, r)
+    L.tape_register_backward_fn(RELU_BWD, C.cast(cb, C.c_void_p).value)
+    L.malus_set_abort_on_error(0)
+    try:
+        L.backward(r)
+        err = rt.last_error()
+        L.malus_clear_error()
+    finally:
+        L.malus_set_abort_on_error(1)
+        L.tape_register_backward_fn(RELU_BWD, prev)
+        L.tape_reset()
+    assert len(seen) == 1
+    assert "backward slot 9 failed" in err and "matmul shape mismatch" in err, err
+    # the library is usable afterwards, and the default slot is back
+    y = L.malus_std_unary(M.RELU, x)
+    assert np.array_equal(rt.numpy(y), [0.0, 2.0, 3.0])
+    rt.free(a, b, x, r, y)
