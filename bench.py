@@ -411,6 +411,8 @@ def run_gpt(rt, a, cfg):
         L.malus_gpt_set_fused_forward(g, 0)
         L.malus_gpt_set_fused_optimizer(g, 0)
         L.malus_tape_set_fused_vjps(0)
+    if a.f32_activations:
+        L.malus_gpt_set_bf16_activations(g, 0)
     # docs/adr/0037-bf16-autocast.md:5-12: the whole step inside `with autocast:`
     L.malus_autocast(1 if a.autocast else 0)
     n = cfg["B"] * cfg["T"]
@@ -524,7 +526,10 @@ def run_gpt(rt, a, cfg):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 GEMM operands, f32 accumulation and everything else f32 (autocast)" if a.autocast else "f32",
+        "dtype": ("bf16 GEMM operands, f32 accumulation; the activations read only by GEMMs stored in bf16 "
+                  "(layernorm-scale outputs, gelu(h), dh), everything else f32 (autocast)")
+                 if a.autocast and not a.f32_activations else
+                 "bf16 GEMM operands, f32 accumulation and everything else f32 (autocast)" if a.autocast else "f32",
         "data": "synthetic int32 tokens i.i.d. uniform in [0,65), drawn on the device inside each timed step "
                 "(rand_int per token, Philox keyed by call index); weights randn*0.02 (Philox, call 0)",
         "attention": a.attention,
@@ -569,6 +574,9 @@ def main():
                     help="the op sequence an unchanged nanogpt_modular.ml issues through the C ABI: forward fusions, "
                          "fused VJPs and the fused optimizer off, composed attention, eager launches; reported "
                          "beside the headline, never in its place")
+    ap.add_argument("--f32-activations", action="store_true",
+                    help="with --autocast: keep every activation in f32 (the same values; for comparison with the "
+                         "default bf16 storage of the activations only bf16 GEMMs read)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemm-pass", action="store_true",
                     help="skip the event-timed eager GEMM pass after the headline steps (for a kernel trace of the "

@@ -292,6 +292,10 @@ int64_t malus_std_reduce_all_sum_fwd(int64_t x);                             /* 
 int64_t malus_std_softmax_fwd(int64_t x, int64_t axis);                      /* softmax.ml:30-40 */
 int64_t malus_std_layernorm_fwd(int64_t x, int64_t axis, int64_t* var_out);  /* layernorm.ml:59-72 */
 int64_t malus_std_gelu_fwd(int64_t x);                                       /* gelu.ml:12-14 */
+/* No reference counterpart (docs/adr/0037-bf16-autocast.md:30: f32<->bf16
+ * conversion kernels join the stdlib): x converted to dtype (0 = F32,
+ * 2 = BF16; round to nearest even into bf16, exact into f32). */
+int64_t malus_std_cast(int64_t x, int32_t dtype);
 int64_t malus_std_cross_entropy_fwd(int64_t logits, int64_t targets, int64_t* probs_out); /* cross_entropy.ml:18-28 */
 int64_t malus_std_embedding_fwd(int64_t weight, int64_t indices);            /* embedding.ml:18-23 */
 int64_t malus_std_transpose_2d_fwd(int64_t x);                               /* permute.ml:21-25 */
@@ -348,6 +352,12 @@ void malus_gpt_set_fused_optimizer(void* g, int on);
 int malus_gpt_set_attention(void* gpt, int mode);
 /* 1 (default): forward fusions (attention scale+mask+softmax, residual adds in GEMM epilogues); 0: separate ops (same values and tape). */
 void malus_gpt_set_fused_forward(void* g, int on);
+/* No reference counterpart (the autocast storage policy of
+ * docs/adr/0037-bf16-autocast.md:8).  1 (default): under malus_autocast the
+ * activations read only by bf16 GEMMs (the layernorm-scale outputs, gelu(h),
+ * the GELU VJP's dh) are stored in bf16; the step's values are the same as
+ * with 0 (f32 storage), in half the bytes. */
+void malus_gpt_set_bf16_activations(void* g, int on);
 int64_t malus_gpt_forward_loss(void* g, int64_t toks, int64_t targets); /* nanogpt_modular.ml:75-91 + cross_entropy */
 int64_t malus_gpt_logits(void* g, int64_t toks);
 void malus_gpt_zero_grad(void* g);

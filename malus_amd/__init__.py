@@ -14,7 +14,7 @@ import numpy as np
 
 LIB_PATH = Path(__file__).resolve().parent / "libmalus_hip.so"
 
-F32, I32, I64 = 0, 5, 6
+F32, BF16, I32, I64 = 0, 2, 5, 6
 _NP_DTYPE = {F32: np.float32, I32: np.int32, I64: np.int64}
 _TAG_OF = {np.dtype(np.float32): F32, np.dtype(np.int32): I32, np.dtype(np.int64): I64}
 
@@ -179,6 +179,8 @@ SIGNATURES = {
     "malus_gpt_set_fused_optimizer": (None, [_vp, C.c_int]),
     "malus_gpt_set_attention": (C.c_int, [_vp, C.c_int]),
     "malus_gpt_set_fused_forward": (None, [_vp, C.c_int]),
+    "malus_std_cast": (_i64, [_i64, C.c_int32]),
+    "malus_gpt_set_bf16_activations": (None, [_vp, C.c_int]),
     "malus_tape_set_fused_vjps": (None, [C.c_int]),
     "malus_gpt_forward_loss": (_i64, [_vp, _i64, _i64]),
     "malus_gpt_logits": (_i64, [_vp, _i64]),
@@ -258,11 +260,26 @@ class Runtime:
         return tuple(buf[i] for i in range(nd))
 
     def numpy(self, h: int) -> np.ndarray:
+        """The tensor's values on the host; a bf16 tensor comes back as the
+        float32 array of its (exactly representable) values."""
         tag = self.L.malus_tensor_dtype(h)
         shp = self.shape(h)
+        if tag == BF16:
+            raw = np.empty(shp, dtype=np.uint16)
+            if raw.size:
+                self.L.malus_tensor_read(h, raw.ctypes.data_as(_vp), raw.nbytes)
+            return (raw.astype(np.uint32) << 16).view(np.float32)
         out = np.empty(shp, dtype=_NP_DTYPE[tag])
         if out.size:
             self.L.malus_tensor_read(h, out.ctypes.data_as(_vp), out.nbytes)
+        return out
+
+    def bf16(self, arr) -> int:
+        """A bf16 tensor of arr's values rounded to nearest even (the
+        stdlib's malus_std_cast of an f32 upload)."""
+        h = self.tensor(np.asarray(arr, dtype=np.float32))
+        out = self.L.malus_std_cast(h, BF16)
+        self.free(h)
         return out
 
     def free(self, *hs):

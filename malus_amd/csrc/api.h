@@ -38,12 +38,15 @@ int64_t matmul_bwd_b_impl(int64_t a, int64_t b, int64_t dout, const malus::Tenso
 int64_t layernorm_bwd_impl(int64_t y, int64_t var, int64_t dout, int64_t axis, const malus::TensorBuffer* D);
 // out = layernorm(x, axis=-1) * w in one kernel, and the VJP for x (the
 // layernorm VJP of dout * w, + D); the VJP for w is malus_std_mul_bwd_b(dout, y, w).
-int64_t ln_affine_fwd(int64_t x, int64_t w, int64_t* y_out, int64_t* var_out);
+// out_bf16: out stored in bf16 (its readers being bf16 GEMMs only).
+int64_t ln_affine_fwd(int64_t x, int64_t w, int64_t* y_out, int64_t* var_out, bool out_bf16 = false);
 int64_t ln_affine_bwd_x(int64_t y, int64_t var, int64_t w, int64_t dout, const malus::TensorBuffer* D);
 // The MLP's GELU in GEMM epilogues: h = x @ W1 with gelu(h) (returns h, 0
 // when the fused GEMM does not fit), and dh = gelu_bwd(h, dout @ W2^T) (+ D).
-int64_t matmul_gelu_fwd(int64_t x, int64_t w, int64_t* ge_out);
-int64_t gelu_matmul_bwd_h(int64_t dout, int64_t w, int64_t h, const malus::TensorBuffer* D);
+// ge_bf16 / out_bf16: gelu(h) / dh stored in bf16 (their readers being bf16
+// GEMMs only); x may be bf16.
+int64_t matmul_gelu_fwd(int64_t x, int64_t w, int64_t* ge_out, bool ge_bf16 = false);
+int64_t gelu_matmul_bwd_h(int64_t dout, int64_t w, int64_t h, const malus::TensorBuffer* D, bool out_bf16 = false);
 // Head-folded attention GEMMs (stdlib.cpp): the composed ops' values with
 // the permute copies folded into GEMM addressing.  heads_foldable: shapes
 // the folded layouts support.

@@ -154,6 +154,8 @@ void binary_scalar(int op, const float* p, const float* qdev, float qval, bool s
 void binary_general(int op, const float* p, const float* q, float* out, size_t n, const BcastDesc& d, hipStream_t s);
 void unary(int op, const float* x, float* out, size_t n, hipStream_t s);
 void unary_bwd(int op, const float* xy, const float* dout, float* out, size_t n, hipStream_t s);
+// out = x converted f32 -> bf16 (to_bf16, round to nearest even) or bf16 -> f32 (exact).
+void convert_f32_bf16(const void* x, void* out, size_t n, bool to_bf16, hipStream_t s);
 void fill(float* out, float v, size_t n, hipStream_t s);
 void fill_bytes0(void* out, size_t bytes, hipStream_t s);
 void fill_from_device(float* out, const float* v, size_t n, hipStream_t s);
@@ -259,8 +261,9 @@ void expand_axis(const float* small, float* out, size_t outer, size_t axis, size
 void softmax(const float* x, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 // With w (last axis only): also out = y * w broadcast over rows.
+// out_bf16: out (the affine output) stored in bf16, rounded to nearest even.
 void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s,
-               const float* w = nullptr, float* out = nullptr);
+               const float* w = nullptr, float* out = nullptr, bool out_bf16 = false);
 // With addend: dx = addend + VJP (gradient accumulation folded in).  With w
 // (last axis only): dout is the gradient of y * w, and dy = dout * w is formed
 // in the kernel.
@@ -306,11 +309,18 @@ struct GemmLayout { GemmMap b, r, c; };
 // which leaves every sum's value unchanged.
 // ngroup > 1 (gemm_grouped): up to 3 products with this one shape and
 // layout, group g reading ga[g] / gb[g] and writing gc[g].
+// io: operands stored in bf16 (kIo* bits; such a GEMM runs on the bf16 MFMA
+// whatever the autocast state, and its maps and ext_* count bf16 elements).
+constexpr int kIoA16 = 1;  // A stored in bf16
+constexpr int kIoB16 = 2;  // B stored in bf16
+constexpr int kIoC16 = 4;  // C written in bf16 (no addend, no K split)
+constexpr int kIoE16 = 8;  // the GELU epilogues' E (written or read) in bf16
 struct GemmLayouts {
   GemmLayout a, b, c;
   int ext_a, ext_b;
   int tri_a = 0;
   int ngroup = 1;
+  int io = 0;
   const float* ga[3] = {nullptr, nullptr, nullptr};
   const float* gb[3] = {nullptr, nullptr, nullptr};
   float* gc[3] = {nullptr, nullptr, nullptr};
@@ -324,8 +334,10 @@ inline GemmLayout dense_layout(long ld, long batch_stride) {
 // With D (C's layout and batch stride), C = D + op(A) @ op(B): the GEMM
 // result is rounded to f32 before the add, exactly as a separate add of the
 // stored product would round.
+// io: kIoA16 / kIoB16 operands stored in bf16 (LDS-DMA shapes only; fails
+// loudly otherwise).
 void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB,
-          long strideA, long strideB, long strideC, hipStream_t s, const float* D = nullptr);
+          long strideA, long strideB, long strideC, hipStream_t s, const float* D = nullptr, int io = 0);
 // gemm with every operand addressed through its layout (D shares C's).
 // Returns false, launching nothing, when the LDS-DMA kernels cannot take
 // the layouts: K % 16 != 0, a contiguous dimension whose maps are not unit
@@ -337,8 +349,10 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
 //   backward (backward = true, transB): C = gelu_bwd(E, A @ B^T) (+ D), with E
 //   the GELU's input: the GELU VJP of the product, rounded as the separate
 //   kernels round it.
+// io: kIoA16 for a bf16 A; kIoE16 for a bf16 E (the forward's gelu(C)
+// output, the backward's GELU input); kIoC16 for a bf16 C (backward, no D).
 bool gemm_gelu(const float* A, const float* B, float* C, float* E, int M, int N, int K, bool transB, bool backward,
-               hipStream_t s, const float* D = nullptr);
+               hipStream_t s, const float* D = nullptr, int io = 0);
 // Grouped GEMMs on the mapped LDS-DMA kernel (batch 1): L.ngroup products
 // of one shape and layout, operands L.ga / L.gb.
 //   accumulate = false: L.gc[g] = op(A_g) @ op(B_g), all groups in one

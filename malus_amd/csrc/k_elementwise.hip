@@ -240,6 +240,17 @@ __global__ __launch_bounds__(kBlock) void k_iota_rows(int32_t* __restrict__ out,
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = (int32_t)(i % t);
 }
 
+// f32 <-> bf16 conversions (the autocast storage type): to bf16 rounds to
+// nearest even (NaN stays NaN), to f32 is exact.
+__global__ __launch_bounds__(kBlock) void k_f32_to_bf16(const float* __restrict__ x, __bf16* __restrict__ out, size_t n) {
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = (__bf16)x[i];
+}
+__global__ __launch_bounds__(kBlock) void k_bf16_to_f32(const __bf16* __restrict__ x, float* __restrict__ out, size_t n) {
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = (float)x[i];
+}
+
 template <class F>
 void dispatch_binop(int op, F f) {
   switch (op) {
@@ -329,6 +340,13 @@ void unary_bwd(int op, const float* xy, const float* dout, float* out, size_t n,
     default: fail("malus: bad unary bwd op %d", op);
   }
   post_launch("unary_bwd");
+}
+
+void convert_f32_bf16(const void* x, void* out, size_t n, bool to_bf16, hipStream_t s) {
+  if (!n) return;
+  if (to_bf16) k_f32_to_bf16<<<ew_grid(n), kBlock, 0, s>>>(static_cast<const float*>(x), static_cast<__bf16*>(out), n);
+  else k_bf16_to_f32<<<ew_grid(n), kBlock, 0, s>>>(static_cast<const __bf16*>(x), static_cast<float*>(out), n);
+  post_launch("convert");
 }
 
 void fill(float* out, float v, size_t n, hipStream_t s) {

@@ -28,50 +28,11 @@
 #include <cstdlib>
 #include <cstring>
 
-#include "common.h"
-#include "k_gelu.h"
+#include "k_gemm_dma.h"
 
 namespace malus {
 namespace k {
 namespace {
-
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-constexpr int BK = 16;
-
-// The MFMA work of one 16-deep K step from each lane's 8 fragment values
-// (k = 8h + s for lane half h, the same k slots in A and B): eight FP32
-// 32x32x2 steps, or under autocast (BF) one 32x32x16 bf16 MFMA over the same
-// 16 k values, with both operands rounded to bf16 (round to nearest even,
-// v_cvt_pk_bf16_f32).  A bf16 product is exact in f32, so BF differs from
-// the f32 product only in the operands' rounding and the order of the f32
-// accumulation.
-template <int TM, int TN, bool BF>
-__device__ __forceinline__ void mfma_kstep(const float (&fa)[TM][8], const float (&fb)[TN][8], v16f (&acc)[TM][TN]) {
-  if constexpr (BF) {
-    bf16x8 a[TM], b[TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) a[i][e] = (__bf16)fa[i][e];
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) b[j][e] = (__bf16)fb[j][e];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-  } else {
-#pragma unroll
-    for (int st = 0; st < 8; ++st)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st], fb[j][st], acc[i][j], 0, 0, 0);
-  }
-}
 
 // One operand's tile: BX rows of its free dimension x (m for A, n for B) by
 // BK of k, staged in LDS in the operand's global orientation, so staging
@@ -244,375 +205,6 @@ __global__ __launch_bounds__(256, 2) void k_sgemm(const float* __restrict__ A, c
     }
 }
 
-// ---- LDS-DMA path --------------------------------------------------------------
-// When K is a multiple of 16 (and the x-contiguous operands' rows are
-// 16-byte multiples), operand slabs move global -> LDS with
-// buffer_load_dwordx4 ... lds: no VGPR staging and no LDS store
-// instructions.  Lane l of such a wave instruction writes LDS bytes
-// [16 l, 16 l + 16) past the wave's base (M0), so each instruction fills a
-// dense 1 KB run; the runtime picks which global 16-byte chunk each lane
-// fetches.  Layouts (dense, no padding):
-//   KC slab: [BX rows][16 k], chunk c of row r stored at chunk c ^ ((r >> 1) & 3)
-//            (the swizzle makes the two 128-bit fragment reads per lane
-//            bank-conflict-free);
-//   XC slab: [16 k][BX] (a half-wave reads 32 consecutive floats).
-// Buffer loads past the descriptor's byte count return 0; other reads past a
-// matrix edge only feed output rows/columns that are never stored.
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) const float lds_float;
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef float v2f __attribute__((ext_vector_type(2)));
-
-#if defined(__HIP_DEVICE_COMPILE__)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* p, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, (int)bytes, 0x00020000);
-}
-#endif
-
-// Element x of an index map (strides in floats); see GemmMap.  MAP = false
-// instances serve dense operands, whose maps are all x * s0.
-template <bool MAP>
-__device__ __forceinline__ int map_at(const GemmMap& f, int x) {
-  if (!MAP) return x * f.s0;
-  return f.div ? (x / f.div) * f.s1 + (x % f.div) * f.s0 : x * f.s0;
-}
-
-// Byte offset of k row/column k along a k map, advanced one 16-deep slab at
-// a time without a division (the host keeps div a multiple of 16).
-template <bool MAP>
-struct KCursor {
-  int q, r;  // k = q * div + r  (r = k for dense maps)
-  __device__ __forceinline__ void init(const GemmMap& f, int k) {
-    if (MAP && f.div) { q = k / f.div; r = k % f.div; } else { q = 0; r = k; }
-  }
-  __device__ __forceinline__ int bytes(const GemmMap& f) const { return 4 * ((MAP && f.div) ? q * f.s1 + r * f.s0 : r * f.s0); }
-  __device__ __forceinline__ void advance(const GemmMap& f) {
-    r += BK;
-    if (MAP && f.div && r == f.div) { r = 0; ++q; }
-  }
-};
-
-// s_waitcnt with vmcnt = N and no wait on the other counters (gfx9
-// encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
-template <int N>
-__device__ __forceinline__ void waitcnt_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-template <int BX, bool KC>
-struct DmaSlab {
-  static constexpr int SIZE = BX * BK;        // floats
-  static constexpr int PER_WAVE = SIZE / 1024;  // 1 KB instructions per wave (4 waves)
-  static constexpr int READS = KC ? 2 : 4;    // LDS read instructions of one 32-row fragment
-  int off[PER_WAVE];                          // byte offset of this lane's chunk at k0 = 0
-
-  // x0: first row/column of the tile.  fx maps the operand's free index x
-  // (m for A, n for B), fk its k index; the host guarantees that 4
-  // consecutive values of the contiguous index and 16 consecutive k never
-  // straddle a map's div (so one slab's k rows sit at fk(k0) + r * fk.s0).
-  template <bool MAP>
-  __device__ __forceinline__ void init(int x0, const GemmMap& fx, const GemmMap& fk, int wave, int lane) {
-#pragma unroll
-    for (int q = 0; q < PER_WAVE; ++q) {
-      const int c = q * 4 + wave;  // 256-float run of the slab
-      if (KC) {
-        const int r = c * 16 + lane / 4;
-        const int chunk = (lane & 3) ^ ((r >> 1) & 3);
-        off[q] = (map_at<MAP>(fx, x0 + r) + 4 * chunk) * 4;
-      } else {
-        const int f = c * 256 + 4 * lane;
-        off[q] = (map_at<MAP>(fx, x0 + f % BX) + (f / BX) * fk.s0) * 4;
-      }
-    }
-  }
-#if defined(__HIP_DEVICE_COMPILE__)
-  // dk: byte offset of k row/column k0 (fk(k0) * 4), uniform over the block
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, float* S, int wave, int dk) const {
-#pragma unroll
-    for (int q = 0; q < PER_WAVE; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(S + (q * 4 + wave) * 256), 16, off[q] + dk, 0, 0, 0);
-  }
-#endif
-  // The 8 MFMA-step values (k = 8h .. 8h + 7) of lane (i, h) for tile rows xw ..
-  // The reads are inline asm: the compiler treats any LDS read after an
-  // LDS-DMA load as a possible alias of it and would wait for every DMA in
-  // flight, including the slabs prefetched into other stages.  The caller
-  // waits (lgkmcnt) before the values are used.
-  __device__ __forceinline__ static void frag(const float* __restrict__ S, int xw, float f[8]) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
-    const unsigned base = (unsigned)(uintptr_t)(const lds_float*)S;
-    if (KC) {
-      const int r = xw + i, sw = (r >> 1) & 3;
-      v4f a, b;
-      asm volatile("ds_read_b128 %0, %1" : "=v"(a) : "v"(base + 4u * (r * BK + 4 * ((2 * h) ^ sw))));
-      asm volatile("ds_read_b128 %0, %1" : "=v"(b) : "v"(base + 4u * (r * BK + 4 * ((2 * h + 1) ^ sw))));
-      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-      f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-    } else {
-      // rows 8h + s, s = 0..7, are BX floats apart: pairs via the 64-dword stride form
-      static_assert(BX % 64 == 0, "x-contiguous slab rows are whole 64-dword strides");
-      constexpr int ST = BX / 64;
-      const unsigned a0 = base + 4u * (8 * h * BX + xw + i);
-      v2f p0, p1, p2, p3;
-      asm volatile("ds_read2st64_b32 %0, %1 offset1:%2" : "=v"(p0) : "v"(a0), "i"(ST));
-      asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(p1) : "v"(a0), "i"(2 * ST), "i"(3 * ST));
-      asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(p2) : "v"(a0), "i"(4 * ST), "i"(5 * ST));
-      asm volatile("ds_read2st64_b32 %0, %1 offset0:%2 offset1:%3" : "=v"(p3) : "v"(a0), "i"(6 * ST), "i"(7 * ST));
-      f[0] = p0.x; f[1] = p0.y; f[2] = p1.x; f[3] = p1.y;
-      f[4] = p2.x; f[5] = p2.y; f[6] = p3.x; f[7] = p3.y;
-    }
-#endif
-  }
-};
-
-// Same contract as k_sgemm, with each operand addressed through its
-// GemmLayout (batch, row and column maps of the stored matrix; C's also
-// addresses D).  Dense row-major operands are the maps {0, 0, ld}.  The
-// host guarantees K % 16 == 0, the map conditions above, and every byte
-// offset below 2^31; a split-K launch writes dense partials.
-// EPI: 0 plain; 1 also E = gelu(C) (the GELU after a GEMM, no D); 2 C =
-// gelu_bwd(E, product) (+ D): the GELU VJP applied to the product, with E
-// the GELU input; 3 accumulate L.ngroup products in group order,
-// C = ((D + A0 op B0) + A1 op B1) + ..., each product rounded to f32 before
-// its add (the rounding of one GEMM per group with its addend chained).
-// E shares C's layout.  Grouped launches (L.ngroup > 1, MAP only): with
-// EPI != 3, workgroup z runs group z (its own A, B, C); the batch index is 0.
-template <int TM, int TN, bool TA, bool TB, bool MAP, int EPI = 0, bool BF = false>
-__global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ A, const float* __restrict__ B,
-                                                      float* __restrict__ C, int M, int N, int K, GemmLayouts L,
-                                                      int k_chunk, int tiles_n, long split_stride,
-                                                      const float* __restrict__ D, float* __restrict__ E) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int BM = 64 * TM, BN = 64 * TN;
-  using SlabA = DmaSlab<BM, !TA>;  // A [M][K] is k-contiguous
-  using SlabB = DmaSlab<BN, TB>;   // B^T [N][K] is k-contiguous
-  // Two-stage ring of KS 16-deep slabs per stage: stage st + 1 is in
-  // flight while stage st is consumed.  Under autocast (BF) a slab's MFMA
-  // work is one bf16 instruction per accumulator, so the barrier and the
-  // fragment reads dominate; two slabs per stage halve the barriers and let
-  // the second slab's reads overlap the first slab's MFMAs (f32 K steps are
-  // long enough that one slab per stage measured faster).
-  // (Three- and four-stage rings measured no faster for either precision.)
-  constexpr bool BFS = BF && (BM + BN <= 256);
-  constexpr int NS = 2, KS = BFS ? 2 : 1;
-  constexpr int PER_SLAB = SlabA::PER_WAVE + SlabB::PER_WAVE;  // DMA instructions per slab and wave
-  // LDS reads of one slab's fragments (lgkmcnt is 4 bits)
-  constexpr int READS = TM * SlabA::READS + TN * SlabB::READS;
-  __shared__ __attribute__((aligned(1024))) float As[NS][KS][SlabA::SIZE];
-  __shared__ __attribute__((aligned(1024))) float Bs[NS][KS][SlabB::SIZE];
-
-  // Workgroups are dealt to the 8 XCDs round-robin in dispatch order (x
-  // fastest, then y), and each XCD has its own L2.  Tile ids are remapped so
-  // that every XCD gets a contiguous range of the work: consecutive tiles of
-  // one output row without a K split; with one (the weight gradients, K =
-  // tokens), a contiguous range of the split-major list, so an XCD's
-  // workgroups share one k range of both operands instead of every XCD
-  // reading the whole K range of some output columns (3x fewer HBM bytes
-  // on the C5 weight gradients).
-  const int nt = gridDim.x, ns = gridDim.y;
-  int tile, split;
-  if (ns == 1) {
-    tile = blockIdx.x;
-    if ((nt & 7) == 0) tile = (tile & 7) * (nt >> 3) + (tile >> 3);
-    split = 0;
-  } else {
-    const int total = nt * ns, lin = blockIdx.x + nt * blockIdx.y;
-    const int w = (total & 7) == 0 ? (lin & 7) * (total >> 3) + (lin >> 3) : lin;
-    split = w / nt;
-    tile = w % nt;
-  }
-  const int tm = tile / tiles_n, tn = tile % tiles_n;
-  const int m0 = tm * BM, n0 = tn * BN;
-  const bool grouped = MAP && L.ngroup > 1;
-  const int b = grouped ? 0 : blockIdx.z;
-  if (grouped && EPI != 3) {
-    A = L.ga[blockIdx.z];
-    B = L.gb[blockIdx.z];
-    C = L.gc[blockIdx.z];
-  }
-  const int ba = map_at<MAP>(L.a.b, b), bb = map_at<MAP>(L.b.b, b);
-  C += map_at<MAP>(L.c.b, b) + (long)split * split_stride;
-  if (D) D += map_at<MAP>(L.c.b, b);
-  if (EPI == 1 || EPI == 2) E += map_at<MAP>(L.c.b, b);
-  int kbeg = split * k_chunk;
-  int kend = min(K, kbeg + k_chunk);
-  if (MAP && L.tri_a) {  // op(A) row m is zero past k = m (A) or before k = m (A^T stored lower-triangular)
-    if (TA) kbeg = max(kbeg, m0);
-    else kend = min(kend, m0 + BM);
-  }
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = (wave >> 1) * 32 * TM, wn = (wave & 1) * 32 * TN;
-  const int li = lane & 31, lk = lane >> 5;
-  // stored A: [M][K] (rows m) or [K][M] (rows k); stored B: [K][N] or [N][K]
-  const GemmMap& fam = TA ? L.a.c : L.a.r;
-  const GemmMap& fak = TA ? L.a.r : L.a.c;
-  const GemmMap& fbn = TB ? L.b.r : L.b.c;
-  const GemmMap& fbk = TB ? L.b.c : L.b.r;
-  SlabA sa;
-  SlabB sb;
-  sa.template init<MAP>(m0, fam, fak, wave, lane);
-  sb.template init<MAP>(n0, fbn, fbk, wave, lane);
-
-  v16f acc[TM][TN];
-  const int nk = kend > kbeg ? (kend - kbeg) / BK : 0;
-  // acc = op(A) @ op(B) over [kbeg, kend) for operands Ap, Bp
-  auto run_k = [&](const float* Ap, const float* Bp) {
-    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(Ap + ba, (unsigned)((L.ext_a - ba) * 4));
-    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(Bp + bb, (unsigned)((L.ext_b - bb) * 4));
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = v16f{0};
-    KCursor<MAP> ka, kb;
-    ka.init(fak, kbeg);
-    kb.init(fbk, kbeg);
-    const int nst = (nk + KS - 1) / KS;
-    auto issue_stage = [&](int st, int buf) {
-#pragma unroll
-      for (int u = 0; u < KS; ++u)
-        if (st * KS + u < nk) {
-          sa.issue(ra, As[buf][u], wave, ka.bytes(fak));
-          sb.issue(rb, Bs[buf][u], wave, kb.bytes(fbk));
-          ka.advance(fak);
-          kb.advance(fbk);
-        }
-    };
-#pragma unroll
-    for (int p = 0; p < NS - 1; ++p)
-      if (p < nst) issue_stage(p, p);
-    int cur = 0;
-    for (int st = 0; st < nst; ++st) {
-      // stage st has landed once at most the NS - 2 full stages issued after
-      // it are in flight (this wave's loads complete in order); the barrier
-      // makes every wave's part visible and retires the reads of stage st - 1
-      if (st + NS - 2 < nst - 1) waitcnt_vm<(NS - 2) * KS * PER_SLAB>();
-      else waitcnt_vm<0>();
-      __builtin_amdgcn_s_barrier();
-      const bool two = KS == 2 && st * KS + 1 < nk;
-      float fa[KS][TM][8], fb[KS][TN][8];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) SlabA::frag(As[cur][0], wm + 32 * i, fa[0][i]);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][0], wn + 32 * j, fb[0][j]);
-      __builtin_amdgcn_sched_barrier(0);
-      // stage st - 1 (= st + NS - 1 mod NS) was last read before the barrier
-      const int nxt = cur == 0 ? NS - 1 : cur - 1;
-      if (st + NS - 1 < nst) issue_stage(st + NS - 1, nxt);
-      if constexpr (KS == 2) {
-        // The second slab's fragments are read on every path, also in a last
-        // stage that holds one slab (an odd slab count; the values then go
-        // unused), so the waits below do not depend on a branch.
-#pragma unroll
-        for (int i = 0; i < TM; ++i) SlabA::frag(As[cur][KS - 1], wm + 32 * i, fa[KS - 1][i]);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][KS - 1], wn + 32 * j, fb[KS - 1][j]);
-        // LDS reads complete in order: the first slab's are done when at
-        // most the second slab's READS are outstanding
-        if constexpr (READS <= 15) asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(READS) : "memory");
-        else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      } else {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the fragment reads above
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      // a wave with MFMAs to issue goes ahead of the CU's other waves (measured
-      // 1 % on the C5 step; raising it from the barrier on instead lost 2 %)
-      __builtin_amdgcn_s_setprio(1);
-      mfma_kstep<TM, TN, BF>(fa[0], fb[0], acc);
-      __builtin_amdgcn_s_setprio(0);
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (KS == 2) {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        if (two) {
-          __builtin_amdgcn_s_setprio(1);
-          mfma_kstep<TM, TN, BF>(fa[KS - 1], fb[KS - 1], acc);
-          __builtin_amdgcn_s_setprio(0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      cur = cur == NS - 1 ? 0 : cur + 1;
-    }
-    __syncthreads();  // every wave is done with the stages before they are reused
-  };
-
-  // Element (i, j, r) of the wave's accumulators is C at offset
-  // cn(i, j) + dm(r) * row stride; C rows come in aligned 32-row groups (the
-  // host keeps the row map's div a multiple of 32), so one map evaluation
-  // per group and per column.
-  auto for_each = [&](auto&& f) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int rbase = map_at<MAP>(L.c.r, m0 + wm + 32 * i);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn + 32 * j + li;
-        const int cn = map_at<MAP>(L.c.c, n) + rbase;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int dm = 8 * (r >> 2) + 4 * lk + (r & 3);
-          const int m = m0 + wm + 32 * i + dm;
-          f(i, j, r, n < N && m < M, cn + dm * L.c.r.s0);
-        }
-      }
-    }
-  };
-
-  // The epilogue's operand read (the addend D, or E for the GELU VJP) is
-  // issued before the K loop, so its latency hides under the MFMAs instead
-  // of stalling every workgroup's epilogue at once.  Small wave tiles only:
-  // it holds another TM * TN * 16 registers, so only instances that read
-  // one (the dense GEMMs that take an addend, the GELU VJP, the grouped
-  // accumulation) carry it.  Without it (4 -> 6 workgroups per CU on the
-  // 128x64 tiles) the C5 step measured 0.7 % slower for the GELU VJP alone
-  // and 1.7 % slower for the dense forms.
-  constexpr bool PF = TM * TN <= 2 && ((EPI == 0 && !MAP) || EPI == 2 || EPI == 3);
-  const float* pre_src = EPI == 2 ? E : D;
-  v16f pre[PF ? TM : 1][PF ? TN : 1];
-  if (PF && pre_src)
-    for_each([&](int i, int j, int r, bool live, int o) {
-      if (PF) pre[i][j][r] = live ? pre_src[o] : 0.0f;
-    });
-  auto pre_at = [&](int i, int j, int r, int o) -> float {
-    if constexpr (PF) return pre[i][j][r];
-    else return pre_src[o];
-  };
-
-  if constexpr (EPI == 3) {
-    v16f tot[TM][TN];
-    for (int g = 0; g < L.ngroup; ++g) {
-      run_k(L.ga[g], L.gb[g]);
-      if (g == 0) {
-        for_each([&](int i, int j, int r, bool live, int o) {
-          tot[i][j][r] = D && live ? pre_at(i, j, r, o) + acc[i][j][r] : acc[i][j][r];
-        });
-      } else {
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) tot[i][j][r] = tot[i][j][r] + acc[i][j][r];
-      }
-    }
-    for_each([&](int i, int j, int r, bool live, int o) {
-      if (live) C[o] = tot[i][j][r];
-    });
-  } else {
-    run_k(A, B);
-    for_each([&](int i, int j, int r, bool live, int o) {
-      if (live) {
-        float v = acc[i][j][r];
-        if (EPI == 2) v = gelu_bwd(pre_at(i, j, r, o), v);
-        C[o] = D ? (EPI == 2 ? D[o] : pre_at(i, j, r, o)) + v : v;
-        if (EPI == 1) E[o] = gelu_fwd(v);
-      }
-    });
-  }
-#endif
-}
 
 // C[i] = sum over splits s (in order) of partial[s * mn + i], then + D[i]
 // when an addend is given (the same rounding as adding to the stored sum).
@@ -666,10 +258,13 @@ struct TileCfg { int tm, tn; };
 constexpr TileCfg kTiles[] = {{2, 3}, {2, 2}, {2, 1}, {1, 2}, {1, 1}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-// Variant code: bit 8 = bf16 MFMA (autocast), bit 7 = grouped accumulation,
-// bit 6 = GELU epilogues, bit 5 = mapped operands, bit 4 = LDS-DMA path,
-// bits 3..0 = transA, transB, vecA, vecB.
+// Variant code: bits 12..9 = GemmLayouts::io (bf16-stored operands, the
+// instances of k_gemm_io.hip), bit 8 = bf16 MFMA (autocast), bit 7 =
+// grouped accumulation, bit 6 = GELU epilogues, bit 5 = mapped operands,
+// bit 4 = LDS-DMA path, bits 3..0 = transA, transB, vecA, vecB.
 constexpr int kVarBf16 = 256;
+constexpr int kVarIoShift = 9;
+constexpr int kVarCount = 16 << kVarIoShift;
 inline int variant(bool ta, bool tb, bool va, bool vb, bool dma) {
   return (dma << 4) | (ta << 3) | (tb << 2) | (va << 1) | (int)vb;
 }
@@ -715,13 +310,14 @@ const void* kernel_for_prec(int ti, int v) {
 }
 
 const void* kernel_for(int ti, int v) {
+  if (v >> kVarIoShift) return gemm_io_kernel(ti, v);
   return (v & kVarBf16) ? kernel_for_prec<true>(ti, v) : kernel_for_prec<false>(ti, v);
 }
 
 // Co-resident workgroups per CU of each kernel variant (VGPR and LDS
 // limited), from the runtime's occupancy calculator; cached per variant.
 int occupancy(int ti, int v) {
-  static int cache[kNumTiles][512];
+  static int cache[kNumTiles][kVarCount];
   int& o = cache[ti][v];
   if (o == 0) {
     int n = 0;
@@ -760,7 +356,8 @@ bool g_allow_dma = true;   // LDS-DMA path where the shape allows it
 // GEMMs, K = tokens) split K so the grid fills the chip's workgroup slots.
 // tri: A lower-triangular (GemmLayouts::tri_a); a tile row then runs on
 // average (n + 1) / (2 n) of K for n tile rows, which favours short tiles.
-Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false, int only_tile = -1) {
+// bf: the launch runs on the bf16 MFMA (autocast, or bf16-stored operands).
+Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false, int only_tile = -1, bool bf = false) {
   if (g_forced_tile == -2) {  // MALUS_GEMM_TILE=TMxTN pins a tile (tuning sweeps)
     g_forced_tile = -1;
     if (const char* e = getenv("MALUS_GEMM_TILE"))
@@ -781,7 +378,7 @@ Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false, int only
   // time, and the 128x192 tile (more MFMA work per staged byte) with the
   // cost model's split measured 10-20 % faster on the same shapes.
   const bool wgrad = (v & 16) && (v & 8) && batch == 1 && K >= 4096 && g_forced_tile < 0 && g_split_target == 0;
-  const bool wgrad_bf = wgrad && g_autocast;
+  const bool wgrad_bf = wgrad && (g_autocast || bf);
   if (wgrad_bf) only_tile = 0;  // kTiles[0] = 128x192
   for (int ti = 0; ti < kNumTiles; ++ti) {
     if (g_forced_tile >= 0 && ti != g_forced_tile) continue;
@@ -861,13 +458,21 @@ double launch_dma(const float* A, const float* B, float* C, int batch, int M, in
                   GemmLayouts L, hipStream_t s, const float* D, bool split_ok, bool mapped, float* E = nullptr,
                   int epi = 0) {
   // mapped operands run the MAP instance on the dense shape's plan, so a
-  // mapped GEMM splits K exactly like its dense twin
+  // mapped GEMM splits K exactly like its dense twin; bf16-stored operands
+  // take the plan of the autocast GEMM on f32 copies of them, so the sums
+  // run in the same order
   const int v = variant(transA, transB, false, false, true);
+  const bool bf = g_autocast || L.io;
+  const int vb = (epi ? v | 64 : mapped ? v | 32 : v) | (bf ? kVarBf16 : 0) | (L.io << kVarIoShift);
+  const void* fn = kernel_for(0, vb);
+  if (!fn) fail("malus: gemm: no kernel for epilogue %d with transA=%d transB=%d and bf16 storage mask %d", epi, transA,
+                transB, L.io);
+  if ((L.io & kIoC16) && D) fail("malus: gemm: a bf16 output takes no addend");
   // Under autocast the GELU GEMM (h = x W1, K = 384, a 3072-workgroup grid
   // at 128x64) measured 20 % faster on 128x192 tiles.
-  Plan p = plan_gemm(batch, M, N, K, v, mapped && L.tri_a, g_autocast && epi == 1 ? 0 : -1);
+  Plan p = plan_gemm(batch, M, N, K, v, mapped && L.tri_a, bf && epi == 1 ? 0 : -1, bf);
   const char* tag = mapped ? " mapped" : "";
-  if ((!split_ok || epi) && p.nsplit > 1) {
+  if ((!split_ok || epi || (L.io & kIoC16)) && p.nsplit > 1) {
     p.nsplit = 1;
     p.k_chunk = K;
   }
@@ -885,9 +490,7 @@ double launch_dma(const float* A, const float* B, float* C, int batch, int M, in
   long split_stride = nsplit > 1 ? (long)mn : 0;
   const float* Dk = nsplit > 1 ? nullptr : D;  // split-K applies the addend in the reduction
   void* args[] = {&A, &B, &dst, &M, &N, &K, &L, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk, &E};
-  const int vb = (epi ? v | 64 : mapped ? v | 32 : v) | (g_autocast ? kVarBf16 : 0);
-  const void* fn = kernel_for(p.ti, vb);
-  if (!fn) fail("malus: gemm: no kernel for epilogue %d with transA=%d transB=%d", epi, transA, transB);
+  fn = kernel_for(p.ti, vb);
   MALUS_HIP(hipLaunchKernel(fn, dim3((unsigned)tiles, (unsigned)nsplit, (unsigned)batch), dim3(256), args, 0, s));
   if (nsplit > 1) split_reduce(dst, C, mn, nsplit, D, s, bucket);
   if (!(mapped && L.tri_a)) return 2.0 * batch * (double)M * N * K;
@@ -900,7 +503,7 @@ double launch_dma(const float* A, const float* B, float* C, int batch, int M, in
   return 2.0 * batch * (double)N * rk;
 }
 
-bool map_contig4(const GemmMap& f) { return f.s0 == 1 && (f.div == 0 || f.div % 4 == 0); }
+bool map_contig(const GemmMap& f, int run) { return f.s0 == 1 && (f.div == 0 || f.div % run == 0); }
 bool map_k16(const GemmMap& f) { return f.div == 0 || f.div % 16 == 0; }
 // largest offset the map reaches for x in [0, n)
 long map_max(const GemmMap& f, long n) {
@@ -913,7 +516,7 @@ long map_max(const GemmMap& f, long n) {
 }  // namespace
 
 void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int K, bool transA, bool transB, long sA,
-          long sB, long sC, hipStream_t s, const float* D) {
+          long sB, long sC, hipStream_t s, const float* D, int io) {
   if (batch <= 0 || M <= 0 || N <= 0) return;
   if (K <= 0) {  // empty inner dimension: all-zero result (metal.rs:837-839 falls to the CPU loop)
     fill(C, 0.0f, (size_t)batch * M * N, s);
@@ -923,14 +526,21 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
   const long lda = transA ? M : K, ldb = transB ? K : N;
   const long ext_a = (long)(batch - 1) * sA + (long)M * K, ext_b = (long)(batch - 1) * sB + (long)K * N;
   // LDS-DMA path: whole 16-deep K slabs, 16-byte rows, 32-bit byte offsets
-  const bool dma = K % 16 == 0 && (transA ? M % 4 == 0 : true) && (transB ? true : N % 4 == 0) &&
+  // (a bf16 operand's x-contiguous rows: runs of 8 elements)
+  const int xa = io & kIoA16 ? 8 : 4, xb = io & kIoB16 ? 8 : 4;
+  const bool dma = K % 16 == 0 && (transA ? M % xa == 0 : true) && (transB ? true : N % xb == 0) &&
                    (size_t)ext_a * 4 < (1ull << 31) && (size_t)ext_b * 4 < (1ull << 31) &&
                    ((size_t)(batch - 1) * sC + (size_t)M * N) * 4 < (1ull << 31) && g_allow_dma;
+  if (io & ~(kIoA16 | kIoB16)) fail("malus: gemm: bf16 storage mask %d is not an operand mask", io);
   if (dma) {
     GemmLayouts L{dense_layout(lda, sA), dense_layout(ldb, sB), dense_layout(N, sC), (int)ext_a, (int)ext_b};
+    L.io = io;
     launch_dma(A, B, C, batch, M, N, K, transA, transB, L, s, D, true, false);
     return;
   }
+  if (io)
+    fail("malus: gemm: bf16-stored operands need the LDS-DMA kernels (%dx%dx%d, transA=%d transB=%d: K %% 16, "
+         "the contiguous dimension of a bf16 operand %% 8)", M, N, K, transA, transB);
   // float4 staging needs the contiguous dim of each operand to be a multiple of 4
   const bool va = transA ? (M % 4 == 0) : (K % 4 == 0);
   const bool vb = transB ? (K % 4 == 0) : (N % 4 == 0);
@@ -954,7 +564,7 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
 }
 
 bool gemm_gelu(const float* A, const float* B, float* C, float* E, int M, int N, int K, bool transB, bool backward,
-               hipStream_t s, const float* D) {
+               hipStream_t s, const float* D, int io) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 || N % 4 || !g_allow_dma || (!backward && (D || transB)) ||
       (backward && !transB))
     return false;
@@ -962,6 +572,7 @@ bool gemm_gelu(const float* A, const float* B, float* C, float* E, int M, int N,
   if ((size_t)ext_a * 4 >= (1ull << 31) || (size_t)ext_b * 4 >= (1ull << 31) || (size_t)M * N * 4 >= (1ull << 31))
     return false;
   GemmLayouts L{dense_layout(K, 0), dense_layout(transB ? K : N, 0), dense_layout(N, 0), (int)ext_a, (int)ext_b};
+  L.io = io;
   launch_dma(A, B, C, 1, M, N, K, false, transB, L, s, D, false, false, E, backward ? 2 : 1);
   return true;
 }
@@ -976,7 +587,8 @@ bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayou
   if (accumulate && !(!transA && transB)) return false;  // built for the projections' dA (NT) only
   GemmLayouts L = Lin;
   const int v = variant(transA, transB, false, false, true);
-  Plan p = plan_gemm(1, M, N, K, v);
+  const bool bf = g_autocast || L.io;
+  Plan p = plan_gemm(1, M, N, K, v, false, -1, bf);
   const bool c_dense = L.c.r.div == 0 && L.c.c.div == 0 && L.c.c.s0 == 1 && L.c.r.s0 == N;
   if (accumulate || !c_dense) {
     p.nsplit = 1;
@@ -1019,8 +631,8 @@ bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayou
   float* Cp = accumulate ? C : L.gc[0];
   const float *A0 = L.ga[0], *B0 = L.gb[0];
   void* args[] = {&A0, &B0, &Cp, &M, &N, &K, &L, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk, &E};
-  const void* fn = kernel_for(p.ti, (accumulate ? v | 128 : v | 32) | (g_autocast ? kVarBf16 : 0));
-  if (!fn) fail("malus: gemm_grouped: no kernel for transA=%d transB=%d", transA, transB);
+  const void* fn = kernel_for(p.ti, (accumulate ? v | 128 : v | 32) | (bf ? kVarBf16 : 0) | (L.io << kVarIoShift));
+  if (!fn) fail("malus: gemm_grouped: no kernel for transA=%d transB=%d and bf16 storage mask %d", transA, transB, L.io);
   MALUS_HIP(hipLaunchKernel(fn, dim3((unsigned)tiles, (unsigned)nsplit, accumulate ? 1u : (unsigned)L.ngroup), dim3(256),
                             args, 0, s));
   if (nsplit > 1) {
@@ -1059,12 +671,15 @@ bool gemm_mapped(const float* A, const float* B, float* C, int batch, int M, int
 namespace {
 bool mapped_ok(int batch, int M, int N, int K, bool transA, bool transB, const GemmLayouts& L) {
   if (batch <= 0 || M <= 0 || N <= 0 || K <= 0 || batch > 65535 || K % 16 || !g_allow_dma) return false;
-  // contiguous dimension of each stored operand: runs of 4 floats
+  // contiguous dimension of each stored operand: runs of 4 floats (16
+  // bytes), of 8 elements for a bf16 operand
   const GemmMap& a_contig = L.a.c;  // A [M][K]: k;  A^T [K][M]: m
   const GemmMap& b_contig = L.b.c;  // B [K][N]: n;  B^T [N][K]: k
-  if (!map_contig4(a_contig) || !map_contig4(b_contig)) return false;
-  if (transA ? M % 4 : 0) return false;
-  if (transB ? 0 : N % 4) return false;
+  const int ra = L.io & kIoA16 ? 8 : 4, rb = L.io & kIoB16 ? 8 : 4;
+  if (!map_contig(a_contig, ra) || !map_contig(b_contig, rb)) return false;
+  if (transA ? M % ra : 0) return false;
+  if (transB ? 0 : N % rb) return false;
+  if (L.io & kIoC16) return false;  // mapped outputs stay f32
   const GemmMap& fak = transA ? L.a.r : L.a.c;
   const GemmMap& fbk = transB ? L.b.c : L.b.r;
   if (!map_k16(fak) || !map_k16(fbk)) return false;

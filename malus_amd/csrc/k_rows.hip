@@ -250,7 +250,8 @@ __device__ __forceinline__ float hsum(float v) {
 }
 constexpr int kHalfRowsPerBlock = 8;
 
-template <int NV>
+// OB: out stored in bf16 (each product rounded to nearest even).
+template <int NV, bool OB = false>
 __global__ __launch_bounds__(256) void k_layernorm_rows32(const float* __restrict__ x, float* __restrict__ y,
                                                           float* __restrict__ var, size_t rows, float eps,
                                                           const float* __restrict__ w, float* __restrict__ out) {
@@ -284,11 +285,17 @@ __global__ __launch_bounds__(256) void k_layernorm_rows32(const float* __restric
   if (hl == 0 && var) var[row] = va;
   if (w) {
     const float4* wr = reinterpret_cast<const float4*>(w);
-    float4* orow = reinterpret_cast<float4*>(out + row * axis);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const float4 g = wr[hl + 32 * j];
-      orow[hl + 32 * j] = make_float4(v[4 * j] * g.x, v[4 * j + 1] * g.y, v[4 * j + 2] * g.z, v[4 * j + 3] * g.w);
+      const float4 o = make_float4(v[4 * j] * g.x, v[4 * j + 1] * g.y, v[4 * j + 2] * g.z, v[4 * j + 3] * g.w);
+      if constexpr (OB) {
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(out) + row * axis)[hl + 32 * j] =
+            bf16x4{(__bf16)o.x, (__bf16)o.y, (__bf16)o.z, (__bf16)o.w};
+      } else {
+        reinterpret_cast<float4*>(out + row * axis)[hl + 32 * j] = o;
+      }
     }
   }
 }
@@ -686,10 +693,20 @@ void softmax_bwd(const float* y, const float* dout, float* out, size_t outer, si
 }
 
 void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, size_t inner, float eps, hipStream_t s,
-               const float* w, float* out) {
+               const float* w, float* out, bool out_bf16) {
   if (!outer || !axis || !inner) return;
   const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  if (inner == 1 && axis % 128 == 0 && axis <= 512 && a16(x) && a16(y) && a16(w) && a16(out)) {
+  const bool rows32 = inner == 1 && axis % 128 == 0 && axis <= 512 && a16(x) && a16(y) && a16(w) && a16(out);
+  if (out_bf16) {
+    if (!rows32 || !w) fail("malus: layernorm: a bf16 affine output needs the last axis, a multiple of 128 up to 512");
+    const unsigned grid = (unsigned)((outer + kHalfRowsPerBlock - 1) / kHalfRowsPerBlock);
+    switch (axis / 128) {
+      case 1: k_layernorm_rows32<1, true><<<grid, 256, 0, s>>>(x, y, var, outer, eps, w, out); break;
+      case 2: k_layernorm_rows32<2, true><<<grid, 256, 0, s>>>(x, y, var, outer, eps, w, out); break;
+      case 3: k_layernorm_rows32<3, true><<<grid, 256, 0, s>>>(x, y, var, outer, eps, w, out); break;
+      default: k_layernorm_rows32<4, true><<<grid, 256, 0, s>>>(x, y, var, outer, eps, w, out); break;
+    }
+  } else if (rows32) {
     const unsigned grid = (unsigned)((outer + kHalfRowsPerBlock - 1) / kHalfRowsPerBlock);
     switch (axis / 128) {
       case 1: k_layernorm_rows32<1><<<grid, 256, 0, s>>>(x, y, var, outer, eps, w, out); break;

@@ -90,13 +90,14 @@ int64_t layernorm(int64_t x) {
 // layernorm(x, axis=1) * w: one kernel and one LayerNormScale tape node when
 // fused (the same values; y and the variance are saved for the VJPs), else
 // the reference's LAYERNORM and MUL records.  *y gets the normalized rows.
-int64_t ln_scale(bool fused, int64_t x, int64_t w, int64_t* y) {
+// bf16_out (fused only): the product is stored in bf16 for bf16 GEMMs.
+int64_t ln_scale(bool fused, int64_t x, int64_t w, int64_t* y, bool bf16_out = false) {
   if (!fused) {
     *y = layernorm(x);
     return binop(OP_MUL, *y, w);
   }
   int64_t var;
-  int64_t out = ln_affine_fwd(x, w, y, &var);
+  int64_t out = ln_affine_fwd(x, w, y, &var, bf16_out);
   tape_record_fused(TAG_LN_SCALE, {x, w, *y, var}, out, {});
   tensor_release(var);  // the tape holds it
   return out;
@@ -129,6 +130,9 @@ struct Gpt {
   bool inplace_opt = false;
   const float* bc_dev = nullptr;
   int attn_mode = ATTN_AUTO;
+  // Under autocast, the activations whose only readers are bf16 GEMMs are
+  // stored in bf16 (see block_forward).
+  bool bf16_act = true;
   std::vector<int64_t> p, m, v;  // block l params at 8l..8l+7, then wte, wpe, ln_f, lm_head
   int64_t pos = 0;               // [B*T] i32 position ids
   int64_t attn_scale = 0;        // [1,1] 1/sqrt(hs) of the fused attention (built on first use)
@@ -140,13 +144,21 @@ struct Gpt {
 int64_t block_forward(Gpt& g, int l, int64_t x) {
   const size_t B = g.B, Tn = g.Tn, C = g.C, H = g.H, hs = C / H, N = B * Tn;
   int64_t* P = &g.p[8 * l];
-  // nanogpt_modular.ml:47-68
-  int64_t y1;
-  int64_t xn1 = ln_scale(g.fused_fwd, x, P[0], &y1);
   // Fused heads: the head fold / unfold permutes and K's transpose are
   // folded into GEMM addressing (one tape node per projection, per score
   // product and per attention output; the same values as the composed ops).
   const bool fused_heads = g.fused_fwd && heads_foldable(B, Tn, H, hs);
+  // The autocast storage policy (docs/adr/0037-bf16-autocast.md:8: matmuls
+  // and forward elementwise kernels in bf16): the two layernorm-scale
+  // outputs, gelu(h) and the GELU VJP's dh are read only by bf16 GEMMs, which
+  // round their operands to bf16 anyway, so they are stored in bf16 by the
+  // kernels that produce them; every value of the step is unchanged, and the
+  // GEMMs that read them move half the bytes.  h (the GELU VJP's input),
+  // the residual stream, parameters, gradients and optimizer state stay f32.
+  const bool bf_act = g.bf16_act && k::autocast_on() && fused_heads && C % 128 == 0 && C <= 512 && N % 8 == 0;
+  // nanogpt_modular.ml:47-68
+  int64_t y1;
+  int64_t xn1 = ln_scale(g.fused_fwd, x, P[0], &y1, bf_act);
   auto head_fold = [&](int64_t w) {
     if (fused_heads) {
       int64_t Qh = head_proj_fwd(xn1, w, B, Tn, H);
@@ -272,9 +284,9 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
     x2 = binop(OP_ADD, x, proj);
   }
   int64_t y2;
-  int64_t xn2 = ln_scale(g.fused_fwd, x2, P[5], &y2);
+  int64_t xn2 = ln_scale(g.fused_fwd, x2, P[5], &y2, bf_act);
   int64_t ge = 0, mo, x3;
-  int64_t h = g.fused_fwd ? matmul_gelu_fwd(xn2, P[6], &ge) : 0;
+  int64_t h = g.fused_fwd ? matmul_gelu_fwd(xn2, P[6], &ge, bf_act) : 0;
   if (h) {
     // MLP: gelu in the first GEMM's epilogue; out = x2 + ge @ W2 with the add
     // in the second's.  Tape: MATMUL(xn2, W1 -> h), GeluMatmul(h, W2; ge ->
@@ -518,6 +530,7 @@ int64_t malus_gpt_moment(void* gp, int i, int which) {
 // kernel, and the residual adds folded into the producing GEMM's epilogue;
 // 0: every op separately.  Values and tape records are the same either way.
 void malus_gpt_set_fused_forward(void* gp, int on) { static_cast<Gpt*>(gp)->fused_fwd = on != 0; }
+void malus_gpt_set_bf16_activations(void* gp, int on) { static_cast<Gpt*>(gp)->bf16_act = on != 0; }
 
 void malus_gpt_set_fused_optimizer(void* gp, int on) { static_cast<Gpt*>(gp)->fused_opt = on != 0; }
 // 0: automatic, 1: flash attention, 2: the row-register fused kernel, 3: composed ops

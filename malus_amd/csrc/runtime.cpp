@@ -332,8 +332,12 @@ void pool_release_graph(int graph) {
 // ============================================================================
 // tensors
 // ============================================================================
+// The reference's dtypes (metal.rs:368-377), plus bf16 for the autocast
+// paths (docs/adr/0037-bf16-autocast.md consequences: the Bf16 tag stops
+// panicking on the autocast-covered paths only; tensor_alloc_gpu keeps the
+// reference's check).
 TensorBuffer* alloc_tensor(int32_t dtype, const size_t* shape, int ndim) {
-  if (dtype != F32 && dtype != I32 && dtype != I64)
+  if (dtype != F32 && dtype != I32 && dtype != I64 && dtype != BF16)
     fail("malus: unsupported dtype tag %d; supported: f32, i32, i64", dtype);
   if (ndim < 0 || ndim > kMaxRank) fail("malus: tensor rank %d exceeds %d", ndim, kMaxRank);
   auto* t = new TensorBuffer();
@@ -587,6 +591,8 @@ void malus_init(void) { API_TRY ensure_init(); API_CATCH() }
 
 int64_t tensor_alloc_gpu(int32_t dtype, const size_t* shape, size_t ndim, const void* data) {
   API_TRY
+  if (dtype != F32 && dtype != I32 && dtype != I64)
+    fail("malus: unsupported dtype tag %d; supported: f32, i32, i64", dtype);
   TensorBuffer* t = alloc_tensor(dtype, shape, (int)ndim);
   if (data && t->len) {
     upload(t->data(), data, t->bytes());

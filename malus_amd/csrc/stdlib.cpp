@@ -38,6 +38,15 @@ void need_f32(const TensorBuffer* t, const char* what) {
   if (t->dtype != F32) fail("malus: %s expects a Tensor<f32>, got dtype tag %d", what, t->dtype);
 }
 
+// GEMM operands may be f32 or bf16 (the autocast activations); the mask of
+// bf16-stored operands for GemmLayouts::io.
+int gemm_io(const TensorBuffer* a, const TensorBuffer* b, const char* what) {
+  for (const TensorBuffer* t : {a, b})
+    if (t->dtype != F32 && t->dtype != BF16)
+      fail("malus: %s expects Tensor<f32> or Tensor<bf16> operands, got dtype tag %d", what, t->dtype);
+  return (a->dtype == BF16 ? k::kIoA16 : 0) | (b->dtype == BF16 ? k::kIoB16 : 0);
+}
+
 int64_t done(TensorBuffer* t, const char* name) {
   t->write_seq = enqueue_mark(name);
   return H(t);
@@ -196,12 +205,13 @@ TensorBuffer* as_i32_indices(TensorBuffer* idx, bool* owned) {
 
 int64_t gemm_out(TensorBuffer* a, TensorBuffer* b, bool ta, bool tb, int batch, int M, int N, int K, long sA, long sB,
                  const size_t* oshape, int ond, const TensorBuffer* addend = nullptr) {
+  const int io = gemm_io(a, b, "matmul");
   TensorBuffer* c = alloc_tensor(F32, oshape, ond);
   if (addend && (addend->dtype != F32 || addend->len != c->len))
     fail("malus: matmul accumulate: addend %s does not match the product %s", shape_str(addend).c_str(), shape_str(c).c_str());
   KTimer* kt = ktimer_begin("gemm");
   k::gemm(a->f32(), b->f32(), c->f32(), batch, M, N, K, ta, tb, sA, sB, (long)M * N, stream(),
-          addend ? addend->f32() : nullptr);
+          addend ? addend->f32() : nullptr, io);
   ktimer_end(kt, 2.0 * batch * (double)M * N * K);
   return done(c, "matmul");
 }
@@ -257,6 +267,22 @@ int64_t malus_std_unary(int32_t op, int64_t x) {
   API_CATCH(0)
 }
 int64_t malus_std_gelu_fwd(int64_t x) { return malus_std_unary(k::GELU, x); }
+
+// The stdlib's f32 <-> bf16 conversion (docs/adr/0037-bf16-autocast.md:30,
+// "conversion kernels (f32<->bf16) join the stdlib"): a new tensor of the
+// same shape in `dtype` (F32 or BF16); to bf16 rounds to nearest even, to
+// f32 is exact; a same-dtype cast copies.
+int64_t malus_std_cast(int64_t x, int32_t dtype) {
+  API_TRY
+  TensorBuffer* t = T(x);
+  if ((t->dtype != F32 && t->dtype != BF16) || (dtype != F32 && dtype != BF16))
+    fail("malus: cast supports f32 and bf16 only (dtype tags %d -> %d)", t->dtype, dtype);
+  TensorBuffer* out = alloc_tensor(dtype, t->shape, t->ndim);
+  if (t->dtype == dtype) k::copy(t->data(), out->data(), t->bytes(), stream());
+  else k::convert_f32_bf16(t->data(), out->data(), t->len, dtype == BF16, stream());
+  return done(out, "cast");
+  API_CATCH(0)
+}
 
 // ---- axis reductions (reduce_{sum,mean,max,var}.ml) ------------------------
 int64_t malus_std_reduce_fwd(int32_t op, int64_t x, int64_t axis, int64_t keepdim) {
@@ -848,8 +874,7 @@ int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout) {
 // is how a gradient accumulation or residual add folds into the GEMM.
 int64_t matmul_impl(int64_t ha, int64_t hb, const TensorBuffer* D) {
   TensorBuffer *a = T(ha), *b = T(hb);
-  need_f32(a, "matmul");
-  need_f32(b, "matmul");
+  gemm_io(a, b, "matmul");
   if (a->ndim == 2 && b->ndim == 2) {
     size_t m = a->shape[0], k = a->shape[1], k2 = b->shape[0], n = b->shape[1];
     if (k != k2)
@@ -898,7 +923,9 @@ int64_t layernorm_bwd_impl(int64_t y, int64_t var, int64_t dout, int64_t axis, c
 
 // out = layernorm(x, axis=-1) * w (nanogpt_modular.ml:47 and :62) from one
 // kernel; *y_out gets the normalized rows, *var_out the keepdim variance.
-int64_t ln_affine_fwd(int64_t hx, int64_t hw, int64_t* y_out, int64_t* var_out) {
+// out_bf16: out is stored in bf16 (rounded to nearest even), for a caller
+// whose only readers of it are bf16 GEMMs.
+int64_t ln_affine_fwd(int64_t hx, int64_t hw, int64_t* y_out, int64_t* var_out, bool out_bf16) {
   TensorBuffer *t = T(hx), *w = T(hw);
   need_f32(t, "layernorm");
   const size_t a = t->shape[t->ndim - 1];
@@ -906,11 +933,11 @@ int64_t ln_affine_fwd(int64_t hx, int64_t hw, int64_t* y_out, int64_t* var_out) 
     fail("malus: fused layernorm scale: weight %s does not match the last axis of %s", shape_str(w).c_str(),
          shape_str(t).c_str());
   TensorBuffer* y = alloc_like(t);
-  TensorBuffer* out = alloc_like(t);
+  TensorBuffer* out = alloc_tensor(out_bf16 ? BF16 : F32, t->shape, t->ndim);
   size_t vsh[kMaxRank];
   for (int i = 0; i < t->ndim; ++i) vsh[i] = i == t->ndim - 1 ? 1 : t->shape[i];
   TensorBuffer* var = alloc_tensor(F32, vsh, t->ndim);
-  k::layernorm(t->f32(), y->f32(), var->f32(), t->len / a, a, 1, 1e-5f, stream(), w->f32(), out->f32());
+  k::layernorm(t->f32(), y->f32(), var->f32(), t->len / a, a, 1, 1e-5f, stream(), w->f32(), out->f32(), out_bf16);
   uint64_t seq = enqueue_mark("layernorm_affine");
   y->write_seq = var->write_seq = out->write_seq = seq;
   *y_out = H(y);
@@ -958,16 +985,19 @@ int64_t ln_affine_bwd_xw(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const
 
 // h = x @ W1 and ge = gelu(h) from one GEMM (nanogpt_modular.ml:63);
 // returns h, *ge_out gets gelu(h).  0 when the shape does not fit the fused
-// epilogue (nothing launched).
-int64_t matmul_gelu_fwd(int64_t hx, int64_t hw, int64_t* ge_out) {
+// epilogue (nothing launched).  x may be bf16; ge_bf16 stores ge in bf16
+// (for a caller whose readers of ge are bf16 GEMMs); h stays f32.
+int64_t matmul_gelu_fwd(int64_t hx, int64_t hw, int64_t* ge_out, bool ge_bf16) {
   TensorBuffer *x = T(hx), *w = T(hw);
   if (x->ndim != 2 || w->ndim != 2 || x->shape[1] != w->shape[0]) return 0;
+  const int io = gemm_io(x, w, "matmul") | (ge_bf16 ? k::kIoE16 : 0);
   const size_t M = x->shape[0], K = x->shape[1], N = w->shape[1];
   const size_t sh[2] = {M, N};
   TensorBuffer* h = alloc_tensor(F32, sh, 2);
-  TensorBuffer* ge = alloc_tensor(F32, sh, 2);
+  TensorBuffer* ge = alloc_tensor(ge_bf16 ? BF16 : F32, sh, 2);
   KTimer* kt = ktimer_begin("gemm");
-  if (!k::gemm_gelu(x->f32(), w->f32(), h->f32(), ge->f32(), (int)M, (int)N, (int)K, false, false, stream())) {
+  if (!k::gemm_gelu(x->f32(), w->f32(), h->f32(), ge->f32(), (int)M, (int)N, (int)K, false, false, stream(), nullptr,
+                    io)) {
     ktimer_end(kt, 0);
     release(h);
     release(ge);
@@ -978,18 +1008,24 @@ int64_t matmul_gelu_fwd(int64_t hx, int64_t hw, int64_t* ge_out) {
   *ge_out = H(ge);
   return H(h);
 }
-// dh of mo = gelu(h) @ W2: gelu_bwd(h, dout @ W2^T) (+ D) from one GEMM
-int64_t gelu_matmul_bwd_h(int64_t hd, int64_t hw, int64_t hh, const TensorBuffer* D) {
+// dh of mo = gelu(h) @ W2: gelu_bwd(h, dout @ W2^T) (+ D) from one GEMM;
+// out_bf16 stores dh in bf16 (no D) for a caller whose readers of dh are
+// bf16 GEMMs.
+int64_t gelu_matmul_bwd_h(int64_t hd, int64_t hw, int64_t hh, const TensorBuffer* D, bool out_bf16) {
   TensorBuffer *d = T(hd), *w = T(hw), *h = T(hh);
   const size_t N = w->shape[0], K = w->shape[1], M = d->len / K;
   if (h->len != M * N || d->len != M * K) fail("malus: gelu matmul VJP: dout %s, w %s, h %s", shape_str(d).c_str(),
                                                shape_str(w).c_str(), shape_str(h).c_str());
   if (D && (D->dtype != F32 || D->len != h->len))
     fail("malus: gelu matmul VJP accumulate: addend %s does not match %s", shape_str(D).c_str(), shape_str(h).c_str());
-  TensorBuffer* out = alloc_like(h);
+  need_f32(d, "gelu matmul VJP");
+  need_f32(w, "gelu matmul VJP");
+  need_f32(h, "gelu matmul VJP");
+  if (D && out_bf16) fail("malus: gelu matmul VJP: a bf16 result takes no addend");
+  TensorBuffer* out = alloc_tensor(out_bf16 ? BF16 : F32, h->shape, h->ndim);
   KTimer* kt = ktimer_begin("gemm");
   if (!k::gemm_gelu(d->f32(), w->f32(), out->f32(), h->f32(), (int)M, (int)N, (int)K, true, true, stream(),
-                    D ? D->f32() : nullptr))
+                    D ? D->f32() : nullptr, out_bf16 ? k::kIoC16 : 0))
     fail("malus: gelu matmul VJP: no fused GEMM for %zux%zux%zu", M, N, K);
   ktimer_end(kt, 2.0 * M * N * K);
   return done(out, "gelu_matmul_bwd");
@@ -1045,9 +1081,11 @@ void check_addend(const TensorBuffer* D, const TensorBuffer* c) {
 int64_t mapped(TensorBuffer* a, TensorBuffer* b, TensorBuffer* c, bool ta, bool tb, int batch, int M, int N, int K,
                const GemmLayouts& L, const TensorBuffer* D, const char* what) {
   check_addend(D, c);
+  GemmLayouts Lio = L;
+  Lio.io = gemm_io(a, b, what);
   KTimer* kt = ktimer_begin("gemm");
   double flops = 0;
-  if (!k::gemm_mapped(a->f32(), b->f32(), c->f32(), batch, M, N, K, ta, tb, L, stream(), D ? D->f32() : nullptr,
+  if (!k::gemm_mapped(a->f32(), b->f32(), c->f32(), batch, M, N, K, ta, tb, Lio, stream(), D ? D->f32() : nullptr,
                       &flops))
     fail("malus: %s: head-folded GEMM layout rejected (T %% 32, hs %% 16 and sizes below 2 GiB are required)", what);
   ktimer_end(kt, flops);  // executed work: causal GEMMs skip the zero triangle
@@ -1099,9 +1137,10 @@ void head_proj_fwd3(int64_t hx, const int64_t* hw, size_t B, size_t T, size_t H,
   GemmLayouts L{dense_layout((long)x->shape[1], 0), dense_layout((long)C, 0), heads_as_rows(T, H, hs), (int)x->len,
                 (int)w0->len};
   L.ngroup = 3;
+  L.io = gemm_io(x, w0, "head_proj_fwd3");
   TensorBuffer* o[3];
   for (int g = 0; g < 3; ++g) {
-    if (T_(hw[g])->len != w0->len) fail("malus: head_proj_fwd3: weights differ in shape");
+    if (T_(hw[g])->len != w0->len || T_(hw[g])->dtype != w0->dtype) fail("malus: head_proj_fwd3: weights differ in shape");
     o[g] = alloc_tensor(F32, sh, 3);
     L.ga[g] = x->f32();
     L.gb[g] = T_(hw[g])->f32();
@@ -1150,8 +1189,10 @@ void head_proj_bwd_w3(int64_t hx, const int64_t* hdq, size_t B, size_t T, size_t
   GemmLayouts L{dense_layout((long)Cin, 0), heads_as_rows(T, H, hs), dense_layout((long)C, 0), (int)x->len,
                 (int)T_(hdq[0])->len};
   L.ngroup = 3;
+  L.io = gemm_io(x, T_(hdq[0]), "head_proj_bwd_w3");
   TensorBuffer* o[3];
   for (int g = 0; g < 3; ++g) {
+    if (T_(hdq[g])->dtype != T_(hdq[0])->dtype) fail("malus: head_proj_bwd_w3: gradients differ in dtype");
     o[g] = alloc_tensor(F32, sh, 2);
     L.ga[g] = x->f32();
     L.gb[g] = T_(hdq[g])->f32();

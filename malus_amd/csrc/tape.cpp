@@ -614,7 +614,10 @@ void backward(int64_t loss) {
         need_values(h);
         need_values(w);
         need_values(ge);
-        if (na) fold_grad(grads, h, [&](const TensorBuffer* o) { return gelu_matmul_bwd_h(dout, w, h, o); });
+        // a bf16 gelu(h) comes from the autocast storage policy, whose h has
+        // this node as its one reader: dh is then read by bf16 GEMMs only
+        const bool dh_bf16 = T(ge)->dtype == BF16;
+        if (na) fold_grad(grads, h, [&](const TensorBuffer* o) { return gelu_matmul_bwd_h(dout, w, h, o, dh_bf16 && !o); });
         if (nb) fold_grad(grads, w, [&](const TensorBuffer* o) { return matmul_bwd_b_impl(ge, w, dout, o); });
         break;
       }
