@@ -354,9 +354,10 @@ int malus_gpt_set_attention(void* gpt, int mode);
 void malus_gpt_set_fused_forward(void* g, int on);
 /* No reference counterpart (the autocast storage policy of
  * docs/adr/0037-bf16-autocast.md:8).  1 (default): under malus_autocast the
- * activations read only by bf16 GEMMs (the layernorm-scale outputs, gelu(h),
- * the GELU VJP's dh) are stored in bf16; the step's values are the same as
- * with 0 (f32 storage), in half the bytes. */
+ * activations read only as bf16 MFMA operands (the layernorm-scale outputs,
+ * gelu(h), the GELU VJP's dh and, with flash attention, q, k, v and their
+ * gradients) are stored in bf16; the step's values are the same as with 0
+ * (f32 storage), in half the bytes. */
 void malus_gpt_set_bf16_activations(void* g, int on);
 int64_t malus_gpt_forward_loss(void* g, int64_t toks, int64_t targets); /* nanogpt_modular.ml:75-91 + cross_entropy */
 int64_t malus_gpt_logits(void* g, int64_t toks);

@@ -56,7 +56,8 @@ int64_t head_proj_bwd_x(int64_t dqh, int64_t w, size_t B, size_t T, size_t H, co
 int64_t head_proj_bwd_w(int64_t x, int64_t dqh, size_t B, size_t T, size_t H, const malus::TensorBuffer* D);
 // causal: P (and dS) are lower-triangular with exact zeros above the
 // diagonal, so the GEMMs skip those k slabs (same values).
-void head_proj_fwd3(int64_t x, const int64_t* w, size_t B, size_t T, size_t H, int64_t* out);
+// out_bf16: q, k, v stored in bf16 (for readers that round them to bf16).
+void head_proj_fwd3(int64_t x, const int64_t* w, size_t B, size_t T, size_t H, int64_t* out, bool out_bf16 = false);
 // Three head projections of one input together (group order = the tape's
 // VJP order): the accumulated dx, and the three dW into out[0..2].
 int64_t head_proj_bwd_x3(const int64_t* dqh, const int64_t* w, size_t B, size_t T, size_t H,

@@ -227,11 +227,13 @@ bool attn_bwd(const float* dO, size_t ldo, size_t heads, const float* V, const f
 // mask)) @ V written at O + (b / heads) * t * ldo + (b % heads) * hs +
 // i * ldo (ldo = heads * hs: the [B*T, C] layout; ldo = hs, heads = 1:
 // dense), and lse[b * t + i] = row max + log(row sum).  bf16: products on
-// the bf16 MFMA (autocast).  False (nothing launched) when the shape or an
-// alignment does not fit.
+// the bf16 MFMA (autocast).  qkv_bf16 (with bf16): Q, K, V stored in bf16,
+// and in flash_bwd dQ, dK, dV written in bf16 (no addends).  False (nothing
+// launched) when the shape or an alignment does not fit.
 bool flash_supported(size_t bh, size_t t, size_t hs);
 bool flash_fwd(const float* Q, const float* K, const float* V, const float* scale, float* O, size_t ldo, size_t heads,
-               float* lse, size_t bh, size_t t, size_t hs, bool causal, bool bf16, hipStream_t s);
+               float* lse, size_t bh, size_t t, size_t hs, bool causal, bool bf16, hipStream_t s,
+               bool qkv_bf16 = false);
 // Backward: dQ = Dq + dS K, dK = Dk + dS^T Q, dV = Dv + P^T dO with P
 // recomputed from lse and dS = P (dP - rowsum(dO O)) scale; O and dO use the
 // forward's O addressing, Q K V dQ dK dV (and the optional addends) are
@@ -242,7 +244,7 @@ struct FlashBwd {
   const float *Dq, *Dk, *Dv;
 };
 bool flash_bwd(const FlashBwd& a, size_t ldo, size_t heads, size_t bh, size_t t, size_t hs, bool causal, bool bf16,
-               hipStream_t s);
+               hipStream_t s, bool qkv_bf16 = false);
 // The autocast scope's state (GEMMs and flash attention on the bf16 MFMA).
 bool autocast_on();
 // Sum over the axis of x * y (y has x's layout); each product rounded to f32.

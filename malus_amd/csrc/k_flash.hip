@@ -69,6 +69,48 @@ __device__ __forceinline__ void load8(const float* __restrict__ p, float (&v)[8]
   }
 }
 
+// Q, K, V and their gradients in the model's storage type: f32, or bf16
+// under the autocast storage policy (S16; element offsets either way).  A
+// bf16 value widens to f32 exactly, and the bf16 MFMA rounds it back to
+// itself, so the products see the same operands as from an f32 copy of the
+// rounded values.
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+template <bool S16>
+__device__ __forceinline__ void ld8(const float* __restrict__ base, size_t i, float (&v)[8]) {
+  if constexpr (S16) {
+    const bf16x8 h = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const __bf16*>(base) + i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (float)h[e];
+  } else {
+    load8(base + i, v);
+  }
+}
+template <bool S16>
+__device__ __forceinline__ v4f ld4(const float* __restrict__ base, size_t i) {
+  if constexpr (S16) {
+    const bf16x4 h = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const __bf16*>(base) + i);
+    return v4f{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+  } else {
+    return *reinterpret_cast<const v4f*>(base + i);
+  }
+}
+template <bool S16>
+__device__ __forceinline__ float ld1(const float* __restrict__ base, size_t i) {
+  if constexpr (S16) return (float)reinterpret_cast<const __bf16*>(base)[i];
+  else return base[i];
+}
+template <bool S16>
+__device__ __forceinline__ void st4(float* __restrict__ base, size_t i, v4f w) {
+  if constexpr (S16)
+    *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(base) + i) = bf16x4{(__bf16)w[0], (__bf16)w[1], (__bf16)w[2], (__bf16)w[3]};
+  else *reinterpret_cast<v4f*>(base + i) = w;
+}
+template <bool S16>
+__device__ __forceinline__ void st1(float* __restrict__ base, size_t i, float w) {
+  if constexpr (S16) reinterpret_cast<__bf16*>(base)[i] = (__bf16)w;
+  else base[i] = w;
+}
+
 // A head's row `row` of a [B*T, H*HS] tensor (O, dO) or of [B*H, T, HS].
 __device__ __forceinline__ const float* head_row(const float* base, int bh, int H, int T, int ld, int hs, int row) {
   return base + (size_t)(bh / H) * T * ld + (size_t)(bh % H) * hs + (size_t)row * ld;
@@ -88,26 +130,26 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // Forward: query tile qt of head bh.  O^T = V^T P^T keeps the output with
 // lane = query, so the online rescale is a per-lane factor.
-template <int HS, bool CAUSAL, bool BF>
+template <int HS, bool CAUSAL, bool BF, bool S16 = false>
 __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q, const float* __restrict__ K,
                                                   const float* __restrict__ V, const float* __restrict__ scale,
                                                   float* __restrict__ O, int ldo, int H, float* __restrict__ lse, int T,
                                                   int BH) {
+  static_assert(BF || !S16, "bf16 storage runs on the bf16 MFMA");
   constexpr int NKB = HS / 16, NN = HS / 32;
   const int NT = T / 32;
   const int qt = NT - 1 - (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
   const int lane = threadIdx.x, x = lane & 31, lk = lane >> 5;
   const size_t head = (size_t)bh * T * HS;
-  const float *Qh = Q + head, *Kh = K + head, *Vh = V + head;
   const int i0 = 32 * qt;
   const float sc = scale[0];
 
   float qb[NKB][8];  // B of S^T = K Q^T: Q[i0 + x][16 kb + 8 lk + e]
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) load8(Qh + (size_t)(i0 + x) * HS + 16 * kb + 8 * lk, qb[kb]);
+  for (int kb = 0; kb < NKB; ++kb) ld8<S16>(Q, head + (size_t)(i0 + x) * HS + 16 * kb + 8 * lk, qb[kb]);
   float ka[NKB][8];  // A of S^T: K[32 j + perm_row(x)][16 kb + 8 lk + e]
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) load8(Kh + (size_t)perm_row(x) * HS + 16 * kb + 8 * lk, ka[kb]);
+  for (int kb = 0; kb < NKB; ++kb) ld8<S16>(K, head + (size_t)perm_row(x) * HS + 16 * kb + 8 * lk, ka[kb]);
 
   v16f o[NN];
 #pragma unroll
@@ -126,7 +168,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q
 #pragma unroll
       for (int u = 0; u < PER; ++u) {
         const int f = lane + 64 * u;
-        vn[u] = *reinterpret_cast<const v4f*>(Vh + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
+        vn[u] = ld4<S16>(V, head + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
       }
       wave_lds_sync();  // the last tile's reads of Vs are done
 #pragma unroll
@@ -148,7 +190,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q
     if (j < last) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
-        load8(Kh + (size_t)(32 * (j + 1) + perm_row(x)) * HS + 16 * kb + 8 * lk, ka[kb]);
+        ld8<S16>(K, head + (size_t)(32 * (j + 1) + perm_row(x)) * HS + 16 * kb + 8 * lk, ka[kb]);
     }
     // lane = query i0 + x, register r = key 32 j + perm_index(r, lk)
     float mt = -INFINITY;
@@ -199,7 +241,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q
 
 // Backward, query-centric: dQ (+ Dq) of query tile qt, and D = rowsum(dO*O)
 // of its rows into dsum for the key-centric pass.
-template <int HS, bool CAUSAL, bool BF>
+template <int HS, bool CAUSAL, bool BF, bool S16 = false>
 __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict__ Q, const float* __restrict__ K,
                                                      const float* __restrict__ V, const float* __restrict__ O,
                                                      const float* __restrict__ dO, int ldo, int H,
@@ -211,7 +253,6 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
   const int qt = NT - 1 - (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
   const int lane = threadIdx.x, x = lane & 31, lk = lane >> 5;
   const size_t head = (size_t)bh * T * HS;
-  const float *Qh = Q + head, *Kh = K + head, *Vh = V + head;
   const int i0 = 32 * qt, i = i0 + x;
   const float sc = scale[0];
 
@@ -221,7 +262,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
   float d = 0.0f;
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    load8(Qh + (size_t)i * HS + 16 * kb + 8 * lk, qb[kb]);
+    ld8<S16>(Q, head + (size_t)i * HS + 16 * kb + 8 * lk, qb[kb]);
     load8(dorow + 16 * kb + 8 * lk, ob[kb]);
     float ov[8];
     load8(orow + 16 * kb + 8 * lk, ov);
@@ -247,8 +288,8 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int f = lane + 64 * u;
-      kn[u] = *reinterpret_cast<const v4f*>(Kh + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
-      vn[u] = *reinterpret_cast<const v4f*>(Vh + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
+      kn[u] = ld4<S16>(K, head + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
+      vn[u] = ld4<S16>(V, head + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
     }
   };
   for (int j = 0; j <= last; ++j) {
@@ -297,29 +338,29 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
       for (int n = 0; n < NN; ++n) dq[n] = slab<BF>(ab, kc[n][h], dq[n]);
     }
   }
-  // dQ[i0 + 8 (r >> 2) + 4 lk + (r & 3)][32 n + x] (+ Dq: every addend loaded before the first add)
-  float* dqh = dQ + head;
-  auto off = [&](int n, int r) { return (size_t)(i0 + 8 * (r >> 2) + 4 * lk + (r & 3)) * HS + 32 * n + x; };
-  if (Dq) {
+  // dQ[i0 + 8 (r >> 2) + 4 lk + (r & 3)][32 n + x] (+ Dq: every addend loaded
+  // before the first add; f32 storage only)
+  auto off = [&](int n, int r) { return head + (size_t)(i0 + 8 * (r >> 2) + 4 * lk + (r & 3)) * HS + 32 * n + x; };
+  if (!S16 && Dq) {
     float a[NN][16];
 #pragma unroll
     for (int n = 0; n < NN; ++n)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) a[n][r] = Dq[head + off(n, r)];
+      for (int r = 0; r < 16; ++r) a[n][r] = Dq[off(n, r)];
 #pragma unroll
     for (int n = 0; n < NN; ++n)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dqh[off(n, r)] = a[n][r] + dq[n][r];
+      for (int r = 0; r < 16; ++r) dQ[off(n, r)] = a[n][r] + dq[n][r];
   } else {
 #pragma unroll
     for (int n = 0; n < NN; ++n)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dqh[off(n, r)] = dq[n][r];
+      for (int r = 0; r < 16; ++r) st1<S16>(dQ, off(n, r), dq[n][r]);
   }
 }
 
 // Backward, key-centric: dK (+ Dk) and dV (+ Dv) of key tile kt.
-template <int HS, bool CAUSAL, bool BF>
+template <int HS, bool CAUSAL, bool BF, bool S16 = false>
 __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict__ Q, const float* __restrict__ K,
                                                       const float* __restrict__ V, const float* __restrict__ dO, int ldo,
                                                       int H, const float* __restrict__ lse,
@@ -332,7 +373,6 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
   const int kt = (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
   const int lane = threadIdx.x, x = lane & 31, lk = lane >> 5;
   const size_t head = (size_t)bh * T * HS;
-  const float *Qh = Q + head, *Kh = K + head, *Vh = V + head;
   const int j0 = 32 * kt, key = j0 + x;
   const float sc = scale[0];
   const float* lseh = lse + (size_t)bh * T;
@@ -341,8 +381,8 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
   float kb_[NKB][8], vb[NKB][8];  // B of S = Q K^T and of dP = dO V^T: rows j0 + x of K, V
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    load8(Kh + (size_t)key * HS + 16 * kb + 8 * lk, kb_[kb]);
-    load8(Vh + (size_t)key * HS + 16 * kb + 8 * lk, vb[kb]);
+    ld8<S16>(K, head + (size_t)key * HS + 16 * kb + 8 * lk, kb_[kb]);
+    ld8<S16>(V, head + (size_t)key * HS + 16 * kb + 8 * lk, vb[kb]);
   }
   v16f dvt[NN], dkt[NN];  // dV^T, dK^T: lane = key, rows = head dims
 #pragma unroll
@@ -368,7 +408,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
 #pragma unroll
       for (int u = 0; u < PER; ++u) {
         const int f = lane + 64 * u;
-        qn[u] = *reinterpret_cast<const v4f*>(Qh + (size_t)(i0 + f / Q4) * HS + 4 * (f % Q4));
+        qn[u] = ld4<S16>(Q, head + (size_t)(i0 + f / Q4) * HS + 4 * (f % Q4));
         on[u] = *reinterpret_cast<const v4f*>(head_row(dO, bh, H, T, ldo, HS, i0 + f / Q4) + 4 * (f % Q4));
       }
       wave_lds_sync();  // the last tile's reads of Qs and Os are done
@@ -393,7 +433,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
         float qa[8], oa[8];  // A: rows perm_row(x) of Q_i, dO_i
-        load8(Qh + (size_t)qrow * HS + 16 * kb + 8 * lk, qa);
+        ld8<S16>(Q, head + (size_t)qrow * HS + 16 * kb + 8 * lk, qa);
         load8(dorow + 16 * kb + 8 * lk, oa);
         s = slab<BF>(qa, kb_[kb], s);
         dp = slab<BF>(oa, vb[kb], dp);
@@ -436,7 +476,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
           } else {
             const int q = i0 + 16 * h + 8 * lk + e;
             oa[e] = head_row(dO, bh, H, T, ldo, HS, q)[32 * n + x];
-            qa[e] = Qh[(size_t)q * HS + 32 * n + x];
+            qa[e] = ld1<S16>(Q, head + (size_t)q * HS + 32 * n + x);
           }
         }
         dvt[n] = slab<BF>(oa, pb, dvt[n]);
@@ -452,8 +492,8 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const size_t off = head + (size_t)key * HS + 32 * n + 8 * g + 4 * lk;
-      if (Dv) av[n][g] = *reinterpret_cast<const v4f*>(Dv + off);
-      if (Dk) ak[n][g] = *reinterpret_cast<const v4f*>(Dk + off);
+      if (!S16 && Dv) av[n][g] = *reinterpret_cast<const v4f*>(Dv + off);
+      if (!S16 && Dk) ak[n][g] = *reinterpret_cast<const v4f*>(Dk + off);
     }
 #pragma unroll
   for (int n = 0; n < NN; ++n)
@@ -466,41 +506,58 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
         wv[c] = dvt[n][4 * g + c];
         wk[c] = dkt[n][4 * g + c];
       }
-      if (Dv) wv = av[n][g] + wv;
-      if (Dk) wk = ak[n][g] + wk;
-      *reinterpret_cast<v4f*>(dV + off) = wv;
-      *reinterpret_cast<v4f*>(dK + off) = wk;
+      if (!S16 && Dv) wv = av[n][g] + wv;
+      if (!S16 && Dk) wk = ak[n][g] + wk;
+      st4<S16>(dV, off, wv);
+      st4<S16>(dK, off, wk);
     }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-template <int HS, bool CAUSAL, bool BF>
+template <int HS, bool CAUSAL, bool BF, bool S16>
 void fwd_launch(const float* Q, const float* K, const float* V, const float* scale, float* O, int ldo, int H,
                 float* lse, int T, int BH, hipStream_t s) {
-  k_flash_fwd<HS, CAUSAL, BF><<<(unsigned)(T / 32 * BH), 64, 0, s>>>(Q, K, V, scale, O, ldo, H, lse, T, BH);
+  k_flash_fwd<HS, CAUSAL, BF, S16><<<(unsigned)(T / 32 * BH), 64, 0, s>>>(Q, K, V, scale, O, ldo, H, lse, T, BH);
 }
 
-template <int HS, bool CAUSAL, bool BF>
+template <int HS, bool CAUSAL, bool BF, bool S16>
 void bwd_launch(const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
   const unsigned grid = (unsigned)(T / 32 * BH);
-  k_flash_bwd_dq<HS, CAUSAL, BF><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.O, a.dO, ldo, H, a.lse, a.scale, a.dQ, a.Dq,
-                                                      a.dsum, T, BH);
-  k_flash_bwd_dkv<HS, CAUSAL, BF><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.dO, ldo, H, a.lse, a.dsum, a.scale, a.dK, a.Dk,
-                                                       a.dV, a.Dv, T, BH);
+  k_flash_bwd_dq<HS, CAUSAL, BF, S16><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.O, a.dO, ldo, H, a.lse, a.scale, a.dQ,
+                                                           a.Dq, a.dsum, T, BH);
+  k_flash_bwd_dkv<HS, CAUSAL, BF, S16><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.dO, ldo, H, a.lse, a.dsum, a.scale, a.dK,
+                                                            a.Dk, a.dV, a.Dv, T, BH);
 }
 
-template <bool CAUSAL, bool BF>
-void fwd_hs(size_t hs, const float* Q, const float* K, const float* V, const float* scale, float* O, int ldo, int H,
-            float* lse, int T, int BH, hipStream_t s) {
-  if (hs == 64) fwd_launch<64, CAUSAL, BF>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
-  else fwd_launch<32, CAUSAL, BF>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
+// precision: 0 f32, 1 bf16 MFMA on f32 storage, 2 bf16 MFMA on bf16 q, k, v
+// (and their gradients)
+template <int HS, bool CAUSAL>
+void fwd_prec(int prec, const float* Q, const float* K, const float* V, const float* scale, float* O, int ldo, int H,
+              float* lse, int T, int BH, hipStream_t s) {
+  if (prec == 2) fwd_launch<HS, CAUSAL, true, true>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
+  else if (prec == 1) fwd_launch<HS, CAUSAL, true, false>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
+  else fwd_launch<HS, CAUSAL, false, false>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
 }
 
-template <bool CAUSAL, bool BF>
-void bwd_hs(size_t hs, const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
-  if (hs == 64) bwd_launch<64, CAUSAL, BF>(a, ldo, H, T, BH, s);
-  else bwd_launch<32, CAUSAL, BF>(a, ldo, H, T, BH, s);
+template <bool CAUSAL>
+void fwd_hs(size_t hs, int prec, const float* Q, const float* K, const float* V, const float* scale, float* O, int ldo,
+            int H, float* lse, int T, int BH, hipStream_t s) {
+  if (hs == 64) fwd_prec<64, CAUSAL>(prec, Q, K, V, scale, O, ldo, H, lse, T, BH, s);
+  else fwd_prec<32, CAUSAL>(prec, Q, K, V, scale, O, ldo, H, lse, T, BH, s);
+}
+
+template <int HS, bool CAUSAL>
+void bwd_prec(int prec, const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
+  if (prec == 2) bwd_launch<HS, CAUSAL, true, true>(a, ldo, H, T, BH, s);
+  else if (prec == 1) bwd_launch<HS, CAUSAL, true, false>(a, ldo, H, T, BH, s);
+  else bwd_launch<HS, CAUSAL, false, false>(a, ldo, H, T, BH, s);
+}
+
+template <bool CAUSAL>
+void bwd_hs(size_t hs, int prec, const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
+  if (hs == 64) bwd_prec<64, CAUSAL>(prec, a, ldo, H, T, BH, s);
+  else bwd_prec<32, CAUSAL>(prec, a, ldo, H, T, BH, s);
 }
 
 }  // namespace
@@ -511,37 +568,30 @@ bool flash_supported(size_t bh, size_t t, size_t hs) {
 }
 
 bool flash_fwd(const float* Q, const float* K, const float* V, const float* scale, float* O, size_t ldo, size_t heads,
-               float* lse, size_t bh, size_t t, size_t hs, bool causal, bool bf16, hipStream_t s) {
+               float* lse, size_t bh, size_t t, size_t hs, bool causal, bool bf16, hipStream_t s, bool qkv_bf16) {
   if (!flash_supported(bh, t, hs) || heads == 0 || bh % heads || ldo < hs * heads || ldo % 4) return false;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O) || !lse || !scale) return false;
   const int T = (int)t, BH = (int)bh, l = (int)ldo, H = (int)heads;
-  if (causal) {
-    if (bf16) fwd_hs<true, true>(hs, Q, K, V, scale, O, l, H, lse, T, BH, s);
-    else fwd_hs<true, false>(hs, Q, K, V, scale, O, l, H, lse, T, BH, s);
-  } else {
-    if (bf16) fwd_hs<false, true>(hs, Q, K, V, scale, O, l, H, lse, T, BH, s);
-    else fwd_hs<false, false>(hs, Q, K, V, scale, O, l, H, lse, T, BH, s);
-  }
+  const int prec = qkv_bf16 ? 2 : bf16 ? 1 : 0;
+  if (causal) fwd_hs<true>(hs, prec, Q, K, V, scale, O, l, H, lse, T, BH, s);
+  else fwd_hs<false>(hs, prec, Q, K, V, scale, O, l, H, lse, T, BH, s);
   MALUS_HIP(hipGetLastError());
   return true;
 }
 
 bool flash_bwd(const FlashBwd& a, size_t ldo, size_t heads, size_t bh, size_t t, size_t hs, bool causal, bool bf16,
-               hipStream_t s) {
+               hipStream_t s, bool qkv_bf16) {
   if (!flash_supported(bh, t, hs) || heads == 0 || bh % heads || ldo < hs * heads || ldo % 4) return false;
   for (const void* p : {(const void*)a.Q, (const void*)a.K, (const void*)a.V, (const void*)a.O, (const void*)a.dO,
                         (const void*)a.dQ, (const void*)a.dK, (const void*)a.dV, (const void*)a.lse,
                         (const void*)a.dsum})
     if (!p || !aligned16(p)) return false;
   if ((a.Dk && !aligned16(a.Dk)) || (a.Dv && !aligned16(a.Dv)) || !a.scale) return false;
+  if (qkv_bf16 && (a.Dq || a.Dk || a.Dv)) return false;  // bf16 gradients take no addends
   const int T = (int)t, BH = (int)bh, l = (int)ldo, H = (int)heads;
-  if (causal) {
-    if (bf16) bwd_hs<true, true>(hs, a, l, H, T, BH, s);
-    else bwd_hs<true, false>(hs, a, l, H, T, BH, s);
-  } else {
-    if (bf16) bwd_hs<false, true>(hs, a, l, H, T, BH, s);
-    else bwd_hs<false, false>(hs, a, l, H, T, BH, s);
-  }
+  const int prec = qkv_bf16 ? 2 : bf16 ? 1 : 0;
+  if (causal) bwd_hs<true>(hs, prec, a, l, H, T, BH, s);
+  else bwd_hs<false>(hs, prec, a, l, H, T, BH, s);
   MALUS_HIP(hipGetLastError());
   return true;
 }

@@ -590,7 +590,7 @@ bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayou
   const bool bf = g_autocast || L.io;
   Plan p = plan_gemm(1, M, N, K, v, false, -1, bf);
   const bool c_dense = L.c.r.div == 0 && L.c.c.div == 0 && L.c.c.s0 == 1 && L.c.r.s0 == N;
-  if (accumulate || !c_dense) {
+  if (accumulate || !c_dense || (L.io & kIoC16)) {  // split partials are f32 and dense
     p.nsplit = 1;
     p.k_chunk = K;
   }
@@ -679,7 +679,6 @@ bool mapped_ok(int batch, int M, int N, int K, bool transA, bool transB, const G
   if (!map_contig(a_contig, ra) || !map_contig(b_contig, rb)) return false;
   if (transA ? M % ra : 0) return false;
   if (transB ? 0 : N % rb) return false;
-  if (L.io & kIoC16) return false;  // mapped outputs stay f32
   const GemmMap& fak = transA ? L.a.r : L.a.c;
   const GemmMap& fbk = transB ? L.b.c : L.b.r;
   if (!map_k16(fak) || !map_k16(fbk)) return false;

@@ -14,7 +14,11 @@ template <int TM, int TN>
 const void* io_instance(int v) {
   const int io = v >> 9;
   const bool ta = v & 8, tb = v & 4, mapped = v & 32, gelu = v & 64;
-  if (v & 128) return nullptr;
+  if (v & 128) {  // the head projections' dx = dq Wq^T + dk Wk^T + dv Wv^T from bf16 dq, dk, dv
+    if (!ta && tb && io == kIoA16)
+      return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, true, 3, true, kIoA16>);
+    return nullptr;
+  }
   if (gelu) {
     // h = x W1 with ge = gelu(h) in bf16 (x the bf16 layernorm output)
     if (!ta && !tb && io == (kIoA16 | kIoE16))
@@ -25,11 +29,19 @@ const void* io_instance(int v) {
     return nullptr;
   }
   if (mapped) {
-    // the head projections of a bf16 layernorm output, and their weight gradients
+    // the head projections of a bf16 layernorm output (q, k, v in f32 or
+    // bf16), their weight gradients (from f32 or bf16 dq) and, one
+    // projection at a time, their dx
     if (!ta && !tb && io == kIoA16)
       return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, false, true, 0, true, kIoA16>);
+    if (!ta && !tb && io == (kIoA16 | kIoC16))
+      return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, false, true, 0, true, kIoA16 | kIoC16>);
     if (ta && !tb && io == kIoA16)
       return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, true, false, true, 0, true, kIoA16>);
+    if (ta && !tb && io == (kIoA16 | kIoB16))
+      return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, true, false, true, 0, true, kIoA16 | kIoB16>);
+    if (!ta && tb && io == kIoA16)
+      return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, true, 0, true, kIoA16>);
     return nullptr;
   }
   if (!ta && !tb && io == kIoA16)  // out = x2 + ge W2

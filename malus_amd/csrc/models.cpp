@@ -150,11 +150,13 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   const bool fused_heads = g.fused_fwd && heads_foldable(B, Tn, H, hs);
   // The autocast storage policy (docs/adr/0037-bf16-autocast.md:8: matmuls
   // and forward elementwise kernels in bf16): the two layernorm-scale
-  // outputs, gelu(h) and the GELU VJP's dh are read only by bf16 GEMMs, which
-  // round their operands to bf16 anyway, so they are stored in bf16 by the
-  // kernels that produce them; every value of the step is unchanged, and the
-  // GEMMs that read them move half the bytes.  h (the GELU VJP's input),
-  // the residual stream, parameters, gradients and optimizer state stay f32.
+  // outputs, gelu(h), the GELU VJP's dh and, with flash attention, q, k, v
+  // and their gradients are read only as bf16 MFMA operands, which are
+  // rounded to bf16 anyway, so the kernels that produce them store bf16;
+  // every value of the step is unchanged, and their readers move half the
+  // bytes.  h (the GELU VJP's input), the attention output (its VJP's
+  // rowsum(dO * O) is f32 arithmetic), the residual stream, parameters,
+  // gradients and optimizer state stay f32.
   const bool bf_act = g.bf16_act && k::autocast_on() && fused_heads && C % 128 == 0 && C <= 512 && N % 8 == 0;
   // nanogpt_modular.ml:47-68
   int64_t y1;
@@ -172,11 +174,22 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
     rel({q, q4, qp});
     return Q;
   };
+  const bool rows_ok = fused_heads && k::attn_scores_supported(B * H, Tn, hs);
+  const bool flash_ok = fused_heads && k::flash_supported(B * H, Tn, hs);
+  // AUTO: in f32 the row-register kernel where it is built (at T = 256 its
+  // backward reads the stored P instead of recomputing it, and is faster);
+  // under autocast flash attention, whose products run on the bf16 MFMA
+  const bool flash = flash_ok && (g.attn_mode == ATTN_FLASH ||
+                                  (g.attn_mode == ATTN_AUTO && (!rows_ok || k::autocast_on())));
+  const bool fused_attention = !flash && rows_ok && (g.attn_mode == ATTN_AUTO || g.attn_mode == ATTN_ROWS);
+  // Under the storage policy flash attention reads q, k, v only as bf16 MFMA
+  // operands, and their gradients feed only bf16 GEMMs: all six in bf16.
+  const bool qkv_bf16 = bf_act && flash;
   int64_t Q, K, Vv;
   if (fused_heads) {  // the three projections in one grouped launch, three tape nodes
     const int64_t w[3] = {P[1], P[2], P[3]};
     int64_t qkv[3];
-    head_proj_fwd3(xn1, w, B, Tn, H, qkv);
+    head_proj_fwd3(xn1, w, B, Tn, H, qkv, qkv_bf16);
     for (int i = 0; i < 3; ++i) tape_record_fused(TAG_HEAD_PROJ, {xn1, w[i]}, qkv[i], {(int64_t)B, (int64_t)Tn, (int64_t)H});
     Q = qkv[0];
     K = qkv[1];
@@ -187,14 +200,6 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
     Vv = head_fold(P[3]);
   }
   int64_t Kt = fused_heads ? 0 : permute(K, {0, 2, 1});
-  const bool rows_ok = fused_heads && k::attn_scores_supported(B * H, Tn, hs);
-  const bool flash_ok = fused_heads && k::flash_supported(B * H, Tn, hs);
-  // AUTO: in f32 the row-register kernel where it is built (at T = 256 its
-  // backward reads the stored P instead of recomputing it, and is faster);
-  // under autocast flash attention, whose products run on the bf16 MFMA
-  const bool flash = flash_ok && (g.attn_mode == ATTN_FLASH ||
-                                  (g.attn_mode == ATTN_AUTO && (!rows_ok || k::autocast_on())));
-  const bool fused_attention = !flash && rows_ok && (g.attn_mode == ATTN_AUTO || g.attn_mode == ATTN_ROWS);
   int64_t scale;
   if (fused_attention || flash) {
     // variable(ones(1,1) * (1/sqrt(hs))) is the same value every forward and

@@ -1129,7 +1129,7 @@ int64_t head_proj_bwd_w(int64_t hx, int64_t hdq, size_t B, size_t T, size_t H, c
   return mapped(x, dq, c, true, false, 1, (int)Cin, (int)C, (int)N, L, D, "head_proj_bwd_w");
 }
 // Qh_g = heads(x @ W_g) for three weights in one launch.
-void head_proj_fwd3(int64_t hx, const int64_t* hw, size_t B, size_t T, size_t H, int64_t* out) {
+void head_proj_fwd3(int64_t hx, const int64_t* hw, size_t B, size_t T, size_t H, int64_t* out, bool out_bf16) {
   TensorBuffer* x = T_(hx);
   TensorBuffer* w0 = T_(hw[0]);
   const size_t C = w0->shape[1], hs = C / H, N = B * T;
@@ -1137,11 +1137,11 @@ void head_proj_fwd3(int64_t hx, const int64_t* hw, size_t B, size_t T, size_t H,
   GemmLayouts L{dense_layout((long)x->shape[1], 0), dense_layout((long)C, 0), heads_as_rows(T, H, hs), (int)x->len,
                 (int)w0->len};
   L.ngroup = 3;
-  L.io = gemm_io(x, w0, "head_proj_fwd3");
+  L.io = gemm_io(x, w0, "head_proj_fwd3") | (out_bf16 ? k::kIoC16 : 0);
   TensorBuffer* o[3];
   for (int g = 0; g < 3; ++g) {
     if (T_(hw[g])->len != w0->len || T_(hw[g])->dtype != w0->dtype) fail("malus: head_proj_fwd3: weights differ in shape");
-    o[g] = alloc_tensor(F32, sh, 3);
+    o[g] = alloc_tensor(out_bf16 ? BF16 : F32, sh, 3);
     L.ga[g] = x->f32();
     L.gb[g] = T_(hw[g])->f32();
     L.gc[g] = o[g]->f32();
@@ -1170,7 +1170,9 @@ int64_t head_proj_bwd_x3(const int64_t* hdq, const int64_t* hw, size_t B, size_t
   GemmLayouts L{heads_as_rows(T, H, hs), dense_layout((long)C, 0), dense_layout((long)Cin, 0), (int)T_(hdq[0])->len,
                 (int)w0->len};
   L.ngroup = 3;
+  L.io = gemm_io(T_(hdq[0]), w0, "head_proj_bwd_x3");
   for (int g = 0; g < 3; ++g) {
+    if (T_(hdq[g])->dtype != T_(hdq[0])->dtype) fail("malus: head_proj_bwd_x3: gradients differ in dtype");
     L.ga[g] = T_(hdq[g])->f32();
     L.gb[g] = T_(hw[g])->f32();
   }
@@ -1309,6 +1311,14 @@ void attn_bwd_all_impl(int64_t hda, int64_t hq, int64_t hk, int64_t hv, int64_t 
   *dk = malus::H(ok);
   *dv = malus::H(ov);
 }
+// Q, K and V all f32 (false) or all bf16 (true, the autocast storage policy:
+// the kernels then run on the bf16 MFMA whatever the scope's state).
+bool flash_qkv_bf16(const TensorBuffer* q, const TensorBuffer* kk, const TensorBuffer* v) {
+  const int d = q->dtype;
+  if ((d != F32 && d != BF16) || kk->dtype != d || v->dtype != d)
+    fail("malus: flash attention: Q, K, V must be all f32 or all bf16 (dtype tags %d %d %d)", d, kk->dtype, v->dtype);
+  return d == BF16;
+}
 // Flash attention of the model: Q, K, V [B*H, T, hs] -> att [B*T, H*hs]
 // (causal); *lse_out [B*H, T].
 int64_t flash_fwd_impl(int64_t hq, int64_t hk, int64_t hv, int64_t hscale, size_t B, size_t T, size_t H,
@@ -1316,10 +1326,11 @@ int64_t flash_fwd_impl(int64_t hq, int64_t hk, int64_t hv, int64_t hscale, size_
   TensorBuffer *q = T_(hq), *kk = T_(hk), *v = T_(hv), *sc = T_(hscale);
   const size_t hs = q->shape[2], bh = B * H, C = H * hs;
   const size_t lsh[2] = {bh, T}, osh[2] = {B * T, C};
+  const bool s16 = flash_qkv_bf16(q, kk, v);
   TensorBuffer* lse = alloc_tensor(F32, lsh, 2);
   TensorBuffer* out = alloc_tensor(F32, osh, 2);
   if (!k::flash_fwd(q->f32(), kk->f32(), v->f32(), sc->f32(), out->f32(), C, H, lse->f32(), bh, T, hs, true,
-                    k::autocast_on(), stream()))
+                    k::autocast_on() || s16, stream(), s16))
     fail("malus: flash attention: no kernel for t=%zu hs=%zu", T, hs);
   const uint64_t seq = enqueue_mark("flash_attn_fwd");
   lse->write_seq = seq;
@@ -1333,13 +1344,15 @@ void flash_bwd_impl(int64_t hda, int64_t hq, int64_t hk, int64_t hv, int64_t ho,
                     int64_t* dv, size_t B, size_t T, size_t H) {
   TensorBuffer *da = T_(hda), *q = T_(hq), *kk = T_(hk), *v = T_(hv), *o = T_(ho), *lse = T_(hlse), *sc = T_(hscale);
   const size_t hs = q->shape[2], bh = B * H, C = H * hs;
+  const bool s16 = flash_qkv_bf16(q, kk, v);  // the gradients take Q, K, V's type
+  if (s16 && (Dq || Dk || Dv)) fail("malus: flash attention VJP: bf16 gradients take no addends");
   TensorBuffer *oq = alloc_like(q), *ok = alloc_like(kk), *ov = alloc_like(v);
   size_t bucket;
   float* dsum = static_cast<float*>(pool_alloc(bh * T * sizeof(float), &bucket));
   const k::FlashBwd a{q->f32(), kk->f32(), v->f32(), o->f32(), da->f32(), lse->f32(), sc->f32(),
                       oq->f32(), ok->f32(), ov->f32(), dsum,
                       Dq ? Dq->f32() : nullptr, Dk ? Dk->f32() : nullptr, Dv ? Dv->f32() : nullptr};
-  if (!k::flash_bwd(a, C, H, bh, T, hs, true, k::autocast_on(), stream()))
+  if (!k::flash_bwd(a, C, H, bh, T, hs, true, k::autocast_on() || s16, stream(), s16))
     fail("malus: flash attention VJP: no kernel for t=%zu hs=%zu", T, hs);
   pool_free(dsum, bucket);
   const uint64_t seq = enqueue_mark("flash_attn_bwd");
