@@ -526,8 +526,9 @@ def run_gpt(rt, a, cfg):
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("bf16 GEMM operands, f32 accumulation; the activations read only by GEMMs stored in bf16 "
-                  "(layernorm-scale outputs, gelu(h), dh), everything else f32 (autocast)")
+        "dtype": ("bf16 GEMM and attention operands, f32 accumulation; the activations read only as bf16 operands "
+                  "stored in bf16 (layernorm-scale outputs, gelu(h), dh, q, k, v and their gradients), everything "
+                  "else f32 (autocast)")
                  if a.autocast and not a.f32_activations else
                  "bf16 GEMM operands, f32 accumulation and everything else f32 (autocast)" if a.autocast else "f32",
         "data": "synthetic int32 tokens i.i.d. uniform in [0,65), drawn on the device inside each timed step "
