@@ -52,6 +52,13 @@ struct TensorBuffer {
   size_t shape[kMaxRank] = {0};
   std::atomic<int64_t> rc{1};
   uint64_t write_seq = 0;        // stream sequence of the last GPU write (0 = ready)
+  // A bf16 copy of this tensor's values for bf16 GEMM operands (the
+  // autocast storage policy keeps one per weight matrix; this holds a
+  // reference).  It stands for this tensor while copy->copy_of == this and
+  // copy->copy_seq == write_seq: refreshed after the tensor's last write.
+  TensorBuffer* bf16_copy = nullptr;
+  const TensorBuffer* copy_of = nullptr;  // on a copy: the tensor it was last refreshed from
+  uint64_t copy_seq = 0;                  // ... and that tensor's write_seq at the refresh
 
   float* f32() const { return static_cast<float*>(st->ptr); }
   int32_t* i32() const { return static_cast<int32_t*>(st->ptr); }
@@ -156,6 +163,13 @@ void unary(int op, const float* x, float* out, size_t n, hipStream_t s);
 void unary_bwd(int op, const float* xy, const float* dout, float* out, size_t n, hipStream_t s);
 // out = x converted f32 -> bf16 (to_bf16, round to nearest even) or bf16 -> f32 (exact).
 void convert_f32_bf16(const void* x, void* out, size_t n, bool to_bf16, hipStream_t s);
+// Many f32 -> bf16 conversions (round to nearest even) in one launch.
+struct Bf16Copy {
+  const float* src;
+  void* dst;
+  size_t n;
+};
+void to_bf16_multi(const Bf16Copy* segs_host, int count, hipStream_t s);
 void fill(float* out, float v, size_t n, hipStream_t s);
 void fill_bytes0(void* out, size_t bytes, hipStream_t s);
 void fill_from_device(float* out, const float* v, size_t n, hipStream_t s);

@@ -251,6 +251,28 @@ __global__ __launch_bounds__(kBlock) void k_bf16_to_f32(const __bf16* __restrict
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = (float)x[i];
 }
 
+constexpr int kCvtMaxSegs = 64;
+constexpr size_t kCvtChunk = 2048;  // elements per workgroup
+struct CvtTable {
+  Bf16Copy seg[kCvtMaxSegs];
+  uint32_t first_chunk[kCvtMaxSegs + 1];
+  int count;
+};
+static_assert(sizeof(CvtTable) + 64 <= 4096, "the segment table travels in the 4 KB of kernel arguments");
+__global__ __launch_bounds__(kBlock) void k_to_bf16_multi(const CvtTable t) {
+  int lo = 0, hi = t.count - 1;  // the segment holding chunk blockIdx.x
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (t.first_chunk[mid] <= blockIdx.x) lo = mid;
+    else hi = mid - 1;
+  }
+  const Bf16Copy& sg = t.seg[lo];
+  const size_t first = (size_t)(blockIdx.x - t.first_chunk[lo]) * kCvtChunk;
+  const size_t end = first + kCvtChunk < sg.n ? first + kCvtChunk : sg.n;
+  __bf16* dst = static_cast<__bf16*>(sg.dst);
+  for (size_t i = first + threadIdx.x; i < end; i += blockDim.x) dst[i] = (__bf16)sg.src[i];
+}
+
 template <class F>
 void dispatch_binop(int op, F f) {
   switch (op) {
@@ -347,6 +369,24 @@ void convert_f32_bf16(const void* x, void* out, size_t n, bool to_bf16, hipStrea
   if (to_bf16) k_f32_to_bf16<<<ew_grid(n), kBlock, 0, s>>>(static_cast<const float*>(x), static_cast<__bf16*>(out), n);
   else k_bf16_to_f32<<<ew_grid(n), kBlock, 0, s>>>(static_cast<const __bf16*>(x), static_cast<float*>(out), n);
   post_launch("convert");
+}
+
+void to_bf16_multi(const Bf16Copy* segs_host, int count, hipStream_t s) {
+  for (int base = 0; base < count; base += kCvtMaxSegs) {
+    CvtTable t{};
+    t.count = count - base < kCvtMaxSegs ? count - base : kCvtMaxSegs;
+    size_t chunks = 0;
+    for (int i = 0; i < t.count; ++i) {
+      t.seg[i] = segs_host[base + i];
+      t.first_chunk[i] = (uint32_t)chunks;
+      chunks += (t.seg[i].n + kCvtChunk - 1) / kCvtChunk;
+    }
+    t.first_chunk[t.count] = (uint32_t)chunks;
+    if (chunks == 0) continue;
+    if (chunks > 0x7fffffffu) fail("malus: bf16 copies: too many elements");
+    k_to_bf16_multi<<<(unsigned)chunks, kBlock, 0, s>>>(t);
+    post_launch("to_bf16_multi");
+  }
 }
 
 void fill(float* out, float v, size_t n, hipStream_t s) {

@@ -13,6 +13,8 @@ namespace k {
 // variant whose bits 12..9 carry GemmLayouts::io (k_gemm_io.hip); null for
 // the combinations no caller uses.
 const void* gemm_io_kernel(int ti, int v);
+// The same for the instances with a bf16 weight as B (k_gemm_io_w.hip).
+const void* gemm_io_weight_kernel(int ti, int v);
 
 namespace {
 

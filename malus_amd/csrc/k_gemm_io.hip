@@ -58,6 +58,8 @@ const void* io_instance(int v) {
 }  // namespace
 
 const void* gemm_io_kernel(int ti, int v) {
+  // B in bf16 outside the weight-gradient forms: a weight's bf16 copy
+  if (((v >> 9) & kIoB16) && !(v & 8)) return gemm_io_weight_kernel(ti, v);
   switch (ti) {  // the host's tile table: 128x192, 128x128, 128x64, 64x128, 64x64
     case 0: return io_instance<2, 3>(v);
     case 1: return io_instance<2, 2>(v);

@@ -131,8 +131,10 @@ struct Gpt {
   const float* bc_dev = nullptr;
   int attn_mode = ATTN_AUTO;
   // Under autocast, the activations whose only readers are bf16 GEMMs are
-  // stored in bf16 (see block_forward).
+  // stored in bf16 (see block_forward), and the blocks' weight matrices get
+  // bf16 copies for the GEMMs (refresh_weight_copies); w16[i] is param i's.
   bool bf16_act = true;
+  std::vector<int64_t> w16;
   std::vector<int64_t> p, m, v;  // block l params at 8l..8l+7, then wte, wpe, ln_f, lm_head
   int64_t pos = 0;               // [B*T] i32 position ids
   int64_t attn_scale = 0;        // [1,1] 1/sqrt(hs) of the fused attention (built on first use)
@@ -140,6 +142,51 @@ struct Gpt {
   int np() const { return 8 * L + 4; }
   int64_t& top(int j) { return p[8 * L + j]; }
 };
+
+// The autocast storage policy applies (below): the fused forward with the
+// head-folded GEMMs, on shapes the bf16 kernels take.
+bool storage_policy(const Gpt& g) {
+  const size_t C = g.C, hs = C / g.H, N = (size_t)g.B * g.Tn;
+  return g.bf16_act && k::autocast_on() && g.fused_fwd && heads_foldable(g.B, g.Tn, g.H, hs) && C % 128 == 0 &&
+         C <= 512 && N % 8 == 0;
+}
+
+// Under the storage policy, bf16 copies of the blocks' weight matrices (q,
+// k, v, o, W1, W2) for the GEMMs that read them (forward products and the
+// dx products of the VJPs), refreshed in one launch at every forward: those
+// products round their operands to bf16 anyway, so every value is the same,
+// and the GEMMs move half the weight bytes.  A copy stands for its weight
+// only while the weight is unchanged (TensorBuffer::bf16_copy).
+void refresh_weight_copies(Gpt& g) {
+  if (!storage_policy(g)) return;
+  if (g.w16.size() != g.p.size()) g.w16.assign(g.p.size(), 0);
+  std::vector<k::Bf16Copy> segs;
+  std::vector<TensorBuffer*> ws;
+  for (int l = 0; l < g.L; ++l)
+    for (int j : {1, 2, 3, 4, 6, 7}) {
+      const size_t i = 8 * (size_t)l + j;
+      TensorBuffer* w = T(g.p[i]);
+      if (w->dtype != F32) continue;
+      if (!g.w16[i]) g.w16[i] = malus::H(alloc_tensor(BF16, w->shape, w->ndim));
+      TensorBuffer* c = T(g.w16[i]);
+      if (w->bf16_copy != c) {  // the weight's handle is new (updates that replace it)
+        retain(c);
+        if (w->bf16_copy) release(w->bf16_copy);
+        w->bf16_copy = c;
+      }
+      segs.push_back(k::Bf16Copy{w->f32(), c->data(), w->len});
+      ws.push_back(w);
+    }
+  if (segs.empty()) return;
+  k::to_bf16_multi(segs.data(), (int)segs.size(), stream());
+  const uint64_t seq = enqueue_mark("weights_bf16");
+  for (TensorBuffer* w : ws) {
+    TensorBuffer* c = w->bf16_copy;
+    c->write_seq = seq;
+    c->copy_of = w;
+    c->copy_seq = w->write_seq;
+  }
+}
 
 int64_t block_forward(Gpt& g, int l, int64_t x) {
   const size_t B = g.B, Tn = g.Tn, C = g.C, H = g.H, hs = C / H, N = B * Tn;
@@ -157,7 +204,7 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   // bytes.  h (the GELU VJP's input), the attention output (its VJP's
   // rowsum(dO * O) is f32 arithmetic), the residual stream, parameters,
   // gradients and optimizer state stay f32.
-  const bool bf_act = g.bf16_act && k::autocast_on() && fused_heads && C % 128 == 0 && C <= 512 && N % 8 == 0;
+  const bool bf_act = storage_policy(g);
   // nanogpt_modular.ml:47-68
   int64_t y1;
   int64_t xn1 = ln_scale(g.fused_fwd, x, P[0], &y1, bf_act);
@@ -319,6 +366,7 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
 
 // GPT.forward (nanogpt_modular.ml:75-91) + cross_entropy (lib.rs:2945-2972)
 int64_t gpt_forward_loss(Gpt& g, int64_t toks, int64_t targets, int64_t* logits_out) {
+  refresh_weight_copies(g);
   int64_t te, pe, x;
   TensorBuffer *wte = T(g.top(0)), *wpe = T(g.top(1)), *tk = T(toks), *ps = T(g.pos);
   if (g.fused_fwd && tk->dtype == I32 && ps->dtype == I32 && tk->ndim == 1 && tk->len == ps->len &&
@@ -519,6 +567,7 @@ void malus_gpt_free(void* gp) {
   auto* g = static_cast<Gpt*>(gp);
   if (!g) return;
   for (size_t i = 0; i < g->p.size(); ++i) rel({g->p[i], g->m[i], g->v[i]});
+  for (int64_t c : g->w16) rel({c});  // a weight handle still alive elsewhere keeps its own reference
   tensor_release(g->pos);
   tensor_release(g->attn_scale);
   delete g;

@@ -408,6 +408,7 @@ void release(TensorBuffer* t) {
          (unsigned long long)H(t));
   if (prev == 1) {
     tape_on_release(H(t));  // metal.rs:534: leaf registry cleanup first
+    if (t->bf16_copy) release(t->bf16_copy);
     Storage* st = t->st;
     if (--st->aliases == 0) {
       pool_free(st->ptr, st->bytes);

@@ -47,6 +47,15 @@ int gemm_io(const TensorBuffer* a, const TensorBuffer* b, const char* what) {
   return (a->dtype == BF16 ? k::kIoA16 : 0) | (b->dtype == BF16 ? k::kIoB16 : 0);
 }
 
+// The tensor a GEMM reads for operand t: under autocast, t's bf16 copy
+// when it holds t's current values (refreshed after t's last write); the
+// bf16 MFMA rounds t to those values anyway.
+const TensorBuffer* gemm_operand(const TensorBuffer* t) {
+  const TensorBuffer* c = t->bf16_copy;
+  if (c && k::autocast_on() && c->copy_of == t && c->copy_seq == t->write_seq) return c;
+  return t;
+}
+
 int64_t done(TensorBuffer* t, const char* name) {
   t->write_seq = enqueue_mark(name);
   return H(t);
@@ -203,8 +212,10 @@ TensorBuffer* as_i32_indices(TensorBuffer* idx, bool* owned) {
   fail("malus: index tensors must be Tensor<i32> (got dtype tag %d)", idx->dtype);
 }
 
-int64_t gemm_out(TensorBuffer* a, TensorBuffer* b, bool ta, bool tb, int batch, int M, int N, int K, long sA, long sB,
-                 const size_t* oshape, int ond, const TensorBuffer* addend = nullptr) {
+int64_t gemm_out(const TensorBuffer* a, const TensorBuffer* b, bool ta, bool tb, int batch, int M, int N, int K, long sA,
+                 long sB, const size_t* oshape, int ond, const TensorBuffer* addend = nullptr) {
+  a = gemm_operand(a);
+  b = gemm_operand(b);
   const int io = gemm_io(a, b, "matmul");
   TensorBuffer* c = alloc_tensor(F32, oshape, ond);
   if (addend && (addend->dtype != F32 || addend->len != c->len))
@@ -988,7 +999,7 @@ int64_t ln_affine_bwd_xw(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const
 // epilogue (nothing launched).  x may be bf16; ge_bf16 stores ge in bf16
 // (for a caller whose readers of ge are bf16 GEMMs); h stays f32.
 int64_t matmul_gelu_fwd(int64_t hx, int64_t hw, int64_t* ge_out, bool ge_bf16) {
-  TensorBuffer *x = T(hx), *w = T(hw);
+  const TensorBuffer *x = gemm_operand(T(hx)), *w = gemm_operand(T(hw));
   if (x->ndim != 2 || w->ndim != 2 || x->shape[1] != w->shape[0]) return 0;
   const int io = gemm_io(x, w, "matmul") | (ge_bf16 ? k::kIoE16 : 0);
   const size_t M = x->shape[0], K = x->shape[1], N = w->shape[1];
@@ -1012,20 +1023,20 @@ int64_t matmul_gelu_fwd(int64_t hx, int64_t hw, int64_t* ge_out, bool ge_bf16) {
 // out_bf16 stores dh in bf16 (no D) for a caller whose readers of dh are
 // bf16 GEMMs.
 int64_t gelu_matmul_bwd_h(int64_t hd, int64_t hw, int64_t hh, const TensorBuffer* D, bool out_bf16) {
-  TensorBuffer *d = T(hd), *w = T(hw), *h = T(hh);
+  const TensorBuffer *d = T(hd), *w = gemm_operand(T(hw)), *h = T(hh);
   const size_t N = w->shape[0], K = w->shape[1], M = d->len / K;
   if (h->len != M * N || d->len != M * K) fail("malus: gelu matmul VJP: dout %s, w %s, h %s", shape_str(d).c_str(),
                                                shape_str(w).c_str(), shape_str(h).c_str());
   if (D && (D->dtype != F32 || D->len != h->len))
     fail("malus: gelu matmul VJP accumulate: addend %s does not match %s", shape_str(D).c_str(), shape_str(h).c_str());
   need_f32(d, "gelu matmul VJP");
-  need_f32(w, "gelu matmul VJP");
   need_f32(h, "gelu matmul VJP");
+  const int io = gemm_io(d, w, "gelu matmul VJP") | (out_bf16 ? k::kIoC16 : 0);
   if (D && out_bf16) fail("malus: gelu matmul VJP: a bf16 result takes no addend");
   TensorBuffer* out = alloc_tensor(out_bf16 ? BF16 : F32, h->shape, h->ndim);
   KTimer* kt = ktimer_begin("gemm");
   if (!k::gemm_gelu(d->f32(), w->f32(), out->f32(), h->f32(), (int)M, (int)N, (int)K, true, true, stream(),
-                    D ? D->f32() : nullptr, out_bf16 ? k::kIoC16 : 0))
+                    D ? D->f32() : nullptr, io))
     fail("malus: gelu matmul VJP: no fused GEMM for %zux%zux%zu", M, N, K);
   ktimer_end(kt, 2.0 * M * N * K);
   return done(out, "gelu_matmul_bwd");
@@ -1078,9 +1089,11 @@ void check_addend(const TensorBuffer* D, const TensorBuffer* c) {
   if (D && (D->dtype != F32 || D->len != c->len))
     fail("malus: fused attention accumulate: addend %s does not match %s", shape_str(D).c_str(), shape_str(c).c_str());
 }
-int64_t mapped(TensorBuffer* a, TensorBuffer* b, TensorBuffer* c, bool ta, bool tb, int batch, int M, int N, int K,
-               const GemmLayouts& L, const TensorBuffer* D, const char* what) {
+int64_t mapped(const TensorBuffer* a, const TensorBuffer* b, TensorBuffer* c, bool ta, bool tb, int batch, int M, int N,
+               int K, const GemmLayouts& L, const TensorBuffer* D, const char* what) {
   check_addend(D, c);
+  a = gemm_operand(a);
+  b = gemm_operand(b);
   GemmLayouts Lio = L;
   Lio.io = gemm_io(a, b, what);
   KTimer* kt = ktimer_begin("gemm");
@@ -1137,13 +1150,14 @@ void head_proj_fwd3(int64_t hx, const int64_t* hw, size_t B, size_t T, size_t H,
   GemmLayouts L{dense_layout((long)x->shape[1], 0), dense_layout((long)C, 0), heads_as_rows(T, H, hs), (int)x->len,
                 (int)w0->len};
   L.ngroup = 3;
-  L.io = gemm_io(x, w0, "head_proj_fwd3") | (out_bf16 ? k::kIoC16 : 0);
+  const TensorBuffer* w[3] = {gemm_operand(w0), gemm_operand(T_(hw[1])), gemm_operand(T_(hw[2]))};
+  L.io = gemm_io(x, w[0], "head_proj_fwd3") | (out_bf16 ? k::kIoC16 : 0);
   TensorBuffer* o[3];
   for (int g = 0; g < 3; ++g) {
-    if (T_(hw[g])->len != w0->len || T_(hw[g])->dtype != w0->dtype) fail("malus: head_proj_fwd3: weights differ in shape");
+    if (w[g]->len != w0->len || w[g]->dtype != w[0]->dtype) fail("malus: head_proj_fwd3: weights differ in shape or dtype");
     o[g] = alloc_tensor(out_bf16 ? BF16 : F32, sh, 3);
     L.ga[g] = x->f32();
-    L.gb[g] = T_(hw[g])->f32();
+    L.gb[g] = w[g]->f32();
     L.gc[g] = o[g]->f32();
   }
   KTimer* kt = ktimer_begin("gemm");
@@ -1170,11 +1184,13 @@ int64_t head_proj_bwd_x3(const int64_t* hdq, const int64_t* hw, size_t B, size_t
   GemmLayouts L{heads_as_rows(T, H, hs), dense_layout((long)C, 0), dense_layout((long)Cin, 0), (int)T_(hdq[0])->len,
                 (int)w0->len};
   L.ngroup = 3;
-  L.io = gemm_io(T_(hdq[0]), w0, "head_proj_bwd_x3");
+  const TensorBuffer* w[3] = {gemm_operand(w0), gemm_operand(T_(hw[1])), gemm_operand(T_(hw[2]))};
+  L.io = gemm_io(T_(hdq[0]), w[0], "head_proj_bwd_x3");
   for (int g = 0; g < 3; ++g) {
-    if (T_(hdq[g])->dtype != T_(hdq[0])->dtype) fail("malus: head_proj_bwd_x3: gradients differ in dtype");
+    if (T_(hdq[g])->dtype != T_(hdq[0])->dtype || w[g]->dtype != w[0]->dtype)
+      fail("malus: head_proj_bwd_x3: gradients or weights differ in dtype");
     L.ga[g] = T_(hdq[g])->f32();
-    L.gb[g] = T_(hw[g])->f32();
+    L.gb[g] = w[g]->f32();
   }
   KTimer* kt = ktimer_begin("gemm");
   double flops = 0;

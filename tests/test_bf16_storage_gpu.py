@@ -74,7 +74,11 @@ GEMM_SHAPES = [(512, 384, 1536), (1008, 384, 1536), (528, 1536, 384), (4096, 384
 # name: (entry point, operands uploaded in bf16); a [M, K], b [K, N], d [M, N]
 FORMS = {
     "NN A16": ("tensor_matmul", "a"),               # C = a @ b
+    "NN B16": ("tensor_matmul", "b"),
+    "NN A16 B16": ("tensor_matmul", "ab"),
     "NT A16": ("malus_std_matmul_bwd_a", "d"),      # dA = d @ b^T
+    "NT B16": ("malus_std_matmul_bwd_a", "b"),
+    "NT A16 B16": ("malus_std_matmul_bwd_a", "db"),
     "TN A16": ("malus_std_matmul_bwd_b", "a"),      # dB = a^T @ d
     "TN A16 B16": ("malus_std_matmul_bwd_b", "ad"),
 }
@@ -136,8 +140,8 @@ def test_bf16_operands_the_kernels_cannot_take_are_errors(rt):
             h = rt.L.tensor_matmul(rt.bf16(rand(5, 7)), rt.tensor(rand(7, 3)))
             assert h == 0 and "LDS-DMA" in rt.last_error()
             rt.L.malus_clear_error()
-            # a bf16 B of the plain product has no instance
-            h = rt.L.tensor_matmul(rt.tensor(rand(64, 64)), rt.bf16(rand(64, 64)))
+            # a weight gradient from an f32 activation and a bf16 gradient has no instance
+            h = rt.L.malus_std_matmul_bwd_b(rt.tensor(rand(64, 64)), rt.tensor(rand(64, 64)), rt.bf16(rand(64, 64)))
             assert h == 0 and "bf16 storage mask" in rt.last_error()
             rt.L.malus_clear_error()
         # elementwise ops take f32 only
