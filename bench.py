@@ -527,8 +527,8 @@ def run_gpt(rt, a, cfg):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": ("bf16 GEMM and attention operands, f32 accumulation; the activations read only as bf16 operands "
-                  "stored in bf16 (layernorm-scale outputs, gelu(h), dh, q, k, v and their gradients), everything "
-                  "else f32 (autocast)")
+                  "stored in bf16 (layernorm-scale outputs, gelu(h), dh, q, k, v and their gradients) and bf16 "
+                  "copies of the block weights as GEMM operands; everything else f32 (autocast)")
                  if a.autocast and not a.f32_activations else
                  "bf16 GEMM operands, f32 accumulation and everything else f32 (autocast)" if a.autocast else "f32",
         "data": "synthetic int32 tokens i.i.d. uniform in [0,65), drawn on the device inside each timed step "
@@ -576,8 +576,8 @@ def main():
                          "fused VJPs and the fused optimizer off, composed attention, eager launches; reported "
                          "beside the headline, never in its place")
     ap.add_argument("--f32-activations", action="store_true",
-                    help="with --autocast: keep every activation in f32 (the same values; for comparison with the "
-                         "default bf16 storage of the activations only bf16 GEMMs read)")
+                    help="with --autocast: keep every activation and weight operand in f32 (the same values; for "
+                         "comparison with the default bf16 storage of what only bf16 products read)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemm-pass", action="store_true",
                     help="skip the event-timed eager GEMM pass after the headline steps (for a kernel trace of the "

@@ -356,8 +356,9 @@ void malus_gpt_set_fused_forward(void* g, int on);
  * docs/adr/0037-bf16-autocast.md:8).  1 (default): under malus_autocast the
  * activations read only as bf16 MFMA operands (the layernorm-scale outputs,
  * gelu(h), the GELU VJP's dh and, with flash attention, q, k, v and their
- * gradients) are stored in bf16; the step's values are the same as with 0
- * (f32 storage), in half the bytes. */
+ * gradients) are stored in bf16, and the GEMMs read bf16 copies of the block
+ * weights refreshed at each forward; the step's values are the same as with
+ * 0 (f32 storage), in half the bytes. */
 void malus_gpt_set_bf16_activations(void* g, int on);
 int64_t malus_gpt_forward_loss(void* g, int64_t toks, int64_t targets); /* nanogpt_modular.ml:75-91 + cross_entropy */
 int64_t malus_gpt_logits(void* g, int64_t toks);
