@@ -310,7 +310,8 @@ void permute(const float* x, float* out, int ndim, const size_t* in_shape, const
 
 // Operand addressing for gemm_mapped: element (i, j) of a stored matrix
 // (rows i, columns j) of batch b sits at  b-map(b) + r-map(i) + c-map(j)
-// floats past the operand's pointer, each map being
+// elements (floats, or bf16 for an operand GemmLayouts::io marks) past the
+// operand's pointer, each map being
 //   x -> (x / div) * s1 + (x % div) * s0     (div == 0: x * s0),
 // which covers dense row-major storage ({0, 0, ld} rows, {0, 0, 1} columns)
 // and the head-folded views of multi-head attention (a [B*T, H*hs] matrix
@@ -318,7 +319,7 @@ void permute(const float* x, float* out, int ndim, const size_t* in_shape, const
 // Offsets stay below 2^29 floats (2^31 bytes), so the fields are 32-bit.
 struct GemmMap { int div, s1, s0; };
 struct GemmLayout { GemmMap b, r, c; };
-// ext_a / ext_b: floats addressable past A / B (the whole allocation).
+// ext_a / ext_b: elements addressable past A / B (the whole allocation).
 // tri_a: every stored A matrix is square and lower-triangular, with exact
 // zeros above the diagonal (causal attention probabilities and their
 // gradients); a tile then skips the k slabs whose A values are all zero,

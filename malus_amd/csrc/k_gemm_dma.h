@@ -1,5 +1,5 @@
 // LDS-DMA GEMM kernels for gfx950 (v_mfma_f32_32x32x2_f32, and the bf16
-// MFMA under autocast), shared by k_gemm.hip and k_gemm_io.hip.
+// MFMA under autocast), shared by k_gemm.hip, k_gemm_io.hip and k_gemm_io_w.hip.
 #pragma once
 #include <type_traits>
 
@@ -98,7 +98,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const float* p, un
 }
 #endif
 
-// Element x of an index map (strides in floats); see GemmMap.  MAP = false
+// Element x of an index map (strides in elements of the stored type); see
+// GemmMap.  MAP = false
 // instances serve dense operands, whose maps are all x * s0.
 template <bool MAP>
 __device__ __forceinline__ int map_at(const GemmMap& f, int x) {
