@@ -210,3 +210,35 @@ def test_c5_bf16_activations_equal_f32_storage(rt):
     for i, (a, b) in enumerate(zip(runs[True][1], runs[False][1])):
         assert np.array_equal(bits(a), bits(b)), f"state tensor {i} differs"
     assert live[False] - live[True] >= 0.9 * 6 * (2 * n * 384 + n * 1536) * 2
+
+
+C4 = dict(V=65, T=64, C=128, H=4, L=4, B=32)
+
+
+@pytest.mark.parametrize("attention", [1, 2], ids=["flash", "rows"])
+def test_c4_bf16_activations_equal_f32_storage(rt, attention):
+    """The policy at C4 (head size 32) under both fused attentions: with the
+    row-register attention q, k, v stay f32 while the layernorm outputs,
+    gelu(h), dh and the weight copies are bf16 (the head-projection GEMMs then
+    take a bf16 A with an f32 C, and their dx a bf16 weight with f32 dq).
+    3 steps with the policy on equal the steps with it off, bit for bit."""
+    n = C4["B"] * C4["T"]
+    batches = [(O.rand_tokens((7 << 32) + 2 * n * k, n, C4["V"]), O.rand_tokens((7 << 32) + 2 * n * k + n, n, C4["V"]))
+               for k in range(3)]
+    runs = {}
+    with M.autocast():
+        for on in (True, False):
+            g = _make(rt, C4, on)
+            assert rt.L.malus_gpt_set_attention(g, attention) == 0
+            losses = []
+            for k, (x, y) in enumerate(batches):
+                hx, hy = rt.tensor(x), rt.tensor(y)
+                hl = rt.L.malus_gpt_step(g, hx, hy, k + 1)
+                losses.append(rt.numpy(hl)[0])
+                rt.free(hl, hx, hy)
+            runs[on] = (losses, _state(rt, g))
+            rt.L.malus_gpt_free(g)
+            rt.L.tape_reset()
+    assert runs[True][0] == runs[False][0]
+    for i, (a, b) in enumerate(zip(runs[True][1], runs[False][1])):
+        assert np.array_equal(bits(a), bits(b)), f"state tensor {i} differs"
