@@ -124,7 +124,7 @@ int64_t kernel_dispatch_v2(uint64_t kernel_id, const int64_t* handles, size_t ha
                            const void* uniforms, size_t uniforms_bytes); /* metal.rs:1944-2065 */
 
 /* ---- matmul, shapes, masks, RNG ----------------------------------------- */
-int64_t tensor_matmul(int64_t a, int64_t b);                            /* metal.rs:820-962 (FP32 MFMA) */
+int64_t tensor_matmul(int64_t a, int64_t b); /* metal.rs:820-962 (split bf16 products or FP32 MFMA: malus_gemm_set_f32_split) */
 int64_t tensor_reshape(int64_t h, const size_t* dims, size_t ndim);     /* metal.rs:1421-1435 */
 int64_t tensor_permute(int64_t h, const size_t* perm, size_t ndims);    /* metal.rs:1405-1417 */
 int64_t tensor_causal_mask(int64_t t);                                  /* metal.rs:1600-1612 */
@@ -217,6 +217,15 @@ int malus_gemm_set_tile(int tm, int tn);
 void malus_gemm_set_split(int target_blocks);
 /* Tuning: 0 keeps every GEMM on the register-staged path; 1 (default) allows the LDS-DMA path. */
 void malus_gemm_set_dma(int on);
+/* f32 GEMM arithmetic (no reference counterpart; the products of
+ * metal.rs:802-962): 1 (default) computes every f32 GEMM on the LDS-DMA
+ * kernels, and the fused attention kernels' products, as the sum of six
+ * exact bf16 piece products on the bf16 MFMA (each operand value split
+ * exactly into three bf16 pieces, f32 accumulation); 0 runs them on the
+ * FP32 MFMA.  The environment variable MALUS_F32_GEMM=fp32 sets 0 at
+ * start-up.  Returns the previous setting.  A captured graph keeps the
+ * arithmetic it was captured with. */
+int malus_gemm_set_f32_split(int on);
 /* The `with autocast:` scope of docs/adr/0037-bf16-autocast.md:5-12 (the
  * reference fixes the policy, not yet an entry point): while on, every GEMM
  * (tensor_matmul, the model's projections and their VJPs) rounds its f32

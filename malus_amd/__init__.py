@@ -115,6 +115,7 @@ SIGNATURES = {
     "malus_gemm_set_tile": (C.c_int, [C.c_int, C.c_int]),
     "malus_gemm_set_split": (None, [C.c_int]),
     "malus_gemm_set_dma": (None, [C.c_int]),
+    "malus_gemm_set_f32_split": (C.c_int, [C.c_int]),
     "malus_autocast": (C.c_int, [C.c_int]),
     "malus_std_attn_scores_softmax": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "malus_std_attn_scores_bwd": (_i64, [_i64, _i64, _i64, _i64, _i32]),

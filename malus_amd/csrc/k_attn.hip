@@ -30,6 +30,7 @@
 // expf(-1e9 - max) = +0 exactly and their partial sums are +0, which is what
 // the kernel stores and adds, and their products with V add exact zeros.
 #include "common.h"
+#include "k_split.h"
 
 namespace malus {
 namespace k {
@@ -107,30 +108,47 @@ __device__ __forceinline__ void store_tile(const v16f (&o)[NN], float* __restric
 // with A in the key-tile registers of the layout above and M staged in LDS
 // (padded rows).  The slabs run in key order, as the GEMM's do.  out/D of
 // row i, column d sit at i * ld + d from the head's base.
-template <int NT, int HS>
+template <int NT, int HS, bool X3>
 __device__ __forceinline__ void product_from_registers(const v16f (&a)[NT], int live, const float* Ms, int i0,
                                                        float* __restrict__ out, const float* __restrict__ D, int ld) {
   constexpr int LD = HS + 4, NN = HS / 32;
   const int lane = threadIdx.x & 63, x = lane & 31, lk = lane >> 5;
-  v16f o[NN];
+  v16f o[1][NN];
 #pragma unroll
-  for (int n = 0; n < NN; ++n) o[n] = v16f{0};
+  for (int n = 0; n < NN; ++n) o[0][n] = v16f{0};
   __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     if (t < live) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (X3) {  // slab 2 t + h: keys 32 t + 16 h + 8 lk + s
+          float af[8], bf[NN][8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const float* mr = Ms + (32 * t + 16 * h + 8 * lk + s) * LD + x;
+          for (int s = 0; s < 8; ++s) {
+            af[s] = a[t][8 * h + s];
+            const float* mr = Ms + (32 * t + 16 * h + 8 * lk + s) * LD + x;
 #pragma unroll
-          for (int n = 0; n < NN; ++n) o[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t][8 * h + s], mr[32 * n], o[n], 0, 0, 0);
+            for (int n = 0; n < NN; ++n) bf[n][s] = mr[32 * n];
+          }
+          Split3 sa[1] = {split3(af)}, sb[NN];
+#pragma unroll
+          for (int n = 0; n < NN; ++n) sb[n] = split3(bf[n]);
+          x3_slab<false, 1, NN>(sa, sb, o);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 8; ++s) {
+            const float* mr = Ms + (32 * t + 16 * h + 8 * lk + s) * LD + x;
+#pragma unroll
+            for (int n = 0; n < NN; ++n)
+              o[0][n] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[t][8 * h + s], mr[32 * n], o[0][n], 0, 0, 0);
+          }
         }
+      }
     }
   }
   __builtin_amdgcn_s_setprio(0);
-  store_tile<NN>(o, out, D, [&](int n, int r) { return (size_t)(i0 + 8 * (r >> 2) + 4 * lk + (r & 3)) * ld + 32 * n + x; });
+  store_tile<NN>(o[0], out, D, [&](int n, int r) { return (size_t)(i0 + 8 * (r >> 2) + 4 * lk + (r & 3)) * ld + 32 * n + x; });
 }
 
 // Stage one head's [TT, HS] rows that sit ld floats apart (the [B*T, C]
@@ -161,7 +179,10 @@ __device__ __forceinline__ void stage_rows(const float* __restrict__ src_head, i
 // (P = 0 above the diagonal), and the GEMM either skips them too or adds
 // those zero products to a +0 accumulator.  A's slab pairs are loaded two
 // pairs ahead of their MFMAs.  out/D rows are HS floats apart.
-template <int TT, int HS, bool CAUSAL>
+// SWAP (split products): the composed ops form this product with the
+// operands in the other roles (dK: the VJP of Q @ Kt with respect to Kt is
+// Q^T @ dS, then permuted), so the piece products run in that GEMM's order.
+template <int TT, int HS, bool CAUSAL, bool X3, bool SWAP>
 __device__ __forceinline__ void transposed_product(const float* __restrict__ Ah, int j, const float* Ms,
                                                    float* __restrict__ out, const float* __restrict__ D) {
   constexpr int LD = HS + 4, NN = HS / 32, NSL = TT / 16;
@@ -174,9 +195,9 @@ __device__ __forceinline__ void transposed_product(const float* __restrict__ Ah,
 #pragma unroll
       for (int s = 0; s < 8; ++s) r[8 * u + s] = ap[(size_t)(16 * (sl + u) + s) * TT];
   };
-  v16f o[NN];
+  v16f o[1][NN];
 #pragma unroll
-  for (int n = 0; n < NN; ++n) o[n] = v16f{0};
+  for (int n = 0; n < NN; ++n) o[0][n] = v16f{0};
   constexpr int PD = 2;  // slab pairs loaded ahead of their MFMAs (one ahead measured 1.5 % slower)
   float a[PD + 1][16];
 #pragma unroll
@@ -191,20 +212,37 @@ __device__ __forceinline__ void transposed_product(const float* __restrict__ Ah,
     if (sl + 2 * PD < NSL) load(sl + 2 * PD, a[PD]);
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < 2; ++u) {
+      if constexpr (X3) {  // slab sl + u: queries 16 (sl + u) + 8 lk + s
+        float af[8], bf[NN][8];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const float* mr = Ms + (16 * (sl + u) + 8 * lk + s) * LD + x;
+        for (int s = 0; s < 8; ++s) {
+          af[s] = a[0][8 * u + s];
+          const float* mr = Ms + (16 * (sl + u) + 8 * lk + s) * LD + x;
 #pragma unroll
-        for (int n = 0; n < NN; ++n) o[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0][8 * u + s], mr[32 * n], o[n], 0, 0, 0);
+          for (int n = 0; n < NN; ++n) bf[n][s] = mr[32 * n];
+        }
+        Split3 sa[1] = {split3(af)}, sb[NN];
+#pragma unroll
+        for (int n = 0; n < NN; ++n) sb[n] = split3(bf[n]);
+        x3_slab<SWAP, 1, NN>(sa, sb, o);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const float* mr = Ms + (16 * (sl + u) + 8 * lk + s) * LD + x;
+#pragma unroll
+          for (int n = 0; n < NN; ++n)
+            o[0][n] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0][8 * u + s], mr[32 * n], o[0][n], 0, 0, 0);
+        }
       }
+    }
     __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int d = 0; d < PD; ++d)
 #pragma unroll
       for (int e = 0; e < 16; ++e) a[d][e] = a[d + 1][e];
   }
-  store_tile<NN>(o, out, D, [&](int n, int r) { return (size_t)(32 * j + 8 * (r >> 2) + 4 * lk + (r & 3)) * HS + 32 * n + x; });
+  store_tile<NN>(o[0], out, D, [&](int n, int r) { return (size_t)(32 * j + 8 * (r >> 2) + 4 * lk + (r & 3)) * HS + 32 * n + x; });
 }
 
 // Query tiles are dealt to the waves in pairs (p, NT-1-p): wave w runs both
@@ -219,7 +257,7 @@ __device__ __forceinline__ int pair_tile(int w, int which) {
 // One wave's query tile qt (rows 32 qt ..): S^T = K Q^T from K staged in LDS
 // (rows in key_row order), scale, mask, the row softmax, and the store of the
 // P rows.  Leaves P in acc (zeros in the skipped key tiles).
-template <int TT, int HS, bool CAUSAL>
+template <int TT, int HS, bool CAUSAL, bool X3>
 __device__ __forceinline__ void softmax_tile(const float* __restrict__ Qh, const float* Ks, const float* __restrict__ scale,
                                              const float* __restrict__ mask, float* __restrict__ Ph, int qt,
                                              v16f (&acc)[TT / 32], bool full) {
@@ -247,11 +285,18 @@ __device__ __forceinline__ void softmax_tile(const float* __restrict__ Qh, const
       for (int kb = 0; kb < NKB; ++kb) {
         const v4f a = *reinterpret_cast<const v4f*>(kr + 16 * kb);
         const v4f b = *reinterpret_cast<const v4f*>(kr + 16 * kb + 4);
+        if constexpr (X3) {  // S^T = K Q^T: the composed GEMM's operands swapped
+          const float af[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+          const float bf[8] = {qv[2 * kb][0], qv[2 * kb][1], qv[2 * kb][2], qv[2 * kb][3],
+                               qv[2 * kb + 1][0], qv[2 * kb + 1][1], qv[2 * kb + 1][2], qv[2 * kb + 1][3]};
+          acc[t] = x3_one<true>(split3(af), split3(bf), acc[t]);
+        } else {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], qv[2 * kb][s], acc[t], 0, 0, 0);
+          for (int s = 0; s < 4; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], qv[2 * kb][s], acc[t], 0, 0, 0);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[s], qv[2 * kb + 1][s], acc[t], 0, 0, 0);
+          for (int s = 0; s < 4; ++s)
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[s], qv[2 * kb + 1][s], acc[t], 0, 0, 0);
+        }
       }
     }
   }
@@ -350,7 +395,7 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ Xh, int qt, 
 // first one's P goes to memory, the second stays in registers), then, with V
 // staged where K was, P @ V for the second tile from the registers and for
 // the first from its reloaded rows.
-template <int TT, int HS, bool CAUSAL, bool PV>
+template <int TT, int HS, bool CAUSAL, bool PV, bool X3>
 __global__ __launch_bounds__(256, 2) void k_attn_fwd(const float* __restrict__ Q, const float* __restrict__ Kh,
                                                     const float* __restrict__ V, const float* __restrict__ scale,
                                                     const float* __restrict__ mask, float* __restrict__ P,
@@ -370,8 +415,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const float* __restrict__ Q
   __syncthreads();
   v16f acc[NT];
   if (active) {
-    softmax_tile<TT, HS, CAUSAL>(Q + head, S, scale, mask, Ph, qa, acc, full);
-    softmax_tile<TT, HS, CAUSAL>(Q + head, S, scale, mask, Ph, qb, acc, full);
+    softmax_tile<TT, HS, CAUSAL, X3>(Q + head, S, scale, mask, Ph, qa, acc, full);
+    softmax_tile<TT, HS, CAUSAL, X3>(Q + head, S, scale, mask, Ph, qb, acc, full);
   }
   if constexpr (PV) {
     __syncthreads();  // every wave is done with K
@@ -379,24 +424,33 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd(const float* __restrict__ Q
     __syncthreads();
     if (active) {
       float* Oh = O + (size_t)(bh / H) * TT * ldo + (size_t)(bh % H) * HS;
-      product_from_registers<NT, HS>(acc, CAUSAL ? qb + 1 : NT, S, 32 * qb, Oh, nullptr, ldo);
+      product_from_registers<NT, HS, X3>(acc, CAUSAL ? qb + 1 : NT, S, 32 * qb, Oh, nullptr, ldo);
       load_tile<TT>(Ph, qa, CAUSAL ? qa + 1 : NT, acc);
-      product_from_registers<NT, HS>(acc, CAUSAL ? qa + 1 : NT, S, 32 * qa, Oh, nullptr, ldo);
+      product_from_registers<NT, HS, X3>(acc, CAUSAL ? qa + 1 : NT, S, 32 * qa, Oh, nullptr, ldo);
     }
   }
 }
 
+template <int TT, int HS, bool X3>
+void launch_prec(const float* Q, const float* K, const float* V, const float* scale, const float* mask, float* P,
+                 float* O, int ldo, int H, int bh, bool causal, bool full, hipStream_t s) {
+  const dim3 grid(1, (unsigned)bh);  // one workgroup per head
+  if (O) {
+    if (causal) k_attn_fwd<TT, HS, true, true, X3><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, full);
+    else k_attn_fwd<TT, HS, false, true, X3><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, true);
+  } else {
+    if (causal) k_attn_fwd<TT, HS, true, false, X3><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, full);
+    else k_attn_fwd<TT, HS, false, false, X3><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, true);
+  }
+}
+
+// The products run as the GEMMs run theirs (gemm_f32_split), so the fused
+// kernels keep the composed ops' bits.
 template <int TT, int HS>
 void launch(const float* Q, const float* K, const float* V, const float* scale, const float* mask, float* P, float* O,
             int ldo, int H, int bh, bool causal, bool full, hipStream_t s) {
-  const dim3 grid(1, (unsigned)bh);  // one workgroup per head
-  if (O) {
-    if (causal) k_attn_fwd<TT, HS, true, true><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, full);
-    else k_attn_fwd<TT, HS, false, true><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, true);
-  } else {
-    if (causal) k_attn_fwd<TT, HS, true, false><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, full);
-    else k_attn_fwd<TT, HS, false, false><<<grid, 256, 0, s>>>(Q, K, V, scale, mask, P, O, ldo, H, true);
-  }
+  if (gemm_f32_split()) launch_prec<TT, HS, true>(Q, K, V, scale, mask, P, O, ldo, H, bh, causal, full, s);
+  else launch_prec<TT, HS, false>(Q, K, V, scale, mask, P, O, ldo, H, bh, causal, full, s);
 }
 
 // Zero the 32 x 32 tiles of P [bh, TT, TT] wholly above the diagonal: one
@@ -413,7 +467,7 @@ __global__ __launch_bounds__(256) void k_attn_zero_upper(float* __restrict__ P, 
 // One wave's query tile qt of the scores backward: dP^T = V dO^T from V
 // staged in LDS, dS = P * (dP - sum(dP * P)) * scale, and the store of the dS
 // rows.  Leaves dS in acc.
-template <int TT, int HS, bool CAUSAL>
+template <int TT, int HS, bool CAUSAL, bool X3>
 __device__ __forceinline__ void dscores_tile(const float* __restrict__ dOh, int ldo, const float* Vs,
                                              const float* __restrict__ Ph, const float* __restrict__ scale,
                                              float* __restrict__ dSh, int qt, v16f (&acc)[TT / 32], bool full) {
@@ -439,11 +493,18 @@ __device__ __forceinline__ void dscores_tile(const float* __restrict__ dOh, int 
       for (int kb = 0; kb < NKB; ++kb) {
         const v4f a = *reinterpret_cast<const v4f*>(vr + 16 * kb);
         const v4f b = *reinterpret_cast<const v4f*>(vr + 16 * kb + 4);
+        if constexpr (X3) {  // dP^T = V dO^T: the composed GEMM's operands swapped
+          const float af[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+          const float bf[8] = {ov[2 * kb][0], ov[2 * kb][1], ov[2 * kb][2], ov[2 * kb][3],
+                               ov[2 * kb + 1][0], ov[2 * kb + 1][1], ov[2 * kb + 1][2], ov[2 * kb + 1][3]};
+          acc[t] = x3_one<true>(split3(af), split3(bf), acc[t]);
+        } else {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], ov[2 * kb][s], acc[t], 0, 0, 0);
+          for (int s = 0; s < 4; ++s) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], ov[2 * kb][s], acc[t], 0, 0, 0);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[s], ov[2 * kb + 1][s], acc[t], 0, 0, 0);
+          for (int s = 0; s < 4; ++s)
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[s], ov[2 * kb + 1][s], acc[t], 0, 0, 0);
+        }
       }
     }
   }
@@ -513,7 +574,7 @@ __device__ __forceinline__ void dscores_tile(const float* __restrict__ dOh, int 
 // each wave taking the key tiles of its pair (the same balance as the query
 // tiles: under a causal mask key tile j meets the NT - j query tiles from j
 // on).  The dS rows other waves stored are read back after a barrier.
-template <int TT, int HS, bool CAUSAL, bool DQ, bool KV>
+template <int TT, int HS, bool CAUSAL, bool DQ, bool KV, bool X3>
 __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ dO, int ldo, int H,
                                                     const float* __restrict__ V, const float* __restrict__ P,
                                                     const float* __restrict__ scale, float* __restrict__ dS,
@@ -536,8 +597,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ d
   __syncthreads();
   v16f acc[NT];
   if (active) {
-    dscores_tile<TT, HS, CAUSAL>(dOh, ldo, S, Ph, scale, dSh, qa, acc, full);
-    dscores_tile<TT, HS, CAUSAL>(dOh, ldo, S, Ph, scale, dSh, qb, acc, full);
+    dscores_tile<TT, HS, CAUSAL, X3>(dOh, ldo, S, Ph, scale, dSh, qa, acc, full);
+    dscores_tile<TT, HS, CAUSAL, X3>(dOh, ldo, S, Ph, scale, dSh, qb, acc, full);
   }
   if constexpr (DQ) {
     __syncthreads();  // every wave is done with V
@@ -545,9 +606,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ d
     __syncthreads();
     if (active) {
       const float* Dh = Dq ? Dq + head : nullptr;
-      product_from_registers<NT, HS>(acc, CAUSAL ? qb + 1 : NT, S, 32 * qb, dQ + head, Dh, HS);
+      product_from_registers<NT, HS, X3>(acc, CAUSAL ? qb + 1 : NT, S, 32 * qb, dQ + head, Dh, HS);
       load_tile<TT>(dSh, qa, CAUSAL ? qa + 1 : NT, acc);
-      product_from_registers<NT, HS>(acc, CAUSAL ? qa + 1 : NT, S, 32 * qa, dQ + head, Dh, HS);
+      product_from_registers<NT, HS, X3>(acc, CAUSAL ? qa + 1 : NT, S, 32 * qa, dQ + head, Dh, HS);
     }
   }
   if constexpr (KV) {
@@ -556,17 +617,41 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd(const float* __restrict__ d
     __syncthreads();
     if (active) {
       const float* Dv = kv.Dv ? kv.Dv + head : nullptr;
-      transposed_product<TT, HS, CAUSAL>(Ph, qa, S, kv.dV + head, Dv);
-      transposed_product<TT, HS, CAUSAL>(Ph, qb, S, kv.dV + head, Dv);
+      transposed_product<TT, HS, CAUSAL, X3, false>(Ph, qa, S, kv.dV + head, Dv);  // P^T @ dO
+      transposed_product<TT, HS, CAUSAL, X3, false>(Ph, qb, S, kv.dV + head, Dv);
     }
     __syncthreads();  // every wave is done with dO
     stage_head<TT, HS>(kv.Q + head, S);
     __syncthreads();
     if (active) {
       const float* Dk = kv.Dk ? kv.Dk + head : nullptr;
-      transposed_product<TT, HS, CAUSAL>(dSh, qa, S, kv.dK + head, Dk);
-      transposed_product<TT, HS, CAUSAL>(dSh, qb, S, kv.dK + head, Dk);
+      transposed_product<TT, HS, CAUSAL, X3, true>(dSh, qa, S, kv.dK + head, Dk);  // (Q^T @ dS)^T
+      transposed_product<TT, HS, CAUSAL, X3, true>(dSh, qb, S, kv.dK + head, Dk);
     }
+  }
+}
+
+template <int TT, int HS, bool X3>
+void launch_bwd_prec(const float* dO, int ldo, int H, const float* V, const float* P, const float* scale, float* dS,
+                     const float* K, float* dQ, const float* Dq, int bh, bool causal, const AttnKV* kv, bool full,
+                     hipStream_t s) {
+  const dim3 grid(1, (unsigned)bh);  // one workgroup per head
+  const AttnKV a = kv ? *kv : AttnKV{};
+  if (kv) {
+    if (causal)
+      k_attn_bwd<TT, HS, true, true, true, X3><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, full);
+    else
+      k_attn_bwd<TT, HS, false, true, true, X3><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, true);
+  } else if (dQ) {
+    if (causal)
+      k_attn_bwd<TT, HS, true, true, false, X3><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, full);
+    else
+      k_attn_bwd<TT, HS, false, true, false, X3><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, true);
+  } else {
+    if (causal)
+      k_attn_bwd<TT, HS, true, false, false, X3><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, full);
+    else
+      k_attn_bwd<TT, HS, false, false, false, X3><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, true);
   }
 }
 
@@ -574,18 +659,10 @@ template <int TT, int HS>
 void launch_bwd(const float* dO, int ldo, int H, const float* V, const float* P, const float* scale, float* dS,
                 const float* K, float* dQ, const float* Dq, int bh, bool causal, const AttnKV* kv, bool full,
                 hipStream_t s) {
-  const dim3 grid(1, (unsigned)bh);  // one workgroup per head
-  const AttnKV a = kv ? *kv : AttnKV{};
-  if (kv) {
-    if (causal) k_attn_bwd<TT, HS, true, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, full);
-    else k_attn_bwd<TT, HS, false, true, true><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, true);
-  } else if (dQ) {
-    if (causal) k_attn_bwd<TT, HS, true, true, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, full);
-    else k_attn_bwd<TT, HS, false, true, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, true);
-  } else {
-    if (causal) k_attn_bwd<TT, HS, true, false, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, full);
-    else k_attn_bwd<TT, HS, false, false, false><<<grid, 256, 0, s>>>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, a, true);
-  }
+  if (gemm_f32_split())
+    launch_bwd_prec<TT, HS, true>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, bh, causal, kv, full, s);
+  else
+    launch_bwd_prec<TT, HS, false>(dO, ldo, H, V, P, scale, dS, K, dQ, Dq, bh, causal, kv, full, s);
 }
 
 }  // namespace

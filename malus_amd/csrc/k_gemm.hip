@@ -264,24 +264,14 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 // bit 4 = LDS-DMA path, bits 3..0 = transA, transB, vecA, vecB.
 constexpr int kVarBf16 = 256;
 constexpr int kVarIoShift = 9;
-constexpr int kVarCount = 16 << kVarIoShift;
+constexpr int kVarX3 = 1 << 13;  // f32 product as split bf16 pieces (LDS-DMA kernels)
+constexpr int kVarCount = 1 << 14;
 inline int variant(bool ta, bool tb, bool va, bool vb, bool dma) {
   return (dma << 4) | (ta << 3) | (tb << 2) | (va << 1) | (int)vb;
 }
 
 template <int TM, int TN, bool TA, bool TB, bool BF>
-const void* kernel_of(int v) {
-  if (v & 128) {  // grouped accumulation: mapped NT (the head projections' dA)
-    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, true, 3, BF>);
-    return nullptr;
-  }
-  if (v & 64) {  // GELU epilogues: dense NN (forward) and NT (the VJP's dA)
-    if constexpr (!TA && !TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, false, false, 1, BF>);
-    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, false, 2, BF>);
-    return nullptr;
-  }
-  if (v & 32) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, true, 0, BF>);
-  if (v & 16) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, false, 0, BF>);
+const void* kernel_of_reg(int v) {
   const bool va = v & 2, vb = v & 1;
   if (va && vb) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, true, BF>);
   if (va) return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, true, false, BF>);
@@ -289,29 +279,50 @@ const void* kernel_of(int v) {
   return reinterpret_cast<const void*>(&k_sgemm<TM, TN, TA, TB, false, false, BF>);
 }
 
-template <int TM, int TN, bool BF>
-const void* kernel_of_layout(int v) {
-  const bool ta = v & 8, tb = v & 4;
-  if (!ta && !tb) return kernel_of<TM, TN, false, false, BF>(v);
-  if (!ta && tb) return kernel_of<TM, TN, false, true, BF>(v);
-  if (ta && !tb) return kernel_of<TM, TN, true, false, BF>(v);
-  return kernel_of<TM, TN, true, true, BF>(v);
+// P: 0 f32 MFMA, 1 bf16 MFMA (autocast), 2 the f32 product as split bf16
+// pieces (LDS-DMA kernels; the register-staged ones stay on the f32 MFMA)
+template <int TM, int TN, bool TA, bool TB, int P>
+const void* kernel_of(int v) {
+  constexpr bool BF = P != 0, X3 = P == 2;
+  if (v & 128) {  // grouped accumulation: mapped NT (the head projections' dA)
+    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, true, 3, BF, 0, X3>);
+    return nullptr;
+  }
+  if (v & 64) {  // GELU epilogues: dense NN (forward) and NT (the VJP's dA)
+    if constexpr (!TA && !TB)
+      return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, false, false, 1, BF, 0, X3>);
+    if constexpr (!TA && TB) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, false, true, false, 2, BF, 0, X3>);
+    return nullptr;
+  }
+  if (v & 32) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, true, 0, BF, 0, X3>);
+  if (v & 16) return reinterpret_cast<const void*>(&k_sgemm_dma<TM, TN, TA, TB, false, 0, BF, 0, X3>);
+  return kernel_of_reg<TM, TN, TA, TB, P == 1>(v);
 }
 
-template <bool BF>
+template <int TM, int TN, int P>
+const void* kernel_of_layout(int v) {
+  const bool ta = v & 8, tb = v & 4;
+  if (!ta && !tb) return kernel_of<TM, TN, false, false, P>(v);
+  if (!ta && tb) return kernel_of<TM, TN, false, true, P>(v);
+  if (ta && !tb) return kernel_of<TM, TN, true, false, P>(v);
+  return kernel_of<TM, TN, true, true, P>(v);
+}
+
+template <int P>
 const void* kernel_for_prec(int ti, int v) {
   switch (ti) {
-    case 0: return kernel_of_layout<2, 3, BF>(v);
-    case 1: return kernel_of_layout<2, 2, BF>(v);
-    case 2: return kernel_of_layout<2, 1, BF>(v);
-    case 3: return kernel_of_layout<1, 2, BF>(v);
-    default: return kernel_of_layout<1, 1, BF>(v);
+    case 0: return kernel_of_layout<2, 3, P>(v);
+    case 1: return kernel_of_layout<2, 2, P>(v);
+    case 2: return kernel_of_layout<2, 1, P>(v);
+    case 3: return kernel_of_layout<1, 2, P>(v);
+    default: return kernel_of_layout<1, 1, P>(v);
   }
 }
 
 const void* kernel_for(int ti, int v) {
-  if (v >> kVarIoShift) return gemm_io_kernel(ti, v);
-  return (v & kVarBf16) ? kernel_for_prec<true>(ti, v) : kernel_for_prec<false>(ti, v);
+  if ((v >> kVarIoShift) & 15) return gemm_io_kernel(ti, v);
+  if (v & kVarX3) return kernel_for_prec<2>(ti, v);
+  return (v & kVarBf16) ? kernel_for_prec<1>(ti, v) : kernel_for_prec<0>(ti, v);
 }
 
 // Co-resident workgroups per CU of each kernel variant (VGPR and LDS
@@ -348,6 +359,16 @@ int g_forced_tile = -2;    // -2: read MALUS_GEMM_TILE once; -1: automatic
 bool g_autocast = false;   // GEMM products in bf16 with f32 accumulation (autocast scope)
 int g_split_target = 0;    // workgroups a split-K launch aims for; 0: model
 bool g_allow_dma = true;   // LDS-DMA path where the shape allows it
+int g_f32_x3 = -1;         // f32 GEMMs as split bf16 products; -1: read MALUS_F32_GEMM once
+
+// Default on; MALUS_F32_GEMM=fp32 starts the process on the FP32 MFMA.
+bool f32_x3() {
+  if (g_f32_x3 < 0) {
+    const char* e = getenv("MALUS_F32_GEMM");
+    g_f32_x3 = e && !strcmp(e, "fp32") ? 0 : 1;
+  }
+  return g_f32_x3 == 1;
+}
 
 // Pick the tile and the K split with the smallest modelled time: the
 // busiest CU's MFMA work (256 CUs at 75 % of 157.3 TFLOP/s, scaled by the
@@ -356,8 +377,11 @@ bool g_allow_dma = true;   // LDS-DMA path where the shape allows it
 // GEMMs, K = tokens) split K so the grid fills the chip's workgroup slots.
 // tri: A lower-triangular (GemmLayouts::tri_a); a tile row then runs on
 // average (n + 1) / (2 n) of K for n tile rows, which favours short tiles.
-// bf: the launch runs on the bf16 MFMA (autocast, or bf16-stored operands).
-Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false, int only_tile = -1, bool bf = false) {
+// bf: the launch runs on the bf16 MFMA (autocast, or bf16-stored operands);
+// x3: the f32 product as split bf16 pieces (LDS-DMA kernels); groups: the
+// products one grouped launch runs side by side.
+Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false, int only_tile = -1, bool bf = false,
+               bool x3 = false, int groups = 1) {
   if (g_forced_tile == -2) {  // MALUS_GEMM_TILE=TMxTN pins a tile (tuning sweeps)
     g_forced_tile = -1;
     if (const char* e = getenv("MALUS_GEMM_TILE"))
@@ -378,8 +402,24 @@ Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false, int only
   // time, and the 128x192 tile (more MFMA work per staged byte) with the
   // cost model's split measured 10-20 % faster on the same shapes.
   const bool wgrad = (v & 16) && (v & 8) && batch == 1 && K >= 4096 && g_forced_tile < 0 && g_split_target == 0;
-  const bool wgrad_bf = wgrad && (g_autocast || bf);
-  if (wgrad_bf) only_tile = 0;  // kTiles[0] = 128x192
+  // The split f32 product (six bf16 MFMAs per staged f32 slab) is bound by
+  // moving f32 operands through L2 and LDS, so wider tiles (fewer staged
+  // bytes per product) pay where the grid still fills the chip.  Per call
+  // in the C5 step (kernel trace, 128x64 against the wider tile): the three
+  // grouped q/k/v weight gradients 124 -> 114 us on 128x128 with the cost
+  // model's split, and the K = 1536, N = 384 products (fc2, fc1's dX)
+  // 141-148 -> 137-141 us on 128x128 with a split of 2.  The single 384x384
+  // weight gradient (41 against 53 us), the 1536-wide ones and the GELU VJP
+  // (160 against 226 us: the wider tiles lose its epilogue prefetch) keep
+  // the f32 plan; the GELU forward takes 128x192 (153 -> 135 us) from the
+  // caller.
+  const bool wgrad_bf = wgrad && (g_autocast || bf || (x3 && groups > 1));
+  if (wgrad_bf) only_tile = x3 && !g_autocast && !bf ? 1 : 0;  // kTiles[0] = 128x192, kTiles[1] = 128x128
+  if (x3 && !wgrad && (v & 16) && !(v & 64) && only_tile < 0 && g_forced_tile < 0 && batch == 1 && K >= 1024)
+    only_tile = 1;
+  // the occupancy the cost model sees: the split kernels' own for the wide
+  // tiles picked above (it sets their K split), else the f32 kernels'
+  const int occ_v = x3 && only_tile >= 0 ? (v & ~64) | kVarX3 : v & ~64;
   for (int ti = 0; ti < kNumTiles; ++ti) {
     if (g_forced_tile >= 0 && ti != g_forced_tile) continue;
     if (only_tile >= 0 && g_forced_tile < 0 && ti != only_tile) continue;
@@ -388,7 +428,7 @@ Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false, int only
         !((kTiles[ti].tm == 2 && kTiles[ti].tn == 1) || (kTiles[ti].tm == 1 && kTiles[ti].tn == 2)))
       continue;
     const long tiles = (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch;
-    const int occ = occupancy(ti, v);
+    const int occ = occupancy(ti, occ_v);
     int cand[3] = {1, 1, 1};
     if (batch == 1 && K >= 1024) {
       const int max_split = K / 512;  // >= 32 K steps per workgroup amortize its prologue and partial tile
@@ -462,15 +502,16 @@ double launch_dma(const float* A, const float* B, float* C, int batch, int M, in
   // take the plan of the autocast GEMM on f32 copies of them, so the sums
   // run in the same order
   const int v = variant(transA, transB, false, false, true);
-  const bool bf = g_autocast || L.io;
-  const int vb = (epi ? v | 64 : mapped ? v | 32 : v) | (bf ? kVarBf16 : 0) | (L.io << kVarIoShift);
+  const bool bf = g_autocast || L.io, x3 = !bf && f32_x3();
+  const int vb = (epi ? v | 64 : mapped ? v | 32 : v) | (bf ? kVarBf16 : 0) | (L.io << kVarIoShift) | (x3 ? kVarX3 : 0);
   const void* fn = kernel_for(0, vb);
   if (!fn) fail("malus: gemm: no kernel for epilogue %d with transA=%d transB=%d and bf16 storage mask %d", epi, transA,
                 transB, L.io);
   if ((L.io & kIoC16) && D) fail("malus: gemm: a bf16 output takes no addend");
   // Under autocast the GELU GEMM (h = x W1, K = 384, a 3072-workgroup grid
   // at 128x64) measured 20 % faster on 128x192 tiles.
-  Plan p = plan_gemm(batch, M, N, K, v, mapped && L.tri_a, bf && epi == 1 ? 0 : -1, bf);
+  Plan p = plan_gemm(batch, M, N, K, v | (x3 && epi ? 64 : 0), mapped && L.tri_a, (bf || x3) && epi == 1 ? 0 : -1, bf,
+                     x3);
   const char* tag = mapped ? " mapped" : "";
   if ((!split_ok || epi || (L.io & kIoC16)) && p.nsplit > 1) {
     p.nsplit = 1;
@@ -587,8 +628,8 @@ bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayou
   if (accumulate && !(!transA && transB)) return false;  // built for the projections' dA (NT) only
   GemmLayouts L = Lin;
   const int v = variant(transA, transB, false, false, true);
-  const bool bf = g_autocast || L.io;
-  Plan p = plan_gemm(1, M, N, K, v, false, -1, bf);
+  const bool bf = g_autocast || L.io, x3 = !bf && f32_x3();
+  Plan p = plan_gemm(1, M, N, K, v, false, -1, bf, x3, L.ngroup);
   const bool c_dense = L.c.r.div == 0 && L.c.c.div == 0 && L.c.c.s0 == 1 && L.c.r.s0 == N;
   if (accumulate || !c_dense || (L.io & kIoC16)) {  // split partials are f32 and dense
     p.nsplit = 1;
@@ -631,7 +672,8 @@ bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayou
   float* Cp = accumulate ? C : L.gc[0];
   const float *A0 = L.ga[0], *B0 = L.gb[0];
   void* args[] = {&A0, &B0, &Cp, &M, &N, &K, &L, &k_chunk, const_cast<int*>(&tiles_n), &split_stride, &Dk, &E};
-  const void* fn = kernel_for(p.ti, (accumulate ? v | 128 : v | 32) | (bf ? kVarBf16 : 0) | (L.io << kVarIoShift));
+  const void* fn = kernel_for(p.ti, (accumulate ? v | 128 : v | 32) | (bf ? kVarBf16 : 0) | (L.io << kVarIoShift) |
+                                        (x3 ? kVarX3 : 0));
   if (!fn) fail("malus: gemm_grouped: no kernel for transA=%d transB=%d and bf16 storage mask %d", transA, transB, L.io);
   MALUS_HIP(hipLaunchKernel(fn, dim3((unsigned)tiles, (unsigned)nsplit, accumulate ? 1u : (unsigned)L.ngroup), dim3(256),
                             args, 0, s));
@@ -721,6 +763,20 @@ extern "C" int malus_autocast(int on) {
   const bool prev = malus::k::g_autocast;
   malus::k::g_autocast = on != 0;
   return prev ? 1 : 0;
+}
+
+// f32 GEMMs on the LDS-DMA kernels as split bf16 products (1) or on the
+// f32 MFMA (0); returns the previous setting.
+namespace malus {
+namespace k {
+bool gemm_f32_split() { return f32_x3(); }
+}  // namespace k
+}  // namespace malus
+
+extern "C" int malus_gemm_set_f32_split(int on) {
+  const int prev = malus::k::f32_x3() ? 1 : 0;
+  malus::k::g_f32_x3 = on != 0 ? 1 : 0;
+  return prev;
 }
 
 // Tuning knob: 0 keeps every GEMM on the register-staged path (for A/B

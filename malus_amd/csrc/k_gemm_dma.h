@@ -5,6 +5,7 @@
 
 #include "common.h"
 #include "k_gelu.h"
+#include "k_split.h"
 
 namespace malus {
 namespace k {
@@ -18,8 +19,6 @@ const void* gemm_io_weight_kernel(int ti, int v);
 
 namespace {
 
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float v4f_raw __attribute__((ext_vector_type(4)));  // 4 words of packed bf16 pairs
 
 constexpr int BK = 16;
@@ -35,10 +34,21 @@ constexpr int BK = 16;
 // stored in bf16): words 0..3 of its 8 slots hold the 8 bf16 values, k
 // order unchanged, so the instruction sees the same values as when an f32
 // copy of the rounded operand is rounded here.
-template <int TM, int TN, bool BF, bool A16 = false, bool B16 = false>
+// X3: the f32 product on the bf16 MFMA from exact three-way splits of
+// both operands (k_split.h), the same slab step the fused attention
+// kernels run.
+template <int TM, int TN, bool BF, bool A16 = false, bool B16 = false, bool X3 = false>
 __device__ __forceinline__ void mfma_kstep(const float (&fa)[TM][8], const float (&fb)[TN][8], v16f (&acc)[TM][TN]) {
   static_assert(BF || !(A16 || B16), "bf16-stored operands run on the bf16 MFMA");
-  if constexpr (BF) {
+  static_assert(!X3 || (BF && !A16 && !B16), "the split product reads f32 operands");
+  if constexpr (X3) {
+    Split3 a[TM], b[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i] = split3(fa[i]);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b[j] = split3(fb[j]);
+    x3_slab<false, TM, TN>(a, b, acc);
+  } else if constexpr (BF) {
     bf16x8 a[TM], b[TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -295,7 +305,7 @@ struct DmaSlab16 {
 // rounding the MFMA applies to an f32 operand) or, for EPI 2, read E in
 // bf16; every layout offset counts elements of the stored type.  D and
 // split-K partials stay f32.
-template <int TM, int TN, bool TA, bool TB, bool MAP, int EPI = 0, bool BF = false, int IO = 0>
+template <int TM, int TN, bool TA, bool TB, bool MAP, int EPI = 0, bool BF = false, int IO = 0, bool X3 = false>
 __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ A, const float* __restrict__ B,
                                                       float* __restrict__ C, int M, int N, int K, GemmLayouts L,
                                                       int k_chunk, int tiles_n, long split_stride,
@@ -315,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   // the second slab's reads overlap the first slab's MFMAs (f32 K steps are
   // long enough that one slab per stage measured faster).
   // (Three- and four-stage rings measured no faster for either precision.)
-  constexpr bool BFS = BF && (BM + BN <= 256);
+  constexpr bool BFS = BF && !X3 && (BM + BN <= 256);
   constexpr int NS = 2, KS = BFS ? 2 : 1;
   constexpr int PER_SLAB = SlabA::PER_WAVE + SlabB::PER_WAVE;  // DMA instructions per slab and wave
   // LDS reads of one slab's fragments (lgkmcnt is 4 bits)
@@ -445,7 +455,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
       // a wave with MFMAs to issue goes ahead of the CU's other waves (measured
       // 1 % on the C5 step; raising it from the barrier on instead lost 2 %)
       __builtin_amdgcn_s_setprio(1);
-      mfma_kstep<TM, TN, BF, A16, B16>(fa[0], fb[0], acc);
+      mfma_kstep<TM, TN, BF, A16, B16, X3>(fa[0], fb[0], acc);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (KS == 2) {
@@ -453,7 +463,7 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
         __builtin_amdgcn_sched_barrier(0);
         if (two) {
           __builtin_amdgcn_s_setprio(1);
-          mfma_kstep<TM, TN, BF, A16, B16>(fa[KS - 1], fb[KS - 1], acc);
+          mfma_kstep<TM, TN, BF, A16, B16, X3>(fa[KS - 1], fb[KS - 1], acc);
           __builtin_amdgcn_s_setprio(0);
         }
         __builtin_amdgcn_sched_barrier(0);

@@ -1388,15 +1388,22 @@ int64_t scores_bwd_q(int64_t hds, int64_t hk, const TensorBuffer* D, bool causal
                 dense_layout((long)hs, (long)(t * hs)), (int)ds->len, (int)kk->len, 1};
   return mapped(ds, kk, c, false, false, (int)bh, (int)t, (int)hs, (int)t, L, D, "scores_bwd_q");
 }
+// dK as the composed ops form it (nanogpt_modular.ml:54-57): the VJP of
+// Q @ Kt with respect to Kt is Q^T @ dS [hs, t], permuted back to [t, hs].
+// One GEMM with A = Q^T and B = dS writes that product through a transposed
+// C layout (element (d, key) at key * hs + d), so the operands keep the
+// composed GEMM's roles (the split-bf16 products depend on which operand is
+// A).  Under a causal mask dS is zero above the diagonal and the full sum
+// only adds exact zeros.
 int64_t scores_bwd_k(int64_t hds, int64_t hq, const TensorBuffer* D, bool causal) {
+  (void)causal;
   TensorBuffer *ds = T_(hds), *q = T_(hq);
   const size_t bh = q->shape[0], t = q->shape[1], hs = q->shape[2];
-  if (!causal)
-    return gemm_out(ds, q, true, false, (int)bh, (int)t, (int)hs, (int)t, (long)(t * t), (long)(t * hs), q->shape, 3, D);
   TensorBuffer* c = alloc_tensor(F32, q->shape, 3);
-  GemmLayouts L{dense_layout((long)t, (long)(t * t)), dense_layout((long)hs, (long)(t * hs)),
-                dense_layout((long)hs, (long)(t * hs)), (int)ds->len, (int)q->len, 1};
-  return mapped(ds, q, c, true, false, (int)bh, (int)t, (int)hs, (int)t, L, D, "scores_bwd_k");
+  const GemmLayout ct{{0, 0, (int)(t * hs)}, {0, 0, 1}, {0, 0, (int)hs}};
+  GemmLayouts L{dense_layout((long)hs, (long)(t * hs)), dense_layout((long)t, (long)(t * t)), ct, (int)q->len,
+                (int)ds->len};
+  return mapped(q, ds, c, true, false, (int)bh, (int)hs, (int)t, (int)t, L, D, "scores_bwd_k");
 }
 
 extern "C" {

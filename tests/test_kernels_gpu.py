@@ -326,8 +326,10 @@ def test_attn_bwd_dq_equals_composed_ops(rt, t, hs, causal):
                                              (64, 64, 0, 5), (256, 64, 1, 300), (64, 32, 0, 600)])
 def test_attn_bwd_all_equals_composed_ops(rt, t, hs, causal, bh):
     # The whole attention VJP from one kernel: dS and dQ as the kernel
-    # without the key-side products, dK = dS^T @ Q and dV = P^T @ dO as the
-    # batched matmuls of the transposed operands (every output bit-exact).
+    # without the key-side products; dK and dV as the composed ops of
+    # nanogpt_modular.ml:54-61 form them: dK = (Q^T @ dS)^T (the VJP of
+    # Q @ Kt with respect to Kt, permuted back) and dV = P^T @ dO (the VJP
+    # of attn @ V with respect to V), every output bit-exact.
     # Up to 600 heads: more workgroups than CUs.
     q, kk, v = (rand(bh, t, hs, lo=-2, hi=2) for _ in range(3))
     d = rand(bh, t, hs)
@@ -353,14 +355,15 @@ def test_attn_bwd_all_equals_composed_ops(rt, t, hs, causal, bh):
     tag = f"t={t} hs={hs} causal={causal}"
     assert_bitexact(ds, rt.numpy(hds2), f"attn_bwd_all dS {tag}")
     assert_bitexact(dq, run(rt, hdq2.value), f"attn_bwd_all dQ {tag}")
-    hdst = rt.L.tensor_permute(hds2, M.sizes([0, 2, 1]), 3)
+    hqt = rt.L.tensor_permute(hq, M.sizes([0, 2, 1]), 3)
     hpt = rt.L.tensor_permute(hp, M.sizes([0, 2, 1]), 3)
-    assert_bitexact(dk, run(rt, rt.L.tensor_matmul(hdst, hq)), f"attn_bwd_all dK {tag}")
+    hdkt = rt.L.tensor_matmul(hqt, hds2)
+    assert_bitexact(dk, run(rt, rt.L.tensor_permute(hdkt, M.sizes([0, 2, 1]), 3)), f"attn_bwd_all dK {tag}")
     assert_bitexact(dv, run(rt, rt.L.tensor_matmul(hpt, hd)), f"attn_bwd_all dV {tag}")
     p = rt.numpy(hp)
     assert_normwise(dk, O.matmul(np.ascontiguousarray(ds.transpose(0, 2, 1)), q), 1e-5, "dK vs oracle matmul")
     assert_normwise(dv, O.matmul(np.ascontiguousarray(p.transpose(0, 2, 1)), d), 1e-5, "dV vs oracle matmul")
-    rt.free(hq, hk, hv, hd, hsc, hm, hp, hds2, hdst, hpt)
+    rt.free(hq, hk, hv, hd, hsc, hm, hp, hds2, hqt, hdkt, hpt)
 
 
 def test_attn_scores_softmax_rejects_unbuilt_shapes(rt):
