@@ -13,8 +13,10 @@
 // other streams from L2; a streamed tile needed in a transposed orientation
 // (V in the forward, K in dQ, Q and dO in the f32 dK/dV) is staged in LDS.
 //
-// MFMA layout (v_mfma_f32_32x32x2f32, or under autocast one
-// v_mfma_f32_32x32x16_bf16 per 16-deep slab): lane l = x + 32 lk supplies
+// MFMA layout (v_mfma_f32_32x32x2f32; under autocast one
+// v_mfma_f32_32x32x16_bf16 per 16-deep slab; with split f32 products (X3,
+// k_split.h) six of them per slab on the operands' exact bf16 pieces, the
+// operand a pass holds in registers split once per pass): lane l = x + 32 lk supplies
 // row / column x of its operand; in each 16-deep slab lane half lk supplies
 // the 8 consecutive k values 8 lk .. 8 lk + 7.  The accumulator of lane l
 // holds column x and rows 8 (r >> 2) + 4 lk + (r & 3), r = 0..15.  A row
@@ -29,6 +31,7 @@
 // pass (S, dP, dV^T += dO^T P, dK^T += Q^T dS).  Each gradient element is
 // written by one wave: no atomics, and the results are deterministic.
 #include "common.h"
+#include "k_split.h"
 
 namespace malus {
 namespace k {
@@ -42,9 +45,11 @@ __device__ __forceinline__ int perm_row(int x) { return x ^ ((((x >> 2) ^ (x >> 
 __device__ __forceinline__ int perm_index(int r, int lk) { return 16 * (r >> 3) + 8 * lk + (r & 7); }
 
 // One 16-deep slab: acc += A B over the 8 k values of each lane half.
-template <bool BF>
+template <bool BF, bool X3 = false>
 __device__ __forceinline__ v16f slab(const float (&a)[8], const float (&b)[8], v16f c) {
-  if constexpr (BF) {
+  if constexpr (X3) {
+    return x3_one<false>(split3(a), split3(b), c);
+  } else if constexpr (BF) {
     bf16x8 x, y;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -130,7 +135,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // Forward: query tile qt of head bh.  O^T = V^T P^T keeps the output with
 // lane = query, so the online rescale is a per-lane factor.
-template <int HS, bool CAUSAL, bool BF, bool S16 = false>
+template <int HS, bool CAUSAL, bool BF, bool S16 = false, bool X3 = false>
 __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q, const float* __restrict__ K,
                                                   const float* __restrict__ V, const float* __restrict__ scale,
                                                   float* __restrict__ O, int ldo, int H, float* __restrict__ lse, int T,
@@ -150,6 +155,10 @@ __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q
   float ka[NKB][8];  // A of S^T: K[32 j + perm_row(x)][16 kb + 8 lk + e]
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) ld8<S16>(K, head + (size_t)perm_row(x) * HS + 16 * kb + 8 * lk, ka[kb]);
+  Split3 qs[X3 ? NKB : 1];
+  if constexpr (X3)
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) qs[kb] = split3(qb[kb]);
 
   v16f o[NN];
 #pragma unroll
@@ -186,7 +195,10 @@ __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q
     }
     v16f st = v16f{0};
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) st = slab<BF>(ka[kb], qb[kb], st);
+    for (int kb = 0; kb < NKB; ++kb) {
+      if constexpr (X3) st = x3_one<false>(split3(ka[kb]), qs[kb], st);
+      else st = slab<BF>(ka[kb], qb[kb], st);
+    }
     if (j < last) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
@@ -221,8 +233,14 @@ __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q
       float pb[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) pb[e] = st[8 * h + e];
+      if constexpr (X3) {
+        const Split3 ps = split3(pb);
 #pragma unroll
-      for (int n = 0; n < NN; ++n) o[n] = slab<BF>(va[n][h], pb, o[n]);
+        for (int n = 0; n < NN; ++n) o[n] = x3_one<false>(split3(va[n][h]), ps, o[n]);
+      } else {
+#pragma unroll
+        for (int n = 0; n < NN; ++n) o[n] = slab<BF>(va[n][h], pb, o[n]);
+      }
     }
   }
   // O[i0 + x][32 n + 8 g + 4 lk + c] = o[n][4 g + c] / l
@@ -241,7 +259,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q
 
 // Backward, query-centric: dQ (+ Dq) of query tile qt, and D = rowsum(dO*O)
 // of its rows into dsum for the key-centric pass.
-template <int HS, bool CAUSAL, bool BF, bool S16 = false>
+template <int HS, bool CAUSAL, bool BF, bool S16 = false, bool X3 = false>
 __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict__ Q, const float* __restrict__ K,
                                                      const float* __restrict__ V, const float* __restrict__ O,
                                                      const float* __restrict__ dO, int ldo, int H,
@@ -271,6 +289,13 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
   }
   d += __shfl_xor(d, 32, 64);
   if (lk == 0) dsum[(size_t)bh * T + i] = d;
+  Split3 qs[X3 ? NKB : 1], os[X3 ? NKB : 1];
+  if constexpr (X3)
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      qs[kb] = split3(qb[kb]);
+      os[kb] = split3(ob[kb]);
+    }
   const float L = lse[(size_t)bh * T + i];
 
   v16f dq[NN];
@@ -311,8 +336,13 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
     v16f st = v16f{0}, dp = v16f{0};
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      st = slab<BF>(ka[kb], qb[kb], st);
-      dp = slab<BF>(vr[kb], ob[kb], dp);
+      if constexpr (X3) {
+        st = x3_one<false>(split3(ka[kb]), qs[kb], st);
+        dp = x3_one<false>(split3(vr[kb]), os[kb], dp);
+      } else {
+        st = slab<BF>(ka[kb], qb[kb], st);
+        dp = slab<BF>(vr[kb], ob[kb], dp);
+      }
     }
     float kc[NN][2][8];  // B of dQ = dS K: K[32 j + 16 h + 8 lk + e][32 n + x]
 #pragma unroll
@@ -334,8 +364,14 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
       float ab[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) ab[e] = st[8 * h + e];
+      if constexpr (X3) {
+        const Split3 as = split3(ab);
 #pragma unroll
-      for (int n = 0; n < NN; ++n) dq[n] = slab<BF>(ab, kc[n][h], dq[n]);
+        for (int n = 0; n < NN; ++n) dq[n] = x3_one<false>(as, split3(kc[n][h]), dq[n]);
+      } else {
+#pragma unroll
+        for (int n = 0; n < NN; ++n) dq[n] = slab<BF>(ab, kc[n][h], dq[n]);
+      }
     }
   }
   // dQ[i0 + 8 (r >> 2) + 4 lk + (r & 3)][32 n + x] (+ Dq: every addend loaded
@@ -360,7 +396,7 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
 }
 
 // Backward, key-centric: dK (+ Dk) and dV (+ Dv) of key tile kt.
-template <int HS, bool CAUSAL, bool BF, bool S16 = false>
+template <int HS, bool CAUSAL, bool BF, bool S16 = false, bool X3 = false>
 __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict__ Q, const float* __restrict__ K,
                                                       const float* __restrict__ V, const float* __restrict__ dO, int ldo,
                                                       int H, const float* __restrict__ lse,
@@ -384,6 +420,13 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
     ld8<S16>(K, head + (size_t)key * HS + 16 * kb + 8 * lk, kb_[kb]);
     ld8<S16>(V, head + (size_t)key * HS + 16 * kb + 8 * lk, vb[kb]);
   }
+  Split3 ks[X3 ? NKB : 1], vs[X3 ? NKB : 1];
+  if constexpr (X3)
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      ks[kb] = split3(kb_[kb]);
+      vs[kb] = split3(vb[kb]);
+    }
   v16f dvt[NN], dkt[NN];  // dV^T, dK^T: lane = key, rows = head dims
 #pragma unroll
   for (int n = 0; n < NN; ++n) {
@@ -424,8 +467,13 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
         float qa[8], oa[8];  // A: rows perm_row(x) of Q_i, dO_i
         load8(Qs + perm_row(x) * LD + 16 * kb + 8 * lk, qa);
         load8(Os + perm_row(x) * LD + 16 * kb + 8 * lk, oa);
-        s = slab<BF>(qa, kb_[kb], s);
-        dp = slab<BF>(oa, vb[kb], dp);
+        if constexpr (X3) {
+          s = x3_one<false>(split3(qa), ks[kb], s);
+          dp = x3_one<false>(split3(oa), vs[kb], dp);
+        } else {
+          s = slab<BF>(qa, kb_[kb], s);
+          dp = slab<BF>(oa, vb[kb], dp);
+        }
       }
     } else {
       const int qrow = i0 + perm_row(x);
@@ -464,6 +512,11 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
         pb[e] = s[8 * h + e];
         db[e] = dp[8 * h + e];
       }
+      Split3 pbs, dbs;
+      if constexpr (X3) {
+        pbs = split3(pb);
+        dbs = split3(db);
+      }
 #pragma unroll
       for (int n = 0; n < NN; ++n) {
         float oa[8], qa[8];  // A of dV^T = dO^T P and dK^T = Q^T dS: [i0 + 16 h + 8 lk + e][32 n + x]
@@ -479,8 +532,13 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
             qa[e] = ld1<S16>(Q, head + (size_t)q * HS + 32 * n + x);
           }
         }
-        dvt[n] = slab<BF>(oa, pb, dvt[n]);
-        dkt[n] = slab<BF>(qa, db, dkt[n]);
+        if constexpr (X3) {
+          dvt[n] = x3_one<false>(split3(oa), pbs, dvt[n]);
+          dkt[n] = x3_one<false>(split3(qa), dbs, dkt[n]);
+        } else {
+          dvt[n] = slab<BF>(oa, pb, dvt[n]);
+          dkt[n] = slab<BF>(qa, db, dkt[n]);
+        }
       }
     }
   }
@@ -515,27 +573,28 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-template <int HS, bool CAUSAL, bool BF, bool S16>
+template <int HS, bool CAUSAL, bool BF, bool S16, bool X3 = false>
 void fwd_launch(const float* Q, const float* K, const float* V, const float* scale, float* O, int ldo, int H,
                 float* lse, int T, int BH, hipStream_t s) {
-  k_flash_fwd<HS, CAUSAL, BF, S16><<<(unsigned)(T / 32 * BH), 64, 0, s>>>(Q, K, V, scale, O, ldo, H, lse, T, BH);
+  k_flash_fwd<HS, CAUSAL, BF, S16, X3><<<(unsigned)(T / 32 * BH), 64, 0, s>>>(Q, K, V, scale, O, ldo, H, lse, T, BH);
 }
 
-template <int HS, bool CAUSAL, bool BF, bool S16>
+template <int HS, bool CAUSAL, bool BF, bool S16, bool X3 = false>
 void bwd_launch(const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
   const unsigned grid = (unsigned)(T / 32 * BH);
-  k_flash_bwd_dq<HS, CAUSAL, BF, S16><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.O, a.dO, ldo, H, a.lse, a.scale, a.dQ,
-                                                           a.Dq, a.dsum, T, BH);
-  k_flash_bwd_dkv<HS, CAUSAL, BF, S16><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.dO, ldo, H, a.lse, a.dsum, a.scale, a.dK,
-                                                            a.Dk, a.dV, a.Dv, T, BH);
+  k_flash_bwd_dq<HS, CAUSAL, BF, S16, X3><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.O, a.dO, ldo, H, a.lse, a.scale, a.dQ,
+                                                               a.Dq, a.dsum, T, BH);
+  k_flash_bwd_dkv<HS, CAUSAL, BF, S16, X3><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.dO, ldo, H, a.lse, a.dsum, a.scale,
+                                                                a.dK, a.Dk, a.dV, a.Dv, T, BH);
 }
 
-// precision: 0 f32, 1 bf16 MFMA on f32 storage, 2 bf16 MFMA on bf16 q, k, v
-// (and their gradients)
+// precision: 0 f32 (FP32 MFMA), 1 bf16 MFMA on f32 storage, 2 bf16 MFMA on
+// bf16 q, k, v (and their gradients), 3 f32 as split bf16 products
 template <int HS, bool CAUSAL>
 void fwd_prec(int prec, const float* Q, const float* K, const float* V, const float* scale, float* O, int ldo, int H,
               float* lse, int T, int BH, hipStream_t s) {
-  if (prec == 2) fwd_launch<HS, CAUSAL, true, true>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
+  if (prec == 3) fwd_launch<HS, CAUSAL, false, false, true>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
+  else if (prec == 2) fwd_launch<HS, CAUSAL, true, true>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
   else if (prec == 1) fwd_launch<HS, CAUSAL, true, false>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
   else fwd_launch<HS, CAUSAL, false, false>(Q, K, V, scale, O, ldo, H, lse, T, BH, s);
 }
@@ -549,7 +608,8 @@ void fwd_hs(size_t hs, int prec, const float* Q, const float* K, const float* V,
 
 template <int HS, bool CAUSAL>
 void bwd_prec(int prec, const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
-  if (prec == 2) bwd_launch<HS, CAUSAL, true, true>(a, ldo, H, T, BH, s);
+  if (prec == 3) bwd_launch<HS, CAUSAL, false, false, true>(a, ldo, H, T, BH, s);
+  else if (prec == 2) bwd_launch<HS, CAUSAL, true, true>(a, ldo, H, T, BH, s);
   else if (prec == 1) bwd_launch<HS, CAUSAL, true, false>(a, ldo, H, T, BH, s);
   else bwd_launch<HS, CAUSAL, false, false>(a, ldo, H, T, BH, s);
 }
@@ -572,7 +632,7 @@ bool flash_fwd(const float* Q, const float* K, const float* V, const float* scal
   if (!flash_supported(bh, t, hs) || heads == 0 || bh % heads || ldo < hs * heads || ldo % 4) return false;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O) || !lse || !scale) return false;
   const int T = (int)t, BH = (int)bh, l = (int)ldo, H = (int)heads;
-  const int prec = qkv_bf16 ? 2 : bf16 ? 1 : 0;
+  const int prec = qkv_bf16 ? 2 : bf16 ? 1 : gemm_f32_split() ? 3 : 0;
   if (causal) fwd_hs<true>(hs, prec, Q, K, V, scale, O, l, H, lse, T, BH, s);
   else fwd_hs<false>(hs, prec, Q, K, V, scale, O, l, H, lse, T, BH, s);
   MALUS_HIP(hipGetLastError());
@@ -589,7 +649,7 @@ bool flash_bwd(const FlashBwd& a, size_t ldo, size_t heads, size_t bh, size_t t,
   if ((a.Dk && !aligned16(a.Dk)) || (a.Dv && !aligned16(a.Dv)) || !a.scale) return false;
   if (qkv_bf16 && (a.Dq || a.Dk || a.Dv)) return false;  // bf16 gradients take no addends
   const int T = (int)t, BH = (int)bh, l = (int)ldo, H = (int)heads;
-  const int prec = qkv_bf16 ? 2 : bf16 ? 1 : 0;
+  const int prec = qkv_bf16 ? 2 : bf16 ? 1 : gemm_f32_split() ? 3 : 0;
   if (causal) bwd_hs<true>(hs, prec, a, l, H, T, BH, s);
   else bwd_hs<false>(hs, prec, a, l, H, T, BH, s);
   MALUS_HIP(hipGetLastError());

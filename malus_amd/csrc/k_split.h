@@ -14,10 +14,14 @@
 // slab, so one 16-deep slab rounds six times where the FP32 MFMA
 // (v_mfma_f32_32x32x2_f32, 8 steps of 2) rounds eight times.
 //
-// Non-finite operands: an infinite value's residual is inf - inf = NaN, and
-// the residual of its pair partner (the other half of the same packed word)
-// takes 0 * inf = NaN as well, so every output an infinite operand reaches
-// is NaN (the FP32 MFMA gives +-inf where no inf * 0 or inf - inf arises).
+// A lane splits its 8 values of a slab with one v_cvt_pk_bf16_f32 per pair
+// and piece, and a shift or mask plus a subtraction per residual (5.5 VALU
+// instructions per value; a v_dot2_f32_bf16 form of the residual, 3.5 per
+// value, measured 0.4 % slower on the C5 step).
+//
+// Non-finite operands: an infinite value's residual is inf - inf = NaN, so
+// every output an infinite operand reaches is NaN (the FP32 MFMA gives
+// +-inf where no inf * 0 or inf - inf arises).
 #pragma once
 
 #include "common.h"
@@ -37,17 +41,9 @@ __device__ __forceinline__ unsigned pack_bf16(float a, float b) {
   return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }
 
-// x minus the bf16 value in the low (HI = false) or high half of p, in one
-// v_dot2_f32_bf16 (p . (-1, 0) + x): exact whenever the difference is an
-// f32 value, as the split's residuals are.  The (-1, 0) / (0, -1) operand
-// sits in a register: the compiler would otherwise encode it as an inline
-// constant, which this operand does not read as that bf16 pair.
-template <bool HI>
-__device__ __forceinline__ float minus_bf16(unsigned p, float x) {
-  unsigned c;
-  asm("v_mov_b32 %0, %1" : "=v"(c) : "i"(HI ? 0xbf800000u : 0x0000bf80u));
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), __builtin_bit_cast(bf16x2, c), x, false);
-}
+// The bf16 value in the low / high half-word of p, as f32.
+__device__ __forceinline__ float bf16_low(unsigned p) { return __builtin_bit_cast(float, p << 16); }
+__device__ __forceinline__ float bf16_high(unsigned p) { return __builtin_bit_cast(float, p & 0xffff0000u); }
 
 // The three pieces of a lane's 8 fragment values, packed as the MFMA reads
 // them (value e in half-word e).
@@ -60,9 +56,9 @@ __device__ __forceinline__ Split3 split3(const float (&f)[8]) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     hp[q] = pack_bf16(f[2 * q], f[2 * q + 1]);
-    const float ra = minus_bf16<false>(hp[q], f[2 * q]), rb = minus_bf16<true>(hp[q], f[2 * q + 1]);
+    const float ra = f[2 * q] - bf16_low(hp[q]), rb = f[2 * q + 1] - bf16_high(hp[q]);
     mp[q] = pack_bf16(ra, rb);
-    lp[q] = pack_bf16(minus_bf16<false>(mp[q], ra), minus_bf16<true>(mp[q], rb));
+    lp[q] = pack_bf16(ra - bf16_low(mp[q]), rb - bf16_high(mp[q]));
   }
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
   return Split3{__builtin_bit_cast(bf16x8, (u32x4){hp[0], hp[1], hp[2], hp[3]}),
@@ -76,28 +72,30 @@ __device__ __forceinline__ Split3 split3(const float (&f)[8]) {
 // caller's a holds the GEMM's B and b the GEMM's A (a kernel that forms the
 // transposed tile); each MFMA then takes its operands in the caller's roles
 // and the same sequence of piece products, so the accumulators round the
-// same sums in the same order.
+// same sums in the same order.  x3_step issues piece product STEP (0..5)
+// for every accumulator; x3_slab issues all six.
+template <bool SWAP, int STEP, int TM, int TN>
+__device__ __forceinline__ void x3_step(const Split3 (&a)[TM], const Split3 (&b)[TN], v16f (&acc)[TM][TN]) {
+  // pieces (of the GEMM's A, of the GEMM's B) per step
+  constexpr int PA = STEP == 0 ? 2 : STEP == 1 ? 0 : STEP == 2 ? 1 : STEP == 3 ? 1 : STEP == 4 ? 0 : 0;
+  constexpr int PB = STEP == 0 ? 0 : STEP == 1 ? 2 : STEP == 2 ? 1 : STEP == 3 ? 0 : STEP == 4 ? 1 : 0;
+  constexpr int XA = SWAP ? PB : PA, XB = SWAP ? PA : PB;  // the caller's operands
+  auto piece = [](const Split3& s, int which) -> const bf16x8& { return which == 0 ? s.h : which == 1 ? s.m : s.l; };
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(piece(a[i], XA), piece(b[j], XB), acc[i][j], 0, 0, 0);
+}
+
 template <bool SWAP, int TM, int TN>
 __device__ __forceinline__ void x3_slab(const Split3 (&a)[TM], const Split3 (&b)[TN], v16f (&acc)[TM][TN]) {
-#define MALUS_X3_STEP(PA, PB)                                                                          \
-  _Pragma("unroll") for (int i = 0; i < TM; ++i) _Pragma("unroll") for (int j = 0; j < TN; ++j)        \
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i].PA, b[j].PB, acc[i][j], 0, 0, 0);
-  if constexpr (SWAP) {
-    MALUS_X3_STEP(h, l)
-    MALUS_X3_STEP(l, h)
-    MALUS_X3_STEP(m, m)
-    MALUS_X3_STEP(h, m)
-    MALUS_X3_STEP(m, h)
-    MALUS_X3_STEP(h, h)
-  } else {
-    MALUS_X3_STEP(l, h)
-    MALUS_X3_STEP(h, l)
-    MALUS_X3_STEP(m, m)
-    MALUS_X3_STEP(m, h)
-    MALUS_X3_STEP(h, m)
-    MALUS_X3_STEP(h, h)
-  }
-#undef MALUS_X3_STEP
+  x3_step<SWAP, 0>(a, b, acc);
+  x3_step<SWAP, 1>(a, b, acc);
+  x3_step<SWAP, 2>(a, b, acc);
+  x3_step<SWAP, 3>(a, b, acc);
+  x3_step<SWAP, 4>(a, b, acc);
+  x3_step<SWAP, 5>(a, b, acc);
 }
 
 // The same step for one accumulator (a single 32 x 32 tile).

@@ -112,9 +112,9 @@ def test_split_error_vs_float64_no_larger_than_fp32_mfma(rt, form, t, k, n):
 @pytest.mark.parametrize("split", [True, False], ids=["split", "fp32"])
 def test_nonfinite_operands_reach_only_their_outputs(rt, split):
     # An inf in A row r (or B column j) makes row r (column j) non-finite --
-    # NaN on the split path, where the inf's residual and its packed
-    # neighbour's are NaN -- and leaves every other output bit-identical to
-    # the product without it (rows and columns of a GEMM are independent).
+    # NaN on the split path, where the inf's residual inf - inf is NaN -- and
+    # leaves every other output bit-identical to the product without it
+    # (rows and columns of a GEMM are independent).
     a = RNG.uniform(-1, 1, (256, 64)).astype(np.float32)
     b = RNG.uniform(-1, 1, (64, 160)).astype(np.float32)
     with split_mode(rt, split):
