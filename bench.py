@@ -520,11 +520,12 @@ def run_gpt(rt, a, cfg):
     split = not a.autocast and a.f32_gemm == "split"
     if split:
         # every f32 product of the LDS-DMA GEMMs runs six exact bf16 piece
-        # products on the bf16 MFMA; the register-staged launches (the
-        # 65-wide vocabulary products, 2.45 of the 1046.1 GFLOP) run on the
-        # FP32 MFMA
+        # products on the bf16 MFMA; the register-staged launches (the three
+        # 65-wide vocabulary products: logits, their dX and dW, 6 n V C FLOP)
+        # run on the FP32 MFMA
         gf = gflop.value / gsteps / 1e9
-        exec_tflops = gemm_tflops * (6.0 * (gf - 2.45) + 2.45) / gf if gf > 2.45 else gemm_tflops
+        vocab = 6.0 * n * cfg["V"] * cfg["C"] / 1e9
+        exec_tflops = gemm_tflops * (6.0 * (gf - vocab) + vocab) / gf if gf > vocab else gemm_tflops
         executed = {"pipe": "bf16 MFMA (v_mfma_f32_32x32x16_bf16), six piece products per f32 product",
                     "achieved": round(exec_tflops, 2), "peak": PEAK_BF16_MFMA_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(exec_tflops / PEAK_BF16_MFMA_TFLOPS, 4)}

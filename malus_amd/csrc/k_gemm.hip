@@ -415,7 +415,9 @@ Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false, int only
   // caller.
   const bool wgrad_bf = wgrad && (g_autocast || bf || (x3 && groups > 1));
   if (wgrad_bf) only_tile = x3 && !g_autocast && !bf ? 1 : 0;  // kTiles[0] = 128x192, kTiles[1] = 128x128
-  if (x3 && !wgrad && (v & 16) && !(v & 64) && only_tile < 0 && g_forced_tile < 0 && batch == 1 && K >= 1024)
+  const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128) * batch;
+  if (x3 && !wgrad && (v & 16) && !(v & 64) && only_tile < 0 && g_forced_tile < 0 && batch == 1 && K >= 1024 &&
+      tiles128 >= 256)
     only_tile = 1;
   // the occupancy the cost model sees: the split kernels' own for the wide
   // tiles picked above (it sets their K split), else the f32 kernels'
@@ -510,8 +512,10 @@ double launch_dma(const float* A, const float* B, float* C, int batch, int M, in
   if ((L.io & kIoC16) && D) fail("malus: gemm: a bf16 output takes no addend");
   // Under autocast the GELU GEMM (h = x W1, K = 384, a 3072-workgroup grid
   // at 128x64) measured 20 % faster on 128x192 tiles.
-  Plan p = plan_gemm(batch, M, N, K, v | (x3 && epi ? 64 : 0), mapped && L.tri_a, (bf || x3) && epi == 1 ? 0 : -1, bf,
-                     x3);
+  // The GELU forward GEMM takes 128x192 tiles under autocast, and with split
+  // products where that still gives 512 workgroups (C5's 16384 x 1536).
+  const bool gelu_wide = epi == 1 && (bf || (x3 && (long)((M + 127) / 128) * ((N + 191) / 192) * batch >= 512));
+  Plan p = plan_gemm(batch, M, N, K, v | (x3 && epi ? 64 : 0), mapped && L.tri_a, gelu_wide ? 0 : -1, bf, x3);
   const char* tag = mapped ? " mapped" : "";
   if ((!split_ok || epi || (L.io & kIoC16)) && p.nsplit > 1) {
     p.nsplit = 1;
