@@ -367,7 +367,11 @@ void malus_gpt_set_fused_forward(void* g, int on);
  * gelu(h), the GELU VJP's dh and, with flash attention, q, k, v and their
  * gradients) are stored in bf16, and the GEMMs read bf16 copies of the block
  * weights refreshed at each forward; the step's values are the same as with
- * 0 (f32 storage), in half the bytes. */
+ * 0 (f32 storage), in half the bytes.  With split f32 products
+ * (malus_gemm_set_f32_split) the block weights get split copies instead
+ * (the three bf16 planes of their pieces, refreshed at each forward), which
+ * the forward GEMMs read as B without splitting it; the same values as
+ * with 0. */
 void malus_gpt_set_bf16_activations(void* g, int on);
 int64_t malus_gpt_forward_loss(void* g, int64_t toks, int64_t targets); /* nanogpt_modular.ml:75-91 + cross_entropy */
 int64_t malus_gpt_logits(void* g, int64_t toks);

@@ -56,9 +56,13 @@ struct TensorBuffer {
   // autocast storage policy keeps one per weight matrix; this holds a
   // reference).  It stands for this tensor while copy->copy_of == this and
   // copy->copy_seq == write_seq: refreshed after the tensor's last write.
+  // With split f32 products the model keeps a split copy in this slot
+  // instead (split3): the three bf16 pieces of every value, h, m and l, as
+  // three planes of the tensor's layout one after another.
   TensorBuffer* bf16_copy = nullptr;
   const TensorBuffer* copy_of = nullptr;  // on a copy: the tensor it was last refreshed from
   uint64_t copy_seq = 0;                  // ... and that tensor's write_seq at the refresh
+  bool split3 = false;                    // on a copy: the three-plane split form
 
   float* f32() const { return static_cast<float*>(st->ptr); }
   int32_t* i32() const { return static_cast<int32_t*>(st->ptr); }
@@ -170,6 +174,9 @@ struct Bf16Copy {
   size_t n;
 };
 void to_bf16_multi(const Bf16Copy* segs_host, int count, hipStream_t s);
+// Many split copies in one launch: dst (bf16) gets the h, m and l pieces of
+// src's n values as three planes of n (the pieces the split GEMM forms).
+void to_split3_multi(const Bf16Copy* segs_host, int count, hipStream_t s);
 void fill(float* out, float v, size_t n, hipStream_t s);
 void fill_bytes0(void* out, size_t bytes, hipStream_t s);
 void fill_from_device(float* out, const float* v, size_t n, hipStream_t s);
@@ -261,6 +268,10 @@ bool flash_bwd(const FlashBwd& a, size_t ldo, size_t heads, size_t bh, size_t t,
                hipStream_t s, bool qkv_bf16 = false);
 // The autocast scope's state (GEMMs and flash attention on the bf16 MFMA).
 bool autocast_on();
+// Whether f32 GEMMs (and the fused attention kernels, which reproduce the
+// composed GEMMs' bits) compute their products as split bf16 pieces
+// (malus_gemm_set_f32_split; k_split.h).
+bool gemm_f32_split();
 // Sum over the axis of x * y (y has x's layout); each product rounded to f32.
 void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 // The split of reduce_axis_prod's column reduction over [axis, inner]
@@ -332,6 +343,8 @@ constexpr int kIoA16 = 1;  // A stored in bf16
 constexpr int kIoB16 = 2;  // B stored in bf16
 constexpr int kIoC16 = 4;  // C written in bf16 (no addend, no K split)
 constexpr int kIoE16 = 8;  // the GELU epilogues' E (written or read) in bf16
+constexpr int kIoB3 = 16;  // B as the three bf16 planes of its split pieces (split products only;
+                           // plane p of element x at x + p * ext_b)
 struct GemmLayouts {
   GemmLayout a, b, c;
   int ext_a, ext_b;

@@ -7,6 +7,7 @@
 // one-op-per-kernel f32 arithmetic.
 #include "common.h"
 #include "k_gelu.h"
+#include "k_split.h"
 
 namespace malus {
 namespace k {
@@ -273,6 +274,51 @@ __global__ __launch_bounds__(kBlock) void k_to_bf16_multi(const CvtTable t) {
   for (size_t i = first + threadIdx.x; i < end; i += blockDim.x) dst[i] = (__bf16)sg.src[i];
 }
 
+// The split copies: split3 (k_split.h) on runs of 8 values, so the pieces
+// are the bits the split GEMM forms from the same values itself.  Chunks
+// start at multiples of 8; a run cut short by the end of a tensor is
+// padded with zeros and only its own values are stored.
+__global__ __launch_bounds__(kBlock) void k_split3_multi(const CvtTable t) {
+  int lo = 0, hi = t.count - 1;  // the segment holding chunk blockIdx.x
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (t.first_chunk[mid] <= blockIdx.x) lo = mid;
+    else hi = mid - 1;
+  }
+  const Bf16Copy& sg = t.seg[lo];
+  const size_t first = (size_t)(blockIdx.x - t.first_chunk[lo]) * kCvtChunk;
+  const size_t end = first + kCvtChunk < sg.n ? first + kCvtChunk : sg.n;
+  __bf16* ph = static_cast<__bf16*>(sg.dst);
+  __bf16* pm = ph + sg.n;
+  __bf16* pl = pm + sg.n;
+  const bool vec = sg.n % 8 == 0 && ((reinterpret_cast<uintptr_t>(sg.src) | reinterpret_cast<uintptr_t>(sg.dst)) & 15) == 0;
+  for (size_t i = first + 8 * (size_t)threadIdx.x; i < end; i += 8 * (size_t)blockDim.x) {
+    float f[8];
+    if (vec) {
+      const float4 a = reinterpret_cast<const float4*>(sg.src + i)[0], b = reinterpret_cast<const float4*>(sg.src + i)[1];
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+      f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = i + e < end ? sg.src[i + e] : 0.0f;
+    }
+    const Split3 p = split3(f);
+    if (vec) {
+      *reinterpret_cast<bf16x8*>(ph + i) = p.h;
+      *reinterpret_cast<bf16x8*>(pm + i) = p.m;
+      *reinterpret_cast<bf16x8*>(pl + i) = p.l;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (i + e < end) {
+          ph[i + e] = p.h[e];
+          pm[i + e] = p.m[e];
+          pl[i + e] = p.l[e];
+        }
+    }
+  }
+}
+
 template <class F>
 void dispatch_binop(int op, F f) {
   switch (op) {
@@ -386,6 +432,24 @@ void to_bf16_multi(const Bf16Copy* segs_host, int count, hipStream_t s) {
     if (chunks > 0x7fffffffu) fail("malus: bf16 copies: too many elements");
     k_to_bf16_multi<<<(unsigned)chunks, kBlock, 0, s>>>(t);
     post_launch("to_bf16_multi");
+  }
+}
+
+void to_split3_multi(const Bf16Copy* segs_host, int count, hipStream_t s) {
+  for (int base = 0; base < count; base += kCvtMaxSegs) {
+    CvtTable t{};
+    t.count = count - base < kCvtMaxSegs ? count - base : kCvtMaxSegs;
+    size_t chunks = 0;
+    for (int i = 0; i < t.count; ++i) {
+      t.seg[i] = segs_host[base + i];
+      t.first_chunk[i] = (uint32_t)chunks;
+      chunks += (t.seg[i].n + kCvtChunk - 1) / kCvtChunk;
+    }
+    t.first_chunk[t.count] = (uint32_t)chunks;
+    if (chunks == 0) continue;
+    if (chunks > 0x7fffffffu) fail("malus: split copies: too many elements");
+    k_split3_multi<<<(unsigned)chunks, kBlock, 0, s>>>(t);
+    post_launch("to_split3_multi");
   }
 }
 

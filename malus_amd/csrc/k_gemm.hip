@@ -258,14 +258,15 @@ struct TileCfg { int tm, tn; };
 constexpr TileCfg kTiles[] = {{2, 3}, {2, 2}, {2, 1}, {1, 2}, {1, 1}};
 constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 
-// Variant code: bits 12..9 = GemmLayouts::io (bf16-stored operands, the
-// instances of k_gemm_io.hip), bit 8 = bf16 MFMA (autocast), bit 7 =
+// Variant code: bit 14 = split f32 products, bits 13..9 = GemmLayouts::io
+// (bf16-stored operands and split copies, the instances of k_gemm_io*.hip),
+// bit 8 = bf16 MFMA (autocast), bit 7 =
 // grouped accumulation, bit 6 = GELU epilogues, bit 5 = mapped operands,
 // bit 4 = LDS-DMA path, bits 3..0 = transA, transB, vecA, vecB.
 constexpr int kVarBf16 = 256;
 constexpr int kVarIoShift = 9;
-constexpr int kVarX3 = 1 << 13;  // f32 product as split bf16 pieces (LDS-DMA kernels)
-constexpr int kVarCount = 1 << 14;
+constexpr int kVarX3 = 1 << 14;  // f32 product as split bf16 pieces (LDS-DMA kernels)
+constexpr int kVarCount = 1 << 15;
 inline int variant(bool ta, bool tb, bool va, bool vb, bool dma) {
   return (dma << 4) | (ta << 3) | (tb << 2) | (va << 1) | (int)vb;
 }
@@ -320,7 +321,7 @@ const void* kernel_for_prec(int ti, int v) {
 }
 
 const void* kernel_for(int ti, int v) {
-  if ((v >> kVarIoShift) & 15) return gemm_io_kernel(ti, v);
+  if ((v >> kVarIoShift) & 31) return gemm_io_kernel(ti, v);
   if (v & kVarX3) return kernel_for_prec<2>(ti, v);
   return (v & kVarBf16) ? kernel_for_prec<1>(ti, v) : kernel_for_prec<0>(ti, v);
 }
@@ -504,7 +505,10 @@ double launch_dma(const float* A, const float* B, float* C, int batch, int M, in
   // take the plan of the autocast GEMM on f32 copies of them, so the sums
   // run in the same order
   const int v = variant(transA, transB, false, false, true);
-  const bool bf = g_autocast || L.io, x3 = !bf && f32_x3();
+  // a split copy of B (kIoB3) feeds the split product; any other io mask
+  // is bf16 storage, which runs on the bf16 MFMA
+  const bool bf = g_autocast || (L.io & ~kIoB3), x3 = !bf && f32_x3();
+  if ((L.io & kIoB3) && !x3) fail("malus: gemm: a split copy of B needs split f32 products (io mask %d)", L.io);
   const int vb = (epi ? v | 64 : mapped ? v | 32 : v) | (bf ? kVarBf16 : 0) | (L.io << kVarIoShift) | (x3 ? kVarX3 : 0);
   const void* fn = kernel_for(0, vb);
   if (!fn) fail("malus: gemm: no kernel for epilogue %d with transA=%d transB=%d and bf16 storage mask %d", epi, transA,
@@ -572,11 +576,11 @@ void gemm(const float* A, const float* B, float* C, int batch, int M, int N, int
   const long ext_a = (long)(batch - 1) * sA + (long)M * K, ext_b = (long)(batch - 1) * sB + (long)K * N;
   // LDS-DMA path: whole 16-deep K slabs, 16-byte rows, 32-bit byte offsets
   // (a bf16 operand's x-contiguous rows: runs of 8 elements)
-  const int xa = io & kIoA16 ? 8 : 4, xb = io & kIoB16 ? 8 : 4;
+  const int xa = io & kIoA16 ? 8 : 4, xb = io & (kIoB16 | kIoB3) ? 8 : 4;
   const bool dma = K % 16 == 0 && (transA ? M % xa == 0 : true) && (transB ? true : N % xb == 0) &&
-                   (size_t)ext_a * 4 < (1ull << 31) && (size_t)ext_b * 4 < (1ull << 31) &&
+                   (size_t)ext_a * 4 < (1ull << 31) && (size_t)ext_b * ((io & kIoB3) ? 6 : 4) < (1ull << 31) &&
                    ((size_t)(batch - 1) * sC + (size_t)M * N) * 4 < (1ull << 31) && g_allow_dma;
-  if (io & ~(kIoA16 | kIoB16)) fail("malus: gemm: bf16 storage mask %d is not an operand mask", io);
+  if (io & ~(kIoA16 | kIoB16 | kIoB3)) fail("malus: gemm: bf16 storage mask %d is not an operand mask", io);
   if (dma) {
     GemmLayouts L{dense_layout(lda, sA), dense_layout(ldb, sB), dense_layout(N, sC), (int)ext_a, (int)ext_b};
     L.io = io;
@@ -614,7 +618,8 @@ bool gemm_gelu(const float* A, const float* B, float* C, float* E, int M, int N,
       (backward && !transB))
     return false;
   const long ext_a = (long)M * K, ext_b = (long)K * N;
-  if ((size_t)ext_a * 4 >= (1ull << 31) || (size_t)ext_b * 4 >= (1ull << 31) || (size_t)M * N * 4 >= (1ull << 31))
+  if ((size_t)ext_a * 4 >= (1ull << 31) || (size_t)ext_b * ((io & kIoB3) ? 6 : 4) >= (1ull << 31) ||
+      (size_t)M * N * 4 >= (1ull << 31))
     return false;
   GemmLayouts L{dense_layout(K, 0), dense_layout(transB ? K : N, 0), dense_layout(N, 0), (int)ext_a, (int)ext_b};
   L.io = io;
@@ -632,7 +637,8 @@ bool gemm_grouped(int M, int N, int K, bool transA, bool transB, const GemmLayou
   if (accumulate && !(!transA && transB)) return false;  // built for the projections' dA (NT) only
   GemmLayouts L = Lin;
   const int v = variant(transA, transB, false, false, true);
-  const bool bf = g_autocast || L.io, x3 = !bf && f32_x3();
+  const bool bf = g_autocast || (L.io & ~kIoB3), x3 = !bf && f32_x3();
+  if ((L.io & kIoB3) && !x3) fail("malus: gemm_grouped: a split copy of B needs split f32 products");
   Plan p = plan_gemm(1, M, N, K, v, false, -1, bf, x3, L.ngroup);
   const bool c_dense = L.c.r.div == 0 && L.c.c.div == 0 && L.c.c.s0 == 1 && L.c.r.s0 == N;
   if (accumulate || !c_dense || (L.io & kIoC16)) {  // split partials are f32 and dense
@@ -721,7 +727,7 @@ bool mapped_ok(int batch, int M, int N, int K, bool transA, bool transB, const G
   // bytes), of 8 elements for a bf16 operand
   const GemmMap& a_contig = L.a.c;  // A [M][K]: k;  A^T [K][M]: m
   const GemmMap& b_contig = L.b.c;  // B [K][N]: n;  B^T [N][K]: k
-  const int ra = L.io & kIoA16 ? 8 : 4, rb = L.io & kIoB16 ? 8 : 4;
+  const int ra = L.io & kIoA16 ? 8 : 4, rb = L.io & (kIoB16 | kIoB3) ? 8 : 4;
   if (!map_contig(a_contig, ra) || !map_contig(b_contig, rb)) return false;
   if (transA ? M % ra : 0) return false;
   if (transB ? 0 : N % rb) return false;
@@ -735,6 +741,7 @@ bool mapped_ok(int batch, int M, int N, int K, bool transA, bool transB, const G
   const long eb = map_max(L.b.b, batch) + map_max(L.b.r, transB ? N : K) + map_max(L.b.c, transB ? K : N) + 1;
   const long ec = map_max(L.c.b, batch) + map_max(L.c.r, (M + 127) / 128 * 128) + map_max(L.c.c, N) + 1;
   if (ea > L.ext_a || eb > L.ext_b || L.ext_a >= lim || L.ext_b >= lim || ec >= lim) return false;
+  if ((L.io & kIoB3) && (long)L.ext_b * 6 >= (1l << 31)) return false;  // the three planes' byte offsets
   return true;
 }
 }  // namespace

@@ -16,6 +16,9 @@ namespace k {
 const void* gemm_io_kernel(int ti, int v);
 // The same for the instances with a bf16 weight as B (k_gemm_io_w.hip).
 const void* gemm_io_weight_kernel(int ti, int v);
+// The same for the split-product instances with a weight's split copy as B
+// (kIoB3, k_gemm_io_x3.hip).
+const void* gemm_io_x3_kernel(int ti, int v);
 
 namespace {
 
@@ -37,6 +40,26 @@ constexpr int BK = 16;
 // X3: the f32 product on the bf16 MFMA from exact three-way splits of
 // both operands (k_split.h), the same slab step the fused attention
 // kernels run.
+// X3 with B read as its three stored pieces (kIoB3: a weight's split copy):
+// fb holds TN fragments of each plane, h first; words 0..3 of a fragment
+// hold its 8 bf16 values, as in a bf16-stored operand.  Only A is split.
+template <int TM, int TN>
+__device__ __forceinline__ void mfma_kstep_b3(const float (&fa)[TM][8], const float (&fb)[3 * TN][8],
+                                              v16f (&acc)[TM][TN]) {
+  Split3 a[TM], b[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) a[i] = split3(fa[i]);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    auto plane = [&](int p) {
+      const float(&f)[8] = fb[p * TN + j];
+      return __builtin_bit_cast(bf16x8, (v4f_raw){f[0], f[1], f[2], f[3]});
+    };
+    b[j] = Split3{plane(0), plane(1), plane(2)};
+  }
+  x3_slab<false, TM, TN>(a, b, acc);
+}
+
 template <int TM, int TN, bool BF, bool A16 = false, bool B16 = false, bool X3 = false>
 __device__ __forceinline__ void mfma_kstep(const float (&fa)[TM][8], const float (&fb)[TN][8], v16f (&acc)[TM][TN]) {
   static_assert(BF || !(A16 || B16), "bf16-stored operands run on the bf16 MFMA");
@@ -312,12 +335,14 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
                                                       const float* __restrict__ D, float* __restrict__ E) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int BM = 64 * TM, BN = 64 * TN;
-  constexpr bool A16 = IO & kIoA16, B16 = IO & kIoB16, C16 = IO & kIoC16, E16 = IO & kIoE16;
+  constexpr bool A16 = IO & kIoA16, B16 = IO & kIoB16, C16 = IO & kIoC16, E16 = IO & kIoE16, B3 = IO & kIoB3;
   static_assert(BF || IO == 0, "bf16 storage runs on the bf16 MFMA");
-  constexpr int ESA = A16 ? 2 : 4, ESB = B16 ? 2 : 4;
+  static_assert(!B3 || (X3 && !B16 && !A16), "a split copy of B feeds the split product");
+  constexpr int ESA = A16 ? 2 : 4, ESB = (B16 || B3) ? 2 : 4;
+  constexpr int NPB = B3 ? 3 : 1;  // planes of B (its h, m and l pieces)
   // A [M][K] and B^T [N][K] are k-contiguous
   using SlabA = std::conditional_t<A16, DmaSlab16<BM, !TA>, DmaSlab<BM, !TA>>;
-  using SlabB = std::conditional_t<B16, DmaSlab16<BN, TB>, DmaSlab<BN, TB>>;
+  using SlabB = std::conditional_t<B16 || B3, DmaSlab16<BN, TB>, DmaSlab<BN, TB>>;
   // Two-stage ring of KS 16-deep slabs per stage: stage st + 1 is in
   // flight while stage st is consumed.  Under autocast (BF) a slab's MFMA
   // work is one bf16 instruction per accumulator, so the barrier and the
@@ -327,11 +352,11 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
   // (Three- and four-stage rings measured no faster for either precision.)
   constexpr bool BFS = BF && !X3 && (BM + BN <= 256);
   constexpr int NS = 2, KS = BFS ? 2 : 1;
-  constexpr int PER_SLAB = SlabA::PER_WAVE + SlabB::PER_WAVE;  // DMA instructions per slab and wave
+  constexpr int PER_SLAB = SlabA::PER_WAVE + NPB * SlabB::PER_WAVE;  // DMA instructions per slab and wave
   // LDS reads of one slab's fragments (lgkmcnt is 4 bits)
-  constexpr int READS = TM * SlabA::READS + TN * SlabB::READS;
+  constexpr int READS = TM * SlabA::READS + NPB * TN * SlabB::READS;
   __shared__ __attribute__((aligned(1024))) float As[NS][KS][SlabA::SIZE];
-  __shared__ __attribute__((aligned(1024))) float Bs[NS][KS][SlabB::SIZE];
+  __shared__ __attribute__((aligned(1024))) float Bs[NS][KS][NPB * SlabB::SIZE];  // plane p at p * SIZE
 
   // Workgroups are dealt to the 8 XCDs round-robin in dispatch order (x
   // fastest, then y), and each XCD has its own L2.  Tile ids are remapped so
@@ -396,7 +421,8 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(reinterpret_cast<const float*>(reinterpret_cast<const char*>(Ap) + (long)ba * ESA),
                                                   (unsigned)((L.ext_a - ba) * ESA));
     const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(reinterpret_cast<const float*>(reinterpret_cast<const char*>(Bp) + (long)bb * ESB),
-                                                  (unsigned)((L.ext_b - bb) * ESB));
+                                                  (unsigned)(((long)NPB * L.ext_b - bb) * ESB));
+    const int plane_bytes = L.ext_b * ESB;  // B3: the m and l planes follow h
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -410,7 +436,9 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
       for (int u = 0; u < KS; ++u)
         if (st * KS + u < nk) {
           sa.issue(ra, As[buf][u], wave, ka.template bytes<ESA>(fak));
-          sb.issue(rb, Bs[buf][u], wave, kb.template bytes<ESB>(fbk));
+#pragma unroll
+          for (int p = 0; p < NPB; ++p)
+            sb.issue(rb, Bs[buf][u] + p * SlabB::SIZE, wave, kb.template bytes<ESB>(fbk) + p * plane_bytes);
           ka.advance(fak);
           kb.advance(fbk);
         }
@@ -427,11 +455,13 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
       else waitcnt_vm<0>();
       __builtin_amdgcn_s_barrier();
       const bool two = KS == 2 && st * KS + 1 < nk;
-      float fa[KS][TM][8], fb[KS][TN][8];
+      float fa[KS][TM][8], fb[KS][NPB * TN][8];
 #pragma unroll
       for (int i = 0; i < TM; ++i) SlabA::frag(As[cur][0], wm + 32 * i, fa[0][i]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][0], wn + 32 * j, fb[0][j]);
+      for (int p = 0; p < NPB; ++p)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][0] + p * SlabB::SIZE, wn + 32 * j, fb[0][p * TN + j]);
       __builtin_amdgcn_sched_barrier(0);
       // stage st - 1 (= st + NS - 1 mod NS) was last read before the barrier
       const int nxt = cur == 0 ? NS - 1 : cur - 1;
@@ -443,7 +473,8 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
 #pragma unroll
         for (int i = 0; i < TM; ++i) SlabA::frag(As[cur][KS - 1], wm + 32 * i, fa[KS - 1][i]);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) SlabB::frag(Bs[cur][KS - 1], wn + 32 * j, fb[KS - 1][j]);
+        for (int j = 0; j < NPB * TN; ++j)
+          SlabB::frag(Bs[cur][KS - 1] + (j / TN) * SlabB::SIZE, wn + 32 * (j % TN), fb[KS - 1][j]);
         // LDS reads complete in order: the first slab's are done when at
         // most the second slab's READS are outstanding
         if constexpr (READS <= 15) asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(READS) : "memory");
@@ -455,7 +486,8 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
       // a wave with MFMAs to issue goes ahead of the CU's other waves (measured
       // 1 % on the C5 step; raising it from the barrier on instead lost 2 %)
       __builtin_amdgcn_s_setprio(1);
-      mfma_kstep<TM, TN, BF, A16, B16, X3>(fa[0], fb[0], acc);
+      if constexpr (B3) mfma_kstep_b3<TM, TN>(fa[0], fb[0], acc);
+      else mfma_kstep<TM, TN, BF, A16, B16, X3>(fa[0], fb[0], acc);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (KS == 2) {
@@ -463,7 +495,8 @@ __global__ __launch_bounds__(256, 2) void k_sgemm_dma(const float* __restrict__ 
         __builtin_amdgcn_sched_barrier(0);
         if (two) {
           __builtin_amdgcn_s_setprio(1);
-          mfma_kstep<TM, TN, BF, A16, B16, X3>(fa[KS - 1], fb[KS - 1], acc);
+          if constexpr (B3) mfma_kstep_b3<TM, TN>(fa[KS - 1], fb[KS - 1], acc);
+          else mfma_kstep<TM, TN, BF, A16, B16, X3>(fa[KS - 1], fb[KS - 1], acc);
           __builtin_amdgcn_s_setprio(0);
         }
         __builtin_amdgcn_sched_barrier(0);

@@ -12,7 +12,7 @@ namespace {
 // 64 GELU epilogues, 128 grouped accumulation; io = v >> 9.
 template <int TM, int TN>
 const void* io_instance(int v) {
-  const int io = v >> 9;
+  const int io = (v >> 9) & 15;
   const bool ta = v & 8, tb = v & 4, mapped = v & 32, gelu = v & 64;
   if (v & 128) {  // the head projections' dx = dq Wq^T + dk Wk^T + dv Wv^T from bf16 dq, dk, dv
     if (!ta && tb && io == kIoA16)
@@ -58,6 +58,7 @@ const void* io_instance(int v) {
 }  // namespace
 
 const void* gemm_io_kernel(int ti, int v) {
+  if ((v >> 9) & kIoB3) return gemm_io_x3_kernel(ti, v);  // a weight's split copy
   // B in bf16 outside the weight-gradient forms: a weight's bf16 copy
   if (((v >> 9) & kIoB16) && !(v & 8)) return gemm_io_weight_kernel(ti, v);
   switch (ti) {  // the host's tile table: 128x192, 128x128, 128x64, 64x128, 64x64

@@ -19,7 +19,7 @@ const void* inst() {
 template <int TM, int TN>
 const void* weight_instance(int v) {
   constexpr int A = kIoA16, B = kIoB16, C = kIoC16, E = kIoE16;
-  const int io = v >> 9;
+  const int io = (v >> 9) & 15;
   const bool ta = v & 8, tb = v & 4, mapped = v & 32, gelu = v & 64;
   if (ta) return nullptr;  // weight gradients take no weight operand
   if (v & 128) {           // the head projections' dx = dq Wq^T + dk Wk^T + dv Wv^T

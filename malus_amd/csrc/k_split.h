@@ -109,9 +109,6 @@ __device__ __forceinline__ v16f x3_one(const Split3& a, const Split3& b, v16f c)
 
 }  // namespace
 
-// Whether f32 GEMMs (and the fused attention kernels, which reproduce the
-// composed GEMMs' bits) compute their products as split bf16 pieces.
-bool gemm_f32_split();
 
 }  // namespace k
 }  // namespace malus

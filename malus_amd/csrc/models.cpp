@@ -133,6 +133,7 @@ struct Gpt {
   // Under autocast, the activations whose only readers are bf16 GEMMs are
   // stored in bf16 (see block_forward), and the blocks' weight matrices get
   // bf16 copies for the GEMMs (refresh_weight_copies); w16[i] is param i's.
+  // With split f32 products the weight matrices get split copies instead.
   bool bf16_act = true;
   std::vector<int64_t> w16;
   std::vector<int64_t> p, m, v;  // block l params at 8l..8l+7, then wte, wpe, ln_f, lm_head
@@ -151,14 +152,29 @@ bool storage_policy(const Gpt& g) {
          C <= 512 && N % 8 == 0;
 }
 
-// Under the storage policy, bf16 copies of the blocks' weight matrices (q,
-// k, v, o, W1, W2) for the GEMMs that read them (forward products and the
-// dx products of the VJPs), refreshed in one launch at every forward: those
-// products round their operands to bf16 anyway, so every value is the same,
-// and the GEMMs move half the weight bytes.  A copy stands for its weight
-// only while the weight is unchanged (TensorBuffer::bf16_copy).
+// With split f32 products (the default f32 GEMM arithmetic), outside
+// autocast: the same operand copies as split copies (below), on shapes the
+// split-copy kernels take.
+bool split_policy(const Gpt& g) {
+  return g.bf16_act && !k::autocast_on() && k::gemm_f32_split() && g.C % 16 == 0;
+}
+
+// Operand copies of the blocks' weight matrices (q, k, v, o, W1, W2) for
+// the GEMMs that read them as B, refreshed in one launch at every forward;
+// a copy stands for its weight only while the weight is unchanged
+// (TensorBuffer::bf16_copy).
+// - Under the storage policy, bf16 copies for the forward products and the
+//   dx products of the VJPs: those products round their operands to bf16
+//   anyway, so every value is the same, and the GEMMs move half the weight
+//   bytes.
+// - With split f32 products, split copies for the forward products: the
+//   three bf16 planes of each value's pieces, formed once per step by the
+//   split the GEMMs would run in every workgroup, so every product is the
+//   same and those GEMMs split only their A operand (C5: 9.36 -> 9.26 ms;
+//   the dx products read the planes slower than they split the weight).
 void refresh_weight_copies(Gpt& g) {
-  if (!storage_policy(g)) return;
+  const bool split = split_policy(g);
+  if (!split && !storage_policy(g)) return;
   if (g.w16.size() != g.p.size()) g.w16.assign(g.p.size(), 0);
   std::vector<k::Bf16Copy> segs;
   std::vector<TensorBuffer*> ws;
@@ -167,7 +183,24 @@ void refresh_weight_copies(Gpt& g) {
       const size_t i = 8 * (size_t)l + j;
       TensorBuffer* w = T(g.p[i]);
       if (w->dtype != F32) continue;
-      if (!g.w16[i]) g.w16[i] = malus::H(alloc_tensor(BF16, w->shape, w->ndim));
+      if (g.w16[i] && T(g.w16[i])->split3 != split) {  // the other kind: replace it
+        TensorBuffer* old = T(g.w16[i]);
+        if (w->bf16_copy == old) {
+          w->bf16_copy = nullptr;
+          release(old);
+        }
+        rel({g.w16[i]});
+        g.w16[i] = 0;
+      }
+      if (!g.w16[i]) {
+        TensorBuffer* c = alloc_tensor(BF16, w->shape, w->ndim);
+        if (split) {  // three planes of the weight's layout
+          pool_free(c->st->ptr, c->st->bytes);
+          c->st->ptr = pool_alloc(3 * w->len * sizeof(uint16_t), &c->st->bytes);
+          c->split3 = true;
+        }
+        g.w16[i] = malus::H(c);
+      }
       TensorBuffer* c = T(g.w16[i]);
       if (w->bf16_copy != c) {  // the weight's handle is new (updates that replace it)
         retain(c);
@@ -178,8 +211,9 @@ void refresh_weight_copies(Gpt& g) {
       ws.push_back(w);
     }
   if (segs.empty()) return;
-  k::to_bf16_multi(segs.data(), (int)segs.size(), stream());
-  const uint64_t seq = enqueue_mark("weights_bf16");
+  if (split) k::to_split3_multi(segs.data(), (int)segs.size(), stream());
+  else k::to_bf16_multi(segs.data(), (int)segs.size(), stream());
+  const uint64_t seq = enqueue_mark(split ? "weights_split3" : "weights_bf16");
   for (TensorBuffer* w : ws) {
     TensorBuffer* c = w->bf16_copy;
     c->write_seq = seq;

@@ -44,16 +44,22 @@ int gemm_io(const TensorBuffer* a, const TensorBuffer* b, const char* what) {
   for (const TensorBuffer* t : {a, b})
     if (t->dtype != F32 && t->dtype != BF16)
       fail("malus: %s expects Tensor<f32> or Tensor<bf16> operands, got dtype tag %d", what, t->dtype);
-  return (a->dtype == BF16 ? k::kIoA16 : 0) | (b->dtype == BF16 ? k::kIoB16 : 0);
+  if (a->split3) fail("malus: %s: a split copy is read only as B", what);
+  return (a->dtype == BF16 ? k::kIoA16 : 0) | (b->split3 ? k::kIoB3 : b->dtype == BF16 ? k::kIoB16 : 0);
 }
 
-// The tensor a GEMM reads for operand t: under autocast, t's bf16 copy
-// when it holds t's current values (refreshed after t's last write); the
-// bf16 MFMA rounds t to those values anyway.
-const TensorBuffer* gemm_operand(const TensorBuffer* t) {
+// The tensor a GEMM reads for operand t: t's copy when it holds t's
+// current values (refreshed after t's last write).  Under autocast that is
+// t's bf16 copy (the bf16 MFMA rounds t to those values anyway).  With
+// split f32 products it is t's split copy (the pieces the product would
+// split t into, so the same bits), for the B operand of a GEMM with neither
+// operand transposed (split_b: the forward products; on the NT dx products
+// the three planes measured slower than splitting the weight in place).
+const TensorBuffer* gemm_operand(const TensorBuffer* t, bool split_b = false) {
   const TensorBuffer* c = t->bf16_copy;
-  if (c && k::autocast_on() && c->copy_of == t && c->copy_seq == t->write_seq) return c;
-  return t;
+  if (!c || c->copy_of != t || c->copy_seq != t->write_seq) return t;
+  if (c->split3) return split_b && !k::autocast_on() && k::gemm_f32_split() ? c : t;
+  return k::autocast_on() ? c : t;
 }
 
 int64_t done(TensorBuffer* t, const char* name) {
@@ -215,7 +221,7 @@ TensorBuffer* as_i32_indices(TensorBuffer* idx, bool* owned) {
 int64_t gemm_out(const TensorBuffer* a, const TensorBuffer* b, bool ta, bool tb, int batch, int M, int N, int K, long sA,
                  long sB, const size_t* oshape, int ond, const TensorBuffer* addend = nullptr) {
   a = gemm_operand(a);
-  b = gemm_operand(b);
+  b = gemm_operand(b, !ta && !tb);
   const int io = gemm_io(a, b, "matmul");
   TensorBuffer* c = alloc_tensor(F32, oshape, ond);
   if (addend && (addend->dtype != F32 || addend->len != c->len))
@@ -999,7 +1005,7 @@ int64_t ln_affine_bwd_xw(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const
 // epilogue (nothing launched).  x may be bf16; ge_bf16 stores ge in bf16
 // (for a caller whose readers of ge are bf16 GEMMs); h stays f32.
 int64_t matmul_gelu_fwd(int64_t hx, int64_t hw, int64_t* ge_out, bool ge_bf16) {
-  const TensorBuffer *x = gemm_operand(T(hx)), *w = gemm_operand(T(hw));
+  const TensorBuffer *x = gemm_operand(T(hx)), *w = gemm_operand(T(hw), true);
   if (x->ndim != 2 || w->ndim != 2 || x->shape[1] != w->shape[0]) return 0;
   const int io = gemm_io(x, w, "matmul") | (ge_bf16 ? k::kIoE16 : 0);
   const size_t M = x->shape[0], K = x->shape[1], N = w->shape[1];
@@ -1093,7 +1099,7 @@ int64_t mapped(const TensorBuffer* a, const TensorBuffer* b, TensorBuffer* c, bo
                int K, const GemmLayouts& L, const TensorBuffer* D, const char* what) {
   check_addend(D, c);
   a = gemm_operand(a);
-  b = gemm_operand(b);
+  b = gemm_operand(b, !ta && !tb);
   GemmLayouts Lio = L;
   Lio.io = gemm_io(a, b, what);
   KTimer* kt = ktimer_begin("gemm");
@@ -1150,7 +1156,7 @@ void head_proj_fwd3(int64_t hx, const int64_t* hw, size_t B, size_t T, size_t H,
   GemmLayouts L{dense_layout((long)x->shape[1], 0), dense_layout((long)C, 0), heads_as_rows(T, H, hs), (int)x->len,
                 (int)w0->len};
   L.ngroup = 3;
-  const TensorBuffer* w[3] = {gemm_operand(w0), gemm_operand(T_(hw[1])), gemm_operand(T_(hw[2]))};
+  const TensorBuffer* w[3] = {gemm_operand(w0, true), gemm_operand(T_(hw[1]), true), gemm_operand(T_(hw[2]), true)};
   L.io = gemm_io(x, w[0], "head_proj_fwd3") | (out_bf16 ? k::kIoC16 : 0);
   TensorBuffer* o[3];
   for (int g = 0; g < 3; ++g) {

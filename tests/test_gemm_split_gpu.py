@@ -160,3 +160,31 @@ def test_set_f32_split_returns_previous(rt):
         assert L.malus_gemm_set_f32_split(1) == 1
     finally:
         L.malus_gemm_set_f32_split(prev)
+
+
+def test_weight_split_copies_give_the_same_steps(rt):
+    # With split products the model's forward GEMMs read B from split copies
+    # of the block weights (three bf16 planes, refreshed each forward)
+    # instead of splitting the weights themselves: three steps
+    # with the copies (malus_gpt_set_bf16_activations 1, the default) equal
+    # three without, bit for bit (losses, parameters and both moments).
+    from tests.test_models_gpu import GpuGpt, tokens
+
+    cfg = dict(V=65, T=64, C=128, H=4, L=2, B=8)
+    x, y = tokens(cfg, 777)
+    out = []
+    with split_mode(rt, True):
+        for copies in (1, 0):
+            g = GpuGpt(rt, cfg)
+            try:
+                rt.L.malus_gpt_set_bf16_activations(g.g, copies)
+                losses = [g.step(x, y, t) for t in (1, 2, 3)]
+                state = [g.param(i) for i in range(8 * cfg["L"] + 4)]
+                state += [rt.numpy(rt.L.malus_gpt_moment(g.g, i, m)).ravel() for m in (0, 1)
+                          for i in range(8 * cfg["L"] + 4)]
+            finally:
+                g.close()
+            out.append((losses, state))
+    assert out[0][0] == out[1][0]
+    for i, (u, v) in enumerate(zip(out[0][1], out[1][1])):
+        np.testing.assert_array_equal(u, v, err_msg=f"state {i}")
