@@ -193,11 +193,16 @@ void refresh_weight_copies(Gpt& g) {
         g.w16[i] = 0;
       }
       if (!g.w16[i]) {
-        TensorBuffer* c = alloc_tensor(BF16, w->shape, w->ndim);
-        if (split) {  // three planes of the weight's layout
-          pool_free(c->st->ptr, c->st->bytes);
-          c->st->ptr = pool_alloc(3 * w->len * sizeof(uint16_t), &c->st->bytes);
+        TensorBuffer* c;
+        if (split) {  // storage for three planes; the tensor describes plane h, in the weight's layout
+          const size_t n3[1] = {3 * w->len};
+          c = alloc_tensor(BF16, n3, 1);
+          c->ndim = w->ndim;
+          for (int d = 0; d < w->ndim; ++d) c->shape[d] = w->shape[d];
+          c->len = w->len;
           c->split3 = true;
+        } else {
+          c = alloc_tensor(BF16, w->shape, w->ndim);
         }
         g.w16[i] = malus::H(c);
       }
