@@ -403,23 +403,19 @@ Plan plan_gemm(int batch, int M, int N, int K, int v, bool tri = false, int only
   // time, and the 128x192 tile (more MFMA work per staged byte) with the
   // cost model's split measured 10-20 % faster on the same shapes.
   const bool wgrad = (v & 16) && (v & 8) && batch == 1 && K >= 4096 && g_forced_tile < 0 && g_split_target == 0;
-  // The split f32 product (six bf16 MFMAs per staged f32 slab) is bound by
-  // moving f32 operands through L2 and LDS, so wider tiles (fewer staged
-  // bytes per product) pay where the grid still fills the chip.  Per call
-  // in the C5 step (kernel trace, 128x64 against the wider tile): the three
-  // grouped q/k/v weight gradients 124 -> 114 us on 128x128 with the cost
-  // model's split, and the K = 1536, N = 384 products (fc2, fc1's dX)
-  // 141-148 -> 137-141 us on 128x128 with a split of 2.  The single 384x384
-  // weight gradient (41 against 53 us), the 1536-wide ones and the GELU VJP
-  // (160 against 226 us: the wider tiles lose its epilogue prefetch) keep
-  // the f32 plan; the GELU forward takes 128x192 (153 -> 135 us) from the
-  // caller.
+  // The split f32 product (six bf16 MFMAs per staged f32 slab) favours
+  // wider tiles (fewer staged bytes per product) where the grid still fills
+  // the chip.  Per call in the C5 step (kernel trace, 128x64 against the
+  // wider tile): the three grouped q/k/v weight gradients 124 -> 114 us on
+  // 128x128 with the cost model's split.  The single 384x384 weight
+  // gradient (41 against 53 us), the 1536-wide ones, the GELU VJP (160
+  // against 226 us: the wider tiles lose its epilogue prefetch) and the
+  // K = 1536, N = 384 products keep the f32 plan (128x128 with a split of 2
+  // gained 3-7 us a call before the forward GEMMs read split weights, and
+  // measured 0.3 % slower on the step after); the GELU forward takes
+  // 128x192 (153 -> 135 us) from the caller.
   const bool wgrad_bf = wgrad && (g_autocast || bf || (x3 && groups > 1));
   if (wgrad_bf) only_tile = x3 && !g_autocast && !bf ? 1 : 0;  // kTiles[0] = 128x192, kTiles[1] = 128x128
-  const long tiles128 = (long)((M + 127) / 128) * ((N + 127) / 128) * batch;
-  if (x3 && !wgrad && (v & 16) && !(v & 64) && only_tile < 0 && g_forced_tile < 0 && batch == 1 && K >= 1024 &&
-      tiles128 >= 256)
-    only_tile = 1;
   // the occupancy the cost model sees: the split kernels' own for the wide
   // tiles picked above (it sets their K split), else the f32 kernels'
   const int occ_v = x3 && only_tile >= 0 ? (v & ~64) | kVarX3 : v & ~64;
