@@ -52,9 +52,9 @@ enum Op : int32_t {
   TAG_LN_SCALE = 104, TAG_GELU_MATMUL = 105, TAG_FLASH = 106  // fused nodes (tape.cpp)
 };
 
-// Attention kernel choice: AUTO takes flash attention under autocast, else
-// the row-register kernel where its shapes are built, else flash attention,
-// else the composed ops.
+// Attention kernel choice: AUTO takes flash attention under autocast and,
+// with split f32 products, from T = 256 on; else the row-register kernel
+// where its shapes are built, else flash attention, else the composed ops.
 enum AttnMode : int { ATTN_AUTO = 0, ATTN_FLASH = 1, ATTN_ROWS = 2, ATTN_COMPOSED = 3 };
 
 // grad-tracked binop: lower + tape_record_binop (codegen-cpu/lib.rs:1531-1552)
@@ -262,11 +262,14 @@ int64_t block_forward(Gpt& g, int l, int64_t x) {
   };
   const bool rows_ok = fused_heads && k::attn_scores_supported(B * H, Tn, hs);
   const bool flash_ok = fused_heads && k::flash_supported(B * H, Tn, hs);
-  // AUTO: in f32 the row-register kernel where it is built (at T = 256 its
-  // backward reads the stored P instead of recomputing it, and is faster);
-  // under autocast flash attention, whose products run on the bf16 MFMA
-  const bool flash = flash_ok && (g.attn_mode == ATTN_FLASH ||
-                                  (g.attn_mode == ATTN_AUTO && (!rows_ok || k::autocast_on())));
+  // AUTO: flash attention under autocast (its products on the bf16 MFMA)
+  // and, with split f32 products, from T = 256 on (C5: 8.90-8.92 against
+  // 8.94 ms/step with the row-register kernels, three interleaved pairs; P,
+  // 9/16 of [B*H, T, T] f32 a layer, is never written); else the
+  // row-register kernel where it is built (with the FP32 MFMA's products its
+  // backward, which reads the stored P, is the faster one).
+  const bool auto_flash = !rows_ok || k::autocast_on() || (k::gemm_f32_split() && Tn >= 256);
+  const bool flash = flash_ok && (g.attn_mode == ATTN_FLASH || (g.attn_mode == ATTN_AUTO && auto_flash));
   const bool fused_attention = !flash && rows_ok && (g.attn_mode == ATTN_AUTO || g.attn_mode == ATTN_ROWS);
   // Under the storage policy flash attention reads q, k, v only as bf16 MFMA
   // operands, and their gradients feed only bf16 GEMMs: all six in bf16.

@@ -162,15 +162,17 @@ def test_failed_graph_create_leaves_eager_steps_unchanged(rt):
 C5 = dict(V=65, T=256, C=384, H=6, L=6, B=64)
 
 
-@pytest.mark.parametrize("autocast", [False, True], ids=["f32_rows_attention", "autocast_flash"])
-def test_c5_graph_replays_equal_eager_steps(rt, autocast):
+@pytest.mark.parametrize("autocast,attention", [(False, 2), (False, 0), (True, 0)],
+                         ids=["f32_rows_attention", "f32_auto_flash_attention", "autocast_flash"])
+def test_c5_graph_replays_equal_eager_steps(rt, autocast, attention):
     """The headline workload as the bench runs it: C5 (examples/nanogpt_modular.ml
     step, lines 167-189) captured once with its token draw and replayed.  At
     B*T = 16,384 tokens the weight-gradient GEMMs split K (partials summed by
     the split reduction in pool memory the capture reserves), the q/k/v
     projections run grouped, and the attention is the row-register kernel
-    pair in f32 (its tiles above the diagonal left unwritten) or flash
-    attention under autocast.  The replayed steps draw their ids on the
+    pair (its tiles above the diagonal left unwritten) or flash attention
+    (the automatic choice at C5, in f32 with split products and under
+    autocast).  The replayed steps draw their ids on the
     device (call indices past 2^32, so both key words move); eager steps get
     the oracle's draw of the same calls uploaded.  Replays equal eager steps
     bit for bit (losses, parameters, both moments); in f32 the first two
@@ -181,6 +183,7 @@ def test_c5_graph_replays_equal_eager_steps(rt, autocast):
     batches = [(O.rand_tokens(cx, n, C5["V"]), O.rand_tokens(cy, n, C5["V"])) for cx, cy in calls]
     with M.autocast(autocast):
         g = make(rt, C5)
+        rt.L.malus_gpt_set_attention(g, attention)
         eager = []
         for k, (x, y) in enumerate(batches):
             hx, hy = rt.tensor(x), rt.tensor(y)
@@ -192,6 +195,7 @@ def test_c5_graph_replays_equal_eager_steps(rt, autocast):
         rt.L.tape_reset()
 
         g = make(rt, C5)
+        rt.L.malus_gpt_set_attention(g, attention)
         l0 = C.c_int64()
         gr = rt.L.malus_gpt_graph_create_drawn(g, calls[0][0], calls[0][1], 1, C.byref(l0))
         assert gr, rt.last_error()
@@ -206,7 +210,7 @@ def test_c5_graph_replays_equal_eager_steps(rt, autocast):
         rt.L.malus_gpt_graph_free(gr)
         rt.L.malus_gpt_free(g)
         rt.L.tape_reset()
-    print(f"C5 {'autocast' if autocast else 'f32'} losses: graph {graph} eager {eager}")
+    print(f"C5 {'autocast' if autocast else 'f32'} attention {attention} losses: graph {graph} eager {eager}")
     np.testing.assert_array_equal(np.array(graph), np.array(eager))
     for i, (a, b) in enumerate(zip(graph_state, eager_state)):
         assert np.array_equal(a, b), f"state tensor {i} differs between the graph and the eager steps"

@@ -165,6 +165,7 @@ def test_gpt_fusions_equal_separate_ops(rt, cfg):
     for fa in (True, False):
         rt.L.malus_tape_set_fused_vjps(int(fa))
         g = GpuGpt(rt, cfg, fused_forward=fa)
+        rt.L.malus_gpt_set_attention(g.g, 2)  # the row-register fused kernels where built (not flash)
         try:
             loss = g.loss_and_grads(x, y)
             grads = [g.grad(i) for i in range(8 * cfg["L"] + 4)]
@@ -197,6 +198,7 @@ def test_fused_attention_unwritten_tiles(rt, cfg):
         rt.free(*poison)
         rt.L.malus_tape_set_fused_vjps(int(fv))
         g = GpuGpt(rt, cfg, fused_forward=True)
+        rt.L.malus_gpt_set_attention(g.g, 2)  # the row-register fused kernels
         try:
             loss = g.loss_and_grads(x, y)
             grads = [g.grad(i) for i in range(8 * cfg["L"] + 4)]
