@@ -102,128 +102,127 @@ __global__ __launch_bounds__(256) void k_emb_accum(const float* __restrict__ dou
 
 // Two-launch form for small vocabularies (v * t list slots fit the pool).
 // k_emb_list: block per vocab row v writes the positions of its tokens, in
-// increasing order, at pos[v * t ..] and their count.  Thread i owns the
-// contiguous tokens [i * per, (i + 1) * per) (per a multiple of 4, read as
-// int4 with VEC); a block exclusive scan of the per-thread hit counts
-// (thread order = token order) places them.
+// increasing order, at pos[v * t ..] and their count.  The tokens are taken
+// in passes of 1024 x 16: thread i owns the 16 contiguous tokens
+// [16 i, 16 i + 16) of a pass and keeps them in registers from its count to
+// its writes (four int4 loads with VEC, all in flight together); a block
+// exclusive scan of the per-thread hit counts (thread order = token order)
+// places them.
 template <bool VEC>
-__global__ __launch_bounds__(256) void k_emb_list(const int32_t* __restrict__ idx, size_t t, uint32_t* __restrict__ pos,
-                                                  uint32_t* __restrict__ count) {
-  __shared__ uint32_t wave_tot[4];
+__global__ __launch_bounds__(1024) void k_emb_list(const int32_t* __restrict__ idx, size_t t, uint32_t* __restrict__ pos,
+                                                   uint32_t* __restrict__ count) {
+  constexpr int kWaves = 16, kPer = 16;
+  __shared__ uint32_t wave_tot[kWaves];
   const int32_t v = (int32_t)blockIdx.x;
-  const size_t per = ((t + 255) / 256 + 3) / 4 * 4;
-  const size_t beg = min(t, (size_t)threadIdx.x * per), end = min(t, beg + per);
-  const int4* idx4 = reinterpret_cast<const int4*>(idx);
-  uint32_t c = 0;
-  if (VEC) {  // t % 4 == 0, so [beg, end) is whole int4s
-#pragma unroll 4
-    for (size_t q = beg / 4; q < end / 4; ++q) {
-      const int4 x = idx4[q];
-      c += (x.x == v ? 1u : 0u) + (x.y == v ? 1u : 0u) + (x.z == v ? 1u : 0u) + (x.w == v ? 1u : 0u);
-    }
-  } else {
-#pragma unroll 4
-    for (size_t i = beg; i < end; ++i) c += idx[i] == v ? 1u : 0u;
-  }
-  // inclusive scan over the wave, then over the four waves
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-  uint32_t inc = c;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t o = __shfl_up(inc, off, 64);
-    if (lane >= off) inc += o;
-  }
-  if (lane == 63) wave_tot[wave] = inc;
-  __syncthreads();
-  uint32_t base = inc - c;
-  for (int q = 0; q < wave; ++q) base += wave_tot[q];
   uint32_t* out = pos + (size_t)blockIdx.x * t;
-  if (c) {
-    if (VEC) {
-#pragma unroll 4
-      for (size_t q = beg / 4; q < end / 4; ++q) {
-        const int4 x = idx4[q];
-        const uint32_t i = (uint32_t)(4 * q);
-        if (x.x == v) out[base++] = i;
-        if (x.y == v) out[base++] = i + 1;
-        if (x.z == v) out[base++] = i + 2;
-        if (x.w == v) out[base++] = i + 3;
+  uint32_t done = 0;  // hits in earlier passes
+  for (size_t s = 0; s < t; s += (size_t)kPer * 1024) {
+    const size_t beg = s + (size_t)kPer * threadIdx.x;
+    int32_t x[kPer];
+    if (VEC) {  // t % 4 == 0 and idx 16-byte aligned: whole int4s up to t
+#pragma unroll
+      for (int u = 0; u < kPer / 4; ++u) {
+        int4 q = make_int4(-1, -1, -1, -1);
+        if (beg + 4 * u + 4 <= t) q = reinterpret_cast<const int4*>(idx + beg)[u];
+        x[4 * u] = q.x;
+        x[4 * u + 1] = q.y;
+        x[4 * u + 2] = q.z;
+        x[4 * u + 3] = q.w;
       }
     } else {
-      for (size_t i = beg; i < end; ++i)
-        if (idx[i] == v) out[base++] = (uint32_t)i;
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) x[u] = beg + u < t ? idx[beg + u] : -1;
     }
+    uint32_t c = 0;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) c += x[u] == v ? 1u : 0u;
+    // inclusive scan over the wave, then over the waves
+    uint32_t inc = c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += o;
+    }
+    if (lane == 63) wave_tot[wave] = inc;
+    __syncthreads();
+    uint32_t base = done + inc - c, pass = 0;
+#pragma unroll
+    for (int q = 0; q < kWaves; ++q) {
+      base += q < wave ? wave_tot[q] : 0u;
+      pass += wave_tot[q];
+    }
+    if (c) {
+#pragma unroll
+      for (int u = 0; u < kPer; ++u)
+        if (x[u] == v) out[base++] = (uint32_t)(beg + u);
+    }
+    done += pass;
+    __syncthreads();  // wave_tot is rewritten by the next pass
   }
-  if (threadIdx.x == 255) count[blockIdx.x] = base;
+  if (threadIdx.x == 0) count[blockIdx.x] = done;
 }
 
-// k_emb_rows: dw[v, 4c .. 4c + 3] = the sum of dout[t, 4c ..] over row v's
-// token list, in list order (the same adds as k_emb_accum).  One lane per
-// (row, 4-column group), lanes packed across rows.  Each chain is a run of
-// dependent adds over its list, so the list is walked in batches of R
-// float4 loads that are all in flight before their adds, with the next
-// batch's positions loaded meanwhile (a chain of ~250 tokens then costs a
-// handful of memory round trips instead of one per 16 tokens).
-template <int R>
-__global__ __launch_bounds__(64) void k_emb_rows(const float4* __restrict__ dout, const uint32_t* __restrict__ pos,
-                                                 const uint32_t* __restrict__ count, float4* __restrict__ dw, size_t t,
-                                                 uint32_t d4, uint32_t chains) {
-  static_assert(R % 4 == 0, "positions are loaded four at a time");
-  const uint32_t g = blockIdx.x * 64 + threadIdx.x;
-  if (g >= chains) return;
-  const uint32_t row = g / d4, c = g % d4;
+// k_emb_cols: dw[v, c0 .. c0 + 32) = the sum of dout[p, c0 ..] over row v's
+// token list p, in list order (the same adds as k_emb_accum).  Block
+// (32-column block, row v), 256 threads.  Each sum is a chain of dependent
+// adds, so the rows the list names are staged through LDS CH tokens at a
+// time by all the block's threads (a token's 128-byte segment read by 8
+// lanes as float4, 32 tokens per pass); lanes 0..31 of wave 0 then add the
+// chunk in list order, one column each, while the next chunk's loads are in
+// flight.  The list slot holds t entries, so the first chunk's positions are
+// read beside the count that bounds them (entries past the count are never
+// used as addresses), and each later chunk's a chunk ahead of its loads.
+template <int CH>
+__global__ __launch_bounds__(256) void k_emb_cols(const float* __restrict__ dout, const uint32_t* __restrict__ pos,
+                                                  const uint32_t* __restrict__ count, float* __restrict__ dw, size_t t,
+                                                  uint32_t d) {
+  constexpr int kW = 32, kLoads = CH / 32;
+  static_assert(CH % 32 == 0, "32 tokens per pass");
+  __shared__ float4 buf[CH * kW / 4];
+  const uint32_t row = blockIdx.y, c0 = blockIdx.x * kW;
+  const uint32_t* p = pos + (size_t)row * t;
+  const uint32_t seg = threadIdx.x % 8, tok = threadIdx.x / 8;
+  const bool col_ok = c0 + 4 * seg < d;  // d % 4 == 0: a float4 is wholly in or out
+  const float4* src = reinterpret_cast<const float4*>(dout + c0) + seg;
+  const size_t d4 = d / 4;
+  uint32_t pn[kLoads];
+#pragma unroll
+  for (int j = 0; j < kLoads; ++j) pn[j] = tok + 32 * j < t ? p[tok + 32 * j] : 0u;
   const uint32_t n = count[row];
-  const uint32_t* p = pos + (size_t)row * t;  // R > 0: 16-byte aligned (the host takes this form for t % 4 == 0)
-  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  uint32_t k = 0;
-  if constexpr (R > 0) {
-    uint4 ix[R / 4];
-    if (R <= n) {
+  float4 r[kLoads];
 #pragma unroll
-      for (int u = 0; u < R / 4; ++u) ix[u] = reinterpret_cast<const uint4*>(p)[u];
-    }
-    for (; k + R <= n; k += R) {
-      float4 a[R];
+  for (int j = 0; j < kLoads; ++j) {
+    r[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (col_ok && tok + 32 * j < n) r[j] = src[(size_t)pn[j] * d4];
+  }
 #pragma unroll
-      for (int u = 0; u < R / 4; ++u) {
-        a[4 * u] = dout[(size_t)ix[u].x * d4 + c];
-        a[4 * u + 1] = dout[(size_t)ix[u].y * d4 + c];
-        a[4 * u + 2] = dout[(size_t)ix[u].z * d4 + c];
-        a[4 * u + 3] = dout[(size_t)ix[u].w * d4 + c];
-      }
-      if (k + 2 * R <= n) {
+  for (int j = 0; j < kLoads; ++j) pn[j] = CH + tok + 32 * j < n ? p[CH + tok + 32 * j] : 0u;
+  float acc = 0.0f;
+  const float* lds = reinterpret_cast<const float*>(buf) + threadIdx.x;  // wave 0: lane = column
+  for (uint32_t k = 0; k < n; k += CH) {
+    const uint32_t m = min((uint32_t)CH, n - k);
 #pragma unroll
-        for (int u = 0; u < R / 4; ++u) ix[u] = reinterpret_cast<const uint4*>(p + k + R)[u];
-      }
+    for (int j = 0; j < kLoads; ++j)
+      if (tok + 32 * j < m) buf[(tok + 32 * j) * (kW / 4) + seg] = r[j];
+    __syncthreads();
+    if (k + CH < n) {  // chunk k + CH's loads (positions in pn), then chunk k + 2 CH's positions
 #pragma unroll
-      for (int u = 0; u < R; ++u) {
-        acc.x += a[u].x;
-        acc.y += a[u].y;
-        acc.z += a[u].z;
-        acc.w += a[u].w;
+      for (int j = 0; j < kLoads; ++j)
+        if (col_ok && k + CH + tok + 32 * j < n) r[j] = src[(size_t)pn[j] * d4];
+#pragma unroll
+      for (int j = 0; j < kLoads; ++j) {
+        const uint32_t i = k + 2 * CH + tok + 32 * j;
+        pn[j] = i < n ? p[i] : 0u;
       }
     }
-  }
-  for (; k + 8 <= n; k += 8) {
-    float4 a[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] = dout[(size_t)p[k + u] * d4 + c];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      acc.x += a[u].x;
-      acc.y += a[u].y;
-      acc.z += a[u].z;
-      acc.w += a[u].w;
+    if (threadIdx.x < kW) {
+#pragma unroll 16
+      for (uint32_t i = 0; i < m; ++i) acc += lds[i * kW];
     }
+    __syncthreads();  // the chunk is read before the next one is stored
   }
-  for (; k < n; ++k) {
-    const float4 a = dout[(size_t)p[k] * d4 + c];
-    acc.x += a.x;
-    acc.y += a.y;
-    acc.z += a.z;
-    acc.w += a.w;
-  }
-  dw[(size_t)row * d4 + c] = acc;
+  if (threadIdx.x < kW && c0 + threadIdx.x < d) dw[(size_t)row * d + c0 + threadIdx.x] = acc;
 }
 
 struct PermDesc {
@@ -333,19 +332,18 @@ void embedding_bwd(const float* dout, const int32_t* idx, float* dw, size_t t, s
   if (!t) { fill(dw, 0.0f, v * d, s); return; }
   size_t b_count, b_offs, b_pos;
   const auto aligned = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  if (d % 4 == 0 && v * t <= ((size_t)1 << 24) && v * (d / 4) < ((size_t)1 << 31) && aligned(dout) && aligned(dw)) {
+  if (d % 4 == 0 && v * t <= ((size_t)1 << 24) && v <= 65535 && d < ((size_t)1 << 31) && aligned(dout) && aligned(dw)) {
     uint32_t* count = static_cast<uint32_t*>(pool_alloc(v * sizeof(uint32_t), &b_count));
     uint32_t* pos = static_cast<uint32_t*>(pool_alloc(v * t * sizeof(uint32_t), &b_pos));
-    if (t % 4 == 0 && aligned(idx)) k_emb_list<true><<<(unsigned)v, 256, 0, s>>>(idx, t, pos, count);
-    else k_emb_list<false><<<(unsigned)v, 256, 0, s>>>(idx, t, pos, count);
+    if (t % 4 == 0 && aligned(idx)) k_emb_list<true><<<(unsigned)v, 1024, 0, s>>>(idx, t, pos, count);
+    else k_emb_list<false><<<(unsigned)v, 1024, 0, s>>>(idx, t, pos, count);
     MALUS_HIP(hipGetLastError());
-    const uint32_t d4 = (uint32_t)(d / 4), chains = (uint32_t)(v * d4);
-    if (t % 4 == 0)
-      k_emb_rows<48><<<(chains + 63) / 64, 64, 0, s>>>(reinterpret_cast<const float4*>(dout), pos, count,
-                                                        reinterpret_cast<float4*>(dw), t, d4, chains);
-    else
-      k_emb_rows<0><<<(chains + 63) / 64, 64, 0, s>>>(reinterpret_cast<const float4*>(dout), pos, count,
-                                                       reinterpret_cast<float4*>(dw), t, d4, chains);
+    // chunk size from the mean list length: one chunk for most rows
+    const dim3 grid((unsigned)((d + 31) / 32), (unsigned)v);
+    const size_t mean = t / v;
+    if (mean > 128) k_emb_cols<256><<<grid, 256, 0, s>>>(dout, pos, count, dw, t, (uint32_t)d);
+    else if (mean > 64) k_emb_cols<128><<<grid, 256, 0, s>>>(dout, pos, count, dw, t, (uint32_t)d);
+    else k_emb_cols<64><<<grid, 256, 0, s>>>(dout, pos, count, dw, t, (uint32_t)d);
     MALUS_HIP(hipGetLastError());
     pool_free(count, b_count);
     pool_free(pos, b_pos);

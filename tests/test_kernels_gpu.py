@@ -479,7 +479,8 @@ def test_cross_entropy_fwd_bwd(rt, n, v):
 
 # ------------------------------------------------------------ index ops
 @pytest.mark.parametrize("v,d,t", [(65, 384, 4096), (256, 384, 2048), (65, 65, 777), (4, 3, 4), (3, 128, 16384),
-                                   (65, 384, 4097), (2048, 64, 9000), (400, 32, 4096), (65, 384, 16384), (256, 384, 16384)])
+                                   (65, 384, 4097), (2048, 64, 9000), (400, 32, 4096), (65, 384, 16384), (256, 384, 16384),
+                                   (1000, 36, 500), (5, 100, 40001)])
 def test_embedding_fwd_bwd_bitexact(rt, v, d, t):
     w = rand(v, d)
     idx = RNG.integers(0, v, t).astype(np.int32)
