@@ -354,10 +354,11 @@ int malus_gpt_nparams(void* g);
 int64_t malus_gpt_param(void* g, int i);              /* borrowed */
 int64_t malus_gpt_moment(void* g, int i, int which);  /* borrowed; which 0 = m, 1 = v */
 void malus_gpt_set_fused_optimizer(void* g, int on);
-/* Attention of the model: 0 automatic (under malus_autocast flash
- * attention; else the row-register fused kernel where its shapes are built,
- * else flash, else composed), 1 flash attention, 2 the row-register kernel,
- * 3 the composed ops.  Returns 0 or -1. */
+/* Attention of the model: 0 automatic (flash attention under
+ * malus_autocast, and with split f32 GEMM products at T >= 256; else the
+ * row-register fused kernel where its shapes are built, else flash, else
+ * composed), 1 flash attention, 2 the row-register kernel, 3 the composed
+ * ops.  Returns 0 or -1. */
 int malus_gpt_set_attention(void* gpt, int mode);
 /* 1 (default): forward fusions (attention scale+mask+softmax, residual adds in GEMM epilogues); 0: separate ops (same values and tape). */
 void malus_gpt_set_fused_forward(void* g, int on);
