@@ -474,7 +474,7 @@ def run_gpt(rt, a, cfg):
         nodes = L.malus_gpt_graph_nodes(graph)
         L.malus_gpt_graph_free(graph)
         graph = None
-        log(f"graph: one hipGraphLaunch per step, {nodes} nodes (kernels, the token draw and 2 input copies)")
+        log(f"graph: one hipGraphLaunch per step, {nodes} nodes (kernels, the token draw and its input copy)")
     a_graph, a.graph = a.graph, False  # the GEMM pass below runs eagerly (event timers are not graph nodes)
 
     # a separate pass for the GEMM class: HIP events around every GEMM launch

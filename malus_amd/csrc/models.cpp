@@ -787,13 +787,13 @@ struct GptGraph {
   // Where a step's token and target ids come from: copied from host arrays
   // (`pinned` holds [n] i32 tokens, [n] i32 targets, [2] f32 bias
   // corrections), or drawn on the device (`drawn`: `pinned` holds the two
-  // [2] u64 call indices, then the [2] f32 bias corrections, and a kernel node
-  // draws the ids).
+  // u64 call indices, then the [2] f32 bias corrections, copied by one node
+  // into `calls`, and a kernel node draws the ids).
   bool drawn = false;
   char* pinned = nullptr;
   int64_t toks = 0, tgts = 0;    // fixed device inputs [n] i32
-  int64_t calls = 0;             // drawn: [2] i64 call indices on the device
-  TensorBuffer* bc = nullptr;    // [2] f32 on the device
+  int64_t calls = 0;             // drawn: [3] i64 on the device, the call indices then the bias corrections
+  TensorBuffer* bc = nullptr;    // ids copied from the host: [2] f32 on the device
   int64_t loss = 0;              // written by every replay
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -830,9 +830,7 @@ void graph_set_inputs(GptGraph& gr, const int32_t* x, const int32_t* y, uint64_t
 int64_t graph_step_body(GptGraph& gr, int64_t t) {
   Gpt& g = *gr.g;
   if (gr.drawn) {
-    const uint64_t* calls = reinterpret_cast<const uint64_t*>(gr.pinned);
-    MALUS_HIP(hipMemcpyAsync(T(gr.calls)->data(), calls, 2 * sizeof(uint64_t), hipMemcpyHostToDevice, stream()));
-    MALUS_HIP(hipMemcpyAsync(gr.bc->data(), calls + 2, 2 * sizeof(float), hipMemcpyHostToDevice, stream()));
+    MALUS_HIP(hipMemcpyAsync(T(gr.calls)->data(), gr.pinned, pinned_bytes(gr), hipMemcpyHostToDevice, stream()));
     k::rand_tokens(T(gr.toks)->i32(), T(gr.tgts)->i32(), gr.n, static_cast<const uint64_t*>(T(gr.calls)->data()), 0,
                    0, (uint32_t)g.V, stream());
   } else {
@@ -842,7 +840,9 @@ int64_t graph_step_body(GptGraph& gr, int64_t t) {
     MALUS_HIP(hipMemcpyAsync(gr.bc->data(), ids + 2 * gr.n, 2 * sizeof(float), hipMemcpyHostToDevice, stream()));
   }
   const uint64_t seq = enqueue_mark("graph inputs");
-  T(gr.toks)->write_seq = T(gr.tgts)->write_seq = gr.bc->write_seq = seq;
+  T(gr.toks)->write_seq = T(gr.tgts)->write_seq = seq;
+  if (gr.drawn) T(gr.calls)->write_seq = seq;
+  else gr.bc->write_seq = seq;
   malus_gpt_zero_grad(&g);
   int64_t loss = gpt_forward_loss(g, gr.toks, gr.tgts, nullptr);
   backward(loss);
@@ -896,15 +896,21 @@ GptGraph* graph_create(Gpt* g, bool drawn, const int32_t* x, const int32_t* y, u
   int64_t eager_loss = 0;
   try {
     MALUS_HIP(hipHostMalloc(reinterpret_cast<void**>(&gr->pinned), pinned_bytes(*gr), hipHostMallocDefault));
-    const size_t sh[1] = {gr->n}, sh2[1] = {2};
+    const size_t sh[1] = {gr->n}, sh2[1] = {2}, sh3[1] = {3};
     gr->toks = H(alloc_tensor(I32, sh, 1));
     gr->tgts = H(alloc_tensor(I32, sh, 1));
-    if (drawn) gr->calls = H(alloc_tensor(I64, sh2, 1));
-    gr->bc = alloc_tensor(F32, sh2, 1);
+    float* bc_dev;
+    if (drawn) {  // the bias corrections share the calls' copy: the two f32 in its third word
+      gr->calls = H(alloc_tensor(I64, sh3, 1));
+      bc_dev = reinterpret_cast<float*>(static_cast<uint64_t*>(T(gr->calls)->data()) + 2);
+    } else {
+      gr->bc = alloc_tensor(F32, sh2, 1);
+      bc_dev = gr->bc->f32();
+    }
     MALUS_HIP(hipEventCreateWithFlags(&gr->done, hipEventDisableTiming));
     gr->g = g;
     g->inplace_opt = true;
-    g->bc_dev = gr->bc->f32();
+    g->bc_dev = bc_dev;
     // eager step t
     graph_set_inputs(*gr, x, y, cx, cy, t);
     eager_loss = graph_step_body(*gr, t);
