@@ -493,6 +493,29 @@ def test_embedding_fwd_bwd_bitexact(rt, v, d, t):
     rt.free(hw, hi, hd)
 
 
+@pytest.mark.parametrize("counts,v", [
+    ([256, 257, 0, 255, 512, 1, 2000], 7),      # mean t / v = 468: 256-token chunks
+    ([64, 65, 128, 129, 0, 1, 63, 200], 16),    # mean 40 (rows 8..15 unused): 64-token chunks
+    ([96, 97, 33, 0, 160], 5),                  # mean 77: 128-token chunks
+], ids=["chunk256", "chunk64", "chunk128"])
+def test_embedding_bwd_chunk_boundaries(rt, counts, v):
+    # The VJP stages each vocabulary row's listed tokens through LDS in
+    # chunks of 64, 128 or 256 (chosen from the mean list length t / v):
+    # rows whose lists end on, just past and just short of a chunk, empty
+    # rows, and one long row, with the tokens of all rows interleaved, must
+    # give the token-ordered sums bit for bit.
+    rng = np.random.default_rng(len(counts))
+    idx = np.concatenate([np.full(c, r, np.int32) for r, c in enumerate(counts)])
+    rng.shuffle(idx)
+    t, d = len(idx), 100  # d: three 32-column blocks and a 4-column tail
+    w = rand(v, d)
+    dout = rand(t, d)
+    hw, hi, hd = rt.tensor(w), rt.tensor(idx), rt.tensor(dout)
+    gb = run(rt, rt.L.malus_std_embedding_bwd(hw, hi, hd))
+    assert_bitexact(gb, O.embedding_bwd(dout, idx, v), f"embedding bwd, row counts {counts}")
+    rt.free(hw, hi, hd)
+
+
 def test_embedding_kat(rt):
     for kat in KATS["embedding"]:
         hw, hi = rt.tensor(np.array(kat["w"], np.float32)), rt.tensor(np.array(kat["idx"], np.int32))
