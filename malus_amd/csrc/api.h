@@ -68,8 +68,10 @@ int64_t attn_out_bwd_p(int64_t datt, int64_t v, size_t B, size_t T, size_t H, co
 int64_t attn_out_bwd_v(int64_t p, int64_t datt, size_t B, size_t T, size_t H, const malus::TensorBuffer* D,
                        bool causal);
 int64_t attn_scores_bwd_impl(int64_t datt, int64_t v, int64_t p, int64_t scale, size_t B, size_t T, size_t H);
+// defer_dw: dw's column combine waits for the thread's next
+// k::col_combine_flush (dw unread until then).
 int64_t ln_affine_bwd_xw(int64_t y, int64_t var, int64_t w, int64_t dout, const malus::TensorBuffer* D,
-                         int64_t* dw_out);
+                         int64_t* dw_out, bool defer_dw = false);
 int64_t attn_fwd_impl(int64_t q, int64_t k, int64_t v, int64_t scale, size_t B, size_t T, size_t H, int64_t* p_out);
 int64_t attn_bwd_impl(int64_t datt, int64_t v, int64_t p, int64_t scale, int64_t k, const malus::TensorBuffer* D, int64_t* dq,
                       size_t B, size_t T, size_t H);

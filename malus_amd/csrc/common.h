@@ -281,6 +281,13 @@ void reduce_axis_prod(const float* x, const float* y, float* out, size_t outer, 
 bool col_prod_split(size_t axis, size_t inner, uint32_t* nsplit, size_t* chunk, int* row_threads);
 // out[c] = the sum over s of partial[s * cols + c], as that reduction combines them.
 void col_combine_sum(const float* partial, float* out, size_t cols, uint32_t nsplit, size_t axis, hipStream_t s);
+// col_combine_sum of a pool block the call takes over (pool_free'd after its
+// last use).  defer (and nsplit % 4 == 0): the sum is queued, and runs with
+// every other queued one in one launch at the thread's next
+// col_combine_flush; `out` must not be read before then.
+void col_combine_sum_owned(float* partial, size_t bucket, float* out, size_t cols, uint32_t nsplit, size_t axis,
+                           bool defer, hipStream_t s);
+void col_combine_flush(hipStream_t s);
 // Broadcast [outer, inner] back to [outer, axis, inner] (expand_axis).
 void expand_axis(const float* small, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s);
 
@@ -297,8 +304,10 @@ void layernorm(const float* x, float* y, float* var, size_t outer, size_t axis, 
 // layernorm_bwd with the scale w, plus dw = reduce_axis_prod(dout, y) over
 // the rows, from one row kernel and the combine (bit-identical to the two
 // separate calls).  False (nothing launched) when the shape has no such form.
+// defer_dw: dw's combine is queued for col_combine_flush.
 bool layernorm_bwd_scale(const float* y, const float* var, const float* dout, float* dx, float* dw, size_t rows,
-                         size_t axis, float eps, hipStream_t s, const float* addend, const float* w);
+                         size_t axis, float eps, hipStream_t s, const float* addend, const float* w,
+                         bool defer_dw = false);
 void layernorm_bwd(const float* y, const float* var, const float* dout, float* dx, size_t outer, size_t axis, size_t inner,
                    float eps, hipStream_t s,
                    const float* addend = nullptr, const float* w = nullptr);

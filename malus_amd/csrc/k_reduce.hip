@@ -302,16 +302,17 @@ __global__ __launch_bounds__(256) void k_col_combine(const float* __restrict__ p
 // (level w: slot l += slot l + w for l < w, w = 32 .. 1).  So both layouts
 // give the same sums, bit for bit.  CC columns per block, G = 256 / CC slot
 // groups, 64 / G slots per thread.
+// col_combine_tree_cols: columns [bx CC, bx CC + CC) of one [nsplit][inner]
+// partial block into out[0 .. inner).
 template <int OP, bool VEC, int CC>
-__global__ __launch_bounds__(256) void k_col_combine_tree(const float* __restrict__ partial, float* __restrict__ out,
-                                                          uint32_t nsplit, size_t inner, uint32_t count) {
+__device__ __forceinline__ void col_combine_tree_cols(const float* __restrict__ partial, float* __restrict__ out,
+                                                      uint32_t nsplit, size_t inner, uint32_t count, size_t bx) {
   constexpr int G = 256 / CC, LPT = kWave / G;
   static_assert(kWave % G == 0, "whole lane slots per thread");
   __shared__ float red[kWave][CC];
   const int lc = threadIdx.x % CC, g = threadIdx.x / CC;
-  const size_t o = blockIdx.y;
-  const size_t i = (size_t)blockIdx.x * CC + lc;
-  const float* p = partial + o * nsplit * inner + i;
+  const size_t i = bx * CC + lc;
+  const float* p = partial + i;
   // step k reads, for every slot of the thread, its k-th run (VEC: four
   // partials, else one) before folding any of them: one memory round trip
   // per step
@@ -350,7 +351,32 @@ __global__ __launch_bounds__(256) void k_col_combine_tree(const float* __restric
     }
     __syncthreads();
   }
-  if (g == 0 && i < inner) out[o * inner + i] = rfinal<OP>(red[0][lc], count);
+  if (g == 0 && i < inner) out[i] = rfinal<OP>(red[0][lc], count);
+}
+
+template <int OP, bool VEC, int CC>
+__global__ __launch_bounds__(256) void k_col_combine_tree(const float* __restrict__ partial, float* __restrict__ out,
+                                                          uint32_t nsplit, size_t inner, uint32_t count) {
+  const size_t o = blockIdx.y;
+  col_combine_tree_cols<OP, VEC, CC>(partial + o * nsplit * inner, out + o * inner, nsplit, inner, count, blockIdx.x);
+}
+
+// Several column sums (nsplit % 4 == 0) in one launch: block (x, j) runs
+// column block x of job j, the same sums k_col_combine_tree forms for it
+// alone.
+struct ColSumJobs {
+  static constexpr int kMax = 32;
+  const float* partial[kMax];
+  float* out[kMax];
+  uint32_t nsplit[kMax], inner[kMax], count[kMax];
+};
+
+template <int CC>
+__global__ __launch_bounds__(256) void k_col_combine_tree_jobs(const ColSumJobs jobs) {
+  const int j = blockIdx.y;
+  if ((size_t)blockIdx.x * CC >= jobs.inner[j]) return;  // the grid spans the widest job
+  col_combine_tree_cols<R_SUM, true, CC>(jobs.partial[j], jobs.out[j], jobs.nsplit[j], jobs.inner[j], jobs.count[j],
+                                         blockIdx.x);
 }
 
 // Launch k_col_combine_tree over [outer][nsplit][inner] partials.
@@ -636,6 +662,54 @@ bool col_prod_split(size_t axis, size_t inner, uint32_t* nsplit, size_t* chunk, 
 void col_combine_sum(const float* partial, float* out, size_t cols, uint32_t nsplit, size_t axis, hipStream_t s) {
   launch_col_combine_tree<R_SUM>(partial, out, 1, nsplit, cols, (uint32_t)axis, s);
   MALUS_HIP(hipGetLastError());
+}
+
+namespace {
+struct DeferredColSum {
+  float* partial;
+  size_t bucket;
+  float* out;
+  uint32_t nsplit, inner, count;
+};
+thread_local std::vector<DeferredColSum> t_colsums;
+}  // namespace
+
+void col_combine_sum_owned(float* partial, size_t bucket, float* out, size_t cols, uint32_t nsplit, size_t axis,
+                           bool defer, hipStream_t s) {
+  if (defer && nsplit % 4 == 0 && cols <= UINT32_MAX && axis <= UINT32_MAX) {
+    t_colsums.push_back({partial, bucket, out, nsplit, (uint32_t)cols, (uint32_t)axis});
+    return;
+  }
+  col_combine_sum(partial, out, cols, nsplit, axis, s);
+  pool_free(partial, bucket);
+}
+
+void col_combine_flush(hipStream_t s) {
+  std::vector<DeferredColSum> jobs;
+  jobs.swap(t_colsums);
+  constexpr int CC = 8;  // as launch_col_combine_tree
+  try {
+    for (size_t b = 0; b < jobs.size(); b += ColSumJobs::kMax) {
+      const int n = (int)std::min<size_t>(ColSumJobs::kMax, jobs.size() - b);
+      ColSumJobs t{};
+      uint32_t widest = 0;
+      for (int j = 0; j < n; ++j) {
+        const DeferredColSum& d = jobs[b + j];
+        t.partial[j] = d.partial;
+        t.out[j] = d.out;
+        t.nsplit[j] = d.nsplit;
+        t.inner[j] = d.inner;
+        t.count[j] = d.count;
+        widest = std::max(widest, d.inner);
+      }
+      k_col_combine_tree_jobs<CC><<<dim3((widest + CC - 1) / CC, (unsigned)n), 256, 0, s>>>(t);
+      MALUS_HIP(hipGetLastError());
+    }
+  } catch (...) {
+    for (const DeferredColSum& d : jobs) pool_free(d.partial, d.bucket);
+    throw;
+  }
+  for (const DeferredColSum& d : jobs) pool_free(d.partial, d.bucket);
 }
 
 void expand_axis(const float* small, float* out, size_t outer, size_t axis, size_t inner, hipStream_t s) {

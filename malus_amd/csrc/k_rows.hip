@@ -750,7 +750,7 @@ void layernorm_bwd(const float* y, const float* var, const float* dout, float* d
 }
 
 bool layernorm_bwd_scale(const float* y, const float* var, const float* dout, float* dx, float* dw, size_t rows,
-                         size_t axis, float eps, hipStream_t s, const float* addend, const float* w) {
+                         size_t axis, float eps, hipStream_t s, const float* addend, const float* w, bool defer_dw) {
   const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   if (!rows || axis % 128 != 0 || axis > 512 || !w || !a16(y) || !a16(dout) || !a16(dx) || !a16(addend) || !a16(w))
     return false;
@@ -768,8 +768,7 @@ bool layernorm_bwd_scale(const float* y, const float* var, const float* dout, fl
     default: k_layernorm_bwd_scale_rows32<4><<<nsplit, 256, 0, s>>>(y, var, dout, dx, rows, eps, addend, w, partial, nsplit); break;
   }
   MALUS_HIP(hipGetLastError());
-  col_combine_sum(partial, dw, axis, nsplit, rows, s);
-  pool_free(partial, bucket);
+  col_combine_sum_owned(partial, bucket, dw, axis, nsplit, rows, defer_dw, s);
   return true;
 }
 

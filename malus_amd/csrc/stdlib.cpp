@@ -979,7 +979,8 @@ int64_t ln_affine_bwd_x(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const 
 // ln_affine_bwd_x and the scale's gradient mul_bwd_b(dout, y, w) from one
 // row kernel (bit-identical to the two calls); *dw_out gets dw.  0 when the
 // shape has no fused form (nothing launched).
-int64_t ln_affine_bwd_xw(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const TensorBuffer* D, int64_t* dw_out) {
+int64_t ln_affine_bwd_xw(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const TensorBuffer* D, int64_t* dw_out,
+                         bool defer_dw) {
   TensorBuffer *ty = T(hy), *tv = T(hvar), *tw = T(hw), *td = T(hd);
   const size_t a = ty->shape[ty->ndim - 1], o = ty->len / a;
   if (tv->len != o || tw->len != a || td->len != ty->len || tw->ndim != 1) return 0;
@@ -988,7 +989,7 @@ int64_t ln_affine_bwd_xw(int64_t hy, int64_t hvar, int64_t hw, int64_t hd, const
   TensorBuffer* out = alloc_like(ty);
   TensorBuffer* dw = alloc_tensor(F32, tw->shape, tw->ndim);
   if (!k::layernorm_bwd_scale(ty->f32(), tv->f32(), td->f32(), out->f32(), dw->f32(), o, a, 1e-5f, stream(),
-                              D ? D->f32() : nullptr, tw->f32())) {
+                              D ? D->f32() : nullptr, tw->f32(), defer_dw)) {
     release(out);
     release(dw);
     return 0;

@@ -487,6 +487,23 @@ void backward(int64_t loss) {
     grads.emplace(loss, H(seed));
   }
   GradLiveness need(nodes);
+  // A layernorm scale whose weight is a live leaf that no other record
+  // reads gets its weight gradient only at the leaf fold below, so the
+  // column combines of those gradients are queued and run in one launch
+  // before it (the same sums per column); the guard runs them if backward
+  // stops early.
+  std::unordered_map<int64_t, int> reads;
+  for (const TapeNode& n : nodes)
+    for (int64_t h : n.saved) ++reads[h];
+  std::vector<int64_t> deferred;  // gradients whose combine is queued
+  struct FlushGuard {
+    ~FlushGuard() {
+      try {
+        k::col_combine_flush(stream());
+      } catch (...) {
+      }
+    }
+  } flush_guard;
   for (auto it = nodes.rbegin(); it != nodes.rend(); ++it) {
     const TapeNode& n = *it;
     auto g = grads.find(n.output);
@@ -628,10 +645,12 @@ void backward(int64_t loss) {
         // the multiply's VJPs (dy, then dw), then the layernorm VJP of dy
         if (na && nb && slot_is(MulBwdB, &malus_std_mul_bwd_b)) {  // both from one row kernel where it applies
           int64_t dw = 0;
+          const bool defer_dw = reads[w] == 1 && t_leaves.count(w) && !grads.count(w);
           fold_grad(grads, x, [&](const TensorBuffer* o) {
-            const int64_t dx = ln_affine_bwd_xw(y, var, w, dout, o, &dw);
+            const int64_t dx = ln_affine_bwd_xw(y, var, w, dout, o, &dw, defer_dw);
             return dx ? dx : ln_affine_bwd_x(y, var, w, dout, o);
           });
+          if (dw && defer_dw) deferred.push_back(dw);
           accumulate(grads, w, dw ? dw : slot_fn<Fn3>(MulBwdB)(dout, y, w));
           break;
         }
@@ -727,6 +746,11 @@ void backward(int64_t loss) {
       case Embedding: accumulate(grads, n.saved[0], slot_fn<Fn3>(EmbeddingBwd)(n.saved[0], n.saved[1], dout)); break;
       default: fail("malus: backward: unhandled op tag %d", n.op);
     }
+  }
+  k::col_combine_flush(stream());
+  if (!deferred.empty()) {  // host reads of those gradients wait for the combine
+    const uint64_t seq = enqueue_mark("layernorm scale gradients");
+    for (int64_t h : deferred) T(h)->write_seq = seq;
   }
   // fold leaf grads into the persistent registry (tape.rs:694-721)
   std::vector<int64_t> to_release;
