@@ -68,6 +68,12 @@ int64_t attn_out_bwd_p(int64_t datt, int64_t v, size_t B, size_t T, size_t H, co
 int64_t attn_out_bwd_v(int64_t p, int64_t datt, size_t B, size_t T, size_t H, const malus::TensorBuffer* D,
                        bool causal);
 int64_t attn_scores_bwd_impl(int64_t datt, int64_t v, int64_t p, int64_t scale, size_t B, size_t T, size_t H);
+// The VJPs of two embeddings read through one gradient (the token and
+// position tables of an embedding sum): *dwa, *dwb from one list launch and
+// one sum launch, the same values as two malus_std_embedding_bwd calls.
+// False (nothing launched) when the two do not share t, the row width and
+// the i32 indices, or the shapes have no such form.
+bool embedding_bwd2_impl(int64_t wa, int64_t ia, int64_t wb, int64_t ib, int64_t dout, int64_t* dwa, int64_t* dwb);
 // defer_dw: dw's column combine waits for the thread's next
 // k::col_combine_flush (dw unread until then).
 int64_t ln_affine_bwd_xw(int64_t y, int64_t var, int64_t w, int64_t dout, const malus::TensorBuffer* D,

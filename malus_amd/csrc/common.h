@@ -326,6 +326,12 @@ void embedding(const float* w, const int32_t* idx, float* out, size_t t, size_t 
 void embedding2(const float* wa, const int32_t* ia, size_t va, const float* wb, const int32_t* ib, size_t vb, float* out,
                 size_t t, size_t d, int32_t* err, hipStream_t s);
 void embedding_bwd(const float* dout, const int32_t* idx, float* dw, size_t t, size_t v, size_t d, hipStream_t s);
+// embedding_bwd of two tables (va and vb rows of width d) indexed by idx_a
+// and idx_b (t each) with one dout, from one list launch and one sum launch
+// (the same values as two embedding_bwd calls).  False (nothing launched)
+// when the shapes do not take that form.
+bool embedding_bwd2(const float* dout, const int32_t* idx_a, float* dw_a, size_t va, const int32_t* idx_b,
+                    float* dw_b, size_t vb, size_t t, size_t d, hipStream_t s);
 void permute(const float* x, float* out, int ndim, const size_t* in_shape, const size_t* perm, hipStream_t s);
 
 // Operand addressing for gemm_mapped: element (i, j) of a stored matrix

@@ -101,19 +101,25 @@ __global__ __launch_bounds__(256) void k_emb_accum(const float* __restrict__ dou
 }
 
 // Two-launch form for small vocabularies (v * t list slots fit the pool).
-// k_emb_list: block per vocab row v writes the positions of its tokens, in
-// increasing order, at pos[v * t ..] and their count.  The tokens are taken
+// Both kernels take the rows of one or two tables (the token and position
+// tables of one embedding sum share t and dout): global row r < va is row r
+// of table a (idx_a, dw_a), a later one row r - va of table b.
+// k_emb_list: block per global row r writes the positions of its tokens, in
+// increasing order, at pos[r * t ..] and their count.  The tokens are taken
 // in passes of 1024 x 16: thread i owns the 16 contiguous tokens
 // [16 i, 16 i + 16) of a pass and keeps them in registers from its count to
 // its writes (four int4 loads with VEC, all in flight together); a block
 // exclusive scan of the per-thread hit counts (thread order = token order)
 // places them.
 template <bool VEC>
-__global__ __launch_bounds__(1024) void k_emb_list(const int32_t* __restrict__ idx, size_t t, uint32_t* __restrict__ pos,
-                                                   uint32_t* __restrict__ count) {
+__global__ __launch_bounds__(1024) void k_emb_list(const int32_t* __restrict__ idx_a, uint32_t va,
+                                                   const int32_t* __restrict__ idx_b, size_t t,
+                                                   uint32_t* __restrict__ pos, uint32_t* __restrict__ count) {
   constexpr int kWaves = 16, kPer = 16;
   __shared__ uint32_t wave_tot[kWaves];
-  const int32_t v = (int32_t)blockIdx.x;
+  const bool in_a = blockIdx.x < va;
+  const int32_t* __restrict__ idx = in_a ? idx_a : idx_b;
+  const int32_t v = (int32_t)(in_a ? blockIdx.x : blockIdx.x - va);
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   uint32_t* out = pos + (size_t)blockIdx.x * t;
   uint32_t done = 0;  // hits in earlier passes
@@ -165,7 +171,7 @@ __global__ __launch_bounds__(1024) void k_emb_list(const int32_t* __restrict__ i
 
 // k_emb_cols: dw[v, c0 .. c0 + 32) = the sum of dout[p, c0 ..] over row v's
 // token list p, in list order (the same adds as k_emb_accum).  Block
-// (32-column block, row v), 256 threads.  Each sum is a chain of dependent
+// (32-column block, global row), 256 threads.  Each sum is a chain of dependent
 // adds, so the rows the list names are staged through LDS CH tokens at a
 // time by all the block's threads (a token's 128-byte segment read by 8
 // lanes as float4, 32 tokens per pass); lanes 0..31 of wave 0 then add the
@@ -175,8 +181,8 @@ __global__ __launch_bounds__(1024) void k_emb_list(const int32_t* __restrict__ i
 // used as addresses), and each later chunk's a chunk ahead of its loads.
 template <int CH>
 __global__ __launch_bounds__(256) void k_emb_cols(const float* __restrict__ dout, const uint32_t* __restrict__ pos,
-                                                  const uint32_t* __restrict__ count, float* __restrict__ dw, size_t t,
-                                                  uint32_t d) {
+                                                  const uint32_t* __restrict__ count, float* __restrict__ dw_a,
+                                                  uint32_t va, float* __restrict__ dw_b, size_t t, uint32_t d) {
   constexpr int kW = 32, kLoads = CH / 32;
   static_assert(CH % 32 == 0, "32 tokens per pass");
   __shared__ float4 buf[CH * kW / 4];
@@ -222,7 +228,8 @@ __global__ __launch_bounds__(256) void k_emb_cols(const float* __restrict__ dout
     }
     __syncthreads();  // the chunk is read before the next one is stored
   }
-  if (threadIdx.x < kW && c0 + threadIdx.x < d) dw[(size_t)row * d + c0 + threadIdx.x] = acc;
+  float* __restrict__ dw = row < va ? dw_a + (size_t)row * d : dw_b + (size_t)(row - va) * d;
+  if (threadIdx.x < kW && c0 + threadIdx.x < d) dw[c0 + threadIdx.x] = acc;
 }
 
 struct PermDesc {
@@ -327,28 +334,56 @@ void embedding(const float* w, const int32_t* idx, float* out, size_t t, size_t 
   MALUS_HIP(hipGetLastError());
 }
 
+namespace {
+bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
+
+// Whether rows of width d (t tokens, v rows in all) take the list-and-stage
+// form.
+bool emb_lists_fit(size_t t, size_t v, size_t d, const float* dout) {
+  return d % 4 == 0 && v * t <= ((size_t)1 << 24) && v <= 65535 && d < ((size_t)1 << 31) && aligned16(dout);
+}
+
+// The list-and-stage form over va rows of table a and vb of table b (vb = 0:
+// one table); the caller has checked emb_lists_fit for va + vb rows.
+void emb_lists_and_sums(const float* dout, const int32_t* idx_a, float* dw_a, size_t va, const int32_t* idx_b,
+                        float* dw_b, size_t vb, size_t t, size_t d, hipStream_t s) {
+  const size_t v = va + vb;
+  size_t b_count, b_pos;
+  uint32_t* count = static_cast<uint32_t*>(pool_alloc(v * sizeof(uint32_t), &b_count));
+  uint32_t* pos = static_cast<uint32_t*>(pool_alloc(v * t * sizeof(uint32_t), &b_pos));
+  if (t % 4 == 0 && aligned16(idx_a) && aligned16(idx_b))
+    k_emb_list<true><<<(unsigned)v, 1024, 0, s>>>(idx_a, (uint32_t)va, idx_b, t, pos, count);
+  else
+    k_emb_list<false><<<(unsigned)v, 1024, 0, s>>>(idx_a, (uint32_t)va, idx_b, t, pos, count);
+  MALUS_HIP(hipGetLastError());
+  // chunk size from the mean list length: one chunk for most rows
+  const dim3 grid((unsigned)((d + 31) / 32), (unsigned)v);
+  const size_t mean = t * (vb ? 2 : 1) / v;
+  if (mean > 128) k_emb_cols<256><<<grid, 256, 0, s>>>(dout, pos, count, dw_a, (uint32_t)va, dw_b, t, (uint32_t)d);
+  else if (mean > 64) k_emb_cols<128><<<grid, 256, 0, s>>>(dout, pos, count, dw_a, (uint32_t)va, dw_b, t, (uint32_t)d);
+  else k_emb_cols<64><<<grid, 256, 0, s>>>(dout, pos, count, dw_a, (uint32_t)va, dw_b, t, (uint32_t)d);
+  MALUS_HIP(hipGetLastError());
+  pool_free(count, b_count);
+  pool_free(pos, b_pos);
+}
+}  // namespace
+
+bool embedding_bwd2(const float* dout, const int32_t* idx_a, float* dw_a, size_t va, const int32_t* idx_b,
+                    float* dw_b, size_t vb, size_t t, size_t d, hipStream_t s) {
+  if (!t || !d || !va || !vb || !emb_lists_fit(t, va + vb, d, dout) || !aligned16(dw_a) || !aligned16(dw_b))
+    return false;
+  emb_lists_and_sums(dout, idx_a, dw_a, va, idx_b, dw_b, vb, t, d, s);
+  return true;
+}
+
 void embedding_bwd(const float* dout, const int32_t* idx, float* dw, size_t t, size_t v, size_t d, hipStream_t s) {
   if (!v || !d) return;
   if (!t) { fill(dw, 0.0f, v * d, s); return; }
-  size_t b_count, b_offs, b_pos;
-  const auto aligned = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  if (d % 4 == 0 && v * t <= ((size_t)1 << 24) && v <= 65535 && d < ((size_t)1 << 31) && aligned(dout) && aligned(dw)) {
-    uint32_t* count = static_cast<uint32_t*>(pool_alloc(v * sizeof(uint32_t), &b_count));
-    uint32_t* pos = static_cast<uint32_t*>(pool_alloc(v * t * sizeof(uint32_t), &b_pos));
-    if (t % 4 == 0 && aligned(idx)) k_emb_list<true><<<(unsigned)v, 1024, 0, s>>>(idx, t, pos, count);
-    else k_emb_list<false><<<(unsigned)v, 1024, 0, s>>>(idx, t, pos, count);
-    MALUS_HIP(hipGetLastError());
-    // chunk size from the mean list length: one chunk for most rows
-    const dim3 grid((unsigned)((d + 31) / 32), (unsigned)v);
-    const size_t mean = t / v;
-    if (mean > 128) k_emb_cols<256><<<grid, 256, 0, s>>>(dout, pos, count, dw, t, (uint32_t)d);
-    else if (mean > 64) k_emb_cols<128><<<grid, 256, 0, s>>>(dout, pos, count, dw, t, (uint32_t)d);
-    else k_emb_cols<64><<<grid, 256, 0, s>>>(dout, pos, count, dw, t, (uint32_t)d);
-    MALUS_HIP(hipGetLastError());
-    pool_free(count, b_count);
-    pool_free(pos, b_pos);
+  if (emb_lists_fit(t, v, d, dout) && aligned16(dw)) {
+    emb_lists_and_sums(dout, idx, dw, v, idx, dw, 0, t, d, s);
     return;
   }
+  size_t b_count, b_offs, b_pos;
   uint32_t* count = static_cast<uint32_t*>(pool_alloc(v * sizeof(uint32_t), &b_count));
   uint32_t* offs = static_cast<uint32_t*>(pool_alloc((v + 1) * sizeof(uint32_t), &b_offs));
   uint32_t* pos = static_cast<uint32_t*>(pool_alloc(t * sizeof(uint32_t), &b_pos));

@@ -885,6 +885,26 @@ int64_t malus_std_embedding_bwd(int64_t weight, int64_t indices, int64_t dout) {
 
 }  // extern "C"
 
+bool embedding_bwd2_impl(int64_t wa, int64_t ia, int64_t wb, int64_t ib, int64_t dout, int64_t* dwa, int64_t* dwb) {
+  TensorBuffer *A = T(wa), *IA = T(ia), *B = T(wb), *IB = T(ib), *d = T(dout);
+  if (A->ndim != 2 || B->ndim != 2 || A->shape[1] != B->shape[1] || IA->dtype != I32 || IB->dtype != I32 ||
+      IA->len != IB->len || d->dtype != F32 || d->len != IA->len * A->shape[1])
+    return false;
+  TensorBuffer* oa = alloc_tensor(F32, A->shape, 2);
+  TensorBuffer* ob = alloc_tensor(F32, B->shape, 2);
+  if (!k::embedding_bwd2(d->f32(), IA->i32(), oa->f32(), A->shape[0], IB->i32(), ob->f32(), B->shape[0], IA->len,
+                         A->shape[1], stream())) {
+    release(oa);
+    release(ob);
+    return false;
+  }
+  const uint64_t seq = enqueue_mark("embedding_bwd2");
+  oa->write_seq = ob->write_seq = seq;
+  *dwa = malus::H(oa);
+  *dwb = malus::H(ob);
+  return true;
+}
+
 // ---- matmul (metal.rs:820-962) and its VJPs (matmul_bwd.ml:15-29) ---------------------
 // The *_impl forms take an optional addend D of the output's shape and
 // return D + product (one GEMM, the product rounded before the add), which

@@ -541,6 +541,23 @@ void backward(int64_t loss) {
         continue;
       }
     }
+    if (n.op == Embedding && std::distance(it, nodes.rend()) >= 2 && na &&
+        slot_is(EmbeddingBwd, &malus_std_embedding_bwd)) {
+      // The token and position embeddings of one sum sit back to back on
+      // the tape with one gradient: both VJPs from one list launch and one
+      // sum launch, accumulated in this same order.
+      const TapeNode& n1 = *(it + 1);
+      auto g1 = grads.find(n1.output);
+      int64_t dwa = 0, dwb = 0;
+      if (n1.op == Embedding && g1 != grads.end() && g1->second == dout && need(n1.saved[0]) &&
+          n1.saved[0] != n.saved[0] &&
+          embedding_bwd2_impl(n.saved[0], n.saved[1], n1.saved[0], n1.saved[1], dout, &dwa, &dwb)) {
+        accumulate(grads, n.saved[0], dwa);
+        accumulate(grads, n1.saved[0], dwb);
+        ++it;
+        continue;
+      }
+    }
     switch (n.op) {
       case Matmul: {
         int64_t a = n.saved[0], b = n.saved[1];
