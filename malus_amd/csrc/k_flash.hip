@@ -258,9 +258,14 @@ __global__ __launch_bounds__(64, 2) void k_flash_fwd(const float* __restrict__ Q
 }
 
 // Backward, query-centric: dQ (+ Dq) of query tile qt, and D = rowsum(dO*O)
-// of its rows into dsum for the key-centric pass.
-template <int HS, bool CAUSAL, bool BF, bool S16 = false, bool X3 = false>
-__global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict__ Q, const float* __restrict__ K,
+// of its rows into dsum for the key-centric pass.  W waves per workgroup:
+// W = 1, one query tile; W = 4, query tiles 4 g .. 4 g + 3 of one head, one
+// per wave, sharing each staged key tile (each thread stages a quarter of it,
+// so tile j + 1's loads are issued before tile j's products without the
+// registers of a whole tile per wave).  Each wave's products are the same
+// either way.
+template <int HS, bool CAUSAL, bool BF, bool S16 = false, bool X3 = false, int W = 1>
+__global__ __launch_bounds__(64 * W, 2) void k_flash_bwd_dq(const float* __restrict__ Q, const float* __restrict__ K,
                                                      const float* __restrict__ V, const float* __restrict__ O,
                                                      const float* __restrict__ dO, int ldo, int H,
                                                      const float* __restrict__ lse, const float* __restrict__ scale,
@@ -268,8 +273,10 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
                                                      float* __restrict__ dsum, int T, int BH) {
   constexpr int NKB = HS / 16, NN = HS / 32;
   const int NT = T / 32;
-  const int qt = NT - 1 - (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
-  const int lane = threadIdx.x, x = lane & 31, lk = lane >> 5;
+  const int lane = threadIdx.x % 64, x = lane & 31, lk = lane >> 5, wave = threadIdx.x / 64;
+  // W = 1: the longest tiles first; W = 4: the groups of four tiles, longest first
+  const int qt = W == 1 ? NT - 1 - (int)(blockIdx.x / BH) : W * (NT / W - 1 - (int)(blockIdx.x / BH)) + wave;
+  const int bh = (int)(blockIdx.x % BH);
   const size_t head = (size_t)bh * T * HS;
   const int i0 = 32 * qt, i = i0 + x;
   const float sc = scale[0];
@@ -302,31 +309,46 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dq(const float* __restrict_
 #pragma unroll
   for (int n = 0; n < NN; ++n) dq[n] = v16f{0};
   const int last = CAUSAL ? qt : NT - 1;
+  // the workgroup's key tiles: its longest wave's
+  const int jmax = W == 1 ? last : (CAUSAL ? W * (qt / W) + W - 1 : NT - 1);
   // Key tile j of K and V goes through LDS (rows padded to HS + 4 floats):
   // one 16-byte global load per 4 floats, and both of K's orientations (the
-  // rows for S^T, the columns for dQ = dS K) read back from LDS.  (Fetching
-  // tile j + 1 into registers during tile j measured no faster and spilled.)
-  constexpr int LD = HS + 4, Q4 = HS / 4, PER = 32 * Q4 / 64;
+  // rows for S^T, the columns for dQ = dS K) read back from LDS.  (With one
+  // wave per workgroup, fetching tile j + 1 into registers during tile j
+  // measured no faster and spilled.)
+  constexpr int LD = HS + 4, Q4 = HS / 4, PER = 32 * Q4 / (64 * W);
   __shared__ __attribute__((aligned(16))) float Ks[32 * LD], Vs[32 * LD];
   v4f kn[PER], vn[PER];
   auto fetch = [&](int j) {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-      const int f = lane + 64 * u;
+      const int f = threadIdx.x + 64 * W * u;
       kn[u] = ld4<S16>(K, head + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
       vn[u] = ld4<S16>(V, head + (size_t)(32 * j + f / Q4) * HS + 4 * (f % Q4));
     }
   };
-  for (int j = 0; j <= last; ++j) {
-    fetch(j);
-    wave_lds_sync();  // the last tile's reads of Ks and Vs are done
+  auto stage = [&]() {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-      const int f = lane + 64 * u;
+      const int f = threadIdx.x + 64 * W * u;
       *reinterpret_cast<v4f*>(Ks + (f / Q4) * LD + 4 * (f % Q4)) = kn[u];
       *reinterpret_cast<v4f*>(Vs + (f / Q4) * LD + 4 * (f % Q4)) = vn[u];
     }
-    wave_lds_sync();  // this tile's stores are visible to every lane
+  };
+  if (W > 1) fetch(0);
+  for (int j = 0; j <= jmax; ++j) {
+    if (W == 1) {
+      fetch(j);
+      wave_lds_sync();  // the last tile's reads of Ks and Vs are done
+      stage();
+      wave_lds_sync();  // this tile's stores are visible to every lane
+    } else {
+      __syncthreads();  // every wave's reads of the last tile are done
+      stage();
+      __syncthreads();  // this tile is visible to every wave
+      if (j < jmax) fetch(j + 1);  // in flight during this tile's products
+      if (j > last) continue;      // past this wave's diagonal: the barriers only
+    }
     float ka[NKB][8], vr[NKB][8];  // A of S^T and dP^T: rows perm_row(x) of K_j, V_j
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
@@ -582,8 +604,20 @@ void fwd_launch(const float* Q, const float* K, const float* V, const float* sca
 template <int HS, bool CAUSAL, bool BF, bool S16, bool X3 = false>
 void bwd_launch(const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
   const unsigned grid = (unsigned)(T / 32 * BH);
-  k_flash_bwd_dq<HS, CAUSAL, BF, S16, X3><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.O, a.dO, ldo, H, a.lse, a.scale, a.dQ,
-                                                               a.Dq, a.dsum, T, BH);
+  // Split products at T >= 1024: four query tiles per workgroup (dQ pass 4-7 %
+  // faster at T = 1024 ... 4096; at T = 256 a head has two groups, the short
+  // one's waves mostly wait at its barriers, and it measured 5 % slower, two
+  // tiles per workgroup 3 % slower).
+  bool grouped = false;
+  if constexpr (X3) grouped = T / 32 >= 32 && (T / 32) % 4 == 0;
+  if constexpr (X3) {
+    if (grouped)
+      k_flash_bwd_dq<HS, CAUSAL, BF, S16, X3, 4><<<grid / 4, 256, 0, s>>>(a.Q, a.K, a.V, a.O, a.dO, ldo, H, a.lse,
+                                                                          a.scale, a.dQ, a.Dq, a.dsum, T, BH);
+  }
+  if (!grouped)
+    k_flash_bwd_dq<HS, CAUSAL, BF, S16, X3><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.O, a.dO, ldo, H, a.lse, a.scale,
+                                                                 a.dQ, a.Dq, a.dsum, T, BH);
   k_flash_bwd_dkv<HS, CAUSAL, BF, S16, X3><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.dO, ldo, H, a.lse, a.dsum, a.scale,
                                                                 a.dK, a.Dk, a.dV, a.Dv, T, BH);
 }

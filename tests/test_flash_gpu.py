@@ -55,7 +55,8 @@ def composed_bwd(q, k, v, p, d, sc):
 
 
 SHAPES = [(6, 64, 32, 1), (6, 64, 32, 0), (5, 128, 64, 1), (4, 256, 64, 1), (4, 256, 64, 0), (3, 96, 64, 1),
-          (2, 512, 64, 1), (1, 1024, 32, 1), (2, 32, 64, 1)]
+          (2, 512, 64, 1), (1, 1024, 32, 1), (2, 32, 64, 1),
+          (2, 1024, 64, 1), (1, 1024, 64, 0)]  # T >= 1024: the dQ pass runs four query tiles per workgroup
 
 
 @pytest.mark.parametrize("bh,t,hs,causal", SHAPES, ids=[f"bh{a}t{b}hs{c}{'c' if d else 'n'}" for a, b, c, d in SHAPES])
