@@ -417,9 +417,11 @@ __global__ __launch_bounds__(64 * W, 2) void k_flash_bwd_dq(const float* __restr
   }
 }
 
-// Backward, key-centric: dK (+ Dk) and dV (+ Dv) of key tile kt.
-template <int HS, bool CAUSAL, bool BF, bool S16 = false, bool X3 = false>
-__global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict__ Q, const float* __restrict__ K,
+// Backward, key-centric: dK (+ Dk) and dV (+ Dv) of key tile kt.  W waves
+// per workgroup as in the dQ pass: W = 4 runs key tiles 4 g .. 4 g + 3 of one
+// head, one per wave, sharing each staged query tile (f32 staging only).
+template <int HS, bool CAUSAL, bool BF, bool S16 = false, bool X3 = false, int W = 1>
+__global__ __launch_bounds__(64 * W, 2) void k_flash_bwd_dkv(const float* __restrict__ Q, const float* __restrict__ K,
                                                       const float* __restrict__ V, const float* __restrict__ dO, int ldo,
                                                       int H, const float* __restrict__ lse,
                                                       const float* __restrict__ dsum, const float* __restrict__ scale,
@@ -428,8 +430,8 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
                                                       int BH) {
   constexpr int NKB = HS / 16, NN = HS / 32;
   const int NT = T / 32;
-  const int kt = (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
-  const int lane = threadIdx.x, x = lane & 31, lk = lane >> 5;
+  const int lane = threadIdx.x % 64, x = lane & 31, lk = lane >> 5, wave = threadIdx.x / 64;
+  const int kt = W * (int)(blockIdx.x / BH) + wave, bh = (int)(blockIdx.x % BH);
   const size_t head = (size_t)bh * T * HS;
   const int j0 = 32 * kt, key = j0 + x;
   const float sc = scale[0];
@@ -463,27 +465,60 @@ __global__ __launch_bounds__(64, 2) void k_flash_bwd_dkv(const float* __restrict
   // staging's round trip: there the operands come straight from L2 (the LDS
   // form measured 3 % faster at T = 256 but 3-20 % slower at T = 1024-4096).
   constexpr bool STAGE = !BF;
-  constexpr int LD = HS + 4, Q4 = HS / 4, PER = 32 * Q4 / 64;
+  static_assert(W == 1 || STAGE, "several key tiles per workgroup share the f32 staging");
+  constexpr int LD = HS + 4, Q4 = HS / 4, PER = 32 * Q4 / (64 * W);
   __shared__ __attribute__((aligned(16))) float Qs[STAGE ? 32 * LD : 1], Os[STAGE ? 32 * LD : 1];
-  for (int it = first; it < NT; ++it) {
+  // W > 1: the workgroup's query tiles start at its first wave's, and tile
+  // it + 1's loads (a 1 / W share per thread) are issued before tile it's
+  // products
+  const int wg_first = W == 1 ? first : (CAUSAL ? W * (kt / W) : 0);
+  v4f qf[W > 1 ? PER : 1], of[W > 1 ? PER : 1];
+  if constexpr (W > 1)
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int f = threadIdx.x + 64 * W * u;
+      qf[u] = ld4<S16>(Q, head + (size_t)(32 * wg_first + f / Q4) * HS + 4 * (f % Q4));
+      of[u] = *reinterpret_cast<const v4f*>(head_row(dO, bh, H, T, ldo, HS, 32 * wg_first + f / Q4) + 4 * (f % Q4));
+    }
+  for (int it = wg_first; it < NT; ++it) {
     const int i0 = 32 * it;
     v16f s = v16f{0}, dp = v16f{0};
+    if constexpr (STAGE && W > 1) {
+      __syncthreads();  // every wave's reads of the last tile are done
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int f = threadIdx.x + 64 * W * u;
+        *reinterpret_cast<v4f*>(Qs + (f / Q4) * LD + 4 * (f % Q4)) = qf[u];
+        *reinterpret_cast<v4f*>(Os + (f / Q4) * LD + 4 * (f % Q4)) = of[u];
+      }
+      __syncthreads();  // this tile is visible to every wave
+      if (it + 1 < NT)  // in flight during this tile's products
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          const int f = threadIdx.x + 64 * W * u;
+          qf[u] = ld4<S16>(Q, head + (size_t)(i0 + 32 + f / Q4) * HS + 4 * (f % Q4));
+          of[u] = *reinterpret_cast<const v4f*>(head_row(dO, bh, H, T, ldo, HS, i0 + 32 + f / Q4) + 4 * (f % Q4));
+        }
+      if (it < first) continue;  // before this wave's diagonal: the barriers only
+    }
     if constexpr (STAGE) {
-      v4f qn[PER], on[PER];
+      if constexpr (W == 1) {
+        v4f qn[PER], on[PER];
 #pragma unroll
-      for (int u = 0; u < PER; ++u) {
-        const int f = lane + 64 * u;
-        qn[u] = ld4<S16>(Q, head + (size_t)(i0 + f / Q4) * HS + 4 * (f % Q4));
-        on[u] = *reinterpret_cast<const v4f*>(head_row(dO, bh, H, T, ldo, HS, i0 + f / Q4) + 4 * (f % Q4));
-      }
-      wave_lds_sync();  // the last tile's reads of Qs and Os are done
+        for (int u = 0; u < PER; ++u) {
+          const int f = lane + 64 * u;
+          qn[u] = ld4<S16>(Q, head + (size_t)(i0 + f / Q4) * HS + 4 * (f % Q4));
+          on[u] = *reinterpret_cast<const v4f*>(head_row(dO, bh, H, T, ldo, HS, i0 + f / Q4) + 4 * (f % Q4));
+        }
+        wave_lds_sync();  // the last tile's reads of Qs and Os are done
 #pragma unroll
-      for (int u = 0; u < PER; ++u) {
-        const int f = lane + 64 * u;
-        *reinterpret_cast<v4f*>(Qs + (f / Q4) * LD + 4 * (f % Q4)) = qn[u];
-        *reinterpret_cast<v4f*>(Os + (f / Q4) * LD + 4 * (f % Q4)) = on[u];
+        for (int u = 0; u < PER; ++u) {
+          const int f = lane + 64 * u;
+          *reinterpret_cast<v4f*>(Qs + (f / Q4) * LD + 4 * (f % Q4)) = qn[u];
+          *reinterpret_cast<v4f*>(Os + (f / Q4) * LD + 4 * (f % Q4)) = on[u];
+        }
+        wave_lds_sync();  // this tile's stores are visible to every lane
       }
-      wave_lds_sync();  // this tile's stores are visible to every lane
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
         float qa[8], oa[8];  // A: rows perm_row(x) of Q_i, dO_i
@@ -604,7 +639,7 @@ void fwd_launch(const float* Q, const float* K, const float* V, const float* sca
 template <int HS, bool CAUSAL, bool BF, bool S16, bool X3 = false>
 void bwd_launch(const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s) {
   const unsigned grid = (unsigned)(T / 32 * BH);
-  // Split products at T >= 1024: four query tiles per workgroup (dQ pass 4-7 %
+  // Split products at T >= 1024: four query (key) tiles per workgroup (dQ pass 4-7 %
   // faster at T = 1024 ... 4096; at T = 256 a head has two groups, the short
   // one's waves mostly wait at its barriers, and it measured 5 % slower, two
   // tiles per workgroup 3 % slower).
@@ -618,8 +653,14 @@ void bwd_launch(const FlashBwd& a, int ldo, int H, int T, int BH, hipStream_t s)
   if (!grouped)
     k_flash_bwd_dq<HS, CAUSAL, BF, S16, X3><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.O, a.dO, ldo, H, a.lse, a.scale,
                                                                  a.dQ, a.Dq, a.dsum, T, BH);
-  k_flash_bwd_dkv<HS, CAUSAL, BF, S16, X3><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.dO, ldo, H, a.lse, a.dsum, a.scale,
-                                                                a.dK, a.Dk, a.dV, a.Dv, T, BH);
+  if constexpr (X3) {
+    if (grouped)
+      k_flash_bwd_dkv<HS, CAUSAL, BF, S16, X3, 4><<<grid / 4, 256, 0, s>>>(a.Q, a.K, a.V, a.dO, ldo, H, a.lse, a.dsum,
+                                                                           a.scale, a.dK, a.Dk, a.dV, a.Dv, T, BH);
+  }
+  if (!grouped)
+    k_flash_bwd_dkv<HS, CAUSAL, BF, S16, X3><<<grid, 64, 0, s>>>(a.Q, a.K, a.V, a.dO, ldo, H, a.lse, a.dsum, a.scale,
+                                                                  a.dK, a.Dk, a.dV, a.Dv, T, BH);
 }
 
 // precision: 0 f32 (FP32 MFMA), 1 bf16 MFMA on f32 storage, 2 bf16 MFMA on
